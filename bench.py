@@ -1,0 +1,274 @@
+"""Benchmark of the Lancius hot path on one MI355X.
+
+Headline (its largest square case): one fp32 GEMM
+C = A.B with M = N = K = 4096, A and B ~ N(0,1) (SplitMix64, seed 43), inputs
+resident in HBM.  A step is one GEMM launch; `value` is GFLOP/s = 2MNK /
+(seconds per step), timed with HIP events on the stream the kernel runs on.
+
+The same JSON line carries:
+  roofline      the GEMM against the fp32 MFMA peak (157.3 TFLOP/s)
+  cpu_baseline  the reference's own graph MATMUL node (IKJ, one thread by
+                construction, B/src/runtime/lancius_scheduler.c:222-234),
+                compiled from source into oracle/_ref, timed on this host on
+                a bounded row sample of the same product
+  all_configs   every other BASELINE.json config measured in this run:
+                GEMM 1024^3 / 2048^3 / 16x4096x4096, attention B8 H16 D64
+                S512/S2048 causal/non-causal, conv 3x3 N32 64->128 56^2 +ReLU,
+                and the MLP and transformer-block graphs through the device
+                executor (forward latency).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from lancius_amd import (Device, DeviceProgram, abi, device_count, graph_lib, graphs,  # noqa: E402
+                         prng)
+
+PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
+PEAK_HBM = 8000.0       # GB/s
+METRIC = "GFLOP/s + % of fp32 MFMA peak (GEMM/attn/conv); graph fwd latency ms"
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def log(msg: str) -> None:
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+def time_steps(dev: Device, fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn over `steps` calls, HIP events on the
+    context stream, after `warmup` untimed calls."""
+    for _ in range(warmup):
+        fn()
+    dev.synchronize()
+    dev.timer_start()
+    for _ in range(steps):
+        fn()
+    ms = dev.timer_stop()
+    dev.synchronize()
+    return ms / steps
+
+
+def gemm_case(dev, M, K, N, seed, steps, warmup):
+    A = dev.upload(prng.normal(seed, (M, K)))
+    B = dev.upload(prng.normal(seed + 1000, (K, N)))
+    Cb = dev.alloc(M * N * 4)
+    ms = time_steps(dev, lambda: dev.gemm(Cb, A, B, M, K, N), steps, warmup)
+    for b in (A, B, Cb):
+        b.free()
+    flops = 2.0 * M * N * K
+    nbytes = 4.0 * (M * K + K * N + M * N)
+    return ms, flops, nbytes
+
+
+def attention_case(dev, B, S, H, D, causal, seed, steps, warmup):
+    shape = (B, S, H, D)
+    q, k, v = (dev.upload(prng.normal(seed + i, shape)) for i in range(3))
+    o = dev.alloc(int(np.prod(shape)) * 4)
+    ms = time_steps(dev, lambda: dev.attention(o, q, k, v, B, S, H, D, causal=causal), steps, warmup)
+    for b in (q, k, v, o):
+        b.free()
+    flops = 4.0 * B * H * D * (S * (S + 1) / 2 if causal else S * S)
+    return ms, flops, 16.0 * B * S * H * D
+
+
+def conv_case(dev, steps, warmup):
+    N, C_in, H, W, C_out = 32, 64, 56, 56, 128
+    x = dev.upload(prng.normal(45, (N, C_in, H, W)))
+    w = dev.upload(prng.normal(145, (C_out, C_in, 3, 3), std=float(np.sqrt(2.0 / (9 * C_in)))))
+    o = dev.alloc(N * C_out * H * W * 4)
+    ms = time_steps(dev, lambda: dev.conv2d(o, x, w, None, N, C_in, H, W, C_out, 3, 3, 1, 1, 1), steps, warmup)
+    for b in (x, w, o):
+        b.free()
+    flops = 2.0 * N * C_out * H * W * C_in * 9
+    return ms, flops, 4.0 * (N * C_in * H * W + C_out * C_in * 9 + N * C_out * H * W)
+
+
+def graph_case(dev, bg, feeds, steps, warmup):
+    lib = graph_lib()
+    lib.lancius_graph_set_dtype(bg.g, abi.DTYPE_FP32)
+    sched = lib.lancius_ir_schedule(bg.g)
+    plan = lib.lancius_build_memory_plan(sched, bg.g)
+    prog = DeviceProgram(dev, bg.g, sched, plan)
+    for name in bg.inputs:
+        prog.upload(bg.node(name), feeds[name])
+    ms = time_steps(dev, prog.run, steps, warmup)
+    info = prog.info()
+    prog.close()
+    lib.lancius_memory_plan_destroy(plan)
+    lib.lancius_schedule_destroy(sched)
+    return ms, info
+
+
+def cpu_baseline(M, K, N, target_s: float = 12.0) -> dict | None:
+    """The reference graph MATMUL node on a row sample of the headline GEMM."""
+    try:
+        import oracle
+    except Exception as e:  # pragma: no cover - reported, not fatal
+        log(f"cpu baseline unavailable: {e}")
+        return None
+    ref = oracle.ref_lib()
+    kind = "reference"
+    a_full = prng.normal(43, (M, K)).astype(np.float64)
+    b = np.ascontiguousarray(prng.normal(1043, (K, N)).astype(np.float64))
+
+    def run(rows: int) -> float:
+        a = np.ascontiguousarray(a_full[:rows])
+        if ref is not None:
+            g = ref.lancius_graph_create()
+            na, nb = ref.lancius_input(g, rows, K), ref.lancius_input(g, K, N)
+            ref.lancius_matmul(g, na, nb)
+            na.contents.runtime_data = a.ctypes.data_as(C.POINTER(C.c_double))
+            nb.contents.runtime_data = b.ctypes.data_as(C.POINTER(C.c_double))
+            sched = ref.lancius_ir_schedule(g)
+            arena = ref.lancius_arena_create(rows * N * 8 + (1 << 20))
+            t0 = time.perf_counter()
+            ref.lancius_schedule_execute(sched, arena)
+            dt = time.perf_counter() - t0
+            na.contents.runtime_data = None
+            nb.contents.runtime_data = None
+            ref.lancius_schedule_destroy(sched)
+            ref.lancius_arena_destroy(arena)
+            ref.lancius_graph_destroy(g)
+            return dt
+        oracle.set_threads(1)
+        t0 = time.perf_counter()
+        oracle.matmul(a, b, rows=(0, rows))
+        return time.perf_counter() - t0
+
+    if ref is None:
+        kind = "port"
+    probe_rows = 32
+    dt = run(probe_rows)
+    rows = int(min(M, max(probe_rows, probe_rows * target_s / max(dt, 1e-6))))
+    rows = max(probe_rows, (rows // 32) * 32)
+    dt = run(rows)
+    gflops = 2.0 * rows * K * N / dt / 1e9
+    cpu = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(gflops, 3), "unit": "GFLOP/s", "cores": 1, "kind": kind,
+            "sample": f"rows 0-{rows - 1} of the {M}x{K}x{N} fp64 product through the "
+                      f"{'reference' if kind == 'reference' else 'oracle'} graph MATMUL node (IKJ, 1 thread), "
+                      f"{dt:.1f} s on {cpu} ({os.cpu_count()} logical CPUs visible)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--quick", action="store_true", help="headline only (no other configs)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
+              f"(see DESIGN.md for how the path would shard)", file=sys.stderr)
+        return 2
+    if device_count() < 1:
+        print("bench.py: no GPU visible to HIP", file=sys.stderr)
+        return 1
+    dev = Device(0)
+    M = N = K = 4096
+    log("headline gemm 4096^3")
+    ms, flops, nbytes = gemm_case(dev, M, K, N, 43, args.steps, args.warmup)
+    gflops = flops / (ms * 1e-3) / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("gemm_f32_mfma 4096^3")
+    result = {
+        "metric": METRIC,
+        "value": round(gflops, 1),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic: SplitMix64 seed 43, A,B ~ N(0,1) fp32, resident in HBM",
+        "config": {"workload": "gemm_f32 C=A.B row-major M=N=K=4096 (BASELINE.json configs[1])",
+                   "M": M, "N": N, "K": K, "parallelism": "1 GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(flops / (ms * 1e-3) / 1e12, 2), "peak": PEAK_FP32_MFMA,
+                     "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA, 4),
+                     "traffic": traffic, "algorithmic_bytes": nbytes},
+    }
+    extra = {}
+    if not args.quick:
+        steps = max(5, args.steps)
+        for name, (m, k, n) in (("gemm_1024", (1024, 1024, 1024)), ("gemm_2048", (2048, 2048, 2048)),
+                                ("gemm_16x4096x4096", (16, 4096, 4096))):
+            log(name)
+            t, f, b = gemm_case(dev, m, k, n, 43, steps, 3)
+            extra[name] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
+                           "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4),
+                           "GB/s": round(b / t / 1e6, 1), "frac_hbm": round(b / t / 1e6 / PEAK_HBM, 4)}
+        for S in (512, 2048):
+            for causal in (True, False):
+                name = f"attention_B8_H16_D64_S{S}_{'causal' if causal else 'noncausal'}"
+                log(name)
+                t, f, b = attention_case(dev, 8, S, 16, 64, causal, 44, steps, 3)
+                extra[name] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
+                               "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
+        log("conv")
+        t, f, b = conv_case(dev, steps, 3)
+        extra["conv3x3_N32_64to128_56x56_relu"] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
+                                                   "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
+        log("mlp graph")
+        lib = graph_lib()
+        bg = graphs.build_mlp(lib)
+        feeds = {"x": prng.uniform(42, (64, 784), -1.0, 1.0), "W1": prng.normal(142, (784, 256), 0, 0.02),
+                 "b1": np.zeros((1, 256), np.float32), "W2": prng.normal(342, (256, 10), 0, 0.02),
+                 "b2": np.zeros((1, 10), np.float32)}
+        t, info = graph_case(dev, bg, feeds, max(20, steps), 5)
+        bg.destroy()
+        extra["mlp_graph_64x784x256x10"] = {"fwd_latency_ms": round(t, 4), "launches": info["launches"],
+                                            "GFLOP/s": round(26.02e6 / t / 1e6, 1)}
+        log("transformer block graph")
+        bg = graphs.build_block(lib)
+        feeds = {}
+        for i, name in enumerate(bg.inputs):
+            shape = abi.node_shape(bg.node(name))
+            if name.startswith("x"):
+                feeds[name] = prng.normal(46 + 1000 * i, shape)
+            elif name in ("g1", "g2"):
+                feeds[name] = np.ones(shape, np.float32)
+            else:
+                feeds[name] = prng.normal(46 + 1000 * i, shape, 0, 0.02)
+        t, info = graph_case(dev, bg, feeds, 10, 3)
+        bg.destroy()
+        extra["transformer_block_B4_S1024_d1024_H16_F4096"] = {
+            "fwd_latency_ms": round(t, 3), "launches": info["launches"],
+            "GFLOP/s": round(111.7e9 / t / 1e6, 1), "arena_MiB": round(info["arena_bytes"] / 2 ** 20, 1)}
+        result["all_configs"] = extra
+    dev.close()
+    if not args.no_cpu:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(M, K, N)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

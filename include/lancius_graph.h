@@ -1,0 +1,104 @@
+/*
+ * lancius_graph.h - the C host side of the Lancius graph path, rebuilt for the
+ * MI355X backend: graph IR builders, wave scheduler, linear-scan memory planner
+ * and the Conv+ReLU fusion pass (library liblancius_graph).
+ *
+ * Names, signatures, struct layouts (lancius_abi.h) and results follow the
+ * reference so that a program written against the reference headers builds
+ * graphs with either library:
+ *   builders ............ bleeding/v11A1/src/ir/lancius_ir.c:72-299
+ *   lancius_ir_schedule . bleeding/v11A1/src/runtime/lancius_scheduler.c:12-59
+ *   planner ............. bleeding/v11A1/src/runtime/lancius_memory_planner.c:33-182
+ *   fusion .............. bleeding/v11A1/src/compiler/lancius_optimizer.c:15-41
+ *   arena ............... bleeding/v11A1/src/core/lancius_arena.c:30-100
+ *   errors .............. bleeding/v11A1/src/core/lancius_error.c:5-34
+ *
+ * One deliberate difference: the reference planner never stores the offset it
+ * assigns into its active-interval list (lancius_memory_planner.c:140,167), so
+ * every block it frees re-enters the free list at offset 0 and later tensors
+ * can overlap live ones.  lancius_build_memory_plan here runs the same
+ * first-fit / LIFO / no-coalescing / sink-pinning scan with the offset kept,
+ * which gives identical offsets whenever the reference's are overlap-free.
+ */
+#ifndef LANCIUS_AMD_GRAPH_H
+#define LANCIUS_AMD_GRAPH_H
+
+#include "lancius_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- errors (lancius_error.h:6-18) ---- */
+#ifndef LANCIUS_ERROR_H
+#define LANCIUS_ERROR_H
+typedef enum {
+    LANCIUS_ERROR_OK = 0,
+    LANCIUS_ERROR_OOM = -1,
+    LANCIUS_ERROR_NULL_PTR = -2,
+    LANCIUS_ERROR_SHAPE_MISMATCH = -3,
+    LANCIUS_ERROR_UNSUPPORTED_OP = -4,
+    LANCIUS_ERROR_UNSUPPORTED_DTYPE = -5,
+    LANCIUS_ERROR_INVALID_MODEL = -6,
+    LANCIUS_ERROR_VERSION_MISMATCH = -7,
+    LANCIUS_ERROR_IO = -8,
+    LANCIUS_ERROR_OVERFLOW = -9,
+    LANCIUS_ERROR_INTERNAL = -10
+} lancius_error;
+void lancius_set_error(lancius_error err);
+lancius_error lancius_get_error(void);
+void lancius_clear_error(void);
+const char* lancius_error_string(lancius_error err);
+#endif
+
+/* ---- host bump arena (lancius_arena.h:12-15) ---- */
+lancius_arena* lancius_arena_create(size_t block_size);
+void* lancius_arena_alloc(lancius_arena* arena, size_t size, size_t alignment);
+void lancius_arena_reset(lancius_arena* arena);
+void lancius_arena_destroy(lancius_arena* arena);
+
+/* ---- graph IR (lancius_ir.h:80-123, the ops on the device path) ---- */
+lancius_graph* lancius_graph_create(void);
+void lancius_graph_destroy(lancius_graph* g);
+
+lancius_node* lancius_input(lancius_graph* g, size_t r, size_t c);
+lancius_node* lancius_input_4d(lancius_graph* g, size_t n, size_t c, size_t h, size_t w);
+lancius_node* lancius_const(lancius_graph* g, double val, size_t r, size_t c);
+lancius_node* lancius_add(lancius_graph* g, const lancius_node* a, const lancius_node* b);
+lancius_node* lancius_matmul(lancius_graph* g, const lancius_node* a, const lancius_node* b);
+lancius_node* lancius_relu(lancius_graph* g, const lancius_node* a);
+lancius_node* lancius_softmax(lancius_graph* g, const lancius_node* a);
+lancius_node* lancius_broadcast(lancius_graph* g, const lancius_node* a, size_t r, size_t c);
+lancius_node* lancius_conv2d(lancius_graph* g, const lancius_node* in, const lancius_node* w, uint32_t stride,
+                             uint32_t pad);
+lancius_node* lancius_flatten(lancius_graph* g, const lancius_node* in);
+lancius_node* lancius_reshape(lancius_graph* g, const lancius_node* in, uint8_t ndim, size_t s0, size_t s1, size_t s2,
+                              size_t s3);
+lancius_node* lancius_attention(lancius_graph* g, const lancius_node* q, const lancius_node* k, const lancius_node* v);
+lancius_node* lancius_layernorm(lancius_graph* g, const lancius_node* in, const lancius_node* gamma,
+                                const lancius_node* beta);
+lancius_node* lancius_gelu(lancius_graph* g, const lancius_node* in);
+
+/* Conv2D + ReLU fusion pass (lancius_optimizer.c:15-41). */
+void lancius_optimize_fusion(lancius_graph* g);
+
+/* ---- scheduler (lancius_scheduler.h:14-29) ---- */
+lancius_schedule* lancius_ir_schedule(lancius_graph* g);
+void lancius_schedule_destroy(lancius_schedule* schedule);
+void lancius_schedule_attach_pool(lancius_schedule* schedule, void* flat_buffer, struct lancius_memory_plan* plan);
+size_t lancius_schedule_peak_memory(lancius_schedule* schedule);
+
+/* ---- memory planner (lancius_memory_planner.h:20-23) ---- */
+lancius_memory_plan* lancius_build_memory_plan(lancius_schedule* sched, lancius_graph* g);
+void lancius_memory_plan_destroy(lancius_memory_plan* plan);
+
+/* Sets the dtype of every node (e.g. LANCIUS_DTYPE_FP32 before planning the
+ * device arena; the reference sizes plan blocks by dtype, lancius_ir.h:75-78).
+ * No reference counterpart. */
+void lancius_graph_set_dtype(lancius_graph* g, lancius_dtype dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LANCIUS_AMD_GRAPH_H */

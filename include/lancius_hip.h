@@ -1,0 +1,161 @@
+/*
+ * lancius_hip.h - C ABI of the MI355X (gfx950) kernel backend for Lancius.
+ *
+ * Pure C.  Every pointer named "device" is an address in GPU memory (HBM);
+ * buffers are owned by the caller.  Every entry point returns an int status:
+ * 0 on success or a negative code with the values of the reference error
+ * model (bleeding/v11A1/include/lancius/lancius_error.h:6-18):
+ *   -1 out of memory, -2 null pointer, -3 shape mismatch / bad size,
+ *   -4 unsupported op, -10 internal (any other HIP failure).
+ * A thread-local message for the last failure is available from
+ * lancius_hip_last_error().  No entry point aborts the process.
+ *
+ * Kernel launches are asynchronous on the stream of the context; two
+ * contexts on different streams may be used from different host threads
+ * concurrently (the reference runs nodes of one wave from a pthread pool,
+ * bleeding/v11A1/src/runtime/lancius_scheduler.c:405-411).
+ */
+#ifndef LANCIUS_HIP_H
+#define LANCIUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(_WIN32)
+#define LANCIUS_HIP_EXPORT __declspec(dllexport)
+#else
+#define LANCIUS_HIP_EXPORT __attribute__((visibility("default")))
+#endif
+
+/* Status codes; same numbers as lancius_error (lancius_error.h:6-18). */
+#define LANCIUS_HIP_OK                 0
+#define LANCIUS_HIP_ERR_OOM           (-1)
+#define LANCIUS_HIP_ERR_NULL_PTR      (-2)
+#define LANCIUS_HIP_ERR_SHAPE         (-3)
+#define LANCIUS_HIP_ERR_UNSUPPORTED   (-4)
+#define LANCIUS_HIP_ERR_DTYPE         (-5)
+#define LANCIUS_HIP_ERR_INTERNAL      (-10)
+
+/* Epilogue activation of the GEMM / conv kernels. */
+#define LANCIUS_HIP_ACT_NONE 0
+#define LANCIUS_HIP_ACT_RELU 1   /* max(x, 0): lancius_scheduler.c:305-308       */
+#define LANCIUS_HIP_ACT_GELU 2   /* tanh GELU with +-100 clamp: lancius_kernels.c:238-246 */
+
+typedef struct lancius_hip_ctx lancius_hip_ctx;
+
+/* ---- context, memory, timing --------------------------------------- */
+
+/* Creates a context on `device`.  `stream` is a hipStream_t passed as an
+ * opaque pointer; NULL selects the device's null stream. */
+LANCIUS_HIP_EXPORT int lancius_hip_ctx_create(int device, void* stream, lancius_hip_ctx** out);
+LANCIUS_HIP_EXPORT void lancius_hip_ctx_destroy(lancius_hip_ctx* ctx);
+LANCIUS_HIP_EXPORT const char* lancius_hip_last_error(void);
+/* Number of GPUs visible to HIP (0 when none; never fails). */
+LANCIUS_HIP_EXPORT int lancius_hip_device_count(void);
+
+LANCIUS_HIP_EXPORT int lancius_hip_malloc(lancius_hip_ctx* ctx, void** device_ptr, size_t bytes);
+LANCIUS_HIP_EXPORT int lancius_hip_free(lancius_hip_ctx* ctx, void* device_ptr);
+/* Synchronous copies (they wait for the context's stream). */
+LANCIUS_HIP_EXPORT int lancius_hip_upload(lancius_hip_ctx* ctx, void* device_dst, const void* host_src, size_t bytes);
+LANCIUS_HIP_EXPORT int lancius_hip_download(lancius_hip_ctx* ctx, void* host_dst, const void* device_src, size_t bytes);
+LANCIUS_HIP_EXPORT int lancius_hip_synchronize(lancius_hip_ctx* ctx);
+
+/* HIP events on the context's stream: start, then stop returns the
+ * elapsed milliseconds between the two records (waits for the stop). */
+LANCIUS_HIP_EXPORT int lancius_hip_timer_start(lancius_hip_ctx* ctx);
+LANCIUS_HIP_EXPORT int lancius_hip_timer_stop(lancius_hip_ctx* ctx, float* elapsed_ms);
+
+/* ---- kernels (device pointers, fp32, row-major) --------------------- */
+
+/* C[M,N] = epilogue(A[M,K] . B[K,N]).
+ * Epilogue order: y = acc + bias[n] (bias may be NULL); y = act(y);
+ * y = y + residual[m,n] (residual may be NULL; it may alias C).
+ * Replaces the MATMUL branch (lancius_scheduler.c:222-234) plus the
+ * BROADCAST/ADD/RELU/GELU nodes that follow it in a graph. */
+LANCIUS_HIP_EXPORT int lancius_hip_gemm_f32(lancius_hip_ctx* ctx, float* C, const float* A, const float* B,
+                                            size_t M, size_t K, size_t N,
+                                            const float* bias, int act, const float* residual);
+
+/* `count` independent GEMMs of one shape in a single launch (the branches of
+ * one scheduler wave).  Every array is a host array of `count` device
+ * pointers; B[g] and bias[g] may repeat; bias and residual may be NULL (the
+ * array) or hold NULLs.  count <= LANCIUS_HIP_MAX_GROUP. */
+#define LANCIUS_HIP_MAX_GROUP 16
+LANCIUS_HIP_EXPORT int lancius_hip_gemm_grouped_f32(lancius_hip_ctx* ctx, size_t count,
+                                                    float* const* C, const float* const* A, const float* const* B,
+                                                    size_t M, size_t K, size_t N,
+                                                    const float* const* bias, int act, const float* const* residual);
+
+/* out[N,C_out,H_out,W_out] = act(conv(in[N,C_in,H,W], w[C_out,C_in,K_h,K_w]) + bias[C_out]).
+ * Cross-correlation with zero padding, H_out = (H + 2 pad - K_h)/stride + 1
+ * (lancius_kernels.c:28-60, ReLU variant :140-173).  bias may be NULL;
+ * act is LANCIUS_HIP_ACT_NONE or LANCIUS_HIP_ACT_RELU. */
+LANCIUS_HIP_EXPORT int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* w,
+                                              const float* bias,
+                                              size_t N, size_t C_in, size_t H, size_t W,
+                                              size_t C_out, size_t K_h, size_t K_w,
+                                              size_t stride, size_t pad, int act);
+
+/* Scaled-dot-product attention over [batch, S, H, D] row-major tensors
+ * (row (b,i,h) starts at ((b*S + i)*H + h)*D).  causal != 0 masks keys
+ * j > i exactly as lancius_kernels.c:307; scale multiplies q.k
+ * (the reference uses 1/sqrt(D), :284).  batch = 1, causal = 1,
+ * scale = 1/sqrt(D) is the reference kernel_attention (:278-332). */
+LANCIUS_HIP_EXPORT int lancius_hip_attention_f32(lancius_hip_ctx* ctx, float* out,
+                                                 const float* q, const float* k, const float* v,
+                                                 size_t batch, size_t S, size_t H, size_t D,
+                                                 int causal, float scale);
+
+/* Same, for `count` independent [S,H,D] problems given by host arrays of
+ * device pointers (count <= LANCIUS_HIP_MAX_GROUP). */
+LANCIUS_HIP_EXPORT int lancius_hip_attention_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* out,
+                                                         const float* const* q, const float* const* k,
+                                                         const float* const* v,
+                                                         size_t S, size_t H, size_t D, int causal, float scale);
+
+/* Row LayerNorm: two-pass mean and biased variance, then
+ * (x - mean) * (1/sqrt(var + eps)) * gamma + beta (lancius_kernels.c:217-236). */
+LANCIUS_HIP_EXPORT int lancius_hip_layernorm_f32(lancius_hip_ctx* ctx, float* out, const float* in,
+                                                 const float* gamma, const float* beta,
+                                                 size_t rows, size_t hidden, float eps);
+
+/* Row softmax (max-subtracted, lancius_scheduler.c:284-294).  When argmax
+ * is not NULL it receives int32 per row: the index of the first maximum of
+ * the output probabilities, the strict '>' scan from -1e9 that the callers
+ * run over a softmax output (B/examples/train_mnist.c:206-209,
+ * B/examples/run_edge.c:82-88). */
+LANCIUS_HIP_EXPORT int lancius_hip_softmax_f32(lancius_hip_ctx* ctx, float* probs, int32_t* argmax,
+                                               const float* in, size_t rows, size_t cols);
+
+/* Elementwise ops (lancius_scheduler.c:169-189, 268-278, 305-308;
+ * lancius_kernels.c:238-246). */
+LANCIUS_HIP_EXPORT int lancius_hip_add_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n);
+LANCIUS_HIP_EXPORT int lancius_hip_relu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n);
+LANCIUS_HIP_EXPORT int lancius_hip_gelu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n);
+/* out[r,c] = row[c] for r < rows (row has `cols` values); with cols_in == 1
+ * every element is row[0] (the scalar branch, lancius_scheduler.c:271-273). */
+LANCIUS_HIP_EXPORT int lancius_hip_broadcast_f32(lancius_hip_ctx* ctx, float* out, const float* row,
+                                                 size_t rows, size_t cols, size_t cols_in);
+LANCIUS_HIP_EXPORT int lancius_hip_fill_f32(lancius_hip_ctx* ctx, float* out, float value, size_t n);
+LANCIUS_HIP_EXPORT int lancius_hip_copy_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n);
+
+/* ---- reference-ABI bridge ------------------------------------------- */
+
+/* The fp32 matmul that the reference declares but never defines
+ * (bleeding/v11A1/include/lancius/lancius_kernels.h:55).  HOST pointers,
+ * row-major out[M,N] = a[M,K] . b[K,N]; stages through the device of a
+ * process-wide default context (device 0, null stream) and returns when
+ * `out` holds the result.  Failures are reported by
+ * lancius_hip_last_status() (void return, as declared by the reference). */
+LANCIUS_HIP_EXPORT void kernel_matmul_f32(float* out, const float* a, const float* b, size_t M, size_t K, size_t N);
+LANCIUS_HIP_EXPORT int lancius_hip_last_status(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LANCIUS_HIP_H */

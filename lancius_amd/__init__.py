@@ -1,0 +1,17 @@
+"""MI355X (gfx950) kernel backend for the Lancius graph path.
+
+Native libraries (built in-tree by `python -m lancius_amd.build`):
+  liblancius_hip.so    C ABI of the HIP kernels and the device executor
+                       (include/lancius_hip.h, include/lancius_hip_graph.h)
+  liblancius_graph.so  C graph IR / scheduler / planner (include/lancius_graph.h)
+
+This Python package only loads and wraps them; it computes nothing itself.
+"""
+from . import abi, prng
+from .runtime import (ACT_GELU, ACT_NONE, ACT_RELU, DEVICE_KEEP_ALL, DEVICE_NO_FUSION, DEVICE_NO_GROUP, Device,
+                      DeviceProgram, HipError, device_count, graph_lib, hip_lib)
+
+__all__ = [
+    "abi", "prng", "Device", "DeviceProgram", "HipError", "device_count", "graph_lib", "hip_lib",
+    "ACT_NONE", "ACT_RELU", "ACT_GELU", "DEVICE_NO_FUSION", "DEVICE_KEEP_ALL", "DEVICE_NO_GROUP",
+]

@@ -1,0 +1,330 @@
+// Fused scaled-dot-product attention, fp32, on the gfx950 matrix cores.
+//
+// Semantics: bleeding/v11A1/src/math/lancius_kernels.c:278-332 (kernel_attention):
+// for each query row i and head h, s_j = (q_i . k_j) * scale, keys j > i get
+// -1e9 when causal (:307), online softmax with running max m and sum l
+// (:309-319), out = o / l (:322-327).  Tensors are [batch, S, H, D] row-major;
+// the reference is batch = 1, causal, scale = 1/sqrt(D) (:284, :293).
+// Skipping key blocks that lie entirely above the diagonal is exactly the
+// reference's masking: exp(-1e9 - m) is 0 and the correction factor is 1.
+//
+// Fast kernel (D = 64), "transposed" formulation so that every softmax
+// statistic is lane-local:
+//   S^T[key][q] = K . Q^T    MFMA A = K tile (LDS), B = Q^T (registers)
+//   O^T[d][q]  += V^T . P^T  MFMA A = V^T (LDS),    B = P^T (the S^T registers)
+// With v_mfma_f32_32x32x2_f32, lane l holds query l%32 in both accumulators,
+// so the row max / sum need one swap with lane l^32 and the O rescale is a
+// per-lane multiply.  The P^T accumulator is fed back as the B operand without
+// any data movement: step s of the PV product uses register s, whose key index
+// 8*(s/4) + 4*(l/32) + s%4 is matched by the V^T operand address.
+// The score tile never leaves registers.  Each workgroup (4 waves) owns 128
+// queries of one (batch, head); K/V blocks of 64 keys are double-buffered in
+// LDS and shared by the 4 waves.  Q is pre-scaled by scale*log2(e) so the
+// exponentials are exp2.
+#include <math.h>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lancius {
+namespace {
+
+struct AttnParams {
+    float* O[LANCIUS_HIP_MAX_GROUP];
+    const float* Q[LANCIUS_HIP_MAX_GROUP];
+    const float* K[LANCIUS_HIP_MAX_GROUP];
+    const float* V[LANCIUS_HIP_MAX_GROUP];
+    int batch;  // batches per group entry
+    int S, H, D;
+    int causal;
+    float qscale;  // scale * log2(e)
+    int q_tiles;
+};
+
+constexpr int kD = 64;
+constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
+constexpr int kBKV = 64;   // keys per LDS block
+constexpr int kLDK = kD + 1;  // K rows padded: lanes read 32 different keys at one d
+constexpr int kLDV = kD + 4;  // V rows: lanes read 32 consecutive d of one key
+
+__global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
+    __shared__ __attribute__((aligned(16))) float Ks[2][kBKV][kLDK];
+    __shared__ __attribute__((aligned(16))) float Vs[2][kBKV][kLDV];
+
+    const int z = blockIdx.z;
+    const int g = z / p.batch, b = z % p.batch;
+    const int h = blockIdx.y;
+    // Causal: the tiles with the most keys start first.
+    const int qt = p.causal ? (p.q_tiles - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+    const int S = p.S, H = p.H;
+    const size_t row_stride = (size_t)H * kD;
+    const size_t base = ((size_t)b * S * H + h) * kD;
+    const float* __restrict__ Qg = p.Q[g] + base;
+    const float* __restrict__ Kg = p.K[g] + base;
+    const float* __restrict__ Vg = p.V[g] + base;
+    float* __restrict__ Og = p.O[g] + base;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int lq = lane & 31, lk = lane >> 5;
+    const int q0 = qt * kBQ;
+    const int qw0 = q0 + wave * 32;   // first query of this wave
+    const int q = qw0 + lq;           // this lane's query
+    const bool q_valid = q < S;
+
+    // Q^T operand: step s uses d = s + 32*(l/32); the K operand uses the same d.
+    float qf[32];
+    if (q_valid) {
+        const f32x4* src = (const f32x4*)(Qg + (size_t)q * row_stride + 32 * lk);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const f32x4 v = src[i];
+            qf[4 * i + 0] = v.x * p.qscale;
+            qf[4 * i + 1] = v.y * p.qscale;
+            qf[4 * i + 2] = v.z * p.qscale;
+            qf[4 * i + 3] = v.w * p.qscale;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
+    }
+
+    // Key range of this workgroup.
+    const int kv_end = p.causal ? min(S, q0 + kBQ) : S;
+    const int nblocks = (kv_end + kBKV - 1) / kBKV;
+
+    // K/V global -> register staging: 64 keys x 64 d = 1024 float4 per tensor.
+    f32x4 kreg[4], vreg[4];
+    auto load_kv = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = tid + 256 * i;
+            const int key = idx >> 4, dq = idx & 15;
+            const int gk = kb + key;
+            if (gk < S) {
+                kreg[i] = *(const f32x4*)(Kg + (size_t)gk * row_stride + 4 * dq);
+                vreg[i] = *(const f32x4*)(Vg + (size_t)gk * row_stride + 4 * dq);
+            } else {
+                kreg[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+                vreg[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    };
+    auto store_kv = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = tid + 256 * i;
+            const int key = idx >> 4, dq = idx & 15;
+            float* kd = &Ks[buf][key][4 * dq];
+            kd[0] = kreg[i].x;
+            kd[1] = kreg[i].y;
+            kd[2] = kreg[i].z;
+            kd[3] = kreg[i].w;
+            *(f32x4*)&Vs[buf][key][4 * dq] = vreg[i];
+        }
+    };
+
+    f32x16 o_acc[2];  // O^T for d-blocks 0..31 and 32..63
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        o_acc[0][r] = 0.0f;
+        o_acc[1][r] = 0.0f;
+    }
+    float m_run = -1e30f;  // running max (log2 domain); finite so exp2 never sees inf - inf
+    float l_part = 0.0f;   // this lane's share of the running sum
+
+    load_kv(0);
+    store_kv(0);
+    __syncthreads();
+
+    for (int blk = 0; blk < nblocks; ++blk) {
+        const int cur = blk & 1;
+        const int kb = blk * kBKV;
+        const bool more = blk + 1 < nblocks;
+        if (more) load_kv(kb + kBKV);
+
+        // Wave-uniform skip of blocks entirely above this wave's diagonal.
+        const bool active = !p.causal || kb <= qw0 + 31;
+        if (active) {
+            f32x16 s_acc[2];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s_acc[0][r] = 0.0f;
+                s_acc[1][r] = 0.0f;
+            }
+#pragma unroll
+            for (int s = 0; s < 32; ++s) {
+                const int d = s + 32 * lk;
+                const float k0 = Ks[cur][lq][d];
+                const float k1 = Ks[cur][32 + lq][d];
+                s_acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0, qf[s], s_acc[0], 0, 0, 0);
+                s_acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1, qf[s], s_acc[1], 0, 0, 0);
+            }
+            // Register r of lane l holds key kb + 32*sb + 8*(r/4) + 4*(l/32) + r%4.
+            const bool need_mask = (p.causal && kb + kBKV - 1 > qw0) || (kb + kBKV > S);
+            if (need_mask) {
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kb + 32 * sb + 8 * (r >> 2) + 4 * lk + (r & 3);
+                        if (key >= S || (p.causal && key > q)) s_acc[sb][r] = -INFINITY;
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s_acc[0][r], s_acc[1][r]));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m_run, mx);
+            const float corr = exp2f(m_run - m_new);
+            m_run = m_new;
+            float psum = 0.0f;
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float pv = exp2f(s_acc[sb][r] - m_new);
+                    s_acc[sb][r] = pv;
+                    psum += pv;
+                }
+            l_part = l_part * corr + psum;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                o_acc[0][r] *= corr;
+                o_acc[1][r] *= corr;
+            }
+            // O^T += V^T . P^T over the 64 keys of this block.
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int s = 0; s < 16; ++s) {
+                    const int key = 32 * sb + 8 * (s >> 2) + 4 * lk + (s & 3);
+                    const float v0 = Vs[cur][key][lq];
+                    const float v1 = Vs[cur][key][32 + lq];
+                    o_acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v0, s_acc[sb][s], o_acc[0], 0, 0, 0);
+                    o_acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1, s_acc[sb][s], o_acc[1], 0, 0, 0);
+                }
+        }
+        if (more) store_kv(cur ^ 1);
+        __syncthreads();
+    }
+
+    const float l_tot = l_part + __shfl_xor(l_part, 32);
+    if (!q_valid) return;
+    const float inv_l = 1.0f / l_tot;
+    float* dst = Og + (size_t)q * row_stride;
+    // O^T register r of lane l: d = 32*db + 8*(r/4) + 4*(l/32) + r%4.
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f32x4 o;
+            o.x = o_acc[db][4 * j + 0] * inv_l;
+            o.y = o_acc[db][4 * j + 1] * inv_l;
+            o.z = o_acc[db][4 * j + 2] * inv_l;
+            o.w = o_acc[db][4 * j + 3] * inv_l;
+            *(f32x4*)(dst + 32 * db + 8 * j + 4 * lk) = o;
+        }
+}
+
+// Any head_dim: one thread per (query row, head), the reference's online loop
+// in fp32 with the output row as the accumulator.  Used for shapes the fast
+// kernel does not cover.
+__global__ void __launch_bounds__(256) attention_rowwise(const AttnParams p) {
+    const size_t rows = (size_t)p.S * p.H;
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= rows) return;
+    const int z = blockIdx.z;
+    const int g = z / p.batch, b = z % p.batch;
+    const int i = (int)(t / p.H), h = (int)(t % p.H);
+    const int D = p.D;
+    const size_t rs = (size_t)p.H * D;
+    const size_t base = (size_t)b * p.S * rs + (size_t)h * D;
+    const float* q = p.Q[g] + base + (size_t)i * rs;
+    const float* K = p.K[g] + base;
+    const float* V = p.V[g] + base;
+    float* o = p.O[g] + base + (size_t)i * rs;
+    for (int d = 0; d < D; ++d) o[d] = 0.0f;
+    float m = -1e30f, l = 0.0f;
+    const int jend = p.causal ? i + 1 : p.S;
+    for (int j = 0; j < jend; ++j) {
+        const float* k = K + (size_t)j * rs;
+        float s = 0.0f;
+        for (int d = 0; d < D; ++d) s += q[d] * k[d];
+        s *= p.qscale;
+        const float m_new = fmaxf(m, s);
+        const float c = exp2f(m - m_new);
+        const float pj = exp2f(s - m_new);
+        l = l * c + pj;
+        const float* v = V + (size_t)j * rs;
+        for (int d = 0; d < D; ++d) o[d] = o[d] * c + pj * v[d];
+        m = m_new;
+    }
+    const float inv = 1.0f / l;
+    for (int d = 0; d < D; ++d) o[d] *= inv;
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, const float* const* Q,
+                       const float* const* K, const float* const* V, size_t batch, size_t S, size_t H, size_t D,
+                       int causal, float scale) {
+    LANCIUS_REQUIRE(ctx && O && Q && K && V, LANCIUS_HIP_ERR_NULL_PTR, "attention: NULL argument");
+    LANCIUS_REQUIRE(count >= 1 && count <= LANCIUS_HIP_MAX_GROUP, LANCIUS_HIP_ERR_SHAPE,
+                    "attention: group count %zu", count);
+    LANCIUS_REQUIRE(batch >= 1 && S >= 1 && H >= 1 && D >= 1, LANCIUS_HIP_ERR_SHAPE,
+                    "attention: empty shape batch=%zu S=%zu H=%zu D=%zu", batch, S, H, D);
+    LANCIUS_REQUIRE(S < (1u << 24) && H < 65536 && D <= 4096 && count * batch < 65536, LANCIUS_HIP_ERR_SHAPE,
+                    "attention: shape too large");
+    if (int rc = bind_device(ctx)) return rc;
+    AttnParams p{};
+    bool vec = true;
+    for (size_t g = 0; g < count; ++g) {
+        LANCIUS_REQUIRE(O[g] && Q[g] && K[g] && V[g], LANCIUS_HIP_ERR_NULL_PTR, "attention: NULL operand %zu", g);
+        p.O[g] = O[g];
+        p.Q[g] = Q[g];
+        p.K[g] = K[g];
+        p.V[g] = V[g];
+        vec = vec && aligned16(O[g]) && aligned16(Q[g]) && aligned16(K[g]) && aligned16(V[g]);
+    }
+    p.batch = (int)batch;
+    p.S = (int)S;
+    p.H = (int)H;
+    p.D = (int)D;
+    p.causal = causal ? 1 : 0;
+    p.qscale = scale * 1.4426950408889634f;  // log2(e)
+    const unsigned z = (unsigned)(count * batch);
+    if (D == kD && vec) {
+        p.q_tiles = (int)((S + kBQ - 1) / kBQ);
+        hipLaunchKernelGGL(attention_d64, dim3((unsigned)p.q_tiles, (unsigned)H, z), dim3(256), 0, ctx->stream, p);
+        if (int rc = check_launch("attention_d64")) return rc;
+    } else {
+        hipLaunchKernelGGL(attention_rowwise, dim3(ceil_div(S * H, 256), 1, z), dim3(256), 0, ctx->stream, p);
+        if (int rc = check_launch("attention_rowwise")) return rc;
+    }
+    return ok();
+}
+
+}  // namespace
+}  // namespace lancius
+
+using namespace lancius;
+
+extern "C" {
+
+int lancius_hip_attention_f32(lancius_hip_ctx* ctx, float* out, const float* q, const float* k, const float* v,
+                              size_t batch, size_t S, size_t H, size_t D, int causal, float scale) {
+    float* o1[1] = {out};
+    const float* q1[1] = {q};
+    const float* k1[1] = {k};
+    const float* v1[1] = {v};
+    return attention_dispatch(ctx, 1, o1, q1, k1, v1, batch, S, H, D, causal, scale);
+}
+
+int lancius_hip_attention_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* out, const float* const* q,
+                                      const float* const* k, const float* const* v, size_t S, size_t H, size_t D,
+                                      int causal, float scale) {
+    return attention_dispatch(ctx, count, out, q, k, v, 1, S, H, D, causal, scale);
+}
+
+}  // extern "C"

@@ -1,0 +1,191 @@
+// Context, memory, timing and error entry points of liblancius_hip, plus the
+// host-pointer bridge kernel_matmul_f32 declared by the reference
+// (bleeding/v11A1/include/lancius/lancius_kernels.h:55).
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <mutex>
+
+#include "common.hpp"
+
+namespace lancius {
+
+static thread_local int t_status = 0;
+static thread_local char t_message[512] = "success";
+
+int set_error(int code, const char* fmt, ...) {
+    t_status = code;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(t_message, sizeof(t_message), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int ok() {
+    t_status = 0;
+    return 0;
+}
+
+int from_hip(hipError_t e, const char* what) {
+    int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? LANCIUS_HIP_ERR_OOM
+                                                                           : LANCIUS_HIP_ERR_INTERNAL;
+    return set_error(code, "%s: %s", what, hipGetErrorString(e));
+}
+
+int check_launch(const char* kernel) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return from_hip(e, kernel);
+    return 0;
+}
+
+int bind_device(lancius_hip_ctx* ctx) {
+    int cur = -1;
+    LANCIUS_HIP_TRY(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != ctx->device) LANCIUS_HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");
+    return 0;
+}
+
+}  // namespace lancius
+
+using namespace lancius;
+
+extern "C" {
+
+const char* lancius_hip_last_error(void) { return t_message; }
+int lancius_hip_last_status(void) { return t_status; }
+
+int lancius_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+int lancius_hip_ctx_create(int device, void* stream, lancius_hip_ctx** out) {
+    LANCIUS_REQUIRE(out != nullptr, LANCIUS_HIP_ERR_NULL_PTR, "ctx_create: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    LANCIUS_HIP_TRY(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    LANCIUS_REQUIRE(device >= 0 && device < n, LANCIUS_HIP_ERR_SHAPE, "ctx_create: device %d of %d", device, n);
+    LANCIUS_HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    lancius_hip_ctx* c = (lancius_hip_ctx*)calloc(1, sizeof(lancius_hip_ctx));
+    LANCIUS_REQUIRE(c != nullptr, LANCIUS_HIP_ERR_OOM, "ctx_create: host allocation failed");
+    c->device = device;
+    c->stream = (hipStream_t)stream;
+    hipError_t e = hipEventCreate(&c->ev_start);
+    if (e == hipSuccess) e = hipEventCreate(&c->ev_stop);
+    if (e != hipSuccess) {
+        free(c);
+        return from_hip(e, "hipEventCreate");
+    }
+    *out = c;
+    return ok();
+}
+
+void lancius_hip_ctx_destroy(lancius_hip_ctx* ctx) {
+    if (!ctx) return;
+    (void)bind_device(ctx);
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipEventDestroy(ctx->ev_start);
+    (void)hipEventDestroy(ctx->ev_stop);
+    free(ctx);
+}
+
+int lancius_hip_malloc(lancius_hip_ctx* ctx, void** device_ptr, size_t bytes) {
+    LANCIUS_REQUIRE(ctx && device_ptr, LANCIUS_HIP_ERR_NULL_PTR, "malloc: NULL argument");
+    *device_ptr = nullptr;
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipMalloc(device_ptr, bytes ? bytes : 1), "hipMalloc");
+    return ok();
+}
+
+int lancius_hip_free(lancius_hip_ctx* ctx, void* device_ptr) {
+    LANCIUS_REQUIRE(ctx, LANCIUS_HIP_ERR_NULL_PTR, "free: NULL context");
+    if (!device_ptr) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    LANCIUS_HIP_TRY(hipFree(device_ptr), "hipFree");
+    return ok();
+}
+
+int lancius_hip_upload(lancius_hip_ctx* ctx, void* device_dst, const void* host_src, size_t bytes) {
+    LANCIUS_REQUIRE(ctx && device_dst && host_src, LANCIUS_HIP_ERR_NULL_PTR, "upload: NULL argument");
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipMemcpyAsync(device_dst, host_src, bytes, hipMemcpyHostToDevice, ctx->stream), "upload");
+    LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "upload sync");
+    return ok();
+}
+
+int lancius_hip_download(lancius_hip_ctx* ctx, void* host_dst, const void* device_src, size_t bytes) {
+    LANCIUS_REQUIRE(ctx && host_dst && device_src, LANCIUS_HIP_ERR_NULL_PTR, "download: NULL argument");
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipMemcpyAsync(host_dst, device_src, bytes, hipMemcpyDeviceToHost, ctx->stream), "download");
+    LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "download sync");
+    return ok();
+}
+
+int lancius_hip_synchronize(lancius_hip_ctx* ctx) {
+    LANCIUS_REQUIRE(ctx, LANCIUS_HIP_ERR_NULL_PTR, "synchronize: NULL context");
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return ok();
+}
+
+int lancius_hip_timer_start(lancius_hip_ctx* ctx) {
+    LANCIUS_REQUIRE(ctx, LANCIUS_HIP_ERR_NULL_PTR, "timer_start: NULL context");
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipEventRecord(ctx->ev_start, ctx->stream), "hipEventRecord");
+    ctx->timer_armed = 1;
+    return ok();
+}
+
+int lancius_hip_timer_stop(lancius_hip_ctx* ctx, float* elapsed_ms) {
+    LANCIUS_REQUIRE(ctx && elapsed_ms, LANCIUS_HIP_ERR_NULL_PTR, "timer_stop: NULL argument");
+    LANCIUS_REQUIRE(ctx->timer_armed, LANCIUS_HIP_ERR_UNSUPPORTED, "timer_stop without timer_start");
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipEventRecord(ctx->ev_stop, ctx->stream), "hipEventRecord");
+    LANCIUS_HIP_TRY(hipEventSynchronize(ctx->ev_stop), "hipEventSynchronize");
+    LANCIUS_HIP_TRY(hipEventElapsedTime(elapsed_ms, ctx->ev_start, ctx->ev_stop), "hipEventElapsedTime");
+    ctx->timer_armed = 0;
+    return ok();
+}
+
+// ---- reference-ABI bridge: host pointers in, host pointers out ----------
+
+static std::mutex g_bridge_mu;
+static lancius_hip_ctx* g_bridge_ctx = nullptr;
+static void* g_bridge_buf = nullptr;
+static size_t g_bridge_cap = 0;
+
+void kernel_matmul_f32(float* out, const float* a, const float* b, size_t M, size_t K, size_t N) {
+    if (!out || !a || !b) {
+        set_error(LANCIUS_HIP_ERR_NULL_PTR, "kernel_matmul_f32: NULL argument");
+        return;
+    }
+    std::lock_guard<std::mutex> lock(g_bridge_mu);
+    if (!g_bridge_ctx && lancius_hip_ctx_create(0, nullptr, &g_bridge_ctx) != 0) return;
+    const size_t ea = M * K, eb = K * N, ec = M * N;
+    const size_t bytes = (ea + eb + ec) * sizeof(float) + 3 * 256;
+    if (bytes > g_bridge_cap) {
+        if (g_bridge_buf) lancius_hip_free(g_bridge_ctx, g_bridge_buf);
+        g_bridge_buf = nullptr;
+        g_bridge_cap = 0;
+        if (lancius_hip_malloc(g_bridge_ctx, &g_bridge_buf, bytes) != 0) return;
+        g_bridge_cap = bytes;
+    }
+    auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    char* base = (char*)g_bridge_buf;
+    float* dA = (float*)base;
+    float* dB = (float*)(base + align(ea * sizeof(float)));
+    float* dC = (float*)(base + align(ea * sizeof(float)) + align(eb * sizeof(float)));
+    if (lancius_hip_upload(g_bridge_ctx, dA, a, ea * sizeof(float)) != 0) return;
+    if (lancius_hip_upload(g_bridge_ctx, dB, b, eb * sizeof(float)) != 0) return;
+    if (lancius_hip_gemm_f32(g_bridge_ctx, dC, dA, dB, M, K, N, nullptr, LANCIUS_HIP_ACT_NONE, nullptr) != 0) return;
+    (void)lancius_hip_download(g_bridge_ctx, out, dC, ec * sizeof(float));
+}
+
+}  // extern "C"

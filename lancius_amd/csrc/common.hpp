@@ -1,0 +1,50 @@
+// Internal helpers shared by the HIP translation units of liblancius_hip.
+// Nothing here is visible through the public C headers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "lancius_hip.h"
+
+struct lancius_hip_ctx {
+    int device;
+    hipStream_t stream;
+    hipEvent_t ev_start;
+    hipEvent_t ev_stop;
+    int timer_armed;
+};
+
+namespace lancius {
+
+// Records a failure in the thread-local status/message and returns the code.
+int set_error(int code, const char* fmt, ...);
+// Clears the thread-local status and returns 0.
+int ok();
+// Maps a HIP error to a status (OOM -> -1, everything else -> -10).
+int from_hip(hipError_t e, const char* what);
+
+// Checks a kernel launch: reads hipGetLastError() after <<<>>>.
+int check_launch(const char* kernel);
+
+// Makes `ctx->device` current for the calling thread.
+int bind_device(lancius_hip_ctx* ctx);
+
+static inline unsigned int ceil_div(size_t a, size_t b) { return (unsigned int)((a + b - 1) / b); }
+
+// Largest grid dimension we launch in x (hardware limit is 2^32-1 work-items).
+constexpr size_t kMaxGridX = (size_t)1 << 30;
+
+}  // namespace lancius
+
+#define LANCIUS_REQUIRE(cond, code, ...)                                  \
+    do {                                                                  \
+        if (!(cond)) return ::lancius::set_error((code), __VA_ARGS__);    \
+    } while (0)
+
+#define LANCIUS_HIP_TRY(expr, what)                                       \
+    do {                                                                  \
+        hipError_t _e = (expr);                                           \
+        if (_e != hipSuccess) return ::lancius::from_hip(_e, (what));     \
+    } while (0)

@@ -1,0 +1,288 @@
+// fp32 GEMM on the gfx950 matrix cores: C[M,N] = epilogue(A[M,K] . B[K,N]),
+// row-major, no transposes - the layout of the graph MATMUL node
+// (bleeding/v11A1/src/runtime/lancius_scheduler.c:222-234, which reads
+// M = a.shape[0], K = a.shape[1], N = b.shape[1]).
+//
+// Design:
+//  * 256 threads = 4 wave64s arranged WGM x WGN; each wave owns a
+//    (BM/WGM) x (BN/WGN) block of C held in v_mfma_f32_32x32x2_f32
+//    accumulators (16 fp32 per lane per 32x32 sub-tile).
+//  * A and B tiles are staged in LDS in k-major order (A is transposed on the
+//    way in), so the MFMA operand of lane l - element (row l%32, k l/32) - is
+//    one conflict-free 32-float row segment.  Two LDS buffers: the global loads
+//    of tile k+1 are issued before the MFMAs of tile k and written to the other
+//    buffer after them, one barrier per k-tile.
+//  * The epilogue adds bias[n], applies ReLU/GELU and adds a residual before
+//    the single store of C (the BROADCAST + ADD + activation nodes of a graph).
+//  * Workgroup ids are renumbered XCD-contiguously and rastered in groups of
+//    tile-rows so that each XCD's L2 sees a compact set of A/B panels.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lancius {
+namespace {
+
+struct GemmParams {
+    float* C[LANCIUS_HIP_MAX_GROUP];
+    const float* A[LANCIUS_HIP_MAX_GROUP];
+    const float* R[LANCIUS_HIP_MAX_GROUP];     // residuals (may be null)
+    const float* B[LANCIUS_HIP_MAX_GROUP];
+    const float* bias[LANCIUS_HIP_MAX_GROUP];  // may be null
+    int M, N, K;
+    int act;
+    uint32_t tiles_m, tiles_n;
+};
+
+constexpr int kThreads = 256;
+
+template <int BM, int BN, int BK, int WGM, int WGN, bool VEC>
+__global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
+    static_assert(WGM * WGN == 4, "4 waves per workgroup");
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "wave tile is a multiple of 32");
+    static_assert(BK % 4 == 0, "BK multiple of 4");
+    constexpr int LDA = BM + 4;  // As[k][m]
+    constexpr int LDB = BN + 4;  // Bs[k][n]
+    __shared__ __attribute__((aligned(16))) float As[2][BK][LDA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LDB];
+
+    const int g = blockIdx.z;
+    const float* __restrict__ A = p.A[g];
+    const float* __restrict__ B = p.B[g];
+    float* __restrict__ C = p.C[g];
+    const float* __restrict__ R = p.R[g];
+    const int M = p.M, N = p.N, K = p.K;
+
+    const uint32_t ntiles = p.tiles_m * p.tiles_n;
+    uint32_t tm_id, tn_id;
+    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
+    const int m0 = (int)tm_id * BM;
+    const int n0 = (int)tn_id * BN;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    // ---- global -> register staging -------------------------------------
+    constexpr int A_VEC = VEC ? (BM * BK / 4) / kThreads : 0;
+    constexpr int B_VEC = VEC ? (BK * BN / 4) / kThreads : 0;
+    constexpr int A_SCL = VEC ? 0 : (BM * BK) / kThreads;
+    constexpr int B_SCL = VEC ? 0 : (BK * BN) / kThreads;
+    static_assert(!VEC || (A_VEC * kThreads * 4 == BM * BK && B_VEC * kThreads * 4 == BK * BN), "even split");
+    static_assert(VEC || (A_SCL * kThreads == BM * BK && B_SCL * kThreads == BK * BN), "even split");
+    f32x4 a_v[A_VEC > 0 ? A_VEC : 1];
+    f32x4 b_v[B_VEC > 0 ? B_VEC : 1];
+    float a_s[A_SCL > 0 ? A_SCL : 1];
+    float b_s[B_SCL > 0 ? B_SCL : 1];
+
+    auto load_tile = [&](int k0) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < A_VEC; ++i) {
+                const int idx = tid + i * kThreads;
+                const int r = idx / (BK / 4), kq = idx % (BK / 4);
+                const int gm = m0 + r, gk = k0 + 4 * kq;
+                a_v[i] = (gm < M && gk < K) ? *(const f32x4*)(A + (size_t)gm * K + gk) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int i = 0; i < B_VEC; ++i) {
+                const int idx = tid + i * kThreads;
+                const int kr = idx / (BN / 4), nq = idx % (BN / 4);
+                const int gk = k0 + kr, gn = n0 + 4 * nq;
+                b_v[i] = (gk < K && gn < N) ? *(const f32x4*)(B + (size_t)gk * N + gn) : f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_SCL; ++i) {
+                const int idx = tid + i * kThreads;
+                const int r = idx / BK, kk = idx % BK;
+                const int gm = m0 + r, gk = k0 + kk;
+                a_s[i] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < B_SCL; ++i) {
+                const int idx = tid + i * kThreads;
+                const int kr = idx / BN, n = idx % BN;
+                const int gk = k0 + kr, gn = n0 + n;
+                b_s[i] = (gk < K && gn < N) ? B[(size_t)gk * N + gn] : 0.0f;
+            }
+        }
+    };
+
+    auto store_tile = [&](int buf) {
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < A_VEC; ++i) {
+                const int idx = tid + i * kThreads;
+                const int r = idx / (BK / 4), kq = idx % (BK / 4);
+                As[buf][4 * kq + 0][r] = a_v[i].x;
+                As[buf][4 * kq + 1][r] = a_v[i].y;
+                As[buf][4 * kq + 2][r] = a_v[i].z;
+                As[buf][4 * kq + 3][r] = a_v[i].w;
+            }
+#pragma unroll
+            for (int i = 0; i < B_VEC; ++i) {
+                const int idx = tid + i * kThreads;
+                const int kr = idx / (BN / 4), nq = idx % (BN / 4);
+                *(f32x4*)&Bs[buf][kr][4 * nq] = b_v[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_SCL; ++i) {
+                const int idx = tid + i * kThreads;
+                As[buf][idx % BK][idx / BK] = a_s[i];
+            }
+#pragma unroll
+            for (int i = 0; i < B_SCL; ++i) {
+                const int idx = tid + i * kThreads;
+                Bs[buf][idx / BN][idx % BN] = b_s[i];
+            }
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const int ktiles = (K + BK - 1) / BK;
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) load_tile((kt + 1) * BK);
+#pragma unroll
+        for (int kp = 0; kp < BK / 2; ++kp) {
+            float af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) af[i] = As[cur][2 * kp + lk][wm * WM + i * 32 + lr];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = Bs[cur][2 * kp + lk][wn * WN + j * 32 + lr];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) store_tile(cur ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue: bias, activation, residual, one store -----------------
+    // Accumulator layout of v_mfma_f32_32x32x2_f32: register r of lane l holds
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 sub-tile.
+    const float* __restrict__ bias = p.bias[g];
+    const int act = p.act;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lr;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + 8 * (r >> 2) + (r & 3);
+                if (row < M) {
+                    float v = acc[i][j][r] + bv;
+                    v = apply_act(v, act);
+                    const size_t o = (size_t)row * N + col;
+                    if (R) v += R[o];
+                    C[o] = v;
+                }
+            }
+        }
+    }
+}
+
+struct TileCfg {
+    int bm, bn;
+};
+
+template <int BM, int BN, int BK, int WGM, int WGN>
+int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
+    p.tiles_m = (uint32_t)((p.M + BM - 1) / BM);
+    p.tiles_n = (uint32_t)((p.N + BN - 1) / BN);
+    dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)count);
+    if (vec)
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true>), grid, dim3(kThreads), 0, ctx->stream, p);
+    else
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false>), grid, dim3(kThreads), 0, ctx->stream, p);
+    return check_launch("gemm_f32_mfma");
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
+                  const float* const* B, size_t M, size_t K, size_t N, const float* const* bias, int act,
+                  const float* const* residual) {
+    LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm: NULL argument");
+    LANCIUS_REQUIRE(count >= 1 && count <= LANCIUS_HIP_MAX_GROUP, LANCIUS_HIP_ERR_SHAPE, "gemm: group count %zu",
+                    count);
+    LANCIUS_REQUIRE(M > 0 && N > 0 && K > 0, LANCIUS_HIP_ERR_SHAPE, "gemm: empty shape M=%zu K=%zu N=%zu", M, K, N);
+    LANCIUS_REQUIRE(M < (1u << 30) && N < (1u << 30) && K < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
+                    "gemm: dimension too large");
+    LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_GELU, LANCIUS_HIP_ERR_UNSUPPORTED,
+                    "gemm: activation %d", act);
+    if (int rc = bind_device(ctx)) return rc;
+
+    GemmParams p{};
+    bool vec = (K % 4 == 0) && (N % 4 == 0);
+    for (size_t g = 0; g < count; ++g) {
+        LANCIUS_REQUIRE(C[g] && A[g] && B[g], LANCIUS_HIP_ERR_NULL_PTR, "gemm: NULL operand in group %zu", g);
+        p.C[g] = C[g];
+        p.A[g] = A[g];
+        p.B[g] = B[g];
+        p.bias[g] = bias ? bias[g] : nullptr;
+        p.R[g] = residual ? residual[g] : nullptr;
+        vec = vec && aligned16(A[g]) && aligned16(B[g]);
+    }
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.act = act;
+
+    // Tile choice: the 128x128 tile when it yields enough workgroups to cover
+    // the 256 CUs, else 64x64.
+    const size_t big_tiles = count * ((M + 127) / 128) * ((N + 127) / 128);
+    int rc;
+    if (big_tiles >= 256)
+        rc = launch_cfg<128, 128, 16, 2, 2>(ctx, p, (int)count, vec);
+    else
+        rc = launch_cfg<64, 64, 16, 2, 2>(ctx, p, (int)count, vec);
+    return rc ? rc : ok();
+}
+
+}  // namespace
+}  // namespace lancius
+
+using namespace lancius;
+
+extern "C" {
+
+int lancius_hip_gemm_f32(lancius_hip_ctx* ctx, float* C, const float* A, const float* B, size_t M, size_t K,
+                         size_t N, const float* bias, int act, const float* residual) {
+    float* c1[1] = {C};
+    const float* a1[1] = {A};
+    const float* b1[1] = {B};
+    const float* s1[1] = {bias};
+    const float* r1[1] = {residual};
+    return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, s1, act, r1);
+}
+
+int lancius_hip_gemm_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
+                                 const float* const* B, size_t M, size_t K, size_t N, const float* const* bias,
+                                 int act, const float* const* residual) {
+    return gemm_dispatch(ctx, count, C, A, B, M, K, N, bias, act, residual);
+}
+
+}  // extern "C"

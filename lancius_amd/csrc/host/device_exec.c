@@ -1,0 +1,875 @@
+/*
+ * Device executor: compiles a scheduled Lancius graph into a launch list over
+ * one HBM arena and replays it through the lancius_hip_* C ABI.
+ * Replaces bleeding/v11A1/src/runtime/lancius_scheduler.c:61-520 (dispatch
+ * and executors) for the ops of the device path; see lancius_hip_graph.h.
+ */
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "lancius_hip_graph.h"
+
+#define NONE UINT32_MAX
+#define MAXG LANCIUS_HIP_MAX_GROUP
+#define ALIGN_DEV 256u
+
+typedef enum { L_GEMM, L_CONV, L_ATTN, L_LN, L_SOFTMAX, L_ADD, L_RELU, L_GELU, L_BCAST } lkind;
+
+enum { ROLE_NONE = 0, ROLE_INPUT, ROLE_CONST, ROLE_POOLED, ROLE_ALIAS, ROLE_FUSED };
+
+typedef struct {
+    uint32_t out;   /* node id written */
+    uint32_t in[4]; /* node ids read (alias roots), NONE when unused */
+} member_t;
+
+typedef struct {
+    lkind kind;
+    uint32_t wave, order;
+    uint32_t count;
+    member_t m[MAXG];
+    size_t d[9];
+    int act, causal, has_bias, has_res;
+} launch_t;
+
+struct lancius_device_program {
+    lancius_hip_ctx* ctx;
+    uint32_t n_ids;
+    char* arena;
+    char** ptr;
+    size_t* bytes;
+    uint8_t* role;
+    uint8_t* readable;
+    int32_t** argmax;
+    size_t* rows;
+    launch_t* launches;
+    uint32_t n_launches;
+    lancius_device_program_info info;
+};
+
+static size_t elems(const lancius_node* n) {
+    size_t e = 1;
+    for (uint8_t d = 0; d < n->ndim; d++) e *= n->shape[d];
+    return e;
+}
+
+static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+static int fail(int code, const char* what) {
+    fprintf(stderr, "[LANCIUS DEVICE] %s\n", what);
+    return code;
+}
+
+/* ---- compile-time scratch ---------------------------------------------------- */
+
+typedef struct {
+    const lancius_graph* g;
+    const lancius_node** node;  /* by id */
+    uint32_t* wave;             /* by id */
+    uint32_t* order;            /* by id: index inside its wave */
+    uint32_t* consumers;        /* by id */
+    uint32_t* sole;             /* by id: the consumer when consumers == 1 */
+    uint32_t* root;             /* by id: buffer owner through RESHAPE/FLATTEN */
+    uint8_t* absorbed;          /* by id: folded into a later node's GEMM */
+    uint32_t* chain_head;       /* by id of a chain's final node: its MATMUL */
+    uint32_t* chain_bias;       /* by final node: bias source (root) */
+    uint32_t* chain_res;        /* by final node: residual (root) */
+    int* chain_act;             /* by final node */
+} cstate;
+
+static void cstate_free(cstate* c) {
+    free(c->node);
+    free(c->wave);
+    free(c->order);
+    free(c->consumers);
+    free(c->sole);
+    free(c->root);
+    free(c->absorbed);
+    free(c->chain_head);
+    free(c->chain_bias);
+    free(c->chain_res);
+    free(c->chain_act);
+}
+
+static const lancius_node* other_operand(const lancius_node* add, uint32_t cur) {
+    if (add->input_count != 2 || !add->inputs[0] || !add->inputs[1]) return NULL;
+    if (add->inputs[0]->id == cur) return add->inputs[1];
+    if (add->inputs[1]->id == cur) return add->inputs[0];
+    return NULL;
+}
+
+/* MATMUL -> ADD(BROADCAST row) -> RELU|GELU -> ADD(residual), each link only
+ * when the intermediate has exactly one consumer; epilogue order matches the
+ * node order: ((acc + bias) -> act) + residual. */
+static void fuse_gemm_chain(cstate* c, const lancius_node* mm) {
+    const size_t M = mm->inputs[0]->shape[0], N = mm->inputs[1]->shape[1];
+    uint32_t cur = mm->id;
+    uint32_t bias = NONE, res = NONE;
+    int act = LANCIUS_HIP_ACT_NONE;
+    /* bias */
+    if (c->consumers[cur] == 1) {
+        const lancius_node* add = c->node[c->sole[cur]];
+        const lancius_node* o = add ? other_operand(add, cur) : NULL;
+        if (add && add->op == LANCIUS_OP_ADD && o && o->op == LANCIUS_OP_BROADCAST && c->consumers[o->id] == 1 &&
+            o->ndim == 2 && o->shape[0] == M && o->shape[1] == N && elems(add) == M * N && o->inputs[0] &&
+            elems(o->inputs[0]) >= N && elems(o->inputs[0]) != 1) {
+            bias = c->root[o->inputs[0]->id];
+            c->absorbed[cur] = 1;
+            c->absorbed[o->id] = 1;
+            cur = add->id;
+        }
+    }
+    /* activation */
+    if (c->consumers[cur] == 1) {
+        const lancius_node* a = c->node[c->sole[cur]];
+        if (a && (a->op == LANCIUS_OP_RELU || a->op == LANCIUS_OP_GELU) && elems(a) == M * N) {
+            act = a->op == LANCIUS_OP_RELU ? LANCIUS_HIP_ACT_RELU : LANCIUS_HIP_ACT_GELU;
+            c->absorbed[cur] = 1;
+            cur = a->id;
+        }
+    }
+    /* residual */
+    if (c->consumers[cur] == 1) {
+        const lancius_node* add = c->node[c->sole[cur]];
+        const lancius_node* o = add ? other_operand(add, cur) : NULL;
+        if (add && add->op == LANCIUS_OP_ADD && o && elems(add) == M * N && elems(o) >= M * N) {
+            res = c->root[o->id];
+            c->absorbed[cur] = 1;
+            cur = add->id;
+        }
+    }
+    if (cur != mm->id) {
+        c->chain_head[cur] = mm->id;
+        c->chain_bias[cur] = bias;
+        c->chain_res[cur] = res;
+        c->chain_act[cur] = act;
+    }
+}
+
+static int supported(lancius_opcode op) {
+    switch (op) {
+        case LANCIUS_OP_NOP:
+        case LANCIUS_OP_INPUT:
+        case LANCIUS_OP_CONST:
+        case LANCIUS_OP_MATMUL:
+        case LANCIUS_OP_ADD:
+        case LANCIUS_OP_BROADCAST:
+        case LANCIUS_OP_RELU:
+        case LANCIUS_OP_GELU:
+        case LANCIUS_OP_SOFTMAX:
+        case LANCIUS_OP_LAYERNORM:
+        case LANCIUS_OP_ATTENTION:
+        case LANCIUS_OP_CONV2D:
+        case LANCIUS_OP_CONV2D_RELU_FUSED:
+        case LANCIUS_OP_RESHAPE:
+        case LANCIUS_OP_FLATTEN:
+            return 1;
+        default:
+            return 0;
+    }
+}
+
+#define IN(n, j) ((n)->inputs[j] ? c->root[(n)->inputs[j]->id] : NONE)
+
+/* Builds the launch for final node `n`; checks the operand sizes the
+ * reference kernels would read. */
+static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
+    memset(L, 0, sizeof(*L));
+    L->wave = c->wave[n->id];
+    L->order = c->order[n->id];
+    L->count = 1;
+    member_t* m = &L->m[0];
+    m->out = n->id;
+    for (int j = 0; j < 4; j++) m->in[j] = NONE;
+    for (uint32_t j = 0; j < n->input_count; j++)
+        if (!n->inputs[j]) return fail(LANCIUS_HIP_ERR_NULL_PTR, "node with a NULL input");
+    const size_t e = elems(n);
+    const uint32_t head = c->chain_head[n->id];
+    if (head != NONE || n->op == LANCIUS_OP_MATMUL) {
+        const lancius_node* mm = head != NONE ? c->node[head] : n;
+        const lancius_node* a = mm->inputs[0];
+        const lancius_node* b = mm->inputs[1];
+        const size_t M = a->shape[0], K = a->shape[1], N = b->shape[1];
+        if (M * N > e || elems(a) < M * K || elems(b) < K * N || !M || !K || !N)
+            return fail(LANCIUS_HIP_ERR_SHAPE, "MATMUL operand shapes");
+        L->kind = L_GEMM;
+        L->d[0] = M;
+        L->d[1] = K;
+        L->d[2] = N;
+        m->in[0] = c->root[a->id];
+        m->in[1] = c->root[b->id];
+        if (head != NONE) {
+            m->in[2] = c->chain_bias[n->id];
+            m->in[3] = c->chain_res[n->id];
+            L->act = c->chain_act[n->id];
+        }
+        L->has_bias = m->in[2] != NONE;
+        L->has_res = m->in[3] != NONE;
+        return 0;
+    }
+    switch (n->op) {
+        case LANCIUS_OP_ADD:
+            if (elems(n->inputs[0]) < e || elems(n->inputs[1]) < e) return fail(LANCIUS_HIP_ERR_SHAPE, "ADD sizes");
+            L->kind = L_ADD;
+            L->d[0] = e;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            return 0;
+        case LANCIUS_OP_RELU:
+        case LANCIUS_OP_GELU:
+            if (elems(n->inputs[0]) < e) return fail(LANCIUS_HIP_ERR_SHAPE, "unary sizes");
+            L->kind = n->op == LANCIUS_OP_RELU ? L_RELU : L_GELU;
+            L->d[0] = e;
+            m->in[0] = IN(n, 0);
+            return 0;
+        case LANCIUS_OP_BROADCAST: {
+            const size_t in_e = elems(n->inputs[0]);
+            L->kind = L_BCAST;
+            if (in_e == 1) { /* scalar: every element (lancius_scheduler.c:271-273) */
+                L->d[0] = e;
+                L->d[1] = 1;
+                L->d[2] = 1;
+            } else { /* rows x cols of the 2-D view (:275-276) */
+                if (n->ndim < 2 || in_e < n->shape[1]) return fail(LANCIUS_HIP_ERR_SHAPE, "BROADCAST sizes");
+                L->d[0] = n->shape[0];
+                L->d[1] = n->shape[1];
+                L->d[2] = in_e;
+            }
+            m->in[0] = IN(n, 0);
+            return 0;
+        }
+        case LANCIUS_OP_SOFTMAX:
+            if (n->ndim != 2 || elems(n->inputs[0]) < e) return fail(LANCIUS_HIP_ERR_SHAPE, "SOFTMAX sizes");
+            L->kind = L_SOFTMAX;
+            L->d[0] = n->shape[0];
+            L->d[1] = n->shape[1];
+            m->in[0] = IN(n, 0);
+            return 0;
+        case LANCIUS_OP_LAYERNORM: {
+            /* rows = shape[0], hidden = shape[1] (lancius_scheduler.c:114) */
+            const size_t rows = n->shape[0], hid = n->ndim > 1 ? n->shape[1] : 1;
+            if (elems(n->inputs[0]) < rows * hid || elems(n->inputs[1]) < hid || elems(n->inputs[2]) < hid)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "LAYERNORM sizes");
+            L->kind = L_LN;
+            L->d[0] = rows;
+            L->d[1] = hid;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            m->in[2] = IN(n, 2);
+            return 0;
+        }
+        case LANCIUS_OP_ATTENTION: {
+            const size_t S = n->shape[0], H = n->shape[1], D = n->shape[2];
+            const size_t need = S * H * D;
+            if (n->ndim != 3 || !need || elems(n->inputs[0]) < need || elems(n->inputs[1]) < need ||
+                elems(n->inputs[2]) < need)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "ATTENTION sizes");
+            L->kind = L_ATTN;
+            L->d[0] = S;
+            L->d[1] = H;
+            L->d[2] = D;
+            L->causal = n->axes[0] != 1;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            m->in[2] = IN(n, 2);
+            return 0;
+        }
+        case LANCIUS_OP_CONV2D:
+        case LANCIUS_OP_CONV2D_RELU_FUSED: {
+            const lancius_node* x = n->inputs[0];
+            const lancius_node* w = n->inputs[1];
+            if (x->ndim != 4 || w->ndim != 4 || w->shape[1] != x->shape[1] || n->stride == 0 ||
+                x->shape[2] + 2 * (size_t)n->pad < w->shape[2] || x->shape[3] + 2 * (size_t)n->pad < w->shape[3])
+                return fail(LANCIUS_HIP_ERR_SHAPE, "CONV2D shapes");
+            const size_t Ho = (x->shape[2] + 2 * (size_t)n->pad - w->shape[2]) / n->stride + 1;
+            const size_t Wo = (x->shape[3] + 2 * (size_t)n->pad - w->shape[3]) / n->stride + 1;
+            if (x->shape[0] * w->shape[0] * Ho * Wo > e) return fail(LANCIUS_HIP_ERR_SHAPE, "CONV2D output size");
+            L->kind = L_CONV;
+            L->d[0] = x->shape[0];
+            L->d[1] = x->shape[1];
+            L->d[2] = x->shape[2];
+            L->d[3] = x->shape[3];
+            L->d[4] = w->shape[0];
+            L->d[5] = w->shape[2];
+            L->d[6] = w->shape[3];
+            L->d[7] = n->stride;
+            L->d[8] = n->pad;
+            L->act = n->op == LANCIUS_OP_CONV2D_RELU_FUSED ? LANCIUS_HIP_ACT_RELU : LANCIUS_HIP_ACT_NONE;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            return 0;
+        }
+        default:
+            return fail(LANCIUS_HIP_ERR_UNSUPPORTED, "op outside the device path");
+    }
+}
+
+static int same_group(const launch_t* a, const launch_t* b) {
+    if (a->kind != b->kind || a->wave != b->wave || a->count >= MAXG) return 0;
+    if (a->kind == L_GEMM)
+        return a->d[0] == b->d[0] && a->d[1] == b->d[1] && a->d[2] == b->d[2] && a->act == b->act &&
+               a->has_bias == b->has_bias && a->has_res == b->has_res;
+    if (a->kind == L_ATTN)
+        return a->d[0] == b->d[0] && a->d[1] == b->d[1] && a->d[2] == b->d[2] && a->causal == b->causal;
+    return 0;
+}
+
+static int cmp_launch(const void* x, const void* y) {
+    const launch_t* a = (const launch_t*)x;
+    const launch_t* b = (const launch_t*)y;
+    if (a->wave != b->wave) return a->wave < b->wave ? -1 : 1;
+    if (a->order != b->order) return a->order < b->order ? -1 : 1;
+    return 0;
+}
+
+/* ---- planning over the launch list --------------------------------------------- */
+
+typedef struct {
+    uint32_t id, birth, death;
+    size_t size, offset;
+} ivl_t;
+
+typedef struct fblk {
+    size_t off, size;
+    struct fblk* next;
+} fblk;
+
+/* First fit over a LIFO free list, no coalescing, blocks split from the front
+ * (the scan of lancius_memory_planner.c:117-168 with each interval's offset
+ * kept).  Returns the region size, or SIZE_MAX on allocation failure. */
+static size_t first_fit(ivl_t* iv, uint32_t n) {
+    ivl_t** active = (ivl_t**)malloc(sizeof(ivl_t*) * (n ? n : 1));
+    fblk* fl = (fblk*)malloc(sizeof(fblk));
+    if (!active || !fl) {
+        free(active);
+        free(fl);
+        return SIZE_MAX;
+    }
+    fl->off = 0;
+    fl->size = SIZE_MAX;
+    fl->next = NULL;
+    size_t peak = 0;
+    uint32_t na = 0;
+    size_t result = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        ivl_t* cur = &iv[i];
+        uint32_t keep = 0;
+        for (uint32_t a = 0; a < na; a++) {
+            if (active[a]->death < cur->birth) {
+                fblk* b = (fblk*)malloc(sizeof(fblk));
+                if (!b) {
+                    result = SIZE_MAX;
+                    goto done;
+                }
+                b->off = active[a]->offset;
+                b->size = active[a]->size;
+                b->next = fl;
+                fl = b;
+            } else {
+                active[keep++] = active[a];
+            }
+        }
+        na = keep;
+        fblk *prev = NULL, *b = fl;
+        while (b && b->size < cur->size) {
+            prev = b;
+            b = b->next;
+        }
+        if (!b) {
+            result = SIZE_MAX;
+            goto done;
+        }
+        cur->offset = b->off;
+        if (b->size > cur->size) {
+            b->off += cur->size;
+            b->size -= cur->size;
+        } else {
+            if (prev) prev->next = b->next;
+            else fl = b->next;
+            free(b);
+        }
+        if (cur->offset + cur->size > peak) peak = cur->offset + cur->size;
+        active[na++] = cur;
+    }
+    result = peak;
+done:
+    while (fl) {
+        fblk* nx = fl->next;
+        free(fl);
+        fl = nx;
+    }
+    free(active);
+    return result;
+}
+
+static int caller_plan_fits(const lancius_memory_plan* plan, const ivl_t* iv, uint32_t n, uint32_t n_ids,
+                            size_t* region) {
+    size_t top = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if (iv[i].id >= n_ids || !plan->is_pooled[iv[i].id]) return 0;
+        const size_t off = plan->offsets[iv[i].id];
+        if (off > SIZE_MAX - iv[i].size) return 0;
+        if (off + iv[i].size > top) top = off + iv[i].size;
+    }
+    for (uint32_t i = 0; i < n; i++) {
+        const size_t ai = plan->offsets[iv[i].id], bi = ai + iv[i].size;
+        for (uint32_t j = i + 1; j < n; j++) {
+            if (iv[i].birth > iv[j].death || iv[j].birth > iv[i].death) continue; /* not live together */
+            const size_t aj = plan->offsets[iv[j].id], bj = aj + iv[j].size;
+            if (ai < bj && aj < bi) return 0;
+        }
+    }
+    *region = top;
+    return 1;
+}
+
+static int cmp_ivl_birth(const void* x, const void* y) {
+    const ivl_t* a = (const ivl_t*)x;
+    const ivl_t* b = (const ivl_t*)y;
+    if (a->birth != b->birth) return a->birth < b->birth ? -1 : 1;
+    return 0;
+}
+
+/* ---- program ------------------------------------------------------------------------ */
+
+void lancius_device_program_destroy(lancius_device_program* p) {
+    if (!p) return;
+    if (p->arena) lancius_hip_free(p->ctx, p->arena);
+    free(p->ptr);
+    free(p->bytes);
+    free(p->role);
+    free(p->readable);
+    free(p->argmax);
+    free(p->rows);
+    free(p->launches);
+    free(p);
+}
+
+int lancius_device_program_info_get(const lancius_device_program* p, lancius_device_program_info* info) {
+    if (!p || !info) return LANCIUS_HIP_ERR_NULL_PTR;
+    *info = p->info;
+    return 0;
+}
+
+#define CALLOC(ptr, n) ((ptr) = calloc((n) ? (n) : 1, sizeof(*(ptr))))
+
+int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, const lancius_schedule* sched,
+                                  const lancius_memory_plan* plan, uint32_t flags, lancius_device_program** out) {
+    if (!ctx || !g || !sched || !out) return LANCIUS_HIP_ERR_NULL_PTR;
+    *out = NULL;
+    if (flags & LANCIUS_DEVICE_KEEP_ALL) flags |= LANCIUS_DEVICE_NO_FUSION;
+    const uint32_t ids = g->next_id;
+    int rc = 0;
+    cstate c;
+    memset(&c, 0, sizeof(c));
+    c.g = g;
+    lancius_device_program* p = (lancius_device_program*)calloc(1, sizeof(*p));
+    ivl_t* iv = NULL;
+    uint32_t* birth = NULL;
+    uint32_t* last = NULL;
+    uint8_t* pinned = NULL;
+    float* fillbuf = NULL;
+    if (!p) return LANCIUS_HIP_ERR_OOM;
+    p->ctx = ctx;
+    p->n_ids = ids;
+    if (!CALLOC(c.node, ids) || !CALLOC(c.wave, ids) || !CALLOC(c.order, ids) || !CALLOC(c.consumers, ids) ||
+        !CALLOC(c.sole, ids) || !CALLOC(c.root, ids) || !CALLOC(c.absorbed, ids) || !CALLOC(c.chain_head, ids) ||
+        !CALLOC(c.chain_bias, ids) || !CALLOC(c.chain_res, ids) || !CALLOC(c.chain_act, ids) ||
+        !CALLOC(p->ptr, ids) || !CALLOC(p->bytes, ids) || !CALLOC(p->role, ids) || !CALLOC(p->readable, ids) ||
+        !CALLOC(p->argmax, ids) || !CALLOC(p->rows, ids) || !CALLOC(birth, ids) || !CALLOC(last, ids) ||
+        !CALLOC(pinned, ids)) {
+        rc = LANCIUS_HIP_ERR_OOM;
+        goto out;
+    }
+    for (uint32_t i = 0; i < ids; i++) {
+        c.wave[i] = NONE;
+        c.chain_head[i] = NONE;
+        c.root[i] = i;
+        birth[i] = NONE;
+    }
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        if (n->id >= ids) {
+            rc = fail(LANCIUS_HIP_ERR_SHAPE, "node id beyond graph next_id");
+            goto out;
+        }
+        c.node[n->id] = n;
+        p->bytes[n->id] = elems(n) * sizeof(float);
+        if (!supported(n->op)) {
+            fprintf(stderr, "[LANCIUS DEVICE] op %d (node %u) is not on the device path\n", (int)n->op, n->id);
+            rc = LANCIUS_HIP_ERR_UNSUPPORTED;
+            goto out;
+        }
+        for (uint32_t j = 0; j < n->input_count; j++) {
+            if (!n->inputs[j]) continue;
+            const uint32_t in = n->inputs[j]->id;
+            if (in >= ids) {
+                rc = fail(LANCIUS_HIP_ERR_SHAPE, "input id beyond graph next_id");
+                goto out;
+            }
+            c.consumers[in]++;
+            c.sole[in] = n->id;
+        }
+    }
+    uint32_t scheduled = 0;
+    for (uint32_t w = 0; w < sched->wave_count; w++)
+        for (uint32_t i = 0; i < sched->waves[w].node_count; i++) {
+            const lancius_node* n = sched->waves[w].nodes[i];
+            if (n->id >= ids || c.node[n->id] != n) {
+                rc = fail(LANCIUS_HIP_ERR_SHAPE, "schedule holds a node of another graph");
+                goto out;
+            }
+            c.wave[n->id] = w;
+            c.order[n->id] = i;
+            scheduled++;
+        }
+    if (scheduled != g->node_count) {
+        rc = fail(LANCIUS_HIP_ERR_SHAPE, "schedule does not cover the graph (cycle?)");
+        goto out;
+    }
+
+    /* roles and aliases, in wave order so an alias's input is resolved first */
+    for (uint32_t w = 0; w < sched->wave_count; w++)
+        for (uint32_t i = 0; i < sched->waves[w].node_count; i++) {
+            const lancius_node* n = sched->waves[w].nodes[i];
+            if (n->op == LANCIUS_OP_INPUT) {
+                p->role[n->id] = ROLE_INPUT;
+            } else if (n->op == LANCIUS_OP_CONST) {
+                p->role[n->id] = ROLE_CONST;
+            } else if (n->op == LANCIUS_OP_NOP) {
+                p->role[n->id] = ROLE_NONE;
+            } else if (n->op == LANCIUS_OP_RESHAPE || n->op == LANCIUS_OP_FLATTEN) {
+                if (!n->inputs || !n->inputs[0]) {
+                    rc = fail(LANCIUS_HIP_ERR_NULL_PTR, "RESHAPE without input");
+                    goto out;
+                }
+                const uint32_t r = c.root[n->inputs[0]->id];
+                if (elems(n) > elems(c.node[r])) {
+                    rc = fail(LANCIUS_HIP_ERR_SHAPE, "RESHAPE larger than its input");
+                    goto out;
+                }
+                c.root[n->id] = r;
+                p->role[n->id] = ROLE_ALIAS;
+            }
+        }
+
+    if (!(flags & LANCIUS_DEVICE_NO_FUSION))
+        for (uint32_t w = 0; w < sched->wave_count; w++)
+            for (uint32_t i = 0; i < sched->waves[w].node_count; i++) {
+                const lancius_node* n = sched->waves[w].nodes[i];
+                if (n->op == LANCIUS_OP_MATMUL && !c.absorbed[n->id] && n->inputs && n->inputs[0] && n->inputs[1])
+                    fuse_gemm_chain(&c, n);
+            }
+
+    /* launches, one per final node, sorted by (wave, position) */
+    p->launches = (launch_t*)calloc(g->node_count ? g->node_count : 1, sizeof(launch_t));
+    if (!p->launches) {
+        rc = LANCIUS_HIP_ERR_OOM;
+        goto out;
+    }
+    uint32_t nl = 0;
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        const uint8_t role = p->role[n->id];
+        if (role == ROLE_INPUT || role == ROLE_CONST || role == ROLE_ALIAS || n->op == LANCIUS_OP_NOP) continue;
+        if (c.absorbed[n->id]) {
+            p->role[n->id] = ROLE_FUSED;
+            p->info.fused_nodes++;
+            continue;
+        }
+        if ((rc = make_launch(&c, n, &p->launches[nl]))) goto out;
+        p->role[n->id] = ROLE_POOLED;
+        nl++;
+    }
+    qsort(p->launches, nl, sizeof(launch_t), cmp_launch);
+    /* merge branches of one wave */
+    if (!(flags & (LANCIUS_DEVICE_NO_FUSION | LANCIUS_DEVICE_NO_GROUP))) {
+        uint32_t k = 0;
+        for (uint32_t i = 0; i < nl; i++) {
+            int merged = 0;
+            for (uint32_t j = k; j-- > 0;) {
+                if (p->launches[j].wave != p->launches[i].wave) break;
+                if (same_group(&p->launches[j], &p->launches[i])) {
+                    p->launches[j].m[p->launches[j].count++] = p->launches[i].m[0];
+                    merged = 1;
+                    break;
+                }
+            }
+            if (!merged) p->launches[k++] = p->launches[i];
+        }
+        nl = k;
+    }
+    p->n_launches = nl;
+    p->info.launches = nl;
+
+    /* lifetimes over launch steps */
+    for (uint32_t s = 0; s < nl; s++) {
+        const launch_t* L = &p->launches[s];
+        for (uint32_t k = 0; k < L->count; k++) {
+            birth[L->m[k].out] = s;
+            if (last[L->m[k].out] < s) last[L->m[k].out] = s;
+            for (int j = 0; j < 4; j++) {
+                const uint32_t r = L->m[k].in[j];
+                if (r != NONE && last[r] < s) last[r] = s;
+            }
+        }
+    }
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        if (p->role[n->id] == ROLE_ALIAS) p->info.aliased_nodes++;
+        const int sink = c.consumers[n->id] == 0 && n->op != LANCIUS_OP_NOP;
+        if (sink || (flags & LANCIUS_DEVICE_KEEP_ALL)) {
+            pinned[c.root[n->id]] = 1;
+            p->readable[n->id] = p->role[n->id] != ROLE_FUSED && p->role[n->id] != ROLE_NONE;
+        }
+        if (p->role[n->id] == ROLE_INPUT || p->role[n->id] == ROLE_CONST) p->readable[n->id] = 1;
+    }
+    iv = (ivl_t*)calloc(nl * MAXG + 1, sizeof(ivl_t));
+    if (!iv) {
+        rc = LANCIUS_HIP_ERR_OOM;
+        goto out;
+    }
+    uint32_t niv = 0;
+    for (uint32_t i = 0; i < g->node_count; i++) { /* graph order, then stable by birth */
+        const uint32_t id = g->nodes[i]->id;
+        if (p->role[id] != ROLE_POOLED) continue;
+        iv[niv].id = id;
+        iv[niv].birth = birth[id];
+        iv[niv].death = pinned[id] ? UINT32_MAX - 1 : last[id];
+        iv[niv].size = align_up(p->bytes[id] ? p->bytes[id] : 1, 32);
+        niv++;
+    }
+    /* insertion sort keeps graph order among equal births */
+    for (uint32_t i = 1; i < niv; i++) {
+        ivl_t key = iv[i];
+        uint32_t j = i;
+        while (j > 0 && cmp_ivl_birth(&iv[j - 1], &key) > 0) {
+            iv[j] = iv[j - 1];
+            j--;
+        }
+        iv[j] = key;
+    }
+    size_t region = 0;
+    if (plan && plan->offsets && plan->is_pooled && caller_plan_fits(plan, iv, niv, ids, &region)) {
+        for (uint32_t i = 0; i < niv; i++) iv[i].offset = plan->offsets[iv[i].id];
+        p->info.used_caller_plan = 1;
+    } else {
+        p->info.replanned = plan != NULL;
+        region = first_fit(iv, niv);
+        if (region == SIZE_MAX) {
+            rc = LANCIUS_HIP_ERR_OOM;
+            goto out;
+        }
+    }
+    const size_t plan_bytes = align_up(region, ALIGN_DEV);
+    size_t in_bytes = 0;
+    size_t* in_off = (size_t*)calloc(ids ? ids : 1, sizeof(size_t));
+    size_t* am_off = (size_t*)calloc(ids ? ids : 1, sizeof(size_t));
+    if (!in_off || !am_off) {
+        free(in_off);
+        free(am_off);
+        rc = LANCIUS_HIP_ERR_OOM;
+        goto out;
+    }
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        if (p->role[n->id] == ROLE_INPUT || p->role[n->id] == ROLE_CONST) {
+            in_off[n->id] = in_bytes;
+            in_bytes += align_up(p->bytes[n->id] ? p->bytes[n->id] : 1, ALIGN_DEV);
+        }
+        if (n->op == LANCIUS_OP_SOFTMAX && p->role[n->id] == ROLE_POOLED) {
+            am_off[n->id] = in_bytes;
+            p->rows[n->id] = n->shape[0];
+            in_bytes += align_up(n->shape[0] * sizeof(int32_t) + 1, ALIGN_DEV);
+        }
+    }
+    p->info.plan_bytes = plan_bytes;
+    p->info.input_bytes = in_bytes;
+    p->info.arena_bytes = plan_bytes + in_bytes;
+    void* arena = NULL;
+    rc = lancius_hip_malloc(ctx, &arena, p->info.arena_bytes ? p->info.arena_bytes : ALIGN_DEV);
+    if (rc) {
+        free(in_off);
+        free(am_off);
+        goto out;
+    }
+    p->arena = (char*)arena;
+    for (uint32_t i = 0; i < niv; i++) p->ptr[iv[i].id] = p->arena + iv[i].offset;
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        if (p->role[n->id] == ROLE_INPUT || p->role[n->id] == ROLE_CONST) p->ptr[n->id] = p->arena + plan_bytes + in_off[n->id];
+        if (p->rows[n->id]) p->argmax[n->id] = (int32_t*)(p->arena + plan_bytes + am_off[n->id]);
+    }
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        if (p->role[n->id] == ROLE_ALIAS) p->ptr[n->id] = p->ptr[c.root[n->id]];
+    }
+    free(in_off);
+    free(am_off);
+    /* CONST nodes are filled once; the region is never reused */
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        if (p->role[n->id] != ROLE_CONST) continue;
+        rc = lancius_hip_fill_f32(ctx, (float*)p->ptr[n->id], (float)n->attr_val, elems(n));
+        if (rc) goto out;
+    }
+    rc = lancius_hip_synchronize(ctx);
+
+out:
+    free(fillbuf);
+    free(iv);
+    free(birth);
+    free(last);
+    free(pinned);
+    cstate_free(&c);
+    if (rc) {
+        lancius_device_program_destroy(p);
+        return rc;
+    }
+    *out = p;
+    return 0;
+}
+
+/* ---- run ---------------------------------------------------------------------------- */
+
+#define P(id) ((id) == NONE ? NULL : (float*)prog->ptr[(id)])
+
+static int run_launch(lancius_device_program* prog, const launch_t* L) {
+    lancius_hip_ctx* ctx = prog->ctx;
+    const member_t* m = &L->m[0];
+    switch (L->kind) {
+        case L_GEMM: {
+            float* C[MAXG];
+            const float *A[MAXG], *B[MAXG], *bias[MAXG], *res[MAXG];
+            for (uint32_t k = 0; k < L->count; k++) {
+                C[k] = P(L->m[k].out);
+                A[k] = P(L->m[k].in[0]);
+                B[k] = P(L->m[k].in[1]);
+                bias[k] = P(L->m[k].in[2]);
+                res[k] = P(L->m[k].in[3]);
+            }
+            return lancius_hip_gemm_grouped_f32(ctx, L->count, C, A, B, L->d[0], L->d[1], L->d[2], bias, L->act,
+                                                res);
+        }
+        case L_ATTN: {
+            float* O[MAXG];
+            const float *Q[MAXG], *K[MAXG], *V[MAXG];
+            for (uint32_t k = 0; k < L->count; k++) {
+                O[k] = P(L->m[k].out);
+                Q[k] = P(L->m[k].in[0]);
+                K[k] = P(L->m[k].in[1]);
+                V[k] = P(L->m[k].in[2]);
+            }
+            return lancius_hip_attention_grouped_f32(ctx, L->count, O, Q, K, V, L->d[0], L->d[1], L->d[2], L->causal,
+                                                     (float)(1.0 / sqrt((double)L->d[2])));
+        }
+        case L_CONV:
+            return lancius_hip_conv2d_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), NULL, L->d[0], L->d[1], L->d[2],
+                                          L->d[3], L->d[4], L->d[5], L->d[6], L->d[7], L->d[8], L->act);
+        case L_LN:
+            return lancius_hip_layernorm_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), P(m->in[2]), L->d[0],
+                                             L->d[1], 1e-5f);
+        case L_SOFTMAX:
+            return lancius_hip_softmax_f32(ctx, P(m->out), prog->argmax[m->out], P(m->in[0]), L->d[0], L->d[1]);
+        case L_ADD:
+            return lancius_hip_add_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0]);
+        case L_RELU:
+            return lancius_hip_relu_f32(ctx, P(m->out), P(m->in[0]), L->d[0]);
+        case L_GELU:
+            return lancius_hip_gelu_f32(ctx, P(m->out), P(m->in[0]), L->d[0]);
+        case L_BCAST:
+            return lancius_hip_broadcast_f32(ctx, P(m->out), P(m->in[0]), L->d[0], L->d[1], L->d[2]);
+    }
+    return LANCIUS_HIP_ERR_INTERNAL;
+}
+
+int lancius_device_run(lancius_device_program* prog) {
+    if (!prog) return LANCIUS_HIP_ERR_NULL_PTR;
+    for (uint32_t s = 0; s < prog->n_launches; s++) {
+        const int rc = run_launch(prog, &prog->launches[s]);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+void* lancius_device_buffer(lancius_device_program* prog, const lancius_node* n) {
+    if (!prog || !n || n->id >= prog->n_ids) return NULL;
+    return prog->ptr[n->id];
+}
+
+int lancius_device_upload(lancius_device_program* prog, const lancius_node* n, const void* host,
+                          lancius_dtype host_dtype) {
+    if (!prog || !n || !host) return LANCIUS_HIP_ERR_NULL_PTR;
+    if (n->id >= prog->n_ids || (prog->role[n->id] != ROLE_INPUT && prog->role[n->id] != ROLE_CONST))
+        return LANCIUS_HIP_ERR_UNSUPPORTED;
+    const size_t e = elems(n);
+    if (host_dtype == LANCIUS_DTYPE_FP32) return lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e * 4);
+    if (host_dtype != LANCIUS_DTYPE_FP64) return LANCIUS_HIP_ERR_DTYPE;
+    float* tmp = (float*)malloc(e * sizeof(float) + 1);
+    if (!tmp) return LANCIUS_HIP_ERR_OOM;
+    const double* src = (const double*)host;
+    for (size_t k = 0; k < e; k++) tmp[k] = (float)src[k];
+    const int rc = lancius_hip_upload(prog->ctx, prog->ptr[n->id], tmp, e * 4);
+    free(tmp);
+    return rc;
+}
+
+int lancius_device_download(lancius_device_program* prog, const lancius_node* n, void* host,
+                            lancius_dtype host_dtype) {
+    if (!prog || !n || !host) return LANCIUS_HIP_ERR_NULL_PTR;
+    if (n->id >= prog->n_ids || !prog->readable[n->id] || !prog->ptr[n->id]) return LANCIUS_HIP_ERR_UNSUPPORTED;
+    const size_t e = elems(n);
+    if (host_dtype == LANCIUS_DTYPE_FP32) return lancius_hip_download(prog->ctx, host, prog->ptr[n->id], e * 4);
+    if (host_dtype != LANCIUS_DTYPE_FP64) return LANCIUS_HIP_ERR_DTYPE;
+    float* tmp = (float*)malloc(e * sizeof(float) + 1);
+    if (!tmp) return LANCIUS_HIP_ERR_OOM;
+    int rc = lancius_hip_download(prog->ctx, tmp, prog->ptr[n->id], e * 4);
+    if (!rc) {
+        double* dst = (double*)host;
+        for (size_t k = 0; k < e; k++) dst[k] = (double)tmp[k];
+    }
+    free(tmp);
+    return rc;
+}
+
+int lancius_device_download_argmax(lancius_device_program* prog, const lancius_node* n, int32_t* host) {
+    if (!prog || !n || !host) return LANCIUS_HIP_ERR_NULL_PTR;
+    if (n->id >= prog->n_ids || !prog->argmax[n->id]) return LANCIUS_HIP_ERR_UNSUPPORTED;
+    return lancius_hip_download(prog->ctx, host, prog->argmax[n->id], prog->rows[n->id] * sizeof(int32_t));
+}
+
+int lancius_schedule_execute_device(lancius_schedule* schedule, lancius_graph* g, lancius_hip_ctx* ctx) {
+    if (!schedule || !g || !ctx) return LANCIUS_HIP_ERR_NULL_PTR;
+    lancius_device_program* prog = NULL;
+    int rc = lancius_device_program_create(ctx, g, schedule, schedule->plan, 0, &prog);
+    if (rc) return rc;
+    for (uint32_t i = 0; i < g->node_count && !rc; i++) {
+        lancius_node* n = g->nodes[i];
+        if (n->op == LANCIUS_OP_INPUT) {
+            if (!n->runtime_data) rc = fail(LANCIUS_HIP_ERR_NULL_PTR, "INPUT node without runtime_data");
+            else rc = lancius_device_upload(prog, n, n->runtime_data, LANCIUS_DTYPE_FP64);
+        }
+    }
+    if (!rc) rc = lancius_device_run(prog);
+    if (!rc) rc = lancius_hip_synchronize(ctx);
+    for (uint32_t i = 0; i < g->node_count && !rc; i++) {
+        lancius_node* n = g->nodes[i];
+        if (n->op == LANCIUS_OP_INPUT || n->op == LANCIUS_OP_CONST || !prog->readable[n->id]) continue;
+        if (!n->runtime_data) {
+            n->runtime_data = (double*)malloc(elems(n) * sizeof(double) + 1);
+            if (!n->runtime_data) {
+                rc = LANCIUS_HIP_ERR_OOM;
+                break;
+            }
+            if (n->rt) {
+                n->rt->buffer = n->runtime_data;
+                n->rt->owner = LANCIUS_MEMORY_OWNED_HEAP;
+                n->rt->buffer_owner = LANCIUS_MEMORY_OWNED_HEAP;
+            }
+        }
+        rc = lancius_device_download(prog, n, n->runtime_data, LANCIUS_DTYPE_FP64);
+    }
+    lancius_device_program_destroy(prog);
+    return rc;
+}

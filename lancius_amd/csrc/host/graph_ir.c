@@ -1,0 +1,419 @@
+/*
+ * Graph IR of the host library: error state, bump arena, graph and node
+ * builders for the ops on the device path.
+ *
+ * Shapes and input wiring follow bleeding/v11A1/src/ir/lancius_ir.c (cited per
+ * builder); node storage lives in the graph's arena so node addresses are
+ * stable for the life of the graph.
+ */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "lancius_graph.h"
+
+/* ---- error state: thread-local code (lancius_error.c:5-34) ---------------- */
+
+static _Thread_local lancius_error t_error = LANCIUS_ERROR_OK;
+
+void lancius_set_error(lancius_error err) { t_error = err; }
+lancius_error lancius_get_error(void) { return t_error; }
+void lancius_clear_error(void) { t_error = LANCIUS_ERROR_OK; }
+
+const char* lancius_error_string(lancius_error err) {
+    switch (err) {
+        case LANCIUS_ERROR_OK: return "success";
+        case LANCIUS_ERROR_OOM: return "out of memory";
+        case LANCIUS_ERROR_NULL_PTR: return "null pointer";
+        case LANCIUS_ERROR_SHAPE_MISMATCH: return "shape mismatch";
+        case LANCIUS_ERROR_UNSUPPORTED_OP: return "unsupported op";
+        case LANCIUS_ERROR_UNSUPPORTED_DTYPE: return "unsupported dtype";
+        case LANCIUS_ERROR_INVALID_MODEL: return "invalid model";
+        case LANCIUS_ERROR_VERSION_MISMATCH: return "version mismatch";
+        case LANCIUS_ERROR_IO: return "io error";
+        case LANCIUS_ERROR_OVERFLOW: return "overflow";
+        case LANCIUS_ERROR_INTERNAL: return "internal error";
+        default: return "unknown error";
+    }
+}
+
+/* ---- bump arena ------------------------------------------------------------
+ * Chained blocks, allocations rounded to 32 bytes and aligned to a power of
+ * two (32 by default), O(1) reset that keeps the first block
+ * (lancius_arena.c:39-89). */
+
+typedef struct arena_block {
+    struct arena_block* next;
+    size_t size, used;
+    unsigned char* mem;
+} arena_block;
+
+struct lancius_arena {
+    arena_block* head;
+    arena_block* tail;
+    size_t block_size;
+};
+
+static arena_block* arena_block_new(size_t size) {
+    arena_block* b = (arena_block*)malloc(sizeof(arena_block));
+    if (!b) return NULL;
+    b->mem = (unsigned char*)malloc(size);
+    if (!b->mem) {
+        free(b);
+        return NULL;
+    }
+    b->next = NULL;
+    b->size = size;
+    b->used = 0;
+    return b;
+}
+
+lancius_arena* lancius_arena_create(size_t block_size) {
+    lancius_arena* a = (lancius_arena*)calloc(1, sizeof(lancius_arena));
+    if (!a) return NULL;
+    a->block_size = block_size ? block_size : ((size_t)16 << 20);
+    a->head = a->tail = arena_block_new(a->block_size);
+    if (!a->head) {
+        free(a);
+        return NULL;
+    }
+    return a;
+}
+
+void* lancius_arena_alloc(lancius_arena* a, size_t size, size_t alignment) {
+    if (!a) return NULL;
+    if (alignment == 0) alignment = 32;
+    if (alignment & (alignment - 1)) return NULL;
+    if (size == 0) size = 1;
+    if (size > SIZE_MAX - 64 - alignment) return NULL; /* rounding below must not wrap */
+    size = (size + 31) & ~(size_t)31;
+    arena_block* b = a->tail;
+    uintptr_t at = (uintptr_t)(b->mem + b->used);
+    size_t pad = (size_t)(((at + alignment - 1) & ~(uintptr_t)(alignment - 1)) - at);
+    if (pad + size > b->size - b->used) {
+        size_t want = size + alignment;
+        arena_block* nb = arena_block_new(want > a->block_size ? want : a->block_size);
+        if (!nb) return NULL;
+        b->next = nb;
+        a->tail = b = nb;
+        at = (uintptr_t)b->mem;
+        pad = (size_t)(((at + alignment - 1) & ~(uintptr_t)(alignment - 1)) - at);
+    }
+    b->used += pad + size;
+    return (void*)(at + pad);
+}
+
+void lancius_arena_reset(lancius_arena* a) {
+    if (!a) return;
+    arena_block* b = a->head->next;
+    while (b) {
+        arena_block* n = b->next;
+        free(b->mem);
+        free(b);
+        b = n;
+    }
+    a->head->next = NULL;
+    a->head->used = 0;
+    a->tail = a->head;
+}
+
+void lancius_arena_destroy(lancius_arena* a) {
+    if (!a) return;
+    arena_block* b = a->head;
+    while (b) {
+        arena_block* n = b->next;
+        free(b->mem);
+        free(b);
+        b = n;
+    }
+    free(a);
+}
+
+/* ---- graph ------------------------------------------------------------------ */
+
+lancius_graph* lancius_graph_create(void) {
+    lancius_graph* g = (lancius_graph*)calloc(1, sizeof(lancius_graph));
+    if (!g) {
+        lancius_set_error(LANCIUS_ERROR_OOM);
+        return NULL;
+    }
+    g->arena = lancius_arena_create(1 << 20);
+    g->node_cap = 256;
+    g->nodes = (lancius_node**)malloc(sizeof(lancius_node*) * g->node_cap);
+    if (!g->arena || !g->nodes) {
+        lancius_arena_destroy(g->arena);
+        free(g->nodes);
+        free(g);
+        lancius_set_error(LANCIUS_ERROR_OOM);
+        return NULL;
+    }
+    return g;
+}
+
+void lancius_graph_destroy(lancius_graph* g) {
+    if (!g) return;
+    free(g->nodes);
+    free(g->rt_states);
+    lancius_arena_destroy(g->arena);
+    free(g);
+}
+
+void lancius_graph_set_dtype(lancius_graph* g, lancius_dtype dtype) {
+    if (!g) return;
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        g->nodes[i]->dtype = dtype;
+        if (g->nodes[i]->rt) g->nodes[i]->rt->dtype = dtype;
+    }
+}
+
+/* A node with its input array and runtime-state record, all in the arena. */
+static lancius_node* new_node(lancius_graph* g, lancius_opcode op, uint8_t ndim, uint32_t n_in) {
+    if (!g) return NULL;
+    if (g->node_count == g->node_cap) {
+        uint32_t cap = g->node_cap * 2;
+        lancius_node** grown = (lancius_node**)realloc(g->nodes, sizeof(lancius_node*) * cap);
+        if (!grown) {
+            lancius_set_error(LANCIUS_ERROR_OOM);
+            return NULL;
+        }
+        g->nodes = grown;
+        g->node_cap = cap;
+    }
+    lancius_node* n = (lancius_node*)lancius_arena_alloc(g->arena, sizeof(lancius_node), 8);
+    lancius_runtime_state* rt = (lancius_runtime_state*)lancius_arena_alloc(g->arena, sizeof(*rt), 8);
+    const lancius_node** ins = NULL;
+    if (n_in) ins = (const lancius_node**)lancius_arena_alloc(g->arena, sizeof(lancius_node*) * n_in, 8);
+    if (!n || !rt || (n_in && !ins)) {
+        lancius_set_error(LANCIUS_ERROR_OOM);
+        return NULL;
+    }
+    memset(n, 0, sizeof(*n));
+    memset(rt, 0, sizeof(*rt));
+    rt->dtype = LANCIUS_DTYPE_FP64;
+    rt->scale = 1.0;
+    n->id = g->next_id++;
+    n->op = op;
+    n->ndim = ndim;
+    n->input_count = n_in;
+    n->inputs = ins;
+    n->rt = rt;
+    n->dtype = LANCIUS_DTYPE_FP64;
+    g->nodes[g->node_count++] = n;
+    return n;
+}
+
+static void copy_shape(lancius_node* n, const lancius_node* from) {
+    for (uint8_t d = 0; d < from->ndim && d < 4; d++) n->shape[d] = from->shape[d];
+}
+
+/* lancius_ir.c:145-148 */
+lancius_node* lancius_input(lancius_graph* g, size_t r, size_t c) {
+    lancius_node* n = new_node(g, LANCIUS_OP_INPUT, 2, 0);
+    if (n) {
+        n->shape[0] = r;
+        n->shape[1] = c;
+    }
+    return n;
+}
+
+/* lancius_ir.c:149-152 */
+lancius_node* lancius_input_4d(lancius_graph* g, size_t nn, size_t c, size_t h, size_t w) {
+    lancius_node* n = new_node(g, LANCIUS_OP_INPUT, 4, 0);
+    if (n) {
+        n->shape[0] = nn;
+        n->shape[1] = c;
+        n->shape[2] = h;
+        n->shape[3] = w;
+    }
+    return n;
+}
+
+/* lancius_ir.c:153-156: value filled in by the executor from attr_val. */
+lancius_node* lancius_const(lancius_graph* g, double val, size_t r, size_t c) {
+    lancius_node* n = new_node(g, LANCIUS_OP_CONST, 2, 0);
+    if (n) {
+        n->shape[0] = r;
+        n->shape[1] = c;
+        n->attr_val = val;
+    }
+    return n;
+}
+
+/* lancius_ir.c:157-163: shape of `a`, no shape check (a bias must come through
+ * a BROADCAST node). */
+lancius_node* lancius_add(lancius_graph* g, const lancius_node* a, const lancius_node* b) {
+    if (!a || !b) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_ADD, a->ndim, 2);
+    if (n) {
+        copy_shape(n, a);
+        n->inputs[0] = a;
+        n->inputs[1] = b;
+    }
+    return n;
+}
+
+/* lancius_ir.c:178-196: uses the last two dims of each operand; 2-D result. */
+lancius_node* lancius_matmul(lancius_graph* g, const lancius_node* a, const lancius_node* b) {
+    if (!a || !b || a->ndim < 2 || b->ndim < 2) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    const size_t ar = a->shape[a->ndim - 2], ac = a->shape[a->ndim - 1];
+    const size_t br = b->shape[b->ndim - 2], bc = b->shape[b->ndim - 1];
+    if (ac != br) {
+        fprintf(stderr, "[LANCIUS IR] MATMUL mismatch: [%zux%zu] x [%zux%zu]\n", ar, ac, br, bc);
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_MATMUL, 2, 2);
+    if (n) {
+        n->shape[0] = ar;
+        n->shape[1] = bc;
+        n->inputs[0] = a;
+        n->inputs[1] = b;
+    }
+    return n;
+}
+
+static lancius_node* unary(lancius_graph* g, lancius_opcode op, const lancius_node* a) {
+    if (!a) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, op, a->ndim, 1);
+    if (n) {
+        copy_shape(n, a);
+        n->inputs[0] = a;
+    }
+    return n;
+}
+
+/* lancius_ir.c:197-201 */
+lancius_node* lancius_relu(lancius_graph* g, const lancius_node* a) { return unary(g, LANCIUS_OP_RELU, a); }
+
+/* lancius_ir.c:202-206: 2-D only. */
+lancius_node* lancius_softmax(lancius_graph* g, const lancius_node* a) {
+    if (!a || a->ndim != 2) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    return unary(g, LANCIUS_OP_SOFTMAX, a);
+}
+
+/* lancius_ir.c:212-216 */
+lancius_node* lancius_broadcast(lancius_graph* g, const lancius_node* a, size_t r, size_t c) {
+    if (!a) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_BROADCAST, 2, 1);
+    if (n) {
+        n->shape[0] = r;
+        n->shape[1] = c;
+        n->inputs[0] = a;
+    }
+    return n;
+}
+
+/* lancius_ir.c:243-261: NCHW input, OIHW weights, output [N, C_out, H_out, W_out]. */
+lancius_node* lancius_conv2d(lancius_graph* g, const lancius_node* in, const lancius_node* w, uint32_t stride,
+                             uint32_t pad) {
+    if (!in || !w || in->ndim != 4 || w->ndim != 4 || stride == 0) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    const size_t N = in->shape[0], C_in = in->shape[1], H = in->shape[2], W = in->shape[3];
+    const size_t C_out = w->shape[0], K_h = w->shape[2], K_w = w->shape[3];
+    if (C_in != w->shape[1] || H + 2 * (size_t)pad < K_h || W + 2 * (size_t)pad < K_w) {
+        fprintf(stderr, "[LANCIUS IR] CONV2D shape mismatch\n");
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_CONV2D, 4, 2);
+    if (n) {
+        n->shape[0] = N;
+        n->shape[1] = C_out;
+        n->shape[2] = (H + 2 * (size_t)pad - K_h) / stride + 1;
+        n->shape[3] = (W + 2 * (size_t)pad - K_w) / stride + 1;
+        n->kernel_h = (uint32_t)K_h;
+        n->kernel_w = (uint32_t)K_w;
+        n->stride = stride;
+        n->pad = pad;
+        n->inputs[0] = in;
+        n->inputs[1] = w;
+    }
+    return n;
+}
+
+/* lancius_ir.c:281-288 */
+lancius_node* lancius_flatten(lancius_graph* g, const lancius_node* in) {
+    if (!in || in->ndim != 4) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_FLATTEN, 2, 1);
+    if (n) {
+        n->shape[0] = in->shape[0];
+        n->shape[1] = in->shape[1] * in->shape[2] * in->shape[3];
+        n->inputs[0] = in;
+    }
+    return n;
+}
+
+/* lancius_ir.c:291-299: the executor copies the first elems(out) values. */
+lancius_node* lancius_reshape(lancius_graph* g, const lancius_node* in, uint8_t ndim, size_t s0, size_t s1, size_t s2,
+                              size_t s3) {
+    if (!in || ndim == 0 || ndim > 4) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_RESHAPE, ndim, 1);
+    if (n) {
+        const size_t s[4] = {s0, s1, s2, s3};
+        for (uint8_t d = 0; d < ndim; d++) n->shape[d] = s[d];
+        n->inputs[0] = in;
+    }
+    return n;
+}
+
+/* lancius_ir.c:72-77: output takes q's 3-D shape [S, H, D]. */
+lancius_node* lancius_attention(lancius_graph* g, const lancius_node* q, const lancius_node* k,
+                                const lancius_node* v) {
+    if (!q || !k || !v) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_ATTENTION, 3, 3);
+    if (n) {
+        n->shape[0] = q->shape[0];
+        n->shape[1] = q->shape[1];
+        n->shape[2] = q->shape[2];
+        n->inputs[0] = q;
+        n->inputs[1] = k;
+        n->inputs[2] = v;
+    }
+    return n;
+}
+
+/* lancius_ir.c:78-83 */
+lancius_node* lancius_layernorm(lancius_graph* g, const lancius_node* in, const lancius_node* gamma,
+                                const lancius_node* beta) {
+    if (!in || !gamma || !beta) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_LAYERNORM, in->ndim, 3);
+    if (n) {
+        copy_shape(n, in);
+        n->inputs[0] = in;
+        n->inputs[1] = gamma;
+        n->inputs[2] = beta;
+    }
+    return n;
+}
+
+/* lancius_ir.c:84-89 */
+lancius_node* lancius_gelu(lancius_graph* g, const lancius_node* in) { return unary(g, LANCIUS_OP_GELU, in); }

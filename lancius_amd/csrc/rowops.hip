@@ -1,0 +1,303 @@
+// Memory-bound row and elementwise kernels: LayerNorm, softmax(+argmax),
+// GELU, ReLU, ADD, BROADCAST, fill, copy.
+//
+// Row kernels use one wave64 per row and keep the row in registers, so a row
+// is read from HBM once and written once; reductions are wave shuffles
+// (no LDS, no barriers).  Elementwise kernels use float4 accesses and a
+// grid-stride loop sized to the device.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lancius {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    return v;
+}
+
+constexpr int kRowThreads = 256;  // 4 rows per workgroup
+constexpr int kRowsPerBlock = kRowThreads / 64;
+
+// LayerNorm, NV float4 per lane (hidden == 256 * NV), row cached in registers.
+// Statistics follow bleeding/v11A1/src/math/lancius_kernels.c:217-236: mean,
+// then the biased variance of (x - mean), then (x - mean) * inv_std * g + b.
+template <int NV>
+__global__ void __launch_bounds__(kRowThreads) layernorm_regs(float* __restrict__ out, const float* __restrict__ in,
+                                                              const float* __restrict__ gamma,
+                                                              const float* __restrict__ beta, int rows, float eps) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    constexpr int H = 256 * NV;
+    const float* x = in + (size_t)row * H;
+    f32x4 v[NV];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        v[i] = *(const f32x4*)(x + 4 * lane + 256 * i);
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+    const float mean = wave_sum(s) * (1.0f / H);
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+        q += (a * a + b * b) + (c * c + d * d);
+    }
+    const float var = wave_sum(q) * (1.0f / H);
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    float* y = out + (size_t)row * H;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * lane + 256 * i;
+        const f32x4 g = *(const f32x4*)(gamma + c0);
+        const f32x4 b = *(const f32x4*)(beta + c0);
+        f32x4 o;
+        o.x = (v[i].x - mean) * inv_std * g.x + b.x;
+        o.y = (v[i].y - mean) * inv_std * g.y + b.y;
+        o.z = (v[i].z - mean) * inv_std * g.z + b.z;
+        o.w = (v[i].w - mean) * inv_std * g.w + b.w;
+        *(f32x4*)(y + c0) = o;
+    }
+}
+
+// Any hidden size: three passes over the row (re-reads hit L2).
+__global__ void __launch_bounds__(kRowThreads) layernorm_any(float* __restrict__ out, const float* __restrict__ in,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, int rows, int hidden,
+                                                             float eps) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* x = in + (size_t)row * hidden;
+    float s = 0.0f;
+    for (int c = lane; c < hidden; c += 64) s += x[c];
+    const float mean = wave_sum(s) / (float)hidden;
+    float q = 0.0f;
+    for (int c = lane; c < hidden; c += 64) {
+        const float d = x[c] - mean;
+        q += d * d;
+    }
+    const float var = wave_sum(q) / (float)hidden;
+    const float inv_std = 1.0f / sqrtf(var + eps);
+    float* y = out + (size_t)row * hidden;
+    for (int c = lane; c < hidden; c += 64) y[c] = (x[c] - mean) * inv_std * gamma[c] + beta[c];
+}
+
+// Row softmax (lancius_scheduler.c:284-294): max, exp(x - max), sum, divide.
+// argmax: first index of the largest probability, scanning with strict '>'
+// from -1e9 like the callers (B/examples/train_mnist.c:206-209); ties are
+// resolved to the smaller index.
+__global__ void __launch_bounds__(kRowThreads) softmax_rows(float* __restrict__ probs, int32_t* __restrict__ argmax,
+                                                            const float* __restrict__ in, int rows, int cols) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* x = in + (size_t)row * cols;
+    float* y = probs + (size_t)row * cols;
+    float m = -INFINITY;
+    for (int c = lane; c < cols; c += 64) m = fmaxf(m, x[c]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int c = lane; c < cols; c += 64) s += expf(x[c] - m);
+    s = wave_sum(s);
+    const float inv = 1.0f / s;
+    float best = -1e9f;
+    int best_i = 0x7fffffff;
+    for (int c = lane; c < cols; c += 64) {
+        const float pv = expf(x[c] - m) / s;
+        y[c] = pv;
+        if (pv > best) {
+            best = pv;
+            best_i = c;
+        }
+    }
+    (void)inv;
+    if (argmax) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ob = __shfl_xor(best, off);
+            const int oi = __shfl_xor(best_i, off);
+            if (ob > best || (ob == best && oi < best_i)) {
+                best = ob;
+                best_i = oi;
+            }
+        }
+        if (lane == 0) argmax[row] = best_i == 0x7fffffff ? 0 : best_i;
+    }
+}
+
+// ---- elementwise --------------------------------------------------------
+
+enum EwOp : int { kAdd = 0, kRelu = 1, kGelu = 2, kCopy = 3 };
+
+template <int OP>
+__device__ __forceinline__ float ew(float a, float b) {
+    if constexpr (OP == kAdd) return a + b;
+    if constexpr (OP == kRelu) return relu_ref(a);
+    if constexpr (OP == kGelu) return gelu_ref(a);
+    return a;
+}
+
+template <int OP>
+__global__ void __launch_bounds__(256) elementwise_vec(float* __restrict__ out, const float* __restrict__ a,
+                                                       const float* __restrict__ b, size_t n4) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const f32x4 x = ((const f32x4*)a)[i];
+        const f32x4 y = (OP == kAdd) ? ((const f32x4*)b)[i] : x;
+        f32x4 o;
+        o.x = ew<OP>(x.x, y.x);
+        o.y = ew<OP>(x.y, y.y);
+        o.z = ew<OP>(x.z, y.z);
+        o.w = ew<OP>(x.w, y.w);
+        ((f32x4*)out)[i] = o;
+    }
+}
+
+template <int OP>
+__global__ void __launch_bounds__(256) elementwise_scalar(float* __restrict__ out, const float* __restrict__ a,
+                                                          const float* __restrict__ b, size_t begin, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = begin + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = ew<OP>(a[i], OP == kAdd ? b[i] : 0.0f);
+}
+
+__global__ void __launch_bounds__(256) broadcast_rows(float* __restrict__ out, const float* __restrict__ row,
+                                                      size_t rows, size_t cols, size_t cols_in) {
+    const size_t n = rows * cols;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = cols_in == 1 ? row[0] : row[i % cols];
+}
+
+__global__ void __launch_bounds__(256) fill_kernel(float* __restrict__ out, float value, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = value;
+}
+
+unsigned int ew_grid(size_t work) {
+    // 256 CUs x 8 workgroups of 256 threads covers the device; more only adds
+    // scheduling overhead for a grid-stride loop.
+    const size_t cap = 2048;
+    size_t g = (work + 255) / 256;
+    if (g < 1) g = 1;
+    return (unsigned int)(g < cap ? g : cap);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <int OP>
+int run_elementwise(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n, const char* name) {
+    LANCIUS_REQUIRE(ctx && out && a && (OP != kAdd || b), LANCIUS_HIP_ERR_NULL_PTR, "%s: NULL argument", name);
+    if (n == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    const bool vec = aligned16(out) && aligned16(a) && (OP != kAdd || aligned16(b));
+    size_t done = 0;
+    if (vec && n >= 4) {
+        const size_t n4 = n / 4;
+        hipLaunchKernelGGL(elementwise_vec<OP>, dim3(ew_grid(n4)), dim3(256), 0, ctx->stream, out, a, b, n4);
+        if (int rc = check_launch(name)) return rc;
+        done = n4 * 4;
+    }
+    if (done < n) {
+        hipLaunchKernelGGL(elementwise_scalar<OP>, dim3(ew_grid(n - done)), dim3(256), 0, ctx->stream, out, a, b,
+                           done, n);
+        if (int rc = check_launch(name)) return rc;
+    }
+    return ok();
+}
+
+}  // namespace
+}  // namespace lancius
+
+using namespace lancius;
+
+extern "C" {
+
+int lancius_hip_layernorm_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* gamma,
+                              const float* beta, size_t rows, size_t hidden, float eps) {
+    LANCIUS_REQUIRE(ctx && out && in && gamma && beta, LANCIUS_HIP_ERR_NULL_PTR, "layernorm: NULL argument");
+    LANCIUS_REQUIRE(hidden > 0 && hidden < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
+                    "layernorm: rows=%zu hidden=%zu", rows, hidden);
+    if (rows == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    const dim3 grid(ceil_div(rows, kRowsPerBlock)), block(kRowThreads);
+    const bool vec = aligned16(out) && aligned16(in) && aligned16(gamma) && aligned16(beta);
+    const int r = (int)rows;
+    if (vec && hidden == 256)
+        hipLaunchKernelGGL(layernorm_regs<1>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
+    else if (vec && hidden == 512)
+        hipLaunchKernelGGL(layernorm_regs<2>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
+    else if (vec && hidden == 1024)
+        hipLaunchKernelGGL(layernorm_regs<4>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
+    else if (vec && hidden == 2048)
+        hipLaunchKernelGGL(layernorm_regs<8>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
+    else if (vec && hidden == 4096)
+        hipLaunchKernelGGL(layernorm_regs<16>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
+    else
+        hipLaunchKernelGGL(layernorm_any, grid, block, 0, ctx->stream, out, in, gamma, beta, r, (int)hidden, eps);
+    if (int rc = check_launch("layernorm")) return rc;
+    return ok();
+}
+
+int lancius_hip_softmax_f32(lancius_hip_ctx* ctx, float* probs, int32_t* argmax, const float* in, size_t rows,
+                            size_t cols) {
+    LANCIUS_REQUIRE(ctx && probs && in, LANCIUS_HIP_ERR_NULL_PTR, "softmax: NULL argument");
+    LANCIUS_REQUIRE(cols > 0 && cols < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
+                    "softmax: rows=%zu cols=%zu", rows, cols);
+    if (rows == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(softmax_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0, ctx->stream, probs,
+                       argmax, in, (int)rows, (int)cols);
+    if (int rc = check_launch("softmax")) return rc;
+    return ok();
+}
+
+int lancius_hip_add_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n) {
+    return run_elementwise<kAdd>(ctx, out, a, b, n, "add");
+}
+
+int lancius_hip_relu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n) {
+    return run_elementwise<kRelu>(ctx, out, a, nullptr, n, "relu");
+}
+
+int lancius_hip_gelu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n) {
+    return run_elementwise<kGelu>(ctx, out, a, nullptr, n, "gelu");
+}
+
+int lancius_hip_copy_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n) {
+    return run_elementwise<kCopy>(ctx, out, in, nullptr, n, "copy");
+}
+
+int lancius_hip_broadcast_f32(lancius_hip_ctx* ctx, float* out, const float* row, size_t rows, size_t cols,
+                              size_t cols_in) {
+    LANCIUS_REQUIRE(ctx && out && row, LANCIUS_HIP_ERR_NULL_PTR, "broadcast: NULL argument");
+    LANCIUS_REQUIRE(cols_in == 1 || cols_in >= cols, LANCIUS_HIP_ERR_SHAPE,
+                    "broadcast: input has %zu values for %zu columns", cols_in, cols);
+    if (rows * cols == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(broadcast_rows, dim3(ew_grid(rows * cols)), dim3(256), 0, ctx->stream, out, row, rows, cols,
+                       cols_in);
+    if (int rc = check_launch("broadcast")) return rc;
+    return ok();
+}
+
+int lancius_hip_fill_f32(lancius_hip_ctx* ctx, float* out, float value, size_t n) {
+    LANCIUS_REQUIRE(ctx && out, LANCIUS_HIP_ERR_NULL_PTR, "fill: NULL argument");
+    if (n == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(fill_kernel, dim3(ew_grid(n)), dim3(256), 0, ctx->stream, out, value, n);
+    if (int rc = check_launch("fill")) return rc;
+    return ok();
+}
+
+}  // extern "C"

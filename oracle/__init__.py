@@ -1,0 +1,201 @@
+"""TEST INFRASTRUCTURE ONLY: numpy wrappers of the fp64 CPU oracle
+(oracle/liboracle.so, restated from the reference C sources) and of the
+reference library compiled from source into oracle/_ref/ (when present).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this package, and only to check or to time the CPU path - never as the
+measured or shipped computation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+from lancius_amd import abi
+
+HERE = Path(__file__).resolve().parent
+ORACLE_LIB = HERE / "liboracle.so"
+REF_LIB = HERE / "_ref" / "liblancius_ref.so"
+
+_lib: C.CDLL | None = None
+_ref: C.CDLL | None = None
+
+_D = C.POINTER(C.c_double)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not ORACLE_LIB.exists():
+            raise RuntimeError(f"{ORACLE_LIB} missing: run `python -m lancius_amd.build`")
+        L = C.CDLL(str(ORACLE_LIB))
+        sz = C.c_size_t
+        L.oracle_matmul_rows.argtypes = [_D, _D, _D, sz, sz, sz, sz, sz]
+        L.oracle_conv2d.argtypes = [_D, _D, _D, sz, sz, sz, sz, sz, sz, sz, sz, sz, C.c_int, sz, sz]
+        L.oracle_attention.argtypes = [_D, _D, _D, _D, sz, sz, sz, sz, C.c_int, C.c_double, sz, sz, sz, sz]
+        L.oracle_layernorm.argtypes = [_D, _D, _D, _D, sz, sz, C.c_double]
+        L.oracle_gelu.argtypes = [_D, _D, sz]
+        L.oracle_softmax.argtypes = [_D, _D, sz, sz]
+        L.oracle_argmax.argtypes = [C.POINTER(C.c_int32), _D, sz, sz]
+        L.oracle_add.argtypes = [_D, _D, _D, sz]
+        L.oracle_relu.argtypes = [_D, _D, sz]
+        L.oracle_broadcast.argtypes = [_D, _D, sz, sz, sz]
+        L.oracle_set_threads.argtypes = [C.c_int]
+        L.oracle_set_threads.restype = None
+        L.oracle_schedule_execute.argtypes = [abi.ScheduleP, C.c_int]
+        L.oracle_schedule_execute.restype = C.c_int
+        L.oracle_release_buffers.argtypes = [abi.GraphP]
+        L.oracle_release_buffers.restype = None
+        for name in ("oracle_matmul_rows", "oracle_conv2d", "oracle_attention", "oracle_layernorm", "oracle_gelu",
+                     "oracle_softmax", "oracle_argmax", "oracle_add", "oracle_relu", "oracle_broadcast"):
+            getattr(L, name).restype = None
+        _lib = L
+    return _lib
+
+
+def ref_lib() -> C.CDLL | None:
+    """The reference's own C, compiled from /root/reference into oracle/_ref
+    (None when it was not built)."""
+    global _ref
+    if _ref is None and REF_LIB.exists():
+        L = abi.declare_graph_api(C.CDLL(str(REF_LIB)))
+        sz = C.c_size_t
+        L.lancius_schedule_execute.argtypes = [abi.ScheduleP, C.c_void_p]
+        L.lancius_schedule_execute.restype = None
+        L.lancius_arena_create.argtypes = [sz]
+        L.lancius_arena_create.restype = C.c_void_p
+        L.lancius_arena_destroy.argtypes = [C.c_void_p]
+        L.lancius_arena_destroy.restype = None
+        L.kernel_matmul.argtypes = [_D, _D, _D, sz, sz, sz]
+        L.kernel_conv2d_fwd.argtypes = [_D, _D, _D] + [sz] * 9
+        L.kernel_conv2d_relu_fwd.argtypes = [_D, _D, _D] + [sz] * 9
+        L.kernel_layernorm.argtypes = [_D, _D, _D, _D, sz, sz, C.c_double]
+        L.kernel_gelu.argtypes = [_D, _D, sz]
+        L.kernel_attention.argtypes = [_D, _D, _D, _D, sz, sz, sz]
+        for name in ("kernel_matmul", "kernel_conv2d_fwd", "kernel_conv2d_relu_fwd", "kernel_layernorm",
+                     "kernel_gelu", "kernel_attention"):
+            getattr(L, name).restype = None
+        _ref = L
+    return _ref
+
+
+def _d(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float64)
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_D)
+
+
+def matmul(a, b, rows: tuple[int, int] | None = None) -> np.ndarray:
+    """fp64 rows [r0, r1) of a @ b (all rows by default); other rows are 0."""
+    a, b = _d(a), _d(b)
+    M, K = a.shape
+    N = b.shape[1]
+    r0, r1 = rows if rows else (0, M)
+    out = np.zeros((M, N))
+    lib().oracle_matmul_rows(_p(out), _p(a), _p(b), M, K, N, r0, r1)
+    return out
+
+
+def conv2d(x, w, stride=1, pad=0, relu=False, images: tuple[int, int] | None = None) -> np.ndarray:
+    x, w = _d(x), _d(w)
+    N, C_in, H, W = x.shape
+    C_out, _, KH, KW = w.shape
+    Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    n0, n1 = images if images else (0, N)
+    out = np.zeros((N, C_out, Ho, Wo))
+    lib().oracle_conv2d(_p(out), _p(x), _p(w), N, C_in, H, W, C_out, KH, KW, stride, pad, int(relu), n0, n1)
+    return out
+
+
+def attention(q, k, v, causal=True, scale=None, batches: tuple[int, int] | None = None,
+              rows: tuple[int, int] | None = None) -> np.ndarray:
+    """q, k, v: [B, S, H, D] (or [S, H, D] for batch 1)."""
+    squeeze = q.ndim == 3
+    q, k, v = (_d(t)[None] if squeeze else _d(t) for t in (q, k, v))
+    B, S, H, D = q.shape
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    b0, b1 = batches if batches else (0, B)
+    i0, i1 = rows if rows else (0, S)
+    out = np.zeros_like(q)
+    lib().oracle_attention(_p(out), _p(q), _p(k), _p(v), B, S, H, D, int(bool(causal)), float(scale), b0, b1, i0, i1)
+    return out[0] if squeeze else out
+
+
+def layernorm(x, gamma, beta, eps=1e-5) -> np.ndarray:
+    x, gamma, beta = _d(x), _d(gamma), _d(beta)
+    rows, hidden = x.shape
+    out = np.empty_like(x)
+    lib().oracle_layernorm(_p(out), _p(x), _p(gamma), _p(beta), rows, hidden, eps)
+    return out
+
+
+def gelu(x) -> np.ndarray:
+    x = _d(x)
+    out = np.empty_like(x)
+    lib().oracle_gelu(_p(out), _p(x), x.size)
+    return out
+
+
+def softmax(x) -> np.ndarray:
+    x = _d(x)
+    out = np.empty_like(x)
+    lib().oracle_softmax(_p(out), _p(x), x.shape[0], x.shape[1])
+    return out
+
+
+def argmax(x) -> np.ndarray:
+    x = _d(x)
+    out = np.empty(x.shape[0], dtype=np.int32)
+    lib().oracle_argmax(out.ctypes.data_as(C.POINTER(C.c_int32)), _p(x), x.shape[0], x.shape[1])
+    return out
+
+
+def add(a, b) -> np.ndarray:
+    a, b = _d(a), _d(b)
+    out = np.empty_like(a)
+    lib().oracle_add(_p(out), _p(a), _p(b), a.size)
+    return out
+
+
+def relu(a) -> np.ndarray:
+    a = _d(a)
+    out = np.empty_like(a)
+    lib().oracle_relu(_p(out), _p(a), a.size)
+    return out
+
+
+def broadcast(a, rows, cols) -> np.ndarray:
+    a = _d(a)
+    out = np.empty((rows, cols))
+    lib().oracle_broadcast(_p(out), _p(a), a.size, rows, cols)
+    return out
+
+
+def set_threads(n: int) -> None:
+    lib().oracle_set_threads(int(n))
+
+
+def schedule_execute(sched: abi.ScheduleP, threads: int = 0) -> None:
+    rc = lib().oracle_schedule_execute(sched, threads)
+    if rc != 0:
+        raise RuntimeError(f"oracle_schedule_execute failed: {rc}")
+
+
+def release(g: abi.GraphP) -> None:
+    lib().oracle_release_buffers(g)
+
+
+def normwise_error(y, y_ref) -> float:
+    """max|y - y_ref| / max|y_ref| (S9/audit_pytorch_parity.py:62-64)."""
+    y_ref = np.asarray(y_ref, dtype=np.float64)
+    denom = np.max(np.abs(y_ref))
+    return float(np.max(np.abs(np.asarray(y, dtype=np.float64) - y_ref)) / (denom if denom > 0 else 1.0))
+
+
+def tolerance(k_reduction: int) -> float:
+    """1e-4 * max(1, sqrt(K)/32) for a reduction of length K."""
+    return 1e-4 * max(1.0, np.sqrt(k_reduction) / 32.0)

@@ -1,0 +1,327 @@
+/*
+ * lancius_oracle.c - TEST INFRASTRUCTURE ONLY (see lancius_oracle.h).
+ *
+ * fp64 CPU restatement of the reference hot path.  Paths are relative to the
+ * reference root; B/ = bleeding/v11A1/.  Loop order and accumulation follow
+ * the cited reference code so the results agree with the compiled reference
+ * to rounding (the golden fixtures check this).
+ */
+#include "lancius_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORACLE_OWNED (1u << 8) /* rt->flags bit: buffer malloc'd by this executor */
+
+void oracle_set_threads(int n) {
+#ifdef _OPENMP
+    if (n > 0) omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
+/* B/src/runtime/lancius_scheduler.c:222-234: zero the output, then for each
+ * row r and k, out[r, :] += a[r, k] * b[k, :] (single-threaded in the
+ * reference; rows are independent, so splitting rows over threads gives the
+ * same numbers). */
+void oracle_matmul_rows(double* out, const double* a, const double* b, size_t M, size_t K, size_t N, size_t r0,
+                        size_t r1) {
+    if (r1 > M) r1 = M;
+#pragma omp parallel for schedule(static)
+    for (long long rr = (long long)r0; rr < (long long)r1; rr++) {
+        const size_t r = (size_t)rr;
+        double* o = out + r * N;
+        memset(o, 0, N * sizeof(double));
+        for (size_t k = 0; k < K; k++) {
+            const double av = a[r * K + k];
+            const double* br = b + k * N;
+            for (size_t c = 0; c < N; c++) o[c] += av * br[c];
+        }
+    }
+}
+
+/* B/src/math/lancius_kernels.c:28-60 (and the ReLU variant :140-173): direct
+ * cross-correlation, taps outside the image skipped (:156-158), ReLU applied
+ * on store (:168).  Parallel over (image, output channel) like the reference
+ * (:147). */
+void oracle_conv2d(double* out, const double* in, const double* w, size_t N, size_t C_in, size_t H, size_t W,
+                   size_t C_out, size_t K_h, size_t K_w, size_t stride, size_t pad, int relu, size_t n0, size_t n1) {
+    const size_t Ho = (H + 2 * pad - K_h) / stride + 1;
+    const size_t Wo = (W + 2 * pad - K_w) / stride + 1;
+    if (n1 > N) n1 = N;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (long long ni = (long long)n0; ni < (long long)n1; ni++) {
+        for (long long co = 0; co < (long long)C_out; co++) {
+            for (size_t ho = 0; ho < Ho; ho++) {
+                for (size_t wo = 0; wo < Wo; wo++) {
+                    double sum = 0.0;
+                    for (size_t ci = 0; ci < C_in; ci++) {
+                        for (size_t kh = 0; kh < K_h; kh++) {
+                            for (size_t kw = 0; kw < K_w; kw++) {
+                                const long ih = (long)(ho * stride) - (long)pad + (long)kh;
+                                const long iw = (long)(wo * stride) - (long)pad + (long)kw;
+                                if (ih >= 0 && ih < (long)H && iw >= 0 && iw < (long)W) {
+                                    sum += in[(size_t)ni * (C_in * H * W) + ci * (H * W) + (size_t)ih * W + (size_t)iw] *
+                                           w[(size_t)co * (C_in * K_h * K_w) + ci * (K_h * K_w) + kh * K_w + kw];
+                                }
+                            }
+                        }
+                    }
+                    out[(size_t)ni * (C_out * Ho * Wo) + (size_t)co * (Ho * Wo) + ho * Wo + wo] =
+                        relu ? (sum > 0.0 ? sum : 0.0) : sum;
+                }
+            }
+        }
+    }
+}
+
+/* B/src/math/lancius_kernels.c:278-332 with a batch loop and a causal switch:
+ * for each (i, h): m = -1e9, l = 0, o = 0; for every key j, s = (q.k)*scale,
+ * causal keys j > i get s = -1e9 (:307); m' = max(m, s), c = exp(m - m'),
+ * p = exp(s - m'), l = l*c + p, o = o*c + p*v (:309-319); out = o / l.
+ * Masked keys are still visited, as in the reference. */
+void oracle_attention(double* out, const double* q, const double* k, const double* v, size_t batch, size_t S,
+                      size_t H, size_t D, int causal, double scale, size_t b0, size_t b1, size_t i0, size_t i1) {
+    if (b1 > batch) b1 = batch;
+    if (i1 > S) i1 = S;
+#pragma omp parallel
+    {
+        double* o = (double*)calloc(D ? D : 1, sizeof(double));
+#pragma omp for collapse(3) schedule(static)
+        for (long long b = (long long)b0; b < (long long)b1; b++) {
+            for (long long ii = (long long)i0; ii < (long long)i1; ii++) {
+                for (long long h = 0; h < (long long)H; h++) {
+                    const size_t i = (size_t)ii;
+                    const size_t base = (size_t)b * S * H * D;
+                    const double* qr = q + base + i * H * D + (size_t)h * D;
+                    double m = -1e9, l = 0.0;
+                    memset(o, 0, D * sizeof(double));
+                    for (size_t j = 0; j < S; j++) {
+                        const double* kr = k + base + j * H * D + (size_t)h * D;
+                        const double* vr = v + base + j * H * D + (size_t)h * D;
+                        double s = 0.0;
+                        for (size_t d = 0; d < D; d++) s += qr[d] * kr[d];
+                        s *= scale;
+                        if (causal && j > i) s = -1e9;
+                        const double mn = s > m ? s : m;
+                        const double c = exp(m - mn);
+                        const double p = exp(s - mn);
+                        l = l * c + p;
+                        for (size_t d = 0; d < D; d++) o[d] = o[d] * c + p * vr[d];
+                        m = mn;
+                    }
+                    double* orow = out + base + i * H * D + (size_t)h * D;
+                    const double inv = 1.0 / l;
+                    for (size_t d = 0; d < D; d++) orow[d] = o[d] * inv;
+                }
+            }
+        }
+        free(o);
+    }
+}
+
+/* B/src/math/lancius_kernels.c:217-236: mean, biased variance of (x - mean),
+ * y = (x - mean) * (1/sqrt(var + eps)) * gamma + beta. */
+void oracle_layernorm(double* out, const double* in, const double* gamma, const double* beta, size_t rows,
+                      size_t hidden, double eps) {
+    for (size_t r = 0; r < rows; r++) {
+        const double* x = in + r * hidden;
+        double* y = out + r * hidden;
+        double mean = 0.0;
+        for (size_t i = 0; i < hidden; i++) mean += x[i];
+        mean /= (double)hidden;
+        double var = 0.0;
+        for (size_t i = 0; i < hidden; i++) var += (x[i] - mean) * (x[i] - mean);
+        var /= (double)hidden;
+        const double inv_std = 1.0 / sqrt(var + eps);
+        for (size_t i = 0; i < hidden; i++) y[i] = (x[i] - mean) * inv_std * gamma[i] + beta[i];
+    }
+}
+
+/* B/src/math/lancius_kernels.c:238-246: clamp to [-100, 100], then the tanh
+ * approximation 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))). */
+void oracle_gelu(double* out, const double* in, size_t n) {
+    const double k0 = 0.7978845608028654;
+    for (size_t i = 0; i < n; i++) {
+        double x = in[i];
+        if (x > 100.0) x = 100.0;
+        if (x < -100.0) x = -100.0;
+        out[i] = 0.5 * x * (1.0 + tanh(k0 * (x + 0.044715 * x * x * x)));
+    }
+}
+
+/* B/src/runtime/lancius_scheduler.c:284-294. */
+void oracle_softmax(double* out, const double* in, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; r++) {
+        const double* a = in + r * cols;
+        double* y = out + r * cols;
+        double mx = a[0];
+        for (size_t c = 1; c < cols; c++)
+            if (a[c] > mx) mx = a[c];
+        double sum = 0.0;
+        for (size_t c = 0; c < cols; c++) {
+            y[c] = exp(a[c] - mx);
+            sum += y[c];
+        }
+        for (size_t c = 0; c < cols; c++) y[c] /= sum;
+    }
+}
+
+/* B/examples/train_mnist.c:206-209: pred = 0, best = -1e9, strict '>'. */
+void oracle_argmax(int32_t* idx, const double* in, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; r++) {
+        int32_t pred = 0;
+        double best = -1e9;
+        for (size_t c = 0; c < cols; c++)
+            if (in[r * cols + c] > best) {
+                best = in[r * cols + c];
+                pred = (int32_t)c;
+            }
+        idx[r] = pred;
+    }
+}
+
+/* B/src/runtime/lancius_scheduler.c:188 */
+void oracle_add(double* out, const double* a, const double* b, size_t n) {
+    for (size_t k = 0; k < n; k++) out[k] = a[k] + b[k];
+}
+
+/* B/src/runtime/lancius_scheduler.c:307 (NaN maps to 0) */
+void oracle_relu(double* out, const double* a, size_t n) {
+    for (size_t k = 0; k < n; k++) out[k] = a[k] > 0.0 ? a[k] : 0.0;
+}
+
+/* B/src/runtime/lancius_scheduler.c:268-278 */
+void oracle_broadcast(double* out, const double* a, size_t a_elems, size_t rows, size_t cols) {
+    if (a_elems == 1) {
+        for (size_t k = 0; k < rows * cols; k++) out[k] = a[0];
+    } else {
+        for (size_t r = 0; r < rows; r++)
+            for (size_t c = 0; c < cols; c++) out[r * cols + c] = a[c];
+    }
+}
+
+/* ---- fp64 graph executor ------------------------------------------------------ */
+
+static size_t elems_of(const lancius_node* n) {
+    size_t e = 1;
+    for (uint8_t d = 0; d < n->ndim; d++) e *= n->shape[d];
+    return e;
+}
+
+static int ensure_buffer(lancius_node* n) {
+    if (n->runtime_data) return 0;
+    const size_t e = elems_of(n);
+    n->runtime_data = (double*)calloc(e ? e : 1, sizeof(double));
+    if (!n->runtime_data) return -1;
+    if (n->rt) {
+        n->rt->buffer = n->runtime_data;
+        n->rt->flags |= ORACLE_OWNED;
+    }
+    return 0;
+}
+
+/* One node, the branches of B/src/runtime/lancius_scheduler.c:61-309 and
+ * B/src/runtime/lancius_vision_ops.c:60-81,113-125 that the device path covers. */
+static int run_node(lancius_node* n) {
+    double* y = n->runtime_data;
+    const size_t e = elems_of(n);
+    const lancius_node* const* in = (const lancius_node* const*)n->inputs;
+    switch (n->op) {
+        case LANCIUS_OP_ADD:
+            oracle_add(y, in[0]->runtime_data, in[1]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_MATMUL: {
+            const size_t M = in[0]->shape[0], K = in[0]->shape[1], N = in[1]->shape[1];
+            if (M * N > e) return -3;
+            oracle_matmul_rows(y, in[0]->runtime_data, in[1]->runtime_data, M, K, N, 0, M);
+            return 0;
+        }
+        case LANCIUS_OP_RELU:
+            oracle_relu(y, in[0]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_GELU:
+            oracle_gelu(y, in[0]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_SOFTMAX:
+            oracle_softmax(y, in[0]->runtime_data, n->shape[0], n->shape[1]);
+            return 0;
+        case LANCIUS_OP_BROADCAST:
+            oracle_broadcast(y, in[0]->runtime_data, elems_of(in[0]), n->shape[0], n->shape[1]);
+            return 0;
+        case LANCIUS_OP_LAYERNORM:
+            oracle_layernorm(y, in[0]->runtime_data, in[1]->runtime_data, in[2]->runtime_data, n->shape[0],
+                             n->shape[1], 1e-5);
+            return 0;
+        case LANCIUS_OP_ATTENTION: {
+            const size_t S = n->shape[0], H = n->shape[1], D = n->shape[2];
+            const int causal = n->axes[0] != 1; /* axes[0] == 1 selects the non-causal variant */
+            oracle_attention(y, in[0]->runtime_data, in[1]->runtime_data, in[2]->runtime_data, 1, S, H, D, causal,
+                             1.0 / sqrt((double)D), 0, 1, 0, S);
+            return 0;
+        }
+        case LANCIUS_OP_CONV2D:
+        case LANCIUS_OP_CONV2D_RELU_FUSED: {
+            const lancius_node* x = in[0];
+            const lancius_node* w = in[1];
+            oracle_conv2d(y, x->runtime_data, w->runtime_data, x->shape[0], x->shape[1], x->shape[2], x->shape[3],
+                          w->shape[0], w->shape[2], w->shape[3], n->stride, n->pad,
+                          n->op == LANCIUS_OP_CONV2D_RELU_FUSED, 0, x->shape[0]);
+            return 0;
+        }
+        case LANCIUS_OP_RESHAPE:
+        case LANCIUS_OP_FLATTEN:
+            memcpy(y, in[0]->runtime_data, e * sizeof(double));
+            return 0;
+        default:
+            return -4;
+    }
+}
+
+int oracle_schedule_execute(lancius_schedule* s, int num_threads) {
+    if (!s) return -2;
+#ifdef _OPENMP
+    if (num_threads > 0) omp_set_num_threads(num_threads);
+#else
+    (void)num_threads;
+#endif
+    for (uint32_t w = 0; w < s->wave_count; w++) {
+        for (uint32_t i = 0; i < s->waves[w].node_count; i++) {
+            lancius_node* n = s->waves[w].nodes[i];
+            if (n->op == LANCIUS_OP_INPUT || n->op == LANCIUS_OP_NOP) continue;
+            if (n->op == LANCIUS_OP_CONST) {
+                if (!n->runtime_data) {
+                    if (ensure_buffer(n)) return -1;
+                    const size_t e = elems_of(n);
+                    for (size_t k = 0; k < e; k++) n->runtime_data[k] = n->attr_val;
+                }
+                continue;
+            }
+            for (uint32_t j = 0; j < n->input_count; j++)
+                if (!n->inputs[j] || !n->inputs[j]->runtime_data) return -2;
+            if (ensure_buffer(n)) return -1;
+            const int rc = run_node(n);
+            if (rc) return rc;
+        }
+    }
+    return 0;
+}
+
+void oracle_release_buffers(lancius_graph* g) {
+    if (!g) return;
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        lancius_node* n = g->nodes[i];
+        if (n->rt && (n->rt->flags & ORACLE_OWNED)) {
+            free(n->runtime_data);
+            n->runtime_data = NULL;
+            n->rt->buffer = NULL;
+            n->rt->flags &= ~ORACLE_OWNED;
+        }
+    }
+}

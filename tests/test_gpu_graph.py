@@ -1,0 +1,274 @@
+"""The device executor (lancius_hip_graph.h) on the config graphs, against the
+reference's golden graph outputs and the fp64 oracle executor."""
+import ctypes as C
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from lancius_amd import (DEVICE_KEEP_ALL, DEVICE_NO_FUSION, DeviceProgram, HipError, abi, graph_lib, graphs,
+                         prng)
+from tests.conftest import case
+
+pytestmark = pytest.mark.gpu
+
+GOLD = Path(__file__).resolve().parent / "golden"
+GO = np.load(GOLD / "graph_outputs.npz")
+PLANS = json.loads((GOLD / "graphs.json").read_text())
+
+
+class Planned:
+    """Graph + schedule + fp32 plan from liblancius_graph."""
+
+    def __init__(self, bg, plan=True):
+        self.lib = graph_lib()
+        self.bg = bg
+        self.lib.lancius_graph_set_dtype(bg.g, abi.DTYPE_FP32)
+        self.sched = self.lib.lancius_ir_schedule(bg.g)
+        self.plan = self.lib.lancius_build_memory_plan(self.sched, bg.g) if plan else None
+        self.lib.lancius_graph_set_dtype(bg.g, abi.DTYPE_FP64)
+
+    def program(self, dev, flags=0, plan="own"):
+        p = {"own": self.plan, "none": None}.get(plan, plan) if isinstance(plan, str) else plan
+        return DeviceProgram(dev, self.bg.g, self.sched, p, flags)
+
+    def oracle_run(self, feeds):
+        keep = []
+        for name in self.bg.inputs:
+            arr = np.ascontiguousarray(feeds[name], dtype=np.float64)
+            keep.append(arr)
+            self.bg.node(name).contents.runtime_data = arr.ctypes.data_as(C.POINTER(C.c_double))
+        oracle.schedule_execute(self.sched)
+        out = {}
+        for i in range(self.bg.g.contents.node_count):
+            n = self.bg.g.contents.nodes[i]
+            if n.contents.runtime_data:
+                out[n.contents.id] = np.ctypeslib.as_array(n.contents.runtime_data, shape=(abi.node_elems(n),)).copy()
+        oracle.release(self.bg.g)
+        for name in self.bg.inputs:
+            self.bg.node(name).contents.runtime_data = None
+        return out
+
+    def close(self):
+        if self.plan:
+            self.lib.lancius_memory_plan_destroy(self.plan)
+        self.lib.lancius_schedule_destroy(self.sched)
+        self.bg.destroy()
+
+
+def _plan_from_fixture(rec):
+    ids = len(rec["offsets"])
+    offs = (C.c_size_t * ids)(*rec["offsets"])
+    pooled = (C.c_uint8 * ids)(*rec["is_pooled"])
+    plan = abi.MemoryPlan(rec["peak"], C.cast(offs, C.POINTER(C.c_size_t)), C.cast(pooled, C.POINTER(C.c_uint8)))
+    return plan, (offs, pooled)
+
+
+def _feed(prog, bg, feeds):
+    for name in bg.inputs:
+        prog.upload(bg.node(name), np.asarray(feeds[name], np.float32))
+
+
+# ---- MLP ----------------------------------------------------------------------------
+
+
+def test_mlp_fused_matches_reference(dev):
+    pl = Planned(graphs.build_mlp(graph_lib()))
+    feeds = {n: GO[f"mlp_{n}"] for n in pl.bg.inputs}
+    case("mlp fused")
+    prog = pl.program(dev)
+    _feed(prog, pl.bg, feeds)
+    prog.run()
+    sm = pl.bg.node("softmax")
+    got = prog.download(sm)
+    assert oracle.normwise_error(got, GO["mlp_softmax"]) <= oracle.tolerance(784)
+    assert np.array_equal(prog.argmax(sm), oracle.argmax(GO["mlp_softmax"]))
+    info = prog.info()
+    assert info["launches"] == 3 and info["fused_nodes"] == 5
+    prog.close()
+    pl.close()
+
+
+def test_mlp_unfused_uses_caller_plan(dev):
+    pl = Planned(graphs.build_mlp(graph_lib()))
+    feeds = {n: GO[f"mlp_{n}"] for n in pl.bg.inputs}
+    case("mlp unfused, caller plan")
+    prog = pl.program(dev, flags=DEVICE_NO_FUSION)
+    info = prog.info()
+    assert info["used_caller_plan"] == 1 and info["replanned"] == 0 and info["launches"] == 8
+    # buffers sit at arena + plan offset
+    base = prog.buffer(pl.bg.node("mm1")) - pl.plan.contents.offsets[pl.bg.node("mm1").contents.id]
+    for name in ("bc1", "add1", "relu", "mm2", "add2", "softmax"):
+        n = pl.bg.node(name)
+        assert prog.buffer(n) == base + pl.plan.contents.offsets[n.contents.id]
+    _feed(prog, pl.bg, feeds)
+    prog.run()
+    assert oracle.normwise_error(prog.download(pl.bg.node("softmax")), GO["mlp_softmax"]) <= oracle.tolerance(784)
+    prog.close()
+    pl.close()
+
+
+def test_mlp_reference_plan_is_replanned(dev):
+    # The reference plan puts the second MATMUL on its live input; the
+    # executor detects it and plans its own arena.
+    pl = Planned(graphs.build_mlp(graph_lib()))
+    plan, keep = _plan_from_fixture(PLANS["mlp"])
+    case("mlp reference plan")
+    prog = pl.program(dev, flags=DEVICE_NO_FUSION, plan=C.pointer(plan))
+    info = prog.info()
+    assert info["replanned"] == 1 and info["used_caller_plan"] == 0
+    _feed(prog, pl.bg, {n: GO[f"mlp_{n}"] for n in pl.bg.inputs})
+    prog.run()
+    assert oracle.normwise_error(prog.download(pl.bg.node("softmax")), GO["mlp_softmax"]) <= oracle.tolerance(784)
+    prog.close()
+    pl.close()
+
+
+def test_schedule_execute_device_drop_in(dev):
+    lib = graph_lib()
+    bg = graphs.build_mlp(lib)
+    keep = []
+    for name in bg.inputs:
+        arr = np.ascontiguousarray(GO[f"mlp_{name}"], dtype=np.float64)
+        keep.append(arr)
+        bg.node(name).contents.runtime_data = arr.ctypes.data_as(C.POINTER(C.c_double))
+    sched = lib.lancius_ir_schedule(bg.g)
+    case("lancius_schedule_execute_device")
+    rc = dev.lib.lancius_schedule_execute_device(sched, bg.g, dev.ctx)
+    assert rc == 0, dev.lib.lancius_hip_last_error()
+    sm = bg.node("softmax")
+    got = np.ctypeslib.as_array(sm.contents.runtime_data, shape=(64 * 10,)).reshape(64, 10).copy()
+    assert oracle.normwise_error(got, GO["mlp_softmax"]) <= oracle.tolerance(784)
+    assert sm.contents.rt.contents.buffer_owner == 3  # LANCIUS_MEMORY_OWNED_HEAP
+    import ctypes.util
+
+    libc = C.CDLL(ctypes.util.find_library("c"))
+    libc.free(C.c_void_p(C.addressof(sm.contents.runtime_data.contents)))
+    sm.contents.runtime_data = None
+    for name in bg.inputs:
+        bg.node(name).contents.runtime_data = None
+    lib.lancius_schedule_destroy(sched)
+    bg.destroy()
+
+
+def test_unsupported_op_fails_loudly(dev):
+    lib = graph_lib()
+    g = lib.lancius_graph_create()
+    x = lib.lancius_input(g, 4, 4)
+    n = lib.lancius_relu(g, x)
+    n.contents.op = abi.OP["TRANSPOSE"]
+    sched = lib.lancius_ir_schedule(g)
+    case("unsupported op")
+    with pytest.raises(HipError) as e:
+        DeviceProgram(dev, g, sched, None, 0)
+    assert e.value.code == -4
+    lib.lancius_schedule_destroy(sched)
+    lib.lancius_graph_destroy(g)
+
+
+# ---- conv -----------------------------------------------------------------------------
+
+
+def test_conv_graph_small_golden(dev):
+    pl = Planned(graphs.build_conv(graph_lib(), N=2, C_in=3, H=8, W=8, C_out=4))
+    case("conv graph small")
+    prog = pl.program(dev)
+    _feed(prog, pl.bg, {"x": GO["conv_x"], "w": GO["conv_w"]})
+    prog.run()
+    assert oracle.normwise_error(prog.download(pl.bg.node("relu")), GO["conv_relu"]) <= oracle.tolerance(27)
+    assert prog.info()["launches"] == 1
+    prog.close()
+    pl.close()
+
+
+def test_conv_graph_config(dev):
+    pl = Planned(graphs.build_conv(graph_lib()))
+    x = prng.normal(45, (32, 64, 56, 56))
+    w = prng.normal(145, (128, 64, 3, 3), std=float(np.sqrt(2.0 / 576)))
+    case("conv graph config")
+    prog = pl.program(dev)
+    _feed(prog, pl.bg, {"x": x, "w": w})
+    prog.run()
+    got = prog.download(pl.bg.node("relu"))
+    ref = oracle.conv2d(x, w, 1, 1, True, images=(0, 2))
+    assert oracle.normwise_error(got[:2], ref[:2]) <= oracle.tolerance(576)
+    prog.close()
+    pl.close()
+
+
+# ---- transformer block ----------------------------------------------------------------
+
+
+def _block_feeds(bg, seed=1000):
+    feeds = {}
+    for i, name in enumerate(bg.inputs):
+        shape = abi.node_shape(bg.node(name))
+        if name.startswith("x"):
+            feeds[name] = prng.normal(seed + i, shape)
+        elif name in ("g1", "g2"):
+            feeds[name] = 1.0 + prng.normal(seed + i, shape, 0, 0.02)
+        else:
+            feeds[name] = prng.normal(seed + i, shape, 0, 0.02)
+    return feeds
+
+
+def test_block_small_golden(dev):
+    pl = Planned(graphs.build_block(graph_lib(), batch=2, S=32, d=64, H=4, F=256))
+    feeds = {n: GO[f"block_{n}"] for n in pl.bg.inputs}
+    case("block small fused")
+    prog = pl.program(dev)
+    _feed(prog, pl.bg, feeds)
+    prog.run()
+    for name in pl.bg.outputs:
+        got = prog.download(pl.bg.node(name))
+        assert oracle.normwise_error(got, GO[f"block_out_{name}"]) <= oracle.tolerance(256), name
+    info = prog.info()
+    # LN x2, QKV grouped (6 GEMMs), attention grouped, Wo grouped,
+    # LN x2, FFN1 grouped, FFN2 grouped
+    assert info["launches"] == 9, info
+    prog.close()
+    pl.close()
+
+
+def test_block_small_every_node(dev):
+    pl = Planned(graphs.build_block(graph_lib(), batch=2, S=32, d=64, H=4, F=256))
+    feeds = {n: GO[f"block_{n}"] for n in pl.bg.inputs}
+    ref = pl.oracle_run(feeds)
+    case("block small keep-all")
+    prog = pl.program(dev, flags=DEVICE_KEEP_ALL)
+    _feed(prog, pl.bg, feeds)
+    prog.run()
+    for i in range(pl.bg.g.contents.node_count):
+        n = pl.bg.g.contents.nodes[i]
+        if n.contents.op in (abi.OP["INPUT"],):
+            continue
+        got = prog.download(n).ravel()
+        assert oracle.normwise_error(got, ref[n.contents.id]) <= oracle.tolerance(256), abi.OP_NAME[n.contents.op]
+    prog.close()
+    pl.close()
+
+
+@pytest.mark.parametrize("noncausal", [False, True])
+def test_block_config_branch0(dev, noncausal):
+    """Full config block (B=4, S=1024, d=1024, H=16, F=4096) on the device;
+    sequence 0 checked against the fp64 oracle executor on a batch-1 graph
+    with the same weights."""
+    lib = graph_lib()
+    pl = Planned(graphs.build_block(lib, noncausal=noncausal))
+    feeds = _block_feeds(pl.bg)
+    case(f"block config noncausal={noncausal}")
+    prog = pl.program(dev)
+    _feed(prog, pl.bg, feeds)
+    prog.run()
+    got = prog.download(pl.bg.node("y0"))
+    info = prog.info()
+    prog.close()
+    pl.close()
+    one = Planned(graphs.build_block(lib, batch=1, noncausal=noncausal), plan=False)
+    f1 = {n: feeds[n] for n in one.bg.inputs}
+    ref = one.oracle_run(f1)[one.bg.node("y0").contents.id]
+    one.close()
+    assert oracle.normwise_error(got.ravel(), ref) <= oracle.tolerance(4096)
+    assert info["launches"] == 13, info

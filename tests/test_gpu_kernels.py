@@ -1,0 +1,355 @@
+"""Parity of every HIP kernel, called through the C ABI, against the fp64 CPU
+oracle on identical seeded fp32 inputs.
+
+Bar: normwise error max|y - y_ref| / max|y_ref| <=
+1e-4 * max(1, sqrt(K)/32), K the longest reduction; argmax/indices bit-exact.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from lancius_amd import ACT_GELU, ACT_NONE, ACT_RELU, prng
+from tests.conftest import case
+
+pytestmark = pytest.mark.gpu
+
+TOL_ELEMENTWISE = 1e-6  # fp32 rounding of one op (GELU's tanh included)
+
+
+def _upload(dev, *arrs):
+    return [dev.upload(np.ascontiguousarray(a, dtype=np.float32)) for a in arrs]
+
+
+def _gemm_case(dev, M, K, N, seed, bias=False, act=ACT_NONE, residual=False, rows=None):
+    A = prng.normal(seed, (M, K))
+    B = prng.normal(seed + 1000, (K, N))
+    bv = prng.normal(seed + 2000, (N,)) if bias else None
+    R = prng.normal(seed + 3000, (M, N)) if residual else None
+    dA, dB = _upload(dev, A, B)
+    dbias = dev.upload(bv) if bias else None
+    dR = dev.upload(R) if residual else None
+    dC = dev.alloc(M * N * 4)
+    case(f"gemm M={M} K={K} N={N} bias={bias} act={act} res={residual}")
+    dev.gemm(dC, dA, dB, M, K, N, bias=dbias, act=act, residual=dR)
+    got = dev.download(dC, (M, N))
+    ref = oracle.matmul(A, B, rows=rows)
+    if bias:
+        ref = ref + bv.astype(np.float64)[None, :]
+    if act == ACT_RELU:
+        ref = oracle.relu(ref)
+    elif act == ACT_GELU:
+        ref = oracle.gelu(ref)
+    if residual:
+        ref = ref + R.astype(np.float64)
+    sel = slice(*rows) if rows else slice(None)
+    for b in (dA, dB, dC, dbias, dR):
+        if b is not None:
+            b.free()
+    return got[sel], ref[sel]
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 1, 1), (7, 13, 5), (64, 784, 256), (64, 256, 10), (130, 70, 200),
+                                   (257, 129, 131), (33, 64, 96), (300, 1000, 260)])
+def test_gemm_shapes(dev, M, K, N):
+    got, ref = _gemm_case(dev, M, K, N, seed=100 + M + K + N)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
+@pytest.mark.parametrize("act", [ACT_NONE, ACT_RELU, ACT_GELU])
+@pytest.mark.parametrize("bias,residual", [(True, False), (True, True), (False, True)])
+def test_gemm_epilogues(dev, act, bias, residual):
+    got, ref = _gemm_case(dev, 96, 200, 160, seed=7, bias=bias, act=act, residual=residual)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(200)
+
+
+@pytest.mark.parametrize("M,K,N", [(1024, 1024, 1024), (16, 4096, 4096)])
+def test_gemm_config_full(dev, M, K, N):
+    got, ref = _gemm_case(dev, M, K, N, seed=43)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
+@pytest.mark.parametrize("n", [2048, 4096])
+def test_gemm_config_sampled_rows(dev, n):
+    # Rows [n-96, n) are exact fp64 oracle rows of the full product.
+    got, ref = _gemm_case(dev, n, n, n, seed=43, rows=(n - 96, n))
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(n)
+
+
+def test_gemm_grouped(dev):
+    M, K, N, G = 200, 96, 136, 5
+    As = [prng.normal(500 + g, (M, K)) for g in range(G)]
+    Bs = [prng.normal(600 + g % 2, (K, N)) for g in range(G)]
+    bs = [prng.normal(700 + g, (N,)) for g in range(G)]
+    Rs = [prng.normal(800 + g, (M, N)) for g in range(G)]
+    dA = _upload(dev, *As)
+    dB = _upload(dev, *Bs)
+    db = _upload(dev, *bs)
+    dR = _upload(dev, *Rs)
+    dC = [dev.alloc(M * N * 4) for _ in range(G)]
+    case("gemm grouped")
+    dev.gemm_grouped(dC, dA, dB, M, K, N, biases=db, act=ACT_RELU, residuals=dR)
+    for g in range(G):
+        ref = oracle.relu(oracle.matmul(As[g], Bs[g]) + bs[g].astype(np.float64)) + Rs[g]
+        got = dev.download(dC[g], (M, N))
+        assert oracle.normwise_error(got, ref) <= oracle.tolerance(K), g
+
+
+def test_gemm_deterministic(dev):
+    M = K = N = 512
+    A, B = prng.normal(1, (M, K)), prng.normal(2, (K, N))
+    dA, dB = _upload(dev, A, B)
+    dC = dev.alloc(M * N * 4)
+    case("gemm determinism")
+    dev.gemm(dC, dA, dB, M, K, N)
+    first = dev.download(dC, (M, N))
+    dev.gemm(dC, dA, dB, M, K, N)
+    second = dev.download(dC, (M, N))
+    assert np.array_equal(first.view(np.uint32), second.view(np.uint32))
+
+
+def test_gemm_nan_inf_propagation(dev):
+    # S9/examples/audit_nan_injection.c:13-50: ones . (NaN/Inf alternating)
+    # -> MATMUL NaN in even columns, Inf in odd; ReLU maps NaN to 0 -> 512 of
+    # 1024 outputs stay non-finite.
+    x = np.ones((32, 32), np.float32)
+    w = np.where(np.arange(32 * 32).reshape(32, 32) % 2 == 0, np.nan, np.inf).astype(np.float32)
+    dx, dw = _upload(dev, x, w)
+    dC = dev.alloc(32 * 32 * 4)
+    case("gemm nan/inf")
+    dev.gemm(dC, dx, dw, 32, 32, 32, act=ACT_RELU)
+    got = dev.download(dC, (32, 32))
+    assert int(np.sum(~np.isfinite(got))) == 512
+    assert np.all(got[:, 0::2] == 0.0) and np.all(np.isposinf(got[:, 1::2]))
+
+
+def test_kernel_matmul_f32_bridge(dev):
+    # The reference-declared host-pointer symbol (lancius_kernels.h:55);
+    # audit_ffi closed form: [[-1,2,3],[4,-5,6]] . ones(3,4) = rows of 4 and 5.
+    import ctypes as C
+
+    a = np.array([[-1, 2, 3], [4, -5, 6]], np.float32)
+    b = np.ones((3, 4), np.float32)
+    out = np.zeros((2, 4), np.float32)
+    case("kernel_matmul_f32 bridge")
+    dev.lib.kernel_matmul_f32(out.ctypes.data_as(C.c_void_p), a.ctypes.data_as(C.c_void_p),
+                              b.ctypes.data_as(C.c_void_p), 2, 3, 4)
+    assert dev.lib.lancius_hip_last_status() == 0
+    assert out.tolist() == [[4, 4, 4, 4], [5, 5, 5, 5]]
+
+
+# ---- attention ---------------------------------------------------------------
+
+
+def _attn_case(dev, B, S, H, D, causal, seed, batches=None, rows=None):
+    q = prng.normal(seed, (B, S, H, D))
+    k = prng.normal(seed + 1, (B, S, H, D))
+    v = prng.normal(seed + 2, (B, S, H, D))
+    dq, dk, dv = _upload(dev, q, k, v)
+    do = dev.alloc(q.nbytes)
+    case(f"attention B={B} S={S} H={H} D={D} causal={causal}")
+    dev.attention(do, dq, dk, dv, B, S, H, D, causal=causal)
+    got = dev.download(do, q.shape)
+    ref = oracle.attention(q, k, v, causal=causal, batches=batches, rows=rows)
+    for b in (dq, dk, dv, do):
+        b.free()
+    bs = slice(*batches) if batches else slice(None)
+    rs = slice(*rows) if rows else slice(None)
+    return got[bs, rs], ref[bs, rs]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,S,H,D", [(1, 1, 1, 64), (1, 17, 2, 8), (2, 65, 3, 64), (1, 130, 2, 64),
+                                     (1, 200, 2, 32), (2, 256, 4, 64)])
+def test_attention_shapes(dev, B, S, H, D, causal):
+    got, ref = _attn_case(dev, B, S, H, D, causal, seed=900 + S)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(max(S, D))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_config_s512(dev, causal):
+    got, ref = _attn_case(dev, 8, 512, 16, 64, causal, seed=44, batches=(0, 1))
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(512)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_config_s2048_sampled(dev, causal):
+    got, ref = _attn_case(dev, 8, 2048, 16, 64, causal, seed=44, batches=(7, 8), rows=(1792, 2048))
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(2048)
+
+
+def test_attention_closed_forms(dev):
+    # V constant => output constant; S = 1 => out = v0 (audit_flash_attention semantics)
+    B, S, H, D = 1, 96, 2, 64
+    q = prng.normal(5, (B, S, H, D))
+    k = prng.normal(6, (B, S, H, D))
+    v = np.full((B, S, H, D), 0.375, np.float32)
+    dq, dk, dv = _upload(dev, q, k, v)
+    do = dev.alloc(q.nbytes)
+    case("attention closed forms")
+    dev.attention(do, dq, dk, dv, B, S, H, D, causal=True)
+    assert np.allclose(dev.download(do, q.shape), 0.375, rtol=0, atol=1e-6)
+    # q = 0 with causal mask: output row i is the mean of v[0..i]
+    v = prng.normal(8, (B, S, H, D))
+    dev.write(dq, np.zeros_like(q))
+    dev.write(dv, v)
+    dev.attention(do, dq, dk, dv, B, S, H, D, causal=True)
+    prefix_mean = np.cumsum(v.astype(np.float64), axis=1) / np.arange(1, S + 1)[None, :, None, None]
+    assert oracle.normwise_error(dev.download(do, q.shape), prefix_mean) <= 1e-5
+
+
+def test_attention_grouped(dev):
+    G, S, H, D = 4, 192, 4, 64
+    qs = [prng.normal(10 + g, (S, H, D)) for g in range(G)]
+    ks = [prng.normal(20 + g, (S, H, D)) for g in range(G)]
+    vs = [prng.normal(30 + g, (S, H, D)) for g in range(G)]
+    dq, dk, dv = _upload(dev, *qs), _upload(dev, *ks), _upload(dev, *vs)
+    do = [dev.alloc(qs[0].nbytes) for _ in range(G)]
+    case("attention grouped")
+    dev.attention_grouped(do, dq, dk, dv, S, H, D, causal=True)
+    for g in range(G):
+        ref = oracle.attention(qs[g], ks[g], vs[g], causal=True)
+        assert oracle.normwise_error(dev.download(do[g], (S, H, D)), ref) <= oracle.tolerance(S)
+
+
+# ---- conv2d ------------------------------------------------------------------
+
+
+def _conv_case(dev, N, C_in, H, W, C_out, KH, KW, stride, pad, relu, seed, images=None):
+    x = prng.normal(seed, (N, C_in, H, W))
+    w = prng.normal(seed + 1, (C_out, C_in, KH, KW), std=float(np.sqrt(2.0 / (KH * KW * C_in))))
+    dx, dw = _upload(dev, x, w)
+    Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    do = dev.alloc(N * C_out * Ho * Wo * 4)
+    case(f"conv N={N} C_in={C_in} {H}x{W} C_out={C_out} k={KH}x{KW} s={stride} p={pad} relu={relu}")
+    dev.conv2d(do, dx, dw, None, N, C_in, H, W, C_out, KH, KW, stride, pad, ACT_RELU if relu else ACT_NONE)
+    got = dev.download(do, (N, C_out, Ho, Wo))
+    ref = oracle.conv2d(x, w, stride, pad, relu, images=images)
+    for b in (dx, dw, do):
+        b.free()
+    sel = slice(*images) if images else slice(None)
+    return got[sel], ref[sel]
+
+
+@pytest.mark.parametrize("N,C_in,H,W,C_out,KH,KW,stride,pad,relu", [
+    (1, 1, 5, 5, 1, 3, 3, 1, 1, False),
+    (2, 3, 7, 7, 5, 3, 3, 1, 1, True),
+    (2, 3, 9, 8, 4, 3, 3, 2, 0, False),
+    (1, 4, 6, 6, 8, 1, 1, 1, 0, True),
+    (2, 3, 11, 10, 6, 5, 5, 2, 2, True),
+    (3, 16, 14, 14, 130, 3, 3, 1, 1, True),
+    (1, 8, 32, 32, 64, 3, 3, 1, 1, False),
+])
+def test_conv_shapes(dev, N, C_in, H, W, C_out, KH, KW, stride, pad, relu):
+    got, ref = _conv_case(dev, N, C_in, H, W, C_out, KH, KW, stride, pad, relu, seed=300 + H + C_out)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(C_in * KH * KW)
+
+
+def test_conv_config_sampled(dev):
+    got, ref = _conv_case(dev, 32, 64, 56, 56, 128, 3, 3, 1, 1, True, seed=45, images=(30, 32))
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(64 * 9)
+
+
+def test_conv_bias(dev):
+    N, C_in, H, W, C_out = 2, 4, 9, 9, 6
+    x = prng.normal(71, (N, C_in, H, W))
+    w = prng.normal(72, (C_out, C_in, 3, 3))
+    b = prng.normal(73, (C_out,))
+    dx, dw, db = _upload(dev, x, w, b)
+    do = dev.alloc(N * C_out * H * W * 4)
+    case("conv bias")
+    dev.conv2d(do, dx, dw, db, N, C_in, H, W, C_out, 3, 3, 1, 1, ACT_RELU)
+    ref = oracle.relu(oracle.conv2d(x, w, 1, 1, False) + b.astype(np.float64)[None, :, None, None])
+    assert oracle.normwise_error(dev.download(do, (N, C_out, H, W)), ref) <= oracle.tolerance(36)
+
+
+# ---- row and elementwise ops -----------------------------------------------------
+
+
+@pytest.mark.parametrize("rows,hidden", [(4096, 1024), (7, 100), (3, 256), (5, 4096), (2, 1)])
+def test_layernorm(dev, rows, hidden):
+    x = prng.normal(11, (rows, hidden), mean=0.5, std=2.0)
+    g = prng.normal(12, (hidden,), mean=1.0, std=0.1)
+    b = prng.normal(13, (hidden,), std=0.1)
+    dx, dg, db = _upload(dev, x, g, b)
+    do = dev.alloc(x.nbytes)
+    case(f"layernorm {rows}x{hidden}")
+    dev.layernorm(do, dx, dg, db, rows, hidden)
+    ref = oracle.layernorm(x, g, b)
+    assert oracle.normwise_error(dev.download(do, x.shape), ref) <= oracle.tolerance(hidden)
+
+
+def test_layernorm_constant_row_gives_beta(dev):
+    x = np.full((4, 1024), 3.25, np.float32)
+    g = prng.normal(1, (1024,))
+    b = prng.normal(2, (1024,))
+    dx, dg, db = _upload(dev, x, g, b)
+    do = dev.alloc(x.nbytes)
+    case("layernorm constant row")
+    dev.layernorm(do, dx, dg, db, 4, 1024)
+    assert np.allclose(dev.download(do, x.shape), np.broadcast_to(b, x.shape), atol=1e-6, rtol=0)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 10), (5, 1), (3, 200), (1000, 37)])
+def test_softmax_argmax(dev, rows, cols):
+    x = prng.normal(21, (rows, cols), std=3.0)
+    dx = dev.upload(x)
+    dp = dev.alloc(x.nbytes)
+    di = dev.alloc(rows * 4)
+    case(f"softmax {rows}x{cols}")
+    dev.softmax(dp, di, dx, rows, cols)
+    probs = dev.download(dp, x.shape)
+    idx = dev.download(di, (rows,), np.int32)
+    ref = oracle.softmax(x)
+    assert oracle.normwise_error(probs, ref) <= oracle.tolerance(cols)
+    ref_idx = oracle.argmax(ref)
+    assert np.array_equal(idx, ref_idx)
+
+
+def test_softmax_ties_first_max(dev):
+    x = np.zeros((4, 10), np.float32)
+    x[1, 3] = x[1, 7] = 2.0
+    x[2, 9] = 1.0
+    dx = dev.upload(x)
+    dp = dev.alloc(x.nbytes)
+    di = dev.alloc(16)
+    case("softmax ties")
+    dev.softmax(dp, di, dx, 4, 10)
+    assert dev.download(di, (4,), np.int32).tolist() == [0, 3, 9, 0]
+    assert np.allclose(dev.download(dp, x.shape)[0], 0.1, atol=1e-7)
+
+
+def test_elementwise(dev):
+    n = 1_000_003
+    a = prng.normal(31, (n,), std=60.0)
+    a[:6] = [np.nan, np.inf, -np.inf, 150.0, -150.0, 0.0]
+    b = prng.normal(32, (n,))
+    da, db = _upload(dev, a, b)
+    do = dev.alloc(a.nbytes)
+    case("elementwise add/relu/gelu/copy")
+    dev.add(do, da, db, n)
+    assert oracle.normwise_error(dev.download(do, (n,))[6:], oracle.add(a, b)[6:]) <= TOL_ELEMENTWISE
+    dev.relu(do, da, n)
+    got = dev.download(do, (n,))
+    assert got[0] == 0.0 and np.isposinf(got[1]) and got[2] == 0.0
+    assert np.array_equal(got[3:], oracle.relu(a)[3:].astype(np.float32))
+    dev.gelu(do, da, n)
+    got = dev.download(do, (n,))
+    ref = oracle.gelu(a)
+    assert np.isnan(got[0]) and got[1] == 100.0 and got[2] == 0.0 and got[3] == 100.0 and got[4] == 0.0
+    assert got[5] == 0.0
+    assert oracle.normwise_error(got[1:], ref[1:]) <= TOL_ELEMENTWISE
+    dev.copy(do, db, n)
+    assert np.array_equal(dev.download(do, (n,)), b)
+
+
+def test_broadcast_fill(dev):
+    row = prng.normal(41, (37,))
+    dr = dev.upload(row)
+    do = dev.alloc(50 * 37 * 4)
+    case("broadcast/fill")
+    dev.broadcast(do, dr, 50, 37, 37)
+    assert np.array_equal(dev.download(do, (50, 37)), np.broadcast_to(row, (50, 37)))
+    dev.broadcast(do, dr, 50, 37, 1)
+    assert np.all(dev.download(do, (50, 37)) == row[0])
+    dev.fill(do, 2.5, 50 * 37)
+    assert np.all(dev.download(do, (50, 37)) == 2.5)
