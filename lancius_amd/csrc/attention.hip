@@ -39,6 +39,7 @@ struct AttnParams {
     int causal;
     float qscale;  // scale * log2(e)
     int q_tiles;
+    int Z;         // count * batch independent [S, H, D] problems
 };
 
 constexpr int kD = 64;
@@ -51,11 +52,19 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     __shared__ __attribute__((aligned(16))) float Ks[2][kBKV][kLDK];
     __shared__ __attribute__((aligned(16))) float Vs[2][kBKV][kLDV];
 
-    const int z = blockIdx.z;
+    // 1-D task order, query-tile major: consecutive ids (which the hardware
+    // deals round-robin to the 8 XCDs) are different (batch, head) problems of
+    // the same query tile.  Every XCD therefore gets the same mix of causal
+    // tile lengths (longest first) and always the same (batch, head) subset,
+    // whose K/V stay in its L2.
+    const int hz = p.H * p.Z;
+    const int task = (int)blockIdx.x;
+    const int t_rank = task / hz;
+    const int rem = task - t_rank * hz;
+    const int z = rem / p.H;
+    const int h = rem - z * p.H;
     const int g = z / p.batch, b = z % p.batch;
-    const int h = blockIdx.y;
-    // Causal: the tiles with the most keys start first.
-    const int qt = p.causal ? (p.q_tiles - 1 - (int)blockIdx.x) : (int)blockIdx.x;
+    const int qt = p.causal ? (p.q_tiles - 1 - t_rank) : t_rank;
     const int S = p.S, H = p.H;
     const size_t row_stride = (size_t)H * kD;
     const size_t base = ((size_t)b * S * H + h) * kD;
@@ -294,9 +303,12 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
     p.causal = causal ? 1 : 0;
     p.qscale = scale * 1.4426950408889634f;  // log2(e)
     const unsigned z = (unsigned)(count * batch);
+    p.Z = (int)z;
     if (D == kD && vec) {
         p.q_tiles = (int)((S + kBQ - 1) / kBQ);
-        hipLaunchKernelGGL(attention_d64, dim3((unsigned)p.q_tiles, (unsigned)H, z), dim3(256), 0, ctx->stream, p);
+        const size_t tasks = (size_t)p.q_tiles * H * z;
+        LANCIUS_REQUIRE(tasks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention: too many tiles");
+        hipLaunchKernelGGL(attention_d64, dim3((unsigned)tasks), dim3(256), 0, ctx->stream, p);
         if (int rc = check_launch("attention_d64")) return rc;
     } else {
         hipLaunchKernelGGL(attention_rowwise, dim3(ceil_div(S * H, 256), 1, z), dim3(256), 0, ctx->stream, p);

@@ -40,6 +40,37 @@ int check_launch(const char* kernel) {
     return 0;
 }
 
+int tune(const char* key, int fallback) {
+    static const char* env = getenv("LANCIUS_HIP_TUNE");
+    if (!env || !key) return fallback;
+    const size_t n = strlen(key);
+    for (const char* p = env; p && *p;) {
+        if (strncmp(p, key, n) == 0 && p[n] == '=') return atoi(p + n + 1);
+        p = strchr(p, ',');
+        if (p) ++p;
+    }
+    return fallback;
+}
+
+int workspace(lancius_hip_ctx* ctx, size_t bytes, void** out) {
+    *out = nullptr;
+    if (bytes <= ctx->workspace_bytes && ctx->workspace) {
+        *out = ctx->workspace;
+        return 0;
+    }
+    if (ctx->workspace) {
+        LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "workspace sync");
+        LANCIUS_HIP_TRY(hipFree(ctx->workspace), "workspace free");
+        ctx->workspace = nullptr;
+        ctx->workspace_bytes = 0;
+    }
+    const size_t want = (bytes + ((size_t)1 << 20) - 1) & ~(((size_t)1 << 20) - 1);
+    LANCIUS_HIP_TRY(hipMalloc(&ctx->workspace, want), "workspace hipMalloc");
+    ctx->workspace_bytes = want;
+    *out = ctx->workspace;
+    return 0;
+}
+
 int bind_device(lancius_hip_ctx* ctx) {
     int cur = -1;
     LANCIUS_HIP_TRY(hipGetDevice(&cur), "hipGetDevice");
@@ -90,6 +121,7 @@ void lancius_hip_ctx_destroy(lancius_hip_ctx* ctx) {
     if (!ctx) return;
     (void)bind_device(ctx);
     (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->workspace) (void)hipFree(ctx->workspace);
     (void)hipEventDestroy(ctx->ev_start);
     (void)hipEventDestroy(ctx->ev_stop);
     free(ctx);

@@ -14,6 +14,8 @@ struct lancius_hip_ctx {
     hipEvent_t ev_start;
     hipEvent_t ev_stop;
     int timer_armed;
+    void* workspace;        // split-K partials, transposed conv weights
+    size_t workspace_bytes;
 };
 
 namespace lancius {
@@ -30,6 +32,17 @@ int check_launch(const char* kernel);
 
 // Makes `ctx->device` current for the calling thread.
 int bind_device(lancius_hip_ctx* ctx);
+
+// Tuning override read once from the environment variable LANCIUS_HIP_TUNE,
+// a comma-separated list of key=value integers (e.g. "conv_bn=64,gemm=2").
+// Returns `fallback` for keys that are not set.  Used to sweep launch shapes
+// on hardware; the defaults are the measured best.
+int tune(const char* key, int fallback);
+
+// Device scratch owned by the context, grown with hipMalloc on demand and
+// kept until the context is destroyed.  Calls on one context are ordered by
+// its stream, so one buffer serves every kernel of the context.
+int workspace(lancius_hip_ctx* ctx, size_t bytes, void** out);
 
 static inline unsigned int ceil_div(size_t a, size_t b) { return (unsigned int)((a + b - 1) / b); }
 

@@ -16,6 +16,8 @@
 // coalesce along W.  The MFMA tiling, double-buffered LDS and k-major layout
 // are those of the GEMM kernel; the epilogue writes Out[n][co][ho][wo], where
 // lanes 0..31 of a register cover 32 consecutive pixels of one channel.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -26,6 +28,7 @@ struct ConvParams {
     float* out;
     const float* in;
     const float* w;
+    const float* wt;   // weights re-laid k-major: wt[(tap*C_in + ci)*C_out + co] (CI_INNER path)
     const float* bias;
     int N, C_in, H, W, C_out, KH, KW, stride, pad, Ho, Wo;
     int Kdim;          // C_in * KH * KW
@@ -38,7 +41,7 @@ constexpr int kThreads = 256;
 
 // KH_T/KW_T > 0 fixes the filter size at compile time (cheap k decomposition);
 // 0 means runtime values.
-template <int BM, int BN, int BK, int WGM, int WGN, int KH_T, int KW_T>
+template <int BM, int BN, int BK, int WGM, int WGN, int KH_T, int KW_T, bool CI_INNER>
 __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParams p) {
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -88,36 +91,73 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
 
     constexpr int A_ELEMS = BM * BK / kThreads;
     static_assert(A_ELEMS * kThreads == BM * BK, "even A split");
-    float a_s[A_ELEMS];
+    constexpr int A4 = BM * BK / 4;                        // float4 of one A tile
+    constexpr int A_VEC = (A4 + kThreads - 1) / kThreads;  // float4 per thread (CI_INNER)
+    float a_s[CI_INNER ? 1 : A_ELEMS];
+    f32x4 a_v[A_VEC];
     float b_s[B_ELEMS];
 
-    auto load_tile = [&](int k0) {
+    // CI_INNER: the reduction runs over (kh, kw, ci) with ci innermost, so a
+    // k-tile is BK channels of one filter tap: one bounds test per tile and
+    // channel addresses base + ci*H*W.  Otherwise k = (ci, kh, kw) as stored.
+    const int ctiles = p.C_in / BK;
+    const size_t HW = (size_t)H * W;
+    auto load_tile = [&](int kt) {
+        if constexpr (CI_INNER) {
+            const int tap = kt / ctiles;
+            const int ci0 = (kt - tap * ctiles) * BK;
+            const int kh = tap / KW, kw = tap - (tap / KW) * KW;
+            // A tile straight from the k-major weights: rows k, float4 along co.
+            const float* wrow = p.wt + (size_t)(tap * p.C_in + ci0) * C_out + m0;
 #pragma unroll
-        for (int i = 0; i < A_ELEMS; ++i) {
-            const int idx = tid + i * kThreads;
-            const int r = idx / BK, c = idx % BK;
-            const int co = m0 + r, k = k0 + c;
-            a_s[i] = (co < C_out && k < Kdim) ? wgt[(size_t)co * Kdim + k] : 0.0f;
-        }
-#pragma unroll
-        for (int i = 0; i < B_ELEMS; ++i) {
-            const int k = k0 + kk0 + i * K_STEP;
-            float v = 0.0f;
-            if (p_valid && k < Kdim) {
-                const int ci = k / KHW;
-                const int r = k - ci * KHW;
-                const int kh = r / KW, kw = r - (r / KW) * KW;
-                const int hi = hi0 + kh, wi = wi0 + kw;
-                if (hi >= 0 && hi < H && wi >= 0 && wi < W) v = x_img[((size_t)ci * H + hi) * W + wi];
+            for (int i = 0; i < A_VEC; ++i) {
+                const int idx = tid + i * kThreads;
+                const int c = idx / (BM / 4), rq = idx % (BM / 4);
+                a_v[i] = (idx < A4 && m0 + 4 * rq < C_out) ? *(const f32x4*)(wrow + (size_t)c * C_out + 4 * rq)
+                                                          : f32x4{0.f, 0.f, 0.f, 0.f};
             }
-            b_s[i] = v;
+            const int hi = hi0 + kh, wi = wi0 + kw;
+            const bool inside = p_valid && hi >= 0 && hi < H && wi >= 0 && wi < W;
+            const float* src = x_img + (inside ? (size_t)hi * W + wi : 0) + (size_t)(ci0 + kk0) * HW;
+#pragma unroll
+            for (int i = 0; i < B_ELEMS; ++i) b_s[i] = inside ? src[(size_t)(i * K_STEP) * HW] : 0.0f;
+        } else {
+            const int k0 = kt * BK;
+#pragma unroll
+            for (int i = 0; i < A_ELEMS; ++i) {
+                const int idx = tid + i * kThreads;
+                const int r = idx / BK, c = idx % BK;
+                const int co = m0 + r, k = k0 + c;
+                a_s[i] = (co < C_out && k < Kdim) ? wgt[(size_t)co * Kdim + k] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < B_ELEMS; ++i) {
+                const int k = k0 + kk0 + i * K_STEP;
+                float v = 0.0f;
+                if (p_valid && k < Kdim) {
+                    const int ci = k / KHW;
+                    const int r = k - ci * KHW;
+                    const int kh = r / KW, kw = r - (r / KW) * KW;
+                    const int hi = hi0 + kh, wi = wi0 + kw;
+                    if (hi >= 0 && hi < H && wi >= 0 && wi < W) v = x_img[((size_t)ci * H + hi) * W + wi];
+                }
+                b_s[i] = v;
+            }
         }
     };
     auto store_tile = [&](int buf) {
+        if constexpr (CI_INNER) {
 #pragma unroll
-        for (int i = 0; i < A_ELEMS; ++i) {
-            const int idx = tid + i * kThreads;
-            As[buf][idx % BK][idx / BK] = a_s[i];
+            for (int i = 0; i < A_VEC; ++i) {
+                const int idx = tid + i * kThreads;
+                if (idx < A4) *(f32x4*)&As[buf][idx / (BM / 4)][4 * (idx % (BM / 4))] = a_v[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < A_ELEMS; ++i) {
+                const int idx = tid + i * kThreads;
+                As[buf][idx % BK][idx / BK] = a_s[i];
+            }
         }
 #pragma unroll
         for (int i = 0; i < B_ELEMS; ++i) Bs[buf][kk0 + i * K_STEP][pp] = b_s[i];
@@ -131,14 +171,14 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int ktiles = (Kdim + BK - 1) / BK;
+    const int ktiles = CI_INNER ? KHW * ctiles : (Kdim + BK - 1) / BK;
     load_tile(0);
     store_tile(0);
     __syncthreads();
     for (int kt = 0; kt < ktiles; ++kt) {
         const int cur = kt & 1;
         const bool more = kt + 1 < ktiles;
-        if (more) load_tile((kt + 1) * BK);
+        if (more) load_tile(kt + 1);
 #pragma unroll
         for (int kp = 0; kp < BK / 2; ++kp) {
             float af[TM], bf[TN];
@@ -182,17 +222,56 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
     }
 }
 
+// wt[(tap*C_in + ci)*C_out + co] = w[(co*C_in + ci)*KHW + tap]: the OIHW
+// weights re-laid with the reduction index (tap, ci) major and C_out
+// contiguous, so the conv's A tiles are plain float4 row copies.
+__global__ void __launch_bounds__(256) conv_weights_kmajor(float* __restrict__ wt, const float* __restrict__ w,
+                                                           int C_out, int C_in, int KHW) {
+    const size_t total = (size_t)C_out * C_in * KHW;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x; d < total; d += stride) {
+        const int co = (int)(d % C_out);
+        const size_t kk = d / C_out;
+        const int ci = (int)(kk % C_in), tap = (int)(kk / C_in);
+        wt[d] = w[((size_t)co * C_in + ci) * KHW + tap];
+    }
+}
+
 template <int BM, int BN, int KH_T, int KW_T>
 int launch(lancius_hip_ctx* ctx, ConvParams& p) {
     p.tiles_m = (uint32_t)((p.C_out + BM - 1) / BM);
     p.tiles_n = (uint32_t)((p.Ptotal + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d: too many tiles");
-    constexpr int WGM = BM >= 128 ? 2 : 1;
+    constexpr int WGM = BM >= 64 ? 2 : 1;
     constexpr int WGN = 4 / WGM;
-    hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T>), dim3((unsigned)grid),
-                       dim3(kThreads), 0, ctx->stream, p);
+    if (p.C_in % 16 == 0 && p.C_out % 4 == 0) {
+        const size_t wbytes = (size_t)p.C_out * p.Kdim * sizeof(float);
+        void* ws = nullptr;
+        if (int rc = workspace(ctx, wbytes, &ws)) return rc;
+        p.wt = (const float*)ws;
+        const size_t total = (size_t)p.C_out * p.Kdim;
+        hipLaunchKernelGGL(conv_weights_kmajor, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)),
+                           dim3(256), 0, ctx->stream, (float*)ws, p.w, p.C_out, p.C_in, p.KH * p.KW);
+        if (int rc = check_launch("conv_weights_kmajor")) return rc;
+    }
+    if (p.wt)
+        hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
+                           dim3(kThreads), 0, ctx->stream, p);
+    else
+        hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, false>), dim3((unsigned)grid),
+                           dim3(kThreads), 0, ctx->stream, p);
     return check_launch("conv2d_implicit_gemm");
+}
+
+template <int KH_T, int KW_T>
+int launch_tile(lancius_hip_ctx* ctx, ConvParams& p, int tile) {
+    switch (tile) {
+        case 1: return launch<128, 64, KH_T, KW_T>(ctx, p);
+        case 2: return launch<64, 64, KH_T, KW_T>(ctx, p);
+        case 3: return launch<32, 128, KH_T, KW_T>(ctx, p);
+        default: return launch<128, 128, KH_T, KW_T>(ctx, p);
+    }
 }
 
 }  // namespace
@@ -233,17 +312,10 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     p.Kdim = (int)(C_in * K_h * K_w);
     p.Ptotal = (long long)N * p.Ho * p.Wo;
     p.act = act;
-    int rc;
-    if (C_out > 64) {
-        if (K_h == 3 && K_w == 3)
-            rc = launch<128, 128, 3, 3>(ctx, p);
-        else
-            rc = launch<128, 128, 0, 0>(ctx, p);
-    } else {
-        if (K_h == 3 && K_w == 3)
-            rc = launch<32, 128, 3, 3>(ctx, p);
-        else
-            rc = launch<32, 128, 0, 0>(ctx, p);
-    }
+    // Tiles (C_out x pixels): 0 = 128x128, 1 = 128x64, 2 = 64x64, 3 = 32x128.
+    // 128x64 measured best on the N32 64->128 56x56 config (78.6 TFLOP/s vs
+    // 72.3 for 128x128): twice the workgroups, a shorter tail.
+    const int tile = tune("conv_tile", C_out > 64 ? 1 : 3);
+    const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
     return rc ? rc : ok();
 }

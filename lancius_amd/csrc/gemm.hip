@@ -16,6 +16,8 @@
 //    the single store of C (the BROADCAST + ADD + activation nodes of a graph).
 //  * Workgroup ids are renumbered XCD-contiguously and rastered in groups of
 //    tile-rows so that each XCD's L2 sees a compact set of A/B panels.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -31,11 +33,18 @@ struct GemmParams {
     int M, N, K;
     int act;
     uint32_t tiles_m, tiles_n;
+    float* ws;   // split-K partials [count][splits][M][N]
+    int splits;  // K ranges (blockIdx.y), 1 = no split
+    int kchunk;  // K per split, a multiple of the k-tile
 };
 
 constexpr int kThreads = 256;
 
-template <int BM, int BN, int BK, int WGM, int WGN, bool VEC>
+// SPLIT: the workgroup reduces K range [y*kchunk, (y+1)*kchunk) and stores its
+// raw partial sums; splitk_reduce adds the partials in order y = 0, 1, ...
+// (a fixed order, so results are run-to-run identical) and applies the
+// epilogue.
+template <int BM, int BN, int BK, int WGM, int WGN, bool VEC, bool SPLIT>
 __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
     static_assert(WGM * WGN == 4, "4 waves per workgroup");
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -150,14 +159,18 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int ktiles = (K + BK - 1) / BK;
-    load_tile(0);
+    int kt0 = 0, kt1 = (K + BK - 1) / BK;
+    if constexpr (SPLIT) {
+        kt0 = (int)blockIdx.y * (p.kchunk / BK);
+        kt1 = min(kt1, kt0 + p.kchunk / BK);
+    }
+    load_tile(kt0 * BK);
     store_tile(0);
     __syncthreads();
 
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < ktiles;
+    for (int kt = kt0; kt < kt1; ++kt) {
+        const int cur = (kt - kt0) & 1;
+        const bool more = kt + 1 < kt1;
         if (more) load_tile((kt + 1) * BK);
 #pragma unroll
         for (int kp = 0; kp < BK / 2; ++kp) {
@@ -179,6 +192,24 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
     // ---- epilogue: bias, activation, residual, one store -----------------
     // Accumulator layout of v_mfma_f32_32x32x2_f32: register r of lane l holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of the 32x32 sub-tile.
+    if constexpr (SPLIT) {
+        float* __restrict__ part = p.ws + ((size_t)g * p.splits + blockIdx.y) * (size_t)M * N;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * WN + j * 32 + lr;
+            if (col >= N) continue;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = rbase + 8 * (r >> 2) + (r & 3);
+                    if (row < M) part[(size_t)row * N + col] = acc[i][j][r];
+                }
+            }
+        }
+        return;
+    }
     const float* __restrict__ bias = p.bias[g];
     const int act = p.act;
 #pragma unroll
@@ -204,23 +235,57 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
     }
 }
 
-struct TileCfg {
-    int bm, bn;
-};
+// Sums split-K partials in split order and applies the epilogue.
+__global__ void __launch_bounds__(256) splitk_reduce(const GemmParams p, int count) {
+    const size_t MN = (size_t)p.M * p.N;
+    const size_t total = (size_t)count * MN;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int g = (int)(idx / MN);
+        const size_t e = idx - (size_t)g * MN;
+        const float* part = p.ws + (size_t)g * p.splits * MN + e;
+        float s = 0.0f;
+        for (int y = 0; y < p.splits; ++y) s += part[(size_t)y * MN];
+        const int col = (int)(e % p.N);
+        if (p.bias[g]) s += p.bias[g][col];
+        s = apply_act(s, p.act);
+        if (p.R[g]) s += p.R[g][e];
+        p.C[g][e] = s;
+    }
+}
 
 template <int BM, int BN, int BK, int WGM, int WGN>
 int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
     p.tiles_m = (uint32_t)((p.M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((p.N + BN - 1) / BN);
-    dim3 grid(p.tiles_m * p.tiles_n, 1, (unsigned)count);
-    if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true>), grid, dim3(kThreads), 0, ctx->stream, p);
+    dim3 grid(p.tiles_m * p.tiles_n, (unsigned)p.splits, (unsigned)count);
+    const bool split = p.splits > 1;
+    if (vec && split)
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true>), grid, dim3(kThreads), 0, ctx->stream,
+                           p);
+    else if (vec)
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false>), grid, dim3(kThreads), 0,
+                           ctx->stream, p);
+    else if (split)
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true>), grid, dim3(kThreads), 0,
+                           ctx->stream, p);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false>), grid, dim3(kThreads), 0, ctx->stream, p);
-    return check_launch("gemm_f32_mfma");
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, false>), grid, dim3(kThreads), 0,
+                           ctx->stream, p);
+    if (int rc = check_launch("gemm_f32_mfma")) return rc;
+    if (split) {
+        const size_t total = (size_t)count * p.M * p.N;
+        const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+        hipLaunchKernelGGL(splitk_reduce, dim3(blocks), dim3(256), 0, ctx->stream, p, count);
+        if (int rc = check_launch("splitk_reduce")) return rc;
+    }
+    return 0;
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
+
+constexpr int kBK = 16;
+constexpr size_t kMaxSplitBytes = (size_t)256 << 20;
 
 int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
                   const float* const* B, size_t M, size_t K, size_t N, const float* const* bias, int act,
@@ -251,14 +316,37 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     p.K = (int)K;
     p.act = act;
 
-    // Tile choice: the 128x128 tile when it yields enough workgroups to cover
-    // the 256 CUs, else 64x64.
+    // Tile: 128x128 when that alone gives >= 256 workgroups (one per CU),
+    // else 64x64.  Split-K when the 64x64 grid still leaves CUs idle and K is
+    // long enough: enough K ranges for ~512 workgroups, each >= 128 deep.
     const size_t big_tiles = count * ((M + 127) / 128) * ((N + 127) / 128);
-    int rc;
-    if (big_tiles >= 256)
-        rc = launch_cfg<128, 128, 16, 2, 2>(ctx, p, (int)count, vec);
-    else
-        rc = launch_cfg<64, 64, 16, 2, 2>(ctx, p, (int)count, vec);
+    const size_t small_tiles = count * ((M + 63) / 64) * ((N + 63) / 64);
+    const int tile_sel = tune("gemm_tile", 0);  // 0 auto, 1 = 128x128, 2 = 64x64
+    const bool big = tile_sel == 1 || (tile_sel == 0 && big_tiles >= 256);
+    const size_t tiles = big ? big_tiles : small_tiles;
+    const size_t ktiles = (K + kBK - 1) / kBK;
+    size_t splits = (size_t)tune("gemm_split", 0);
+    if (splits == 0) {
+        splits = 1;
+        if (tiles < 256 && ktiles >= 16) splits = std::min<size_t>({(512 + tiles - 1) / tiles, ktiles / 8, 16});
+    }
+    splits = std::max<size_t>(1, std::min(splits, ktiles));
+    size_t chunk_tiles = (ktiles + splits - 1) / splits;
+    splits = (ktiles + chunk_tiles - 1) / chunk_tiles;  // no empty K range
+    while (splits > 1 && count * splits * M * N * sizeof(float) > kMaxSplitBytes) {
+        splits = (splits + 1) / 2;
+        chunk_tiles = (ktiles + splits - 1) / splits;
+        splits = (ktiles + chunk_tiles - 1) / chunk_tiles;
+    }
+    p.splits = (int)splits;
+    p.kchunk = (int)(chunk_tiles * kBK);
+    if (splits > 1) {
+        void* ws = nullptr;
+        if (int rc = workspace(ctx, count * splits * M * N * sizeof(float), &ws)) return rc;
+        p.ws = (float*)ws;
+    }
+    const int rc = big ? launch_cfg<128, 128, kBK, 2, 2>(ctx, p, (int)count, vec)
+                       : launch_cfg<64, 64, kBK, 2, 2>(ctx, p, (int)count, vec);
     return rc ? rc : ok();
 }
 
