@@ -98,6 +98,54 @@ def conv_case(dev, steps, warmup):
     return ms, flops, 4.0 * (N * C_in * H * W + C_out * C_in * 9 + N * C_out * H * W)
 
 
+def rowop_cases(dev, steps, warmup) -> dict:
+    """Memory-bound kernels at the transformer block's shapes; GB/s counts
+    each tensor read and written once."""
+    out = {}
+    rows, hid = 4096, 1024
+    x = dev.upload(prng.normal(47, (rows, hid)))
+    g = dev.upload(np.ones((hid,), np.float32))
+    b = dev.upload(np.zeros((hid,), np.float32))
+    y = dev.alloc(rows * hid * 4)
+    t = time_steps(dev, lambda: dev.layernorm(y, x, g, b, rows, hid), steps, warmup)
+    nb = 8.0 * rows * hid
+    out["layernorm_4096x1024"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
+                                  "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
+    t = time_steps(dev, lambda: dev.softmax(y, None, x, rows, hid), steps, warmup)
+    out["softmax_4096x1024"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
+                                "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
+    n = 4096 * 4096
+    u = dev.upload(prng.normal(48, (n,)))
+    v = dev.upload(prng.normal(49, (n,)))
+    w = dev.alloc(n * 4)
+    t = time_steps(dev, lambda: dev.gelu(w, u, n), steps, warmup)
+    out["gelu_4096x4096"] = {"ms": round(t, 4), "GB/s": round(8.0 * n / t / 1e6, 1),
+                             "frac_hbm": round(8.0 * n / t / 1e6 / PEAK_HBM, 4)}
+    t = time_steps(dev, lambda: dev.add(w, u, v, n), steps, warmup)
+    out["add_4096x4096"] = {"ms": round(t, 4), "GB/s": round(12.0 * n / t / 1e6, 1),
+                            "frac_hbm": round(12.0 * n / t / 1e6 / PEAK_HBM, 4)}
+    for buf in (x, g, b, y, u, v, w):
+        buf.free()
+    return out
+
+
+def bridge_case(dev, n=4096) -> dict:
+    """kernel_matmul_f32 (host pointers): includes both host->device copies and
+    the copy back, so it is PCIe-bound; never the headline."""
+    a = prng.normal(43, (n, n))
+    bm = prng.normal(1043, (n, n))
+    c = np.empty((n, n), np.float32)
+    vp = C.c_void_p
+    dev.lib.kernel_matmul_f32(c.ctypes.data_as(vp), a.ctypes.data_as(vp), bm.ctypes.data_as(vp), n, n, n)
+    t0 = time.perf_counter()
+    reps = 3
+    for _ in range(reps):
+        dev.lib.kernel_matmul_f32(c.ctypes.data_as(vp), a.ctypes.data_as(vp), bm.ctypes.data_as(vp), n, n, n)
+    dt = (time.perf_counter() - t0) / reps
+    return {"ms": round(dt * 1e3, 3), "GFLOP/s": round(2.0 * n ** 3 / dt / 1e9, 1),
+            "note": "host-pointer bridge, PCIe copies of A, B and C included (wall clock)"}
+
+
 def graph_case(dev, bg, feeds, steps, warmup):
     lib = graph_lib()
     lib.lancius_graph_set_dtype(bg.g, abi.DTYPE_FP32)
@@ -235,6 +283,10 @@ def main() -> int:
         t, f, b = conv_case(dev, steps, 3)
         extra["conv3x3_N32_64to128_56x56_relu"] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
                                                    "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
+        log("row and elementwise kernels")
+        extra.update(rowop_cases(dev, max(20, steps), 5))
+        log("host-pointer bridge")
+        extra["kernel_matmul_f32_host_bridge_4096"] = bridge_case(dev)
         log("mlp graph")
         lib = graph_lib()
         bg = graphs.build_mlp(lib)

@@ -71,6 +71,32 @@ int workspace(lancius_hip_ctx* ctx, size_t bytes, void** out) {
     return 0;
 }
 
+__global__ void zero_u32(unsigned* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+int counters(lancius_hip_ctx* ctx, size_t n, unsigned** out) {
+    *out = nullptr;
+    if (n <= ctx->counters_n && ctx->counters) {
+        *out = ctx->counters;
+        return 0;
+    }
+    if (ctx->counters) {
+        LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "counters sync");
+        LANCIUS_HIP_TRY(hipFree(ctx->counters), "counters free");
+        ctx->counters = nullptr;
+        ctx->counters_n = 0;
+    }
+    const size_t want = (n + 4095) & ~(size_t)4095;
+    LANCIUS_HIP_TRY(hipMalloc((void**)&ctx->counters, want * sizeof(unsigned)), "counters hipMalloc");
+    hipLaunchKernelGGL(zero_u32, dim3(64), dim3(256), 0, ctx->stream, ctx->counters, want);
+    if (int rc = check_launch("zero_u32")) return rc;
+    ctx->counters_n = want;
+    *out = ctx->counters;
+    return 0;
+}
+
 int bind_device(lancius_hip_ctx* ctx) {
     int cur = -1;
     LANCIUS_HIP_TRY(hipGetDevice(&cur), "hipGetDevice");
@@ -122,6 +148,7 @@ void lancius_hip_ctx_destroy(lancius_hip_ctx* ctx) {
     (void)bind_device(ctx);
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->counters) (void)hipFree(ctx->counters);
     (void)hipEventDestroy(ctx->ev_start);
     (void)hipEventDestroy(ctx->ev_stop);
     free(ctx);

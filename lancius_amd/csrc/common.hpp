@@ -16,6 +16,8 @@ struct lancius_hip_ctx {
     int timer_armed;
     void* workspace;        // split-K partials, transposed conv weights
     size_t workspace_bytes;
+    unsigned* counters;     // arrival counters of split reductions, kept at zero between calls
+    size_t counters_n;
 };
 
 namespace lancius {
@@ -43,6 +45,10 @@ int tune(const char* key, int fallback);
 // kept until the context is destroyed.  Calls on one context are ordered by
 // its stream, so one buffer serves every kernel of the context.
 int workspace(lancius_hip_ctx* ctx, size_t bytes, void** out);
+
+// At least n zero-initialised arrival counters (see counters in the context);
+// every kernel that increments a counter returns it to zero before exiting.
+int counters(lancius_hip_ctx* ctx, size_t n, unsigned** out);
 
 static inline unsigned int ceil_div(size_t a, size_t b) { return (unsigned int)((a + b - 1) / b); }
 

@@ -235,6 +235,144 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
     }
 }
 
+// Skinny GEMM (M <= 16*MT): the product is bound by reading B once from HBM,
+// so the kernel is organised around that stream.
+//  * A workgroup owns 64 columns and a K slice of 256 rows; each wave takes
+//    64 of those rows and issues all 16 of its B loads before the first MFMA.
+//  * Every B load is a float4: lane l reads row k0 + 4s + l/16, columns
+//    c0 + 4(l%16) .. +3, so 16 lanes stream 256 contiguous bytes of a row and a
+//    wave keeps 16 KB in flight.  Component j feeds its own
+//    v_mfma_f32_16x16x4_f32, whose column index l%16 then stands for column
+//    c0 + 4(l%16) + j; the four MFMAs cover the 64 columns.
+//  * The four waves' partial sums are added through LDS in wave order.  With
+//    several K slices each workgroup stores its partial and splitk_reduce adds
+//    them in slice order (deterministic).  An in-kernel "last workgroup
+//    reduces" scheme would need agent-scope fences, which on this part write
+//    back and invalidate the per-XCD L2 - measured 4x slower.
+template <int MT>
+__global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
+    constexpr int KS = 256;         // K rows per workgroup
+    constexpr int KW = KS / 4;      // per wave
+    constexpr int STEPS = KW / 4;   // MFMA k-steps per wave
+    constexpr int ROWS = 16 * MT;
+    __shared__ float As[ROWS][KS + 1];
+    __shared__ __attribute__((aligned(16))) float red[4][ROWS][64];
+
+    const int g = blockIdx.z, split = blockIdx.y, cb = blockIdx.x;
+    const int M = p.M, N = p.N, K = p.K;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int kl = lane >> 4, cq = lane & 15;
+    const int c0 = cb * 64;
+    const int col4 = c0 + 4 * cq;
+    const int kslice = split * KS;
+    const int kw0 = kslice + wave * KW;
+    const float* __restrict__ A = p.A[g];
+    const float* __restrict__ B = p.B[g];
+
+    f32x4 bv[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        const int k = kw0 + 4 * s + kl;
+        bv[s] = (k < K && col4 < N) ? *(const f32x4*)(B + (size_t)k * N + col4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    constexpr int A_PER = ROWS * KS / 256;
+    float as[A_PER];
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+        const int idx = tid + 256 * i;
+        const int r = idx / KS, c = idx % KS;
+        as[i] = (r < M && kslice + c < K) ? A[(size_t)r * K + kslice + c] : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < A_PER; ++i) {
+        const int idx = tid + 256 * i;
+        As[idx / KS][idx % KS] = as[i];
+    }
+    __syncthreads();
+
+    f32x4 acc[MT][4];
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[t][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            const float av = As[16 * t + cq][wave * KW + 4 * s + kl];
+            acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].x, acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].y, acc[t][1], 0, 0, 0);
+            acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].z, acc[t][2], 0, 0, 0);
+            acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].w, acc[t][3], 0, 0, 0);
+        }
+    }
+    // Accumulator (t, j), register r of lane l: row 16t + 4(l/16) + r,
+    // column c0 + 4(l%16) + j.
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            *(f32x4*)&red[wave][16 * t + 4 * kl + r][4 * cq] =
+                f32x4{acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]};
+    __syncthreads();
+
+    const float* __restrict__ bias = p.bias[g];
+    const float* __restrict__ R = p.R[g];
+    float* __restrict__ C = p.C[g];
+    auto finish = [&](int row, int col, f32x4 v) {
+        float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float y = o[j] + (bias ? bias[col + j] : 0.0f);
+            y = apply_act(y, p.act);
+            if (R) y += R[(size_t)row * N + col + j];
+            o[j] = y;
+        }
+        *(f32x4*)(C + (size_t)row * N + col) = f32x4{o[0], o[1], o[2], o[3]};
+    };
+    const size_t MN = (size_t)M * N;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+        const int e4 = tid + 256 * i;
+        const int row = e4 / 16, col = c0 + 4 * (e4 % 16);
+        if (row >= M || col >= N) continue;
+        const int cc = 4 * (e4 % 16);
+        f32x4 v = *(const f32x4*)&red[0][row][cc];
+        v += *(const f32x4*)&red[1][row][cc];
+        v += *(const f32x4*)&red[2][row][cc];
+        v += *(const f32x4*)&red[3][row][cc];
+        if (p.splits == 1)
+            finish(row, col, v);
+        else
+            *(f32x4*)(p.ws + ((size_t)g * p.splits + split) * MN + (size_t)row * N + col) = v;
+    }
+}
+
+// splitk_reduce over float4 groups (N % 4 == 0): same order, same epilogue.
+__global__ void __launch_bounds__(256) splitk_reduce_vec4(const GemmParams p, int count) {
+    const size_t MN = (size_t)p.M * p.N;
+    const size_t total4 = (size_t)count * MN / 4;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i4 = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < total4; i4 += stride) {
+        const size_t idx = 4 * i4;
+        const int g = (int)(idx / MN);
+        const size_t e = idx - (size_t)g * MN;
+        const float* part = p.ws + (size_t)g * p.splits * MN + e;
+        f32x4 s = *(const f32x4*)part;
+        for (int y = 1; y < p.splits; ++y) s += *(const f32x4*)(part + (size_t)y * MN);
+        const int col = (int)(e % p.N);
+        float o[4] = {s.x, s.y, s.z, s.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v = o[j] + (p.bias[g] ? p.bias[g][col + j] : 0.0f);
+            v = apply_act(v, p.act);
+            if (p.R[g]) v += p.R[g][e + j];
+            o[j] = v;
+        }
+        *(f32x4*)(p.C[g] + e) = f32x4{o[0], o[1], o[2], o[3]};
+    }
+}
+
 // Sums split-K partials in split order and applies the epilogue.
 __global__ void __launch_bounds__(256) splitk_reduce(const GemmParams p, int count) {
     const size_t MN = (size_t)p.M * p.N;
@@ -315,6 +453,35 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     p.N = (int)N;
     p.K = (int)K;
     p.act = act;
+
+    // M <= 32 with float4-aligned rows: the HBM-streaming skinny kernel, one
+    // workgroup per (64 columns, 256-row K slice).
+    if (M <= 32 && vec && tune("gemm_skinny", 1)) {
+        const size_t splits = (K + 255) / 256;
+        const size_t col_blocks = (N + 63) / 64;
+        const size_t ws_bytes = splits > 1 ? count * splits * M * N * sizeof(float) : 0;
+        if (ws_bytes <= kMaxSplitBytes && splits < 65536 && col_blocks < kMaxGridX) {
+            if (splits > 1) {
+                void* ws = nullptr;
+                if (int rc = workspace(ctx, ws_bytes, &ws)) return rc;
+                p.ws = (float*)ws;
+            }
+            p.splits = (int)splits;
+            const dim3 grid((unsigned)col_blocks, (unsigned)splits, (unsigned)count);
+            if (M <= 16)
+                hipLaunchKernelGGL(gemm_skinny_f32<1>, grid, dim3(256), 0, ctx->stream, p);
+            else
+                hipLaunchKernelGGL(gemm_skinny_f32<2>, grid, dim3(256), 0, ctx->stream, p);
+            if (int rc = check_launch("gemm_skinny_f32")) return rc;
+            if (splits > 1) {
+                const size_t total4 = count * M * N / 4;
+                hipLaunchKernelGGL(splitk_reduce_vec4, dim3((unsigned)std::min<size_t>((total4 + 255) / 256, 4096)),
+                                   dim3(256), 0, ctx->stream, p, (int)count);
+                if (int rc = check_launch("splitk_reduce_vec4")) return rc;
+            }
+            return ok();
+        }
+    }
 
     // Tile: 128x128 when that alone gives >= 256 workgroups (one per CU),
     // else 64x64.  Split-K when the 64x64 grid still leaves CUs idle and K is

@@ -76,7 +76,9 @@ def test_gemm_config_sampled_rows(dev, n):
 
 
 @pytest.mark.parametrize("M,K,N,act", [(100, 2000, 120, ACT_NONE), (33, 1500, 64, ACT_GELU),
-                                       (16, 4096, 260, ACT_RELU), (5, 777, 9, ACT_NONE)])
+                                       (16, 4096, 260, ACT_RELU), (5, 777, 9, ACT_NONE),
+                                       (24, 1024, 200, ACT_GELU), (8, 200, 64, ACT_RELU), (32, 2052, 4100, ACT_NONE),
+                                       (1, 4096, 4096, ACT_NONE)])
 def test_gemm_split_k(dev, M, K, N, act):
     # grids this small split K; partials are summed in a fixed order
     got, ref = _gemm_case(dev, M, K, N, seed=61, bias=True, act=act, residual=True)
