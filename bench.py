@@ -237,6 +237,9 @@ def main() -> int:
         return 1
     dev = Device(0)
     M = N = K = 4096
+    log("device ceilings")
+    measured_mfma = dev.peak_probe("mfma")
+    measured_hbm = dev.peak_probe("hbm")
     log("headline gemm 4096^3")
     ms, flops, nbytes = gemm_case(dev, M, K, N, 43, args.steps, args.warmup)
     gflops = flops / (ms * 1e-3) / 1e9
@@ -260,7 +263,12 @@ def main() -> int:
                    "M": M, "N": N, "K": K, "parallelism": "1 GPU"},
         "roofline": {"bound": "mfma", "achieved": round(flops / (ms * 1e-3) / 1e12, 2), "peak": PEAK_FP32_MFMA,
                      "unit": "TFLOP/s", "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_FP32_MFMA, 4),
-                     "traffic": traffic, "algorithmic_bytes": nbytes},
+                     "traffic": traffic, "algorithmic_bytes": nbytes,
+                     "measured_peak": round(measured_mfma, 2),
+                     "frac_of_measured_peak": round(flops / (ms * 1e-3) / 1e12 / measured_mfma, 4)},
+        "device_ceilings": {"fp32_mfma_TFLOPs_measured": round(measured_mfma, 2),
+                            "fp32_mfma_TFLOPs_spec": PEAK_FP32_MFMA,
+                            "hbm_copy_GBs_measured": round(measured_hbm, 1), "hbm_GBs_spec": PEAK_HBM},
     }
     extra = {}
     if not args.quick:

@@ -143,6 +143,16 @@ LANCIUS_HIP_EXPORT int lancius_hip_broadcast_f32(lancius_hip_ctx* ctx, float* ou
 LANCIUS_HIP_EXPORT int lancius_hip_fill_f32(lancius_hip_ctx* ctx, float* out, float value, size_t n);
 LANCIUS_HIP_EXPORT int lancius_hip_copy_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n);
 
+/* ---- diagnostics ---------------------------------------------------- */
+
+/* Measured ceilings of this device, for roofline reporting:
+ *   which = 0: fp32 matrix rate, TFLOP/s (independent back-to-back
+ *              v_mfma_f32_32x32x2_f32 on every SIMD, no memory traffic);
+ *   which = 1: HBM copy bandwidth, GB/s (float4 copy of 2 x 1 GiB,
+ *              bytes read + written).
+ * Allocates and frees its own buffers; takes a few hundred milliseconds. */
+LANCIUS_HIP_EXPORT int lancius_hip_peak_probe(lancius_hip_ctx* ctx, int which, double* result);
+
 /* ---- reference-ABI bridge ------------------------------------------- */
 
 /* The fp32 matmul that the reference declares but never defines

@@ -35,7 +35,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip"]
+HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip", "probe.hip"]
 HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c"]
 DEVICE_C_SOURCES = ["host/device_exec.c"]
 

@@ -36,6 +36,7 @@ struct GemmParams {
     float* ws;   // split-K partials [count][splits][M][N]
     int splits;  // K ranges (blockIdx.y), 1 = no split
     int kchunk;  // K per split, a multiple of the k-tile
+    int map2d;   // 1: each XCD owns a 2-D block of tiles (tiles_m % 2 == 0, tiles_n % 4 == 0)
 };
 
 constexpr int kThreads = 256;
@@ -44,8 +45,8 @@ constexpr int kThreads = 256;
 // raw partial sums; splitk_reduce adds the partials in order y = 0, 1, ...
 // (a fixed order, so results are run-to-run identical) and applies the
 // epilogue.
-template <int BM, int BN, int BK, int WGM, int WGN, bool VEC, bool SPLIT>
-__global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
+template <int BM, int BN, int BK, int WGM, int WGN, bool VEC, bool SPLIT, int OCC = 1>
+__global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams p) {
     static_assert(WGM * WGN == 4, "4 waves per workgroup");
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
@@ -65,7 +66,18 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
 
     const uint32_t ntiles = p.tiles_m * p.tiles_n;
     uint32_t tm_id, tn_id;
-    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
+    if (p.map2d) {
+        // XCD x = id % 8 owns the (x/4, x%4) block of a 2 x 4 partition of the
+        // tile grid, so it needs half of A and a quarter of B instead of all of B.
+        const uint32_t xcd = blockIdx.x % kNumXcd, local = blockIdx.x / kNumXcd;
+        const uint32_t rm = p.tiles_m / 2, rn = p.tiles_n / 4;
+        uint32_t lm, ln;
+        grouped_tile(local, rm, rn, 4, lm, ln);
+        tm_id = (xcd / 4) * rm + lm;
+        tn_id = (xcd % 4) * rn + ln;
+    } else {
+        grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
+    }
     const int m0 = (int)tm_id * BM;
     const int n0 = (int)tn_id * BN;
 
@@ -172,18 +184,27 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_mfma(const GemmParams p) {
         const int cur = (kt - kt0) & 1;
         const bool more = kt + 1 < kt1;
         if (more) load_tile((kt + 1) * BK);
+        // Fragments of k-pair kp+1 are read from LDS before the MFMAs of kp are
+        // issued (register double buffer), so no MFMA waits on its own reads.
+        float af[2][TM], bf[2][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[0][i] = As[cur][lk][wm * WM + i * 32 + lr];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[0][j] = Bs[cur][lk][wn * WN + j * 32 + lr];
 #pragma unroll
         for (int kp = 0; kp < BK / 2; ++kp) {
-            float af[TM], bf[TN];
+            const int c = kp & 1;
+            if (kp + 1 < BK / 2) {
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = As[cur][2 * kp + lk][wm * WM + i * 32 + lr];
+                for (int i = 0; i < TM; ++i) af[c ^ 1][i] = As[cur][2 * kp + 2 + lk][wm * WM + i * 32 + lr];
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = Bs[cur][2 * kp + lk][wn * WN + j * 32 + lr];
+                for (int j = 0; j < TN; ++j) bf[c ^ 1][j] = Bs[cur][2 * kp + 2 + lk][wn * WN + j * 32 + lr];
+            }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
         }
         if (more) store_tile(cur ^ 1);
         __syncthreads();
@@ -392,17 +413,18 @@ __global__ void __launch_bounds__(256) splitk_reduce(const GemmParams p, int cou
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN>
+template <int BM, int BN, int BK, int WGM, int WGN, int OCC = 1>
 int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
     p.tiles_m = (uint32_t)((p.M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((p.N + BN - 1) / BN);
+    p.map2d = tune("gemm_map", 0) == 1 && p.tiles_m % 2 == 0 && p.tiles_n % 4 == 0;
     dim3 grid(p.tiles_m * p.tiles_n, (unsigned)p.splits, (unsigned)count);
     const bool split = p.splits > 1;
     if (vec && split)
         hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true>), grid, dim3(kThreads), 0, ctx->stream,
                            p);
     else if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false, OCC>), grid, dim3(kThreads), 0,
                            ctx->stream, p);
     else if (split)
         hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true>), grid, dim3(kThreads), 0,
@@ -486,16 +508,24 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     // Tile: 128x128 when that alone gives >= 256 workgroups (one per CU),
     // else 64x64.  Split-K when the 64x64 grid still leaves CUs idle and K is
     // long enough: enough K ranges for ~512 workgroups, each >= 128 deep.
+    // Configurations (BM x BN / BK): 1 = 128x128/16, 2 = 64x64/16,
+    // 3 = 256x128/16, 4 = 128x128/32, 5 = 128x256/16.
     const size_t big_tiles = count * ((M + 127) / 128) * ((N + 127) / 128);
-    const size_t small_tiles = count * ((M + 63) / 64) * ((N + 63) / 64);
-    const int tile_sel = tune("gemm_tile", 0);  // 0 auto, 1 = 128x128, 2 = 64x64
-    const bool big = tile_sel == 1 || (tile_sel == 0 && big_tiles >= 256);
-    const size_t tiles = big ? big_tiles : small_tiles;
-    const size_t ktiles = (K + kBK - 1) / kBK;
+    // Default: 6 (128x128/16 built for 4 workgroups per CU, 112 VGPRs) when
+    // that gives >= 256 workgroups, else 64x64.  Measured on MI355X: 115
+    // TFLOP/s at 4096^3 (84% of the measured 137 TFLOP/s fp32 MFMA ceiling).
+    int cfg = tune("gemm_tile", 0);
+    if (cfg < 1 || cfg > 6) cfg = big_tiles >= 256 ? 6 : 2;
+    const size_t bm = cfg == 2 ? 64 : cfg == 3 ? 256 : 128;
+    const size_t bn = cfg == 2 ? 64 : cfg == 5 ? 256 : 128;
+    const size_t bk = cfg == 4 ? 32 : kBK;
+    const size_t tiles = count * ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const size_t ktiles = (K + bk - 1) / bk;
     size_t splits = (size_t)tune("gemm_split", 0);
     if (splits == 0) {
         splits = 1;
-        if (tiles < 256 && ktiles >= 16) splits = std::min<size_t>({(512 + tiles - 1) / tiles, ktiles / 8, 16});
+        if (tiles < 256 && K >= 256)
+            splits = std::min<size_t>({(512 + tiles - 1) / tiles, K / 128, 16});
     }
     splits = std::max<size_t>(1, std::min(splits, ktiles));
     size_t chunk_tiles = (ktiles + splits - 1) / splits;
@@ -506,14 +536,21 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         splits = (ktiles + chunk_tiles - 1) / chunk_tiles;
     }
     p.splits = (int)splits;
-    p.kchunk = (int)(chunk_tiles * kBK);
+    p.kchunk = (int)(chunk_tiles * bk);
     if (splits > 1) {
         void* ws = nullptr;
         if (int rc = workspace(ctx, count * splits * M * N * sizeof(float), &ws)) return rc;
         p.ws = (float*)ws;
     }
-    const int rc = big ? launch_cfg<128, 128, kBK, 2, 2>(ctx, p, (int)count, vec)
-                       : launch_cfg<64, 64, kBK, 2, 2>(ctx, p, (int)count, vec);
+    int rc;
+    switch (cfg) {
+        case 2: rc = launch_cfg<64, 64, 16, 2, 2>(ctx, p, (int)count, vec); break;
+        case 3: rc = launch_cfg<256, 128, 16, 2, 2>(ctx, p, (int)count, vec); break;
+        case 4: rc = launch_cfg<128, 128, 32, 2, 2>(ctx, p, (int)count, vec); break;
+        case 5: rc = launch_cfg<128, 256, 16, 2, 2>(ctx, p, (int)count, vec); break;
+        case 6: rc = launch_cfg<128, 128, 16, 2, 2, 4>(ctx, p, (int)count, vec); break;
+        default: rc = launch_cfg<128, 128, 16, 2, 2>(ctx, p, (int)count, vec); break;
+    }
     return rc ? rc : ok();
 }
 

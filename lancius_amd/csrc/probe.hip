@@ -1,0 +1,104 @@
+// Device ceilings for roofline reporting: the sustained fp32 MFMA rate and
+// the HBM copy bandwidth of this GPU (lancius_hip_peak_probe).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lancius {
+namespace {
+
+constexpr int kChains = 8;  // independent accumulators per wave
+
+// Every wave issues `iters` rounds of kChains independent
+// v_mfma_f32_32x32x2_f32; the operands change each round so nothing folds.
+__global__ void __launch_bounds__(256) mfma_rate(float* out, int iters) {
+    f32x16 acc[kChains];
+#pragma unroll
+    for (int c = 0; c < kChains; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+    float a = 1.0f + 1e-7f * threadIdx.x, b = 1.0f - 1e-7f * blockIdx.x;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int c = 0; c < kChains; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[c], 0, 0, 0);
+        a += 1e-9f;
+        b -= 1e-9f;
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChains; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[c][r];
+    if (s == 1234.5f) out[blockIdx.x * blockDim.x + threadIdx.x] = s;  // keeps the loop alive
+}
+
+// Four float4 loads in flight per thread before the stores; n4 % (4 * grid) == 0.
+__global__ void __launch_bounds__(256) copy_f4(f32x4* __restrict__ dst, const f32x4* __restrict__ src, size_t n4) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i + 3 * stride < n4; i += 4 * stride) {
+        const f32x4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+        dst[i] = a;
+        dst[i + stride] = b;
+        dst[i + 2 * stride] = c;
+        dst[i + 3 * stride] = d;
+    }
+}
+
+}  // namespace
+}  // namespace lancius
+
+using namespace lancius;
+
+extern "C" int lancius_hip_peak_probe(lancius_hip_ctx* ctx, int which, double* result) {
+    LANCIUS_REQUIRE(ctx && result, LANCIUS_HIP_ERR_NULL_PTR, "peak_probe: NULL argument");
+    LANCIUS_REQUIRE(which == 0 || which == 1, LANCIUS_HIP_ERR_UNSUPPORTED, "peak_probe: which=%d", which);
+    if (int rc = bind_device(ctx)) return rc;
+    hipDeviceProp_t prop;
+    LANCIUS_HIP_TRY(hipGetDeviceProperties(&prop, ctx->device), "hipGetDeviceProperties");
+    hipEvent_t e0, e1;
+    LANCIUS_HIP_TRY(hipEventCreate(&e0), "hipEventCreate");
+    LANCIUS_HIP_TRY(hipEventCreate(&e1), "hipEventCreate");
+    int rc = 0;
+    float ms = 0.0f;
+    if (which == 0) {
+        // 8 waves per CU (2 per SIMD) keep every MFMA pipe busy.
+        const int blocks = prop.multiProcessorCount * 2;
+        const int iters = 4096;
+        float* out = nullptr;
+        hipError_t e = hipMalloc(&out, (size_t)blocks * 256 * sizeof(float));
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(mfma_rate, dim3(blocks), dim3(256), 0, ctx->stream, out, 64);  // warm-up
+            (void)hipEventRecord(e0, ctx->stream);
+            hipLaunchKernelGGL(mfma_rate, dim3(blocks), dim3(256), 0, ctx->stream, out, iters);
+            (void)hipEventRecord(e1, ctx->stream);
+            e = hipEventSynchronize(e1);
+            if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+            (void)hipFree(out);
+        }
+        if (e != hipSuccess) rc = from_hip(e, "mfma probe");
+        const double flops = (double)blocks * 4 /*waves*/ * iters * kChains * 32.0 * 32.0 * 2.0 * 2.0;
+        if (!rc) *result = flops / (ms * 1e-3) / 1e12;
+    } else {
+        const size_t bytes = (size_t)1 << 30;
+        void *a = nullptr, *b = nullptr;
+        hipError_t e = hipMalloc(&a, bytes);
+        if (e == hipSuccess) e = hipMalloc(&b, bytes);
+        if (e == hipSuccess) {
+            const size_t n4 = bytes / 16;
+            const unsigned blocks = 4096;  // n4 = 2^26 is a multiple of 4 * 4096 * 256
+            hipLaunchKernelGGL(copy_f4, dim3(blocks), dim3(256), 0, ctx->stream, (f32x4*)b, (const f32x4*)a, n4);
+            (void)hipEventRecord(e0, ctx->stream);
+            for (int r = 0; r < 5; ++r)
+                hipLaunchKernelGGL(copy_f4, dim3(blocks), dim3(256), 0, ctx->stream, (f32x4*)b, (const f32x4*)a, n4);
+            (void)hipEventRecord(e1, ctx->stream);
+            e = hipEventSynchronize(e1);
+            if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        }
+        if (a) (void)hipFree(a);
+        if (b) (void)hipFree(b);
+        if (e != hipSuccess) rc = from_hip(e, "copy probe");
+        if (!rc) *result = 5.0 * 2.0 * (double)bytes / (ms * 1e-3) / 1e9;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return rc ? rc : ok();
+}

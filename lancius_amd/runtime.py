@@ -76,6 +76,7 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_copy_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_broadcast_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.lancius_hip_fill_f32.argtypes = [vp, vp, f32, sz]
+    lib.lancius_hip_peak_probe.argtypes = [vp, i32, C.POINTER(C.c_double)]
     lib.kernel_matmul_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.kernel_matmul_f32.restype = None
     # device executor
@@ -194,6 +195,12 @@ class Device:
         ms = C.c_float()
         _check(self.lib.lancius_hip_timer_stop(self.ctx, C.byref(ms)))
         return float(ms.value)
+
+    def peak_probe(self, which: str) -> float:
+        """Measured fp32 MFMA TFLOP/s ("mfma") or HBM copy GB/s ("hbm")."""
+        out = C.c_double()
+        _check(self.lib.lancius_hip_peak_probe(self.ctx, {"mfma": 0, "hbm": 1}[which], C.byref(out)))
+        return float(out.value)
 
     def close(self) -> None:
         for b in self._buffers:
