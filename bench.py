@@ -35,8 +35,8 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from lancius_amd import (Device, DeviceProgram, abi, device_count, graph_lib, graphs,  # noqa: E402
-                         prng)
+from lancius_amd import (DEVICE_GRAPH, Device, DeviceProgram, abi, device_count, graph_lib,  # noqa: E402
+                         graphs, prng)
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
@@ -146,12 +146,12 @@ def bridge_case(dev, n=4096) -> dict:
             "note": "host-pointer bridge, PCIe copies of A, B and C included (wall clock)"}
 
 
-def graph_case(dev, bg, feeds, steps, warmup):
+def graph_case(dev, bg, feeds, steps, warmup, flags=0):
     lib = graph_lib()
     lib.lancius_graph_set_dtype(bg.g, abi.DTYPE_FP32)
     sched = lib.lancius_ir_schedule(bg.g)
     plan = lib.lancius_build_memory_plan(sched, bg.g)
-    prog = DeviceProgram(dev, bg.g, sched, plan)
+    prog = DeviceProgram(dev, bg.g, sched, plan, flags)
     for name in bg.inputs:
         prog.upload(bg.node(name), feeds[name])
     ms = time_steps(dev, prog.run, steps, warmup)
@@ -296,15 +296,18 @@ def main() -> int:
         log("host-pointer bridge")
         extra["kernel_matmul_f32_host_bridge_4096"] = bridge_case(dev)
         log("mlp graph")
+        sdev = Device(0, own_stream=True)  # hipGraph replay on a capturable stream
         lib = graph_lib()
         bg = graphs.build_mlp(lib)
         feeds = {"x": prng.uniform(42, (64, 784), -1.0, 1.0), "W1": prng.normal(142, (784, 256), 0, 0.02),
                  "b1": np.zeros((1, 256), np.float32), "W2": prng.normal(342, (256, 10), 0, 0.02),
                  "b2": np.zeros((1, 10), np.float32)}
         t, info = graph_case(dev, bg, feeds, max(20, steps), 5)
+        tg, _ = graph_case(sdev, bg, feeds, max(20, steps), 5, DEVICE_GRAPH)
         bg.destroy()
         extra["mlp_graph_64x784x256x10"] = {"fwd_latency_ms": round(t, 4), "launches": info["launches"],
-                                            "GFLOP/s": round(26.02e6 / t / 1e6, 1)}
+                                            "GFLOP/s": round(26.02e6 / t / 1e6, 1),
+                                            "fwd_latency_ms_hipgraph": round(tg, 4)}
         log("transformer block graph")
         bg = graphs.build_block(lib)
         feeds = {}
@@ -317,11 +320,13 @@ def main() -> int:
             else:
                 feeds[name] = prng.normal(46 + 1000 * i, shape, 0, 0.02)
         t, info = graph_case(dev, bg, feeds, 10, 3)
+        tg, _ = graph_case(sdev, bg, feeds, 10, 3, DEVICE_GRAPH)
         bg.destroy()
         extra["transformer_block_B4_S1024_d1024_H16_F4096"] = {
-            "fwd_latency_ms": round(t, 3), "launches": info["launches"],
+            "fwd_latency_ms": round(t, 3), "fwd_latency_ms_hipgraph": round(tg, 3), "launches": info["launches"],
             "GFLOP/s": round(111.7e9 / t / 1e6, 1), "arena_MiB": round(info["arena_bytes"] / 2 ** 20, 1)}
         result["all_configs"] = extra
+        sdev.close()
     dev.close()
     if not args.no_cpu:
         log("cpu baseline")

@@ -143,6 +143,29 @@ LANCIUS_HIP_EXPORT int lancius_hip_broadcast_f32(lancius_hip_ctx* ctx, float* ou
 LANCIUS_HIP_EXPORT int lancius_hip_fill_f32(lancius_hip_ctx* ctx, float* out, float value, size_t n);
 LANCIUS_HIP_EXPORT int lancius_hip_copy_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n);
 
+/* ---- streams and HIP graphs ------------------------------------------ */
+
+/* A context on a new non-blocking stream of default priority, owned by the
+ * context (destroyed with it). */
+LANCIUS_HIP_EXPORT int lancius_hip_ctx_create_own_stream(int device, lancius_hip_ctx** out);
+/* Device index of a context (-1 for NULL). */
+LANCIUS_HIP_EXPORT int lancius_hip_ctx_device(const lancius_hip_ctx* ctx);
+/* The hipStream_t a context enqueues on (NULL: the null stream). */
+LANCIUS_HIP_EXPORT void* lancius_hip_ctx_stream(const lancius_hip_ctx* ctx);
+/* Work enqueued on `waiter` after this call starts only after everything
+ * enqueued on `signaler` before it (an event recorded and waited). */
+LANCIUS_HIP_EXPORT int lancius_hip_stream_wait(lancius_hip_ctx* waiter, lancius_hip_ctx* signaler);
+
+typedef struct lancius_hip_graph lancius_hip_graph;
+/* Record every launch enqueued on ctx between begin and end into a graph
+ * instead of running it (ctx must own a stream: the null stream cannot be
+ * captured).  Launches that allocate (first use of a workspace) must have
+ * run once before capture. */
+LANCIUS_HIP_EXPORT int lancius_hip_capture_begin(lancius_hip_ctx* ctx);
+LANCIUS_HIP_EXPORT int lancius_hip_capture_end(lancius_hip_ctx* ctx, lancius_hip_graph** out);
+LANCIUS_HIP_EXPORT int lancius_hip_graph_launch(lancius_hip_graph* graph, lancius_hip_ctx* ctx);
+LANCIUS_HIP_EXPORT void lancius_hip_graph_destroy(lancius_hip_graph* graph);
+
 /* ---- diagnostics ---------------------------------------------------- */
 
 /* Measured ceilings of this device, for roofline reporting:

@@ -44,6 +44,10 @@ typedef struct lancius_device_program lancius_device_program;
 #define LANCIUS_DEVICE_NO_FUSION 0x1u /* one launch per node, no grouping */
 #define LANCIUS_DEVICE_KEEP_ALL  0x2u /* every node keeps its own buffer (readable after run) */
 #define LANCIUS_DEVICE_NO_GROUP  0x4u /* fuse epilogues but do not merge branches */
+#define LANCIUS_DEVICE_GRAPH     0x8u /* first run: eager + capture into a HIP graph; later runs
+                                         replay it on the context's stream (on a null-stream
+                                         context: on a private stream, ordered after and before
+                                         the null stream by events) */
 
 typedef struct {
     size_t arena_bytes;    /* the one device allocation */

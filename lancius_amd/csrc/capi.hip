@@ -58,6 +58,9 @@ int workspace(lancius_hip_ctx* ctx, size_t bytes, void** out) {
         *out = ctx->workspace;
         return 0;
     }
+    LANCIUS_REQUIRE(!ctx->capturing, LANCIUS_HIP_ERR_UNSUPPORTED,
+                    "workspace of %zu bytes needed during graph capture: run the launches once before capturing",
+                    bytes);
     if (ctx->workspace) {
         LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "workspace sync");
         LANCIUS_HIP_TRY(hipFree(ctx->workspace), "workspace free");
@@ -82,6 +85,7 @@ int counters(lancius_hip_ctx* ctx, size_t n, unsigned** out) {
         *out = ctx->counters;
         return 0;
     }
+    LANCIUS_REQUIRE(!ctx->capturing, LANCIUS_HIP_ERR_UNSUPPORTED, "counters needed during graph capture");
     if (ctx->counters) {
         LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "counters sync");
         LANCIUS_HIP_TRY(hipFree(ctx->counters), "counters free");
@@ -135,11 +139,29 @@ int lancius_hip_ctx_create(int device, void* stream, lancius_hip_ctx** out) {
     c->stream = (hipStream_t)stream;
     hipError_t e = hipEventCreate(&c->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&c->ev_stop);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&c->ev_order, hipEventDisableTiming);
     if (e != hipSuccess) {
         free(c);
         return from_hip(e, "hipEventCreate");
     }
     *out = c;
+    return ok();
+}
+
+int lancius_hip_ctx_create_own_stream(int device, lancius_hip_ctx** out) {
+    LANCIUS_REQUIRE(out != nullptr, LANCIUS_HIP_ERR_NULL_PTR, "ctx_create_own_stream: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    LANCIUS_HIP_TRY(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    LANCIUS_REQUIRE(device >= 0 && device < n, LANCIUS_HIP_ERR_SHAPE, "ctx_create: device %d of %d", device, n);
+    LANCIUS_HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    hipStream_t s = nullptr;
+    LANCIUS_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    if (int rc = lancius_hip_ctx_create(device, (void*)s, out)) {
+        (void)hipStreamDestroy(s);
+        return rc;
+    }
+    (*out)->owns_stream = 1;
     return ok();
 }
 
@@ -151,7 +173,70 @@ void lancius_hip_ctx_destroy(lancius_hip_ctx* ctx) {
     if (ctx->counters) (void)hipFree(ctx->counters);
     (void)hipEventDestroy(ctx->ev_start);
     (void)hipEventDestroy(ctx->ev_stop);
+    (void)hipEventDestroy(ctx->ev_order);
+    if (ctx->owns_stream) (void)hipStreamDestroy(ctx->stream);
     free(ctx);
+}
+
+int lancius_hip_ctx_device(const lancius_hip_ctx* ctx) { return ctx ? ctx->device : -1; }
+
+void* lancius_hip_ctx_stream(const lancius_hip_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int lancius_hip_stream_wait(lancius_hip_ctx* waiter, lancius_hip_ctx* signaler) {
+    LANCIUS_REQUIRE(waiter && signaler, LANCIUS_HIP_ERR_NULL_PTR, "stream_wait: NULL context");
+    if (waiter->stream == signaler->stream) return ok();
+    if (int rc = bind_device(signaler)) return rc;
+    LANCIUS_HIP_TRY(hipEventRecord(signaler->ev_order, signaler->stream), "hipEventRecord");
+    LANCIUS_HIP_TRY(hipStreamWaitEvent(waiter->stream, signaler->ev_order, 0), "hipStreamWaitEvent");
+    return ok();
+}
+
+int lancius_hip_capture_begin(lancius_hip_ctx* ctx) {
+    LANCIUS_REQUIRE(ctx, LANCIUS_HIP_ERR_NULL_PTR, "capture_begin: NULL context");
+    LANCIUS_REQUIRE(ctx->stream != nullptr, LANCIUS_HIP_ERR_UNSUPPORTED,
+                    "capture_begin: the null stream cannot be captured (use lancius_hip_ctx_create_own_stream)");
+    LANCIUS_REQUIRE(!ctx->capturing, LANCIUS_HIP_ERR_UNSUPPORTED, "capture_begin: already capturing");
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    ctx->capturing = 1;
+    return ok();
+}
+
+int lancius_hip_capture_end(lancius_hip_ctx* ctx, lancius_hip_graph** out) {
+    LANCIUS_REQUIRE(ctx && out, LANCIUS_HIP_ERR_NULL_PTR, "capture_end: NULL argument");
+    LANCIUS_REQUIRE(ctx->capturing, LANCIUS_HIP_ERR_UNSUPPORTED, "capture_end without capture_begin");
+    *out = nullptr;
+    ctx->capturing = 0;
+    hipGraph_t graph = nullptr;
+    LANCIUS_HIP_TRY(hipStreamEndCapture(ctx->stream, &graph), "hipStreamEndCapture");
+    lancius_hip_graph* g = (lancius_hip_graph*)calloc(1, sizeof(lancius_hip_graph));
+    if (!g) {
+        (void)hipGraphDestroy(graph);
+        return set_error(LANCIUS_HIP_ERR_OOM, "capture_end: host allocation failed");
+    }
+    g->graph = graph;
+    hipError_t e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        free(g);
+        return from_hip(e, "hipGraphInstantiate");
+    }
+    *out = g;
+    return ok();
+}
+
+int lancius_hip_graph_launch(lancius_hip_graph* graph, lancius_hip_ctx* ctx) {
+    LANCIUS_REQUIRE(graph && ctx, LANCIUS_HIP_ERR_NULL_PTR, "graph_launch: NULL argument");
+    if (int rc = bind_device(ctx)) return rc;
+    LANCIUS_HIP_TRY(hipGraphLaunch(graph->exec, ctx->stream), "hipGraphLaunch");
+    return ok();
+}
+
+void lancius_hip_graph_destroy(lancius_hip_graph* graph) {
+    if (!graph) return;
+    (void)hipGraphExecDestroy(graph->exec);
+    (void)hipGraphDestroy(graph->graph);
+    free(graph);
 }
 
 int lancius_hip_malloc(lancius_hip_ctx* ctx, void** device_ptr, size_t bytes) {

@@ -18,6 +18,14 @@ struct lancius_hip_ctx {
     size_t workspace_bytes;
     unsigned* counters;     // arrival counters of split reductions, kept at zero between calls
     size_t counters_n;
+    int owns_stream;        // stream created by lancius_hip_ctx_create_own_stream
+    int capturing;          // between lancius_hip_capture_begin and _end
+    hipEvent_t ev_order;    // lancius_hip_stream_wait
+};
+
+struct lancius_hip_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
 };
 
 namespace lancius {

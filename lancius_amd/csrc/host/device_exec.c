@@ -34,7 +34,11 @@ typedef struct {
 } launch_t;
 
 struct lancius_device_program {
-    lancius_hip_ctx* ctx;
+    lancius_hip_ctx* ctx;        /* caller's context: arena, copies, ordering */
+    lancius_hip_ctx* exec;       /* context the launches go to (ctx, or the private one) */
+    lancius_hip_ctx* private_ctx;/* LANCIUS_DEVICE_GRAPH: context the graph is captured on */
+    lancius_hip_graph* graph;    /* captured launch list */
+    int cross_stream;            /* private_ctx has its own stream, ordered by events */
     uint32_t n_ids;
     char* arena;
     char** ptr;
@@ -435,6 +439,8 @@ static int cmp_ivl_birth(const void* x, const void* y) {
 
 void lancius_device_program_destroy(lancius_device_program* p) {
     if (!p) return;
+    if (p->graph) lancius_hip_graph_destroy(p->graph);
+    if (p->private_ctx) lancius_hip_ctx_destroy(p->private_ctx);
     if (p->arena) lancius_hip_free(p->ctx, p->arena);
     free(p->ptr);
     free(p->bytes);
@@ -472,6 +478,7 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
     float* fillbuf = NULL;
     if (!p) return LANCIUS_HIP_ERR_OOM;
     p->ctx = ctx;
+    p->exec = ctx;
     p->n_ids = ids;
     if (!CALLOC(c.node, ids) || !CALLOC(c.wave, ids) || !CALLOC(c.order, ids) || !CALLOC(c.consumers, ids) ||
         !CALLOC(c.sole, ids) || !CALLOC(c.root, ids) || !CALLOC(c.absorbed, ids) || !CALLOC(c.chain_head, ids) ||
@@ -715,6 +722,19 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         if (rc) goto out;
     }
     rc = lancius_hip_synchronize(ctx);
+    if (!rc && (flags & LANCIUS_DEVICE_GRAPH)) {
+        /* A private context keeps the workspace the graph captures away from
+         * the caller's other launches (which may grow and free theirs).  It
+         * shares the caller's stream; the null stream cannot be captured, so
+         * there it gets a stream of its own, ordered against the caller's by
+         * events. */
+        void* stream = lancius_hip_ctx_stream(ctx);
+        const int dev = lancius_hip_ctx_device(ctx);
+        p->cross_stream = stream == NULL;
+        rc = stream ? lancius_hip_ctx_create(dev, stream, &p->private_ctx)
+                    : lancius_hip_ctx_create_own_stream(dev, &p->private_ctx);
+        if (!rc) p->exec = p->private_ctx;
+    }
 
 out:
     free(fillbuf);
@@ -736,7 +756,7 @@ out:
 #define P(id) ((id) == NONE ? NULL : (float*)prog->ptr[(id)])
 
 static int run_launch(lancius_device_program* prog, const launch_t* L) {
-    lancius_hip_ctx* ctx = prog->ctx;
+    lancius_hip_ctx* ctx = prog->exec;
     const member_t* m = &L->m[0];
     switch (L->kind) {
         case L_GEMM: {
@@ -784,13 +804,39 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
     return LANCIUS_HIP_ERR_INTERNAL;
 }
 
-int lancius_device_run(lancius_device_program* prog) {
-    if (!prog) return LANCIUS_HIP_ERR_NULL_PTR;
+static int run_all(lancius_device_program* prog) {
     for (uint32_t s = 0; s < prog->n_launches; s++) {
         const int rc = run_launch(prog, &prog->launches[s]);
         if (rc) return rc;
     }
     return 0;
+}
+
+int lancius_device_run(lancius_device_program* prog) {
+    if (!prog) return LANCIUS_HIP_ERR_NULL_PTR;
+    if (!prog->private_ctx) return run_all(prog);
+    /* graph mode.  On a stream of its own, the replay starts after the
+     * caller's work and the caller's stream continues after it. */
+    int rc = prog->cross_stream ? lancius_hip_stream_wait(prog->private_ctx, prog->ctx) : 0;
+    if (rc) return rc;
+    if (prog->graph) {
+        rc = lancius_hip_graph_launch(prog->graph, prog->exec);
+    } else {
+        /* eager pass (allocates workspaces, produces this run's results), then
+         * record the same launches */
+        rc = run_all(prog);
+        if (!rc) rc = lancius_hip_capture_begin(prog->exec);
+        if (!rc) {
+            const int rc_run = run_all(prog);
+            lancius_hip_graph* g = NULL;
+            const int rc_end = lancius_hip_capture_end(prog->exec, &g);
+            rc = rc_run ? rc_run : rc_end;
+            if (!rc) prog->graph = g;
+            else if (g) lancius_hip_graph_destroy(g);
+        }
+    }
+    const int rc2 = prog->cross_stream ? lancius_hip_stream_wait(prog->ctx, prog->private_ctx) : 0;
+    return rc ? rc : rc2;
 }
 
 void* lancius_device_buffer(lancius_device_program* prog, const lancius_node* n) {

@@ -21,7 +21,7 @@ ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 MAX_GROUP = 16
 
 # LANCIUS_DEVICE_* flags (include/lancius_hip_graph.h)
-DEVICE_NO_FUSION, DEVICE_KEEP_ALL, DEVICE_NO_GROUP = 0x1, 0x2, 0x4
+DEVICE_NO_FUSION, DEVICE_KEEP_ALL, DEVICE_NO_GROUP, DEVICE_GRAPH = 0x1, 0x2, 0x4, 0x8
 
 
 class HipError(RuntimeError):
@@ -76,6 +76,16 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_copy_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_broadcast_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.lancius_hip_fill_f32.argtypes = [vp, vp, f32, sz]
+    lib.lancius_hip_ctx_create_own_stream.argtypes = [i32, C.POINTER(vp)]
+    lib.lancius_hip_ctx_device.argtypes = [vp]
+    lib.lancius_hip_ctx_stream.argtypes = [vp]
+    lib.lancius_hip_ctx_stream.restype = vp
+    lib.lancius_hip_stream_wait.argtypes = [vp, vp]
+    lib.lancius_hip_capture_begin.argtypes = [vp]
+    lib.lancius_hip_capture_end.argtypes = [vp, C.POINTER(vp)]
+    lib.lancius_hip_graph_launch.argtypes = [vp, vp]
+    lib.lancius_hip_graph_destroy.argtypes = [vp]
+    lib.lancius_hip_graph_destroy.restype = None
     lib.lancius_hip_peak_probe.argtypes = [vp, i32, C.POINTER(C.c_double)]
     lib.kernel_matmul_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.kernel_matmul_f32.restype = None
@@ -152,12 +162,16 @@ class Buffer:
 
 
 class Device:
-    """A lancius_hip context on one GPU (null stream by default)."""
+    """A lancius_hip context on one GPU: the null stream by default, a
+    caller's hipStream_t (`stream`), or a stream of its own (`own_stream`)."""
 
-    def __init__(self, device: int = 0, stream: int | None = None):
+    def __init__(self, device: int = 0, stream: int | None = None, own_stream: bool = False):
         self.lib = hip_lib()
         ctx = C.c_void_p()
-        _check(self.lib.lancius_hip_ctx_create(device, C.c_void_p(stream) if stream else None, C.byref(ctx)))
+        if own_stream:
+            _check(self.lib.lancius_hip_ctx_create_own_stream(device, C.byref(ctx)))
+        else:
+            _check(self.lib.lancius_hip_ctx_create(device, C.c_void_p(stream) if stream else None, C.byref(ctx)))
         self.ctx = ctx
         self._buffers: list[Buffer] = []
 

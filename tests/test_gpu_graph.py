@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from lancius_amd import (DEVICE_KEEP_ALL, DEVICE_NO_FUSION, DeviceProgram, HipError, abi, graph_lib, graphs,
+from lancius_amd import (DEVICE_GRAPH, DEVICE_KEEP_ALL, DEVICE_NO_FUSION, DeviceProgram, HipError, abi, graph_lib, graphs,
                          prng)
 from tests.conftest import case
 
@@ -122,6 +122,60 @@ def test_mlp_reference_plan_is_replanned(dev):
     _feed(prog, pl.bg, {n: GO[f"mlp_{n}"] for n in pl.bg.inputs})
     prog.run()
     assert oracle.normwise_error(prog.download(pl.bg.node("softmax")), GO["mlp_softmax"]) <= oracle.tolerance(784)
+    prog.close()
+    pl.close()
+
+
+@pytest.mark.parametrize("stream", ["null", "own"])
+def test_graph_replay_mlp(dev, stream):
+    """LANCIUS_DEVICE_GRAPH: first run eager + capture, then replays; new
+    inputs are uploaded and an unrelated split-K GEMM (which grows the
+    context's workspace) runs on the caller's context between replays, and
+    every replay is checked against the oracle."""
+    from lancius_amd import Device
+
+    d = dev if stream == "null" else Device(0, own_stream=True)
+    pl = Planned(graphs.build_mlp(graph_lib()))
+    case(f"mlp graph replay, {stream} stream")
+    prog = pl.program(d, flags=DEVICE_GRAPH)
+    sm = pl.bg.node("softmax")
+    for rep in range(4):
+        feeds = {"x": prng.uniform(500 + rep, (64, 784), -1.0, 1.0),
+                 "W1": prng.normal(600 + rep, (784, 256), 0, 0.05), "b1": prng.normal(700 + rep, (1, 256), 0, 0.05),
+                 "W2": prng.normal(800 + rep, (256, 10), 0, 0.05), "b2": prng.normal(900 + rep, (1, 10), 0, 0.05)}
+        _feed(prog, pl.bg, feeds)
+        prog.run()
+        got = prog.download(sm)
+        ref = pl.oracle_run(feeds)[sm.contents.id].reshape(64, 10)
+        assert oracle.normwise_error(got, ref) <= oracle.tolerance(784), rep
+        assert np.array_equal(prog.argmax(sm), oracle.argmax(ref)), rep
+        # eager work on the same context between replays
+        m, k, n = 64, 1024 * (rep + 1), 128
+        a, b = prng.normal(rep, (m, k)), prng.normal(rep + 50, (k, n))
+        da, db, dc = d.upload(a), d.upload(b), d.alloc(m * n * 4)
+        d.gemm(dc, da, db, m, k, n)
+        out = d.download(dc, (m, n))
+        assert oracle.normwise_error(out, oracle.matmul(a, b)) <= oracle.tolerance(k), rep
+        for buf in (da, db, dc):
+            buf.free()
+    prog.close()
+    pl.close()
+    if d is not dev:
+        d.close()
+
+
+def test_graph_replay_block_small(dev):
+    pl = Planned(graphs.build_block(graph_lib(), batch=2, S=32, d=64, H=4, F=256))
+    case("block small graph replay")
+    prog = pl.program(dev, flags=DEVICE_GRAPH)
+    for rep in range(3):
+        feeds = _block_feeds(pl.bg, seed=3000 + 100 * rep)
+        _feed(prog, pl.bg, feeds)
+        prog.run()
+        ref = pl.oracle_run(feeds)
+        for name in pl.bg.outputs:
+            n = pl.bg.node(name)
+            assert oracle.normwise_error(prog.download(n).ravel(), ref[n.contents.id]) <= oracle.tolerance(256), rep
     prog.close()
     pl.close()
 
