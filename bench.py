@@ -230,7 +230,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
-              f"(see DESIGN.md for how the path would shard)", file=sys.stderr)
+              f"(every workload here fits one MI355X; the multi-GPU split is a design, not code)",
+              file=sys.stderr)
         return 2
     if device_count() < 1:
         print("bench.py: no GPU visible to HIP", file=sys.stderr)

@@ -79,6 +79,49 @@ lancius_node* lancius_layernorm(lancius_graph* g, const lancius_node* in, const 
                                 const lancius_node* beta);
 lancius_node* lancius_gelu(lancius_graph* g, const lancius_node* in);
 
+/* Builders of the training graph (lancius_ir.c:92-97,164-177,207-241,263-280,300-368). */
+lancius_node* lancius_sub(lancius_graph* g, const lancius_node* a, const lancius_node* b);
+lancius_node* lancius_mul(lancius_graph* g, const lancius_node* a, const lancius_node* b);
+lancius_node* lancius_sum(lancius_graph* g, const lancius_node* a);
+lancius_node* lancius_transpose(lancius_graph* g, const lancius_node* a);
+lancius_node* lancius_relu_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_a);
+lancius_node* lancius_softmax_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_y);
+lancius_node* lancius_sum_axis0(lancius_graph* g, const lancius_node* a);
+lancius_node* lancius_sum_axis1(lancius_graph* g, const lancius_node* a);
+lancius_node* lancius_broadcast_4d(lancius_graph* g, const lancius_node* a, size_t n, size_t c, size_t h, size_t w);
+lancius_node* lancius_maxpool2d(lancius_graph* g, const lancius_node* in, uint32_t kernel, uint32_t stride);
+lancius_node* lancius_cross_entropy(lancius_graph* g, const lancius_node* logits, const lancius_node* targets);
+lancius_node* lancius_cross_entropy_bwd(lancius_graph* g, const lancius_node* logits, const lancius_node* targets,
+                                        const lancius_node* grad_out);
+lancius_node* lancius_conv2d_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_in,
+                                 const lancius_node* fwd_w, uint32_t stride, uint32_t pad);
+lancius_node* lancius_conv2d_bwd_w(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_in,
+                                   uint32_t k_h, uint32_t k_w, uint32_t stride, uint32_t pad);
+lancius_node* lancius_maxpool2d_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_in,
+                                    uint32_t kernel, uint32_t stride);
+/* Built for autodiff; neither executor runs them (no reference branch either). */
+lancius_node* lancius_permute(lancius_graph* g, const lancius_node* in, uint32_t a0, uint32_t a1, uint32_t a2,
+                              uint32_t a3);
+lancius_node* lancius_matmul_batched(lancius_graph* g, const lancius_node* a, const lancius_node* b);
+
+/* ---- reverse-mode autodiff (lancius_autodiff.h:8-17) ----
+ * Copies the forward graph into a new graph and appends the vector-Jacobian
+ * products of every node back to `loss_node`; grad_nodes[id] (for the ids of
+ * the FORWARD graph, max_id of them) is the gradient node of that forward
+ * node in the new graph, or NULL.  Same construction, node order and result
+ * as lancius_autodiff.c:44-207. */
+#ifndef Lancius_LANCIUS_AUTODIFF_H
+#define Lancius_LANCIUS_AUTODIFF_H
+typedef struct {
+    lancius_graph* graph;
+    lancius_node* loss_node;
+    lancius_node** grad_nodes;
+    uint32_t max_id;
+} lancius_training_graph;
+lancius_training_graph* lancius_ir_autodiff(lancius_graph* fwd_g, lancius_node* loss_node);
+void lancius_training_graph_destroy(lancius_training_graph* tg);
+#endif
+
 /* Conv2D + ReLU fusion pass (lancius_optimizer.c:15-41). */
 void lancius_optimize_fusion(lancius_graph* g);
 

@@ -143,6 +143,66 @@ LANCIUS_HIP_EXPORT int lancius_hip_broadcast_f32(lancius_hip_ctx* ctx, float* ou
 LANCIUS_HIP_EXPORT int lancius_hip_fill_f32(lancius_hip_ctx* ctx, float* out, float value, size_t n);
 LANCIUS_HIP_EXPORT int lancius_hip_copy_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n);
 
+/* ---- the rest of the scheduler dispatch: training and reduction ops ---- */
+
+/* out = a - b, out = a * b over n elements (lancius_scheduler.c:236-245). */
+LANCIUS_HIP_EXPORT int lancius_hip_sub_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n);
+LANCIUS_HIP_EXPORT int lancius_hip_mul_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n);
+/* out = fwd > 0 ? grad : 0 (RELU_BWD, lancius_scheduler.c:279-283). */
+LANCIUS_HIP_EXPORT int lancius_hip_relu_bwd_f32(lancius_hip_ctx* ctx, float* out, const float* grad,
+                                                const float* fwd, size_t n);
+/* out[c,r] = in[r,c] for an R x C input (TRANSPOSE, lancius_scheduler.c:246-250). */
+LANCIUS_HIP_EXPORT int lancius_hip_transpose_f32(lancius_hip_ctx* ctx, float* out, const float* in,
+                                                 size_t rows, size_t cols);
+/* Sums with fp64 accumulation in a fixed order (bit-identical from run to
+ * run), stored as fp32:
+ *   sum:       out[0] = sum of n values (SUM, :251-256);
+ *   sum_axis0: out[c] = sum over rows of in[r,c] (SUM_AXIS0, :257-262);
+ *   sum_axis1: out[r] = sum over columns of in[r,c] (SUM_AXIS1, :263-267). */
+LANCIUS_HIP_EXPORT int lancius_hip_sum_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n);
+LANCIUS_HIP_EXPORT int lancius_hip_sum_axis0_f32(lancius_hip_ctx* ctx, float* out, const float* in,
+                                                 size_t rows, size_t cols);
+LANCIUS_HIP_EXPORT int lancius_hip_sum_axis1_f32(lancius_hip_ctx* ctx, float* out, const float* in,
+                                                 size_t rows, size_t cols);
+/* out[r,c] = y[r,c] * (dy[r,c] - sum_c dy[r,c] y[r,c]) (SOFTMAX_BWD, :295-304). */
+LANCIUS_HIP_EXPORT int lancius_hip_softmax_bwd_f32(lancius_hip_ctx* ctx, float* out, const float* dy,
+                                                   const float* y, size_t rows, size_t cols);
+/* Mean cross-entropy of row logits x against targets y (entries equal to
+ * 1.0 select the class), returned as |loss| in out[0]
+ * (CROSS_ENTROPY, lancius_scheduler.c:68-87, including the fabs of :85). */
+LANCIUS_HIP_EXPORT int lancius_hip_cross_entropy_f32(lancius_hip_ctx* ctx, float* out, const float* x,
+                                                     const float* y, size_t rows, size_t cols);
+/* out[r,c] = (softmax(x)[r,c] - y[r,c]) * g[0] / rows, g a device scalar
+ * (CROSS_ENTROPY_BWD, :89-104). */
+LANCIUS_HIP_EXPORT int lancius_hip_cross_entropy_bwd_f32(lancius_hip_ctx* ctx, float* out, const float* x,
+                                                         const float* y, const float* g, size_t rows, size_t cols);
+/* Input gradient of conv2d: dx[N,C_in,H,W] = sum over (co,kh,kw) of
+ * dy[N,C_out,H_out,W_out] * w[C_out,C_in,K_h,K_w] at ho*stride - pad + kh = h
+ * (kernel_conv2d_bwd_in, lancius_kernels.c:62-91). */
+LANCIUS_HIP_EXPORT int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx, const float* dy,
+                                                        const float* w, size_t N, size_t C_in, size_t H, size_t W,
+                                                        size_t C_out, size_t H_out, size_t W_out,
+                                                        size_t K_h, size_t K_w, size_t stride, size_t pad);
+/* Weight gradient of conv2d: dw[C_out,C_in,K_h,K_w] = sum over (n,ho,wo) of
+ * dy[n,co,ho,wo] * x[n,ci,ho*stride-pad+kh,wo*stride-pad+kw]
+ * (kernel_conv2d_bwd_w, lancius_kernels.c:93-136). */
+LANCIUS_HIP_EXPORT int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw, const float* dy,
+                                                         const float* x, size_t N, size_t C_in, size_t H, size_t W,
+                                                         size_t C_out, size_t H_out, size_t W_out,
+                                                         size_t K_h, size_t K_w, size_t stride, size_t pad);
+/* Max pooling, K x K window, no padding, H_out = (H - K)/stride + 1; the
+ * running maximum starts at -1e9 with a strict '>' (MAXPOOL2D,
+ * lancius_vision_ops.c:82-112). */
+LANCIUS_HIP_EXPORT int lancius_hip_maxpool2d_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t N,
+                                                 size_t C, size_t H, size_t W, size_t K, size_t stride);
+/* Its gradient: each dy value goes to the first maximum of its window
+ * (position (0,0) of the plane when no value exceeds -1e9), contributions
+ * summed (MAXPOOL2D_BWD, lancius_vision_ops.c:149-190).  H_out, W_out are
+ * dy's spatial size. */
+LANCIUS_HIP_EXPORT int lancius_hip_maxpool2d_bwd_f32(lancius_hip_ctx* ctx, float* dx, const float* dy,
+                                                     const float* x, size_t N, size_t C, size_t H, size_t W,
+                                                     size_t H_out, size_t W_out, size_t K, size_t stride);
+
 /* ---- streams and HIP graphs ------------------------------------------ */
 
 /* A context on a new non-blocking stream of default priority, owned by the

@@ -115,6 +115,14 @@ def node_shape(n: NodeP) -> tuple[int, ...]:
     return tuple(n.contents.shape[d] for d in range(n.contents.ndim))
 
 
+class TrainingGraph(C.Structure):
+    """lancius_training_graph (B/include/lancius/lancius_autodiff.h:8-13)."""
+    _fields_ = [("graph", GraphP), ("loss_node", NodeP), ("grad_nodes", C.POINTER(NodeP)), ("max_id", C.c_uint32)]
+
+
+TrainingGraphP = C.POINTER(TrainingGraph)
+
+
 def declare_graph_api(lib: C.CDLL) -> C.CDLL:
     """Prototypes of the graph-path functions shared by liblancius_graph and
     the reference library (same names and signatures)."""
@@ -144,6 +152,28 @@ def declare_graph_api(lib: C.CDLL) -> C.CDLL:
     lib.lancius_attention.restype = NodeP
     lib.lancius_layernorm.argtypes = [GraphP, NodeP, NodeP, NodeP]
     lib.lancius_layernorm.restype = NodeP
+    for name in ("lancius_sub", "lancius_mul", "lancius_relu_bwd", "lancius_softmax_bwd", "lancius_cross_entropy"):
+        getattr(lib, name).argtypes = [GraphP, NodeP, NodeP]
+        getattr(lib, name).restype = NodeP
+    for name in ("lancius_sum", "lancius_transpose", "lancius_sum_axis0", "lancius_sum_axis1"):
+        getattr(lib, name).argtypes = [GraphP, NodeP]
+        getattr(lib, name).restype = NodeP
+    lib.lancius_broadcast_4d.argtypes = [GraphP, NodeP, sz, sz, sz, sz]
+    lib.lancius_broadcast_4d.restype = NodeP
+    lib.lancius_maxpool2d.argtypes = [GraphP, NodeP, C.c_uint32, C.c_uint32]
+    lib.lancius_maxpool2d.restype = NodeP
+    lib.lancius_cross_entropy_bwd.argtypes = [GraphP, NodeP, NodeP, NodeP]
+    lib.lancius_cross_entropy_bwd.restype = NodeP
+    lib.lancius_conv2d_bwd.argtypes = [GraphP, NodeP, NodeP, NodeP, C.c_uint32, C.c_uint32]
+    lib.lancius_conv2d_bwd.restype = NodeP
+    lib.lancius_conv2d_bwd_w.argtypes = [GraphP, NodeP, NodeP, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]
+    lib.lancius_conv2d_bwd_w.restype = NodeP
+    lib.lancius_maxpool2d_bwd.argtypes = [GraphP, NodeP, NodeP, C.c_uint32, C.c_uint32]
+    lib.lancius_maxpool2d_bwd.restype = NodeP
+    lib.lancius_ir_autodiff.argtypes = [GraphP, NodeP]
+    lib.lancius_ir_autodiff.restype = TrainingGraphP
+    lib.lancius_training_graph_destroy.argtypes = [TrainingGraphP]
+    lib.lancius_training_graph_destroy.restype = None
     lib.lancius_optimize_fusion.argtypes = [GraphP]
     lib.lancius_optimize_fusion.restype = None
     lib.lancius_ir_schedule.argtypes = [GraphP]

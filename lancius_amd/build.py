@@ -35,8 +35,9 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip", "probe.hip"]
-HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c"]
+HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip", "reduce.hip", "pool.hip",
+               "probe.hip"]
+HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c", "host/graph_autodiff.c"]
 DEVICE_C_SOURCES = ["host/device_exec.c"]
 
 HIP_FLAGS = [
@@ -45,7 +46,8 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-fvisibility=hidden",
-    # Packed fp32 VALU instructions stay off on this pool.
+    # Packed fp32 VALU instructions stay off: some of their forms have given
+    # wrong results on these machines without any error.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",
@@ -63,6 +65,7 @@ REF_SOURCES = [
     "src/core/lancius_error.c",
     "src/ir/lancius_ir.c",
     "src/math/lancius_kernels.c",
+    "src/math/lancius_autodiff.c",
     "src/runtime/lancius_scheduler.c",
     "src/runtime/lancius_memory_planner.c",
     "src/runtime/lancius_vision_ops.c",

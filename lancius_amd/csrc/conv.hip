@@ -237,6 +237,228 @@ __global__ void __launch_bounds__(256) conv_weights_kmajor(float* __restrict__ w
     }
 }
 
+// ---- backward ------------------------------------------------------------
+//
+// Input gradient at stride 1 is itself a convolution: dx = conv(dy, w') with
+// w'[ci][co][kh][kw] = w[co][ci][K_h-1-kh][K_w-1-kw] and padding K-1-pad,
+// since dx[ih] = sum_kh dy[ih + pad - kh] w[kh].  The flipped weights are
+// written straight into the layout the forward kernel reads: k-major
+// ((tap, co) rows, C_in contiguous) when the forward kernel takes that path,
+// OIHW otherwise.
+__global__ void __launch_bounds__(256) dgrad_weights(float* __restrict__ wt, const float* __restrict__ w, int C_out,
+                                                     int C_in, int KH, int KW, int kmajor) {
+    const int KHW = KH * KW;
+    const size_t total = (size_t)C_out * C_in * KHW;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t s = (size_t)blockIdx.x * blockDim.x + threadIdx.x; s < total; s += stride) {
+        const int tap = (int)(s % KHW);
+        const size_t r = s / KHW;
+        const int ci = (int)(r % C_in), co = (int)(r / C_in);
+        const int kh = tap / KW, kw = tap - (tap / KW) * KW;
+        const int ftap = (KH - 1 - kh) * KW + (KW - 1 - kw);  // tap of the flipped filter
+        const float v = w[s];
+        // flipped conv: output channel ci, input channel co
+        if (kmajor)
+            wt[((size_t)ftap * C_out + co) * C_in + ci] = v;
+        else
+            wt[((size_t)ci * C_out + co) * KHW + ftap] = v;
+    }
+}
+
+// Any stride: one thread per dx element, summing over (co, kh, kw) in the
+// reference's order (lancius_kernels.c:62-91 accumulates per output element
+// over co, then ho/wo; the terms are the same).
+__global__ void __launch_bounds__(256) dgrad_direct(float* __restrict__ dx, const float* __restrict__ dy,
+                                                    const float* __restrict__ w, int N, int C_in, int H, int W,
+                                                    int C_out, int Ho, int Wo, int KH, int KW, int stride, int pad) {
+    const size_t total = (size_t)N * C_in * H * W;
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += step) {
+        const int iw = (int)(i % W);
+        const int ih = (int)((i / W) % H);
+        const int ci = (int)((i / ((size_t)W * H)) % C_in);
+        const int n = (int)(i / ((size_t)W * H * C_in));
+        float acc = 0.0f;
+        for (int co = 0; co < C_out; ++co) {
+            const float* g = dy + ((size_t)n * C_out + co) * Ho * Wo;
+            const float* wk = w + ((size_t)co * C_in + ci) * KH * KW;
+            for (int kh = 0; kh < KH; ++kh) {
+                const int hn = ih + pad - kh;
+                if (hn < 0 || hn % stride) continue;
+                const int ho = hn / stride;
+                if (ho >= Ho) continue;
+                for (int kw = 0; kw < KW; ++kw) {
+                    const int wn = iw + pad - kw;
+                    if (wn < 0 || wn % stride) continue;
+                    const int wo = wn / stride;
+                    if (wo >= Wo) continue;
+                    acc += g[(size_t)ho * Wo + wo] * wk[kh * KW + kw];
+                }
+            }
+        }
+        dx[i] = acc;
+    }
+}
+
+// Weight gradient as a GEMM on the matrix cores:
+//   dW[co][j] = sum_P dY[co][P] * X[j][P],  j = (ci, kh, kw), P = (n, ho, wo)
+// with dY[co][P] = dy[n][co][ho][wo] and X[j][P] the im2col value
+// x[n][ci][ho*stride-pad+kh][wo*stride-pad+kw] (0 outside the image).  The
+// reduction over P (N*H_out*W_out, ~10^5 at the conv config) is split across
+// blockIdx.y; partials are added in split order by wgrad_reduce.
+struct WgradParams {
+    float* dw;
+    float* ws;
+    const float* dy;
+    const float* x;
+    int N, C_in, H, W, C_out, Ho, Wo, KH, KW, stride, pad;
+    int J;             // C_in * KH * KW
+    long long Ptotal;  // N * Ho * Wo
+    long long pchunk;  // pixels per split (multiple of BK)
+    int splits;
+    uint32_t tiles_m, tiles_n;
+};
+
+template <int BM, int BN>
+__global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
+    constexpr int BK = 16, WGM = 2, WGN = 2;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int LDA = BM + 4, LDB = BN + 4;
+    __shared__ __attribute__((aligned(16))) float As[2][BK][LDA];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LDB];
+
+    const uint32_t tile = blockIdx.x;
+    const int m0 = (int)(tile / p.tiles_n) * BM;  // first output channel
+    const int j0 = (int)(tile % p.tiles_n) * BN;  // first (ci, kh, kw)
+    const int split = blockIdx.y;
+    const long long pbeg = (long long)split * p.pchunk;
+    const long long pend = pbeg + p.pchunk < p.Ptotal ? pbeg + p.pchunk : p.Ptotal;
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    // Loader mapping: lanes along the pixel index (contiguous in memory).
+    const int kk = tid % BK;
+    const int row0 = tid / BK;                      // 0..15
+    constexpr int A_PER = BM / (256 / BK);          // channels per thread
+    constexpr int B_PER = BN / (256 / BK);          // j per thread
+    const int HWo = p.Ho * p.Wo, KHW = p.KH * p.KW;
+    // The (ci, kh, kw) of each j this thread loads never changes.
+    int b_off[B_PER], b_dh[B_PER], b_dw[B_PER];
+#pragma unroll
+    for (int i = 0; i < B_PER; ++i) {
+        const int j = j0 + row0 + 16 * i;
+        if (j < p.J) {
+            const int ci = j / KHW, t = j - (j / KHW) * KHW;
+            const int kh = t / p.KW, kw = t - (t / p.KW) * p.KW;
+            b_off[i] = ci * p.H * p.W;
+            b_dh[i] = kh - p.pad;
+            b_dw[i] = kw - p.pad;
+        } else {
+            b_off[i] = -1;
+            b_dh[i] = b_dw[i] = 0;
+        }
+    }
+    float a_s[A_PER], b_s[B_PER];
+    auto load_tile = [&](long long kt) {
+        const long long P = pbeg + kt * BK + kk;
+        const bool valid = P < pend;
+        int n = 0, ho = 0, wo = 0;
+        if (valid) {
+            n = (int)(P / HWo);
+            const int pix = (int)(P - (long long)n * HWo);
+            ho = pix / p.Wo;
+            wo = pix - ho * p.Wo;
+        }
+        const float* g = p.dy + ((size_t)n * p.C_out) * HWo + (size_t)ho * p.Wo + wo;
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) {
+            const int co = m0 + row0 + 16 * i;
+            a_s[i] = (valid && co < p.C_out) ? g[(size_t)co * HWo] : 0.0f;
+        }
+        const float* xi = p.x + (size_t)n * p.C_in * p.H * p.W;
+        const int hb = ho * p.stride, wb = wo * p.stride;
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) {
+            const int hi = hb + b_dh[i], wi = wb + b_dw[i];
+            b_s[i] = (valid && b_off[i] >= 0 && hi >= 0 && hi < p.H && wi >= 0 && wi < p.W)
+                         ? xi[(size_t)b_off[i] + (size_t)hi * p.W + wi]
+                         : 0.0f;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_PER; ++i) As[buf][kk][row0 + 16 * i] = a_s[i];
+#pragma unroll
+        for (int i = 0; i < B_PER; ++i) Bs[buf][kk][row0 + 16 * i] = b_s[i];
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    const long long ktiles = pend > pbeg ? (pend - pbeg + BK - 1) / BK : 0;
+    if (ktiles > 0) {
+        load_tile(0);
+        store_tile(0);
+    }
+    __syncthreads();
+    for (long long kt = 0; kt < ktiles; ++kt) {
+        const int cur = (int)(kt & 1);
+        const bool more = kt + 1 < ktiles;
+        if (more) load_tile(kt + 1);
+#pragma unroll
+        for (int kp = 0; kp < BK / 2; ++kp) {
+            float af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) af[i] = As[cur][2 * kp + lk][wm * WM + i * 32 + lr];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = Bs[cur][2 * kp + lk][wn * WN + j * 32 + lr];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) store_tile(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Register r of lane l: channel row 8(r/4) + 4(l/32) + r%4, column l%32.
+    float* dst = p.splits == 1 ? p.dw : p.ws + (size_t)split * p.C_out * p.J;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = j0 + wn * WN + j * 32 + lr;
+        if (col >= p.J) continue;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int cbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int co = cbase + 8 * (r >> 2) + (r & 3);
+                if (co < p.C_out) dst[(size_t)co * p.J + col] = acc[i][j][r];
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) wgrad_reduce(float* __restrict__ dw, const float* __restrict__ ws, size_t n,
+                                                    int splits) {
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        float s = ws[i];
+        for (int k = 1; k < splits; ++k) s += ws[(size_t)k * n + i];
+        dw[i] = s;
+    }
+}
+
 template <int BM, int BN, int KH_T, int KW_T>
 int launch(lancius_hip_ctx* ctx, ConvParams& p) {
     p.tiles_m = (uint32_t)((p.C_out + BM - 1) / BM);
@@ -245,7 +467,7 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d: too many tiles");
     constexpr int WGM = BM >= 64 ? 2 : 1;
     constexpr int WGN = 4 / WGM;
-    if (p.C_in % 16 == 0 && p.C_out % 4 == 0) {
+    if (!p.wt && p.C_in % 16 == 0 && p.C_out % 4 == 0) {
         const size_t wbytes = (size_t)p.C_out * p.Kdim * sizeof(float);
         void* ws = nullptr;
         if (int rc = workspace(ctx, wbytes, &ws)) return rc;
@@ -318,4 +540,124 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     const int tile = tune("conv_tile", C_out > 64 ? 1 : 3);
     const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
     return rc ? rc : ok();
+}
+
+extern "C" int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx, const float* dy, const float* w,
+                                                size_t N, size_t C_in, size_t H, size_t W, size_t C_out,
+                                                size_t H_out, size_t W_out, size_t K_h, size_t K_w, size_t stride,
+                                                size_t pad) {
+    LANCIUS_REQUIRE(ctx && dx && dy && w, LANCIUS_HIP_ERR_NULL_PTR, "conv2d_bwd_input: NULL argument");
+    LANCIUS_REQUIRE(K_h && K_w && stride, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_input: empty filter or stride 0");
+    LANCIUS_REQUIRE(C_in * K_h * K_w < (1u << 30) && C_out * K_h * K_w < (1u << 30) && H * W < (1u << 30) &&
+                        H_out * W_out < (1u << 30) && N * C_in * H * W < ((size_t)1 << 40) &&
+                        N * C_out * H_out * W_out < ((size_t)1 << 40),
+                    LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_input: shape too large");
+    const size_t total = N * C_in * H * W;
+    if (total == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    // Stride 1, square filter, the shapes of a real forward conv
+    // (H = H_out + K - 1 - 2 pad, pad <= K - 1): the forward implicit GEMM
+    // over flipped weights.  Anything else: the direct kernel.
+    const bool as_conv = stride == 1 && K_h == K_w && pad + 1 <= K_h && H_out > 0 && W_out > 0 &&
+                         H + 2 * pad + 1 == H_out + K_h && W + 2 * pad + 1 == W_out + K_w && tune("conv_dgrad", 1);
+    if (!as_conv) {
+        const unsigned grid = (unsigned)std::max<size_t>(1, std::min<size_t>((total + 255) / 256, 16384));
+        hipLaunchKernelGGL(dgrad_direct, dim3(grid), dim3(256), 0, ctx->stream, dx, dy, w, (int)N, (int)C_in, (int)H,
+                           (int)W, (int)C_out, (int)H_out, (int)W_out, (int)K_h, (int)K_w, (int)stride, (int)pad);
+        return check_launch("conv2d_dgrad_direct");
+    }
+    ConvParams p{};
+    p.out = dx;
+    p.in = dy;
+    p.bias = nullptr;
+    p.N = (int)N;
+    p.C_in = (int)C_out;  // the flipped conv reads dy's channels
+    p.H = (int)H_out;
+    p.W = (int)W_out;
+    p.C_out = (int)C_in;
+    p.KH = (int)K_h;
+    p.KW = (int)K_w;
+    p.stride = 1;
+    p.pad = (int)(K_h - 1 - pad);
+    p.Ho = (int)H;
+    p.Wo = (int)W;
+    p.Kdim = (int)(C_out * K_h * K_w);
+    p.Ptotal = (long long)N * H * W;
+    p.act = LANCIUS_HIP_ACT_NONE;
+    const bool kmajor = p.C_in % 16 == 0 && p.C_out % 4 == 0;
+    void* ws = nullptr;
+    if (int rc = workspace(ctx, C_out * C_in * K_h * K_w * sizeof(float), &ws)) return rc;
+    const size_t wn = C_out * C_in * K_h * K_w;
+    hipLaunchKernelGGL(dgrad_weights, dim3((unsigned)std::min<size_t>((wn + 255) / 256, 2048)), dim3(256), 0,
+                       ctx->stream, (float*)ws, w, (int)C_out, (int)C_in, (int)K_h, (int)K_w, (int)kmajor);
+    if (int rc = check_launch("conv2d_dgrad_weights")) return rc;
+    if (kmajor)
+        p.wt = (const float*)ws;
+    else
+        p.w = (const float*)ws;
+    const int tile = tune("conv_tile", p.C_out > 64 ? 1 : 3);
+    const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
+    return rc ? rc : ok();
+}
+
+extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw, const float* dy, const float* x,
+                                                 size_t N, size_t C_in, size_t H, size_t W, size_t C_out,
+                                                 size_t H_out, size_t W_out, size_t K_h, size_t K_w, size_t stride,
+                                                 size_t pad) {
+    LANCIUS_REQUIRE(ctx && dw && dy && x, LANCIUS_HIP_ERR_NULL_PTR, "conv2d_bwd_weight: NULL argument");
+    LANCIUS_REQUIRE(K_h && K_w && stride, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: empty filter or stride 0");
+    LANCIUS_REQUIRE(C_in * K_h * K_w < (1u << 30) && C_out < (1u << 30) && H * W < (1u << 30) &&
+                        C_in * H * W < (1u << 31) && H_out * W_out < (1u << 30) &&
+                        N * C_in * H * W < ((size_t)1 << 40) &&
+                        N * C_out * H_out * W_out < ((size_t)1 << 40),
+                    LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: shape too large");
+    const size_t J = C_in * K_h * K_w;
+    if (C_out * J == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    constexpr int BM = 64, BN = 64;
+    WgradParams p{};
+    p.dw = dw;
+    p.dy = dy;
+    p.x = x;
+    p.N = (int)N;
+    p.C_in = (int)C_in;
+    p.H = (int)H;
+    p.W = (int)W;
+    p.C_out = (int)C_out;
+    p.Ho = (int)H_out;
+    p.Wo = (int)W_out;
+    p.KH = (int)K_h;
+    p.KW = (int)K_w;
+    p.stride = (int)stride;
+    p.pad = (int)pad;
+    p.J = (int)J;
+    p.Ptotal = (long long)(N * H_out * W_out);
+    p.tiles_m = (uint32_t)((C_out + BM - 1) / BM);
+    p.tiles_n = (uint32_t)((J + BN - 1) / BN);
+    const size_t tiles = (size_t)p.tiles_m * p.tiles_n;
+    LANCIUS_REQUIRE(tiles < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: too many tiles");
+    // Split the pixel reduction for ~1024 workgroups, each >= 256 pixels deep.
+    const long long ktiles = (p.Ptotal + 15) / 16;
+    long long splits = tune("conv_wgrad_split", 0);
+    if (splits <= 0) splits = std::max<long long>(1, std::min<long long>((1024 + tiles - 1) / tiles, ktiles / 16));
+    splits = std::max<long long>(1, std::min<long long>({splits, std::max<long long>(ktiles, 1), 65535}));
+    while (splits > 1 && (size_t)splits * C_out * J * sizeof(float) > ((size_t)1 << 28)) splits = (splits + 1) / 2;
+    const long long chunk_tiles = (std::max<long long>(ktiles, 1) + splits - 1) / splits;
+    p.pchunk = chunk_tiles * 16;
+    p.splits = (int)((std::max<long long>(ktiles, 1) + chunk_tiles - 1) / chunk_tiles);
+    if (p.splits > 1) {
+        void* ws = nullptr;
+        if (int rc = workspace(ctx, (size_t)p.splits * C_out * J * sizeof(float), &ws)) return rc;
+        p.ws = (float*)ws;
+    }
+    hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
+                       ctx->stream, p);
+    if (int rc = check_launch("conv2d_wgrad_mfma")) return rc;
+    if (p.splits > 1) {
+        const size_t n = C_out * J;
+        hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096)), dim3(256), 0,
+                           ctx->stream, dw, (const float*)p.ws, n, p.splits);
+        if (int rc = check_launch("conv2d_wgrad_reduce")) return rc;
+    }
+    return ok();
 }

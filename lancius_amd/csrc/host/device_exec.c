@@ -15,7 +15,11 @@
 #define MAXG LANCIUS_HIP_MAX_GROUP
 #define ALIGN_DEV 256u
 
-typedef enum { L_GEMM, L_CONV, L_ATTN, L_LN, L_SOFTMAX, L_ADD, L_RELU, L_GELU, L_BCAST } lkind;
+typedef enum {
+    L_GEMM, L_CONV, L_ATTN, L_LN, L_SOFTMAX, L_ADD, L_RELU, L_GELU, L_BCAST,
+    L_SUB, L_MUL, L_RELU_BWD, L_TRANSPOSE, L_SUM, L_SUM0, L_SUM1, L_SOFTMAX_BWD, L_CE, L_CE_BWD,
+    L_CONV_BWD_IN, L_CONV_BWD_W, L_POOL, L_POOL_BWD
+} lkind;
 
 enum { ROLE_NONE = 0, ROLE_INPUT, ROLE_CONST, ROLE_POOLED, ROLE_ALIAS, ROLE_FUSED };
 
@@ -29,7 +33,7 @@ typedef struct {
     uint32_t wave, order;
     uint32_t count;
     member_t m[MAXG];
-    size_t d[9];
+    size_t d[12];
     int act, causal, has_bias, has_res;
 } launch_t;
 
@@ -168,6 +172,20 @@ static int supported(lancius_opcode op) {
         case LANCIUS_OP_CONV2D_RELU_FUSED:
         case LANCIUS_OP_RESHAPE:
         case LANCIUS_OP_FLATTEN:
+        case LANCIUS_OP_SUB:
+        case LANCIUS_OP_MUL:
+        case LANCIUS_OP_RELU_BWD:
+        case LANCIUS_OP_TRANSPOSE:
+        case LANCIUS_OP_SUM:
+        case LANCIUS_OP_SUM_AXIS0:
+        case LANCIUS_OP_SUM_AXIS1:
+        case LANCIUS_OP_SOFTMAX_BWD:
+        case LANCIUS_OP_CROSS_ENTROPY:
+        case LANCIUS_OP_CROSS_ENTROPY_BWD:
+        case LANCIUS_OP_CONV2D_BWD:
+        case LANCIUS_OP_CONV2D_BWD_W:
+        case LANCIUS_OP_MAXPOOL2D:
+        case LANCIUS_OP_MAXPOOL2D_BWD:
             return 1;
         default:
             return 0;
@@ -302,6 +320,128 @@ static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
             L->act = n->op == LANCIUS_OP_CONV2D_RELU_FUSED ? LANCIUS_HIP_ACT_RELU : LANCIUS_HIP_ACT_NONE;
             m->in[0] = IN(n, 0);
             m->in[1] = IN(n, 1);
+            return 0;
+        }
+        case LANCIUS_OP_SUB:
+        case LANCIUS_OP_MUL:
+        case LANCIUS_OP_RELU_BWD:
+            /* elementwise over the node's elements (lancius_scheduler.c:236-245,279-283) */
+            if (elems(n->inputs[0]) < e || elems(n->inputs[1]) < e) return fail(LANCIUS_HIP_ERR_SHAPE, "binary sizes");
+            L->kind = n->op == LANCIUS_OP_SUB ? L_SUB : n->op == LANCIUS_OP_MUL ? L_MUL : L_RELU_BWD;
+            L->d[0] = e;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            return 0;
+        case LANCIUS_OP_TRANSPOSE:
+        case LANCIUS_OP_SUM_AXIS0:
+        case LANCIUS_OP_SUM_AXIS1: {
+            /* rows x cols of the input's first two dims (:246-267) */
+            const lancius_node* a = n->inputs[0];
+            const size_t R = a->shape[0], Cc = a->ndim > 1 ? a->shape[1] : 1;
+            const size_t need = n->op == LANCIUS_OP_TRANSPOSE ? R * Cc : n->op == LANCIUS_OP_SUM_AXIS0 ? Cc : R;
+            if (elems(a) < R * Cc || e < need) return fail(LANCIUS_HIP_ERR_SHAPE, "TRANSPOSE/SUM_AXIS sizes");
+            L->kind = n->op == LANCIUS_OP_TRANSPOSE ? L_TRANSPOSE : n->op == LANCIUS_OP_SUM_AXIS0 ? L_SUM0 : L_SUM1;
+            L->d[0] = R;
+            L->d[1] = Cc;
+            m->in[0] = IN(n, 0);
+            return 0;
+        }
+        case LANCIUS_OP_SUM:
+            if (e < 1) return fail(LANCIUS_HIP_ERR_SHAPE, "SUM output");
+            L->kind = L_SUM;
+            L->d[0] = elems(n->inputs[0]);
+            m->in[0] = IN(n, 0);
+            return 0;
+        case LANCIUS_OP_SOFTMAX_BWD:
+            if (n->ndim != 2 || elems(n->inputs[0]) < e || elems(n->inputs[1]) < e)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "SOFTMAX_BWD sizes");
+            L->kind = L_SOFTMAX_BWD;
+            L->d[0] = n->shape[0];
+            L->d[1] = n->shape[1];
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            return 0;
+        case LANCIUS_OP_CROSS_ENTROPY: {
+            /* rows x cols of the logits (:70) */
+            const lancius_node* x = n->inputs[0];
+            const size_t R = x->shape[0], Cc = x->ndim > 1 ? x->shape[1] : 1;
+            if (!R || !Cc || e < 1 || elems(x) < R * Cc || elems(n->inputs[1]) < R * Cc)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "CROSS_ENTROPY sizes");
+            L->kind = L_CE;
+            L->d[0] = R;
+            L->d[1] = Cc;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            return 0;
+        }
+        case LANCIUS_OP_CROSS_ENTROPY_BWD: {
+            /* rows x cols of the node (:92) */
+            const size_t R = n->shape[0], Cc = n->ndim > 1 ? n->shape[1] : 1;
+            if (elems(n->inputs[0]) < R * Cc || elems(n->inputs[1]) < R * Cc || elems(n->inputs[2]) < 1 ||
+                e < R * Cc)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "CROSS_ENTROPY_BWD sizes");
+            L->kind = L_CE_BWD;
+            L->d[0] = R;
+            L->d[1] = Cc;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            m->in[2] = IN(n, 2);
+            return 0;
+        }
+        case LANCIUS_OP_CONV2D_BWD:
+        case LANCIUS_OP_CONV2D_BWD_W: {
+            /* CONV2D_BWD: inputs grad, fwd_in, fwd_w; filter from fwd_w
+             * (lancius_vision_ops.c:126-137).  CONV2D_BWD_W: inputs grad,
+             * fwd_in; C_out and filter from the node (:138-148). */
+            const lancius_node* g = n->inputs[0];
+            const lancius_node* x = n->inputs[1];
+            const int bwd_in = n->op == LANCIUS_OP_CONV2D_BWD;
+            const lancius_node* w = bwd_in ? n->inputs[2] : NULL;
+            if (g->ndim != 4 || x->ndim != 4 || (bwd_in && w->ndim != 4) || n->ndim != 4 || n->stride == 0)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "CONV2D backward ranks");
+            const size_t N = x->shape[0], Ci = x->shape[1], H = x->shape[2], W = x->shape[3];
+            const size_t Co = bwd_in ? w->shape[0] : n->shape[0];
+            const size_t Kh = bwd_in ? w->shape[2] : n->shape[2], Kw = bwd_in ? w->shape[3] : n->shape[3];
+            const size_t Ho = g->shape[2], Wo = g->shape[3];
+            if (!Kh || !Kw) return fail(LANCIUS_HIP_ERR_SHAPE, "CONV2D backward filter");
+            /* every (ho, wo) tap the reference visits lies in [-pad, H + pad) */
+            if (elems(g) < N * Co * Ho * Wo || (bwd_in && (w->shape[1] != Ci || elems(w) < Co * Ci * Kh * Kw)) ||
+                (!bwd_in && n->shape[1] != Ci) || elems(x) < N * Ci * H * W ||
+                e < (bwd_in ? N * Ci * H * W : Co * Ci * Kh * Kw))
+                return fail(LANCIUS_HIP_ERR_SHAPE, "CONV2D backward sizes");
+            L->kind = bwd_in ? L_CONV_BWD_IN : L_CONV_BWD_W;
+            const size_t d[11] = {N, Ci, H, W, Co, Ho, Wo, Kh, Kw, n->stride, n->pad};
+            memcpy(L->d, d, sizeof(d));
+            m->in[0] = IN(n, 0);
+            m->in[1] = bwd_in ? IN(n, 2) : IN(n, 1);
+            return 0;
+        }
+        case LANCIUS_OP_MAXPOOL2D:
+        case LANCIUS_OP_MAXPOOL2D_BWD: {
+            /* K = kernel_h (lancius_vision_ops.c:87,155); BWD: inputs grad,
+             * fwd_in, windows from grad's spatial size (:156) */
+            const int bwd = n->op == LANCIUS_OP_MAXPOOL2D_BWD;
+            const lancius_node* x = n->inputs[bwd ? 1 : 0];
+            const size_t K = n->kernel_h, st = n->stride;
+            if (x->ndim != 4 || !K || !st || x->shape[2] < K || x->shape[3] < K)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "MAXPOOL2D shape");
+            const size_t N = x->shape[0], Cc = x->shape[1], H = x->shape[2], W = x->shape[3];
+            size_t Ho = (H - K) / st + 1, Wo = (W - K) / st + 1;
+            if (bwd) {
+                const lancius_node* g = n->inputs[0];
+                if (g->ndim != 4) return fail(LANCIUS_HIP_ERR_SHAPE, "MAXPOOL2D_BWD grad rank");
+                if (g->shape[2] > Ho || g->shape[3] > Wo || elems(g) < N * Cc * g->shape[2] * g->shape[3])
+                    return fail(LANCIUS_HIP_ERR_SHAPE, "MAXPOOL2D_BWD grad windows");
+                Ho = g->shape[2];
+                Wo = g->shape[3];
+            }
+            if (elems(x) < N * Cc * H * W || e < (bwd ? N * Cc * H * W : N * Cc * Ho * Wo))
+                return fail(LANCIUS_HIP_ERR_SHAPE, "MAXPOOL2D sizes");
+            L->kind = bwd ? L_POOL_BWD : L_POOL;
+            const size_t d[8] = {N, Cc, H, W, Ho, Wo, K, st};
+            memcpy(L->d, d, sizeof(d));
+            m->in[0] = IN(n, 0);
+            if (bwd) m->in[1] = IN(n, 1);
             return 0;
         }
         default:
@@ -800,6 +940,41 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
             return lancius_hip_gelu_f32(ctx, P(m->out), P(m->in[0]), L->d[0]);
         case L_BCAST:
             return lancius_hip_broadcast_f32(ctx, P(m->out), P(m->in[0]), L->d[0], L->d[1], L->d[2]);
+        case L_SUB:
+            return lancius_hip_sub_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0]);
+        case L_MUL:
+            return lancius_hip_mul_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0]);
+        case L_RELU_BWD:
+            return lancius_hip_relu_bwd_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0]);
+        case L_TRANSPOSE:
+            return lancius_hip_transpose_f32(ctx, P(m->out), P(m->in[0]), L->d[0], L->d[1]);
+        case L_SUM:
+            return lancius_hip_sum_f32(ctx, P(m->out), P(m->in[0]), L->d[0]);
+        case L_SUM0:
+            return lancius_hip_sum_axis0_f32(ctx, P(m->out), P(m->in[0]), L->d[0], L->d[1]);
+        case L_SUM1:
+            return lancius_hip_sum_axis1_f32(ctx, P(m->out), P(m->in[0]), L->d[0], L->d[1]);
+        case L_SOFTMAX_BWD:
+            return lancius_hip_softmax_bwd_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1]);
+        case L_CE:
+            return lancius_hip_cross_entropy_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1]);
+        case L_CE_BWD:
+            return lancius_hip_cross_entropy_bwd_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), P(m->in[2]), L->d[0],
+                                                     L->d[1]);
+        case L_CONV_BWD_IN:
+            return lancius_hip_conv2d_bwd_input_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1],
+                                                    L->d[2], L->d[3], L->d[4], L->d[5], L->d[6], L->d[7], L->d[8],
+                                                    L->d[9], L->d[10]);
+        case L_CONV_BWD_W:
+            return lancius_hip_conv2d_bwd_weight_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1],
+                                                     L->d[2], L->d[3], L->d[4], L->d[5], L->d[6], L->d[7], L->d[8],
+                                                     L->d[9], L->d[10]);
+        case L_POOL:
+            return lancius_hip_maxpool2d_f32(ctx, P(m->out), P(m->in[0]), L->d[0], L->d[1], L->d[2], L->d[3],
+                                             L->d[6], L->d[7]);
+        case L_POOL_BWD:
+            return lancius_hip_maxpool2d_bwd_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1],
+                                                 L->d[2], L->d[3], L->d[4], L->d[5], L->d[6], L->d[7]);
     }
     return LANCIUS_HIP_ERR_INTERNAL;
 }

@@ -417,3 +417,257 @@ lancius_node* lancius_layernorm(lancius_graph* g, const lancius_node* in, const 
 
 /* lancius_ir.c:84-89 */
 lancius_node* lancius_gelu(lancius_graph* g, const lancius_node* in) { return unary(g, LANCIUS_OP_GELU, in); }
+
+/* ---- builders of the training graph ----------------------------------------- */
+
+/* Two inputs, the shape of `a` (lancius_ir.c:164-177: SUB and MUL, like ADD,
+ * do no shape check). */
+static lancius_node* binary(lancius_graph* g, lancius_opcode op, const lancius_node* a, const lancius_node* b) {
+    if (!a || !b) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, op, a->ndim, 2);
+    if (n) {
+        copy_shape(n, a);
+        n->inputs[0] = a;
+        n->inputs[1] = b;
+    }
+    return n;
+}
+
+/* lancius_ir.c:164-170 */
+lancius_node* lancius_sub(lancius_graph* g, const lancius_node* a, const lancius_node* b) {
+    return binary(g, LANCIUS_OP_SUB, a, b);
+}
+
+/* lancius_ir.c:171-177 */
+lancius_node* lancius_mul(lancius_graph* g, const lancius_node* a, const lancius_node* b) {
+    return binary(g, LANCIUS_OP_MUL, a, b);
+}
+
+/* lancius_ir.c:222-226: shape of the gradient. */
+lancius_node* lancius_relu_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_a) {
+    return binary(g, LANCIUS_OP_RELU_BWD, grad, fwd_a);
+}
+
+/* lancius_ir.c:227-231 */
+lancius_node* lancius_softmax_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_y) {
+    return binary(g, LANCIUS_OP_SOFTMAX_BWD, grad, fwd_y);
+}
+
+/* A 2-D node of `rows` x `cols` with one input. */
+static lancius_node* shaped1(lancius_graph* g, lancius_opcode op, const lancius_node* a, size_t rows, size_t cols) {
+    lancius_node* n = new_node(g, op, 2, 1);
+    if (n) {
+        n->shape[0] = rows;
+        n->shape[1] = cols;
+        n->inputs[0] = a;
+    }
+    return n;
+}
+
+/* lancius_ir.c:207-211: [1,1] over every element of the input. */
+lancius_node* lancius_sum(lancius_graph* g, const lancius_node* a) {
+    if (!a) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    return shaped1(g, LANCIUS_OP_SUM, a, 1, 1);
+}
+
+/* lancius_ir.c:217-221: 2-D only. */
+lancius_node* lancius_transpose(lancius_graph* g, const lancius_node* a) {
+    if (!a || a->ndim != 2) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    return shaped1(g, LANCIUS_OP_TRANSPOSE, a, a->shape[1], a->shape[0]);
+}
+
+/* lancius_ir.c:232-236 */
+lancius_node* lancius_sum_axis0(lancius_graph* g, const lancius_node* a) {
+    if (!a || a->ndim != 2) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    return shaped1(g, LANCIUS_OP_SUM_AXIS0, a, 1, a->shape[1]);
+}
+
+/* lancius_ir.c:237-241 */
+lancius_node* lancius_sum_axis1(lancius_graph* g, const lancius_node* a) {
+    if (!a || a->ndim != 2) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    return shaped1(g, LANCIUS_OP_SUM_AXIS1, a, a->shape[0], 1);
+}
+
+/* lancius_ir.c:92-97: a 4-D BROADCAST (the executor fills it from a scalar). */
+lancius_node* lancius_broadcast_4d(lancius_graph* g, const lancius_node* a, size_t nn, size_t c, size_t h, size_t w) {
+    if (!a) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_BROADCAST, 4, 1);
+    if (n) {
+        n->shape[0] = nn;
+        n->shape[1] = c;
+        n->shape[2] = h;
+        n->shape[3] = w;
+        n->inputs[0] = a;
+    }
+    return n;
+}
+
+/* lancius_ir.c:263-280: no padding, square window. */
+lancius_node* lancius_maxpool2d(lancius_graph* g, const lancius_node* in, uint32_t kernel, uint32_t stride) {
+    if (!in || in->ndim != 4 || kernel == 0 || stride == 0 || in->shape[2] < kernel || in->shape[3] < kernel) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_MAXPOOL2D, 4, 1);
+    if (n) {
+        n->shape[0] = in->shape[0];
+        n->shape[1] = in->shape[1];
+        n->shape[2] = (in->shape[2] - kernel) / stride + 1;
+        n->shape[3] = (in->shape[3] - kernel) / stride + 1;
+        n->kernel_h = kernel;
+        n->kernel_w = kernel;
+        n->stride = stride;
+        n->inputs[0] = in;
+    }
+    return n;
+}
+
+/* lancius_ir.c:337-343: scalar loss of logits against same-shape targets. */
+lancius_node* lancius_cross_entropy(lancius_graph* g, const lancius_node* logits, const lancius_node* targets) {
+    if (!logits || !targets || logits->ndim != 2 || targets->ndim != 2 || logits->shape[0] != targets->shape[0] ||
+        logits->shape[1] != targets->shape[1]) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_CROSS_ENTROPY, 2, 2);
+    if (n) {
+        n->shape[0] = 1;
+        n->shape[1] = 1;
+        n->inputs[0] = logits;
+        n->inputs[1] = targets;
+    }
+    return n;
+}
+
+/* lancius_ir.c:344-350: shape of the logits; inputs logits, targets, scalar
+ * upstream gradient. */
+lancius_node* lancius_cross_entropy_bwd(lancius_graph* g, const lancius_node* logits, const lancius_node* targets,
+                                        const lancius_node* grad_out) {
+    if (!logits || !targets || !grad_out) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_CROSS_ENTROPY_BWD, logits->ndim, 3);
+    if (n) {
+        copy_shape(n, logits);
+        n->inputs[0] = logits;
+        n->inputs[1] = targets;
+        n->inputs[2] = grad_out;
+    }
+    return n;
+}
+
+/* lancius_ir.c:351-359: shape of the forward input; inputs grad, fwd_in, fwd_w. */
+lancius_node* lancius_conv2d_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_in,
+                                 const lancius_node* fwd_w, uint32_t stride, uint32_t pad) {
+    if (!grad || !fwd_in || !fwd_w) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_CONV2D_BWD, 4, 3);
+    if (n) {
+        for (int d = 0; d < 4; d++) n->shape[d] = fwd_in->shape[d];
+        n->stride = stride;
+        n->pad = pad;
+        n->inputs[0] = grad;
+        n->inputs[1] = fwd_in;
+        n->inputs[2] = fwd_w;
+    }
+    return n;
+}
+
+/* lancius_ir.c:300-313: [C_out (grad channels), C_in (fwd_in channels), k_h, k_w]. */
+lancius_node* lancius_conv2d_bwd_w(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_in,
+                                   uint32_t k_h, uint32_t k_w, uint32_t stride, uint32_t pad) {
+    if (!grad || !fwd_in) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_CONV2D_BWD_W, 4, 2);
+    if (n) {
+        n->shape[0] = grad->shape[1];
+        n->shape[1] = fwd_in->shape[1];
+        n->shape[2] = k_h;
+        n->shape[3] = k_w;
+        n->kernel_h = k_h;
+        n->kernel_w = k_w;
+        n->stride = stride;
+        n->pad = pad;
+        n->inputs[0] = grad;
+        n->inputs[1] = fwd_in;
+    }
+    return n;
+}
+
+/* lancius_ir.c:360-368: shape of the forward input; inputs grad, fwd_in. */
+lancius_node* lancius_maxpool2d_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_in,
+                                    uint32_t kernel, uint32_t stride) {
+    if (!grad || !fwd_in) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_MAXPOOL2D_BWD, 4, 2);
+    if (n) {
+        for (int d = 0; d < 4; d++) n->shape[d] = fwd_in->shape[d];
+        n->kernel_h = kernel;
+        n->kernel_w = kernel;
+        n->stride = stride;
+        n->inputs[0] = grad;
+        n->inputs[1] = fwd_in;
+    }
+    return n;
+}
+
+/* lancius_ir.c:315-325: 4-D axis permutation (no executor runs it). */
+lancius_node* lancius_permute(lancius_graph* g, const lancius_node* in, uint32_t a0, uint32_t a1, uint32_t a2,
+                              uint32_t a3) {
+    if (!in || in->ndim != 4 || a0 > 3 || a1 > 3 || a2 > 3 || a3 > 3) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_PERMUTE, 4, 1);
+    if (n) {
+        const uint32_t ax[4] = {a0, a1, a2, a3};
+        for (int d = 0; d < 4; d++) {
+            n->axes[d] = ax[d];
+            n->shape[d] = in->shape[ax[d]];
+        }
+        n->inputs[0] = in;
+    }
+    return n;
+}
+
+/* lancius_ir.c:326-336: [B,M,K] x [B,K,N] -> [B,M,N] (no executor runs it). */
+lancius_node* lancius_matmul_batched(lancius_graph* g, const lancius_node* a, const lancius_node* b) {
+    if (!a || !b || a->ndim != 3 || b->ndim != 3 || a->shape[0] != b->shape[0] || a->shape[2] != b->shape[1]) {
+        lancius_set_error(LANCIUS_ERROR_SHAPE_MISMATCH);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_MATMUL_BATCHED, 3, 2);
+    if (n) {
+        n->shape[0] = a->shape[0];
+        n->shape[1] = a->shape[1];
+        n->shape[2] = b->shape[2];
+        n->inputs[0] = a;
+        n->inputs[1] = b;
+    }
+    return n;
+}

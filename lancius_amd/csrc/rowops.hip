@@ -1,5 +1,6 @@
 // Memory-bound row and elementwise kernels: LayerNorm, softmax(+argmax),
-// GELU, ReLU, ADD, BROADCAST, fill, copy.
+// GELU, ReLU, ADD, SUB, MUL, BROADCAST, fill, copy, and the row ops of the
+// training graphs (RELU_BWD, SOFTMAX_BWD, CROSS_ENTROPY and its gradient).
 //
 // Row kernels use one wave64 per row and keep the row in registers, so a row
 // is read from HBM once and written once; reductions are wave shuffles
@@ -135,13 +136,97 @@ __global__ void __launch_bounds__(kRowThreads) softmax_rows(float* __restrict__ 
     }
 }
 
+// SOFTMAX_BWD (lancius_scheduler.c:295-304): out = y * (dy - sum_c dy*y).
+__global__ void __launch_bounds__(kRowThreads) softmax_bwd_rows(float* __restrict__ out, const float* __restrict__ dy,
+                                                                const float* __restrict__ y, int rows, int cols) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const size_t base = (size_t)row * cols;
+    float dot = 0.0f;
+    for (int c = lane; c < cols; c += 64) dot += dy[base + c] * y[base + c];
+    dot = wave_sum(dot);
+    for (int c = lane; c < cols; c += 64) out[base + c] = y[base + c] * (dy[base + c] - dot);
+}
+
+// Row max and sum of exp(x - max) of one row, for one wave.
+__device__ __forceinline__ void row_lse_parts(const float* __restrict__ x, int cols, int lane, float& m, float& s) {
+    m = -INFINITY;
+    for (int c = lane; c < cols; c += 64) m = fmaxf(m, x[c]);
+    m = wave_max(m);
+    s = 0.0f;
+    for (int c = lane; c < cols; c += 64) s += expf(x[c] - m);
+    s = wave_sum(s);
+}
+
+// CROSS_ENTROPY, first pass (lancius_scheduler.c:68-83): per row,
+// sum over the entries with y == 1 of (x - logsumexp(x)), in fp64.
+__global__ void __launch_bounds__(kRowThreads) cross_entropy_rows(double* __restrict__ row_terms,
+                                                                  const float* __restrict__ x,
+                                                                  const float* __restrict__ y, int rows, int cols) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * cols;
+    const float* yr = y + (size_t)row * cols;
+    float m, s;
+    row_lse_parts(xr, cols, lane, m, s);
+    const double lse = (double)logf(s) + (double)m;
+    double t = 0.0;
+    for (int c = lane; c < cols; c += 64)
+        if (yr[c] == 1.0f) t += (double)xr[c] - lse;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+    if (lane == 0) row_terms[row] = t;
+}
+
+// Second pass: out[0] = |-(sum of row terms) / rows| (:84-85), summed by one
+// workgroup in a fixed order.
+__global__ void __launch_bounds__(256) cross_entropy_finish(float* __restrict__ out,
+                                                            const double* __restrict__ row_terms, int rows) {
+    __shared__ double part[256];
+    double t = 0.0;
+    for (int r = threadIdx.x; r < rows; r += 256) t += row_terms[r];
+    part[threadIdx.x] = t;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = (float)fabs(-part[0] / (double)rows);
+}
+
+// CROSS_ENTROPY_BWD (lancius_scheduler.c:89-104):
+// out = (exp(x - max) / sum - y) * g[0] / rows.
+__global__ void __launch_bounds__(kRowThreads) cross_entropy_bwd_rows(float* __restrict__ out,
+                                                                      const float* __restrict__ x,
+                                                                      const float* __restrict__ y,
+                                                                      const float* __restrict__ g, int rows,
+                                                                      int cols) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const size_t base = (size_t)row * cols;
+    float m, s;
+    row_lse_parts(x + base, cols, lane, m, s);
+    const float scale = (float)((double)g[0] / (double)rows);
+    for (int c = lane; c < cols; c += 64) out[base + c] = (expf(x[base + c] - m) / s - y[base + c]) * scale;
+}
+
 // ---- elementwise --------------------------------------------------------
 
-enum EwOp : int { kAdd = 0, kRelu = 1, kGelu = 2, kCopy = 3 };
+enum EwOp : int { kAdd = 0, kRelu = 1, kGelu = 2, kCopy = 3, kSub = 4, kMul = 5, kReluBwd = 6 };
+
+constexpr bool binary_op(int op) { return op == kAdd || op == kSub || op == kMul || op == kReluBwd; }
 
 template <int OP>
 __device__ __forceinline__ float ew(float a, float b) {
     if constexpr (OP == kAdd) return a + b;
+    if constexpr (OP == kSub) return a - b;
+    if constexpr (OP == kMul) return a * b;
+    // RELU_BWD (lancius_scheduler.c:279-283): a = incoming gradient, b = the
+    // forward input; NaN in b gives 0 like the reference's '>' test.
+    if constexpr (OP == kReluBwd) return b > 0.0f ? a : 0.0f;
     if constexpr (OP == kRelu) return relu_ref(a);
     if constexpr (OP == kGelu) return gelu_ref(a);
     return a;
@@ -153,7 +238,7 @@ __global__ void __launch_bounds__(256) elementwise_vec(float* __restrict__ out, 
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
         const f32x4 x = ((const f32x4*)a)[i];
-        const f32x4 y = (OP == kAdd) ? ((const f32x4*)b)[i] : x;
+        const f32x4 y = binary_op(OP) ? ((const f32x4*)b)[i] : x;
         f32x4 o;
         o.x = ew<OP>(x.x, y.x);
         o.y = ew<OP>(x.y, y.y);
@@ -168,7 +253,7 @@ __global__ void __launch_bounds__(256) elementwise_scalar(float* __restrict__ ou
                                                           const float* __restrict__ b, size_t begin, size_t n) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = begin + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-        out[i] = ew<OP>(a[i], OP == kAdd ? b[i] : 0.0f);
+        out[i] = ew<OP>(a[i], binary_op(OP) ? b[i] : 0.0f);
 }
 
 __global__ void __launch_bounds__(256) broadcast_rows(float* __restrict__ out, const float* __restrict__ row,
@@ -197,10 +282,10 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 template <int OP>
 int run_elementwise(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n, const char* name) {
-    LANCIUS_REQUIRE(ctx && out && a && (OP != kAdd || b), LANCIUS_HIP_ERR_NULL_PTR, "%s: NULL argument", name);
+    LANCIUS_REQUIRE(ctx && out && a && (!binary_op(OP) || b), LANCIUS_HIP_ERR_NULL_PTR, "%s: NULL argument", name);
     if (n == 0) return ok();
     if (int rc = bind_device(ctx)) return rc;
-    const bool vec = aligned16(out) && aligned16(a) && (OP != kAdd || aligned16(b));
+    const bool vec = aligned16(out) && aligned16(a) && (!binary_op(OP) || aligned16(b));
     size_t done = 0;
     if (vec && n >= 4) {
         const size_t n4 = n / 4;
@@ -276,6 +361,57 @@ int lancius_hip_gelu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_
 
 int lancius_hip_copy_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n) {
     return run_elementwise<kCopy>(ctx, out, in, nullptr, n, "copy");
+}
+
+int lancius_hip_sub_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n) {
+    return run_elementwise<kSub>(ctx, out, a, b, n, "sub");
+}
+
+int lancius_hip_mul_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n) {
+    return run_elementwise<kMul>(ctx, out, a, b, n, "mul");
+}
+
+int lancius_hip_relu_bwd_f32(lancius_hip_ctx* ctx, float* out, const float* grad, const float* fwd, size_t n) {
+    return run_elementwise<kReluBwd>(ctx, out, grad, fwd, n, "relu_bwd");
+}
+
+int lancius_hip_softmax_bwd_f32(lancius_hip_ctx* ctx, float* out, const float* dy, const float* y, size_t rows,
+                                size_t cols) {
+    LANCIUS_REQUIRE(ctx && out && dy && y, LANCIUS_HIP_ERR_NULL_PTR, "softmax_bwd: NULL argument");
+    LANCIUS_REQUIRE(cols < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE, "softmax_bwd: rows=%zu cols=%zu",
+                    rows, cols);
+    if (rows == 0 || cols == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(softmax_bwd_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0, ctx->stream, out,
+                       dy, y, (int)rows, (int)cols);
+    return check_launch("softmax_bwd");
+}
+
+int lancius_hip_cross_entropy_f32(lancius_hip_ctx* ctx, float* out, const float* x, const float* y, size_t rows,
+                                  size_t cols) {
+    LANCIUS_REQUIRE(ctx && out && x && y, LANCIUS_HIP_ERR_NULL_PTR, "cross_entropy: NULL argument");
+    LANCIUS_REQUIRE(rows > 0 && cols > 0 && cols < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
+                    "cross_entropy: rows=%zu cols=%zu", rows, cols);
+    if (int rc = bind_device(ctx)) return rc;
+    void* ws = nullptr;
+    if (int rc = workspace(ctx, rows * sizeof(double), &ws)) return rc;
+    hipLaunchKernelGGL(cross_entropy_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0, ctx->stream,
+                       (double*)ws, x, y, (int)rows, (int)cols);
+    if (int rc = check_launch("cross_entropy_rows")) return rc;
+    hipLaunchKernelGGL(cross_entropy_finish, dim3(1), dim3(256), 0, ctx->stream, out, (const double*)ws, (int)rows);
+    return check_launch("cross_entropy_finish");
+}
+
+int lancius_hip_cross_entropy_bwd_f32(lancius_hip_ctx* ctx, float* out, const float* x, const float* y,
+                                      const float* g, size_t rows, size_t cols) {
+    LANCIUS_REQUIRE(ctx && out && x && y && g, LANCIUS_HIP_ERR_NULL_PTR, "cross_entropy_bwd: NULL argument");
+    LANCIUS_REQUIRE(cols < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
+                    "cross_entropy_bwd: rows=%zu cols=%zu", rows, cols);
+    if (rows == 0 || cols == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(cross_entropy_bwd_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0,
+                       ctx->stream, out, x, y, g, (int)rows, (int)cols);
+    return check_launch("cross_entropy_bwd");
 }
 
 int lancius_hip_broadcast_f32(lancius_hip_ctx* ctx, float* out, const float* row, size_t rows, size_t cols,

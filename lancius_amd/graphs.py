@@ -143,3 +143,159 @@ def build_relu_chain(lib: C.CDLL, depth: int = 20, rows: int = 1024, cols: int =
         bg.nodes[f"relu{i}"] = cur
     bg.outputs = [f"relu{depth - 1}"]
     return bg
+
+
+# ---- training graphs (forward + lancius_ir_autodiff) --------------------------
+
+
+def build_mlp_ce(lib: C.CDLL, batch: int = 64, d_in: int = 784, hidden: int = 128, classes: int = 10) -> BuiltGraph:
+    """Forward graph of B/examples/train_mnist.c:87-96 (creation order kept):
+    INPUT X, W1, b1, W2, b2, Y; MATMUL -> ADD(BROADCAST b1) -> RELU -> MATMUL
+    -> ADD(BROADCAST b2) -> CROSS_ENTROPY against Y."""
+    bg = BuiltGraph(lib, _ok(lib.lancius_graph_create(), "graph_create"))
+    g = bg.g
+    x = _inp(bg, "X", batch, d_in)
+    w1 = _inp(bg, "W1", d_in, hidden)
+    b1 = _inp(bg, "b1", 1, hidden)
+    w2 = _inp(bg, "W2", hidden, classes)
+    b2 = _inp(bg, "b2", 1, classes)
+    y = _inp(bg, "Y", batch, classes)
+    z1 = _ok(lib.lancius_matmul(g, x, w1), "Z1")
+    a1 = _ok(lib.lancius_add(g, z1, _ok(lib.lancius_broadcast(g, b1, batch, hidden), "bc1")), "A1")
+    h1 = _ok(lib.lancius_relu(g, a1), "H1")
+    z2 = _ok(lib.lancius_matmul(g, h1, w2), "Z2")
+    a2 = _ok(lib.lancius_add(g, z2, _ok(lib.lancius_broadcast(g, b2, batch, classes), "bc2")), "A2")
+    loss = _ok(lib.lancius_cross_entropy(g, a2, y), "loss")
+    bg.nodes.update(Z1=z1, A1=a1, H1=h1, Z2=z2, A2=a2, loss=loss)
+    bg.outputs = ["loss"]
+    return bg
+
+
+def build_cnn_ce(lib: C.CDLL, batch: int = 8, fuse: bool = False) -> BuiltGraph:
+    """Forward graph of B/examples/train_cifar10.c:89-119 (creation order kept):
+    conv 5x5 pad 2 (3->16) -> RELU -> MAXPOOL 2/2 -> conv 5x5 pad 2 (16->32) ->
+    RELU -> MAXPOOL 2/2 -> FLATTEN -> FC 2048->120 + bias -> RELU -> FC 120->10
+    + bias -> CROSS_ENTROPY.  fuse=True runs lancius_optimize_fusion first
+    (Conv+ReLU pairs become CONV2D_RELU_FUSED + NOP)."""
+    bg = BuiltGraph(lib, _ok(lib.lancius_graph_create(), "graph_create"))
+    g = bg.g
+    x = _inp(bg, "X", batch, 3, 32, 32)
+    w1 = _inp(bg, "W1", 16, 3, 5, 5)
+    c1 = _ok(lib.lancius_conv2d(g, x, w1, 1, 2), "C1")
+    r1 = _ok(lib.lancius_relu(g, c1), "R1")
+    p1 = _ok(lib.lancius_maxpool2d(g, r1, 2, 2), "P1")
+    w2 = _inp(bg, "W2", 32, 16, 5, 5)
+    c2 = _ok(lib.lancius_conv2d(g, p1, w2, 1, 2), "C2")
+    r2 = _ok(lib.lancius_relu(g, c2), "R2")
+    p2 = _ok(lib.lancius_maxpool2d(g, r2, 2, 2), "P2")
+    f = _ok(lib.lancius_flatten(g, p2), "F")
+    w3 = _inp(bg, "W3", 2048, 120)
+    b1 = _inp(bg, "b1", 1, 120)
+    z1 = _ok(lib.lancius_matmul(g, f, w3), "Z1")
+    a1 = _ok(lib.lancius_add(g, z1, _ok(lib.lancius_broadcast(g, b1, batch, 120), "bc1")), "A1")
+    h1 = _ok(lib.lancius_relu(g, a1), "H1")
+    w4 = _inp(bg, "W4", 120, 10)
+    b2 = _inp(bg, "b2", 1, 10)
+    z2 = _ok(lib.lancius_matmul(g, h1, w4), "Z2")
+    a2 = _ok(lib.lancius_add(g, z2, _ok(lib.lancius_broadcast(g, b2, batch, 10), "bc2")), "A2")
+    y = _inp(bg, "Y", batch, 10)
+    loss = _ok(lib.lancius_cross_entropy(g, a2, y), "loss")
+    bg.nodes.update(C1=c1, R1=r1, P1=p1, C2=c2, R2=r2, P2=p2, F=f, Z1=z1, A1=a1, H1=h1, Z2=z2, A2=a2, loss=loss)
+    if fuse:
+        lib.lancius_optimize_fusion(g)
+    bg.outputs = ["loss"]
+    return bg
+
+
+def build_gradcheck(lib: C.CDLL) -> BuiltGraph:
+    """Forward graph of S9/examples/test_grad_check.c:28-37: conv 3x3 (3->4,
+    stride 1, pad 0) on [2,3,8,8] -> RELU -> FLATTEN -> MATMUL [144,5] ->
+    CROSS_ENTROPY."""
+    bg = BuiltGraph(lib, _ok(lib.lancius_graph_create(), "graph_create"))
+    g = bg.g
+    x = _inp(bg, "X", 2, 3, 8, 8)
+    w1 = _inp(bg, "W1", 4, 3, 3, 3)
+    c1 = _ok(lib.lancius_conv2d(g, x, w1, 1, 0), "C1")
+    r1 = _ok(lib.lancius_relu(g, c1), "R1")
+    f1 = _ok(lib.lancius_flatten(g, r1), "F1")
+    w2 = _inp(bg, "W2", 144, 5)
+    z1 = _ok(lib.lancius_matmul(g, f1, w2), "Z1")
+    y = _inp(bg, "Y", 2, 5)
+    loss = _ok(lib.lancius_cross_entropy(g, z1, y), "loss")
+    bg.nodes.update(C1=c1, R1=r1, F1=f1, Z1=z1, loss=loss)
+    bg.outputs = ["loss"]
+    return bg
+
+
+def build_ops_loss(lib: C.CDLL, R: int = 8, Cc: int = 5) -> BuiltGraph:
+    """A scalar loss whose gradient graph holds the remaining dispatch ops
+    (R >= Cc: the BROADCAST of the [R,1] vector v reads v[c] for c < Cc,
+    lancius_scheduler.c:275-276):
+      A = X - Y;  B = A * X;  S = SOFTMAX(B);  S2 = S + BROADCAST(v);
+      M = TRANSPOSE(S2) . Z;  loss = SUM(M * Wm)
+    (the product with Wm keeps the softmax gradient from being constant along
+    rows, which SOFTMAX_BWD would map to exactly zero; v joins after the
+    softmax because row sums of a softmax gradient are zero).
+    Backward: BROADCAST of the seed, MUL, MATMUL/TRANSPOSE, SOFTMAX_BWD,
+    SUM_AXIS1 (v's gradient), SUB's -1 CONST and ADD accumulation into X."""
+    bg = BuiltGraph(lib, _ok(lib.lancius_graph_create(), "graph_create"))
+    g = bg.g
+    x = _inp(bg, "X", R, Cc)
+    y = _inp(bg, "Y", R, Cc)
+    v = _inp(bg, "v", R, 1)
+    z = _inp(bg, "Z", R, Cc)
+    wm = _inp(bg, "Wm", Cc, Cc)
+    a = _ok(lib.lancius_sub(g, x, y), "A")
+    b = _ok(lib.lancius_mul(g, a, x), "B")
+    s = _ok(lib.lancius_softmax(g, b), "S")
+    s2 = _ok(lib.lancius_add(g, s, _ok(lib.lancius_broadcast(g, v, R, Cc), "bcv")), "S2")
+    t = _ok(lib.lancius_transpose(g, s2), "T")
+    m = _ok(lib.lancius_matmul(g, t, z), "M")
+    m2 = _ok(lib.lancius_mul(g, m, wm), "M2")
+    loss = _ok(lib.lancius_sum(g, m2), "loss")
+    bg.nodes.update(A=a, B=b, S=s, S2=s2, T=t, M=m, M2=m2, loss=loss)
+    bg.outputs = ["loss"]
+    return bg
+
+
+@dataclass
+class TrainGraph(BuiltGraph):
+    """The training graph of lancius_ir_autodiff over a forward BuiltGraph.
+    `nodes`/`inputs` name the training graph's INPUT copies after the forward
+    inputs; `grads[name]` is the gradient node of forward input `name` (absent
+    when the loss does not depend on it); outputs = loss + every gradient."""
+    tg: abi.TrainingGraphP = None
+    fwd: BuiltGraph = None
+    grads: dict = field(default_factory=dict)
+
+    def destroy(self) -> None:
+        if self.tg:
+            self.lib.lancius_training_graph_destroy(self.tg)
+            self.tg = None
+            self.g = None
+        if self.fwd:
+            self.fwd.destroy()
+            self.fwd = None
+
+
+def build_training(lib: C.CDLL, fwd: BuiltGraph, loss: str = "loss") -> TrainGraph:
+    tg = lib.lancius_ir_autodiff(fwd.g, fwd.node(loss))
+    if not tg:
+        raise RuntimeError("lancius_ir_autodiff failed")
+    t = TrainGraph(lib, tg.contents.graph, tg=tg, fwd=fwd)
+    g = tg.contents.graph.contents
+    ins = [g.nodes[i] for i in range(g.node_count) if g.nodes[i].contents.op == abi.OP["INPUT"]]
+    if len(ins) != len(fwd.inputs):
+        raise RuntimeError("training graph inputs do not match the forward graph")
+    for name, n in zip(fwd.inputs, ins):
+        t.nodes[name] = n
+        t.inputs.append(name)
+    t.nodes["loss"] = tg.contents.loss_node
+    t.outputs = ["loss"]
+    for name in fwd.inputs:
+        gn = tg.contents.grad_nodes[fwd.node(name).contents.id]
+        if gn:
+            t.grads[name] = gn
+            t.nodes[f"d{name}"] = gn
+            t.outputs.append(f"d{name}")
+    return t

@@ -76,6 +76,19 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_copy_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_broadcast_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.lancius_hip_fill_f32.argtypes = [vp, vp, f32, sz]
+    for name in ("lancius_hip_sub_f32", "lancius_hip_mul_f32", "lancius_hip_relu_bwd_f32"):
+        getattr(lib, name).argtypes = [vp, vp, vp, vp, sz]
+    lib.lancius_hip_transpose_f32.argtypes = [vp, vp, vp, sz, sz]
+    lib.lancius_hip_sum_f32.argtypes = [vp, vp, vp, sz]
+    lib.lancius_hip_sum_axis0_f32.argtypes = [vp, vp, vp, sz, sz]
+    lib.lancius_hip_sum_axis1_f32.argtypes = [vp, vp, vp, sz, sz]
+    lib.lancius_hip_softmax_bwd_f32.argtypes = [vp, vp, vp, vp, sz, sz]
+    lib.lancius_hip_cross_entropy_f32.argtypes = [vp, vp, vp, vp, sz, sz]
+    lib.lancius_hip_cross_entropy_bwd_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz]
+    lib.lancius_hip_conv2d_bwd_input_f32.argtypes = [vp, vp, vp, vp] + [sz] * 11
+    lib.lancius_hip_conv2d_bwd_weight_f32.argtypes = [vp, vp, vp, vp] + [sz] * 11
+    lib.lancius_hip_maxpool2d_f32.argtypes = [vp, vp, vp] + [sz] * 6
+    lib.lancius_hip_maxpool2d_bwd_f32.argtypes = [vp, vp, vp, vp] + [sz] * 8
     lib.lancius_hip_ctx_create_own_stream.argtypes = [i32, C.POINTER(vp)]
     lib.lancius_hip_ctx_device.argtypes = [vp]
     lib.lancius_hip_ctx_stream.argtypes = [vp]
@@ -274,6 +287,52 @@ class Device:
 
     def fill(self, out, value, n) -> None:
         _check(self.lib.lancius_hip_fill_f32(self.ctx, _vp(out), float(value), n))
+
+    # -- training / reduction ops ----------------------------------------------
+    def sub(self, out, a, b, n) -> None:
+        _check(self.lib.lancius_hip_sub_f32(self.ctx, _vp(out), _vp(a), _vp(b), n))
+
+    def mul(self, out, a, b, n) -> None:
+        _check(self.lib.lancius_hip_mul_f32(self.ctx, _vp(out), _vp(a), _vp(b), n))
+
+    def relu_bwd(self, out, grad, fwd, n) -> None:
+        _check(self.lib.lancius_hip_relu_bwd_f32(self.ctx, _vp(out), _vp(grad), _vp(fwd), n))
+
+    def transpose(self, out, a, rows, cols) -> None:
+        _check(self.lib.lancius_hip_transpose_f32(self.ctx, _vp(out), _vp(a), rows, cols))
+
+    def sum(self, out, a, n) -> None:
+        _check(self.lib.lancius_hip_sum_f32(self.ctx, _vp(out), _vp(a), n))
+
+    def sum_axis0(self, out, a, rows, cols) -> None:
+        _check(self.lib.lancius_hip_sum_axis0_f32(self.ctx, _vp(out), _vp(a), rows, cols))
+
+    def sum_axis1(self, out, a, rows, cols) -> None:
+        _check(self.lib.lancius_hip_sum_axis1_f32(self.ctx, _vp(out), _vp(a), rows, cols))
+
+    def softmax_bwd(self, out, dy, y, rows, cols) -> None:
+        _check(self.lib.lancius_hip_softmax_bwd_f32(self.ctx, _vp(out), _vp(dy), _vp(y), rows, cols))
+
+    def cross_entropy(self, out, x, y, rows, cols) -> None:
+        _check(self.lib.lancius_hip_cross_entropy_f32(self.ctx, _vp(out), _vp(x), _vp(y), rows, cols))
+
+    def cross_entropy_bwd(self, out, x, y, g, rows, cols) -> None:
+        _check(self.lib.lancius_hip_cross_entropy_bwd_f32(self.ctx, _vp(out), _vp(x), _vp(y), _vp(g), rows, cols))
+
+    def conv2d_bwd_input(self, dx, dy, w, N, C_in, H, W, C_out, H_out, W_out, K_h, K_w, stride, pad) -> None:
+        _check(self.lib.lancius_hip_conv2d_bwd_input_f32(self.ctx, _vp(dx), _vp(dy), _vp(w), N, C_in, H, W, C_out,
+                                                         H_out, W_out, K_h, K_w, stride, pad))
+
+    def conv2d_bwd_weight(self, dw, dy, x, N, C_in, H, W, C_out, H_out, W_out, K_h, K_w, stride, pad) -> None:
+        _check(self.lib.lancius_hip_conv2d_bwd_weight_f32(self.ctx, _vp(dw), _vp(dy), _vp(x), N, C_in, H, W, C_out,
+                                                          H_out, W_out, K_h, K_w, stride, pad))
+
+    def maxpool2d(self, out, x, N, C, H, W, K, stride) -> None:
+        _check(self.lib.lancius_hip_maxpool2d_f32(self.ctx, _vp(out), _vp(x), N, C, H, W, K, stride))
+
+    def maxpool2d_bwd(self, dx, dy, x, N, C, H, W, H_out, W_out, K, stride) -> None:
+        _check(self.lib.lancius_hip_maxpool2d_bwd_f32(self.ctx, _vp(dx), _vp(dy), _vp(x), N, C, H, W, H_out, W_out,
+                                                      K, stride))
 
 
 def _vp(x) -> C.c_void_p | None:

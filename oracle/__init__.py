@@ -48,8 +48,25 @@ def lib() -> C.CDLL:
         L.oracle_schedule_execute.restype = C.c_int
         L.oracle_release_buffers.argtypes = [abi.GraphP]
         L.oracle_release_buffers.restype = None
+        for name in ("oracle_sub", "oracle_mul", "oracle_relu_bwd"):
+            getattr(L, name).argtypes = [_D, _D, _D, sz]
+        L.oracle_transpose.argtypes = [_D, _D, sz, sz]
+        L.oracle_sum.argtypes = [_D, _D, sz]
+        L.oracle_sum_axis0.argtypes = [_D, _D, sz, sz]
+        L.oracle_sum_axis1.argtypes = [_D, _D, sz, sz]
+        L.oracle_softmax_bwd.argtypes = [_D, _D, _D, sz, sz]
+        L.oracle_cross_entropy.argtypes = [_D, _D, _D, sz, sz]
+        L.oracle_cross_entropy_bwd.argtypes = [_D, _D, _D, _D, sz, sz]
+        L.oracle_conv2d_bwd_input.argtypes = [_D, _D, _D] + [sz] * 11
+        L.oracle_conv2d_bwd_weight.argtypes = [_D, _D, _D] + [sz] * 11
+        L.oracle_maxpool2d.argtypes = [_D, _D] + [sz] * 6
+        L.oracle_maxpool2d_bwd.argtypes = [_D, _D, _D] + [sz] * 8
         for name in ("oracle_matmul_rows", "oracle_conv2d", "oracle_attention", "oracle_layernorm", "oracle_gelu",
-                     "oracle_softmax", "oracle_argmax", "oracle_add", "oracle_relu", "oracle_broadcast"):
+                     "oracle_softmax", "oracle_argmax", "oracle_add", "oracle_relu", "oracle_broadcast",
+                     "oracle_sub", "oracle_mul", "oracle_relu_bwd", "oracle_transpose", "oracle_sum",
+                     "oracle_sum_axis0", "oracle_sum_axis1", "oracle_softmax_bwd", "oracle_cross_entropy",
+                     "oracle_cross_entropy_bwd", "oracle_conv2d_bwd_input", "oracle_conv2d_bwd_weight",
+                     "oracle_maxpool2d", "oracle_maxpool2d_bwd"):
             getattr(L, name).restype = None
         _lib = L
     return _lib
@@ -74,8 +91,10 @@ def ref_lib() -> C.CDLL | None:
         L.kernel_layernorm.argtypes = [_D, _D, _D, _D, sz, sz, C.c_double]
         L.kernel_gelu.argtypes = [_D, _D, sz]
         L.kernel_attention.argtypes = [_D, _D, _D, _D, sz, sz, sz]
+        L.kernel_conv2d_bwd_in.argtypes = [_D, _D, _D] + [sz] * 11
+        L.kernel_conv2d_bwd_w.argtypes = [_D, _D, _D] + [sz] * 11
         for name in ("kernel_matmul", "kernel_conv2d_fwd", "kernel_conv2d_relu_fwd", "kernel_layernorm",
-                     "kernel_gelu", "kernel_attention"):
+                     "kernel_gelu", "kernel_attention", "kernel_conv2d_bwd_in", "kernel_conv2d_bwd_w"):
             getattr(L, name).restype = None
         _ref = L
     return _ref
@@ -172,6 +191,113 @@ def broadcast(a, rows, cols) -> np.ndarray:
     a = _d(a)
     out = np.empty((rows, cols))
     lib().oracle_broadcast(_p(out), _p(a), a.size, rows, cols)
+    return out
+
+
+def sub(a, b) -> np.ndarray:
+    a, b = _d(a), _d(b)
+    out = np.empty_like(a)
+    lib().oracle_sub(_p(out), _p(a), _p(b), a.size)
+    return out
+
+
+def mul(a, b) -> np.ndarray:
+    a, b = _d(a), _d(b)
+    out = np.empty_like(a)
+    lib().oracle_mul(_p(out), _p(a), _p(b), a.size)
+    return out
+
+
+def relu_bwd(grad, fwd) -> np.ndarray:
+    grad, fwd = _d(grad), _d(fwd)
+    out = np.empty_like(grad)
+    lib().oracle_relu_bwd(_p(out), _p(grad), _p(fwd), grad.size)
+    return out
+
+
+def transpose(a) -> np.ndarray:
+    a = _d(a)
+    out = np.empty((a.shape[1], a.shape[0]))
+    lib().oracle_transpose(_p(out), _p(a), a.shape[0], a.shape[1])
+    return out
+
+
+def sum_all(a) -> float:
+    a = _d(a)
+    out = np.zeros(1)
+    lib().oracle_sum(_p(out), _p(a), a.size)
+    return float(out[0])
+
+
+def sum_axis0(a) -> np.ndarray:
+    a = _d(a)
+    out = np.empty((1, a.shape[1]))
+    lib().oracle_sum_axis0(_p(out), _p(a), a.shape[0], a.shape[1])
+    return out
+
+
+def sum_axis1(a) -> np.ndarray:
+    a = _d(a)
+    out = np.empty((a.shape[0], 1))
+    lib().oracle_sum_axis1(_p(out), _p(a), a.shape[0], a.shape[1])
+    return out
+
+
+def softmax_bwd(dy, y) -> np.ndarray:
+    dy, y = _d(dy), _d(y)
+    out = np.empty_like(dy)
+    lib().oracle_softmax_bwd(_p(out), _p(dy), _p(y), dy.shape[0], dy.shape[1])
+    return out
+
+
+def cross_entropy(x, y) -> float:
+    x, y = _d(x), _d(y)
+    out = np.zeros(1)
+    lib().oracle_cross_entropy(_p(out), _p(x), _p(y), x.shape[0], x.shape[1])
+    return float(out[0])
+
+
+def cross_entropy_bwd(x, y, g: float) -> np.ndarray:
+    x, y = _d(x), _d(y)
+    gg = np.array([g], dtype=np.float64)
+    out = np.empty_like(x)
+    lib().oracle_cross_entropy_bwd(_p(out), _p(x), _p(y), _p(gg), x.shape[0], x.shape[1])
+    return out
+
+
+def conv2d_bwd_input(dy, w, x_shape, stride=1, pad=0) -> np.ndarray:
+    dy, w = _d(dy), _d(w)
+    N, C_in, H, W = x_shape
+    C_out, _, KH, KW = w.shape
+    out = np.empty((N, C_in, H, W))
+    lib().oracle_conv2d_bwd_input(_p(out), _p(dy), _p(w), N, C_in, H, W, C_out, dy.shape[2], dy.shape[3], KH, KW,
+                                  stride, pad)
+    return out
+
+
+def conv2d_bwd_weight(dy, x, w_shape, stride=1, pad=0) -> np.ndarray:
+    dy, x = _d(dy), _d(x)
+    N, C_in, H, W = x.shape
+    C_out, _, KH, KW = w_shape
+    out = np.empty((C_out, C_in, KH, KW))
+    lib().oracle_conv2d_bwd_weight(_p(out), _p(dy), _p(x), N, C_in, H, W, C_out, dy.shape[2], dy.shape[3], KH, KW,
+                                   stride, pad)
+    return out
+
+
+def maxpool2d(x, K, stride) -> np.ndarray:
+    x = _d(x)
+    N, Cc, H, W = x.shape
+    out = np.empty((N, Cc, (H - K) // stride + 1, (W - K) // stride + 1))
+    lib().oracle_maxpool2d(_p(out), _p(x), N, Cc, H, W, K, stride)
+    return out
+
+
+def maxpool2d_bwd(dy, x, K, stride) -> np.ndarray:
+    dy, x = _d(dy), _d(x)
+    N, Cc, H, W = x.shape
+    out = np.empty_like(x)
+    lib().oracle_maxpool2d_bwd(_p(out), _p(dy), _p(x), N, Cc, H, W, dy.shape[2], dy.shape[3], K, stride)
     return out
 
 

@@ -207,6 +207,186 @@ void oracle_broadcast(double* out, const double* a, size_t a_elems, size_t rows,
     }
 }
 
+/* ---- the rest of the scheduler dispatch (training and reduction ops) ---------- */
+
+/* B/src/runtime/lancius_scheduler.c:241-245 */
+void oracle_sub(double* out, const double* a, const double* b, size_t n) {
+    for (size_t k = 0; k < n; k++) out[k] = a[k] - b[k];
+}
+
+/* B/src/runtime/lancius_scheduler.c:236-240 */
+void oracle_mul(double* out, const double* a, const double* b, size_t n) {
+    for (size_t k = 0; k < n; k++) out[k] = a[k] * b[k];
+}
+
+/* B/src/runtime/lancius_scheduler.c:279-283: the forward input decides. */
+void oracle_relu_bwd(double* out, const double* grad, const double* fwd, size_t n) {
+    for (size_t k = 0; k < n; k++) out[k] = fwd[k] > 0.0 ? grad[k] : 0.0;
+}
+
+/* B/src/runtime/lancius_scheduler.c:246-250 */
+void oracle_transpose(double* out, const double* a, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) out[c * rows + r] = a[r * cols + c];
+}
+
+/* B/src/runtime/lancius_scheduler.c:251-256 */
+void oracle_sum(double* out, const double* a, size_t n) {
+    double s = 0.0;
+    for (size_t k = 0; k < n; k++) s += a[k];
+    out[0] = s;
+}
+
+/* B/src/runtime/lancius_scheduler.c:257-262 */
+void oracle_sum_axis0(double* out, const double* a, size_t rows, size_t cols) {
+    for (size_t c = 0; c < cols; c++) out[c] = 0.0;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) out[c] += a[r * cols + c];
+}
+
+/* B/src/runtime/lancius_scheduler.c:263-267 */
+void oracle_sum_axis1(double* out, const double* a, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; r++) {
+        double s = 0.0;
+        for (size_t c = 0; c < cols; c++) s += a[r * cols + c];
+        out[r] = s;
+    }
+}
+
+/* B/src/runtime/lancius_scheduler.c:295-304 */
+void oracle_softmax_bwd(double* out, const double* dy, const double* y, size_t rows, size_t cols) {
+    for (size_t r = 0; r < rows; r++) {
+        double dot = 0.0;
+        for (size_t c = 0; c < cols; c++) dot += dy[r * cols + c] * y[r * cols + c];
+        for (size_t c = 0; c < cols; c++) out[r * cols + c] = y[r * cols + c] * (dy[r * cols + c] - dot);
+    }
+}
+
+/* Row maximum (first element, then strict '>') and sum of exp(x - max), as
+ * B/src/runtime/lancius_scheduler.c:74-77 and :95-98 compute them. */
+static void row_max_sumexp(const double* x, size_t cols, double* mx, double* se) {
+    double m = x[0];
+    for (size_t c = 1; c < cols; c++)
+        if (x[c] > m) m = x[c];
+    double s = 0.0;
+    for (size_t c = 0; c < cols; c++) s += exp(x[c] - m);
+    *mx = m;
+    *se = s;
+}
+
+/* B/src/runtime/lancius_scheduler.c:68-87 (the fabs of :85 included) */
+void oracle_cross_entropy(double* out, const double* x, const double* y, size_t rows, size_t cols) {
+    double total = 0.0;
+    for (size_t r = 0; r < rows; r++) {
+        double m, se;
+        row_max_sumexp(x + r * cols, cols, &m, &se);
+        const double lse = log(se) + m;
+        for (size_t c = 0; c < cols; c++)
+            if (y[r * cols + c] == 1.0) total -= x[r * cols + c] - lse;
+    }
+    out[0] = fabs(total / (double)rows);
+}
+
+/* B/src/runtime/lancius_scheduler.c:89-104 */
+void oracle_cross_entropy_bwd(double* out, const double* x, const double* y, const double* g, size_t rows,
+                              size_t cols) {
+    const double scale = g[0] / (double)rows;
+    for (size_t r = 0; r < rows; r++) {
+        double m, se;
+        row_max_sumexp(x + r * cols, cols, &m, &se);
+        for (size_t c = 0; c < cols; c++)
+            out[r * cols + c] = (exp(x[r * cols + c] - m) / se - y[r * cols + c]) * scale;
+    }
+}
+
+/* B/src/math/lancius_kernels.c:62-91: scatter of every dy value through
+ * the filter taps that produced it. */
+void oracle_conv2d_bwd_input(double* dx, const double* dy, const double* w, size_t N, size_t C_in, size_t H,
+                             size_t W, size_t C_out, size_t Ho, size_t Wo, size_t K_h, size_t K_w, size_t stride,
+                             size_t pad) {
+    memset(dx, 0, N * C_in * H * W * sizeof(double));
+#pragma omp parallel for schedule(static)
+    for (size_t n = 0; n < N; n++)
+        for (size_t co = 0; co < C_out; co++)
+            for (size_t ho = 0; ho < Ho; ho++)
+                for (size_t wo = 0; wo < Wo; wo++) {
+                    const double g = dy[((n * C_out + co) * Ho + ho) * Wo + wo];
+                    for (size_t ci = 0; ci < C_in; ci++)
+                        for (size_t kh = 0; kh < K_h; kh++)
+                            for (size_t kw = 0; kw < K_w; kw++) {
+                                const long ih = (long)(ho * stride) - (long)pad + (long)kh;
+                                const long iw = (long)(wo * stride) - (long)pad + (long)kw;
+                                if (ih < 0 || ih >= (long)H || iw < 0 || iw >= (long)W) continue;
+                                dx[((n * C_in + ci) * H + (size_t)ih) * W + (size_t)iw] +=
+                                    g * w[((co * C_in + ci) * K_h + kh) * K_w + kw];
+                            }
+                }
+}
+
+/* B/src/math/lancius_kernels.c:93-136, one accumulator (the reference's
+ * per-thread partials are summed in thread order; the terms are the same). */
+void oracle_conv2d_bwd_weight(double* dw, const double* dy, const double* x, size_t N, size_t C_in, size_t H,
+                              size_t W, size_t C_out, size_t Ho, size_t Wo, size_t K_h, size_t K_w, size_t stride,
+                              size_t pad) {
+    memset(dw, 0, C_out * C_in * K_h * K_w * sizeof(double));
+#pragma omp parallel for schedule(static)
+    for (size_t co = 0; co < C_out; co++)
+        for (size_t n = 0; n < N; n++)
+            for (size_t ho = 0; ho < Ho; ho++)
+                for (size_t wo = 0; wo < Wo; wo++) {
+                    const double g = dy[((n * C_out + co) * Ho + ho) * Wo + wo];
+                    for (size_t ci = 0; ci < C_in; ci++)
+                        for (size_t kh = 0; kh < K_h; kh++)
+                            for (size_t kw = 0; kw < K_w; kw++) {
+                                const long ih = (long)(ho * stride) - (long)pad + (long)kh;
+                                const long iw = (long)(wo * stride) - (long)pad + (long)kw;
+                                if (ih < 0 || ih >= (long)H || iw < 0 || iw >= (long)W) continue;
+                                dw[((co * C_in + ci) * K_h + kh) * K_w + kw] +=
+                                    g * x[((n * C_in + ci) * H + (size_t)ih) * W + (size_t)iw];
+                            }
+                }
+}
+
+/* B/src/runtime/lancius_vision_ops.c:82-112 */
+void oracle_maxpool2d(double* out, const double* in, size_t N, size_t C, size_t H, size_t W, size_t K,
+                      size_t stride) {
+    const size_t Ho = (H - K) / stride + 1, Wo = (W - K) / stride + 1;
+    for (size_t p = 0; p < N * C; p++)
+        for (size_t ho = 0; ho < Ho; ho++)
+            for (size_t wo = 0; wo < Wo; wo++) {
+                double m = -1e9;
+                for (size_t kh = 0; kh < K; kh++)
+                    for (size_t kw = 0; kw < K; kw++) {
+                        const double v = in[(p * H + ho * stride + kh) * W + wo * stride + kw];
+                        if (v > m) m = v;
+                    }
+                out[(p * Ho + ho) * Wo + wo] = m;
+            }
+}
+
+/* B/src/runtime/lancius_vision_ops.c:149-190: each dy value is added at the
+ * first maximum of its window, (0,0) of the plane when none beats -1e9. */
+void oracle_maxpool2d_bwd(double* dx, const double* dy, const double* x, size_t N, size_t C, size_t H, size_t W,
+                          size_t Ho, size_t Wo, size_t K, size_t stride) {
+    memset(dx, 0, N * C * H * W * sizeof(double));
+    for (size_t p = 0; p < N * C; p++)
+        for (size_t ho = 0; ho < Ho; ho++)
+            for (size_t wo = 0; wo < Wo; wo++) {
+                double m = -1e9;
+                size_t at_h = 0, at_w = 0;
+                for (size_t kh = 0; kh < K; kh++)
+                    for (size_t kw = 0; kw < K; kw++) {
+                        const size_t ih = ho * stride + kh, iw = wo * stride + kw;
+                        if (x[(p * H + ih) * W + iw] > m) {
+                            m = x[(p * H + ih) * W + iw];
+                            at_h = ih;
+                            at_w = iw;
+                        }
+                    }
+                dx[(p * H + at_h) * W + at_w] += dy[(p * Ho + ho) * Wo + wo];
+            }
+}
+
 /* ---- fp64 graph executor ------------------------------------------------------ */
 
 static size_t elems_of(const lancius_node* n) {
@@ -228,7 +408,7 @@ static int ensure_buffer(lancius_node* n) {
 }
 
 /* One node, the branches of B/src/runtime/lancius_scheduler.c:61-309 and
- * B/src/runtime/lancius_vision_ops.c:60-81,113-125 that the device path covers. */
+ * B/src/runtime/lancius_vision_ops.c:60-190 that the device path covers. */
 static int run_node(lancius_node* n) {
     double* y = n->runtime_data;
     const size_t e = elems_of(n);
@@ -279,6 +459,63 @@ static int run_node(lancius_node* n) {
         case LANCIUS_OP_FLATTEN:
             memcpy(y, in[0]->runtime_data, e * sizeof(double));
             return 0;
+        case LANCIUS_OP_SUB:
+            oracle_sub(y, in[0]->runtime_data, in[1]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_MUL:
+            oracle_mul(y, in[0]->runtime_data, in[1]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_RELU_BWD:
+            oracle_relu_bwd(y, in[0]->runtime_data, in[1]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_TRANSPOSE:
+            oracle_transpose(y, in[0]->runtime_data, in[0]->shape[0], in[0]->shape[1]);
+            return 0;
+        case LANCIUS_OP_SUM:
+            oracle_sum(y, in[0]->runtime_data, elems_of(in[0]));
+            return 0;
+        case LANCIUS_OP_SUM_AXIS0:
+            oracle_sum_axis0(y, in[0]->runtime_data, in[0]->shape[0], in[0]->shape[1]);
+            return 0;
+        case LANCIUS_OP_SUM_AXIS1:
+            oracle_sum_axis1(y, in[0]->runtime_data, in[0]->shape[0], in[0]->shape[1]);
+            return 0;
+        case LANCIUS_OP_SOFTMAX_BWD:
+            oracle_softmax_bwd(y, in[0]->runtime_data, in[1]->runtime_data, n->shape[0], n->shape[1]);
+            return 0;
+        case LANCIUS_OP_CROSS_ENTROPY:
+            oracle_cross_entropy(y, in[0]->runtime_data, in[1]->runtime_data, in[0]->shape[0], in[0]->shape[1]);
+            return 0;
+        case LANCIUS_OP_CROSS_ENTROPY_BWD:
+            oracle_cross_entropy_bwd(y, in[0]->runtime_data, in[1]->runtime_data, in[2]->runtime_data, n->shape[0],
+                                     n->shape[1]);
+            return 0;
+        case LANCIUS_OP_CONV2D_BWD: { /* inputs: grad, fwd_in, fwd_w (vision_ops.c:126-137) */
+            const lancius_node *g = in[0], *x = in[1], *w = in[2];
+            oracle_conv2d_bwd_input(y, g->runtime_data, w->runtime_data, x->shape[0], x->shape[1], x->shape[2],
+                                    x->shape[3], w->shape[0], g->shape[2], g->shape[3], w->shape[2], w->shape[3],
+                                    n->stride, n->pad);
+            return 0;
+        }
+        case LANCIUS_OP_CONV2D_BWD_W: { /* inputs: grad, fwd_in (vision_ops.c:138-148) */
+            const lancius_node *g = in[0], *x = in[1];
+            oracle_conv2d_bwd_weight(y, g->runtime_data, x->runtime_data, x->shape[0], x->shape[1], x->shape[2],
+                                     x->shape[3], n->shape[0], g->shape[2], g->shape[3], n->shape[2], n->shape[3],
+                                     n->stride, n->pad);
+            return 0;
+        }
+        case LANCIUS_OP_MAXPOOL2D: {
+            const lancius_node* x = in[0];
+            oracle_maxpool2d(y, x->runtime_data, x->shape[0], x->shape[1], x->shape[2], x->shape[3], n->kernel_h,
+                             n->stride);
+            return 0;
+        }
+        case LANCIUS_OP_MAXPOOL2D_BWD: {
+            const lancius_node *g = in[0], *x = in[1];
+            oracle_maxpool2d_bwd(y, g->runtime_data, x->runtime_data, x->shape[0], x->shape[1], x->shape[2],
+                                 x->shape[3], g->shape[2], g->shape[3], n->kernel_h, n->stride);
+            return 0;
+        }
         default:
             return -4;
     }

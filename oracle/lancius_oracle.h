@@ -20,8 +20,20 @@
  *   oracle_layernorm/gelu/softmax/argmax/add/relu/broadcast
  *                         golden vectors + closed forms (constant row => beta,
  *                         GELU(0) = 0 and the +-100 clamp, uniform softmax)
+ *   oracle_sub/mul/relu_bwd/transpose/sum/sum_axis0/sum_axis1/softmax_bwd/
+ *   cross_entropy/cross_entropy_bwd/maxpool2d/maxpool2d_bwd
+ *                         golden vectors of the compiled reference scheduler
+ *                         and vision router; closed forms (transpose twice =
+ *                         identity, sums against numpy, softmax_bwd against
+ *                         the Jacobian product, CE against numpy logsumexp,
+ *                         CE gradient against finite differences)
+ *   oracle_conv2d_bwd_input/_weight
+ *                         golden vectors of kernel_conv2d_bwd_in/_w; adjoint
+ *                         identities <conv(x,w), g> = <x, bwd_in(g,w)> =
+ *                         <w, bwd_w(g,x)>; finite differences
  *   oracle_schedule_execute
- *                         golden sink values of reference graph runs
+ *                         golden sink values of reference graph runs,
+ *                         including autodiff training graphs
  */
 #ifndef LANCIUS_ORACLE_H
 #define LANCIUS_ORACLE_H
@@ -58,6 +70,30 @@ void oracle_argmax(int32_t* idx, const double* in, size_t rows, size_t cols);
 void oracle_add(double* out, const double* a, const double* b, size_t n);
 void oracle_relu(double* out, const double* a, size_t n);
 void oracle_broadcast(double* out, const double* a, size_t a_elems, size_t rows, size_t cols);
+
+/* The rest of the scheduler dispatch (B/src/runtime/lancius_scheduler.c:68-104,
+ * 236-304; B/src/math/lancius_kernels.c:62-136; B/src/runtime/lancius_vision_ops.c:82-190). */
+void oracle_sub(double* out, const double* a, const double* b, size_t n);
+void oracle_mul(double* out, const double* a, const double* b, size_t n);
+void oracle_relu_bwd(double* out, const double* grad, const double* fwd, size_t n);
+void oracle_transpose(double* out, const double* a, size_t rows, size_t cols);
+void oracle_sum(double* out, const double* a, size_t n);
+void oracle_sum_axis0(double* out, const double* a, size_t rows, size_t cols);
+void oracle_sum_axis1(double* out, const double* a, size_t rows, size_t cols);
+void oracle_softmax_bwd(double* out, const double* dy, const double* y, size_t rows, size_t cols);
+void oracle_cross_entropy(double* out, const double* x, const double* y, size_t rows, size_t cols);
+void oracle_cross_entropy_bwd(double* out, const double* x, const double* y, const double* g, size_t rows,
+                              size_t cols);
+void oracle_conv2d_bwd_input(double* dx, const double* dy, const double* w, size_t N, size_t C_in, size_t H,
+                             size_t W, size_t C_out, size_t Ho, size_t Wo, size_t K_h, size_t K_w, size_t stride,
+                             size_t pad);
+void oracle_conv2d_bwd_weight(double* dw, const double* dy, const double* x, size_t N, size_t C_in, size_t H,
+                              size_t W, size_t C_out, size_t Ho, size_t Wo, size_t K_h, size_t K_w, size_t stride,
+                              size_t pad);
+void oracle_maxpool2d(double* out, const double* in, size_t N, size_t C, size_t H, size_t W, size_t K,
+                      size_t stride);
+void oracle_maxpool2d_bwd(double* dx, const double* dy, const double* x, size_t N, size_t C, size_t H, size_t W,
+                          size_t Ho, size_t Wo, size_t K, size_t stride);
 
 /* fp64 CPU execution of a scheduled graph, node by node in wave order, the
  * way the reference's scratch-arena executor does it

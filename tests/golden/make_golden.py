@@ -7,12 +7,22 @@ C code, compiled from /root/reference into oracle/_ref/liblancius_ref.so
 Outputs (data only - inputs and the reference's outputs):
   kernels.npz        kernel_matmul / graph MATMUL, kernel_conv2d_fwd,
                      kernel_conv2d_relu_fwd, kernel_attention,
-                     kernel_layernorm, kernel_gelu, graph SOFTMAX
+                     kernel_layernorm, kernel_gelu, graph SOFTMAX; graph
+                     SUB, MUL, RELU_BWD, TRANSPOSE, SUM, SUM_AXIS0/1,
+                     SOFTMAX_BWD, CROSS_ENTROPY(_BWD), MAXPOOL2D(_BWD) and
+                     kernel_conv2d_bwd_in/_w
   graphs.json        lancius_ir_schedule waves and lancius_build_memory_plan
                      offsets/peaks of the config graphs (fp32 dtypes, as the
                      device plans them) and of the 20 x ReLU chain (fp64)
   graph_outputs.npz  sink values of reference CPU graph runs (scratch-arena
                      executor, B/src/runtime/lancius_scheduler.c:311-362)
+  train_outputs.npz  loss and every input gradient of the reference's
+                     autodiff training graphs (B/src/math/lancius_autodiff.c)
+                     run by the same executor, for the inputs train_feeds()
+                     regenerates from the seeds in TRAIN_SEEDS (the fused
+                     CNN graph is checked to give the unfused graph's values
+                     and is not stored twice); their structure and fp32 plans
+                     go to graphs.json as train_<name>
 Inputs come from lancius_amd.prng with the seeds written next to them.
 """
 from __future__ import annotations
@@ -145,6 +155,7 @@ def main() -> None:
     bg.outputs = ["sm"]
     k["softmax_out"] = run_ref_graph(ref, bg, {"a": k["softmax_x"]})["sm"]
     bg.destroy()
+    training_op_vectors(ref, k)
     np.savez_compressed(OUT / "kernels.npz", **k)
 
     # schedules and plans
@@ -194,7 +205,141 @@ def main() -> None:
     go.update({f"block_out_{n}": v for n, v in res.items()})
     bg.destroy()
     np.savez_compressed(OUT / "graph_outputs.npz", **go)
+
+    # training graphs: structure and plan of the reference's autodiff graphs,
+    # and loss + gradients of reference CPU runs
+    tr = {}
+    trec = {}
+    for name, fwd in TRAIN_GRAPHS.items():
+        t = graphs.build_training(ref, fwd(ref))
+        trec[name] = plan_record(ref, t, abi.DTYPE_FP32)
+        trec[name]["node_inputs"] = [
+            [t.g.contents.nodes[i].contents.inputs[j].contents.id for j in range(t.g.contents.nodes[i].contents.input_count)]
+            for i in range(t.g.contents.node_count)]
+        trec[name]["node_shapes"] = [list(abi.node_shape(t.g.contents.nodes[i])) for i in range(t.g.contents.node_count)]
+        trec[name]["outputs"] = list(t.outputs)
+        feeds = train_feeds(t, TRAIN_SEEDS[name])
+        res = run_ref_graph(ref, t, feeds)
+        if name == "cnn_fused":
+            # the fused graph computes the same values as the unfused one (up
+            # to the order in which the reference's OpenMP threads add their
+            # kernel_conv2d_bwd_w partials, lancius_kernels.c:128-131)
+            for n, v in res.items():
+                np.testing.assert_allclose(v, tr[f"cnn_out_{n}"], rtol=1e-9, atol=1e-12)
+        else:
+            tr.update({f"{name}_out_{n}": v for n, v in res.items()})
+        t.destroy()
+    recs.update({f"train_{k}": v for k, v in trec.items()})
+    (OUT / "graphs.json").write_text(json.dumps(recs, indent=0, sort_keys=True))
+    np.savez_compressed(OUT / "train_outputs.npz", **tr)
     print("fixtures written to", OUT)
+
+
+def ref_op(ref, shapes: dict[str, tuple], build, feeds: dict[str, np.ndarray]) -> np.ndarray:
+    """Output of one reference graph node `build(graph, inputs)` over INPUTs of
+    the given shapes, run by the reference's scratch-arena executor."""
+    bg = graphs.BuiltGraph(ref, ref.lancius_graph_create())
+    ins = {name: graphs._inp(bg, name, *shape) for name, shape in shapes.items()}
+    bg.nodes["out"] = build(bg.g, ins)
+    bg.outputs = ["out"]
+    out = run_ref_graph(ref, bg, feeds)["out"]
+    bg.destroy()
+    return out
+
+
+def training_op_vectors(ref, k: dict) -> None:
+    """Golden vectors of the training/reduction dispatch branches
+    (lancius_scheduler.c:68-104,236-304; lancius_vision_ops.c:82-190) and of
+    kernel_conv2d_bwd_in/_w (lancius_kernels.c:62-136)."""
+    R, Cc = 6, 9
+    a, b = f32(prng.normal(20, (R, Cc))), f32(prng.normal(21, (R, Cc)))
+    a[0, :3] = [0.0, -0.0, 1e-30]  # RELU_BWD decides on fwd > 0
+    k["ew_a"], k["ew_b"] = a, b
+    two = {"a": (R, Cc), "b": (R, Cc)}
+    feeds = {"a": a, "b": b}
+    k["sub_out"] = ref_op(ref, two, lambda g, i: ref.lancius_sub(g, i["a"], i["b"]), feeds)
+    k["mul_out"] = ref_op(ref, two, lambda g, i: ref.lancius_mul(g, i["a"], i["b"]), feeds)
+    k["relu_bwd_out"] = ref_op(ref, two, lambda g, i: ref.lancius_relu_bwd(g, i["b"], i["a"]), feeds)
+    one = {"a": (R, Cc)}
+    k["transpose_out"] = ref_op(ref, one, lambda g, i: ref.lancius_transpose(g, i["a"]), {"a": a})
+    k["sum_out"] = ref_op(ref, one, lambda g, i: ref.lancius_sum(g, i["a"]), {"a": a})
+    k["sum_axis0_out"] = ref_op(ref, one, lambda g, i: ref.lancius_sum_axis0(g, i["a"]), {"a": a})
+    k["sum_axis1_out"] = ref_op(ref, one, lambda g, i: ref.lancius_sum_axis1(g, i["a"]), {"a": a})
+    y = np.exp(a - a.max(1, keepdims=True))
+    y = f32(y / y.sum(1, keepdims=True))
+    k["softmax_bwd_y"] = y
+    k["softmax_bwd_out"] = ref_op(ref, two, lambda g, i: ref.lancius_softmax_bwd(g, i["b"], i["a"]),
+                                  {"a": y, "b": b})
+    # cross-entropy: one-hot targets, plus a row with no 1.0 and a row with two
+    t = np.zeros((R, Cc))
+    t[np.arange(R), [3, 0, 8, 5, 5, 1]] = 1.0
+    t[4] = 0.0
+    t[5, 7] = 1.0
+    x = f32(prng.normal(22, (R, Cc), std=3.0))
+    k["ce_x"], k["ce_y"] = x, t
+    k["ce_out"] = ref_op(ref, two, lambda g, i: ref.lancius_cross_entropy(g, i["a"], i["b"]), {"a": x, "b": t})
+    k["ce_g"] = np.array([[0.75]])
+    k["ce_bwd_out"] = ref_op(ref, {"a": (R, Cc), "b": (R, Cc), "g": (1, 1)},
+                             lambda g, i: ref.lancius_cross_entropy_bwd(g, i["a"], i["b"], i["g"]),
+                             {"a": x, "b": t, "g": k["ce_g"]})
+    # conv backward, kernel level: stride 1 pad 1 and stride 2 pad 2
+    for tag, (N, Ci, H, W, Co, KH, KW, st, pd), seed in (("s1p1", (2, 3, 7, 6, 4, 3, 3, 1, 1), 23),
+                                                        ("s2p2", (1, 2, 9, 8, 3, 5, 5, 2, 2), 24)):
+        Ho, Wo = (H + 2 * pd - KH) // st + 1, (W + 2 * pd - KW) // st + 1
+        xx, ww = f32(prng.normal(seed, (N, Ci, H, W))), f32(prng.normal(seed + 50, (Co, Ci, KH, KW)))
+        gg = f32(prng.normal(seed + 100, (N, Co, Ho, Wo)))
+        dx, dw = np.zeros((N, Ci, H, W)), np.zeros((Co, Ci, KH, KW))
+        ref.kernel_conv2d_bwd_in(p(dx), p(gg), p(ww), N, Ci, H, W, Co, Ho, Wo, KH, KW, st, pd)
+        ref.kernel_conv2d_bwd_w(p(dw), p(gg), p(xx), N, Ci, H, W, Co, Ho, Wo, KH, KW, st, pd)
+        k[f"cbwd_{tag}_x"], k[f"cbwd_{tag}_w"], k[f"cbwd_{tag}_g"] = xx, ww, gg
+        k[f"cbwd_{tag}_dx"], k[f"cbwd_{tag}_dw"] = dx, dw
+    # max pooling: overlapping 3/2 windows with ties, and 2/2 windows, one of
+    # which holds nothing above -1e9 (its gradient goes to plane (0,0))
+    xp = f32(np.round(prng.normal(25, (2, 3, 9, 7)) * 2.0) / 2.0)  # many ties
+    xp[1, 2, 2:4, 2:4] = -2e9
+    k["pool_x"] = xp
+    for tag, (K, st) in (("k3s2", (3, 2)), ("k2s2", (2, 2))):
+        Ho, Wo = (9 - K) // st + 1, (7 - K) // st + 1
+        k[f"pool_{tag}_out"] = ref_op(ref, {"x": (2, 3, 9, 7)}, lambda g, i: ref.lancius_maxpool2d(g, i["x"], K, st),
+                                      {"x": xp})
+        gp = f32(prng.normal(26, (2, 3, Ho, Wo)))
+        k[f"pool_{tag}_g"] = gp
+        k[f"pool_{tag}_dx"] = ref_op(ref, {"g": (2, 3, Ho, Wo), "x": (2, 3, 9, 7)},
+                                     lambda g, i: ref.lancius_maxpool2d_bwd(g, i["g"], i["x"], K, st),
+                                     {"g": gp, "x": xp})
+
+
+TRAIN_GRAPHS = {
+    "mlp": lambda lib: graphs.build_mlp_ce(lib, batch=64, d_in=784, hidden=128, classes=10),
+    "cnn": lambda lib: graphs.build_cnn_ce(lib, batch=4),
+    "cnn_fused": lambda lib: graphs.build_cnn_ce(lib, batch=4, fuse=True),
+    "gradcheck": graphs.build_gradcheck,
+    "ops": graphs.build_ops_loss,
+}
+TRAIN_SEEDS = {"mlp": 5000, "cnn": 6000, "cnn_fused": 6000, "gradcheck": 7000, "ops": 8000}
+
+
+def train_feeds(t, seed: int) -> dict[str, np.ndarray]:
+    """Seeded inputs of a training graph: one-hot targets Y, He-scaled 4-D
+    weights, N(0, 0.05) matrices, N(0,1) data."""
+    feeds = {}
+    for i, name in enumerate(t.inputs):
+        shape = abi.node_shape(t.node(name))
+        s = seed + 17 * i
+        if name == "Y":
+            rows, classes = shape
+            lab = (prng.uniform(s, (rows,), 0.0, 1.0) * classes).astype(np.int64) % classes
+            y = np.zeros(shape)
+            y[np.arange(rows), lab] = 1.0
+            feeds[name] = y
+        elif name.startswith("W") and len(shape) == 4:
+            fan_in = shape[1] * shape[2] * shape[3]
+            feeds[name] = f32(prng.normal(s, shape, 0.0, float(np.sqrt(2.0 / fan_in))))
+        elif name.startswith(("W", "b")):
+            feeds[name] = f32(prng.normal(s, shape, 0.0, 0.05))
+        else:
+            feeds[name] = f32(prng.normal(s, shape))
+    return feeds
 
 
 if __name__ == "__main__":

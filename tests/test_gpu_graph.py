@@ -212,7 +212,7 @@ def test_unsupported_op_fails_loudly(dev):
     g = lib.lancius_graph_create()
     x = lib.lancius_input(g, 4, 4)
     n = lib.lancius_relu(g, x)
-    n.contents.op = abi.OP["TRANSPOSE"]
+    n.contents.op = abi.OP["EMBEDDING"]  # no executor branch in the reference either
     sched = lib.lancius_ir_schedule(g)
     case("unsupported op")
     with pytest.raises(HipError) as e:

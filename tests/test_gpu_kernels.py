@@ -1,7 +1,7 @@
 """Parity of every HIP kernel, called through the C ABI, against the fp64 CPU
 oracle on identical seeded fp32 inputs.
 
-Bar (BASELINE.md section 5): normwise error max|y - y_ref| / max|y_ref| <=
+Bar: normwise error max|y - y_ref| / max|y_ref| <=
 1e-4 * max(1, sqrt(K)/32), K the longest reduction; argmax/indices bit-exact.
 """
 import numpy as np

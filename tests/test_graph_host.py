@@ -17,6 +17,13 @@ BUILDERS = {
     "block": (lambda lib: graphs.build_block(lib), abi.DTYPE_FP32),
     "block_small": (lambda lib: graphs.build_block(lib, batch=2, S=32, d=64, H=4, F=256), abi.DTYPE_FP32),
     "relu_chain": (lambda lib: graphs.build_relu_chain(lib), abi.DTYPE_FP64),
+    # autodiff training graphs (liblancius_graph's lancius_ir_autodiff)
+    "train_mlp": (lambda lib: graphs.build_training(lib, graphs.build_mlp_ce(lib)), abi.DTYPE_FP32),
+    "train_cnn": (lambda lib: graphs.build_training(lib, graphs.build_cnn_ce(lib, batch=4)), abi.DTYPE_FP32),
+    "train_cnn_fused": (lambda lib: graphs.build_training(lib, graphs.build_cnn_ce(lib, batch=4, fuse=True)),
+                        abi.DTYPE_FP32),
+    "train_gradcheck": (lambda lib: graphs.build_training(lib, graphs.build_gradcheck(lib)), abi.DTYPE_FP32),
+    "train_ops": (lambda lib: graphs.build_training(lib, graphs.build_ops_loss(lib)), abi.DTYPE_FP32),
 }
 
 
@@ -52,6 +59,12 @@ def test_node_ops_match_reference(built):
     name, lib, bg, sched, plan = built
     ops = [bg.g.contents.nodes[i].contents.op for i in range(bg.g.contents.node_count)]
     assert ops == GOLD[name]["node_ops"]
+    if "node_inputs" in GOLD[name]:  # training graphs: wiring and shapes too
+        g = bg.g.contents
+        assert [[g.nodes[i].contents.inputs[j].contents.id for j in range(g.nodes[i].contents.input_count)]
+                for i in range(g.node_count)] == GOLD[name]["node_inputs"]
+        assert [list(abi.node_shape(g.nodes[i])) for i in range(g.node_count)] == GOLD[name]["node_shapes"]
+        assert bg.outputs == GOLD[name]["outputs"]
 
 
 def test_model_reproduces_reference_plan(built):
