@@ -13,9 +13,11 @@ The same JSON line carries:
                 a bounded row sample of the same product
   all_configs   every other BASELINE.json config measured in this run:
                 GEMM 1024^3 / 2048^3 / 16x4096x4096, attention B8 H16 D64
-                S512/S2048 causal/non-causal, conv 3x3 N32 64->128 56^2 +ReLU,
-                and the MLP and transformer-block graphs through the device
-                executor (forward latency).
+                S512/S2048 causal/non-causal, conv 3x3 N32 64->128 56^2 +ReLU
+                and its two backward convolutions, the MLP and transformer-block
+                graphs through the device executor (forward latency), and the
+                training steps (autodiff graphs) of the MNIST MLP and CIFAR CNN
+                examples.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
@@ -42,6 +44,12 @@ PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
 METRIC = "GFLOP/s + % of fp32 MFMA peak (GEMM/attn/conv); graph fwd latency ms"
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+# Algorithmic flops of one training step (forward + every gradient):
+# MNIST MLP B64: 3 GEMMs per layer (fwd, dX, dW) of 64x784x128 and 64x128x10
+MLP_TRAIN_GFLOP = 3 * 2.0 * (64 * 784 * 128 + 64 * 128 * 10) / 1e9
+# CIFAR CNN B32: 3 convolutions per conv layer (fwd, dgrad, wgrad) + 3 GEMMs per FC layer
+CNN_TRAIN_GFLOP = 3 * 2.0 * (32 * 16 * 32 * 32 * 3 * 25 + 32 * 32 * 16 * 16 * 16 * 25
+                             + 32 * 2048 * 120 + 32 * 120 * 10) / 1e9
 
 
 def log(msg: str) -> None:
@@ -96,6 +104,69 @@ def conv_case(dev, steps, warmup):
         b.free()
     flops = 2.0 * N * C_out * H * W * C_in * 9
     return ms, flops, 4.0 * (N * C_in * H * W + C_out * C_in * 9 + N * C_out * H * W)
+
+
+def conv_bwd_cases(dev, steps, warmup) -> dict:
+    """Input and weight gradients of the conv config (the two backward
+    convolutions of a training step); same 2*N*C_out*H*W*C_in*9 flops each."""
+    N, C_in, H, W, C_out = 32, 64, 56, 56, 128
+    x = dev.upload(prng.normal(50, (N, C_in, H, W)))
+    w = dev.upload(prng.normal(150, (C_out, C_in, 3, 3), std=float(np.sqrt(2.0 / (9 * C_in)))))
+    g = dev.upload(prng.normal(250, (N, C_out, H, W)))
+    dx, dw = dev.alloc(N * C_in * H * W * 4), dev.alloc(C_out * C_in * 9 * 4)
+    flops = 2.0 * N * C_out * H * W * C_in * 9
+    out = {}
+    t = time_steps(dev, lambda: dev.conv2d_bwd_input(dx, g, w, N, C_in, H, W, C_out, H, W, 3, 3, 1, 1), steps, warmup)
+    out["conv3x3_N32_64to128_56x56_bwd_input"] = {"ms": round(t, 4), "GFLOP/s": round(flops / t / 1e6, 1),
+                                                  "frac_fp32_mfma": round(flops / t / 1e9 / PEAK_FP32_MFMA, 4)}
+    t = time_steps(dev, lambda: dev.conv2d_bwd_weight(dw, g, x, N, C_in, H, W, C_out, H, W, 3, 3, 1, 1), steps,
+                   warmup)
+    out["conv3x3_N32_64to128_56x56_bwd_weight"] = {"ms": round(t, 4), "GFLOP/s": round(flops / t / 1e6, 1),
+                                                   "frac_fp32_mfma": round(flops / t / 1e9 / PEAK_FP32_MFMA, 4)}
+    for b in (x, w, g, dx, dw):
+        b.free()
+    return out
+
+
+def train_feeds(t, seed: int) -> dict:
+    """Synthetic training-step inputs: one-hot Y, He-scaled conv weights,
+    N(0, 0.05) matrices and biases, N(0, 1) data."""
+    feeds = {}
+    for i, name in enumerate(t.inputs):
+        shape = abi.node_shape(t.node(name))
+        if name == "Y":
+            lab = (prng.uniform(seed + i, (shape[0],), 0.0, 1.0) * shape[1]).astype(np.int64) % shape[1]
+            y = np.zeros(shape, np.float32)
+            y[np.arange(shape[0]), lab] = 1.0
+            feeds[name] = y
+        elif name.startswith("W") and len(shape) == 4:
+            feeds[name] = prng.normal(seed + i, shape, 0.0, float(np.sqrt(2.0 / np.prod(shape[1:]))))
+        elif name.startswith(("W", "b")):
+            feeds[name] = prng.normal(seed + i, shape, 0.0, 0.05)
+        else:
+            feeds[name] = prng.normal(seed + i, shape)
+    return feeds
+
+
+def train_case(dev, fwd_builder, steps, warmup, flags=0):
+    """One training step = the whole autodiff graph (forward, loss, every
+    gradient) through the device executor."""
+    lib = graph_lib()
+    t = graphs.build_training(lib, fwd_builder(lib))
+    lib.lancius_graph_set_dtype(t.g, abi.DTYPE_FP32)
+    sched = lib.lancius_ir_schedule(t.g)
+    plan = lib.lancius_build_memory_plan(sched, t.g)
+    prog = DeviceProgram(dev, t.g, sched, plan, flags)
+    feeds = train_feeds(t, 77)
+    for name in t.inputs:
+        prog.upload(t.node(name), feeds[name])
+    ms = time_steps(dev, prog.run, steps, warmup)
+    info = prog.info()
+    prog.close()
+    lib.lancius_memory_plan_destroy(plan)
+    lib.lancius_schedule_destroy(sched)
+    t.destroy()
+    return ms, info
 
 
 def rowop_cases(dev, steps, warmup) -> dict:
@@ -214,10 +285,45 @@ def cpu_baseline(M, K, N, target_s: float = 12.0) -> dict | None:
                 break
     except OSError:
         pass
-    return {"value": round(gflops, 3), "unit": "GFLOP/s", "cores": 1, "kind": kind,
+    other = {}
+    if ref is not None:
+        for name, builder in (("train_step_mnist_mlp_B64_784x128x10", lambda l: graphs.build_mlp_ce(l)),
+                              ("train_step_cifar_cnn_B32", lambda l: graphs.build_cnn_ce(l, batch=32))):
+            other[name] = {"step_latency_ms": round(cpu_train_step_ms(ref, builder), 3),
+                           "note": "reference scratch-arena executor (lancius_schedule_execute), its own "
+                                   "OpenMP threading, median of 3"}
+    return {"value": round(gflops, 3), "unit": "GFLOP/s", "cores": 1, "kind": kind, "other_configs": other,
             "sample": f"rows 0-{rows - 1} of the {M}x{K}x{N} fp64 product through the "
                       f"{'reference' if kind == 'reference' else 'oracle'} graph MATMUL node (IKJ, 1 thread), "
                       f"{dt:.1f} s on {cpu} ({os.cpu_count()} logical CPUs visible)"}
+
+
+def cpu_train_step_ms(ref, builder) -> float:
+    """One training step of the reference's own autodiff graph on its CPU
+    executor (graph, autodiff and executor all the reference's C)."""
+    t = graphs.build_training(ref, builder(ref))
+    feeds = {k: np.ascontiguousarray(v, dtype=np.float64) for k, v in train_feeds(t, 77).items()}
+    for name in t.inputs:
+        t.node(name).contents.runtime_data = feeds[name].ctypes.data_as(C.POINTER(C.c_double))
+    sched = ref.lancius_ir_schedule(t.g)
+    arena = ref.lancius_arena_create(512 << 20)
+    times = []
+    for _ in range(3):
+        g = t.g.contents
+        for i in range(g.node_count):  # fresh intermediates each step, as train_mnist.c:160-166 does
+            n = g.nodes[i]
+            if n.contents.op not in (abi.OP["INPUT"], abi.OP["CONST"]):
+                n.contents.runtime_data = None
+        t0 = time.perf_counter()
+        ref.lancius_schedule_execute(sched, arena)
+        times.append(time.perf_counter() - t0)
+        ref.lancius_arena_reset(arena)
+    ref.lancius_arena_destroy(arena)
+    ref.lancius_schedule_destroy(sched)
+    for name in t.inputs:
+        t.node(name).contents.runtime_data = None
+    t.destroy()
+    return sorted(times)[1] * 1e3
 
 
 def main() -> int:
@@ -292,6 +398,8 @@ def main() -> int:
         t, f, b = conv_case(dev, steps, 3)
         extra["conv3x3_N32_64to128_56x56_relu"] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
                                                    "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
+        log("conv backward")
+        extra.update(conv_bwd_cases(dev, steps, 3))
         log("row and elementwise kernels")
         extra.update(rowop_cases(dev, max(20, steps), 5))
         log("host-pointer bridge")
@@ -326,6 +434,15 @@ def main() -> int:
         extra["transformer_block_B4_S1024_d1024_H16_F4096"] = {
             "fwd_latency_ms": round(t, 3), "fwd_latency_ms_hipgraph": round(tg, 3), "launches": info["launches"],
             "GFLOP/s": round(111.7e9 / t / 1e6, 1), "arena_MiB": round(info["arena_bytes"] / 2 ** 20, 1)}
+        for name, builder, gflop in (
+                ("train_step_mnist_mlp_B64_784x128x10", lambda l: graphs.build_mlp_ce(l), MLP_TRAIN_GFLOP),
+                ("train_step_cifar_cnn_B32", lambda l: graphs.build_cnn_ce(l, batch=32), CNN_TRAIN_GFLOP)):
+            log(name)
+            t, info = train_case(dev, builder, max(20, steps), 5)
+            tg, _ = train_case(sdev, builder, max(20, steps), 5, DEVICE_GRAPH)
+            extra[name] = {"step_latency_ms": round(t, 4), "step_latency_ms_hipgraph": round(tg, 4),
+                           "launches": info["launches"], "GFLOP/s": round(gflop / t * 1e3, 1),
+                           "arena_MiB": round(info["arena_bytes"] / 2 ** 20, 2)}
         result["all_configs"] = extra
         sdev.close()
     dev.close()

@@ -90,6 +90,20 @@ LANCIUS_HIP_EXPORT int lancius_hip_gemm_grouped_f32(lancius_hip_ctx* ctx, size_t
                                                     size_t M, size_t K, size_t N,
                                                     const float* const* bias, int act, const float* const* residual);
 
+/* The same with transposed operands: trans_a != 0 reads A as stored
+ * [K][M] (element (m,k) at A[k*M + m]); trans_b != 0 reads B as stored
+ * [N][K] (element (k,n) at B[n*K + k]).  A TRANSPOSE node feeding a
+ * MATMUL (the autodiff products dX = dY . W^T and dW = X^T . dY,
+ * lancius_autodiff.c:149-153) runs as one of these, with no transposed copy. */
+LANCIUS_HIP_EXPORT int lancius_hip_gemm_ex_f32(lancius_hip_ctx* ctx, float* C, const float* A, const float* B,
+                                               size_t M, size_t K, size_t N, int trans_a, int trans_b,
+                                               const float* bias, int act, const float* residual);
+LANCIUS_HIP_EXPORT int lancius_hip_gemm_grouped_ex_f32(lancius_hip_ctx* ctx, size_t count,
+                                                       float* const* C, const float* const* A,
+                                                       const float* const* B, size_t M, size_t K, size_t N,
+                                                       int trans_a, int trans_b, const float* const* bias, int act,
+                                                       const float* const* residual);
+
 /* out[N,C_out,H_out,W_out] = act(conv(in[N,C_in,H,W], w[C_out,C_in,K_h,K_w]) + bias[C_out]).
  * Cross-correlation with zero padding, H_out = (H + 2 pad - K_h)/stride + 1
  * (lancius_kernels.c:28-60, ReLU variant :140-173).  bias may be NULL;

@@ -449,14 +449,19 @@ __global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
     }
 }
 
+// One wave per weight: lane l adds splits l, l+64, ... in order, then a fixed
+// butterfly over the lanes (deterministic, and the split partials of one
+// weight are read by 64 lanes at once instead of one thread).
 __global__ void __launch_bounds__(256) wgrad_reduce(float* __restrict__ dw, const float* __restrict__ ws, size_t n,
                                                     int splits) {
-    const size_t step = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
-        float s = ws[i];
-        for (int k = 1; k < splits; ++k) s += ws[(size_t)k * n + i];
-        dw[i] = s;
-    }
+    const size_t i = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (i >= n) return;
+    float s = 0.0f;
+    for (int k = lane; k < splits; k += 64) s += ws[(size_t)k * n + i];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) dw[i] = s;
 }
 
 template <int BM, int BN, int KH_T, int KW_T>
@@ -655,8 +660,9 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     if (int rc = check_launch("conv2d_wgrad_mfma")) return rc;
     if (p.splits > 1) {
         const size_t n = C_out * J;
-        hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)std::min<size_t>((n + 255) / 256, 4096)), dim3(256), 0,
-                           ctx->stream, dw, (const float*)p.ws, n, p.splits);
+        LANCIUS_REQUIRE((n + 3) / 4 < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: %zu weights", n);
+        hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, ctx->stream, dw,
+                           (const float*)p.ws, n, p.splits);
         if (int rc = check_launch("conv2d_wgrad_reduce")) return rc;
     }
     return ok();

@@ -45,7 +45,12 @@ constexpr int kThreads = 256;
 // raw partial sums; splitk_reduce adds the partials in order y = 0, 1, ...
 // (a fixed order, so results are run-to-run identical) and applies the
 // epilogue.
-template <int BM, int BN, int BK, int WGM, int WGN, bool VEC, bool SPLIT, int OCC = 1>
+// TA: A is given transposed, stored [K][M] (element (m,k) at A[k*M + m]);
+// TB: B is given transposed, stored [N][K] (element (k,n) at B[n*K + k]).
+// The LDS tiles are the same k-major tiles either way; only the global-load
+// pattern changes (a transposed operand is read along its contiguous axis).
+template <int BM, int BN, int BK, int WGM, int WGN, bool VEC, bool SPLIT, int OCC = 1, bool TA = false,
+          bool TB = false>
 __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams p) {
     static_assert(WGM * WGN == 4, "4 waves per workgroup");
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -98,36 +103,66 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
     float a_s[A_SCL > 0 ? A_SCL : 1];
     float b_s[B_SCL > 0 ? B_SCL : 1];
 
+    // A tile (rows m0.., k0..): along k from A[M][K], along m from A^T[K][M].
+    // B tile (k0.., cols n0..): along n from B[K][N], along k from B^T[N][K].
     auto load_tile = [&](int k0) {
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
                 const int idx = tid + i * kThreads;
-                const int r = idx / (BK / 4), kq = idx % (BK / 4);
-                const int gm = m0 + r, gk = k0 + 4 * kq;
-                a_v[i] = (gm < M && gk < K) ? *(const f32x4*)(A + (size_t)gm * K + gk) : f32x4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (!TA) {
+                    const int r = idx / (BK / 4), kq = idx % (BK / 4);
+                    const int gm = m0 + r, gk = k0 + 4 * kq;
+                    a_v[i] = (gm < M && gk < K) ? *(const f32x4*)(A + (size_t)gm * K + gk)
+                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                } else {
+                    const int kr = idx / (BM / 4), mq = idx % (BM / 4);
+                    const int gk = k0 + kr, gm = m0 + 4 * mq;
+                    a_v[i] = (gk < K && gm < M) ? *(const f32x4*)(A + (size_t)gk * M + gm)
+                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
             }
 #pragma unroll
             for (int i = 0; i < B_VEC; ++i) {
                 const int idx = tid + i * kThreads;
-                const int kr = idx / (BN / 4), nq = idx % (BN / 4);
-                const int gk = k0 + kr, gn = n0 + 4 * nq;
-                b_v[i] = (gk < K && gn < N) ? *(const f32x4*)(B + (size_t)gk * N + gn) : f32x4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (!TB) {
+                    const int kr = idx / (BN / 4), nq = idx % (BN / 4);
+                    const int gk = k0 + kr, gn = n0 + 4 * nq;
+                    b_v[i] = (gk < K && gn < N) ? *(const f32x4*)(B + (size_t)gk * N + gn)
+                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                } else {
+                    const int c = idx / (BK / 4), kq = idx % (BK / 4);
+                    const int gn = n0 + c, gk = k0 + 4 * kq;
+                    b_v[i] = (gn < N && gk < K) ? *(const f32x4*)(B + (size_t)gn * K + gk)
+                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
             }
         } else {
 #pragma unroll
             for (int i = 0; i < A_SCL; ++i) {
                 const int idx = tid + i * kThreads;
-                const int r = idx / BK, kk = idx % BK;
-                const int gm = m0 + r, gk = k0 + kk;
-                a_s[i] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.0f;
+                if constexpr (!TA) {
+                    const int r = idx / BK, kk = idx % BK;
+                    const int gm = m0 + r, gk = k0 + kk;
+                    a_s[i] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.0f;
+                } else {
+                    const int kr = idx / BM, r = idx % BM;
+                    const int gk = k0 + kr, gm = m0 + r;
+                    a_s[i] = (gk < K && gm < M) ? A[(size_t)gk * M + gm] : 0.0f;
+                }
             }
 #pragma unroll
             for (int i = 0; i < B_SCL; ++i) {
                 const int idx = tid + i * kThreads;
-                const int kr = idx / BN, n = idx % BN;
-                const int gk = k0 + kr, gn = n0 + n;
-                b_s[i] = (gk < K && gn < N) ? B[(size_t)gk * N + gn] : 0.0f;
+                if constexpr (!TB) {
+                    const int kr = idx / BN, n = idx % BN;
+                    const int gk = k0 + kr, gn = n0 + n;
+                    b_s[i] = (gk < K && gn < N) ? B[(size_t)gk * N + gn] : 0.0f;
+                } else {
+                    const int c = idx / BK, kk = idx % BK;
+                    const int gn = n0 + c, gk = k0 + kk;
+                    b_s[i] = (gn < N && gk < K) ? B[(size_t)gn * K + gk] : 0.0f;
+                }
             }
         }
     };
@@ -137,28 +172,47 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
                 const int idx = tid + i * kThreads;
-                const int r = idx / (BK / 4), kq = idx % (BK / 4);
-                As[buf][4 * kq + 0][r] = a_v[i].x;
-                As[buf][4 * kq + 1][r] = a_v[i].y;
-                As[buf][4 * kq + 2][r] = a_v[i].z;
-                As[buf][4 * kq + 3][r] = a_v[i].w;
+                if constexpr (!TA) {
+                    const int r = idx / (BK / 4), kq = idx % (BK / 4);
+                    As[buf][4 * kq + 0][r] = a_v[i].x;
+                    As[buf][4 * kq + 1][r] = a_v[i].y;
+                    As[buf][4 * kq + 2][r] = a_v[i].z;
+                    As[buf][4 * kq + 3][r] = a_v[i].w;
+                } else {
+                    const int kr = idx / (BM / 4), mq = idx % (BM / 4);
+                    *(f32x4*)&As[buf][kr][4 * mq] = a_v[i];
+                }
             }
 #pragma unroll
             for (int i = 0; i < B_VEC; ++i) {
                 const int idx = tid + i * kThreads;
-                const int kr = idx / (BN / 4), nq = idx % (BN / 4);
-                *(f32x4*)&Bs[buf][kr][4 * nq] = b_v[i];
+                if constexpr (!TB) {
+                    const int kr = idx / (BN / 4), nq = idx % (BN / 4);
+                    *(f32x4*)&Bs[buf][kr][4 * nq] = b_v[i];
+                } else {
+                    const int c = idx / (BK / 4), kq = idx % (BK / 4);
+                    Bs[buf][4 * kq + 0][c] = b_v[i].x;
+                    Bs[buf][4 * kq + 1][c] = b_v[i].y;
+                    Bs[buf][4 * kq + 2][c] = b_v[i].z;
+                    Bs[buf][4 * kq + 3][c] = b_v[i].w;
+                }
             }
         } else {
 #pragma unroll
             for (int i = 0; i < A_SCL; ++i) {
                 const int idx = tid + i * kThreads;
-                As[buf][idx % BK][idx / BK] = a_s[i];
+                if constexpr (!TA)
+                    As[buf][idx % BK][idx / BK] = a_s[i];
+                else
+                    As[buf][idx / BM][idx % BM] = a_s[i];
             }
 #pragma unroll
             for (int i = 0; i < B_SCL; ++i) {
                 const int idx = tid + i * kThreads;
-                Bs[buf][idx / BN][idx % BN] = b_s[i];
+                if constexpr (!TB)
+                    Bs[buf][idx / BN][idx % BN] = b_s[i];
+                else
+                    Bs[buf][idx % BK][idx / BK] = b_s[i];
             }
         }
     };
@@ -256,28 +310,35 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
     }
 }
 
-// Skinny GEMM (M <= 16*MT): the product is bound by reading B once from HBM,
-// so the kernel is organised around that stream.
+// Skinny GEMM (M <= 16*MT): the product is bound by reading B once from
+// HBM (or, for tiny problems, by latency), so the kernel is organised around
+// that stream.
 //  * A workgroup owns 64 columns and a K slice of 256 rows; each wave takes
 //    64 of those rows and issues all 16 of its B loads before the first MFMA.
-//  * Every B load is a float4: lane l reads row k0 + 4s + l/16, columns
-//    c0 + 4(l%16) .. +3, so 16 lanes stream 256 contiguous bytes of a row and a
-//    wave keeps 16 KB in flight.  Component j feeds its own
-//    v_mfma_f32_16x16x4_f32, whose column index l%16 then stands for column
-//    c0 + 4(l%16) + j; the four MFMAs cover the 64 columns.
-//  * The four waves' partial sums are added through LDS in wave order.  With
-//    several K slices each workgroup stores its partial and splitk_reduce adds
-//    them in slice order (deterministic).  An in-kernel "last workgroup
-//    reduces" scheme would need agent-scope fences, which on this part write
-//    back and invalidate the per-XCD L2 - measured 4x slower.
-template <int MT>
+//  * VB: every B load is a float4: lane l reads row k0 + 4s + l/16, columns
+//    c0 + 4(l%16) .. +3, so 16 lanes stream 256 contiguous bytes of a row and
+//    a wave keeps 16 KB in flight.  Otherwise (N % 4 != 0 or unaligned B) the
+//    same four columns are four bounds-checked scalar loads.  Component j
+//    feeds its own v_mfma_f32_16x16x4_f32, whose column index l%16 then stands
+//    for column c0 + 4(l%16) + j; the four MFMAs cover the 64 columns.
+//  * TA: A is given transposed ([K][M]); the staging loop then walks m fastest.
+//  * The four waves' partial sums are added through LDS in wave order (the
+//    buffer that held the A slice is reused).  With several K slices each
+//    workgroup stores its partial and a reduce kernel adds them in slice order
+//    (deterministic).  An in-kernel "last workgroup reduces" scheme would need
+//    agent-scope fences, which on this part write back and invalidate the
+//    per-XCD L2 - measured 4x slower.
+template <int MT, bool VB, bool TA>
 __global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
     constexpr int KS = 256;         // K rows per workgroup
     constexpr int KW = KS / 4;      // per wave
     constexpr int STEPS = KW / 4;   // MFMA k-steps per wave
     constexpr int ROWS = 16 * MT;
-    __shared__ float As[ROWS][KS + 1];
-    __shared__ __attribute__((aligned(16))) float red[4][ROWS][64];
+    constexpr int A_FLOATS = ROWS * (KS + 1);
+    constexpr int RED_FLOATS = 4 * ROWS * 64;
+    __shared__ __attribute__((aligned(16))) float smem[A_FLOATS > RED_FLOATS ? A_FLOATS : RED_FLOATS];
+    float(*As)[KS + 1] = (float(*)[KS + 1])smem;
+    float(*red)[ROWS][64] = (float(*)[ROWS][64])smem;
 
     const int g = blockIdx.z, split = blockIdx.y, cb = blockIdx.x;
     const int M = p.M, N = p.N, K = p.K;
@@ -294,20 +355,35 @@ __global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
         const int k = kw0 + 4 * s + kl;
-        bv[s] = (k < K && col4 < N) ? *(const f32x4*)(B + (size_t)k * N + col4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (VB) {
+            bv[s] = (k < K && col4 < N) ? *(const f32x4*)(B + (size_t)k * N + col4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+            const float* row = B + (size_t)k * N;
+            const bool kin = k < K;
+            bv[s] = f32x4{(kin && col4 < N) ? row[col4] : 0.f, (kin && col4 + 1 < N) ? row[col4 + 1] : 0.f,
+                          (kin && col4 + 2 < N) ? row[col4 + 2] : 0.f, (kin && col4 + 3 < N) ? row[col4 + 3] : 0.f};
+        }
     }
     constexpr int A_PER = ROWS * KS / 256;
     float as[A_PER];
 #pragma unroll
     for (int i = 0; i < A_PER; ++i) {
         const int idx = tid + 256 * i;
-        const int r = idx / KS, c = idx % KS;
-        as[i] = (r < M && kslice + c < K) ? A[(size_t)r * K + kslice + c] : 0.0f;
+        if constexpr (!TA) {
+            const int r = idx / KS, c = idx % KS;
+            as[i] = (r < M && kslice + c < K) ? A[(size_t)r * K + kslice + c] : 0.0f;
+        } else {
+            const int c = idx / ROWS, r = idx % ROWS;
+            as[i] = (r < M && kslice + c < K) ? A[(size_t)(kslice + c) * M + r] : 0.0f;
+        }
     }
 #pragma unroll
     for (int i = 0; i < A_PER; ++i) {
         const int idx = tid + 256 * i;
-        As[idx / KS][idx % KS] = as[i];
+        if constexpr (!TA)
+            As[idx / KS][idx % KS] = as[i];
+        else
+            As[idx % ROWS][idx / ROWS] = as[i];
     }
     __syncthreads();
 
@@ -327,6 +403,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
             acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].w, acc[t][3], 0, 0, 0);
         }
     }
+    __syncthreads();  // the A slice is no longer read: its LDS becomes red
     // Accumulator (t, j), register r of lane l: row 16t + 4(l/16) + r,
     // column c0 + 4(l%16) + j.
 #pragma unroll
@@ -340,17 +417,6 @@ __global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
     const float* __restrict__ bias = p.bias[g];
     const float* __restrict__ R = p.R[g];
     float* __restrict__ C = p.C[g];
-    auto finish = [&](int row, int col, f32x4 v) {
-        float o[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float y = o[j] + (bias ? bias[col + j] : 0.0f);
-            y = apply_act(y, p.act);
-            if (R) y += R[(size_t)row * N + col + j];
-            o[j] = y;
-        }
-        *(f32x4*)(C + (size_t)row * N + col) = f32x4{o[0], o[1], o[2], o[3]};
-    };
     const size_t MN = (size_t)M * N;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -362,10 +428,26 @@ __global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
         v += *(const f32x4*)&red[1][row][cc];
         v += *(const f32x4*)&red[2][row][cc];
         v += *(const f32x4*)&red[3][row][cc];
-        if (p.splits == 1)
-            finish(row, col, v);
-        else
-            *(f32x4*)(p.ws + ((size_t)g * p.splits + split) * MN + (size_t)row * N + col) = v;
+        float o[4] = {v.x, v.y, v.z, v.w};
+        float* dst = p.splits == 1 ? C + (size_t)row * N + col
+                                   : p.ws + ((size_t)g * p.splits + split) * MN + (size_t)row * N + col;
+        if (p.splits == 1) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (!VB && col + j >= N) break;
+                float y = o[j] + (bias ? bias[col + j] : 0.0f);
+                y = apply_act(y, p.act);
+                if (R) y += R[(size_t)row * N + col + j];
+                o[j] = y;
+            }
+        }
+        if constexpr (VB) {
+            *(f32x4*)dst = f32x4{o[0], o[1], o[2], o[3]};
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (col + j < N) dst[j] = o[j];
+        }
     }
 }
 
@@ -413,7 +495,7 @@ __global__ void __launch_bounds__(256) splitk_reduce(const GemmParams p, int cou
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int OCC = 1>
+template <int BM, int BN, int BK, int WGM, int WGN, int OCC = 1, bool TA = false, bool TB = false>
 int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
     p.tiles_m = (uint32_t)((p.M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((p.N + BN - 1) / BN);
@@ -421,16 +503,16 @@ int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
     dim3 grid(p.tiles_m * p.tiles_n, (unsigned)p.splits, (unsigned)count);
     const bool split = p.splits > 1;
     if (vec && split)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true>), grid, dim3(kThreads), 0, ctx->stream,
-                           p);
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true, 1, TA, TB>), grid, dim3(kThreads), 0,
+                           ctx->stream, p);
     else if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false, OCC>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false, OCC, TA, TB>), grid, dim3(kThreads), 0,
                            ctx->stream, p);
     else if (split)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true, 1, TA, TB>), grid, dim3(kThreads), 0,
                            ctx->stream, p);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, false>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, false, 1, TA, TB>), grid, dim3(kThreads), 0,
                            ctx->stream, p);
     if (int rc = check_launch("gemm_f32_mfma")) return rc;
     if (split) {
@@ -442,14 +524,40 @@ int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
     return 0;
 }
 
+// Transposed operands are built for the two default tile shapes only.
+template <bool TA, bool TB>
+int launch_by_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec, int cfg) {
+    if constexpr (TA || TB) {
+        if (cfg == 2) return launch_cfg<64, 64, 16, 2, 2, 1, TA, TB>(ctx, p, count, vec);
+        return launch_cfg<128, 128, 16, 2, 2, 4, TA, TB>(ctx, p, count, vec);
+    } else {
+        switch (cfg) {
+            case 2: return launch_cfg<64, 64, 16, 2, 2>(ctx, p, count, vec);
+            case 3: return launch_cfg<256, 128, 16, 2, 2>(ctx, p, count, vec);
+            case 4: return launch_cfg<128, 128, 32, 2, 2>(ctx, p, count, vec);
+            case 5: return launch_cfg<128, 256, 16, 2, 2>(ctx, p, count, vec);
+            case 6: return launch_cfg<128, 128, 16, 2, 2, 4>(ctx, p, count, vec);
+            default: return launch_cfg<128, 128, 16, 2, 2>(ctx, p, count, vec);
+        }
+    }
+}
+
+template <int MT, bool TA>
+void launch_skinny(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb) {
+    if (vb)
+        hipLaunchKernelGGL((gemm_skinny_f32<MT, true, TA>), grid, dim3(256), 0, ctx->stream, p);
+    else
+        hipLaunchKernelGGL((gemm_skinny_f32<MT, false, TA>), grid, dim3(256), 0, ctx->stream, p);
+}
+
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 constexpr int kBK = 16;
 constexpr size_t kMaxSplitBytes = (size_t)256 << 20;
 
 int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
-                  const float* const* B, size_t M, size_t K, size_t N, const float* const* bias, int act,
-                  const float* const* residual) {
+                  const float* const* B, size_t M, size_t K, size_t N, int ta, int tb, const float* const* bias,
+                  int act, const float* const* residual) {
     LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm: NULL argument");
     LANCIUS_REQUIRE(count >= 1 && count <= LANCIUS_HIP_MAX_GROUP, LANCIUS_HIP_ERR_SHAPE, "gemm: group count %zu",
                     count);
@@ -459,9 +567,13 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_GELU, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "gemm: activation %d", act);
     if (int rc = bind_device(ctx)) return rc;
+    ta = ta != 0;
+    tb = tb != 0;
 
     GemmParams p{};
-    bool vec = (K % 4 == 0) && (N % 4 == 0);
+    // float4 global loads run along each operand's contiguous axis
+    bool vec = ((ta ? M : K) % 4 == 0) && ((tb ? K : N) % 4 == 0);
+    bool vb = N % 4 == 0;  // skinny: float4 B rows and float4 C / partial stores
     for (size_t g = 0; g < count; ++g) {
         LANCIUS_REQUIRE(C[g] && A[g] && B[g], LANCIUS_HIP_ERR_NULL_PTR, "gemm: NULL operand in group %zu", g);
         p.C[g] = C[g];
@@ -470,15 +582,19 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         p.bias[g] = bias ? bias[g] : nullptr;
         p.R[g] = residual ? residual[g] : nullptr;
         vec = vec && aligned16(A[g]) && aligned16(B[g]);
+        vb = vb && aligned16(B[g]) && aligned16(C[g]);
     }
     p.M = (int)M;
     p.N = (int)N;
     p.K = (int)K;
     p.act = act;
 
-    // M <= 32 with float4-aligned rows: the HBM-streaming skinny kernel, one
-    // workgroup per (64 columns, 256-row K slice).
-    if (M <= 32 && vec && tune("gemm_skinny", 1)) {
+    // M <= 32 (B not transposed): the B-streaming skinny kernel, one
+    // workgroup per (64 columns, 256-row K slice).  Measured on MI355X it
+    // beats the tiled kernel up to M = 32 (16x4096x4096: 22 vs 34 us;
+    // 32x2048x120: 10.6 vs 13.6 us) and loses at M = 64 with four row tiles
+    // (64x4096x4096: 43 vs 38 us; 64x784x256: 13.0 vs 11.8 us).
+    if (M <= 32 && !tb && tune("gemm_skinny", 1)) {
         const size_t splits = (K + 255) / 256;
         const size_t col_blocks = (N + 63) / 64;
         const size_t ws_bytes = splits > 1 ? count * splits * M * N * sizeof(float) : 0;
@@ -491,15 +607,22 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
             p.splits = (int)splits;
             const dim3 grid((unsigned)col_blocks, (unsigned)splits, (unsigned)count);
             if (M <= 16)
-                hipLaunchKernelGGL(gemm_skinny_f32<1>, grid, dim3(256), 0, ctx->stream, p);
+                ta ? launch_skinny<1, true>(ctx, p, grid, vb) : launch_skinny<1, false>(ctx, p, grid, vb);
             else
-                hipLaunchKernelGGL(gemm_skinny_f32<2>, grid, dim3(256), 0, ctx->stream, p);
+                ta ? launch_skinny<2, true>(ctx, p, grid, vb) : launch_skinny<2, false>(ctx, p, grid, vb);
             if (int rc = check_launch("gemm_skinny_f32")) return rc;
             if (splits > 1) {
-                const size_t total4 = count * M * N / 4;
-                hipLaunchKernelGGL(splitk_reduce_vec4, dim3((unsigned)std::min<size_t>((total4 + 255) / 256, 4096)),
-                                   dim3(256), 0, ctx->stream, p, (int)count);
-                if (int rc = check_launch("splitk_reduce_vec4")) return rc;
+                if (vb) {
+                    const size_t total4 = count * M * N / 4;
+                    hipLaunchKernelGGL(splitk_reduce_vec4,
+                                       dim3((unsigned)std::min<size_t>((total4 + 255) / 256, 4096)), dim3(256), 0,
+                                       ctx->stream, p, (int)count);
+                } else {
+                    const size_t total = count * M * N;
+                    hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)),
+                                       dim3(256), 0, ctx->stream, p, (int)count);
+                }
+                if (int rc = check_launch("splitk_reduce")) return rc;
             }
             return ok();
         }
@@ -515,7 +638,7 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     // that gives >= 256 workgroups, else 64x64.  Measured on MI355X: 115
     // TFLOP/s at 4096^3 (84% of the measured 137 TFLOP/s fp32 MFMA ceiling).
     int cfg = tune("gemm_tile", 0);
-    if (cfg < 1 || cfg > 6) cfg = big_tiles >= 256 ? 6 : 2;
+    if (cfg < 1 || cfg > 6 || ((ta || tb) && cfg != 2 && cfg != 6)) cfg = big_tiles >= 256 ? 6 : 2;
     const size_t bm = cfg == 2 ? 64 : cfg == 3 ? 256 : 128;
     const size_t bn = cfg == 2 ? 64 : cfg == 5 ? 256 : 128;
     const size_t bk = cfg == 4 ? 32 : kBK;
@@ -543,14 +666,14 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         p.ws = (float*)ws;
     }
     int rc;
-    switch (cfg) {
-        case 2: rc = launch_cfg<64, 64, 16, 2, 2>(ctx, p, (int)count, vec); break;
-        case 3: rc = launch_cfg<256, 128, 16, 2, 2>(ctx, p, (int)count, vec); break;
-        case 4: rc = launch_cfg<128, 128, 32, 2, 2>(ctx, p, (int)count, vec); break;
-        case 5: rc = launch_cfg<128, 256, 16, 2, 2>(ctx, p, (int)count, vec); break;
-        case 6: rc = launch_cfg<128, 128, 16, 2, 2, 4>(ctx, p, (int)count, vec); break;
-        default: rc = launch_cfg<128, 128, 16, 2, 2>(ctx, p, (int)count, vec); break;
-    }
+    if (ta && tb)
+        rc = launch_by_cfg<true, true>(ctx, p, (int)count, vec, cfg);
+    else if (ta)
+        rc = launch_by_cfg<true, false>(ctx, p, (int)count, vec, cfg);
+    else if (tb)
+        rc = launch_by_cfg<false, true>(ctx, p, (int)count, vec, cfg);
+    else
+        rc = launch_by_cfg<false, false>(ctx, p, (int)count, vec, cfg);
     return rc ? rc : ok();
 }
 
@@ -568,13 +691,29 @@ int lancius_hip_gemm_f32(lancius_hip_ctx* ctx, float* C, const float* A, const f
     const float* b1[1] = {B};
     const float* s1[1] = {bias};
     const float* r1[1] = {residual};
-    return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, s1, act, r1);
+    return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, 0, 0, s1, act, r1);
 }
 
 int lancius_hip_gemm_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
                                  const float* const* B, size_t M, size_t K, size_t N, const float* const* bias,
                                  int act, const float* const* residual) {
-    return gemm_dispatch(ctx, count, C, A, B, M, K, N, bias, act, residual);
+    return gemm_dispatch(ctx, count, C, A, B, M, K, N, 0, 0, bias, act, residual);
+}
+
+int lancius_hip_gemm_ex_f32(lancius_hip_ctx* ctx, float* C, const float* A, const float* B, size_t M, size_t K,
+                            size_t N, int trans_a, int trans_b, const float* bias, int act, const float* residual) {
+    float* c1[1] = {C};
+    const float* a1[1] = {A};
+    const float* b1[1] = {B};
+    const float* s1[1] = {bias};
+    const float* r1[1] = {residual};
+    return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, trans_a, trans_b, s1, act, r1);
+}
+
+int lancius_hip_gemm_grouped_ex_f32(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
+                                    const float* const* B, size_t M, size_t K, size_t N, int trans_a, int trans_b,
+                                    const float* const* bias, int act, const float* const* residual) {
+    return gemm_dispatch(ctx, count, C, A, B, M, K, N, trans_a, trans_b, bias, act, residual);
 }
 
 }  // extern "C"

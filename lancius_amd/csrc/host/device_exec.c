@@ -35,6 +35,7 @@ typedef struct {
     member_t m[MAXG];
     size_t d[12];
     int act, causal, has_bias, has_res;
+    int ta, tb; /* GEMM operands read transposed (an absorbed TRANSPOSE) */
 } launch_t;
 
 struct lancius_device_program {
@@ -84,6 +85,7 @@ typedef struct {
     uint32_t* chain_bias;       /* by final node: bias source (root) */
     uint32_t* chain_res;        /* by final node: residual (root) */
     int* chain_act;             /* by final node */
+    uint32_t* mm_src;           /* by 2*MATMUL id + operand: untransposed source root, NONE if none */
 } cstate;
 
 static void cstate_free(cstate* c) {
@@ -98,6 +100,7 @@ static void cstate_free(cstate* c) {
     free(c->chain_bias);
     free(c->chain_res);
     free(c->chain_act);
+    free(c->mm_src);
 }
 
 static const lancius_node* other_operand(const lancius_node* add, uint32_t cur) {
@@ -105,6 +108,21 @@ static const lancius_node* other_operand(const lancius_node* add, uint32_t cur) 
     if (add->inputs[0]->id == cur) return add->inputs[1];
     if (add->inputs[1]->id == cur) return add->inputs[0];
     return NULL;
+}
+
+/* A 2-D TRANSPOSE whose only consumer is this MATMUL becomes a transposed
+ * read of its input inside the GEMM (no launch, no buffer). */
+static void absorb_transposes(cstate* c, const lancius_node* mm) {
+    for (int j = 0; j < 2; j++) {
+        const lancius_node* t = mm->inputs[j];
+        if (!t || t->op != LANCIUS_OP_TRANSPOSE || c->consumers[t->id] != 1 || t->ndim != 2 || !t->inputs ||
+            !t->inputs[0])
+            continue;
+        const lancius_node* src = t->inputs[0];
+        if (src->ndim != 2 || src->shape[0] != t->shape[1] || src->shape[1] != t->shape[0]) continue;
+        c->absorbed[t->id] = 1;
+        c->mm_src[2 * mm->id + j] = c->root[src->id];
+    }
 }
 
 /* MATMUL -> ADD(BROADCAST row) -> RELU|GELU -> ADD(residual), each link only
@@ -219,8 +237,11 @@ static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
         L->d[0] = M;
         L->d[1] = K;
         L->d[2] = N;
-        m->in[0] = c->root[a->id];
-        m->in[1] = c->root[b->id];
+        const uint32_t sa = c->mm_src[2 * mm->id], sb = c->mm_src[2 * mm->id + 1];
+        L->ta = sa != NONE;
+        L->tb = sb != NONE;
+        m->in[0] = L->ta ? sa : c->root[a->id];
+        m->in[1] = L->tb ? sb : c->root[b->id];
         if (head != NONE) {
             m->in[2] = c->chain_bias[n->id];
             m->in[3] = c->chain_res[n->id];
@@ -453,7 +474,7 @@ static int same_group(const launch_t* a, const launch_t* b) {
     if (a->kind != b->kind || a->wave != b->wave || a->count >= MAXG) return 0;
     if (a->kind == L_GEMM)
         return a->d[0] == b->d[0] && a->d[1] == b->d[1] && a->d[2] == b->d[2] && a->act == b->act &&
-               a->has_bias == b->has_bias && a->has_res == b->has_res;
+               a->has_bias == b->has_bias && a->has_res == b->has_res && a->ta == b->ta && a->tb == b->tb;
     if (a->kind == L_ATTN)
         return a->d[0] == b->d[0] && a->d[1] == b->d[1] && a->d[2] == b->d[2] && a->causal == b->causal;
     return 0;
@@ -623,6 +644,7 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
     if (!CALLOC(c.node, ids) || !CALLOC(c.wave, ids) || !CALLOC(c.order, ids) || !CALLOC(c.consumers, ids) ||
         !CALLOC(c.sole, ids) || !CALLOC(c.root, ids) || !CALLOC(c.absorbed, ids) || !CALLOC(c.chain_head, ids) ||
         !CALLOC(c.chain_bias, ids) || !CALLOC(c.chain_res, ids) || !CALLOC(c.chain_act, ids) ||
+        !CALLOC(c.mm_src, 2 * (size_t)ids) ||
         !CALLOC(p->ptr, ids) || !CALLOC(p->bytes, ids) || !CALLOC(p->role, ids) || !CALLOC(p->readable, ids) ||
         !CALLOC(p->argmax, ids) || !CALLOC(p->rows, ids) || !CALLOC(birth, ids) || !CALLOC(last, ids) ||
         !CALLOC(pinned, ids)) {
@@ -632,6 +654,7 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
     for (uint32_t i = 0; i < ids; i++) {
         c.wave[i] = NONE;
         c.chain_head[i] = NONE;
+        c.mm_src[2 * i] = c.mm_src[2 * i + 1] = NONE;
         c.root[i] = i;
         birth[i] = NONE;
     }
@@ -705,8 +728,10 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         for (uint32_t w = 0; w < sched->wave_count; w++)
             for (uint32_t i = 0; i < sched->waves[w].node_count; i++) {
                 const lancius_node* n = sched->waves[w].nodes[i];
-                if (n->op == LANCIUS_OP_MATMUL && !c.absorbed[n->id] && n->inputs && n->inputs[0] && n->inputs[1])
+                if (n->op == LANCIUS_OP_MATMUL && !c.absorbed[n->id] && n->inputs && n->inputs[0] && n->inputs[1]) {
+                    absorb_transposes(&c, n);
                     fuse_gemm_chain(&c, n);
+                }
             }
 
     /* launches, one per final node, sorted by (wave, position) */
@@ -909,8 +934,8 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
                 bias[k] = P(L->m[k].in[2]);
                 res[k] = P(L->m[k].in[3]);
             }
-            return lancius_hip_gemm_grouped_f32(ctx, L->count, C, A, B, L->d[0], L->d[1], L->d[2], bias, L->act,
-                                                res);
+            return lancius_hip_gemm_grouped_ex_f32(ctx, L->count, C, A, B, L->d[0], L->d[1], L->d[2], L->ta, L->tb,
+                                                   bias, L->act, res);
         }
         case L_ATTN: {
             float* O[MAXG];

@@ -9,10 +9,9 @@
 // its window (row-major scan), or onto plane position (0,0) when no value
 // beats -1e9 (its max_ih = max_iw = 0 start).  Here the scatter is turned
 // into gathers, so no two threads write one element and the order of
-// additions is fixed: pass 1 stores every window's winner; pass 2 gives each
-// input element (other than (0,0)) the dy of the windows that cover it and
-// chose it, in (ho, wo) order; pass 3 sums, per plane, the dy of every window
-// whose winner is (0,0).
+// additions is fixed: each input element other than (0,0) takes the dy of the
+// windows that cover it and chose it, in (ho, wo) order, and per plane one
+// workgroup sums the dy of every window whose winner is (0,0).
 #include <algorithm>
 
 #include "common.hpp"
@@ -53,59 +52,56 @@ __global__ void __launch_bounds__(kThreads) maxpool_fwd(float* __restrict__ out,
     }
 }
 
-__global__ void __launch_bounds__(kThreads) maxpool_winners(int32_t* __restrict__ win, const float* __restrict__ x,
-                                                            size_t total, int H, int W, int Ho, int Wo, int K,
-                                                            int stride) {
-    const size_t step = (size_t)gridDim.x * kThreads;
-    for (size_t o = (size_t)blockIdx.x * kThreads + threadIdx.x; o < total; o += step) {
-        const size_t plane = o / ((size_t)Ho * Wo);
-        const int pix = (int)(o - plane * Ho * Wo);
-        const int ho = pix / Wo, wo = pix - (pix / Wo) * Wo;
-        float best;
-        win[o] = window_argmax(x + plane * H * W, W, ho, wo, K, stride, best);
+// One launch: workgroups [0, planes) each sum, for their plane, the dy of the
+// windows whose winner is (0,0); the others give every other input element
+// the dy of the windows that cover it and choose it, in (ho, wo) order.
+// Winners are recomputed from x (K*K reads per covering window, L2-resident)
+// instead of being stored.
+__global__ void __launch_bounds__(kThreads) maxpool_bwd_fused(float* __restrict__ dx, const float* __restrict__ dy,
+                                                              const float* __restrict__ x, size_t planes, int H,
+                                                              int W, int Ho, int Wo, int K, int stride) {
+    const int HW = H * W, HoWo = Ho * Wo;
+    if (blockIdx.x < planes) {
+        __shared__ float part[kThreads];
+        const size_t plane = blockIdx.x;
+        const float* xp = x + plane * HW;
+        const float* gp = dy + plane * HoWo;
+        float g = 0.0f;
+        for (int o = threadIdx.x; o < HoWo; o += kThreads) {
+            float best;
+            if (window_argmax(xp, W, o / Wo, o - (o / Wo) * Wo, K, stride, best) == 0) g += gp[o];
+        }
+        part[threadIdx.x] = g;
+        __syncthreads();
+        for (int w = kThreads / 2; w >= 1; w >>= 1) {
+            if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+            __syncthreads();
+        }
+        if (threadIdx.x == 0) dx[plane * HW] = part[0];
+        return;
     }
-}
-
-__global__ void __launch_bounds__(kThreads) maxpool_bwd_gather(float* __restrict__ dx, const float* __restrict__ dy,
-                                                               const int32_t* __restrict__ win, size_t total, int H,
-                                                               int W, int Ho, int Wo, int K, int stride) {
-    const size_t step = (size_t)gridDim.x * kThreads;
-    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += step) {
-        const size_t plane = i / ((size_t)H * W);
-        const int pos = (int)(i - plane * H * W);
-        if (pos == 0) continue;  // pass 3
+    const size_t total = planes * HW;
+    const size_t step = (size_t)(gridDim.x - planes) * kThreads;
+    for (size_t i = (size_t)(blockIdx.x - planes) * kThreads + threadIdx.x; i < total; i += step) {
+        const size_t plane = i / HW;
+        const int pos = (int)(i - plane * HW);
+        if (pos == 0) continue;  // the plane's first workgroup writes it
         const int ih = pos / W, iw = pos - (pos / W) * W;
         // windows ho with ho*stride <= ih <= ho*stride + K - 1
         const int ho_lo = ih >= K ? (ih - K) / stride + 1 : 0;
-        const int ho_hi = std::min(Ho - 1, ih / stride);
+        const int ho_hi = min(Ho - 1, ih / stride);
         const int wo_lo = iw >= K ? (iw - K) / stride + 1 : 0;
-        const int wo_hi = std::min(Wo - 1, iw / stride);
-        const size_t pbase = plane * Ho * Wo;
+        const int wo_hi = min(Wo - 1, iw / stride);
+        const float* xp = x + plane * HW;
+        const float* gp = dy + plane * HoWo;
         float g = 0.0f;
         for (int ho = ho_lo; ho <= ho_hi; ++ho)
             for (int wo = wo_lo; wo <= wo_hi; ++wo) {
-                const size_t o = pbase + (size_t)ho * Wo + wo;
-                if (win[o] == pos) g += dy[o];
+                float best;
+                if (window_argmax(xp, W, ho, wo, K, stride, best) == pos) g += gp[ho * Wo + wo];
             }
         dx[i] = g;
     }
-}
-
-__global__ void __launch_bounds__(kThreads) maxpool_bwd_origin(float* __restrict__ dx, const float* __restrict__ dy,
-                                                               const int32_t* __restrict__ win, int HW, int HoWo) {
-    __shared__ float part[kThreads];
-    const size_t plane = blockIdx.x;
-    const size_t pbase = plane * HoWo;
-    float g = 0.0f;
-    for (int o = threadIdx.x; o < HoWo; o += kThreads)
-        if (win[pbase + o] == 0) g += dy[pbase + o];
-    part[threadIdx.x] = g;
-    __syncthreads();
-    for (int w = kThreads / 2; w >= 1; w >>= 1) {
-        if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) dx[plane * HW] = part[0];
 }
 
 unsigned grid_for(size_t work) { return (unsigned)std::max<size_t>(1, std::min<size_t>((work + 255) / 256, 8192)); }
@@ -146,22 +142,12 @@ int lancius_hip_maxpool2d_bwd_f32(lancius_hip_ctx* ctx, float* dx, const float* 
     if (planes == 0 || H * W == 0) return ok();
     LANCIUS_REQUIRE(planes < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "maxpool2d_bwd: %zu planes", planes);
     if (int rc = bind_device(ctx)) return rc;
-    const size_t outs = planes * H_out * W_out;
-    void* ws = nullptr;
-    if (int rc = workspace(ctx, std::max<size_t>(outs, 1) * sizeof(int32_t), &ws)) return rc;
-    int32_t* win = (int32_t*)ws;
-    if (outs) {
-        hipLaunchKernelGGL(maxpool_winners, dim3(grid_for(outs)), dim3(kThreads), 0, ctx->stream, win, x, outs,
-                           (int)H, (int)W, (int)H_out, (int)W_out, (int)K, (int)stride);
-        if (int rc = check_launch("maxpool_winners")) return rc;
-    }
     const size_t total = planes * H * W;
-    hipLaunchKernelGGL(maxpool_bwd_gather, dim3(grid_for(total)), dim3(kThreads), 0, ctx->stream, dx, dy, win, total,
-                       (int)H, (int)W, (int)H_out, (int)W_out, (int)K, (int)stride);
-    if (int rc = check_launch("maxpool_bwd_gather")) return rc;
-    hipLaunchKernelGGL(maxpool_bwd_origin, dim3((unsigned)planes), dim3(kThreads), 0, ctx->stream, dx, dy, win,
-                       (int)(H * W), (int)(H_out * W_out));
-    return check_launch("maxpool_bwd_origin");
+    const size_t gather = std::max<size_t>(1, std::min<size_t>((total + 255) / 256, 8192));
+    LANCIUS_REQUIRE(planes + gather < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "maxpool2d_bwd: %zu planes", planes);
+    hipLaunchKernelGGL(maxpool_bwd_fused, dim3((unsigned)(planes + gather)), dim3(kThreads), 0, ctx->stream, dx, dy,
+                       x, planes, (int)H, (int)W, (int)H_out, (int)W_out, (int)K, (int)stride);
+    return check_launch("maxpool2d_bwd");
 }
 
 }  // extern "C"

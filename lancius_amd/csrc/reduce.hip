@@ -148,8 +148,10 @@ int lancius_hip_sum_axis0_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     if (int rc = bind_device(ctx)) return rc;
     const size_t col_blocks = (cols + kThreads - 1) / kThreads;
     LANCIUS_REQUIRE(col_blocks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "sum_axis0: %zu columns", cols);
-    // Row splits: ~1024 workgroups in all, each over >= 16 rows.
-    size_t splits = std::max<size_t>(1, std::min<size_t>((rows + 15) / 16, 1024 / col_blocks));
+    // Row splits: ~1024 workgroups in all, each over >= 16 rows; none below
+    // 512 rows, where one pass is latency-bound anyway and a second launch
+    // would cost more than it saves.
+    size_t splits = rows <= 512 ? 1 : std::max<size_t>(1, std::min<size_t>((rows + 15) / 16, 1024 / col_blocks));
     splits = std::min<size_t>(splits, 65535);
     const size_t rchunk = rows ? (rows + splits - 1) / splits : 1;
     splits = rows ? (rows + rchunk - 1) / rchunk : 1;

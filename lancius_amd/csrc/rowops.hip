@@ -180,6 +180,35 @@ __global__ void __launch_bounds__(kRowThreads) cross_entropy_rows(double* __rest
     if (lane == 0) row_terms[row] = t;
 }
 
+// Up to 4096 rows: one workgroup does both passes (each wave takes rows
+// w, w+4, ...), so the loss is one launch.
+__global__ void __launch_bounds__(kRowThreads) cross_entropy_small(float* __restrict__ out, const float* __restrict__ x,
+                                                                   const float* __restrict__ y, int rows, int cols) {
+    __shared__ double part[kRowsPerBlock];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    double acc = 0.0;  // this wave's rows, in row order
+    for (int row = wave; row < rows; row += kRowsPerBlock) {
+        const float* xr = x + (size_t)row * cols;
+        const float* yr = y + (size_t)row * cols;
+        float m, s;
+        row_lse_parts(xr, cols, lane, m, s);
+        const double lse = (double)logf(s) + (double)m;
+        double t = 0.0;
+        for (int c = lane; c < cols; c += 64)
+            if (yr[c] == 1.0f) t += (double)xr[c] - lse;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+        acc += t;
+    }
+    if (lane == 0) part[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double total = 0.0;
+        for (int w = 0; w < kRowsPerBlock; ++w) total += part[w];
+        out[0] = (float)fabs(-total / (double)rows);
+    }
+}
+
 // Second pass: out[0] = |-(sum of row terms) / rows| (:84-85), summed by one
 // workgroup in a fixed order.
 __global__ void __launch_bounds__(256) cross_entropy_finish(float* __restrict__ out,
@@ -393,6 +422,11 @@ int lancius_hip_cross_entropy_f32(lancius_hip_ctx* ctx, float* out, const float*
     LANCIUS_REQUIRE(rows > 0 && cols > 0 && cols < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
                     "cross_entropy: rows=%zu cols=%zu", rows, cols);
     if (int rc = bind_device(ctx)) return rc;
+    if (rows <= 4096) {
+        hipLaunchKernelGGL(cross_entropy_small, dim3(1), dim3(kRowThreads), 0, ctx->stream, out, x, y, (int)rows,
+                           (int)cols);
+        return check_launch("cross_entropy_small");
+    }
     void* ws = nullptr;
     if (int rc = workspace(ctx, rows * sizeof(double), &ws)) return rc;
     hipLaunchKernelGGL(cross_entropy_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0, ctx->stream,

@@ -76,6 +76,9 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_copy_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_broadcast_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.lancius_hip_fill_f32.argtypes = [vp, vp, f32, sz]
+    lib.lancius_hip_gemm_ex_f32.argtypes = [vp, vp, vp, vp, sz, sz, sz, i32, i32, vp, i32, vp]
+    lib.lancius_hip_gemm_grouped_ex_f32.argtypes = [vp, sz, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), sz, sz, sz,
+                                                    i32, i32, C.POINTER(vp), i32, C.POINTER(vp)]
     for name in ("lancius_hip_sub_f32", "lancius_hip_mul_f32", "lancius_hip_relu_bwd_f32"):
         getattr(lib, name).argtypes = [vp, vp, vp, vp, sz]
     lib.lancius_hip_transpose_f32.argtypes = [vp, vp, vp, sz, sz]
@@ -241,6 +244,11 @@ class Device:
     def gemm(self, C_, A, B, M, K, N, bias=None, act=ACT_NONE, residual=None) -> None:
         _check(self.lib.lancius_hip_gemm_f32(self.ctx, _vp(C_), _vp(A), _vp(B), M, K, N, _vp(bias), act,
                                              _vp(residual)))
+
+    def gemm_ex(self, C_, A, B, M, K, N, trans_a=False, trans_b=False, bias=None, act=ACT_NONE,
+                residual=None) -> None:
+        _check(self.lib.lancius_hip_gemm_ex_f32(self.ctx, _vp(C_), _vp(A), _vp(B), M, K, N, int(trans_a),
+                                                int(trans_b), _vp(bias), act, _vp(residual)))
 
     def gemm_grouped(self, Cs, As, Bs, M, K, N, biases=None, act=ACT_NONE, residuals=None) -> None:
         n = len(Cs)

@@ -85,6 +85,8 @@ def ref_lib() -> C.CDLL | None:
         L.lancius_arena_create.restype = C.c_void_p
         L.lancius_arena_destroy.argtypes = [C.c_void_p]
         L.lancius_arena_destroy.restype = None
+        L.lancius_arena_reset.argtypes = [C.c_void_p]
+        L.lancius_arena_reset.restype = None
         L.kernel_matmul.argtypes = [_D, _D, _D, sz, sz, sz]
         L.kernel_conv2d_fwd.argtypes = [_D, _D, _D] + [sz] * 9
         L.kernel_conv2d_relu_fwd.argtypes = [_D, _D, _D] + [sz] * 9

@@ -85,6 +85,37 @@ def test_gemm_split_k(dev, M, K, N, act):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
 
 
+@pytest.mark.parametrize("M,K,N", [(32, 784, 128), (32, 128, 10), (17, 300, 77), (3, 1000, 1), (64, 784, 128),
+                                   (64, 128, 10), (48, 300, 77), (40, 4096, 4096)])
+def test_gemm_small_m_and_ragged_n(dev, M, K, N):
+    # M <= 32: the B-streaming kernel, N % 4 != 0 through its scalar-B path;
+    # 33..64: the tiled kernel with split K
+    got, ref = _gemm_case(dev, M, K, N, seed=90 + M + N, bias=True, act=ACT_RELU, residual=True)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 784, 128), (784, 64, 128), (128, 64, 784), (64, 128, 784), (130, 70, 201),
+                                   (300, 1000, 260), (1024, 1024, 1024), (7, 13, 5), (2048, 120, 10), (32, 500, 130),
+                                   (16, 4096, 4096)])
+@pytest.mark.parametrize("ta,tb", [(True, False), (False, True), (True, True)])
+def test_gemm_transposed_operands(dev, M, K, N, ta, tb):
+    """A given as A^T [K][M] and/or B as B^T [N][K] (what an absorbed
+    TRANSPOSE node hands the GEMM)."""
+    A = prng.normal(91 + M, (M, K))
+    B = prng.normal(92 + N, (K, N))
+    bv = prng.normal(93, (N,))
+    dA = dev.upload(np.ascontiguousarray(A.T) if ta else A)
+    dB = dev.upload(np.ascontiguousarray(B.T) if tb else B)
+    db, dC = dev.upload(bv), dev.alloc(M * N * 4)
+    case(f"gemm_ex M={M} K={K} N={N} ta={ta} tb={tb}")
+    dev.gemm_ex(dC, dA, dB, M, K, N, trans_a=ta, trans_b=tb, bias=db, act=ACT_GELU)
+    got = dev.download(dC, (M, N))
+    ref = oracle.gelu(oracle.matmul(A, B) + bv.astype(np.float64)[None, :])
+    for b in (dA, dB, db, dC):
+        b.free()
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
 def test_gemm_split_k_grouped_deterministic(dev):
     M, K, N, G = 50, 3000, 40, 3
     As = [prng.normal(70 + g, (M, K)) for g in range(G)]
