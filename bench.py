@@ -42,6 +42,7 @@ from lancius_amd import (DEVICE_GRAPH, Device, DeviceProgram, abi, device_count,
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
 PEAK_HBM = 8000.0       # GB/s
+PEAK_INT8_MFMA = 5000.0  # TOPS, MI355X dense int8 matrix
 METRIC = "GFLOP/s + % of fp32 MFMA peak (GEMM/attn/conv); graph fwd latency ms"
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 # Algorithmic flops of one training step (forward + every gradient):
@@ -104,6 +105,36 @@ def conv_case(dev, steps, warmup):
         b.free()
     flops = 2.0 * N * C_out * H * W * C_in * 9
     return ms, flops, 4.0 * (N * C_in * H * W + C_out * C_in * 9 + N * C_out * H * W)
+
+
+def int8_cases(dev, steps, warmup) -> dict:
+    """The int8 path at the headline GEMM and conv shapes: one call = dynamic
+    per-tensor quantization of the fp32 activation + int8 MFMA product with
+    int32 accumulation (+ weight re-layout), fp32 out.  TOPS counts 2MNK."""
+    out = {}
+    n = 4096
+    a = dev.upload(prng.normal(43, (n, n)))
+    b = dev.upload(np.round(prng.uniform(1043, (n, n), -127.4, 127.4)).astype(np.int8))
+    c = dev.alloc(n * n * 4)
+    t = time_steps(dev, lambda: dev.gemm_i8(c, a, b, 0.01, n, n, n), steps, warmup)
+    ops = 2.0 * n ** 3
+    out["gemm_i8_4096"] = {"ms": round(t, 4), "TOPS": round(ops / t / 1e9, 1),
+                           "frac_int8_mfma": round(ops / t / 1e9 / PEAK_INT8_MFMA, 4),
+                           "note": "includes quantizing A (fp32 -> int8) and re-laying B each call"}
+    for buf in (a, b, c):
+        buf.free()
+    N, C_in, H, W, C_out = 32, 64, 56, 56, 128
+    x = dev.upload(prng.normal(45, (N, C_in, H, W)))
+    w = dev.upload(np.round(prng.uniform(145, (C_out, C_in, 3, 3), -127.4, 127.4)).astype(np.int8))
+    o = dev.alloc(N * C_out * H * W * 4)
+    t = time_steps(dev, lambda: dev.conv2d_i8(o, x, w, 0.001, None, N, C_in, H, W, C_out, 3, 3, 1, 1, 1), steps,
+                   warmup)
+    ops = 2.0 * N * C_out * H * W * C_in * 9
+    out["conv3x3_N32_64to128_56x56_relu_i8"] = {"ms": round(t, 4), "TOPS": round(ops / t / 1e9, 1),
+                                                "frac_int8_mfma": round(ops / t / 1e9 / PEAK_INT8_MFMA, 4)}
+    for buf in (x, w, o):
+        buf.free()
+    return out
 
 
 def conv_bwd_cases(dev, steps, warmup) -> dict:
@@ -398,6 +429,8 @@ def main() -> int:
         t, f, b = conv_case(dev, steps, 3)
         extra["conv3x3_N32_64to128_56x56_relu"] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
                                                    "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
+        log("int8 path")
+        extra.update(int8_cases(dev, steps, 3))
         log("conv backward")
         extra.update(conv_bwd_cases(dev, steps, 3))
         log("row and elementwise kernels")

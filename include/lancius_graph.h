@@ -122,6 +122,11 @@ lancius_training_graph* lancius_ir_autodiff(lancius_graph* fwd_g, lancius_node* 
 void lancius_training_graph_destroy(lancius_training_graph* tg);
 #endif
 
+/* Per-tensor int8 quantization of conv filters (lancius_quantize.c:6-33,
+ * declared at lancius_ir.h:118): every 4-D INPUT with bound fp64 data gets
+ * runtime_data_int8, scale and dtype INT8 (graph-owned int8 copy). */
+void lancius_quantize_graph(lancius_graph* g);
+
 /* Conv2D + ReLU fusion pass (lancius_optimizer.c:15-41). */
 void lancius_optimize_fusion(lancius_graph* g);
 
@@ -136,8 +141,8 @@ lancius_memory_plan* lancius_build_memory_plan(lancius_schedule* sched, lancius_
 void lancius_memory_plan_destroy(lancius_memory_plan* plan);
 
 /* Sets the dtype of every node (e.g. LANCIUS_DTYPE_FP32 before planning the
- * device arena; the reference sizes plan blocks by dtype, lancius_ir.h:75-78).
- * No reference counterpart. */
+ * device arena; the reference sizes plan blocks by dtype, lancius_ir.h:75-78),
+ * except nodes already quantized to int8.  No reference counterpart. */
 void lancius_graph_set_dtype(lancius_graph* g, lancius_dtype dtype);
 
 #ifdef __cplusplus

@@ -217,6 +217,34 @@ LANCIUS_HIP_EXPORT int lancius_hip_maxpool2d_bwd_f32(lancius_hip_ctx* ctx, float
                                                      const float* x, size_t N, size_t C, size_t H, size_t W,
                                                      size_t H_out, size_t W_out, size_t K, size_t stride);
 
+/* ---- the int8 path (v_mfma_i32_32x32x32_i8) -------------------------- */
+
+/* Per-tensor symmetric quantization, the reference's formula
+ * (lancius_scheduler.c:199-204, lancius_vision_ops.c:28-36,
+ * lancius_quantize.c:14-25): scale = max|x| / 127 (1e-8 for an all-zero
+ * tensor), q[i] = (int8) round(x[i] / scale) in fp64, round half away from
+ * zero.  `scale` is a DEVICE pointer to one double. */
+LANCIUS_HIP_EXPORT int lancius_hip_quantize_i8(lancius_hip_ctx* ctx, int8_t* q, double* scale, const float* x,
+                                               size_t n);
+/* C[M,N] = epilogue((double) sum_k qa[m,k] * B[k,n] * scale_a * scale_b) with
+ * qa the dynamic per-tensor quantization of the fp32 A and B an int8 [K,N]
+ * matrix of scale scale_b: the int8 MATMUL branch
+ * (lancius_scheduler.c:195-220); int32 accumulation, exact.  Epilogue as
+ * lancius_hip_gemm_f32 (bias, act, residual; all may be NULL / NONE). */
+LANCIUS_HIP_EXPORT int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, const int8_t* B,
+                                               double scale_b, size_t M, size_t K, size_t N,
+                                               const float* bias, int act, const float* residual);
+/* conv2d with int8 OIHW weights of scale scale_w and the fp32 NCHW input
+ * quantized per tensor on the fly: kernel_conv2d_int8_fwd
+ * (lancius_kernels.c:177-210) as routed by lancius_vision_ops.c:16-57;
+ * act = LANCIUS_HIP_ACT_RELU is the fused Conv+ReLU (:49-54).  bias may be
+ * NULL (the reference has none). */
+LANCIUS_HIP_EXPORT int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in, const int8_t* w,
+                                                 double scale_w, const float* bias,
+                                                 size_t N, size_t C_in, size_t H, size_t W,
+                                                 size_t C_out, size_t K_h, size_t K_w,
+                                                 size_t stride, size_t pad, int act);
+
 /* ---- streams and HIP graphs ------------------------------------------ */
 
 /* A context on a new non-blocking stream of default priority, owned by the

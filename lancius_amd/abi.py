@@ -174,6 +174,8 @@ def declare_graph_api(lib: C.CDLL) -> C.CDLL:
     lib.lancius_ir_autodiff.restype = TrainingGraphP
     lib.lancius_training_graph_destroy.argtypes = [TrainingGraphP]
     lib.lancius_training_graph_destroy.restype = None
+    lib.lancius_quantize_graph.argtypes = [GraphP]
+    lib.lancius_quantize_graph.restype = None
     lib.lancius_optimize_fusion.argtypes = [GraphP]
     lib.lancius_optimize_fusion.restype = None
     lib.lancius_ir_schedule.argtypes = [GraphP]

@@ -36,7 +36,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip", "reduce.hip", "pool.hip",
-               "probe.hip"]
+               "int8.hip", "probe.hip"]
 HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c", "host/graph_autodiff.c"]
 DEVICE_C_SOURCES = ["host/device_exec.c"]
 
@@ -71,6 +71,7 @@ REF_SOURCES = [
     "src/runtime/lancius_vision_ops.c",
     "src/runtime/lancius_threadpool.c",
     "src/compiler/lancius_optimizer.c",
+    "src/compiler/lancius_quantize.c",
 ]
 
 
@@ -117,7 +118,7 @@ def build_graph() -> Path:
     out = PKG / "liblancius_graph.so"
     tmp = out.with_suffix(".so.tmp")
     _run(["gcc", *C_FLAGS, "-shared", "-o", str(tmp), *[str(CSRC / s) for s in HOST_C_SOURCES],
-          "-Wl,--no-undefined"])
+          "-lm", "-Wl,--no-undefined"])
     os.replace(tmp, out)
     return out
 

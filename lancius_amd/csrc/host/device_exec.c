@@ -36,6 +36,8 @@ typedef struct {
     size_t d[12];
     int act, causal, has_bias, has_res;
     int ta, tb; /* GEMM operands read transposed (an absorbed TRANSPOSE) */
+    int i8;     /* GEMM / conv with an int8 weight operand */
+    double scale_w; /* its per-tensor scale, taken from the node at create time */
 } launch_t;
 
 struct lancius_device_program {
@@ -49,6 +51,7 @@ struct lancius_device_program {
     char** ptr;
     size_t* bytes;
     uint8_t* role;
+    uint8_t* is_i8;  /* by id: INPUT holding int8 weights (1 byte per element) */
     uint8_t* readable;
     int32_t** argmax;
     size_t* rows;
@@ -64,6 +67,12 @@ static size_t elems(const lancius_node* n) {
 }
 
 static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+/* An int8 weight: dtype INT8 (lancius_quantize.c:26, tested by
+ * lancius_vision_ops.c:14) or an int8 copy bound (lancius_scheduler.c:192). */
+static int int8_input(const lancius_node* n) {
+    return n && n->op == LANCIUS_OP_INPUT && (n->dtype == LANCIUS_DTYPE_INT8 || n->runtime_data_int8 != NULL);
+}
 
 static int fail(int code, const char* what) {
     fprintf(stderr, "[LANCIUS DEVICE] %s\n", what);
@@ -86,6 +95,7 @@ typedef struct {
     uint32_t* chain_res;        /* by final node: residual (root) */
     int* chain_act;             /* by final node */
     uint32_t* mm_src;           /* by 2*MATMUL id + operand: untransposed source root, NONE if none */
+    const uint8_t* i8;          /* by id: int8 weight input (the program's is_i8) */
 } cstate;
 
 static void cstate_free(cstate* c) {
@@ -113,6 +123,7 @@ static const lancius_node* other_operand(const lancius_node* add, uint32_t cur) 
 /* A 2-D TRANSPOSE whose only consumer is this MATMUL becomes a transposed
  * read of its input inside the GEMM (no launch, no buffer). */
 static void absorb_transposes(cstate* c, const lancius_node* mm) {
+    if (c->i8[mm->inputs[1]->id]) return; /* the int8 GEMM reads plain operands */
     for (int j = 0; j < 2; j++) {
         const lancius_node* t = mm->inputs[j];
         if (!t || t->op != LANCIUS_OP_TRANSPOSE || c->consumers[t->id] != 1 || t->ndim != 2 || !t->inputs ||
@@ -249,6 +260,10 @@ static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
         }
         L->has_bias = m->in[2] != NONE;
         L->has_res = m->in[3] != NONE;
+        if (c->i8[b->id]) {
+            L->i8 = 1;
+            L->scale_w = b->scale;
+        }
         return 0;
     }
     switch (n->op) {
@@ -341,6 +356,10 @@ static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
             L->act = n->op == LANCIUS_OP_CONV2D_RELU_FUSED ? LANCIUS_HIP_ACT_RELU : LANCIUS_HIP_ACT_NONE;
             m->in[0] = IN(n, 0);
             m->in[1] = IN(n, 1);
+            if (w->dtype == LANCIUS_DTYPE_INT8 && c->i8[w->id]) { /* lancius_vision_ops.c:14-16 */
+                L->i8 = 1;
+                L->scale_w = w->scale;
+            }
             return 0;
         }
         case LANCIUS_OP_SUB:
@@ -471,7 +490,7 @@ static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
 }
 
 static int same_group(const launch_t* a, const launch_t* b) {
-    if (a->kind != b->kind || a->wave != b->wave || a->count >= MAXG) return 0;
+    if (a->kind != b->kind || a->wave != b->wave || a->count >= MAXG || a->i8 || b->i8) return 0;
     if (a->kind == L_GEMM)
         return a->d[0] == b->d[0] && a->d[1] == b->d[1] && a->d[2] == b->d[2] && a->act == b->act &&
                a->has_bias == b->has_bias && a->has_res == b->has_res && a->ta == b->ta && a->tb == b->tb;
@@ -606,6 +625,7 @@ void lancius_device_program_destroy(lancius_device_program* p) {
     free(p->ptr);
     free(p->bytes);
     free(p->role);
+    free(p->is_i8);
     free(p->readable);
     free(p->argmax);
     free(p->rows);
@@ -641,11 +661,13 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
     p->ctx = ctx;
     p->exec = ctx;
     p->n_ids = ids;
+    const size_t ids2 = 2 * (size_t)ids;
     if (!CALLOC(c.node, ids) || !CALLOC(c.wave, ids) || !CALLOC(c.order, ids) || !CALLOC(c.consumers, ids) ||
         !CALLOC(c.sole, ids) || !CALLOC(c.root, ids) || !CALLOC(c.absorbed, ids) || !CALLOC(c.chain_head, ids) ||
         !CALLOC(c.chain_bias, ids) || !CALLOC(c.chain_res, ids) || !CALLOC(c.chain_act, ids) ||
-        !CALLOC(c.mm_src, 2 * (size_t)ids) ||
+        !CALLOC(c.mm_src, ids2) ||
         !CALLOC(p->ptr, ids) || !CALLOC(p->bytes, ids) || !CALLOC(p->role, ids) || !CALLOC(p->readable, ids) ||
+        !CALLOC(p->is_i8, ids) ||
         !CALLOC(p->argmax, ids) || !CALLOC(p->rows, ids) || !CALLOC(birth, ids) || !CALLOC(last, ids) ||
         !CALLOC(pinned, ids)) {
         rc = LANCIUS_HIP_ERR_OOM;
@@ -665,7 +687,7 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
             goto out;
         }
         c.node[n->id] = n;
-        p->bytes[n->id] = elems(n) * sizeof(float);
+        p->is_i8[n->id] = (uint8_t)int8_input(n);
         if (!supported(n->op)) {
             fprintf(stderr, "[LANCIUS DEVICE] op %d (node %u) is not on the device path\n", (int)n->op, n->id);
             rc = LANCIUS_HIP_ERR_UNSUPPORTED;
@@ -682,6 +704,24 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
             c.sole[in] = n->id;
         }
     }
+    /* An int8 INPUT stays int8 only when every consumer reads it as the weight
+     * operand of a MATMUL or conv; one used as an activation (the reference's
+     * quantizer also converts 4-D images) is fed in fp32 and quantized by the
+     * kernel that reads it, which gives the same int8 values. */
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        for (uint32_t j = 0; j < n->input_count; j++) {
+            if (!n->inputs[j] || !p->is_i8[n->inputs[j]->id]) continue;
+            const int weight_slot = j == 1 && (n->op == LANCIUS_OP_MATMUL || n->op == LANCIUS_OP_CONV2D ||
+                                               n->op == LANCIUS_OP_CONV2D_RELU_FUSED);
+            if (!weight_slot) p->is_i8[n->inputs[j]->id] = 0;
+        }
+    }
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        const lancius_node* n = g->nodes[i];
+        p->bytes[n->id] = elems(n) * (p->is_i8[n->id] ? 1 : sizeof(float));
+    }
+    c.i8 = p->is_i8;
     uint32_t scheduled = 0;
     for (uint32_t w = 0; w < sched->wave_count; w++)
         for (uint32_t i = 0; i < sched->waves[w].node_count; i++) {
@@ -925,6 +965,10 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
     const member_t* m = &L->m[0];
     switch (L->kind) {
         case L_GEMM: {
+            if (L->i8)
+                return lancius_hip_gemm_i8_f32(ctx, P(m->out), P(m->in[0]), (const int8_t*)prog->ptr[m->in[1]],
+                                               L->scale_w, L->d[0], L->d[1], L->d[2], P(m->in[2]), L->act,
+                                               P(m->in[3]));
             float* C[MAXG];
             const float *A[MAXG], *B[MAXG], *bias[MAXG], *res[MAXG];
             for (uint32_t k = 0; k < L->count; k++) {
@@ -950,6 +994,10 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
                                                      (float)(1.0 / sqrt((double)L->d[2])));
         }
         case L_CONV:
+            if (L->i8)
+                return lancius_hip_conv2d_i8_f32(ctx, P(m->out), P(m->in[0]), (const int8_t*)prog->ptr[m->in[1]],
+                                                 L->scale_w, NULL, L->d[0], L->d[1], L->d[2], L->d[3], L->d[4],
+                                                 L->d[5], L->d[6], L->d[7], L->d[8], L->act);
             return lancius_hip_conv2d_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), NULL, L->d[0], L->d[1], L->d[2],
                                           L->d[3], L->d[4], L->d[5], L->d[6], L->d[7], L->d[8], L->act);
         case L_LN:
@@ -1050,6 +1098,9 @@ int lancius_device_upload(lancius_device_program* prog, const lancius_node* n, c
     if (n->id >= prog->n_ids || (prog->role[n->id] != ROLE_INPUT && prog->role[n->id] != ROLE_CONST))
         return LANCIUS_HIP_ERR_UNSUPPORTED;
     const size_t e = elems(n);
+    if (prog->is_i8[n->id]) /* int8 weights take their int8 bytes */
+        return host_dtype == LANCIUS_DTYPE_INT8 ? lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e)
+                                                : LANCIUS_HIP_ERR_DTYPE;
     if (host_dtype == LANCIUS_DTYPE_FP32) return lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e * 4);
     if (host_dtype != LANCIUS_DTYPE_FP64) return LANCIUS_HIP_ERR_DTYPE;
     float* tmp = (float*)malloc(e * sizeof(float) + 1);
@@ -1066,6 +1117,9 @@ int lancius_device_download(lancius_device_program* prog, const lancius_node* n,
     if (!prog || !n || !host) return LANCIUS_HIP_ERR_NULL_PTR;
     if (n->id >= prog->n_ids || !prog->readable[n->id] || !prog->ptr[n->id]) return LANCIUS_HIP_ERR_UNSUPPORTED;
     const size_t e = elems(n);
+    if (prog->is_i8[n->id])
+        return host_dtype == LANCIUS_DTYPE_INT8 ? lancius_hip_download(prog->ctx, host, prog->ptr[n->id], e)
+                                                : LANCIUS_HIP_ERR_DTYPE;
     if (host_dtype == LANCIUS_DTYPE_FP32) return lancius_hip_download(prog->ctx, host, prog->ptr[n->id], e * 4);
     if (host_dtype != LANCIUS_DTYPE_FP64) return LANCIUS_HIP_ERR_DTYPE;
     float* tmp = (float*)malloc(e * sizeof(float) + 1);
@@ -1093,7 +1147,10 @@ int lancius_schedule_execute_device(lancius_schedule* schedule, lancius_graph* g
     for (uint32_t i = 0; i < g->node_count && !rc; i++) {
         lancius_node* n = g->nodes[i];
         if (n->op == LANCIUS_OP_INPUT) {
-            if (!n->runtime_data) rc = fail(LANCIUS_HIP_ERR_NULL_PTR, "INPUT node without runtime_data");
+            if (prog->is_i8[n->id])
+                rc = n->runtime_data_int8 ? lancius_device_upload(prog, n, n->runtime_data_int8, LANCIUS_DTYPE_INT8)
+                                          : fail(LANCIUS_HIP_ERR_NULL_PTR, "int8 INPUT node without runtime_data_int8");
+            else if (!n->runtime_data) rc = fail(LANCIUS_HIP_ERR_NULL_PTR, "INPUT node without runtime_data");
             else rc = lancius_device_upload(prog, n, n->runtime_data, LANCIUS_DTYPE_FP64);
         }
     }

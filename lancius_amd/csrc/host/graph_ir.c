@@ -6,6 +6,7 @@
  * builder); node storage lives in the graph's arena so node addresses are
  * stable for the life of the graph.
  */
+#include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -152,6 +153,15 @@ lancius_graph* lancius_graph_create(void) {
 
 void lancius_graph_destroy(lancius_graph* g) {
     if (!g) return;
+    /* int8 copies made by lancius_quantize_graph belong to the graph */
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        lancius_node* n = g->nodes[i];
+        if (n->rt && n->rt->int8_owner == LANCIUS_MEMORY_OWNED_HEAP && n->runtime_data_int8) {
+            free(n->runtime_data_int8);
+            n->runtime_data_int8 = NULL;
+            n->rt->buffer_int8 = NULL;
+        }
+    }
     free(g->nodes);
     free(g->rt_states);
     lancius_arena_destroy(g->arena);
@@ -161,9 +171,50 @@ void lancius_graph_destroy(lancius_graph* g) {
 void lancius_graph_set_dtype(lancius_graph* g, lancius_dtype dtype) {
     if (!g) return;
     for (uint32_t i = 0; i < g->node_count; i++) {
-        g->nodes[i]->dtype = dtype;
-        if (g->nodes[i]->rt) g->nodes[i]->rt->dtype = dtype;
+        lancius_node* n = g->nodes[i];
+        if (n->dtype == LANCIUS_DTYPE_INT8 && n->runtime_data_int8) continue; /* quantized weights stay int8 */
+        n->dtype = dtype;
+        if (n->rt) n->rt->dtype = dtype;
     }
+}
+
+/* lancius_quantize.c:6-33: every 4-D INPUT with bound fp64 data (a conv
+ * filter) gets a per-tensor int8 copy, scale = max|w| / 127 (1e-8 when all
+ * zero), q = (int8) round(w / scale), and dtype INT8, which routes its convs
+ * to the int8 kernels.  The int8 buffer is owned by the graph. */
+void lancius_quantize_graph(lancius_graph* g) {
+    if (!g) return;
+    int count = 0;
+    for (uint32_t i = 0; i < g->node_count; i++) {
+        lancius_node* n = g->nodes[i];
+        if (n->op != LANCIUS_OP_INPUT || !n->runtime_data || n->ndim != 4) continue;
+        size_t e = 1;
+        for (uint8_t d = 0; d < n->ndim; d++) e *= n->shape[d];
+        double m = 0.0;
+        for (size_t j = 0; j < e; j++) {
+            const double a = fabs(n->runtime_data[j]);
+            if (a > m) m = a;
+        }
+        const double scale = m > 0.0 ? m / 127.0 : 1e-8;
+        int8_t* q = (int8_t*)malloc(e ? e : 1);
+        if (!q) {
+            lancius_set_error(LANCIUS_ERROR_OOM);
+            return;
+        }
+        for (size_t j = 0; j < e; j++) q[j] = (int8_t)round(n->runtime_data[j] / scale);
+        if (n->rt && n->rt->int8_owner == LANCIUS_MEMORY_OWNED_HEAP) free(n->runtime_data_int8);
+        n->runtime_data_int8 = q;
+        n->scale = scale;
+        n->dtype = LANCIUS_DTYPE_INT8;
+        if (n->rt) {
+            n->rt->buffer_int8 = q;
+            n->rt->int8_owner = LANCIUS_MEMORY_OWNED_HEAP;
+            n->rt->scale = scale;
+            n->rt->dtype = LANCIUS_DTYPE_INT8;
+        }
+        count++;
+    }
+    printf("[LANCIUS QUANTIZER] %d weight tensors to int8\n", count);
 }
 
 /* A node with its input array and runtime-state record, all in the arena. */

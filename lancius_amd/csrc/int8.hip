@@ -1,0 +1,507 @@
+// The int8 path of the scheduler and the vision router on the gfx950 int8
+// matrix cores (v_mfma_i32_32x32x32_i8, 16 int8 per lane, int32 accumulate).
+//
+// Semantics (bleeding/v11A1/src/runtime/lancius_scheduler.c:195-220 and
+// lancius_vision_ops.c:16-57 with lancius_kernels.c:177-210):
+//  * the fp activation is quantized per tensor on the fly:
+//      scale = max|x| / 127 (1e-8 when the tensor is all zero),
+//      q = (int8) round(x / scale)   (round half away from zero, in fp64);
+//  * the weight is int8 with its own per-tensor scale (lancius_quantize.c:6-31
+//    for conv filters; any int8 B for MATMUL);
+//  * out = (double) sum_k q_a * q_b (int32) * scale_a * scale_b.
+// The int32 sums are exact, so the device output equals the reference's
+// fp64 value rounded once to fp32.
+//
+// Layouts: both MFMA operands are staged k-contiguous, so one lane's 16
+// int8 are one 16-byte LDS read.  The GEMM quantizes A [M][K] row-major
+// (k-contiguous) and re-lays B [K][N] as B^T [N][K]; the conv quantizes its
+// NCHW input into NHWC with the channels padded to a multiple of 16, and
+// re-lays the OIHW weights as [C_out][(kh, kw, ci)] with the same padding,
+// so a k-run of 16 is 16 channels of one filter tap at one pixel: a single
+// 16-byte gather.  The padded weight bytes are zero, which makes whatever
+// the padded activation bytes hold irrelevant.
+#include <algorithm>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace lancius {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kMaxBlocks = 1024;
+
+// ---- quantization ------------------------------------------------------------
+
+__global__ void __launch_bounds__(kThreads) absmax_partials(float* __restrict__ part, const float* __restrict__ x,
+                                                            size_t n) {
+    __shared__ float s[kThreads];
+    float m = 0.0f;
+    const size_t step = (size_t)gridDim.x * kThreads;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += step) m = fmaxf(m, fabsf(x[i]));
+    s[threadIdx.x] = m;
+    __syncthreads();
+    for (int w = kThreads / 2; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) s[threadIdx.x] = fmaxf(s[threadIdx.x], s[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) part[blockIdx.x] = s[0];
+}
+
+// scale = max|x| / 127, or 1e-8 for an all-zero tensor (fp64, as the
+// reference); also stores the other operand's host-given scale at scale[1]
+// when `other` is >= 0 (one launch for both).
+__global__ void __launch_bounds__(kThreads) absmax_scale(double* __restrict__ scale, const float* __restrict__ part,
+                                                         int count, double other) {
+    __shared__ float s[kThreads];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < count; i += kThreads) m = fmaxf(m, part[i]);
+    s[threadIdx.x] = m;
+    __syncthreads();
+    for (int w = kThreads / 2; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) s[threadIdx.x] = fmaxf(s[threadIdx.x], s[threadIdx.x + w]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        scale[0] = s[0] > 0.0f ? (double)s[0] / 127.0 : 1e-8;
+        if (other >= 0.0) scale[1] = other;
+    }
+}
+
+__device__ __forceinline__ int8_t quant(float v, double scale) { return (int8_t)(int)round((double)v / scale); }
+
+// Row-major copy: q[i] = quant(x[i]).
+__global__ void __launch_bounds__(kThreads) quantize_flat(int8_t* __restrict__ q, const float* __restrict__ x,
+                                                          const double* __restrict__ scale, size_t n) {
+    const double sc = scale[0];
+    const size_t step = (size_t)gridDim.x * kThreads;
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += step) q[i] = quant(x[i], sc);
+}
+
+// NCHW fp32 -> NHWC int8 with Cp >= C channels per pixel (padding bytes 0),
+// through a 64 (channels) x 64 (pixels) LDS tile: reads coalesce along the
+// pixels of a channel plane, writes along the channels of a pixel.
+__global__ void __launch_bounds__(kThreads) quantize_nchw_to_nhwc(int8_t* __restrict__ q, const float* __restrict__ x,
+                                                                  const double* __restrict__ scale, int N, int C,
+                                                                  int HW, int Cp, int tiles_p, int tiles_c) {
+    __shared__ int8_t t[64][65];
+    const int tile = blockIdx.x;
+    const int n = tile / (tiles_p * tiles_c);
+    const int rem = tile - n * tiles_p * tiles_c;
+    const int c0 = (rem / tiles_p) * 64, p0 = (rem % tiles_p) * 64;
+    const double sc = scale[0];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const float* xn = x + (size_t)n * C * HW;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int c = c0 + ty + 4 * i, p = p0 + tx;
+        t[ty + 4 * i][tx] = (c < C && p < HW) ? quant(xn[(size_t)c * HW + p], sc) : (int8_t)0;
+    }
+    __syncthreads();
+    int8_t* qn = q + (size_t)n * HW * Cp;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int p = p0 + ty + 4 * i, c = c0 + tx;
+        if (p < HW && c < Cp) qn[(size_t)p * Cp + c] = t[tx][ty + 4 * i];
+    }
+}
+
+// B [K][N] int8 -> B^T [N][Kp] int8 (k padded with zeros to Kp).
+__global__ void __launch_bounds__(kThreads) transpose_i8(int8_t* __restrict__ bt, const int8_t* __restrict__ b, int K,
+                                                         int N, int Kp, int tiles_n) {
+    __shared__ int8_t t[64][65];
+    const int k0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int k = k0 + ty + 4 * i, n = n0 + tx;
+        t[ty + 4 * i][tx] = (k < K && n < N) ? b[(size_t)k * N + n] : (int8_t)0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int n = n0 + ty + 4 * i, k = k0 + tx;
+        if (n < N && k < Kp) bt[(size_t)n * Kp + k] = t[tx][ty + 4 * i];
+    }
+}
+
+// A [M][K] fp32 -> [M][Kp] int8, zeros past K.  One row per blockIdx.y;
+// with K % 4 == 0 each thread converts a float4 into one 32-bit store.
+__global__ void __launch_bounds__(kThreads) quantize_rows_padded(int8_t* __restrict__ q, const float* __restrict__ x,
+                                                                 const double* __restrict__ scale, size_t M, int K,
+                                                                 int Kp, int vec) {
+    const double sc = scale[0];
+    const int step = gridDim.x * kThreads;
+    for (size_t r = blockIdx.y; r < M; r += gridDim.y) {
+    const float* xr = x + r * K;
+    int8_t* qr = q + r * Kp;
+    if (vec) {
+        for (int k4 = blockIdx.x * kThreads + threadIdx.x; 4 * k4 < Kp; k4 += step) {
+            const int k = 4 * k4;
+            uint32_t packed = 0;
+            if (k < K) {
+                const f32x4 v = *(const f32x4*)(xr + k);
+                packed = (uint32_t)(uint8_t)quant(v.x, sc) | (uint32_t)(uint8_t)quant(v.y, sc) << 8 |
+                         (uint32_t)(uint8_t)quant(v.z, sc) << 16 | (uint32_t)(uint8_t)quant(v.w, sc) << 24;
+            }
+            *(uint32_t*)(qr + k) = packed;
+        }
+    } else {
+        for (int k = blockIdx.x * kThreads + threadIdx.x; k < Kp; k += step)
+            qr[k] = k < K ? quant(xr[k], sc) : (int8_t)0;
+    }
+    }
+}
+
+// OIHW int8 weights -> [C_out][Kp] with k = (kh, kw, ci), Cp channels per
+// tap; zero for ci >= C_in and for k >= KHW * Cp.
+__global__ void __launch_bounds__(kThreads) conv_weights_i8_padded(int8_t* __restrict__ wt,
+                                                                   const int8_t* __restrict__ w, int C_out, int C_in,
+                                                                   int KHW, int Cp, int Kp) {
+    const size_t total = (size_t)C_out * Kp;
+    const size_t step = (size_t)gridDim.x * kThreads;
+    for (size_t d = (size_t)blockIdx.x * kThreads + threadIdx.x; d < total; d += step) {
+        const int k = (int)(d % Kp), co = (int)(d / Kp);
+        const int tap = k / Cp, ci = k - (k / Cp) * Cp;
+        wt[d] = (tap < KHW && ci < C_in) ? w[((size_t)co * C_in + ci) * KHW + tap] : (int8_t)0;
+    }
+}
+
+// ---- int8 GEMM / implicit-GEMM conv on v_mfma_i32_32x32x32_i8 ---------------
+
+struct I8Params {
+    float* C;
+    const int8_t* A;     // [M][Kp] k-contiguous (quantized activation or conv weights)
+    const int8_t* B;     // GEMM: B^T [N][Kp]; conv: NHWC activation with Cp channels
+    const float* bias;   // per output column (GEMM) / channel (conv); may be null
+    const float* R;      // residual (GEMM only); may be null
+    const double* scale_a;  // device scalar
+    const double* scale_b;  // device scalar
+    int M, N, Kp;        // Kp: padded k extent (multiple of the k-tile)
+    int act;
+    uint32_t tiles_m, tiles_n;
+    // conv geometry (CONV == true): N = N_img * Ho * Wo pixels
+    int H, W, Cp, KW, KHW, stride, pad, Ho, Wo, HWo;
+    int out_channels;    // conv: C_out (M) for the NCHW store
+};
+
+// CONV selects the B-operand gather (im2col over NHWC) and the NCHW store;
+// otherwise B rows come from B^T and C is row-major [M][N].
+template <int BM, int BN, bool CONV>
+__global__ void __launch_bounds__(kThreads, 2) gemm_i8_mfma(const I8Params p) {
+    constexpr int BK = 128;  // int8 of k per tile
+    constexpr int LDK = BK + 16;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    __shared__ __attribute__((aligned(16))) int8_t As[2][BM][LDK];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN][LDK];
+
+    const uint32_t ntiles = p.tiles_m * p.tiles_n;
+    uint32_t tm_id, tn_id;
+    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
+    const int m0 = (int)tm_id * BM, n0 = (int)tn_id * BN;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / 2, wn = wave % 2;
+    const int lr = lane & 31, lh = lane >> 5;
+
+    // Each thread moves 16-byte chunks: chunk c of a tile row is k bytes
+    // [16c, 16c+16).  A tile: BM rows x 8 chunks, B tile: BN rows x 8 chunks.
+    constexpr int CH = BK / 16;
+    constexpr int A_LD = BM * CH / kThreads, B_LD = BN * CH / kThreads;
+    static_assert(A_LD * kThreads == BM * CH && B_LD * kThreads == BN * CH, "even split");
+    v4i a_v[A_LD], b_v[B_LD];
+
+    // conv: the pixel of each B row this thread loads (fixed for the k loop)
+    int pix_n[B_LD], pix_h[B_LD], pix_w[B_LD];
+    if constexpr (CONV) {
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            const int row = (tid + i * kThreads) / CH;
+            const int P = n0 + row;
+            if (P < p.N) {
+                const int img = P / p.HWo, rem = P - (P / p.HWo) * p.HWo;
+                const int ho = rem / p.Wo, wo = rem - (rem / p.Wo) * p.Wo;
+                pix_n[i] = img;
+                pix_h[i] = ho * p.stride - p.pad;
+                pix_w[i] = wo * p.stride - p.pad;
+            } else {
+                pix_n[i] = -1;
+                pix_h[i] = pix_w[i] = 0;
+            }
+        }
+    }
+
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) {
+            const int idx = tid + i * kThreads;
+            const int row = idx / CH, ch = idx % CH;
+            const int gm = m0 + row;
+            a_v[i] = gm < p.M ? *(const v4i*)(p.A + (size_t)gm * p.Kp + k0 + 16 * ch) : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            const int idx = tid + i * kThreads;
+            const int row = idx / CH, ch = idx % CH;
+            if constexpr (!CONV) {
+                const int gn = n0 + row;
+                b_v[i] = gn < p.N ? *(const v4i*)(p.B + (size_t)gn * p.Kp + k0 + 16 * ch) : v4i{0, 0, 0, 0};
+            } else {
+                // k = (tap, channel run): 16 channels of one tap at one pixel
+                const int k = k0 + 16 * ch;
+                const int tap = k / p.Cp, c = k - (k / p.Cp) * p.Cp;
+                const int kh = tap / p.KW, kw = tap - (tap / p.KW) * p.KW;
+                const int hi = pix_h[i] + kh, wi = pix_w[i] + kw;
+                const bool in = pix_n[i] >= 0 && tap < p.KHW && hi >= 0 && hi < p.H && wi >= 0 && wi < p.W;
+                b_v[i] = in ? *(const v4i*)(p.B + (((size_t)pix_n[i] * p.H + hi) * p.W + wi) * p.Cp + c)
+                            : v4i{0, 0, 0, 0};
+            }
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) {
+            const int idx = tid + i * kThreads;
+            *(v4i*)&As[buf][idx / CH][16 * (idx % CH)] = a_v[i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            const int idx = tid + i * kThreads;
+            *(v4i*)&Bs[buf][idx / CH][16 * (idx % CH)] = b_v[i];
+        }
+    };
+
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    const int ktiles = p.Kp / BK;
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < ktiles;
+        if (more) load_tile((kt + 1) * BK);
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ++ks) {
+            // lane half h holds k bytes [32ks + 16h, +16) of its row / column
+            v4i af[TM], bf[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) af[i] = *(const v4i*)&As[cur][wm * WM + i * 32 + lr][32 * ks + 16 * lh];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = *(const v4i*)&Bs[cur][wn * WN + j * 32 + lr][32 * ks + 16 * lh];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) store_tile(cur ^ 1);
+        __syncthreads();
+    }
+
+    // int32 -> (double) * scale_a * scale_b -> fp32, then bias / act / residual.
+    // Register r of lane l: row 8(r/4) + 4(l/32) + r%4, column l%32.
+    const double scale = p.scale_a[0] * p.scale_b[0];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lr;
+        if (col >= p.N) continue;
+        float* obase = nullptr;
+        if constexpr (CONV) {
+            const int img = col / p.HWo, pix = col - (col / p.HWo) * p.HWo;
+            obase = p.C + (size_t)img * p.out_channels * p.HWo + pix;
+        }
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int rbase = m0 + wm * WM + i * 32 + 4 * lh;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + 8 * (r >> 2) + (r & 3);
+                if (row >= p.M) continue;
+                float v = (float)((double)acc[i][j][r] * scale);
+                if constexpr (CONV) {
+                    if (p.bias) v += p.bias[row];
+                    obase[(size_t)row * p.HWo] = apply_act(v, p.act);
+                } else {
+                    if (p.bias) v += p.bias[col];
+                    v = apply_act(v, p.act);
+                    const size_t o = (size_t)row * p.N + col;
+                    if (p.R) v += p.R[o];
+                    p.C[o] = v;
+                }
+            }
+        }
+    }
+}
+
+unsigned grid_for(size_t work) {
+    return (unsigned)std::max<size_t>(1, std::min<size_t>((work + kThreads - 1) / kThreads, 4096));
+}
+
+// Per-tensor scale of x into scale_dev (two small launches; max is
+// order-independent, so the result does not depend on the grid).
+int absmax_to_scale(lancius_hip_ctx* ctx, double* scale_dev, float* part, const float* x, size_t n,
+                    double other = -1.0) {
+    const unsigned blocks = (unsigned)std::max<size_t>(1, std::min<size_t>((n + 4095) / 4096, kMaxBlocks));
+    hipLaunchKernelGGL(absmax_partials, dim3(blocks), dim3(kThreads), 0, ctx->stream, part, x, n);
+    if (int rc = check_launch("absmax_partials")) return rc;
+    hipLaunchKernelGGL(absmax_scale, dim3(1), dim3(kThreads), 0, ctx->stream, scale_dev, part, (int)blocks, other);
+    return check_launch("absmax_scale");
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace
+}  // namespace lancius
+
+using namespace lancius;
+
+extern "C" {
+
+int lancius_hip_quantize_i8(lancius_hip_ctx* ctx, int8_t* q, double* scale, const float* x, size_t n) {
+    LANCIUS_REQUIRE(ctx && q && scale && x, LANCIUS_HIP_ERR_NULL_PTR, "quantize_i8: NULL argument");
+    if (int rc = bind_device(ctx)) return rc;
+    void* ws = nullptr;
+    if (int rc = workspace(ctx, kMaxBlocks * sizeof(float), &ws)) return rc;
+    if (int rc = absmax_to_scale(ctx, scale, (float*)ws, x, n)) return rc;
+    if (n == 0) return ok();
+    hipLaunchKernelGGL(quantize_flat, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, q, x, (const double*)scale,
+                       n);
+    return check_launch("quantize_flat");
+}
+
+int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, const int8_t* B, double scale_b,
+                            size_t M, size_t K, size_t N, const float* bias, int act, const float* residual) {
+    LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm_i8: NULL argument");
+    LANCIUS_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1u << 30) && N < (1u << 30) && K < (1u << 30),
+                    LANCIUS_HIP_ERR_SHAPE, "gemm_i8: shape M=%zu K=%zu N=%zu", M, K, N);
+    LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_GELU, LANCIUS_HIP_ERR_UNSUPPORTED,
+                    "gemm_i8: activation %d", act);
+    if (int rc = bind_device(ctx)) return rc;
+    constexpr int BM = 128, BN = 128, BK = 128;
+    const size_t Kp = align_up(K, BK);
+    // workspace: scales (2 doubles) | absmax partials | A_q [M][Kp] | B^T [N][Kp]
+    const size_t off_part = 64, off_a = align_up(off_part + kMaxBlocks * sizeof(float), 256);
+    const size_t off_b = align_up(off_a + M * Kp, 256);
+    const size_t bytes = off_b + N * Kp;
+    LANCIUS_REQUIRE(bytes < ((size_t)1 << 36), LANCIUS_HIP_ERR_SHAPE, "gemm_i8: operands too large");
+    char* ws = nullptr;
+    if (int rc = workspace(ctx, bytes, (void**)&ws)) return rc;
+    double* scales = (double*)ws;
+    int8_t* aq = (int8_t*)(ws + off_a);
+    int8_t* bt = (int8_t*)(ws + off_b);
+    // scale_b is a host value; the kernel reads both scales from device memory
+    LANCIUS_REQUIRE(scale_b >= 0.0, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: negative scale");
+    if (int rc = absmax_to_scale(ctx, scales, (float*)(ws + off_part), A, M * K, scale_b)) return rc;
+    // A_q [M][Kp]: row r holds quant(A[r][k]) for k < K, zeros after
+    const bool vec4 = K % 4 == 0 && ((uintptr_t)A & 15u) == 0;
+    const unsigned row_blocks = (unsigned)std::min<size_t>((Kp / (vec4 ? 4 : 1) + kThreads - 1) / kThreads, 64);
+    hipLaunchKernelGGL(quantize_rows_padded, dim3(row_blocks, (unsigned)std::min<size_t>(M, 65535)), dim3(kThreads),
+                       0, ctx->stream, aq, A, (const double*)scales, M, (int)K, (int)Kp, (int)vec4);
+    if (int rc = check_launch("quantize_rows_padded")) return rc;
+    const int tiles_k = (int)((Kp + 63) / 64), tiles_n = (int)((N + 63) / 64);
+    LANCIUS_REQUIRE((size_t)tiles_k * tiles_n < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: B too large");
+    hipLaunchKernelGGL(transpose_i8, dim3((unsigned)(tiles_k * tiles_n)), dim3(kThreads), 0, ctx->stream, bt, B,
+                       (int)K, (int)N, (int)Kp, tiles_n);
+    if (int rc = check_launch("transpose_i8")) return rc;
+    I8Params p{};
+    p.C = C;
+    p.A = aq;
+    p.B = bt;
+    p.bias = bias;
+    p.R = residual;
+    p.scale_a = scales;
+    p.scale_b = scales + 1;
+    p.M = (int)M;
+    p.N = (int)N;
+    p.Kp = (int)Kp;
+    p.act = act;
+    p.tiles_m = (uint32_t)((M + BM - 1) / BM);
+    p.tiles_n = (uint32_t)((N + BN - 1) / BN);
+    const size_t grid = (size_t)p.tiles_m * p.tiles_n;
+    LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: too many tiles");
+    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, false>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
+    if (int rc = check_launch("gemm_i8_mfma")) return rc;
+    return ok();
+}
+
+int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in, const int8_t* w, double scale_w,
+                              const float* bias, size_t N, size_t C_in, size_t H, size_t W, size_t C_out, size_t K_h,
+                              size_t K_w, size_t stride, size_t pad, int act) {
+    LANCIUS_REQUIRE(ctx && out && in && w, LANCIUS_HIP_ERR_NULL_PTR, "conv2d_i8: NULL argument");
+    LANCIUS_REQUIRE(N && C_in && H && W && C_out && K_h && K_w && stride, LANCIUS_HIP_ERR_SHAPE,
+                    "conv2d_i8: empty shape");
+    LANCIUS_REQUIRE(H + 2 * pad >= K_h && W + 2 * pad >= K_w, LANCIUS_HIP_ERR_SHAPE,
+                    "conv2d_i8: spatial dimensions underflow");
+    LANCIUS_REQUIRE(act == LANCIUS_HIP_ACT_NONE || act == LANCIUS_HIP_ACT_RELU, LANCIUS_HIP_ERR_UNSUPPORTED,
+                    "conv2d_i8: activation %d", act);
+    const size_t Cp = align_up(C_in, 16);
+    const size_t KHW = K_h * K_w;
+    const size_t Kp = align_up(KHW * Cp, 128);
+    const size_t Ho = (H + 2 * pad - K_h) / stride + 1, Wo = (W + 2 * pad - K_w) / stride + 1;
+    const size_t P = N * Ho * Wo;
+    LANCIUS_REQUIRE(Kp < (1u << 30) && P < (1u << 31) && N * H * W * Cp < ((size_t)1 << 40) && C_out < (1u << 30),
+                    LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: shape too large");
+    if (int rc = bind_device(ctx)) return rc;
+    // workspace: scales | partials | weights [C_out][Kp] | NHWC activation (+16 B tail)
+    const size_t off_part = 64, off_w = align_up(off_part + kMaxBlocks * sizeof(float), 256);
+    const size_t off_x = align_up(off_w + C_out * Kp, 256);
+    const size_t bytes = off_x + N * H * W * Cp + 16;
+    char* ws = nullptr;
+    if (int rc = workspace(ctx, bytes, (void**)&ws)) return rc;
+    double* scales = (double*)ws;
+    int8_t* wq = (int8_t*)(ws + off_w);
+    int8_t* xq = (int8_t*)(ws + off_x);
+    LANCIUS_REQUIRE(scale_w >= 0.0, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: negative scale");
+    if (int rc = absmax_to_scale(ctx, scales, (float*)(ws + off_part), in, N * C_in * H * W, scale_w)) return rc;
+    const int HW = (int)(H * W);
+    const int tiles_p = (HW + 63) / 64, tiles_c = (int)((Cp + 63) / 64);
+    LANCIUS_REQUIRE((size_t)N * tiles_p * tiles_c < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: input too large");
+    hipLaunchKernelGGL(quantize_nchw_to_nhwc, dim3((unsigned)(N * tiles_p * tiles_c)), dim3(kThreads), 0, ctx->stream,
+                       xq, in, (const double*)scales, (int)N, (int)C_in, HW, (int)Cp, tiles_p, tiles_c);
+    if (int rc = check_launch("quantize_nchw_to_nhwc")) return rc;
+    // weights re-laid k = (kh, kw, ci) and zero-padded to Kp
+    hipLaunchKernelGGL(conv_weights_i8_padded, dim3(grid_for(C_out * Kp)), dim3(kThreads), 0, ctx->stream, wq, w,
+                       (int)C_out, (int)C_in, (int)KHW, (int)Cp, (int)Kp);
+    if (int rc = check_launch("conv_weights_i8")) return rc;
+    constexpr int BM = 128, BN = 128;
+    I8Params p{};
+    p.C = out;
+    p.A = wq;
+    p.B = xq;
+    p.bias = bias;
+    p.scale_a = scales + 1;
+    p.scale_b = scales;
+    p.M = (int)C_out;
+    p.N = (int)P;
+    p.Kp = (int)Kp;
+    p.act = act;
+    p.H = (int)H;
+    p.W = (int)W;
+    p.Cp = (int)Cp;
+    p.KW = (int)K_w;
+    p.KHW = (int)KHW;
+    p.stride = (int)stride;
+    p.pad = (int)pad;
+    p.Ho = (int)Ho;
+    p.Wo = (int)Wo;
+    p.HWo = (int)(Ho * Wo);
+    p.out_channels = (int)C_out;
+    p.tiles_m = (uint32_t)((C_out + BM - 1) / BM);
+    p.tiles_n = (uint32_t)((P + BN - 1) / BN);
+    const size_t grid = (size_t)p.tiles_m * p.tiles_n;
+    LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: too many tiles");
+    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, true>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
+    return check_launch("conv2d_i8_mfma");
+}
+
+}  // extern "C"

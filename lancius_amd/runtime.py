@@ -76,6 +76,9 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_copy_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_broadcast_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.lancius_hip_fill_f32.argtypes = [vp, vp, f32, sz]
+    lib.lancius_hip_quantize_i8.argtypes = [vp, vp, vp, vp, sz]
+    lib.lancius_hip_gemm_i8_f32.argtypes = [vp, vp, vp, vp, C.c_double, sz, sz, sz, vp, i32, vp]
+    lib.lancius_hip_conv2d_i8_f32.argtypes = [vp, vp, vp, vp, C.c_double, vp] + [sz] * 9 + [i32]
     lib.lancius_hip_gemm_ex_f32.argtypes = [vp, vp, vp, vp, sz, sz, sz, i32, i32, vp, i32, vp]
     lib.lancius_hip_gemm_grouped_ex_f32.argtypes = [vp, sz, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), sz, sz, sz,
                                                     i32, i32, C.POINTER(vp), i32, C.POINTER(vp)]
@@ -296,6 +299,20 @@ class Device:
     def fill(self, out, value, n) -> None:
         _check(self.lib.lancius_hip_fill_f32(self.ctx, _vp(out), float(value), n))
 
+    # -- int8 path -------------------------------------------------------------
+    def quantize_i8(self, q, scale, x, n) -> None:
+        """q (int8 device buffer), scale (device buffer of one double)."""
+        _check(self.lib.lancius_hip_quantize_i8(self.ctx, _vp(q), _vp(scale), _vp(x), n))
+
+    def gemm_i8(self, C_, A, B_i8, scale_b, M, K, N, bias=None, act=ACT_NONE, residual=None) -> None:
+        _check(self.lib.lancius_hip_gemm_i8_f32(self.ctx, _vp(C_), _vp(A), _vp(B_i8), float(scale_b), M, K, N,
+                                                _vp(bias), act, _vp(residual)))
+
+    def conv2d_i8(self, out, x, w_i8, scale_w, bias, N, C_in, H, W, C_out, K_h, K_w, stride, pad,
+                  act=ACT_NONE) -> None:
+        _check(self.lib.lancius_hip_conv2d_i8_f32(self.ctx, _vp(out), _vp(x), _vp(w_i8), float(scale_w), _vp(bias),
+                                                  N, C_in, H, W, C_out, K_h, K_w, stride, pad, act))
+
     # -- training / reduction ops ----------------------------------------------
     def sub(self, out, a, b, n) -> None:
         _check(self.lib.lancius_hip_sub_f32(self.ctx, _vp(out), _vp(a), _vp(b), n))
@@ -367,9 +384,10 @@ class DeviceProgram:
 
     def upload(self, node: abi.NodeP, arr: np.ndarray) -> None:
         arr = np.ascontiguousarray(arr)
-        dt = abi.DTYPE_FP32 if arr.dtype == np.float32 else abi.DTYPE_FP64
-        if arr.dtype not in (np.float32, np.float64):
-            raise TypeError("upload takes float32 or float64")
+        dt = {np.dtype(np.float32): abi.DTYPE_FP32, np.dtype(np.float64): abi.DTYPE_FP64,
+              np.dtype(np.int8): abi.DTYPE_INT8}.get(arr.dtype)
+        if dt is None:
+            raise TypeError("upload takes float32, float64 or int8 (quantized weights)")
         if arr.size != abi.node_elems(node):
             raise ValueError(f"node has {abi.node_elems(node)} elements, array {arr.size}")
         _check(self.lib.lancius_device_upload(self.prog, node, arr.ctypes.data_as(C.c_void_p), dt))

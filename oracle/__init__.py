@@ -61,6 +61,13 @@ def lib() -> C.CDLL:
         L.oracle_conv2d_bwd_weight.argtypes = [_D, _D, _D] + [sz] * 11
         L.oracle_maxpool2d.argtypes = [_D, _D] + [sz] * 6
         L.oracle_maxpool2d_bwd.argtypes = [_D, _D, _D] + [sz] * 8
+        I8 = C.POINTER(C.c_int8)
+        L.oracle_quantize_i8.argtypes = [I8, _D, sz]
+        L.oracle_quantize_i8.restype = C.c_double
+        L.oracle_matmul_i8.argtypes = [_D, _D, I8, C.c_double, sz, sz, sz]
+        L.oracle_matmul_i8.restype = C.c_int
+        L.oracle_conv2d_i8.argtypes = [_D, _D, I8, C.c_double] + [sz] * 9 + [C.c_int]
+        L.oracle_conv2d_i8.restype = C.c_int
         for name in ("oracle_matmul_rows", "oracle_conv2d", "oracle_attention", "oracle_layernorm", "oracle_gelu",
                      "oracle_softmax", "oracle_argmax", "oracle_add", "oracle_relu", "oracle_broadcast",
                      "oracle_sub", "oracle_mul", "oracle_relu_bwd", "oracle_transpose", "oracle_sum",
@@ -93,6 +100,11 @@ def ref_lib() -> C.CDLL | None:
         L.kernel_layernorm.argtypes = [_D, _D, _D, _D, sz, sz, C.c_double]
         L.kernel_gelu.argtypes = [_D, _D, sz]
         L.kernel_attention.argtypes = [_D, _D, _D, _D, sz, sz, sz]
+        L.lancius_quantize_graph.argtypes = [abi.GraphP]
+        L.lancius_quantize_graph.restype = None
+        L.kernel_conv2d_int8_fwd.argtypes = [_D, C.POINTER(C.c_int8), C.POINTER(C.c_int8), C.c_double,
+                                             C.c_double] + [sz] * 9
+        L.kernel_conv2d_int8_fwd.restype = None
         L.kernel_conv2d_bwd_in.argtypes = [_D, _D, _D] + [sz] * 11
         L.kernel_conv2d_bwd_w.argtypes = [_D, _D, _D] + [sz] * 11
         for name in ("kernel_matmul", "kernel_conv2d_fwd", "kernel_conv2d_relu_fwd", "kernel_layernorm",
@@ -300,6 +312,39 @@ def maxpool2d_bwd(dy, x, K, stride) -> np.ndarray:
     N, Cc, H, W = x.shape
     out = np.empty_like(x)
     lib().oracle_maxpool2d_bwd(_p(out), _p(dy), _p(x), N, Cc, H, W, dy.shape[2], dy.shape[3], K, stride)
+    return out
+
+
+def _i8(a):
+    return a.ctypes.data_as(C.POINTER(C.c_int8))
+
+
+def quantize_i8(x) -> tuple[np.ndarray, float]:
+    """(int8 values, scale) of the per-tensor quantization."""
+    x = _d(x)
+    q = np.empty(x.shape, np.int8)
+    s = lib().oracle_quantize_i8(_i8(q), _p(x), x.size)
+    return q, float(s)
+
+
+def matmul_i8(a, b_i8, scale_b: float) -> np.ndarray:
+    a = _d(a)
+    b_i8 = np.ascontiguousarray(b_i8, dtype=np.int8)
+    M, K = a.shape
+    N = b_i8.shape[1]
+    out = np.empty((M, N))
+    assert lib().oracle_matmul_i8(_p(out), _p(a), _i8(b_i8), float(scale_b), M, K, N) == 0
+    return out
+
+
+def conv2d_i8(x, w_i8, scale_w: float, stride=1, pad=0, relu=False) -> np.ndarray:
+    x = _d(x)
+    w_i8 = np.ascontiguousarray(w_i8, dtype=np.int8)
+    N, C_in, H, W = x.shape
+    C_out, _, KH, KW = w_i8.shape
+    out = np.empty((N, C_out, (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1))
+    assert lib().oracle_conv2d_i8(_p(out), _p(x), _i8(w_i8), float(scale_w), N, C_in, H, W, C_out, KH, KW, stride,
+                                  pad, int(relu)) == 0
     return out
 
 

@@ -387,6 +387,70 @@ void oracle_maxpool2d_bwd(double* dx, const double* dy, const double* x, size_t 
             }
 }
 
+/* ---- the int8 path --------------------------------------------------------------- */
+
+/* Per-tensor quantization: B/src/runtime/lancius_scheduler.c:199-204 (MATMUL
+ * activation), B/src/runtime/lancius_vision_ops.c:28-36 (conv activation),
+ * B/src/compiler/lancius_quantize.c:14-25 (conv filters).  Returns the scale. */
+double oracle_quantize_i8(int8_t* q, const double* x, size_t n) {
+    double m = 0.0;
+    for (size_t i = 0; i < n; i++) {
+        const double a = fabs(x[i]);
+        if (a > m) m = a;
+    }
+    const double scale = m > 0.0 ? m / 127.0 : 1e-8;
+    for (size_t i = 0; i < n; i++) q[i] = (int8_t)round(x[i] / scale);
+    return scale;
+}
+
+/* B/src/runtime/lancius_scheduler.c:195-220: quantized A times int8 B,
+ * int32 sums scaled by scale_a * scale_b. */
+int oracle_matmul_i8(double* out, const double* a, const int8_t* b, double scale_b, size_t M, size_t K, size_t N) {
+    int8_t* qa = (int8_t*)malloc(M * K ? M * K : 1);
+    if (!qa) return -1;
+    const double scale = oracle_quantize_i8(qa, a, M * K) * scale_b;
+    for (size_t r = 0; r < M; r++)
+        for (size_t c = 0; c < N; c++) {
+            int32_t s = 0;
+            for (size_t k = 0; k < K; k++) s += (int32_t)qa[r * K + k] * (int32_t)b[k * N + c];
+            out[r * N + c] = (double)s * scale;
+        }
+    free(qa);
+    return 0;
+}
+
+/* B/src/math/lancius_kernels.c:177-210 on the activation quantized as
+ * B/src/runtime/lancius_vision_ops.c:28-36 does, then the fused ReLU of :49-54. */
+int oracle_conv2d_i8(double* out, const double* in, const int8_t* w, double scale_w, size_t N, size_t C_in, size_t H,
+                     size_t W, size_t C_out, size_t K_h, size_t K_w, size_t stride, size_t pad, int relu) {
+    const size_t n_in = N * C_in * H * W;
+    int8_t* q = (int8_t*)malloc(n_in ? n_in : 1);
+    if (!q) return -1;
+    const double scale = oracle_quantize_i8(q, in, n_in) * scale_w;
+    const size_t Ho = (H + 2 * pad - K_h) / stride + 1, Wo = (W + 2 * pad - K_w) / stride + 1;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (size_t n = 0; n < N; n++)
+        for (size_t co = 0; co < C_out; co++)
+            for (size_t ho = 0; ho < Ho; ho++)
+                for (size_t wo = 0; wo < Wo; wo++) {
+                    int32_t s = 0;
+                    for (size_t ci = 0; ci < C_in; ci++)
+                        for (size_t kh = 0; kh < K_h; kh++)
+                            for (size_t kw = 0; kw < K_w; kw++) {
+                                const long ih = (long)(ho * stride) - (long)pad + (long)kh;
+                                const long iw = (long)(wo * stride) - (long)pad + (long)kw;
+                                if (ih < 0 || ih >= (long)H || iw < 0 || iw >= (long)W) continue;
+                                s += (int32_t)q[((n * C_in + ci) * H + (size_t)ih) * W + (size_t)iw] *
+                                     (int32_t)w[((co * C_in + ci) * K_h + kh) * K_w + kw];
+                            }
+                    double v = (double)s * scale;
+                    if (relu && v < 0.0) v = 0.0;
+                    out[((n * C_out + co) * Ho + ho) * Wo + wo] = v;
+                }
+    free(q);
+    return 0;
+}
+
 /* ---- fp64 graph executor ------------------------------------------------------ */
 
 static size_t elems_of(const lancius_node* n) {
@@ -420,6 +484,8 @@ static int run_node(lancius_node* n) {
         case LANCIUS_OP_MATMUL: {
             const size_t M = in[0]->shape[0], K = in[0]->shape[1], N = in[1]->shape[1];
             if (M * N > e) return -3;
+            if (in[1]->runtime_data_int8) /* the int8 branch (lancius_scheduler.c:195) */
+                return oracle_matmul_i8(y, in[0]->runtime_data, in[1]->runtime_data_int8, in[1]->scale, M, K, N);
             oracle_matmul_rows(y, in[0]->runtime_data, in[1]->runtime_data, M, K, N, 0, M);
             return 0;
         }
@@ -450,6 +516,10 @@ static int run_node(lancius_node* n) {
         case LANCIUS_OP_CONV2D_RELU_FUSED: {
             const lancius_node* x = in[0];
             const lancius_node* w = in[1];
+            if (w->dtype == LANCIUS_DTYPE_INT8) /* lancius_vision_ops.c:14-16 */
+                return oracle_conv2d_i8(y, x->runtime_data, w->runtime_data_int8, w->scale, x->shape[0], x->shape[1],
+                                        x->shape[2], x->shape[3], w->shape[0], w->shape[2], w->shape[3], n->stride,
+                                        n->pad, n->op == LANCIUS_OP_CONV2D_RELU_FUSED);
             oracle_conv2d(y, x->runtime_data, w->runtime_data, x->shape[0], x->shape[1], x->shape[2], x->shape[3],
                           w->shape[0], w->shape[2], w->shape[3], n->stride, n->pad,
                           n->op == LANCIUS_OP_CONV2D_RELU_FUSED, 0, x->shape[0]);

@@ -31,6 +31,11 @@
  *                         golden vectors of kernel_conv2d_bwd_in/_w; adjoint
  *                         identities <conv(x,w), g> = <x, bwd_in(g,w)> =
  *                         <w, bwd_w(g,x)>; finite differences
+ *   oracle_quantize_i8/matmul_i8/conv2d_i8
+ *                         golden vectors of the compiled reference's int8
+ *                         MATMUL branch and int8 conv route; int32 sums
+ *                         equal to exact integer products (numpy int64);
+ *                         quantization bounds |q| <= 127, q = round(x/s)
  *   oracle_schedule_execute
  *                         golden sink values of reference graph runs,
  *                         including autodiff training graphs
@@ -94,6 +99,14 @@ void oracle_maxpool2d(double* out, const double* in, size_t N, size_t C, size_t 
                       size_t stride);
 void oracle_maxpool2d_bwd(double* dx, const double* dy, const double* x, size_t N, size_t C, size_t H, size_t W,
                           size_t Ho, size_t Wo, size_t K, size_t stride);
+
+/* The int8 path (B/src/runtime/lancius_scheduler.c:195-220,
+ * B/src/math/lancius_kernels.c:177-210, B/src/runtime/lancius_vision_ops.c:16-57,
+ * B/src/compiler/lancius_quantize.c:6-33).  0, or -1 on allocation failure. */
+double oracle_quantize_i8(int8_t* q, const double* x, size_t n);
+int oracle_matmul_i8(double* out, const double* a, const int8_t* b, double scale_b, size_t M, size_t K, size_t N);
+int oracle_conv2d_i8(double* out, const double* in, const int8_t* w, double scale_w, size_t N, size_t C_in, size_t H,
+                     size_t W, size_t C_out, size_t K_h, size_t K_w, size_t stride, size_t pad, int relu);
 
 /* fp64 CPU execution of a scheduled graph, node by node in wave order, the
  * way the reference's scratch-arena executor does it

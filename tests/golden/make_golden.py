@@ -156,6 +156,7 @@ def main() -> None:
     k["softmax_out"] = run_ref_graph(ref, bg, {"a": k["softmax_x"]})["sm"]
     bg.destroy()
     training_op_vectors(ref, k)
+    int8_vectors(ref, k)
     np.savez_compressed(OUT / "kernels.npz", **k)
 
     # schedules and plans
@@ -307,6 +308,67 @@ def training_op_vectors(ref, k: dict) -> None:
         k[f"pool_{tag}_dx"] = ref_op(ref, {"g": (2, 3, Ho, Wo), "x": (2, 3, 9, 7)},
                                      lambda g, i: ref.lancius_maxpool2d_bwd(g, i["g"], i["x"], K, st),
                                      {"g": gp, "x": xp})
+
+
+def int8_vectors(ref, k: dict) -> None:
+    """Golden vectors of the int8 path: the int8 MATMUL branch
+    (lancius_scheduler.c:195-220), lancius_quantize_graph + the int8 conv route
+    (lancius_quantize.c, lancius_vision_ops.c:16-57, also fused with ReLU),
+    and kernel_conv2d_int8_fwd on given int8 tensors."""
+    I8 = C.POINTER(C.c_int8)
+    # MATMUL with an int8 B (its scale set on the node, as a loader would)
+    M, K, N = 9, 37, 11
+    a = f32(prng.normal(30, (M, K), std=1.5))
+    a[0, 0] = 0.5 * float(np.max(np.abs(a)))  # exact .5 quotients appear in rows
+    bq = (np.round(prng.uniform(31, (K, N), -127.4, 127.4))).astype(np.int8)
+    scale_b = 0.0173
+    bg = graphs.BuiltGraph(ref, ref.lancius_graph_create())
+    na = graphs._inp(bg, "a", M, K)
+    nb = graphs._inp(bg, "b", K, N)
+    bg.nodes["out"] = ref.lancius_matmul(bg.g, na, nb)
+    bg.outputs = ["out"]
+    nb.contents.runtime_data_int8 = bq.ctypes.data_as(I8)
+    nb.contents.scale = scale_b
+    k["i8mm_a"], k["i8mm_bq"], k["i8mm_scale_b"] = a, bq, np.array(scale_b)
+    k["i8mm_out"] = run_ref_graph(ref, bg, {"a": a, "b": bq.astype(np.float64) * scale_b})["out"]
+    nb.contents.runtime_data_int8 = None
+    bg.destroy()
+    # conv through lancius_quantize_graph, unfused and fused with ReLU
+    for tag, fuse in (("i8conv", False), ("i8conv_relu", True)):
+        x = f32(prng.normal(32, (2, 5, 9, 8)))
+        w = f32(prng.normal(33, (6, 5, 3, 3), std=0.3))
+        bg = graphs.BuiltGraph(ref, ref.lancius_graph_create())
+        nx = graphs._inp(bg, "x", 2, 5, 9, 8)
+        nw = graphs._inp(bg, "w", 6, 5, 3, 3)
+        conv = ref.lancius_conv2d(bg.g, nx, nw, 1, 1)
+        bg.nodes["out"] = ref.lancius_relu(bg.g, conv) if fuse else conv
+        if fuse:
+            ref.lancius_optimize_fusion(bg.g)
+        bg.outputs = ["out"]
+        keep = [np.ascontiguousarray(x), np.ascontiguousarray(w)]
+        nx.contents.runtime_data = p(keep[0])
+        nw.contents.runtime_data = p(keep[1])
+        ref.lancius_quantize_graph(bg.g)
+        wq = np.ctypeslib.as_array(nw.contents.runtime_data_int8, shape=(w.size,)).copy().reshape(w.shape)
+        k[f"{tag}_x"], k[f"{tag}_w"], k[f"{tag}_wq"] = x, w, wq
+        k[f"{tag}_scale_w"] = np.array(nw.contents.scale)
+        sched = ref.lancius_ir_schedule(bg.g)
+        arena = ref.lancius_arena_create(64 << 20)
+        ref.lancius_schedule_execute(sched, arena)
+        n = bg.node("out")
+        k[f"{tag}_out"] = np.ctypeslib.as_array(n.contents.runtime_data, shape=(abi.node_elems(n),)).copy().reshape(
+            abi.node_shape(n))
+        ref.lancius_schedule_destroy(sched)
+        ref.lancius_arena_destroy(arena)
+        bg.destroy()  # frees the reference's int8 copies
+    # kernel_conv2d_int8_fwd on given int8 tensors, stride 2 pad 2
+    xq = np.round(prng.uniform(34, (1, 3, 11, 10), -127.4, 127.4)).astype(np.int8)
+    xq.flat[0] = 127  # so that re-quantizing xq * 0.01 returns xq
+    wq = np.round(prng.uniform(35, (4, 3, 5, 5), -127.4, 127.4)).astype(np.int8)
+    out = np.zeros((1, 4, 6, 5))
+    ref.kernel_conv2d_int8_fwd(p(out), xq.ctypes.data_as(I8), wq.ctypes.data_as(I8), 0.01, 0.002,
+                               1, 3, 11, 10, 4, 5, 5, 2, 2)
+    k["i8k_xq"], k["i8k_wq"], k["i8k_out"] = xq, wq, out
 
 
 TRAIN_GRAPHS = {

@@ -1,0 +1,196 @@
+"""The int8 path on the device (C ABI and the executor) against the oracle and
+the compiled reference's golden outputs.
+
+The int32 sums are exact and the quantizer runs in fp64 like the reference,
+so int8 values must match bit for bit and every output equals the
+reference's fp64 value rounded once to fp32 (normwise error <= 1e-6, the
+fp32 rounding plus the fp32 epilogue).
+"""
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from lancius_amd import ACT_NONE, ACT_RELU, DeviceProgram, abi, graph_lib, graphs, prng
+from tests.conftest import case
+
+pytestmark = pytest.mark.gpu
+
+K = np.load(Path(__file__).resolve().parent / "golden" / "kernels.npz")
+TOL = 1e-6
+
+
+def f64(a):
+    return np.asarray(a, np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 1_000_003])
+def test_quantize_bit_exact(dev, n):
+    x = prng.normal(70 + n % 13, (n,), std=3.0)
+    dx, dq, ds = dev.upload(x), dev.alloc(n), dev.alloc(8)
+    case(f"quantize_i8 n={n}")
+    dev.quantize_i8(dq, ds, dx, n)
+    q = dev.download(dq, (n,), np.int8)
+    s = float(dev.download(ds, (1,), np.float64)[0])
+    rq, rs = oracle.quantize_i8(f64(x))
+    assert s == rs
+    np.testing.assert_array_equal(q, rq)
+    for b in (dx, dq, ds):
+        b.free()
+
+
+def test_quantize_all_zero(dev):
+    dx, dq, ds = dev.upload(np.zeros(100, np.float32)), dev.alloc(100), dev.alloc(8)
+    case("quantize_i8 zeros")
+    dev.quantize_i8(dq, ds, dx, 100)
+    assert float(dev.download(ds, (1,), np.float64)[0]) == 1e-8
+    assert not dev.download(dq, (100,), np.int8).any()
+    for b in (dx, dq, ds):
+        b.free()
+
+
+def _gemm_i8(dev, a, bq, sb, bias=None, act=ACT_NONE, res=None):
+    M, Kd = a.shape
+    N = bq.shape[1]
+    da, db, dc = dev.upload(a), dev.upload(bq), dev.alloc(4 * M * N)
+    dbias = dev.upload(bias) if bias is not None else None
+    dres = dev.upload(res) if res is not None else None
+    case(f"gemm_i8 M={M} K={Kd} N={N}")
+    dev.gemm_i8(dc, da, db, sb, M, Kd, N, bias=dbias, act=act, residual=dres)
+    got = dev.download(dc, (M, N))
+    for b in (da, db, dc, dbias, dres):
+        if b is not None:
+            b.free()
+    return got
+
+
+def test_gemm_i8_golden(dev):
+    got = _gemm_i8(dev, K["i8mm_a"].astype(np.float32), K["i8mm_bq"], float(K["i8mm_scale_b"]))
+    assert oracle.normwise_error(got, K["i8mm_out"]) <= TOL
+
+
+@pytest.mark.parametrize("M,Kd,N", [(1, 1, 1), (64, 784, 128), (130, 70, 201), (257, 300, 129), (1024, 1024, 1024),
+                                    (33, 4096, 50)])
+def test_gemm_i8_shapes(dev, M, Kd, N):
+    a = prng.normal(80 + M, (M, Kd))
+    bq = np.round(prng.uniform(81 + N, (Kd, N), -127.4, 127.4)).astype(np.int8)
+    got = _gemm_i8(dev, a, bq, 0.0123)
+    assert oracle.normwise_error(got, oracle.matmul_i8(f64(a), bq, 0.0123)) <= TOL
+
+
+def test_gemm_i8_epilogue(dev):
+    M, Kd, N = 96, 200, 72
+    a = prng.normal(90, (M, Kd))
+    bq = np.round(prng.uniform(91, (Kd, N), -127.4, 127.4)).astype(np.int8)
+    bias, res = prng.normal(92, (N,)), prng.normal(93, (M, N))
+    got = _gemm_i8(dev, a, bq, 0.004, bias=bias, act=ACT_RELU, res=res)
+    ref = np.maximum(oracle.matmul_i8(f64(a), bq, 0.004) + f64(bias)[None, :], 0.0) + f64(res)
+    assert oracle.normwise_error(got, ref) <= TOL
+
+
+def _conv_i8(dev, x, wq, sw, stride, pad, act=ACT_NONE):
+    N, Ci, H, W = x.shape
+    Co, _, KH, KW = wq.shape
+    Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    dx, dw, do = dev.upload(x.astype(np.float32)), dev.upload(wq), dev.alloc(4 * N * Co * Ho * Wo)
+    case(f"conv2d_i8 N={N} Ci={Ci} {H}x{W} Co={Co} K={KH}x{KW} s={stride} p={pad}")
+    dev.conv2d_i8(do, dx, dw, sw, None, N, Ci, H, W, Co, KH, KW, stride, pad, act)
+    got = dev.download(do, (N, Co, Ho, Wo))
+    for b in (dx, dw, do):
+        b.free()
+    return got
+
+
+def test_conv_i8_golden(dev):
+    for tag, act in (("i8conv", ACT_NONE), ("i8conv_relu", ACT_RELU)):
+        got = _conv_i8(dev, K[f"{tag}_x"], K[f"{tag}_wq"], float(K[f"{tag}_scale_w"]), 1, 1, act)
+        assert oracle.normwise_error(got, K[f"{tag}_out"]) <= TOL, tag
+    got = _conv_i8(dev, K["i8k_xq"].astype(np.float64) * 0.01, K["i8k_wq"], 0.002, 2, 2)
+    assert oracle.normwise_error(got, K["i8k_out"]) <= TOL
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 32, 32, 16, 5, 5, 1, 2), (4, 16, 16, 16, 32, 5, 5, 1, 2),
+                                   (2, 64, 28, 28, 128, 3, 3, 1, 1), (1, 20, 13, 11, 7, 3, 3, 2, 0),
+                                   (3, 8, 9, 9, 5, 1, 1, 1, 0), (1, 130, 7, 7, 33, 3, 3, 1, 1)])
+def test_conv_i8_shapes(dev, shape):
+    N, Ci, H, W, Co, KH, KW, st, pd = shape
+    x = prng.normal(100 + sum(shape), (N, Ci, H, W))
+    wq = np.round(prng.uniform(101 + sum(shape), (Co, Ci, KH, KW), -127.4, 127.4)).astype(np.int8)
+    got = _conv_i8(dev, x, wq, 0.003, st, pd)
+    assert oracle.normwise_error(got, oracle.conv2d_i8(f64(x), wq, 0.003, st, pd)) <= TOL
+
+
+# ---- through the device executor ------------------------------------------------------
+
+
+def test_int8_conv_graph_on_device(dev):
+    """lancius_quantize_graph + the executor: the filter uploads as int8, the
+    image (also quantized by the pass, as in the reference) stays an fp32
+    activation quantized by the conv itself."""
+    lib = graph_lib()
+    for tag, fuse in (("i8conv", False), ("i8conv_relu", True)):
+        bg = graphs.BuiltGraph(lib, lib.lancius_graph_create())
+        nx = graphs._inp(bg, "x", 2, 5, 9, 8)
+        nw = graphs._inp(bg, "w", 6, 5, 3, 3)
+        conv = lib.lancius_conv2d(bg.g, nx, nw, 1, 1)
+        out = lib.lancius_relu(bg.g, conv) if fuse else conv
+        if fuse:
+            lib.lancius_optimize_fusion(bg.g)
+        keep = [np.ascontiguousarray(K[f"{tag}_x"]), np.ascontiguousarray(K[f"{tag}_w"])]
+        nx.contents.runtime_data = keep[0].ctypes.data_as(C.POINTER(C.c_double))
+        nw.contents.runtime_data = keep[1].ctypes.data_as(C.POINTER(C.c_double))
+        lib.lancius_quantize_graph(bg.g)
+        wq = np.ctypeslib.as_array(nw.contents.runtime_data_int8, shape=(keep[1].size,)).copy()
+        np.testing.assert_array_equal(wq.reshape(K[f"{tag}_wq"].shape), K[f"{tag}_wq"])
+        lib.lancius_graph_set_dtype(bg.g, abi.DTYPE_FP32)
+        assert nw.contents.dtype == abi.DTYPE_INT8  # quantized weights keep their dtype
+        sched = lib.lancius_ir_schedule(bg.g)
+        plan = lib.lancius_build_memory_plan(sched, bg.g)
+        case(f"int8 conv graph {tag}")
+        prog = DeviceProgram(dev, bg.g, sched, plan)
+        prog.upload(nx, K[f"{tag}_x"].astype(np.float32))
+        prog.upload(nw, wq)
+        with pytest.raises(TypeError):
+            prog.upload(nw, np.zeros(3, np.int32))
+        prog.run()
+        got = prog.download(out)
+        assert oracle.normwise_error(got, K[f"{tag}_out"]) <= TOL, tag
+        prog.close()
+        lib.lancius_memory_plan_destroy(plan)
+        lib.lancius_schedule_destroy(sched)
+        nx.contents.runtime_data = None
+        nw.contents.runtime_data = None
+        bg.destroy()
+
+
+def test_int8_matmul_drop_in(dev):
+    """lancius_schedule_execute_device on a MATMUL whose B carries an int8
+    copy and scale (lancius_scheduler.c:192-195): the int8 bytes upload, the
+    result comes back to runtime_data."""
+    lib = graph_lib()
+    a, bq, sb = K["i8mm_a"], K["i8mm_bq"], float(K["i8mm_scale_b"])
+    g = lib.lancius_graph_create()
+    na, nb = lib.lancius_input(g, *a.shape), lib.lancius_input(g, *bq.shape)
+    mm = lib.lancius_matmul(g, na, nb)
+    keep = [np.ascontiguousarray(a), np.ascontiguousarray(bq.astype(np.float64) * sb), np.ascontiguousarray(bq)]
+    na.contents.runtime_data = keep[0].ctypes.data_as(C.POINTER(C.c_double))
+    nb.contents.runtime_data = keep[1].ctypes.data_as(C.POINTER(C.c_double))
+    nb.contents.runtime_data_int8 = keep[2].ctypes.data_as(C.POINTER(C.c_int8))
+    nb.contents.scale = sb
+    sched = lib.lancius_ir_schedule(g)
+    case("int8 matmul drop-in")
+    rc = dev.lib.lancius_schedule_execute_device(sched, g, dev.ctx)
+    assert rc == 0, dev.lib.lancius_hip_last_error()
+    got = np.ctypeslib.as_array(mm.contents.runtime_data, shape=(a.shape[0] * bq.shape[1],)).copy()
+    assert oracle.normwise_error(got, K["i8mm_out"].ravel()) <= TOL
+    import ctypes.util
+
+    libc = C.CDLL(ctypes.util.find_library("c"))
+    libc.free(C.c_void_p(C.addressof(mm.contents.runtime_data.contents)))
+    mm.contents.runtime_data = None
+    na.contents.runtime_data = nb.contents.runtime_data = None
+    nb.contents.runtime_data_int8 = None
+    lib.lancius_schedule_destroy(sched)
+    lib.lancius_graph_destroy(g)
