@@ -107,6 +107,58 @@ def conv_case(dev, steps, warmup):
     return ms, flops, 4.0 * (N * C_in * H * W + C_out * C_in * 9 + N * C_out * H * W)
 
 
+def decode_cases(dev, steps, warmup) -> dict:
+    """Decode-side family at LLM shapes: split-KV decode attention (HBM-bound:
+    the K and V caches read once), GQA prefill with a history, RMSNorm, RoPE,
+    SwiGLU."""
+    out = {}
+    B, Skv, Hq, Hkv, D = 16, 4096, 32, 8, 128
+    q = dev.upload(prng.uniform(60, (B, Hq, D), -1.0, 1.0))
+    k = dev.upload(prng.uniform(61, (B, Skv, Hkv, D), -1.0, 1.0))
+    v = dev.upload(prng.uniform(62, (B, Skv, Hkv, D), -1.0, 1.0))
+    o = dev.alloc(B * Hq * D * 4)
+    t = time_steps(dev, lambda: dev.attention_decode(o, q, k, v, None, B, Skv, Hq, Hkv, D), steps, warmup)
+    nb = 4.0 * (2 * B * Skv * Hkv * D + 2 * B * Hq * D)
+    out[f"attention_decode_B{B}_kv{Skv}_Hq{Hq}_Hkv{Hkv}_D{D}"] = {
+        "ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1), "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
+    for b in (q, k, v, o):
+        b.free()
+    B, Sq, Skv, Hq, Hkv, D = 4, 1024, 2048, 32, 8, 64
+    q = dev.upload(prng.uniform(63, (B, Sq, Hq, D), -1.0, 1.0))
+    k = dev.upload(prng.uniform(64, (B, Skv, Hkv, D), -1.0, 1.0))
+    v = dev.upload(prng.uniform(65, (B, Skv, Hkv, D), -1.0, 1.0))
+    o = dev.alloc(B * Sq * Hq * D * 4)
+    t = time_steps(dev, lambda: dev.attention_gqa(o, q, k, v, B, Sq, Skv, Hq, Hkv, D, True), steps, warmup)
+    # causal with a 1024-token history: query i sees 1024 + i + 1 keys
+    flops = 4.0 * B * Hq * D * sum(Skv - Sq + i + 1 for i in range(Sq))
+    out[f"attention_gqa_prefill_B{B}_q{Sq}_kv{Skv}_Hq{Hq}_Hkv{Hkv}_D{D}"] = {
+        "ms": round(t, 4), "GFLOP/s": round(flops / t / 1e6, 1),
+        "frac_fp32_mfma": round(flops / t / 1e9 / PEAK_FP32_MFMA, 4)}
+    for b in (q, k, v, o):
+        b.free()
+    rows, hid = 4096, 4096
+    x = dev.upload(prng.normal(66, (rows, hid)))
+    g = dev.upload(np.ones((hid,), np.float32))
+    y = dev.alloc(rows * hid * 4)
+    t = time_steps(dev, lambda: dev.rmsnorm(y, x, g, rows, hid), steps, warmup)
+    nb = 8.0 * rows * hid
+    out["rmsnorm_4096x4096"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
+                                "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
+    t = time_steps(dev, lambda: dev.swiglu(y, x, x, rows * hid), steps, warmup)
+    nb = 12.0 * rows * hid
+    out["swiglu_4096x4096"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
+                               "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
+    # q and k of a 4096-token, 32-head, 128-dim layer (2 x 64 MiB)
+    S, H, hd = 4096, 32, 128
+    t = time_steps(dev, lambda: dev.rope(y, x, 2, 1, S, H // 2, hd), steps, warmup)
+    nb = 8.0 * 2 * S * (H // 2) * hd
+    out["rope_q_k_S4096_H16_hd128"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
+                                       "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
+    for b in (x, g, y):
+        b.free()
+    return out
+
+
 def int8_cases(dev, steps, warmup) -> dict:
     """The int8 path at the headline GEMM and conv shapes: one call = dynamic
     per-tensor quantization of the fp32 activation + int8 MFMA product with
@@ -429,6 +481,8 @@ def main() -> int:
         t, f, b = conv_case(dev, steps, 3)
         extra["conv3x3_N32_64to128_56x56_relu"] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
                                                    "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
+        log("decode-side family")
+        extra.update(decode_cases(dev, steps, 3))
         log("int8 path")
         extra.update(int8_cases(dev, steps, 3))
         log("conv backward")

@@ -99,6 +99,11 @@ lancius_node* lancius_conv2d_bwd_w(lancius_graph* g, const lancius_node* grad, c
                                    uint32_t k_h, uint32_t k_w, uint32_t stride, uint32_t pad);
 lancius_node* lancius_maxpool2d_bwd(lancius_graph* g, const lancius_node* grad, const lancius_node* fwd_in,
                                     uint32_t kernel, uint32_t stride);
+/* Decode-side blocks (lancius_ir.c:370-401). */
+lancius_node* lancius_rmsnorm(lancius_graph* g, const lancius_node* in, const lancius_node* gamma);
+lancius_node* lancius_swiglu(lancius_graph* g, const lancius_node* gate, const lancius_node* up);
+lancius_node* lancius_gqa(lancius_graph* g, const lancius_node* q, const lancius_node* k, const lancius_node* v,
+                          uint32_t n_heads_q, uint32_t n_heads_kv);
 /* Built for autodiff; neither executor runs them (no reference branch either). */
 lancius_node* lancius_permute(lancius_graph* g, const lancius_node* in, uint32_t a0, uint32_t a1, uint32_t a2,
                               uint32_t a3);

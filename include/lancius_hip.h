@@ -217,6 +217,46 @@ LANCIUS_HIP_EXPORT int lancius_hip_maxpool2d_bwd_f32(lancius_hip_ctx* ctx, float
                                                      const float* x, size_t N, size_t C, size_t H, size_t W,
                                                      size_t H_out, size_t W_out, size_t K, size_t stride);
 
+/* ---- decode-side attention family ----------------------------------- */
+
+/* Attention with grouped K/V heads and a key sequence that may be longer
+ * than the query sequence: q/out [batch, S_q, H_q, D], k/v [batch, S_kv,
+ * H_kv, D]; query head h reads K/V head h / (H_q / H_kv); causal lets query
+ * i see keys j <= i + (S_kv - S_q) (masked with the reference's -1e9
+ * semantics, lancius_kernels.c:307,428).  S_kv == S_q, causal, scale
+ * 1/sqrt(D) is kernel_gqa (lancius_kernels.c:407-448; the GQA node,
+ * lancius_scheduler.c:146-152); S_kv > S_q is the prefill-with-history case
+ * the reference's q-length-only loop cannot express. */
+LANCIUS_HIP_EXPORT int lancius_hip_attention_gqa_f32(lancius_hip_ctx* ctx, float* out, const float* q,
+                                                     const float* k, const float* v, size_t batch, size_t S_q,
+                                                     size_t S_kv, size_t H_q, size_t H_kv, size_t D, int causal,
+                                                     float scale);
+/* One new query token per sequence against its K/V cache:
+ * q/out [batch, H_q, D], k_cache/v_cache [batch, S_kv, H_kv, D]; sequence b
+ * uses keys [0, kv_lens[b]) (kv_lens NULL: all S_kv).  No mask (every cached
+ * key precedes the query).  batch 1, H_q == H_kv, scale 1/sqrt(D) is
+ * kernel_attention_kv_cache (lancius_kernels.c:338-379).  D <= 128,
+ * H_q / H_kv <= 64.  Split-KV: partials in the context workspace, combined
+ * in a fixed order. */
+LANCIUS_HIP_EXPORT int lancius_hip_attention_decode_f32(lancius_hip_ctx* ctx, float* out, const float* q,
+                                                        const float* k_cache, const float* v_cache,
+                                                        const int32_t* kv_lens, size_t batch, size_t S_kv,
+                                                        size_t H_q, size_t H_kv, size_t D, float scale);
+/* out = x * (1/sqrt(mean(x^2) + eps)) * gamma per row (kernel_rmsnorm,
+ * lancius_kernels.c:381-396; the RMSNORM node uses eps 1e-5). */
+LANCIUS_HIP_EXPORT int lancius_hip_rmsnorm_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* gamma,
+                                               size_t rows, size_t hidden, float eps);
+/* out = gate / (1 + exp(-gate)) * up (kernel_swiglu, lancius_kernels.c:398-405). */
+LANCIUS_HIP_EXPORT int lancius_hip_swiglu_f32(lancius_hip_ctx* ctx, float* out, const float* gate, const float* up,
+                                              size_t n);
+/* Rotary embedding of `count` consecutive [batch, S, H, head_dim] tensors
+ * (kernel_rope, lancius_kernels.c:248-272): pair (d, d+1) at position
+ * s + pos_offset rotates by (s + pos_offset) / 10000^(d / head_dim).  The
+ * ROPE node (lancius_scheduler.c:153-165) is count 2 (its q and k halves),
+ * batch 1, head_dim = shape[2] / 2, pos_offset 0.  out may equal in. */
+LANCIUS_HIP_EXPORT int lancius_hip_rope_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t count,
+                                            size_t batch, size_t S, size_t H, size_t head_dim, int pos_offset);
+
 /* ---- the int8 path (v_mfma_i32_32x32x32_i8) -------------------------- */
 
 /* Per-tensor symmetric quantization, the reference's formula

@@ -174,6 +174,11 @@ def declare_graph_api(lib: C.CDLL) -> C.CDLL:
     lib.lancius_ir_autodiff.restype = TrainingGraphP
     lib.lancius_training_graph_destroy.argtypes = [TrainingGraphP]
     lib.lancius_training_graph_destroy.restype = None
+    for name in ("lancius_rmsnorm", "lancius_swiglu"):
+        getattr(lib, name).argtypes = [GraphP, NodeP, NodeP]
+        getattr(lib, name).restype = NodeP
+    lib.lancius_gqa.argtypes = [GraphP, NodeP, NodeP, NodeP, C.c_uint32, C.c_uint32]
+    lib.lancius_gqa.restype = NodeP
     lib.lancius_quantize_graph.argtypes = [GraphP]
     lib.lancius_quantize_graph.restype = None
     lib.lancius_optimize_fusion.argtypes = [GraphP]

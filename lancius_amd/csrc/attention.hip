@@ -23,6 +23,8 @@
 // exponentials are exp2.
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -35,11 +37,12 @@ struct AttnParams {
     const float* K[LANCIUS_HIP_MAX_GROUP];
     const float* V[LANCIUS_HIP_MAX_GROUP];
     int batch;  // batches per group entry
-    int S, H, D;
-    int causal;
+    int S, H, D;   // queries per sequence, query heads, head dim
+    int Skv, Hkv;  // keys per sequence, K/V heads (query head h reads K/V head h / (H / Hkv))
+    int causal;    // query i sees keys j <= i + (Skv - S)
     float qscale;  // scale * log2(e)
     int q_tiles;
-    int Z;         // count * batch independent [S, H, D] problems
+    int Z;         // count * batch independent problems
 };
 
 constexpr int kD = 64;
@@ -65,12 +68,16 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     const int h = rem - z * p.H;
     const int g = z / p.batch, b = z % p.batch;
     const int qt = p.causal ? (p.q_tiles - 1 - t_rank) : t_rank;
-    const int S = p.S, H = p.H;
+    const int S = p.S, H = p.H, Skv = p.Skv;
+    const int off = Skv - S;  // causal offset of the query rows into the key sequence
+    const int hk = h / (H / p.Hkv);
     const size_t row_stride = (size_t)H * kD;
+    const size_t kv_stride = (size_t)p.Hkv * kD;
     const size_t base = ((size_t)b * S * H + h) * kD;
+    const size_t kv_base = ((size_t)b * Skv * p.Hkv + hk) * kD;
     const float* __restrict__ Qg = p.Q[g] + base;
-    const float* __restrict__ Kg = p.K[g] + base;
-    const float* __restrict__ Vg = p.V[g] + base;
+    const float* __restrict__ Kg = p.K[g] + kv_base;
+    const float* __restrict__ Vg = p.V[g] + kv_base;
     float* __restrict__ Og = p.O[g] + base;
 
     const int tid = threadIdx.x;
@@ -99,7 +106,7 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     }
 
     // Key range of this workgroup.
-    const int kv_end = p.causal ? min(S, q0 + kBQ) : S;
+    const int kv_end = p.causal ? max(0, min(Skv, q0 + kBQ + off)) : Skv;
     const int nblocks = (kv_end + kBKV - 1) / kBKV;
 
     // K/V global -> register staging: 64 keys x 64 d = 1024 float4 per tensor.
@@ -110,9 +117,9 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
             const int idx = tid + 256 * i;
             const int key = idx >> 4, dq = idx & 15;
             const int gk = kb + key;
-            if (gk < S) {
-                kreg[i] = *(const f32x4*)(Kg + (size_t)gk * row_stride + 4 * dq);
-                vreg[i] = *(const f32x4*)(Vg + (size_t)gk * row_stride + 4 * dq);
+            if (gk < Skv) {
+                kreg[i] = *(const f32x4*)(Kg + (size_t)gk * kv_stride + 4 * dq);
+                vreg[i] = *(const f32x4*)(Vg + (size_t)gk * kv_stride + 4 * dq);
             } else {
                 kreg[i] = f32x4{0.f, 0.f, 0.f, 0.f};
                 vreg[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -142,8 +149,10 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     float m_run = -1e30f;  // running max (log2 domain); finite so exp2 never sees inf - inf
     float l_part = 0.0f;   // this lane's share of the running sum
 
-    load_kv(0);
-    store_kv(0);
+    if (nblocks > 0) {
+        load_kv(0);
+        store_kv(0);
+    }
     __syncthreads();
 
     for (int blk = 0; blk < nblocks; ++blk) {
@@ -153,7 +162,7 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
         if (more) load_kv(kb + kBKV);
 
         // Wave-uniform skip of blocks entirely above this wave's diagonal.
-        const bool active = !p.causal || kb <= qw0 + 31;
+        const bool active = !p.causal || kb <= qw0 + 31 + off;
         if (active) {
             f32x16 s_acc[2];
 #pragma unroll
@@ -170,14 +179,14 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
                 s_acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1, qf[s], s_acc[1], 0, 0, 0);
             }
             // Register r of lane l holds key kb + 32*sb + 8*(r/4) + 4*(l/32) + r%4.
-            const bool need_mask = (p.causal && kb + kBKV - 1 > qw0) || (kb + kBKV > S);
+            const bool need_mask = (p.causal && kb + kBKV - 1 > qw0 + off) || (kb + kBKV > Skv);
             if (need_mask) {
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int key = kb + 32 * sb + 8 * (r >> 2) + 4 * lk + (r & 3);
-                        if (key >= S || (p.causal && key > q)) s_acc[sb][r] = -INFINITY;
+                        if (key >= Skv || (p.causal && key > q + off)) s_acc[sb][r] = -INFINITY;
                     }
             }
             float mx = -INFINITY;
@@ -248,16 +257,18 @@ __global__ void __launch_bounds__(256) attention_rowwise(const AttnParams p) {
     const int i = (int)(t / p.H), h = (int)(t % p.H);
     const int D = p.D;
     const size_t rs = (size_t)p.H * D;
+    const size_t rkv = (size_t)p.Hkv * D;
     const size_t base = (size_t)b * p.S * rs + (size_t)h * D;
+    const size_t kv_base = (size_t)b * p.Skv * rkv + (size_t)(h / (p.H / p.Hkv)) * D;
     const float* q = p.Q[g] + base + (size_t)i * rs;
-    const float* K = p.K[g] + base;
-    const float* V = p.V[g] + base;
+    const float* K = p.K[g] + kv_base;
+    const float* V = p.V[g] + kv_base;
     float* o = p.O[g] + base + (size_t)i * rs;
     for (int d = 0; d < D; ++d) o[d] = 0.0f;
     float m = -1e30f, l = 0.0f;
-    const int jend = p.causal ? i + 1 : p.S;
+    const int jend = p.causal ? min(p.Skv, max(0, i + 1 + p.Skv - p.S)) : p.Skv;
     for (int j = 0; j < jend; ++j) {
-        const float* k = K + (size_t)j * rs;
+        const float* k = K + (size_t)j * rkv;
         float s = 0.0f;
         for (int d = 0; d < D; ++d) s += q[d] * k[d];
         s *= p.qscale;
@@ -265,26 +276,177 @@ __global__ void __launch_bounds__(256) attention_rowwise(const AttnParams p) {
         const float c = exp2f(m - m_new);
         const float pj = exp2f(s - m_new);
         l = l * c + pj;
-        const float* v = V + (size_t)j * rs;
+        const float* v = V + (size_t)j * rkv;
         for (int d = 0; d < D; ++d) o[d] = o[d] * c + pj * v[d];
         m = m_new;
     }
-    const float inv = 1.0f / l;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     for (int d = 0; d < D; ++d) o[d] *= inv;
+}
+
+// ---- decode: one query token per sequence against a K/V cache --------------
+//
+// HBM-bound (every cached key and value is read once), so the kernel is built
+// around that read and the VALU does the arithmetic:
+//  * workgroup (sequence b, K/V head hk, split s) owns keys
+//    [s*chunk, min((s+1)*chunk, len_b)) and all G = Hq/Hkv query heads that
+//    share hk (grouped-query attention reads each K/V row once for the group);
+//  * 64-key tiles of K and V are staged in LDS with coalesced float4 loads;
+//    wave w takes query heads w, w+4, ...: lane = key for the scores (one
+//    dot product per lane over D from LDS), wave-wide max / sum for the
+//    online softmax, then lane = d for P.V;
+//  * each split stores (m, l, o[D]) per query head; decode_combine merges
+//    the splits in split order (deterministic).
+// kernel_attention_kv_cache (lancius_kernels.c:338-379) is batch = 1,
+// Hq = Hkv, no mask, scale 1/sqrt(D).
+struct DecodeParams {
+    float* out;             // [B][Hq][D]
+    const float* q;         // [B][Hq][D]
+    const float* k;         // [B][Skv][Hkv][D]
+    const float* v;
+    const int32_t* lens;    // per-sequence cache length (<= Skv) or null
+    float* part;            // [B*Hkv][splits][G][D + 2]
+    int B, Skv, Hq, Hkv, D, G;
+    int splits, chunk;
+    float scale;
+};
+
+constexpr int kDecKeys = 64;
+constexpr int kDecMaxD = 128;  // LDS: 64 keys x (D+1 + D) floats = 66 KB at D = 128
+
+__global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
+    __shared__ float Ks[kDecKeys][kDecMaxD + 1];
+    __shared__ float Vs[kDecKeys][kDecMaxD];
+    const int bh = blockIdx.x, split = blockIdx.y;
+    const int b = bh / p.Hkv, hk = bh - (bh / p.Hkv) * p.Hkv;
+    const int D = p.D, G = p.G;
+    const int len = p.lens ? min(max(p.lens[b], 0), p.Skv) : p.Skv;
+    const int k0 = split * p.chunk, k1 = min(len, k0 + p.chunk);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const size_t kv_row = (size_t)p.Hkv * D;
+    const float* kb = p.k + ((size_t)b * p.Skv * p.Hkv + hk) * D;
+    const float* vb = p.v + ((size_t)b * p.Skv * p.Hkv + hk) * D;
+    // per query head of this wave: running max, sum, and o[d] for d = lane + 64 i
+    constexpr int kMaxRowsPerWave = 16;
+    constexpr int kDPerLane = kDecMaxD / 64;
+    float m_run[kMaxRowsPerWave], l_run[kMaxRowsPerWave], o_run[kMaxRowsPerWave][kDPerLane];
+#pragma unroll
+    for (int r = 0; r < kMaxRowsPerWave; ++r) {
+        m_run[r] = -INFINITY;
+        l_run[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kDPerLane; ++i) o_run[r][i] = 0.0f;
+    }
+    for (int t0 = k0; t0 < k1; t0 += kDecKeys) {
+        const int nk = min(kDecKeys, k1 - t0);
+        __syncthreads();  // previous tile fully consumed
+        for (int idx = tid; idx < kDecKeys * D; idx += 256) {
+            const int key = idx / D, d = idx - (idx / D) * D;
+            const bool in = key < nk;
+            Ks[key][d] = in ? kb[(size_t)(t0 + key) * kv_row + d] : 0.0f;
+            Vs[key][d] = in ? vb[(size_t)(t0 + key) * kv_row + d] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < kMaxRowsPerWave; ++r) {
+            const int row = wave + 4 * r;  // query head within the group
+            if (row >= G) break;
+            const float* qr = p.q + ((size_t)b * p.Hq + (size_t)hk * G + row) * D;
+            // score of key `lane`
+            float sc = 0.0f;
+            for (int d = 0; d < D; ++d) sc += qr[d] * Ks[lane][d];
+            sc = lane < nk ? sc * p.scale : -INFINITY;
+            float mx = sc;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+            const float m_new = fmaxf(m_run[r], mx);
+            const float corr = expf(m_run[r] - m_new);  // 0 on the first tile (m_run = -inf)
+            const float pk = lane < nk ? expf(sc - m_new) : 0.0f;
+            float ps = pk;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) ps += __shfl_xor(ps, off);
+            l_run[r] = l_run[r] * corr + ps;
+            m_run[r] = m_new;
+#pragma unroll
+            for (int i = 0; i < kDPerLane; ++i) o_run[r][i] *= corr;
+            for (int key = 0; key < nk; ++key) {
+                const float pj = __shfl(pk, key);
+#pragma unroll
+                for (int i = 0; i < kDPerLane; ++i) {
+                    const int d = lane + 64 * i;
+                    if (d < D) o_run[r][i] += pj * Vs[key][d];
+                }
+            }
+        }
+    }
+    // partial of this split
+    float* part = p.part + (((size_t)bh * p.splits + split) * G) * (D + 2);
+#pragma unroll
+    for (int r = 0; r < kMaxRowsPerWave; ++r) {
+        const int row = wave + 4 * r;
+        if (row >= G) break;
+        float* pr = part + (size_t)row * (D + 2);
+#pragma unroll
+        for (int i = 0; i < kDPerLane; ++i) {
+            const int d = lane + 64 * i;
+            if (d < D) pr[d] = o_run[r][i];
+        }
+        if (lane == 0) {
+            pr[D] = m_run[r];
+            pr[D + 1] = l_run[r];
+        }
+    }
+}
+
+// out = sum_s o_s exp(m_s - m) / sum_s l_s exp(m_s - m), m = max_s m_s; one
+// wave per (sequence, query head), splits in order.  A sequence with no keys
+// gets zeros.
+__global__ void __launch_bounds__(256) decode_combine(const DecodeParams p) {
+    const int row_id = blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, hq)
+    const int lane = threadIdx.x & 63;
+    if (row_id >= p.B * p.Hq) return;
+    const int b = row_id / p.Hq, hq = row_id - (row_id / p.Hq) * p.Hq;
+    const int hk = hq / p.G, row = hq - (hq / p.G) * p.G;
+    const int D = p.D;
+    const float* base = p.part + (((size_t)(b * p.Hkv + hk) * p.splits) * p.G + row) * (D + 2);
+    const size_t sstride = (size_t)p.G * (D + 2);
+    float m = -INFINITY;
+    for (int s = 0; s < p.splits; ++s) m = fmaxf(m, base[s * sstride + D]);
+    float l = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+        const float ms = base[s * sstride + D];
+        if (ms > -INFINITY) l += base[s * sstride + D + 1] * expf(ms - m);
+    }
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float* o = p.out + ((size_t)b * p.Hq + hq) * D;
+    for (int d = lane; d < D; d += 64) {
+        float acc = 0.0f;
+        for (int s = 0; s < p.splits; ++s) {
+            const float ms = base[s * sstride + D];
+            if (ms > -INFINITY) acc += base[s * sstride + d] * expf(ms - m);
+        }
+        o[d] = acc * inv;
+    }
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
 int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, const float* const* Q,
                        const float* const* K, const float* const* V, size_t batch, size_t S, size_t H, size_t D,
-                       int causal, float scale) {
+                       int causal, float scale, size_t Skv = 0, size_t Hkv = 0) {
+    if (Skv == 0) Skv = S;
+    if (Hkv == 0) Hkv = H;
     LANCIUS_REQUIRE(ctx && O && Q && K && V, LANCIUS_HIP_ERR_NULL_PTR, "attention: NULL argument");
     LANCIUS_REQUIRE(count >= 1 && count <= LANCIUS_HIP_MAX_GROUP, LANCIUS_HIP_ERR_SHAPE,
                     "attention: group count %zu", count);
     LANCIUS_REQUIRE(batch >= 1 && S >= 1 && H >= 1 && D >= 1, LANCIUS_HIP_ERR_SHAPE,
                     "attention: empty shape batch=%zu S=%zu H=%zu D=%zu", batch, S, H, D);
-    LANCIUS_REQUIRE(S < (1u << 24) && H < 65536 && D <= 4096 && count * batch < 65536, LANCIUS_HIP_ERR_SHAPE,
-                    "attention: shape too large");
+    LANCIUS_REQUIRE(S < (1u << 24) && Skv < (1u << 24) && H < 65536 && D <= 4096 && count * batch < 65536,
+                    LANCIUS_HIP_ERR_SHAPE, "attention: shape too large");
+    LANCIUS_REQUIRE(Hkv >= 1 && H % Hkv == 0, LANCIUS_HIP_ERR_SHAPE,
+                    "attention: %zu query heads do not group over %zu K/V heads", H, Hkv);
+    LANCIUS_REQUIRE(!causal || Skv >= S, LANCIUS_HIP_ERR_SHAPE,
+                    "attention: causal with %zu keys for %zu queries", Skv, S);
     if (int rc = bind_device(ctx)) return rc;
     AttnParams p{};
     bool vec = true;
@@ -300,6 +462,8 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
     p.S = (int)S;
     p.H = (int)H;
     p.D = (int)D;
+    p.Skv = (int)Skv;
+    p.Hkv = (int)Hkv;
     p.causal = causal ? 1 : 0;
     p.qscale = scale * 1.4426950408889634f;  // log2(e)
     const unsigned z = (unsigned)(count * batch);
@@ -337,6 +501,60 @@ int lancius_hip_attention_grouped_f32(lancius_hip_ctx* ctx, size_t count, float*
                                       const float* const* k, const float* const* v, size_t S, size_t H, size_t D,
                                       int causal, float scale) {
     return attention_dispatch(ctx, count, out, q, k, v, 1, S, H, D, causal, scale);
+}
+
+int lancius_hip_attention_gqa_f32(lancius_hip_ctx* ctx, float* out, const float* q, const float* k, const float* v,
+                                  size_t batch, size_t S_q, size_t S_kv, size_t H_q, size_t H_kv, size_t D,
+                                  int causal, float scale) {
+    LANCIUS_REQUIRE(S_kv >= 1 && H_kv >= 1, LANCIUS_HIP_ERR_SHAPE, "attention_gqa: S_kv=%zu H_kv=%zu", S_kv, H_kv);
+    float* o1[1] = {out};
+    const float* q1[1] = {q};
+    const float* k1[1] = {k};
+    const float* v1[1] = {v};
+    return attention_dispatch(ctx, 1, o1, q1, k1, v1, batch, S_q, H_q, D, causal, scale, S_kv, H_kv);
+}
+
+int lancius_hip_attention_decode_f32(lancius_hip_ctx* ctx, float* out, const float* q, const float* k_cache,
+                                     const float* v_cache, const int32_t* kv_lens, size_t batch, size_t S_kv,
+                                     size_t H_q, size_t H_kv, size_t D, float scale) {
+    LANCIUS_REQUIRE(ctx && out && q && k_cache && v_cache, LANCIUS_HIP_ERR_NULL_PTR, "attention_decode: NULL argument");
+    LANCIUS_REQUIRE(batch >= 1 && H_q >= 1 && H_kv >= 1 && D >= 1 && H_q % H_kv == 0, LANCIUS_HIP_ERR_SHAPE,
+                    "attention_decode: batch=%zu H_q=%zu H_kv=%zu D=%zu", batch, H_q, H_kv, D);
+    LANCIUS_REQUIRE(D <= kDecMaxD && H_q / H_kv <= 64 && S_kv < (1u << 30) && batch * H_kv < kMaxGridX,
+                    LANCIUS_HIP_ERR_SHAPE, "attention_decode: D=%zu (<= %d) or group %zu (<= 64) unsupported", D,
+                    kDecMaxD, H_q / H_kv);
+    if (int rc = bind_device(ctx)) return rc;
+    DecodeParams p{};
+    p.out = out;
+    p.q = q;
+    p.k = k_cache;
+    p.v = v_cache;
+    p.lens = kv_lens;
+    p.B = (int)batch;
+    p.Skv = (int)S_kv;
+    p.Hq = (int)H_q;
+    p.Hkv = (int)H_kv;
+    p.D = (int)D;
+    p.G = (int)(H_q / H_kv);
+    p.scale = scale;
+    // ~2 workgroups per CU in all, each split >= 256 keys
+    const size_t seqs = batch * H_kv;
+    size_t splits = std::max<size_t>(1, std::min<size_t>((512 + seqs - 1) / seqs, (S_kv + 255) / 256));
+    splits = std::min<size_t>(splits, 65535);
+    const size_t chunk = std::max<size_t>(kDecKeys, (S_kv + splits - 1) / splits);
+    splits = std::max<size_t>(1, (S_kv + chunk - 1) / chunk);
+    p.splits = (int)splits;
+    p.chunk = (int)chunk;
+    void* ws = nullptr;
+    if (int rc = workspace(ctx, seqs * splits * p.G * (D + 2) * sizeof(float), &ws)) return rc;
+    p.part = (float*)ws;
+    hipLaunchKernelGGL(attention_decode, dim3((unsigned)seqs, (unsigned)splits), dim3(256), 0, ctx->stream, p);
+    if (int rc = check_launch("attention_decode")) return rc;
+    const size_t rows = batch * H_q;
+    LANCIUS_REQUIRE((rows + 3) / 4 < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention_decode: too many heads");
+    hipLaunchKernelGGL(decode_combine, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream, p);
+    if (int rc = check_launch("decode_combine")) return rc;
+    return ok();
 }
 
 }  // extern "C"

@@ -18,7 +18,7 @@
 typedef enum {
     L_GEMM, L_CONV, L_ATTN, L_LN, L_SOFTMAX, L_ADD, L_RELU, L_GELU, L_BCAST,
     L_SUB, L_MUL, L_RELU_BWD, L_TRANSPOSE, L_SUM, L_SUM0, L_SUM1, L_SOFTMAX_BWD, L_CE, L_CE_BWD,
-    L_CONV_BWD_IN, L_CONV_BWD_W, L_POOL, L_POOL_BWD
+    L_CONV_BWD_IN, L_CONV_BWD_W, L_POOL, L_POOL_BWD, L_RMSNORM, L_SWIGLU, L_GQA, L_ROPE
 } lkind;
 
 enum { ROLE_NONE = 0, ROLE_INPUT, ROLE_CONST, ROLE_POOLED, ROLE_ALIAS, ROLE_FUSED };
@@ -215,6 +215,10 @@ static int supported(lancius_opcode op) {
         case LANCIUS_OP_CONV2D_BWD_W:
         case LANCIUS_OP_MAXPOOL2D:
         case LANCIUS_OP_MAXPOOL2D_BWD:
+        case LANCIUS_OP_RMSNORM:
+        case LANCIUS_OP_SWIGLU:
+        case LANCIUS_OP_GQA:
+        case LANCIUS_OP_ROPE:
             return 1;
         default:
             return 0;
@@ -482,6 +486,50 @@ static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
             memcpy(L->d, d, sizeof(d));
             m->in[0] = IN(n, 0);
             if (bwd) m->in[1] = IN(n, 1);
+            return 0;
+        }
+        case LANCIUS_OP_RMSNORM: { /* lancius_scheduler.c:134-139: rows shape[0], hidden shape[1] */
+            const size_t rows = n->shape[0], hid = n->ndim > 1 ? n->shape[1] : 1;
+            if (elems(n->inputs[0]) < rows * hid || elems(n->inputs[1]) < hid || e < rows * hid)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "RMSNORM sizes");
+            L->kind = L_RMSNORM;
+            L->d[0] = rows;
+            L->d[1] = hid;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            return 0;
+        }
+        case LANCIUS_OP_SWIGLU: /* :140-145 */
+            if (elems(n->inputs[0]) < e || elems(n->inputs[1]) < e) return fail(LANCIUS_HIP_ERR_SHAPE, "SWIGLU sizes");
+            L->kind = L_SWIGLU;
+            L->d[0] = e;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            return 0;
+        case LANCIUS_OP_GQA: { /* :146-152: S shape[0], Hq kernel_h, Hkv kernel_w, D shape[2] */
+            const size_t S = n->shape[0], Hq = n->kernel_h, Hkv = n->kernel_w, D = n->ndim > 2 ? n->shape[2] : 0;
+            if (n->ndim != 3 || !S || !D || !Hkv || Hq % Hkv || elems(n->inputs[0]) < S * Hq * D ||
+                elems(n->inputs[1]) < S * Hkv * D || elems(n->inputs[2]) < S * Hkv * D || e < S * Hq * D)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "GQA sizes");
+            L->kind = L_GQA;
+            L->d[0] = S;
+            L->d[1] = Hq;
+            L->d[2] = Hkv;
+            L->d[3] = D;
+            m->in[0] = IN(n, 0);
+            m->in[1] = IN(n, 1);
+            m->in[2] = IN(n, 2);
+            return 0;
+        }
+        case LANCIUS_OP_ROPE: { /* :153-165: [S, H, 2 hd]: q then k halves */
+            const size_t S = n->shape[0], H = n->ndim > 1 ? n->shape[1] : 0, hd2 = n->ndim > 2 ? n->shape[2] : 0;
+            if (n->ndim != 3 || hd2 % 2 || hd2 % 4 || elems(n->inputs[0]) < S * H * hd2 || e < S * H * hd2)
+                return fail(LANCIUS_HIP_ERR_SHAPE, "ROPE sizes (shape[2] = 2 x an even head dim)");
+            L->kind = L_ROPE;
+            L->d[0] = S;
+            L->d[1] = H;
+            L->d[2] = hd2 / 2;
+            m->in[0] = IN(n, 0);
             return 0;
         }
         default:
@@ -1045,6 +1093,16 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
         case L_POOL:
             return lancius_hip_maxpool2d_f32(ctx, P(m->out), P(m->in[0]), L->d[0], L->d[1], L->d[2], L->d[3],
                                              L->d[6], L->d[7]);
+        case L_RMSNORM:
+            return lancius_hip_rmsnorm_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1], 1e-5f);
+        case L_SWIGLU:
+            return lancius_hip_swiglu_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0]);
+        case L_GQA:
+            return lancius_hip_attention_gqa_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), P(m->in[2]), 1, L->d[0],
+                                                 L->d[0], L->d[1], L->d[2], L->d[3], 1,
+                                                 (float)(1.0 / sqrt((double)L->d[3])));
+        case L_ROPE:
+            return lancius_hip_rope_f32(ctx, P(m->out), P(m->in[0]), 2, 1, L->d[0], L->d[1], L->d[2], 0);
         case L_POOL_BWD:
             return lancius_hip_maxpool2d_bwd_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1],
                                                  L->d[2], L->d[3], L->d[4], L->d[5], L->d[6], L->d[7]);

@@ -722,3 +722,32 @@ lancius_node* lancius_matmul_batched(lancius_graph* g, const lancius_node* a, co
     }
     return n;
 }
+
+/* lancius_ir.c:370-378 */
+lancius_node* lancius_rmsnorm(lancius_graph* g, const lancius_node* in, const lancius_node* gamma) {
+    return binary(g, LANCIUS_OP_RMSNORM, in, gamma);
+}
+
+/* lancius_ir.c:380-388 */
+lancius_node* lancius_swiglu(lancius_graph* g, const lancius_node* gate, const lancius_node* up) {
+    return binary(g, LANCIUS_OP_SWIGLU, gate, up);
+}
+
+/* lancius_ir.c:390-401: shape of q, head counts in kernel_h / kernel_w. */
+lancius_node* lancius_gqa(lancius_graph* g, const lancius_node* q, const lancius_node* k, const lancius_node* v,
+                          uint32_t n_heads_q, uint32_t n_heads_kv) {
+    if (!q || !k || !v) {
+        lancius_set_error(LANCIUS_ERROR_NULL_PTR);
+        return NULL;
+    }
+    lancius_node* n = new_node(g, LANCIUS_OP_GQA, q->ndim, 3);
+    if (n) {
+        copy_shape(n, q);
+        n->kernel_h = n_heads_q;
+        n->kernel_w = n_heads_kv;
+        n->inputs[0] = q;
+        n->inputs[1] = k;
+        n->inputs[2] = v;
+    }
+    return n;
+}

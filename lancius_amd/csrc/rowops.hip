@@ -242,6 +242,60 @@ __global__ void __launch_bounds__(kRowThreads) cross_entropy_bwd_rows(float* __r
     for (int c = lane; c < cols; c += 64) out[base + c] = (expf(x[base + c] - m) / s - y[base + c]) * scale;
 }
 
+// RMSNorm (lancius_kernels.c:381-396): out = x * (1 / sqrt(mean(x^2) + eps)) * gamma.
+__global__ void __launch_bounds__(kRowThreads) rmsnorm_rows(float* __restrict__ out, const float* __restrict__ in,
+                                                            const float* __restrict__ gamma, int rows, int hidden,
+                                                            float eps) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* x = in + (size_t)row * hidden;
+    float q = 0.0f;
+    for (int c = lane; c < hidden; c += 64) q += x[c] * x[c];
+    q = wave_sum(q);
+    const float inv = 1.0f / sqrtf(q / (float)hidden + eps);
+    float* y = out + (size_t)row * hidden;
+    for (int c = lane; c < hidden; c += 64) y[c] = (x[c] * inv) * gamma[c];
+}
+
+// SwiGLU (lancius_kernels.c:398-405): out = g / (1 + exp(-g)) * up.
+__global__ void __launch_bounds__(256) swiglu_kernel(float* __restrict__ out, const float* __restrict__ gate,
+                                                     const float* __restrict__ up, size_t n) {
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += step) {
+        const float g = gate[i];
+        out[i] = g / (1.0f + expf(-g)) * up[i];
+    }
+}
+
+// RoPE (lancius_kernels.c:248-272): pair (d, d+1) of every head at position
+// s + pos_offset turns by angle pos / 10000^(d / head_dim).  The angle and its
+// sine / cosine are evaluated in fp64 (positions reach thousands of radians,
+// where fp32 argument reduction would lose four digits), once per (sequence
+// position, pair) and applied to every head of `count` consecutive
+// [batch, S, H, head_dim] tensors.
+__global__ void __launch_bounds__(256) rope_kernel(float* __restrict__ out, const float* __restrict__ in, int count,
+                                                   int batch, int S, int H, int hd, int pos_offset) {
+    const int half = hd / 2;
+    const size_t pairs = (size_t)S * half;  // (s, pair) units; heads, batch and tensors inside
+    const size_t step = (size_t)gridDim.x * blockDim.x;
+    const size_t tensor = (size_t)batch * S * H * hd;
+    for (size_t u = (size_t)blockIdx.x * blockDim.x + threadIdx.x; u < pairs; u += step) {
+        const int s = (int)(u / half), d = 2 * (int)(u - (u / half) * half);
+        const double freq = 1.0 / pow(10000.0, (double)d / (double)hd);
+        const double angle = (double)(s + pos_offset) * freq;
+        const float c = (float)cos(angle), sn = (float)sin(angle);
+        for (int t = 0; t < count; ++t)
+            for (int b = 0; b < batch; ++b)
+                for (int h = 0; h < H; ++h) {
+                    const size_t idx = (size_t)t * tensor + (((size_t)b * S + s) * H + h) * hd + d;
+                    const float x0 = in[idx], x1 = in[idx + 1];
+                    out[idx] = x0 * c - x1 * sn;
+                    out[idx + 1] = x0 * sn + x1 * c;
+                }
+    }
+}
+
 // ---- elementwise --------------------------------------------------------
 
 enum EwOp : int { kAdd = 0, kRelu = 1, kGelu = 2, kCopy = 3, kSub = 4, kMul = 5, kReluBwd = 6 };
@@ -390,6 +444,38 @@ int lancius_hip_gelu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_
 
 int lancius_hip_copy_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t n) {
     return run_elementwise<kCopy>(ctx, out, in, nullptr, n, "copy");
+}
+
+int lancius_hip_rmsnorm_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* gamma, size_t rows,
+                            size_t hidden, float eps) {
+    LANCIUS_REQUIRE(ctx && out && in && gamma, LANCIUS_HIP_ERR_NULL_PTR, "rmsnorm: NULL argument");
+    LANCIUS_REQUIRE(hidden > 0 && hidden < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
+                    "rmsnorm: rows=%zu hidden=%zu", rows, hidden);
+    if (rows == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(rmsnorm_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0, ctx->stream, out, in,
+                       gamma, (int)rows, (int)hidden, eps);
+    return check_launch("rmsnorm");
+}
+
+int lancius_hip_swiglu_f32(lancius_hip_ctx* ctx, float* out, const float* gate, const float* up, size_t n) {
+    LANCIUS_REQUIRE(ctx && out && gate && up, LANCIUS_HIP_ERR_NULL_PTR, "swiglu: NULL argument");
+    if (n == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(ew_grid(n)), dim3(256), 0, ctx->stream, out, gate, up, n);
+    return check_launch("swiglu");
+}
+
+int lancius_hip_rope_f32(lancius_hip_ctx* ctx, float* out, const float* in, size_t count, size_t batch, size_t S,
+                         size_t H, size_t head_dim, int pos_offset) {
+    LANCIUS_REQUIRE(ctx && out && in, LANCIUS_HIP_ERR_NULL_PTR, "rope: NULL argument");
+    LANCIUS_REQUIRE(head_dim % 2 == 0 && count * batch * S * H * head_dim < ((size_t)1 << 40) && S < (1u << 30),
+                    LANCIUS_HIP_ERR_SHAPE, "rope: head_dim %zu must be even", head_dim);
+    if (count * batch * S * H * head_dim == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    hipLaunchKernelGGL(rope_kernel, dim3(ew_grid(S * head_dim / 2)), dim3(256), 0, ctx->stream, out, in, (int)count,
+                       (int)batch, (int)S, (int)H, (int)head_dim, pos_offset);
+    return check_launch("rope");
 }
 
 int lancius_hip_sub_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n) {

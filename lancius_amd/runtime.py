@@ -76,6 +76,11 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_copy_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_broadcast_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     lib.lancius_hip_fill_f32.argtypes = [vp, vp, f32, sz]
+    lib.lancius_hip_attention_gqa_f32.argtypes = [vp, vp, vp, vp, vp] + [sz] * 6 + [i32, f32]
+    lib.lancius_hip_attention_decode_f32.argtypes = [vp, vp, vp, vp, vp, vp] + [sz] * 5 + [f32]
+    lib.lancius_hip_rmsnorm_f32.argtypes = [vp, vp, vp, vp, sz, sz, f32]
+    lib.lancius_hip_swiglu_f32.argtypes = [vp, vp, vp, vp, sz]
+    lib.lancius_hip_rope_f32.argtypes = [vp, vp, vp] + [sz] * 5 + [i32]
     lib.lancius_hip_quantize_i8.argtypes = [vp, vp, vp, vp, sz]
     lib.lancius_hip_gemm_i8_f32.argtypes = [vp, vp, vp, vp, C.c_double, sz, sz, sz, vp, i32, vp]
     lib.lancius_hip_conv2d_i8_f32.argtypes = [vp, vp, vp, vp, C.c_double, vp] + [sz] * 9 + [i32]
@@ -298,6 +303,27 @@ class Device:
 
     def fill(self, out, value, n) -> None:
         _check(self.lib.lancius_hip_fill_f32(self.ctx, _vp(out), float(value), n))
+
+    # -- decode-side attention family ------------------------------------------
+    def attention_gqa(self, out, q, k, v, batch, S_q, S_kv, H_q, H_kv, D, causal=True, scale=None) -> None:
+        scale = 1.0 / np.sqrt(D) if scale is None else scale
+        _check(self.lib.lancius_hip_attention_gqa_f32(self.ctx, _vp(out), _vp(q), _vp(k), _vp(v), batch, S_q, S_kv,
+                                                      H_q, H_kv, D, int(bool(causal)), float(scale)))
+
+    def attention_decode(self, out, q, k_cache, v_cache, kv_lens, batch, S_kv, H_q, H_kv, D, scale=None) -> None:
+        scale = 1.0 / np.sqrt(D) if scale is None else scale
+        _check(self.lib.lancius_hip_attention_decode_f32(self.ctx, _vp(out), _vp(q), _vp(k_cache), _vp(v_cache),
+                                                         _vp(kv_lens), batch, S_kv, H_q, H_kv, D, float(scale)))
+
+    def rmsnorm(self, out, x, gamma, rows, hidden, eps=1e-5) -> None:
+        _check(self.lib.lancius_hip_rmsnorm_f32(self.ctx, _vp(out), _vp(x), _vp(gamma), rows, hidden, float(eps)))
+
+    def swiglu(self, out, gate, up, n) -> None:
+        _check(self.lib.lancius_hip_swiglu_f32(self.ctx, _vp(out), _vp(gate), _vp(up), n))
+
+    def rope(self, out, x, count, batch, S, H, head_dim, pos_offset=0) -> None:
+        _check(self.lib.lancius_hip_rope_f32(self.ctx, _vp(out), _vp(x), count, batch, S, H, head_dim,
+                                             int(pos_offset)))
 
     # -- int8 path -------------------------------------------------------------
     def quantize_i8(self, q, scale, x, n) -> None:

@@ -61,6 +61,14 @@ def lib() -> C.CDLL:
         L.oracle_conv2d_bwd_weight.argtypes = [_D, _D, _D] + [sz] * 11
         L.oracle_maxpool2d.argtypes = [_D, _D] + [sz] * 6
         L.oracle_maxpool2d_bwd.argtypes = [_D, _D, _D] + [sz] * 8
+        L.oracle_rmsnorm.argtypes = [_D, _D, _D, sz, sz, C.c_double]
+        L.oracle_swiglu.argtypes = [_D, _D, _D, sz]
+        L.oracle_rope.argtypes = [_D, _D, sz, sz, sz, sz, sz, C.c_int]
+        L.oracle_attention_gqa.argtypes = [_D, _D, _D, _D] + [sz] * 6 + [C.c_int, C.c_double]
+        L.oracle_attention_decode.argtypes = [_D, _D, _D, _D, C.POINTER(C.c_int32)] + [sz] * 5 + [C.c_double]
+        for name in ("oracle_rmsnorm", "oracle_swiglu", "oracle_rope", "oracle_attention_gqa",
+                     "oracle_attention_decode"):
+            getattr(L, name).restype = None
         I8 = C.POINTER(C.c_int8)
         L.oracle_quantize_i8.argtypes = [I8, _D, sz]
         L.oracle_quantize_i8.restype = C.c_double
@@ -100,6 +108,13 @@ def ref_lib() -> C.CDLL | None:
         L.kernel_layernorm.argtypes = [_D, _D, _D, _D, sz, sz, C.c_double]
         L.kernel_gelu.argtypes = [_D, _D, sz]
         L.kernel_attention.argtypes = [_D, _D, _D, _D, sz, sz, sz]
+        L.kernel_rmsnorm.argtypes = [_D, _D, _D, sz, sz, C.c_double]
+        L.kernel_swiglu.argtypes = [_D, _D, _D, sz]
+        L.kernel_rope.argtypes = [_D, _D, sz, sz, sz, sz, C.c_int]
+        L.kernel_gqa.argtypes = [_D, _D, _D, _D, sz, sz, sz, sz]
+        L.kernel_attention_kv_cache.argtypes = [_D, _D, _D, _D, sz, sz, sz]
+        for name in ("kernel_rmsnorm", "kernel_swiglu", "kernel_rope", "kernel_gqa", "kernel_attention_kv_cache"):
+            getattr(L, name).restype = None
         L.lancius_quantize_graph.argtypes = [abi.GraphP]
         L.lancius_quantize_graph.restype = None
         L.kernel_conv2d_int8_fwd.argtypes = [_D, C.POINTER(C.c_int8), C.POINTER(C.c_int8), C.c_double,
@@ -312,6 +327,54 @@ def maxpool2d_bwd(dy, x, K, stride) -> np.ndarray:
     N, Cc, H, W = x.shape
     out = np.empty_like(x)
     lib().oracle_maxpool2d_bwd(_p(out), _p(dy), _p(x), N, Cc, H, W, dy.shape[2], dy.shape[3], K, stride)
+    return out
+
+
+def rmsnorm(x, gamma, eps=1e-5) -> np.ndarray:
+    x, gamma = _d(x), _d(gamma)
+    out = np.empty_like(x)
+    lib().oracle_rmsnorm(_p(out), _p(x), _p(gamma), x.shape[0], x.shape[1], eps)
+    return out
+
+
+def swiglu(gate, up) -> np.ndarray:
+    gate, up = _d(gate), _d(up)
+    out = np.empty_like(gate)
+    lib().oracle_swiglu(_p(out), _p(gate), _p(up), gate.size)
+    return out
+
+
+def rope(x, count, batch, S, H, hd, pos_offset=0) -> np.ndarray:
+    x = _d(x)
+    out = np.empty_like(x)
+    lib().oracle_rope(_p(out), _p(x), count, batch, S, H, hd, int(pos_offset))
+    return out
+
+
+def attention_gqa(q, k, v, causal=True, scale=None) -> np.ndarray:
+    """q [B, Sq, Hq, D], k/v [B, Skv, Hkv, D]."""
+    q, k, v = _d(q), _d(k), _d(v)
+    B, Sq, Hq, D = q.shape
+    Skv, Hkv = k.shape[1], k.shape[2]
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    out = np.empty_like(q)
+    lib().oracle_attention_gqa(_p(out), _p(q), _p(k), _p(v), B, Sq, Skv, Hq, Hkv, D, int(bool(causal)),
+                               float(scale))
+    return out
+
+
+def attention_decode(q, k, v, lens=None, scale=None) -> np.ndarray:
+    """q [B, Hq, D], k/v [B, Skv, Hkv, D], lens int32 [B] or None."""
+    q, k, v = _d(q), _d(k), _d(v)
+    B, Hq, D = q.shape
+    Skv, Hkv = k.shape[1], k.shape[2]
+    scale = 1.0 / np.sqrt(D) if scale is None else scale
+    out = np.empty_like(q)
+    lp = None
+    if lens is not None:
+        lens = np.ascontiguousarray(lens, dtype=np.int32)
+        lp = lens.ctypes.data_as(C.POINTER(C.c_int32))
+    lib().oracle_attention_decode(_p(out), _p(q), _p(k), _p(v), lp, B, Skv, Hq, Hkv, D, float(scale))
     return out
 
 

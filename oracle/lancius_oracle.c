@@ -387,6 +387,124 @@ void oracle_maxpool2d_bwd(double* dx, const double* dy, const double* x, size_t 
             }
 }
 
+/* ---- decode-side attention family ------------------------------------------------ */
+
+/* B/src/math/lancius_kernels.c:381-396 */
+void oracle_rmsnorm(double* out, const double* in, const double* gamma, size_t rows, size_t hidden, double eps) {
+    for (size_t i = 0; i < rows; i++) {
+        const double* x = in + i * hidden;
+        double sq = 0.0;
+        for (size_t j = 0; j < hidden; j++) sq += x[j] * x[j];
+        const double inv = 1.0 / sqrt(sq / (double)hidden + eps);
+        for (size_t j = 0; j < hidden; j++) out[i * hidden + j] = (x[j] * inv) * gamma[j];
+    }
+}
+
+/* B/src/math/lancius_kernels.c:398-405 */
+void oracle_swiglu(double* out, const double* gate, const double* up, size_t n) {
+    for (size_t i = 0; i < n; i++) out[i] = gate[i] / (1.0 + exp(-gate[i])) * up[i];
+}
+
+/* B/src/math/lancius_kernels.c:248-272 applied to `count` consecutive
+ * [batch, S, H, hd] tensors (in place when out == in). */
+void oracle_rope(double* out, const double* in, size_t count, size_t batch, size_t S, size_t H, size_t hd,
+                 int pos_offset) {
+    const size_t tensor = batch * S * H * hd;
+    if (out != in) memcpy(out, in, count * tensor * sizeof(double));
+    for (size_t t = 0; t < count; t++)
+        for (size_t b = 0; b < batch; b++)
+            for (size_t s = 0; s < S; s++) {
+                const int pos = (int)s + pos_offset;
+                for (size_t h = 0; h < H; h++)
+                    for (size_t d = 0; d < hd; d += 2) {
+                        const double freq = 1.0 / pow(10000.0, (double)d / (double)hd);
+                        const double angle = pos * freq;
+                        const double c = cos(angle), sn = sin(angle);
+                        double* x = out + t * tensor + ((b * S + s) * H + h) * hd + d;
+                        const double x0 = x[0], x1 = x[1];
+                        x[0] = x0 * c - x1 * sn;
+                        x[1] = x0 * sn + x1 * c;
+                    }
+            }
+}
+
+/* B/src/math/lancius_kernels.c:407-448 (kernel_gqa: causal, -1e9 masking,
+ * online softmax), generalised to a batch and to S_kv >= S_q keys, query i
+ * seeing keys j <= i + (S_kv - S_q) when causal.  S_kv == S_q, batch 1,
+ * causal, scale 1/sqrt(D) is the reference kernel. */
+void oracle_attention_gqa(double* out, const double* q, const double* k, const double* v, size_t batch, size_t Sq,
+                          size_t Skv, size_t Hq, size_t Hkv, size_t D, int causal, double scale) {
+    const size_t group = Hq / Hkv;
+    const long off = (long)Skv - (long)Sq;
+#pragma omp parallel for collapse(2) schedule(static)
+    for (size_t b = 0; b < batch; b++)
+        for (size_t i = 0; i < Sq; i++) {
+            double* o = (double*)calloc(D, sizeof(double));
+            for (size_t hq = 0; hq < Hq; hq++) {
+                const size_t hk = hq / group;
+                const double* qr = q + ((b * Sq + i) * Hq + hq) * D;
+                double m = -1e9, l = 0.0;
+                for (size_t d = 0; d < D; d++) o[d] = 0.0;
+                for (size_t j = 0; j < Skv; j++) {
+                    const double* kr = k + ((b * Skv + j) * Hkv + hk) * D;
+                    const double* vr = v + ((b * Skv + j) * Hkv + hk) * D;
+                    double s = 0.0;
+                    for (size_t d = 0; d < D; d++) s += qr[d] * kr[d];
+                    s *= scale;
+                    if (causal && (long)j > (long)i + off) s = -1e9;
+                    const double m_new = s > m ? s : m;
+                    const double corr = exp(m - m_new), pj = exp(s - m_new);
+                    l = l * corr + pj;
+                    for (size_t d = 0; d < D; d++) o[d] = o[d] * corr + pj * vr[d];
+                    m = m_new;
+                }
+                double* orow = out + ((b * Sq + i) * Hq + hq) * D;
+                for (size_t d = 0; d < D; d++) orow[d] = o[d] / l;
+            }
+            free(o);
+        }
+}
+
+/* B/src/math/lancius_kernels.c:338-379 (kernel_attention_kv_cache: scores
+ * against every cached key, max from -1e9, softmax, weighted V), for a batch
+ * of sequences with their own cache lengths (lens NULL: all S_kv) and K/V
+ * heads shared by groups of query heads.  A sequence with no keys gives 0. */
+void oracle_attention_decode(double* out, const double* q, const double* k, const double* v, const int32_t* lens,
+                             size_t batch, size_t Skv, size_t Hq, size_t Hkv, size_t D, double scale) {
+    const size_t group = Hq / Hkv;
+    double* sc = (double*)malloc((Skv ? Skv : 1) * sizeof(double));
+    for (size_t b = 0; b < batch; b++) {
+        const size_t len = lens ? (size_t)(lens[b] < 0 ? 0 : (lens[b] > (int32_t)Skv ? (int32_t)Skv : lens[b])) : Skv;
+        for (size_t h = 0; h < Hq; h++) {
+            const size_t hk = h / group;
+            const double* qr = q + (b * Hq + h) * D;
+            double* orow = out + (b * Hq + h) * D;
+            for (size_t d = 0; d < D; d++) orow[d] = 0.0;
+            if (len == 0) continue;
+            double mx = -1e9;
+            for (size_t j = 0; j < len; j++) {
+                const double* kr = k + ((b * Skv + j) * Hkv + hk) * D;
+                double s = 0.0;
+                for (size_t d = 0; d < D; d++) s += qr[d] * kr[d];
+                sc[j] = s * scale;
+                if (sc[j] > mx) mx = sc[j];
+            }
+            double se = 0.0;
+            for (size_t j = 0; j < len; j++) {
+                sc[j] = exp(sc[j] - mx);
+                se += sc[j];
+            }
+            for (size_t j = 0; j < len; j++) sc[j] /= se;
+            for (size_t d = 0; d < D; d++) {
+                double s = 0.0;
+                for (size_t j = 0; j < len; j++) s += sc[j] * v[((b * Skv + j) * Hkv + hk) * D + d];
+                orow[d] = s;
+            }
+        }
+    }
+    free(sc);
+}
+
 /* ---- the int8 path --------------------------------------------------------------- */
 
 /* Per-tensor quantization: B/src/runtime/lancius_scheduler.c:199-204 (MATMUL
@@ -531,6 +649,21 @@ static int run_node(lancius_node* n) {
             return 0;
         case LANCIUS_OP_SUB:
             oracle_sub(y, in[0]->runtime_data, in[1]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_RMSNORM: /* lancius_scheduler.c:134-139 */
+            oracle_rmsnorm(y, in[0]->runtime_data, in[1]->runtime_data, n->shape[0], n->shape[1], 1e-5);
+            return 0;
+        case LANCIUS_OP_SWIGLU: /* :140-145 */
+            oracle_swiglu(y, in[0]->runtime_data, in[1]->runtime_data, e);
+            return 0;
+        case LANCIUS_OP_GQA: /* :146-152: S = shape[0], Hq = kernel_h, Hkv = kernel_w, D = shape[2] */
+            if (n->kernel_w == 0 || n->kernel_h % n->kernel_w) return -3;
+            oracle_attention_gqa(y, in[0]->runtime_data, in[1]->runtime_data, in[2]->runtime_data, 1, n->shape[0],
+                                 n->shape[0], n->kernel_h, n->kernel_w, n->shape[2], 1,
+                                 1.0 / sqrt((double)n->shape[2]));
+            return 0;
+        case LANCIUS_OP_ROPE: /* :153-165: copy, then q = first half, k = second half */
+            oracle_rope(y, in[0]->runtime_data, 2, 1, n->shape[0], n->shape[1], n->shape[2] / 2, 0);
             return 0;
         case LANCIUS_OP_MUL:
             oracle_mul(y, in[0]->runtime_data, in[1]->runtime_data, e);

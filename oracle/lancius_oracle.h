@@ -31,6 +31,14 @@
  *                         golden vectors of kernel_conv2d_bwd_in/_w; adjoint
  *                         identities <conv(x,w), g> = <x, bwd_in(g,w)> =
  *                         <w, bwd_w(g,x)>; finite differences
+ *   oracle_rmsnorm/swiglu/rope/attention_gqa/attention_decode
+ *                         golden vectors of kernel_rmsnorm, kernel_swiglu,
+ *                         kernel_rope, kernel_gqa, kernel_attention_kv_cache
+ *                         and of the RMSNORM/SWIGLU/GQA/ROPE scheduler
+ *                         branches; closed forms (rope is a rotation:
+ *                         norms kept, inverse at -pos; GQA with Hkv = Hq is
+ *                         oracle_attention; decode = last row of causal
+ *                         attention over the cache)
  *   oracle_quantize_i8/matmul_i8/conv2d_i8
  *                         golden vectors of the compiled reference's int8
  *                         MATMUL branch and int8 conv route; int32 sums
@@ -99,6 +107,16 @@ void oracle_maxpool2d(double* out, const double* in, size_t N, size_t C, size_t 
                       size_t stride);
 void oracle_maxpool2d_bwd(double* dx, const double* dy, const double* x, size_t N, size_t C, size_t H, size_t W,
                           size_t Ho, size_t Wo, size_t K, size_t stride);
+
+/* Decode-side attention family (B/src/math/lancius_kernels.c:248-272, 338-448). */
+void oracle_rmsnorm(double* out, const double* in, const double* gamma, size_t rows, size_t hidden, double eps);
+void oracle_swiglu(double* out, const double* gate, const double* up, size_t n);
+void oracle_rope(double* out, const double* in, size_t count, size_t batch, size_t S, size_t H, size_t hd,
+                 int pos_offset);
+void oracle_attention_gqa(double* out, const double* q, const double* k, const double* v, size_t batch, size_t Sq,
+                          size_t Skv, size_t Hq, size_t Hkv, size_t D, int causal, double scale);
+void oracle_attention_decode(double* out, const double* q, const double* k, const double* v, const int32_t* lens,
+                             size_t batch, size_t Skv, size_t Hq, size_t Hkv, size_t D, double scale);
 
 /* The int8 path (B/src/runtime/lancius_scheduler.c:195-220,
  * B/src/math/lancius_kernels.c:177-210, B/src/runtime/lancius_vision_ops.c:16-57,

@@ -157,6 +157,7 @@ def main() -> None:
     bg.destroy()
     training_op_vectors(ref, k)
     int8_vectors(ref, k)
+    decode_vectors(ref, k)
     np.savez_compressed(OUT / "kernels.npz", **k)
 
     # schedules and plans
@@ -369,6 +370,67 @@ def int8_vectors(ref, k: dict) -> None:
     ref.kernel_conv2d_int8_fwd(p(out), xq.ctypes.data_as(I8), wq.ctypes.data_as(I8), 0.01, 0.002,
                                1, 3, 11, 10, 4, 5, 5, 2, 2)
     k["i8k_xq"], k["i8k_wq"], k["i8k_out"] = xq, wq, out
+
+
+def decode_vectors(ref, k: dict) -> None:
+    """Golden vectors of the decode-side family: kernel_rmsnorm, kernel_swiglu,
+    kernel_rope, kernel_gqa, kernel_attention_kv_cache (lancius_kernels.c:
+    248-272, 338-448) and the RMSNORM / SWIGLU / GQA / ROPE scheduler branches
+    (lancius_scheduler.c:134-165)."""
+    x = f32(prng.normal(40, (5, 12), 0.3, 2.0))
+    g = f32(prng.normal(41, (12,), 1.0, 0.2))
+    out = np.zeros((5, 12))
+    ref.kernel_rmsnorm(p(out), p(x), p(g), 5, 12, 1e-5)
+    k["rms_x"], k["rms_g"], k["rms_out"] = x, g, out
+    gate = f32(prng.normal(42, (64,), std=5.0))
+    gate[:4] = [0.0, 80.0, -80.0, -700.0]
+    up = f32(prng.normal(43, (64,)))
+    out = np.zeros(64)
+    ref.kernel_swiglu(p(out), p(gate), p(up), 64)
+    k["swiglu_gate"], k["swiglu_up"], k["swiglu_out"] = gate, up, out
+    # rope: q and k [1, 7, 3, 8] rotated in place, positions from 5
+    q = f32(prng.normal(44, (1, 7, 3, 8)))
+    kk = f32(prng.normal(45, (1, 7, 3, 8)))
+    qr, kr = q.copy(), kk.copy()
+    ref.kernel_rope(p(qr), p(kr), 1, 7, 3, 8, 5)
+    k["rope_q"], k["rope_k"], k["rope_q_out"], k["rope_k_out"] = q, kk, qr, kr
+    # gqa: q [9, 6, 8], k/v [9, 2, 8], causal
+    q = f32(prng.uniform(46, (9, 6, 8), -1.0, 1.0))
+    kv = [f32(prng.uniform(47 + i, (9, 2, 8), -1.0, 1.0)) for i in range(2)]
+    out = np.zeros((9, 6, 8))
+    ref.kernel_gqa(p(out), p(q), p(kv[0]), p(kv[1]), 9, 6, 2, 8)
+    k["gqa_q"], k["gqa_k"], k["gqa_v"], k["gqa_out"] = q, kv[0], kv[1], out
+    # kv-cache decode: one query [4 heads x 16], caches [13, 4, 16]
+    q = f32(prng.uniform(49, (4, 16), -1.0, 1.0))
+    kc, vc = f32(prng.uniform(50, (13, 4, 16), -1.0, 1.0)), f32(prng.uniform(51, (13, 4, 16), -1.0, 1.0))
+    out = np.zeros((4, 16))
+    ref.kernel_attention_kv_cache(p(out), p(q), p(kc), p(vc), 13, 4, 16)
+    k["kvc_q"], k["kvc_k"], k["kvc_v"], k["kvc_out"] = q, kc, vc, out
+    # scheduler branches
+    k["node_rms_out"] = ref_op(ref, {"x": (5, 12), "g": (1, 12)}, lambda gg, i: ref.lancius_rmsnorm(gg, i["x"], i["g"]),
+                               {"x": k["rms_x"], "g": k["rms_g"][None, :]})
+    k["node_swiglu_out"] = ref_op(ref, {"a": (8, 8), "b": (8, 8)}, lambda gg, i: ref.lancius_swiglu(gg, i["a"], i["b"]),
+                                  {"a": gate.reshape(8, 8), "b": up.reshape(8, 8)})
+
+    def gqa_node(gg, i):
+        q3 = ref.lancius_reshape(gg, i["q"], 3, 9, 6, 8, 0)
+        k3 = ref.lancius_reshape(gg, i["k"], 3, 9, 2, 8, 0)
+        v3 = ref.lancius_reshape(gg, i["v"], 3, 9, 2, 8, 0)
+        return ref.lancius_gqa(gg, q3, k3, v3, 6, 2)
+
+    k["node_gqa_out"] = ref_op(ref, {"q": (9, 48), "k": (9, 16), "v": (9, 16)}, gqa_node,
+                               {"q": k["gqa_q"].reshape(9, 48), "k": k["gqa_k"].reshape(9, 16),
+                                "v": k["gqa_v"].reshape(9, 16)})
+
+    def rope_node(gg, i):
+        x3 = ref.lancius_reshape(gg, i["x"], 3, 7, 3, 16, 0)
+        n = ref.lancius_relu(gg, x3)  # a unary node of x3's shape, re-opcoded: the reference has no ROPE builder
+        n.contents.op = abi.OP["ROPE"]
+        return n
+
+    xr = f32(prng.normal(52, (7, 48)))
+    k["node_rope_x"] = xr
+    k["node_rope_out"] = ref_op(ref, {"x": (7, 48)}, rope_node, {"x": xr})
 
 
 TRAIN_GRAPHS = {
