@@ -144,7 +144,9 @@ def decode_cases(dev, steps, warmup) -> dict:
     nb = 8.0 * rows * hid
     out["rmsnorm_4096x4096"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
                                 "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
-    t = time_steps(dev, lambda: dev.swiglu(y, x, x, rows * hid), steps, warmup)
+    u = dev.upload(prng.normal(67, (rows, hid)))
+    t = time_steps(dev, lambda: dev.swiglu(y, x, u, rows * hid), steps, warmup)
+    u.free()
     nb = 12.0 * rows * hid
     out["swiglu_4096x4096"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
                                "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
@@ -268,6 +270,21 @@ def rowop_cases(dev, steps, warmup) -> dict:
     t = time_steps(dev, lambda: dev.softmax(y, None, x, rows, hid), steps, warmup)
     out["softmax_4096x1024"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
                                 "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
+    for buf in (x, g, b, y):
+        buf.free()
+    # HBM-sized rows (256 MiB in, 256 MiB out: past the 256 MB MALL)
+    rows, hid = 16384, 4096
+    x = dev.upload(prng.normal(46, (rows, hid)))
+    g = dev.upload(np.ones((hid,), np.float32))
+    b = dev.upload(np.zeros((hid,), np.float32))
+    y = dev.alloc(rows * hid * 4)
+    nb = 8.0 * rows * hid
+    for name, fn in (("layernorm", lambda: dev.layernorm(y, x, g, b, rows, hid)),
+                     ("softmax", lambda: dev.softmax(y, None, x, rows, hid)),
+                     ("rmsnorm", lambda: dev.rmsnorm(y, x, g, rows, hid))):
+        t = time_steps(dev, fn, steps, warmup)
+        out[f"{name}_{rows}x{hid}"] = {"ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1),
+                                       "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
     n = 4096 * 4096
     u = dev.upload(prng.normal(48, (n,)))
     v = dev.upload(prng.normal(49, (n,)))

@@ -286,17 +286,24 @@ __global__ void __launch_bounds__(256) attention_rowwise(const AttnParams p) {
 
 // ---- decode: one query token per sequence against a K/V cache --------------
 //
-// HBM-bound (every cached key and value is read once), so the kernel is built
-// around that read and the VALU does the arithmetic:
-//  * workgroup (sequence b, K/V head hk, split s) owns keys
-//    [s*chunk, min((s+1)*chunk, len_b)) and all G = Hq/Hkv query heads that
-//    share hk (grouped-query attention reads each K/V row once for the group);
-//  * 64-key tiles of K and V are staged in LDS with coalesced float4 loads;
-//    wave w takes query heads w, w+4, ...: lane = key for the scores (one
-//    dot product per lane over D from LDS), wave-wide max / sum for the
-//    online softmax, then lane = d for P.V;
-//  * each split stores (m, l, o[D]) per query head; decode_combine merges
-//    the splits in split order (deterministic).
+// HBM-bound: every cached key and value is read once, so the kernel streams
+// K and V straight from HBM into registers and keeps the VALU work under the
+// read time.
+//  * workgroup (sequence b, K/V head hk, split s, head chunk c) owns keys
+//    [s*chunk, min((s+1)*chunk, len_b)) and query heads c*GT .. c*GT+GT-1 of
+//    the G = Hq/Hkv heads that share hk (one K/V read serves the chunk);
+//  * 16 lanes own one key row: lane l16 holds NV of its D values (float4
+//    pieces d = 4*l16 + 64*j when D % 4 == 0 and the pointers are 16-byte
+//    aligned, else d = l16 + 16*i), so a key row is one coalesced 256/512-byte
+//    read; a wave runs 4 such key streams, the workgroup 16;
+//  * each stream takes UNR keys per step (stream t reads keys base + 16u + t),
+//    with the next step's rows loading into a second register buffer, forms
+//    the scores with a DPP sum over its 16 lanes and keeps its own online
+//    softmax (m, l, o) per head in the log2 domain;
+//  * the 16 streams merge in a fixed order (xor butterfly over the 4 streams
+//    of a wave, then the 4 waves in order through LDS), so results do not
+//    depend on timing; one split writes the normalised output directly, more
+//    splits write (o, m, l) partials that decode_combine merges in split order.
 // kernel_attention_kv_cache (lancius_kernels.c:338-379) is batch = 1,
 // Hq = Hkv, no mask, scale 1/sqrt(D).
 struct DecodeParams {
@@ -307,98 +314,227 @@ struct DecodeParams {
     const int32_t* lens;    // per-sequence cache length (<= Skv) or null
     float* part;            // [B*Hkv][splits][G][D + 2]
     int B, Skv, Hq, Hkv, D, G;
-    int splits, chunk;
-    float scale;
+    int splits, chunk, hchunks;
+    float qscale;           // softmax scale * log2(e)
 };
 
-constexpr int kDecKeys = 64;
-constexpr int kDecMaxD = 128;  // LDS: 64 keys x (D+1 + D) floats = 66 KB at D = 128
+constexpr int kDecMaxD = 128;
 
-__global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
-    __shared__ float Ks[kDecKeys][kDecMaxD + 1];
-    __shared__ float Vs[kDecKeys][kDecMaxD];
-    const int bh = blockIdx.x, split = blockIdx.y;
-    const int b = bh / p.Hkv, hk = bh - (bh / p.Hkv) * p.Hkv;
-    const int D = p.D, G = p.G;
-    const int len = p.lens ? min(max(p.lens[b], 0), p.Skv) : p.Skv;
-    const int k0 = split * p.chunk, k1 = min(len, k0 + p.chunk);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const size_t kv_row = (size_t)p.Hkv * D;
-    const float* kb = p.k + ((size_t)b * p.Skv * p.Hkv + hk) * D;
-    const float* vb = p.v + ((size_t)b * p.Skv * p.Hkv + hk) * D;
-    // per query head of this wave: running max, sum, and o[d] for d = lane + 64 i
-    constexpr int kMaxRowsPerWave = 16;
-    constexpr int kDPerLane = kDecMaxD / 64;
-    float m_run[kMaxRowsPerWave], l_run[kMaxRowsPerWave], o_run[kMaxRowsPerWave][kDPerLane];
+template <int NV, bool VEC>
+__device__ __forceinline__ void load_piece(const float* __restrict__ row, int l16, int D, float (&x)[NV]) {
+    if constexpr (VEC) {
 #pragma unroll
-    for (int r = 0; r < kMaxRowsPerWave; ++r) {
-        m_run[r] = -INFINITY;
-        l_run[r] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kDPerLane; ++i) o_run[r][i] = 0.0f;
-    }
-    for (int t0 = k0; t0 < k1; t0 += kDecKeys) {
-        const int nk = min(kDecKeys, k1 - t0);
-        __syncthreads();  // previous tile fully consumed
-        for (int idx = tid; idx < kDecKeys * D; idx += 256) {
-            const int key = idx / D, d = idx - (idx / D) * D;
-            const bool in = key < nk;
-            Ks[key][d] = in ? kb[(size_t)(t0 + key) * kv_row + d] : 0.0f;
-            Vs[key][d] = in ? vb[(size_t)(t0 + key) * kv_row + d] : 0.0f;
+        for (int j = 0; j < NV / 4; ++j) {
+            const int d = 4 * l16 + 64 * j;
+            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (d < D) t = *reinterpret_cast<const float4*>(row + d);
+            x[4 * j] = t.x;
+            x[4 * j + 1] = t.y;
+            x[4 * j + 2] = t.z;
+            x[4 * j + 3] = t.w;
         }
-        __syncthreads();
+    } else {
 #pragma unroll
-        for (int r = 0; r < kMaxRowsPerWave; ++r) {
-            const int row = wave + 4 * r;  // query head within the group
-            if (row >= G) break;
-            const float* qr = p.q + ((size_t)b * p.Hq + (size_t)hk * G + row) * D;
-            // score of key `lane`
-            float sc = 0.0f;
-            for (int d = 0; d < D; ++d) sc += qr[d] * Ks[lane][d];
-            sc = lane < nk ? sc * p.scale : -INFINITY;
-            float mx = sc;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-            const float m_new = fmaxf(m_run[r], mx);
-            const float corr = expf(m_run[r] - m_new);  // 0 on the first tile (m_run = -inf)
-            const float pk = lane < nk ? expf(sc - m_new) : 0.0f;
-            float ps = pk;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) ps += __shfl_xor(ps, off);
-            l_run[r] = l_run[r] * corr + ps;
-            m_run[r] = m_new;
-#pragma unroll
-            for (int i = 0; i < kDPerLane; ++i) o_run[r][i] *= corr;
-            for (int key = 0; key < nk; ++key) {
-                const float pj = __shfl(pk, key);
-#pragma unroll
-                for (int i = 0; i < kDPerLane; ++i) {
-                    const int d = lane + 64 * i;
-                    if (d < D) o_run[r][i] += pj * Vs[key][d];
-                }
-            }
-        }
-    }
-    // partial of this split
-    float* part = p.part + (((size_t)bh * p.splits + split) * G) * (D + 2);
-#pragma unroll
-    for (int r = 0; r < kMaxRowsPerWave; ++r) {
-        const int row = wave + 4 * r;
-        if (row >= G) break;
-        float* pr = part + (size_t)row * (D + 2);
-#pragma unroll
-        for (int i = 0; i < kDPerLane; ++i) {
-            const int d = lane + 64 * i;
-            if (d < D) pr[d] = o_run[r][i];
-        }
-        if (lane == 0) {
-            pr[D] = m_run[r];
-            pr[D + 1] = l_run[r];
+        for (int i = 0; i < NV; ++i) {
+            const int d = l16 + 16 * i;
+            x[i] = d < D ? row[d] : 0.0f;
         }
     }
 }
 
-// out = sum_s o_s exp(m_s - m) / sum_s l_s exp(m_s - m), m = max_s m_s; one
+// Sum over the 16 lanes of a row with DPP moves (xor 1, xor 2 in the quad,
+// then half-row and row mirrors, which pair each lane with one of the other
+// half once the halves are uniform); every lane of the row gets the same sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp_mov<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp_mov<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp_mov<0x141>(x);  // row_half_mirror
+    x += dpp_mov<0x140>(x);  // row_mirror
+    return x;
+}
+
+template <int NV, bool VEC>
+__device__ __forceinline__ int piece_d(int l16, int i) {
+    if constexpr (VEC) return 4 * l16 + 64 * (i / 4) + (i & 3);
+    else return l16 + 16 * i;
+}
+
+// (m, l, o) <- merge of itself and (m2, l2, o2); m = -inf means empty.
+template <int NV>
+__device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[NV], float m2, float l2,
+                                            const float (&o2)[NV]) {
+    const float mn = fmaxf(m, m2);
+    const float a = m > -INFINITY ? exp2f(m - mn) : 0.0f;
+    const float c = m2 > -INFINITY ? exp2f(m2 - mn) : 0.0f;
+    l = l * a + l2 * c;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) o[i] = o[i] * a + o2[i] * c;
+    m = mn;
+}
+
+template <int NV, bool VEC, int GT, int UNR>
+__global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
+    __shared__ float red[4][GT][kDecMaxD + 2];
+    // XCD-aware order: consecutive workgroups go to different XCDs, so logical
+    // ids are dealt out in contiguous runs per XCD (the head chunks of one
+    // key range then share that XCD's L2).
+    const int n = gridDim.x, id = blockIdx.x;
+    const int full = n & ~7;
+    const int lid = id < full ? (id & 7) * (full >> 3) + (id >> 3) : id;
+    const int hc = lid % p.hchunks;
+    const int rest = lid / p.hchunks;
+    const int split = rest % p.splits;
+    const int bh = rest / p.splits;
+    const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
+    const int D = p.D, G = p.G;
+    const int len = p.lens ? min(max(p.lens[b], 0), p.Skv) : p.Skv;
+    const int k0 = split * p.chunk, k1 = min(len, k0 + p.chunk);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l16 = lane & 15, stream = wave * 4 + (lane >> 4);
+    const size_t kv_row = (size_t)p.Hkv * D;
+    const float* kb = p.k + ((size_t)b * p.Skv * p.Hkv + hk) * D;
+    const float* vb = p.v + ((size_t)b * p.Skv * p.Hkv + hk) * D;
+    const int h0 = hc * GT;
+
+    float qv[GT][NV], o[GT][NV], m[GT], l[GT];
+#pragma unroll
+    for (int h = 0; h < GT; ++h) {
+        if (h0 + h < G) {
+            load_piece<NV, VEC>(p.q + ((size_t)b * p.Hq + (size_t)hk * G + h0 + h) * D, l16, D, qv[h]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) qv[h][i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            qv[h][i] *= p.qscale;
+            o[h][i] = 0.0f;
+        }
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+    }
+
+    // keys past the range re-read the last row (no branch, so every load
+    // stays ahead of the arithmetic) and are masked
+    auto fetch = [&](int base, float (&kr)[UNR][NV], float (&vr)[UNR][NV], bool (&valid)[UNR]) {
+#pragma unroll
+        for (int u = 0; u < UNR; ++u) {
+            const int key = base + 16 * u + stream;
+            valid[u] = key < k1;
+            const size_t row = (size_t)(valid[u] ? key : k1 - 1) * kv_row;
+            load_piece<NV, VEC>(kb + row, l16, D, kr[u]);
+            load_piece<NV, VEC>(vb + row, l16, D, vr[u]);
+        }
+    };
+    auto consume = [&](const float (&kr)[UNR][NV], const float (&vr)[UNR][NV], const bool (&valid)[UNR]) {
+#pragma unroll
+        for (int h = 0; h < GT; ++h) {
+            float sc[UNR];
+            float mx = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int i = 0; i < NV; ++i) acc += qv[h][i] * kr[u][i];
+                acc = row_sum16(acc);
+                sc[u] = valid[u] ? acc : -INFINITY;
+                mx = fmaxf(mx, sc[u]);
+            }
+            // branch-free: while the stream has seen no key, m = mn = -inf,
+            // corr = 0 and every p = 0, so (o, l) stay 0
+            const float mn = fmaxf(m[h], mx);
+            const float corr = m[h] > -INFINITY ? exp2f(m[h] - mn) : 0.0f;
+            float ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) o[h][i] *= corr;
+#pragma unroll
+            for (int u = 0; u < UNR; ++u) {
+                const float pu = valid[u] ? exp2f(sc[u] - mn) : 0.0f;
+                ps += pu;
+#pragma unroll
+                for (int i = 0; i < NV; ++i) o[h][i] += pu * vr[u][i];
+            }
+            l[h] = l[h] * corr + ps;
+            m[h] = mn;
+        }
+    };
+    // two register buffers: the next step's rows are in flight while the
+    // current step's arithmetic runs
+    float ka[UNR][NV], va[UNR][NV], kn[UNR][NV], vn[UNR][NV];
+    bool oka[UNR], okn[UNR];
+    constexpr int kStep = 16 * UNR;
+    int base = k0;
+    if (base < k1) fetch(base, ka, va, oka);
+    while (base < k1) {
+        if (base + kStep < k1) fetch(base + kStep, kn, vn, okn);
+        consume(ka, va, oka);
+        base += kStep;
+        if (base >= k1) break;
+        if (base + kStep < k1) fetch(base + kStep, ka, va, oka);
+        consume(kn, vn, okn);
+        base += kStep;
+    }
+
+    // merge the 4 streams of each wave, then the 4 waves in order
+#pragma unroll
+    for (int h = 0; h < GT; ++h) {
+#pragma unroll
+        for (int off = 16; off <= 32; off <<= 1) {
+            float o2[NV];
+#pragma unroll
+            for (int i = 0; i < NV; ++i) o2[i] = __shfl_xor(o[h][i], off);
+            const float m2 = __shfl_xor(m[h], off), l2 = __shfl_xor(l[h], off);
+            merge_state<NV>(m[h], l[h], o[h], m2, l2, o2);
+        }
+        if (lane < 16) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int d = piece_d<NV, VEC>(l16, i);
+                if (d < D) red[wave][h][d] = o[h][i];
+            }
+            if (lane == 0) {
+                red[wave][h][kDecMaxD] = m[h];
+                red[wave][h][kDecMaxD + 1] = l[h];
+            }
+        }
+    }
+    __syncthreads();
+    const int nh = min(GT, G - h0);
+    for (int idx = tid; idx < nh * D; idx += 256) {
+        const int h = idx / D, d = idx - (idx / D) * D;
+        float mm = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) mm = fmaxf(mm, red[w][h][kDecMaxD]);
+        float ll = 0.0f, oo = 0.0f;
+        if (mm > -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float mw = red[w][h][kDecMaxD];
+                const float a = mw > -INFINITY ? exp2f(mw - mm) : 0.0f;
+                ll += red[w][h][kDecMaxD + 1] * a;
+                oo += red[w][h][d] * a;
+            }
+        }
+        const int hq = hk * G + h0 + h;
+        if (p.splits == 1) {
+            p.out[((size_t)b * p.Hq + hq) * D + d] = ll > 0.0f ? oo / ll : 0.0f;
+        } else {
+            float* pr = p.part + (((size_t)bh * p.splits + split) * G + h0 + h) * (D + 2);
+            pr[d] = oo;
+            if (d == 0) {
+                pr[D] = mm;
+                pr[D + 1] = ll;
+            }
+        }
+    }
+}
+
+// out = sum_s o_s 2^(m_s - m) / sum_s l_s 2^(m_s - m), m = max_s m_s; one
 // wave per (sequence, query head), splits in order.  A sequence with no keys
 // gets zeros.
 __global__ void __launch_bounds__(256) decode_combine(const DecodeParams p) {
@@ -415,7 +551,7 @@ __global__ void __launch_bounds__(256) decode_combine(const DecodeParams p) {
     float l = 0.0f;
     for (int s = 0; s < p.splits; ++s) {
         const float ms = base[s * sstride + D];
-        if (ms > -INFINITY) l += base[s * sstride + D + 1] * expf(ms - m);
+        if (ms > -INFINITY) l += base[s * sstride + D + 1] * exp2f(ms - m);
     }
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     float* o = p.out + ((size_t)b * p.Hq + hq) * D;
@@ -423,9 +559,19 @@ __global__ void __launch_bounds__(256) decode_combine(const DecodeParams p) {
         float acc = 0.0f;
         for (int s = 0; s < p.splits; ++s) {
             const float ms = base[s * sstride + D];
-            if (ms > -INFINITY) acc += base[s * sstride + d] * expf(ms - m);
+            if (ms > -INFINITY) acc += base[s * sstride + d] * exp2f(ms - m);
         }
         o[d] = acc * inv;
+    }
+}
+
+template <int NV, bool VEC>
+void launch_decode(const DecodeParams& p, unsigned grid, hipStream_t stream, int gt) {
+    switch (gt) {
+        case 1: hipLaunchKernelGGL((attention_decode<NV, VEC, 1, 4>), dim3(grid), dim3(256), 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((attention_decode<NV, VEC, 2, 4>), dim3(grid), dim3(256), 0, stream, p); break;
+        case 4: hipLaunchKernelGGL((attention_decode<NV, VEC, 4, 4>), dim3(grid), dim3(256), 0, stream, p); break;
+        default: hipLaunchKernelGGL((attention_decode<NV, VEC, 8, 2>), dim3(grid), dim3(256), 0, stream, p); break;
     }
 }
 
@@ -520,9 +666,8 @@ int lancius_hip_attention_decode_f32(lancius_hip_ctx* ctx, float* out, const flo
     LANCIUS_REQUIRE(ctx && out && q && k_cache && v_cache, LANCIUS_HIP_ERR_NULL_PTR, "attention_decode: NULL argument");
     LANCIUS_REQUIRE(batch >= 1 && H_q >= 1 && H_kv >= 1 && D >= 1 && H_q % H_kv == 0, LANCIUS_HIP_ERR_SHAPE,
                     "attention_decode: batch=%zu H_q=%zu H_kv=%zu D=%zu", batch, H_q, H_kv, D);
-    LANCIUS_REQUIRE(D <= kDecMaxD && H_q / H_kv <= 64 && S_kv < (1u << 30) && batch * H_kv < kMaxGridX,
-                    LANCIUS_HIP_ERR_SHAPE, "attention_decode: D=%zu (<= %d) or group %zu (<= 64) unsupported", D,
-                    kDecMaxD, H_q / H_kv);
+    LANCIUS_REQUIRE(D <= kDecMaxD && S_kv >= 1 && S_kv < (1u << 30) && H_q < 65536, LANCIUS_HIP_ERR_SHAPE,
+                    "attention_decode: D=%zu (<= %d), S_kv=%zu or H_q=%zu unsupported", D, kDecMaxD, S_kv, H_q);
     if (int rc = bind_device(ctx)) return rc;
     DecodeParams p{};
     p.out = out;
@@ -536,24 +681,38 @@ int lancius_hip_attention_decode_f32(lancius_hip_ctx* ctx, float* out, const flo
     p.Hkv = (int)H_kv;
     p.D = (int)D;
     p.G = (int)(H_q / H_kv);
-    p.scale = scale;
-    // ~2 workgroups per CU in all, each split >= 256 keys
+    p.qscale = scale * 1.4426950408889634f;  // log2(e)
+    const int gt = p.G <= 1 ? 1 : p.G <= 2 ? 2 : p.G <= 4 ? 4 : 8;
+    const size_t hchunks = ((size_t)p.G + gt - 1) / gt;
+    // about 2 workgroups per CU in all (longer key ranges beat more
+    // workgroups here), each split >= 256 keys
     const size_t seqs = batch * H_kv;
-    size_t splits = std::max<size_t>(1, std::min<size_t>((512 + seqs - 1) / seqs, (S_kv + 255) / 256));
-    splits = std::min<size_t>(splits, 65535);
-    const size_t chunk = std::max<size_t>(kDecKeys, (S_kv + splits - 1) / splits);
-    splits = std::max<size_t>(1, (S_kv + chunk - 1) / chunk);
+    const size_t tasks = seqs * hchunks;
+    size_t splits = std::max<size_t>(1, std::min<size_t>((512 + tasks - 1) / tasks, (S_kv + 255) / 256));
+    const size_t chunk = (S_kv + splits - 1) / splits;
+    splits = (S_kv + chunk - 1) / chunk;
+    LANCIUS_REQUIRE(tasks * splits < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention_decode: too many heads");
     p.splits = (int)splits;
     p.chunk = (int)chunk;
-    void* ws = nullptr;
-    if (int rc = workspace(ctx, seqs * splits * p.G * (D + 2) * sizeof(float), &ws)) return rc;
-    p.part = (float*)ws;
-    hipLaunchKernelGGL(attention_decode, dim3((unsigned)seqs, (unsigned)splits), dim3(256), 0, ctx->stream, p);
+    p.hchunks = (int)hchunks;
+    if (splits > 1) {
+        void* ws = nullptr;
+        if (int rc = workspace(ctx, seqs * splits * p.G * (D + 2) * sizeof(float), &ws)) return rc;
+        p.part = (float*)ws;
+    }
+    const bool vec = D % 4 == 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
+    const unsigned grid = (unsigned)(tasks * splits);
+    if (vec && D > 64) launch_decode<8, true>(p, grid, ctx->stream, gt);
+    else if (vec) launch_decode<4, true>(p, grid, ctx->stream, gt);
+    else if (D > 64) launch_decode<8, false>(p, grid, ctx->stream, gt);
+    else launch_decode<4, false>(p, grid, ctx->stream, gt);
     if (int rc = check_launch("attention_decode")) return rc;
-    const size_t rows = batch * H_q;
-    LANCIUS_REQUIRE((rows + 3) / 4 < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention_decode: too many heads");
-    hipLaunchKernelGGL(decode_combine, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream, p);
-    if (int rc = check_launch("decode_combine")) return rc;
+    if (splits > 1) {
+        const size_t rows = batch * H_q;
+        LANCIUS_REQUIRE((rows + 3) / 4 < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention_decode: too many heads");
+        hipLaunchKernelGGL(decode_combine, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream, p);
+        if (int rc = check_launch("decode_combine")) return rc;
+    }
     return ok();
 }
 

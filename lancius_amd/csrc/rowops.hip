@@ -27,38 +27,52 @@ __device__ __forceinline__ float wave_max(float v) {
 constexpr int kRowThreads = 256;  // 4 rows per workgroup
 constexpr int kRowsPerBlock = kRowThreads / 64;
 
-// LayerNorm, NV float4 per lane (hidden == 256 * NV), row cached in registers.
-// Statistics follow bleeding/v11A1/src/math/lancius_kernels.c:217-236: mean,
-// then the biased variance of (x - mean), then (x - mean) * inv_std * g + b.
+// Rows held in registers: lane owns float4 pieces at columns 4*lane + 256*i
+// (i < NV) of a row of `cols` <= 256*NV columns, cols % 4 == 0 and 16-byte
+// aligned; pieces past the row are not loaded and are left out of every
+// statistic.
+template <int NV>
+__device__ __forceinline__ void load_row_f4(const float* __restrict__ x, int cols, int lane, f32x4 (&v)[NV]) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * lane + 256 * i;
+        v[i] = c0 < cols ? *(const f32x4*)(x + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
+// LayerNorm with the row in registers.  Statistics follow
+// bleeding/v11A1/src/math/lancius_kernels.c:217-236: mean, then the biased
+// variance of (x - mean), then (x - mean) * inv_std * g + b.
 template <int NV>
 __global__ void __launch_bounds__(kRowThreads) layernorm_regs(float* __restrict__ out, const float* __restrict__ in,
                                                               const float* __restrict__ gamma,
-                                                              const float* __restrict__ beta, int rows, float eps) {
+                                                              const float* __restrict__ beta, int rows, int H,
+                                                              float eps) {
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
-    constexpr int H = 256 * NV;
     const float* x = in + (size_t)row * H;
     f32x4 v[NV];
+    load_row_f4<NV>(x, H, lane, v);
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        v[i] = *(const f32x4*)(x + 4 * lane + 256 * i);
-        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    }
-    const float mean = wave_sum(s) * (1.0f / H);
+    for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    const float mean = wave_sum(s) / (float)H;
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
-        q += (a * a + b * b) + (c * c + d * d);
+        if (4 * lane + 256 * i < H) {
+            const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+            q += (a * a + b * b) + (c * c + d * d);
+        }
     }
-    const float var = wave_sum(q) * (1.0f / H);
+    const float var = wave_sum(q) / (float)H;
     const float inv_std = 1.0f / sqrtf(var + eps);
     float* y = out + (size_t)row * H;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c0 = 4 * lane + 256 * i;
+        if (c0 >= H) continue;
         const f32x4 g = *(const f32x4*)(gamma + c0);
         const f32x4 b = *(const f32x4*)(beta + c0);
         f32x4 o;
@@ -68,6 +82,15 @@ __global__ void __launch_bounds__(kRowThreads) layernorm_regs(float* __restrict_
         o.w = (v[i].w - mean) * inv_std * g.w + b.w;
         *(f32x4*)(y + c0) = o;
     }
+}
+
+// Smallest register-row width (float4 pieces per lane) for `cols`, 0 if the
+// row does not fit 16 pieces or is not float4-shaped.
+int regs_width(size_t cols, bool aligned) {
+    if (!aligned || cols % 4 != 0 || cols > 4096) return 0;
+    for (int nv = 1; nv <= 16; nv *= 2)
+        if (cols <= (size_t)256 * nv) return nv;
+    return 0;
 }
 
 // Any hidden size: three passes over the row (re-reads hit L2).
@@ -122,6 +145,68 @@ __global__ void __launch_bounds__(kRowThreads) softmax_rows(float* __restrict__ 
         }
     }
     (void)inv;
+    if (argmax) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ob = __shfl_xor(best, off);
+            const int oi = __shfl_xor(best_i, off);
+            if (ob > best || (ob == best && oi < best_i)) {
+                best = ob;
+                best_i = oi;
+            }
+        }
+        if (lane == 0) argmax[row] = best_i == 0x7fffffff ? 0 : best_i;
+    }
+}
+
+
+// softmax_rows with the row in registers: one read of x, exp once per element.
+template <int NV>
+__global__ void __launch_bounds__(kRowThreads) softmax_regs(float* __restrict__ probs, int32_t* __restrict__ argmax,
+                                                            const float* __restrict__ in, int rows, int cols) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    f32x4 v[NV];
+    load_row_f4<NV>(in + (size_t)row * cols, cols, lane, v);
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if (4 * lane + 256 * i < cols) m = fmaxf(m, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if (4 * lane + 256 * i < cols) {
+            v[i].x = expf(v[i].x - m);
+            v[i].y = expf(v[i].y - m);
+            v[i].z = expf(v[i].z - m);
+            v[i].w = expf(v[i].w - m);
+            s += v[i].x;
+            s += v[i].y;
+            s += v[i].z;
+            s += v[i].w;
+        }
+    }
+    s = wave_sum(s);
+    float best = -1e9f;
+    int best_i = 0x7fffffff;
+    float* y = probs + (size_t)row * cols;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * lane + 256 * i;
+        if (c0 >= cols) continue;
+        f32x4 pv;
+        pv.x = v[i].x / s;
+        pv.y = v[i].y / s;
+        pv.z = v[i].z / s;
+        pv.w = v[i].w / s;
+        *(f32x4*)(y + c0) = pv;
+        if (pv.x > best) { best = pv.x; best_i = c0; }
+        if (pv.y > best) { best = pv.y; best_i = c0 + 1; }
+        if (pv.z > best) { best = pv.z; best_i = c0 + 2; }
+        if (pv.w > best) { best = pv.w; best_i = c0 + 3; }
+    }
     if (argmax) {
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) {
@@ -256,6 +341,40 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_rows(float* __restrict__ 
     const float inv = 1.0f / sqrtf(q / (float)hidden + eps);
     float* y = out + (size_t)row * hidden;
     for (int c = lane; c < hidden; c += 64) y[c] = (x[c] * inv) * gamma[c];
+}
+
+template <int NV>
+__global__ void __launch_bounds__(kRowThreads) rmsnorm_regs(float* __restrict__ out, const float* __restrict__ in,
+                                                            const float* __restrict__ gamma, int rows, int hidden,
+                                                            float eps) {
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    f32x4 v[NV];
+    load_row_f4<NV>(in + (size_t)row * hidden, hidden, lane, v);
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        q += v[i].x * v[i].x;
+        q += v[i].y * v[i].y;
+        q += v[i].z * v[i].z;
+        q += v[i].w * v[i].w;
+    }
+    q = wave_sum(q);
+    const float inv = 1.0f / sqrtf(q / (float)hidden + eps);
+    float* y = out + (size_t)row * hidden;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * lane + 256 * i;
+        if (c0 >= hidden) continue;
+        const f32x4 g = *(const f32x4*)(gamma + c0);
+        f32x4 o;
+        o.x = (v[i].x * inv) * g.x;
+        o.y = (v[i].y * inv) * g.y;
+        o.z = (v[i].z * inv) * g.z;
+        o.w = (v[i].w * inv) * g.w;
+        *(f32x4*)(y + c0) = o;
+    }
 }
 
 // SwiGLU (lancius_kernels.c:398-405): out = g / (1 + exp(-g)) * up.
@@ -399,20 +518,18 @@ int lancius_hip_layernorm_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     if (rows == 0) return ok();
     if (int rc = bind_device(ctx)) return rc;
     const dim3 grid(ceil_div(rows, kRowsPerBlock)), block(kRowThreads);
-    const bool vec = aligned16(out) && aligned16(in) && aligned16(gamma) && aligned16(beta);
-    const int r = (int)rows;
-    if (vec && hidden == 256)
-        hipLaunchKernelGGL(layernorm_regs<1>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
-    else if (vec && hidden == 512)
-        hipLaunchKernelGGL(layernorm_regs<2>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
-    else if (vec && hidden == 1024)
-        hipLaunchKernelGGL(layernorm_regs<4>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
-    else if (vec && hidden == 2048)
-        hipLaunchKernelGGL(layernorm_regs<8>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
-    else if (vec && hidden == 4096)
-        hipLaunchKernelGGL(layernorm_regs<16>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, eps);
-    else
-        hipLaunchKernelGGL(layernorm_any, grid, block, 0, ctx->stream, out, in, gamma, beta, r, (int)hidden, eps);
+    const int r = (int)rows, h = (int)hidden;
+    switch (regs_width(hidden, aligned16(out) && aligned16(in) && aligned16(gamma) && aligned16(beta))) {
+        case 1: hipLaunchKernelGGL(layernorm_regs<1>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
+        case 2: hipLaunchKernelGGL(layernorm_regs<2>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
+        case 4: hipLaunchKernelGGL(layernorm_regs<4>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
+        case 8: hipLaunchKernelGGL(layernorm_regs<8>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
+        case 16:
+            hipLaunchKernelGGL(layernorm_regs<16>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps);
+            break;
+        default:
+            hipLaunchKernelGGL(layernorm_any, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps);
+    }
     if (int rc = check_launch("layernorm")) return rc;
     return ok();
 }
@@ -424,8 +541,16 @@ int lancius_hip_softmax_f32(lancius_hip_ctx* ctx, float* probs, int32_t* argmax,
                     "softmax: rows=%zu cols=%zu", rows, cols);
     if (rows == 0) return ok();
     if (int rc = bind_device(ctx)) return rc;
-    hipLaunchKernelGGL(softmax_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0, ctx->stream, probs,
-                       argmax, in, (int)rows, (int)cols);
+    const dim3 grid(ceil_div(rows, kRowsPerBlock)), block(kRowThreads);
+    const int r = (int)rows, c = (int)cols;
+    switch (regs_width(cols, aligned16(probs) && aligned16(in))) {
+        case 1: hipLaunchKernelGGL(softmax_regs<1>, grid, block, 0, ctx->stream, probs, argmax, in, r, c); break;
+        case 2: hipLaunchKernelGGL(softmax_regs<2>, grid, block, 0, ctx->stream, probs, argmax, in, r, c); break;
+        case 4: hipLaunchKernelGGL(softmax_regs<4>, grid, block, 0, ctx->stream, probs, argmax, in, r, c); break;
+        case 8: hipLaunchKernelGGL(softmax_regs<8>, grid, block, 0, ctx->stream, probs, argmax, in, r, c); break;
+        case 16: hipLaunchKernelGGL(softmax_regs<16>, grid, block, 0, ctx->stream, probs, argmax, in, r, c); break;
+        default: hipLaunchKernelGGL(softmax_rows, grid, block, 0, ctx->stream, probs, argmax, in, r, c);
+    }
     if (int rc = check_launch("softmax")) return rc;
     return ok();
 }
@@ -453,8 +578,16 @@ int lancius_hip_rmsnorm_f32(lancius_hip_ctx* ctx, float* out, const float* in, c
                     "rmsnorm: rows=%zu hidden=%zu", rows, hidden);
     if (rows == 0) return ok();
     if (int rc = bind_device(ctx)) return rc;
-    hipLaunchKernelGGL(rmsnorm_rows, dim3(ceil_div(rows, kRowsPerBlock)), dim3(kRowThreads), 0, ctx->stream, out, in,
-                       gamma, (int)rows, (int)hidden, eps);
+    const dim3 grid(ceil_div(rows, kRowsPerBlock)), block(kRowThreads);
+    const int r = (int)rows, h = (int)hidden;
+    switch (regs_width(hidden, aligned16(out) && aligned16(in) && aligned16(gamma))) {
+        case 1: hipLaunchKernelGGL(rmsnorm_regs<1>, grid, block, 0, ctx->stream, out, in, gamma, r, h, eps); break;
+        case 2: hipLaunchKernelGGL(rmsnorm_regs<2>, grid, block, 0, ctx->stream, out, in, gamma, r, h, eps); break;
+        case 4: hipLaunchKernelGGL(rmsnorm_regs<4>, grid, block, 0, ctx->stream, out, in, gamma, r, h, eps); break;
+        case 8: hipLaunchKernelGGL(rmsnorm_regs<8>, grid, block, 0, ctx->stream, out, in, gamma, r, h, eps); break;
+        case 16: hipLaunchKernelGGL(rmsnorm_regs<16>, grid, block, 0, ctx->stream, out, in, gamma, r, h, eps); break;
+        default: hipLaunchKernelGGL(rmsnorm_rows, grid, block, 0, ctx->stream, out, in, gamma, r, h, eps);
+    }
     return check_launch("rmsnorm");
 }
 

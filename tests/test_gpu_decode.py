@@ -27,7 +27,7 @@ def up(dev, a):
     return dev.upload(np.ascontiguousarray(a, dtype=np.float32))
 
 
-@pytest.mark.parametrize("rows,hidden", [(5, 12), (64, 4096), (1000, 257), (1, 1)])
+@pytest.mark.parametrize("rows,hidden", [(5, 12), (64, 4096), (1000, 257), (1, 1), (7, 1000), (3, 2052)])
 def test_rmsnorm(dev, rows, hidden):
     x, g = prng.normal(200 + hidden, (rows, hidden), 0.3, 2.0), prng.normal(201, (hidden,), 1.0, 0.2)
     if (rows, hidden) == (5, 12):
@@ -131,6 +131,10 @@ def test_decode_golden(dev):
     (4, 777, 16, 2, 64, [777, 1, 0, 300]),
     (2, 64, 64, 1, 128, [64, 63]),
     (3, 5000, 4, 4, 96, [4999, 5000, 2500]),
+    (2, 300, 6, 2, 37, None),
+    (1, 1000, 8, 1, 100, [999]),
+    (2, 2000, 32, 2, 80, [1500, 2000]),
+    (16, 4096, 32, 8, 128, None),
 ])
 def test_decode_shapes(dev, B, Skv, Hq, Hkv, D, lens):
     q, k, v, got = _decode(dev, B, Skv, Hq, Hkv, D, lens, 240 + Skv)

@@ -322,7 +322,7 @@ def test_conv_bias(dev):
 # ---- row and elementwise ops -----------------------------------------------------
 
 
-@pytest.mark.parametrize("rows,hidden", [(4096, 1024), (7, 100), (3, 256), (5, 4096), (2, 1)])
+@pytest.mark.parametrize("rows,hidden", [(4096, 1024), (7, 100), (3, 256), (5, 4096), (2, 1), (9, 1500), (3, 4100)])
 def test_layernorm(dev, rows, hidden):
     x = prng.normal(11, (rows, hidden), mean=0.5, std=2.0)
     g = prng.normal(12, (hidden,), mean=1.0, std=0.1)
@@ -346,7 +346,8 @@ def test_layernorm_constant_row_gives_beta(dev):
     assert np.allclose(dev.download(do, x.shape), np.broadcast_to(b, x.shape), atol=1e-6, rtol=0)
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 10), (5, 1), (3, 200), (1000, 37)])
+@pytest.mark.parametrize("rows,cols", [(64, 10), (5, 1), (3, 200), (1000, 37), (8, 1024), (4, 4096), (6, 2000),
+                                       (2, 4104)])
 def test_softmax_argmax(dev, rows, cols):
     x = prng.normal(21, (rows, cols), std=3.0)
     dx = dev.upload(x)
@@ -373,6 +374,21 @@ def test_softmax_ties_first_max(dev):
     dev.softmax(dp, di, dx, 4, 10)
     assert dev.download(di, (4,), np.int32).tolist() == [0, 3, 9, 0]
     assert np.allclose(dev.download(dp, x.shape)[0], 0.1, atol=1e-7)
+
+
+def test_softmax_ties_first_max_register_rows(dev):
+    """Ties inside one float4 piece, across pieces of one lane and across
+    lanes (lane 0's piece 1 holds column 257, lane 1's piece 0 column 4)."""
+    x = np.zeros((4, 1024), np.float32)
+    x[1, 700] = x[1, 300] = 2.0
+    x[2, 5] = x[2, 6] = 1.5
+    x[3, 257] = x[3, 4] = 3.0
+    dx = dev.upload(x)
+    dp = dev.alloc(x.nbytes)
+    di = dev.alloc(16)
+    case("softmax ties 4x1024")
+    dev.softmax(dp, di, dx, 4, 1024)
+    assert dev.download(di, (4,), np.int32).tolist() == [0, 300, 5, 4]
 
 
 def test_elementwise(dev):
