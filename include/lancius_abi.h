@@ -174,6 +174,28 @@ typedef struct lancius_memory_plan {
 } lancius_memory_plan;
 #endif /* LANCIUS_MEMORY_PLANNER_H */
 
+/* Where each INPUT tensor's bytes sit in a .lancius model file: filled by
+ * lancius_graph_load_mapped (liblancius_graph), read by
+ * lancius_device_upload_weights (liblancius_hip).  No reference counterpart. */
+#ifndef LANCIUS_AMD_WEIGHT_MAP_H
+#define LANCIUS_AMD_WEIGHT_MAP_H
+typedef struct {
+    const lancius_node* node; /* INPUT node of the loaded graph */
+    uint64_t file_offset;     /* first byte of the tensor in the file */
+    uint64_t elements;        /* lancius_node_elements(node) */
+    lancius_dtype file_dtype; /* encoding in the file: FP64, FP32 or INT8 */
+    double scale;             /* int8 scale (also in node->scale) */
+} lancius_weight_ref;
+
+typedef struct {
+    uint32_t format;          /* 9, 10, or 2 */
+    uint32_t count;           /* entries of refs */
+    lancius_weight_ref* refs; /* malloc'd; lancius_weight_map_free */
+    uint64_t file_bytes;
+    uint32_t crc32;           /* v2: the verified header checksum; else 0 */
+} lancius_weight_map;
+#endif /* LANCIUS_AMD_WEIGHT_MAP_H */
+
 #ifdef __cplusplus
 }
 #endif

@@ -147,8 +147,77 @@ void lancius_memory_plan_destroy(lancius_memory_plan* plan);
 
 /* Sets the dtype of every node (e.g. LANCIUS_DTYPE_FP32 before planning the
  * device arena; the reference sizes plan blocks by dtype, lancius_ir.h:75-78),
- * except nodes already quantized to int8.  No reference counterpart. */
+ * except int8 weights (INPUT nodes of dtype INT8, quantized or loaded as int8,
+ * and nodes holding int8 data).  No reference counterpart. */
 void lancius_graph_set_dtype(lancius_graph* g, lancius_dtype dtype);
+
+/* ---- .lancius model files (lancius_serialize.c:13-259, lancius_model_format.h) ----
+ *
+ * Three layouts are read, told apart by their contents:
+ *   v10  magic 0x21434E41, node_count, then per node: id u32, op u32, ndim u8,
+ *        shape 4 x u64, input_count u32, input ids u32[], attr_val f64,
+ *        kernel_h/kernel_w/stride/pad u32[4], axes u32[4], is_view u8
+ *        [+ strides 4 x u64, view source id u32], has_weights u8
+ *        [+ dtype u8, scale f64, elements x (i8 when dtype INT8, else f64)];
+ *        what lancius_graph_save writes (lancius_serialize.c:13-63);
+ *   v9   the same records without the is_view byte (stable/v9S, whose
+ *        shipped models the reference's v10+ loader cannot read);
+ *   v2   the 48-byte header declared in lancius_model_format.h:75-92 (magic
+ *        0x32434E41, version 2, CRC-32 of every byte after the header), the
+ *        v10 records with each tensor's payload replaced by (elements u64,
+ *        offset u64) into a weight block at weight_block_offset (4096-aligned,
+ *        every tensor 256-aligned), tensors stored as i8, f32 or f64.
+ * The v9/v10 choice is the layout whose records parse and build and end
+ * exactly at the end of the file (v10 first); failing that, the first layout
+ * whose records parse and build.
+ *
+ * Nodes are rebuilt with the builders, like lancius_graph_load does, for every
+ * op with a builder (the reference loader's subset plus BROADCAST, TRANSPOSE,
+ * GELU, the backward ops, SUM_AXIS0/1, PERMUTE, MATMUL_BATCHED, RMSNORM,
+ * SWIGLU, GQA); ROPE, EMBEDDING and KV_CACHE_READ/WRITE keep the recorded
+ * shape and inputs; NOP and unknown ops are skipped with a warning, as in the
+ * reference, and a node that reads a skipped one fails the load.  Stored
+ * shapes of built ops are ignored (the builders derive them), as in the
+ * reference; kernel_h/kernel_w/stride/pad, axes, attr_val and the view fields
+ * are restored.  Any malformed, truncated or out-of-range field fails the load
+ * with NULL and LANCIUS_ERROR_INVALID_MODEL (LANCIUS_ERROR_IO when the file
+ * cannot be read); limits as in the reference: 1e6 nodes, 16 inputs, 1e8
+ * elements per tensor, ids below node_count + 1000. */
+
+/* INPUT weights land in malloc'd fp64 runtime_data (int8 in
+ * runtime_data_int8), owned by the graph and freed by lancius_graph_destroy
+ * (the reference's graph keeps them until the process ends). */
+lancius_graph* lancius_graph_load(const char* path);
+/* v10 records, byte for byte what lancius_serialize.c:13-63 writes.  Weights
+ * are written for INPUT nodes with data: int8 when dtype is INT8 and an int8
+ * copy exists, else fp64.  Sets LANCIUS_ERROR_IO when the file cannot be
+ * written. */
+void lancius_graph_save(lancius_graph* g, const char* path);
+
+/* v2 container (no reference counterpart: the header is declared there but
+ * nothing writes or reads it).  weight_dtype LANCIUS_DTYPE_FP64 stores the
+ * fp64 data exactly, LANCIUS_DTYPE_FP32 rounds it to fp32 (half the bytes,
+ * the device's own format); int8 tensors stay int8.  Returns 0 or a
+ * lancius_error. */
+#define LANCIUS_MODEL_MAGIC_V1 0x21434E41u
+#define LANCIUS_MODEL_MAGIC_V2 0x32434E41u
+#define LANCIUS_MODEL_HEADER_SIZE_V2 48u
+#define LANCIUS_MODEL_FLAG_LITTLE_ENDIAN (1u << 0)
+#define LANCIUS_MODEL_FLAG_STATIC_GRAPH (1u << 1)
+int lancius_graph_save_v2(const lancius_graph* g, const char* path, lancius_dtype weight_dtype);
+
+/* lancius_weight_ref / lancius_weight_map (lancius_abi.h): where each INPUT
+ * tensor's bytes sit in a model file, for loaders that move them straight to
+ * the device (lancius_device_upload_weights) instead of through host fp64
+ * copies. */
+/* lancius_graph_load without host weight copies: INPUT nodes with stored data
+ * get their dtype and scale but no runtime_data; `map` lists the tensors. */
+lancius_graph* lancius_graph_load_mapped(const char* path, lancius_weight_map* map);
+void lancius_weight_map_free(lancius_weight_map* map);
+
+/* CRC-32 (IEEE 802.3, reflected polynomial 0xEDB88320, the zlib crc32) of
+ * len bytes continuing from crc (0 to start). */
+uint32_t lancius_crc32(uint32_t crc, const void* data, size_t len);
 
 #ifdef __cplusplus
 }

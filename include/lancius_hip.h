@@ -308,6 +308,38 @@ LANCIUS_HIP_EXPORT int lancius_hip_capture_end(lancius_hip_ctx* ctx, lancius_hip
 LANCIUS_HIP_EXPORT int lancius_hip_graph_launch(lancius_hip_graph* graph, lancius_hip_ctx* ctx);
 LANCIUS_HIP_EXPORT void lancius_hip_graph_destroy(lancius_hip_graph* graph);
 
+/* ---- model-file tensors to HBM -------------------------------------- */
+
+/* Element codes of lancius_hip_file_tensor (the lancius_dtype numbers,
+ * bleeding/v11A1/include/lancius/lancius_types.h:9-14). */
+#define LANCIUS_HIP_FILE_F64 0
+#define LANCIUS_HIP_FILE_I8  1
+#define LANCIUS_HIP_FILE_F32 2
+
+/* One tensor stored in a file: `elements` values of `file_dtype` starting at
+ * byte `file_offset`, to land in device memory `dst` as `dst_dtype`:
+ *   F64 -> F32  rounded to nearest on the device;
+ *   F32 -> F32, I8 -> I8  copied;
+ *   I8  -> F32  dequantized, (float)(q * scale) with the product in fp64. */
+typedef struct {
+    void* dst;
+    int dst_dtype;
+    int file_dtype;
+    uint64_t file_offset;
+    uint64_t elements;
+    double scale;
+} lancius_hip_file_tensor;
+
+/* Streams the tensors from `path` straight into device memory: the file is
+ * read in 16 MiB pieces into two pinned host buffers, each piece is copied
+ * to the device while the next is read, and conversions run on the device
+ * (no host fp64/fp32 copy of a tensor is made).  Returns when every tensor
+ * is in place.  Checks every extent against the file size first.  No
+ * reference counterpart: the reference reads weights into host fp64 buffers
+ * (lancius_serialize.c:221-240). */
+LANCIUS_HIP_EXPORT int lancius_hip_upload_file(lancius_hip_ctx* ctx, const char* path, size_t count,
+                                               const lancius_hip_file_tensor* tensors);
+
 /* ---- diagnostics ---------------------------------------------------- */
 
 /* Measured ceilings of this device, for roofline reporting:

@@ -81,6 +81,15 @@ LANCIUS_HIP_EXPORT int lancius_device_download(lancius_device_program* prog, con
 /* argmax (int32 per row, first maximum) of a SOFTMAX node's output. */
 LANCIUS_HIP_EXPORT int lancius_device_download_argmax(lancius_device_program* prog, const lancius_node* n,
                                                       int32_t* host);
+/* Every tensor of `map` (from lancius_graph_load_mapped on `path`, for the
+ * graph this program was built from) streamed from the file straight into
+ * its INPUT buffer in the arena with lancius_hip_upload_file: fp64 and fp32
+ * tensors land as fp32, int8 tensors as int8 when the program keeps the node
+ * int8 (a weight operand) and dequantized to fp32 otherwise.  Returns when
+ * the data is in place.  No reference counterpart (the reference reads
+ * weights into host fp64 buffers, lancius_serialize.c:221-240). */
+LANCIUS_HIP_EXPORT int lancius_device_upload_weights(lancius_device_program* prog, const char* path,
+                                                     const lancius_weight_map* map);
 /* Device address of a node's buffer (NULL for fused intermediates). */
 LANCIUS_HIP_EXPORT void* lancius_device_buffer(lancius_device_program* prog, const lancius_node* n);
 

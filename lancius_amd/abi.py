@@ -123,6 +123,21 @@ class TrainingGraph(C.Structure):
 TrainingGraphP = C.POINTER(TrainingGraph)
 
 
+class WeightRef(C.Structure):
+    """lancius_weight_ref (include/lancius_abi.h)."""
+    _fields_ = [("node", NodeP), ("file_offset", C.c_uint64), ("elements", C.c_uint64), ("file_dtype", C.c_int),
+                ("scale", C.c_double)]
+
+
+class WeightMap(C.Structure):
+    """lancius_weight_map (include/lancius_abi.h)."""
+    _fields_ = [("format", C.c_uint32), ("count", C.c_uint32), ("refs", C.POINTER(WeightRef)),
+                ("file_bytes", C.c_uint64), ("crc32", C.c_uint32)]
+
+
+WeightMapP = C.POINTER(WeightMap)
+
+
 def declare_graph_api(lib: C.CDLL) -> C.CDLL:
     """Prototypes of the graph-path functions shared by liblancius_graph and
     the reference library (same names and signatures)."""
@@ -197,6 +212,28 @@ def declare_graph_api(lib: C.CDLL) -> C.CDLL:
     lib.lancius_memory_plan_destroy.restype = None
     lib.lancius_get_error.restype = C.c_int
     lib.lancius_clear_error.restype = None
+    lib.lancius_graph_load.argtypes = [C.c_char_p]
+    lib.lancius_graph_load.restype = GraphP
+    lib.lancius_graph_save.argtypes = [GraphP, C.c_char_p]
+    lib.lancius_graph_save.restype = None
+    lib.lancius_permute.argtypes = [GraphP, NodeP, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32]
+    lib.lancius_permute.restype = NodeP
+    lib.lancius_matmul_batched.argtypes = [GraphP, NodeP, NodeP]
+    lib.lancius_matmul_batched.restype = NodeP
+    return lib
+
+
+def declare_model_io(lib: C.CDLL) -> C.CDLL:
+    """Model-file functions of liblancius_graph with no reference
+    counterpart (v2 container, mapped loading, CRC-32)."""
+    lib.lancius_graph_save_v2.argtypes = [GraphP, C.c_char_p, C.c_int]
+    lib.lancius_graph_save_v2.restype = C.c_int
+    lib.lancius_graph_load_mapped.argtypes = [C.c_char_p, WeightMapP]
+    lib.lancius_graph_load_mapped.restype = GraphP
+    lib.lancius_weight_map_free.argtypes = [WeightMapP]
+    lib.lancius_weight_map_free.restype = None
+    lib.lancius_crc32.argtypes = [C.c_uint32, C.c_void_p, C.c_size_t]
+    lib.lancius_crc32.restype = C.c_uint32
     return lib
 
 

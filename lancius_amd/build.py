@@ -36,8 +36,8 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip", "reduce.hip", "pool.hip",
-               "int8.hip", "probe.hip"]
-HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c", "host/graph_autodiff.c"]
+               "int8.hip", "io.hip", "probe.hip"]
+HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c", "host/graph_autodiff.c", "host/graph_io.c"]
 DEVICE_C_SOURCES = ["host/device_exec.c"]
 
 HIP_FLAGS = [
@@ -72,6 +72,7 @@ REF_SOURCES = [
     "src/runtime/lancius_threadpool.c",
     "src/compiler/lancius_optimizer.c",
     "src/compiler/lancius_quantize.c",
+    "src/core/lancius_serialize.c",
 ]
 
 

@@ -1170,6 +1170,39 @@ int lancius_device_upload(lancius_device_program* prog, const lancius_node* n, c
     return rc;
 }
 
+int lancius_device_upload_weights(lancius_device_program* prog, const char* path, const lancius_weight_map* map) {
+    if (!prog || !path || !map || (map->count && !map->refs)) return LANCIUS_HIP_ERR_NULL_PTR;
+    lancius_hip_file_tensor* t = (lancius_hip_file_tensor*)calloc(map->count + 1, sizeof(*t));
+    if (!t) return LANCIUS_HIP_ERR_OOM;
+    int rc = 0;
+    for (uint32_t i = 0; i < map->count && !rc; i++) {
+        const lancius_weight_ref* r = &map->refs[i];
+        const lancius_node* n = r->node;
+        if (!n || n->id >= prog->n_ids || prog->role[n->id] != ROLE_INPUT || !prog->ptr[n->id]) {
+            rc = fail(LANCIUS_HIP_ERR_UNSUPPORTED, "weight map entry is not an INPUT of this program");
+        } else if (r->elements != elems(n)) {
+            rc = fail(LANCIUS_HIP_ERR_SHAPE, "weight map entry size differs from its node");
+        } else if (r->file_dtype != LANCIUS_DTYPE_FP64 && r->file_dtype != LANCIUS_DTYPE_FP32 &&
+                   r->file_dtype != LANCIUS_DTYPE_INT8) {
+            rc = fail(LANCIUS_HIP_ERR_DTYPE, "weight map entry dtype");
+        } else if (prog->is_i8[n->id] && r->file_dtype != LANCIUS_DTYPE_INT8) {
+            rc = fail(LANCIUS_HIP_ERR_DTYPE, "int8 weight stored as floating point");
+        } else {
+            t[i].dst = prog->ptr[n->id];
+            t[i].dst_dtype = prog->is_i8[n->id] ? LANCIUS_HIP_FILE_I8 : LANCIUS_HIP_FILE_F32;
+            t[i].file_dtype = r->file_dtype == LANCIUS_DTYPE_INT8   ? LANCIUS_HIP_FILE_I8
+                              : r->file_dtype == LANCIUS_DTYPE_FP32 ? LANCIUS_HIP_FILE_F32
+                                                                    : LANCIUS_HIP_FILE_F64;
+            t[i].file_offset = r->file_offset;
+            t[i].elements = r->elements;
+            t[i].scale = r->scale;
+        }
+    }
+    if (!rc) rc = lancius_hip_upload_file(prog->ctx, path, map->count, t);
+    free(t);
+    return rc;
+}
+
 int lancius_device_download(lancius_device_program* prog, const lancius_node* n, void* host,
                             lancius_dtype host_dtype) {
     if (!prog || !n || !host) return LANCIUS_HIP_ERR_NULL_PTR;

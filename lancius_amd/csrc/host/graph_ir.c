@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include "lancius_graph.h"
+#include "graph_internal.h"
 
 /* ---- error state: thread-local code (lancius_error.c:5-34) ---------------- */
 
@@ -153,13 +154,19 @@ lancius_graph* lancius_graph_create(void) {
 
 void lancius_graph_destroy(lancius_graph* g) {
     if (!g) return;
-    /* int8 copies made by lancius_quantize_graph belong to the graph */
+    /* int8 copies made by lancius_quantize_graph or lancius_graph_load, and
+     * fp64 weights read by lancius_graph_load, belong to the graph */
     for (uint32_t i = 0; i < g->node_count; i++) {
         lancius_node* n = g->nodes[i];
         if (n->rt && n->rt->int8_owner == LANCIUS_MEMORY_OWNED_HEAP && n->runtime_data_int8) {
             free(n->runtime_data_int8);
             n->runtime_data_int8 = NULL;
             n->rt->buffer_int8 = NULL;
+        }
+        if (n->rt && (n->rt->flags & LANCIUS_RT_FLAG_LOADED) && n->runtime_data) {
+            free(n->runtime_data);
+            n->runtime_data = NULL;
+            n->rt->buffer = NULL;
         }
     }
     free(g->nodes);
@@ -172,7 +179,8 @@ void lancius_graph_set_dtype(lancius_graph* g, lancius_dtype dtype) {
     if (!g) return;
     for (uint32_t i = 0; i < g->node_count; i++) {
         lancius_node* n = g->nodes[i];
-        if (n->dtype == LANCIUS_DTYPE_INT8 && n->runtime_data_int8) continue; /* quantized weights stay int8 */
+        /* quantized or int8-loaded weights stay int8 */
+        if (n->dtype == LANCIUS_DTYPE_INT8 && (n->runtime_data_int8 || n->op == LANCIUS_OP_INPUT)) continue;
         n->dtype = dtype;
         if (n->rt) n->rt->dtype = dtype;
     }
@@ -251,6 +259,10 @@ static lancius_node* new_node(lancius_graph* g, lancius_opcode op, uint8_t ndim,
     n->dtype = LANCIUS_DTYPE_FP64;
     g->nodes[g->node_count++] = n;
     return n;
+}
+
+lancius_node* lancius__raw_node(lancius_graph* g, lancius_opcode op, uint8_t ndim, uint32_t n_in) {
+    return new_node(g, op, ndim, n_in);
 }
 
 static void copy_shape(lancius_node* n, const lancius_node* from) {

@@ -32,6 +32,7 @@ class BuiltGraph:
     nodes: dict = field(default_factory=dict)   # name -> NodeP
     inputs: list = field(default_factory=list)  # INPUT node names in creation order
     outputs: list = field(default_factory=list) # sink node names
+    keep: list = field(default_factory=list)    # host arrays bound as runtime_data
 
     def node(self, name: str) -> abi.NodeP:
         return self.nodes[name]
@@ -299,3 +300,76 @@ def build_training(lib: C.CDLL, fwd: BuiltGraph, loss: str = "loss") -> TrainGra
             t.nodes[f"d{name}"] = gn
             t.outputs.append(f"d{name}")
     return t
+
+
+IO_GRAPHS = ("io_mlp", "io_conv_i8")
+
+
+def _bind(bg: BuiltGraph, name: str, arr) -> None:
+    """Bind fp64 host data to an INPUT node (kept alive by the BuiltGraph)."""
+    import numpy as np
+
+    a = np.ascontiguousarray(arr, dtype=np.float64)
+    bg.keep.append(a)
+    bg.node(name).contents.runtime_data = a.ctypes.data_as(C.POINTER(C.c_double))
+
+
+def build_io_graph(lib: C.CDLL, name: str) -> BuiltGraph:
+    """Graphs with stored weights for the model-file tests: the same builder
+    calls give the same node ids and bytes with either library.
+
+    io_mlp: MATMUL, BROADCAST + ADD, RELU marked as a view of the MATMUL
+    (is_view, strides, view_source), CONST, GELU, LAYERNORM, SOFTMAX, and a
+    RESHAPE feeding a non-causal ATTENTION (axes[0] = 1).
+    io_conv_i8: conv + ReLU fused (the fusion pass leaves a NOP), MAXPOOL2D,
+    FLATTEN, MATMUL, after lancius_quantize_graph (int8 image and filter)."""
+    from . import prng
+
+    bg = BuiltGraph(lib, _ok(lib.lancius_graph_create(), "graph_create"))
+    g = bg.g
+    if name == "io_mlp":
+        x = _inp(bg, "x", 4, 8)
+        w1 = _inp(bg, "W1", 8, 16)
+        b1 = _inp(bg, "b1", 1, 16)
+        mm = _ok(lib.lancius_matmul(g, x, w1), "mm")
+        a = _ok(lib.lancius_add(g, mm, _ok(lib.lancius_broadcast(g, b1, 4, 16), "bc")), "add")
+        r = _ok(lib.lancius_relu(g, a), "relu")
+        r.contents.is_view = 1
+        r.contents.strides[0], r.contents.strides[1] = 16, 1
+        r.contents.view_source = mm
+        s = _ok(lib.lancius_add(g, r, _ok(lib.lancius_const(g, 0.5, 4, 16), "const")), "add2")
+        gl = _ok(lib.lancius_gelu(g, s), "gelu")
+        gam = _inp(bg, "gamma", 1, 16)
+        bet = _inp(bg, "beta", 1, 16)
+        ln = _ok(lib.lancius_layernorm(g, gl, gam, bet), "ln")
+        w2 = _inp(bg, "W2", 16, 10)
+        bg.nodes["probs"] = _ok(lib.lancius_softmax(g, _ok(lib.lancius_matmul(g, ln, w2), "mm2")), "softmax")
+        q = _inp(bg, "q", 4, 16)
+        q3 = _ok(lib.lancius_reshape(g, q, 3, 4, 2, 8, 1), "reshape")
+        att = _ok(lib.lancius_attention(g, q3, q3, q3), "attention")
+        att.contents.axes[0] = 1
+        bg.nodes["att"] = att
+        bg.outputs = ["probs", "att"]
+        _bind(bg, "W1", prng.normal(90, (8, 16)))
+        _bind(bg, "b1", prng.normal(91, (1, 16)))
+        _bind(bg, "gamma", prng.normal(92, (1, 16), mean=1.0, std=0.1))
+        _bind(bg, "beta", prng.normal(93, (1, 16), std=0.1))
+        _bind(bg, "W2", prng.normal(94, (16, 10)))
+    elif name == "io_conv_i8":
+        img = _inp(bg, "img", 2, 3, 8, 8)
+        w = _inp(bg, "w", 4, 3, 3, 3)
+        cv = _ok(lib.lancius_conv2d(g, img, w, 1, 1), "conv")
+        r = _ok(lib.lancius_relu(g, cv), "relu")
+        mp = _ok(lib.lancius_maxpool2d(g, r, 2, 2), "pool")
+        fl = _ok(lib.lancius_flatten(g, mp), "flatten")
+        wf = _inp(bg, "Wf", 64, 5)
+        bg.nodes["logits"] = _ok(lib.lancius_matmul(g, fl, wf), "mm")
+        bg.outputs = ["logits"]
+        lib.lancius_optimize_fusion(g)
+        _bind(bg, "img", prng.normal(95, (2, 3, 8, 8)))
+        _bind(bg, "w", prng.normal(96, (4, 3, 3, 3), std=0.4))
+        _bind(bg, "Wf", prng.normal(97, (64, 5)))
+        lib.lancius_quantize_graph(g)
+    else:
+        raise ValueError(name)
+    return bg

@@ -30,6 +30,12 @@ class HipError(RuntimeError):
         self.code = code
 
 
+class FileTensor(C.Structure):
+    """lancius_hip_file_tensor (include/lancius_hip.h)."""
+    _fields_ = [("dst", C.c_void_p), ("dst_dtype", C.c_int), ("file_dtype", C.c_int), ("file_offset", C.c_uint64),
+                ("elements", C.c_uint64), ("scale", C.c_double)]
+
+
 class ProgramInfo(C.Structure):
     _fields_ = [
         ("arena_bytes", C.c_size_t),
@@ -126,6 +132,8 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_device_buffer.restype = vp
     lib.lancius_device_run.argtypes = [vp]
     lib.lancius_schedule_execute_device.argtypes = [abi.ScheduleP, abi.GraphP, vp]
+    lib.lancius_device_upload_weights.argtypes = [vp, C.c_char_p, abi.WeightMapP]
+    lib.lancius_hip_upload_file.argtypes = [vp, C.c_char_p, sz, C.POINTER(FileTensor)]
     return lib
 
 
@@ -144,7 +152,7 @@ def graph_lib() -> C.CDLL:
     if _graph is None:
         if not GRAPH_LIB.exists():
             raise RuntimeError(f"{GRAPH_LIB} is missing: build it with `python -m lancius_amd.build`")
-        lib = abi.declare_graph_api(C.CDLL(str(GRAPH_LIB)))
+        lib = abi.declare_model_io(abi.declare_graph_api(C.CDLL(str(GRAPH_LIB))))
         lib.lancius_graph_set_dtype.argtypes = [abi.GraphP, C.c_int]
         lib.lancius_graph_set_dtype.restype = None
         _graph = lib
@@ -431,6 +439,11 @@ class DeviceProgram:
 
     def buffer(self, node: abi.NodeP) -> int:
         return int(self.lib.lancius_device_buffer(self.prog, node) or 0)
+
+    def upload_weights(self, path, wmap: abi.WeightMap) -> None:
+        """Stream every tensor of a lancius_graph_load_mapped map from the
+        model file into the program's INPUT buffers."""
+        _check(self.lib.lancius_device_upload_weights(self.prog, str(path).encode(), C.byref(wmap)))
 
     def run(self) -> None:
         _check(self.lib.lancius_device_run(self.prog))

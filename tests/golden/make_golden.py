@@ -234,7 +234,123 @@ def main() -> None:
     recs.update({f"train_{k}": v for k, v in trec.items()})
     (OUT / "graphs.json").write_text(json.dumps(recs, indent=0, sort_keys=True))
     np.savez_compressed(OUT / "train_outputs.npz", **tr)
+    model_vectors(ref)
     print("fixtures written to", OUT)
+
+
+def _ref_graph_from_records(ref, recs: list[dict]):
+    """The graph of parsed v9 records rebuilt with the reference's own
+    builders, as its loader does (lancius_serialize.c:137-201) plus BROADCAST,
+    which that loader skips (:175-176); weights bound as its loader binds
+    them (:221-240).  Returns (graph, file id -> node, arrays to keep)."""
+    I8 = C.POINTER(C.c_int8)
+    g = ref.lancius_graph_create()
+    by_id, keep = {}, []
+    for r in recs:
+        op, s, m = r["op"], r["shape"], r["meta"]
+        ins = [by_id.get(i) for i in r["inputs"]]
+        if op == abi.OP["INPUT"]:
+            n = ref.lancius_input_4d(g, *s) if r["ndim"] == 4 else ref.lancius_input(g, s[0], s[1])
+        elif op in (abi.OP["CONV2D"], abi.OP["CONV2D_RELU_FUSED"]):
+            n = ref.lancius_conv2d(g, ins[0], ins[1], m[2], m[3])
+            n.contents.op = op
+        elif op == abi.OP["MAXPOOL2D"]:
+            n = ref.lancius_maxpool2d(g, ins[0], m[0], m[2])
+        elif op == abi.OP["FLATTEN"]:
+            n = ref.lancius_flatten(g, ins[0])
+        elif op == abi.OP["MATMUL"]:
+            n = ref.lancius_matmul(g, ins[0], ins[1])
+        elif op == abi.OP["ADD"]:
+            n = ref.lancius_add(g, ins[0], ins[1])
+        elif op == abi.OP["RELU"]:
+            n = ref.lancius_relu(g, ins[0])
+        elif op == abi.OP["BROADCAST"]:
+            n = ref.lancius_broadcast(g, ins[0], s[0], s[1])
+        elif op == abi.OP["CROSS_ENTROPY"]:
+            n = ref.lancius_cross_entropy(g, ins[0], ins[1])
+        elif op == abi.OP["NOP"]:
+            continue
+        else:
+            raise ValueError(f"op {op} not rebuilt here")
+        n.contents.kernel_h, n.contents.kernel_w, n.contents.stride, n.contents.pad = m
+        for d in range(4):
+            n.contents.axes[d] = r["axes"][d]
+        by_id[r["id"]] = n
+        if r["weights"] is not None:
+            w = np.ascontiguousarray(r["weights"])
+            keep.append(w)
+            n.contents.dtype = r["dtype"]
+            n.contents.scale = r["scale"]
+            if r["dtype"] == abi.DTYPE_INT8:
+                n.contents.runtime_data_int8 = w.ctypes.data_as(I8)
+            else:
+                n.contents.runtime_data = p(w)
+    return g, by_id, keep
+
+
+def _node_values(n) -> np.ndarray:
+    return np.ctypeslib.as_array(n.contents.runtime_data, shape=(abi.node_elems(n),)).copy().reshape(
+        abi.node_shape(n))
+
+
+def model_vectors(ref) -> None:
+    """Model-file fixtures under tests/golden/:
+      models/ref_<io graph>.lancius  lancius_graph_save of the reference on
+                                     graphs.build_io_graph graphs (v10 bytes)
+      model_io.npz  lenet_logits: stable/v9S/pytorch_lenet.lancius, re-laid
+                    as v10 by oracle.model_file, read by the reference's own
+                    lancius_graph_load and run by its executor on
+                    parity_input.bin (the shipped lancius_out.bin is these
+                    logits in fp32 from the v9 build);
+                    cifar_logits / cifar_loss: stable/v9S/cifar10_lenet.lancius
+                    (int8 image and filters, BROADCAST, CROSS_ENTROPY over
+                    its stored batch) rebuilt with the reference's builders
+                    and run by its executor."""
+    import tempfile
+
+    from oracle import model_file as mf
+
+    models = OUT / "models"
+    for name in graphs.IO_GRAPHS:
+        bg = graphs.build_io_graph(ref, name)
+        ref.lancius_graph_save(bg.g, str(models / f"ref_{name}.lancius").encode())
+        for i in range(bg.g.contents.node_count):  # the reference's int8 copies are left to the process
+            bg.g.contents.nodes[i].contents.runtime_data = None
+        bg.destroy()
+    out = {}
+    recs = mf.read_records((models / "pytorch_lenet.lancius").read_bytes(), 9)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "lenet_v10.lancius"
+        path.write_bytes(mf.write_records(recs, 10))
+        g = ref.lancius_graph_load(str(path).encode())
+    nodes = [g.contents.nodes[i] for i in range(g.contents.node_count)]
+    x_node = [n for n in nodes if n.contents.op == abi.OP["INPUT"] and n.contents.ndim == 4
+              and not n.contents.runtime_data][0]  # examples/parity_runner.c:14-18
+    y_node = [n for n in nodes if n.contents.ndim == 2 and n.contents.shape[1] == 10
+              and n.contents.op != abi.OP["INPUT"]][-1]
+    x = np.fromfile(models / "parity_input.bin", dtype="<f4").astype(np.float64)
+    x_node.contents.runtime_data = p(x)
+    sched = ref.lancius_ir_schedule(g)
+    arena = ref.lancius_arena_create(16 << 20)
+    ref.lancius_schedule_execute(sched, arena)
+    out["lenet_logits"] = _node_values(y_node).ravel()
+    shipped = np.fromfile(models / "lancius_out.bin", dtype="<f4")
+    print("lenet logits vs shipped lancius_out.bin:", oracle.normwise_error(shipped, out["lenet_logits"]))
+    x_node.contents.runtime_data = None
+    ref.lancius_schedule_destroy(sched)
+    ref.lancius_arena_destroy(arena)
+
+    recs = mf.read_records((models / "cifar10_lenet.lancius").read_bytes(), 9)
+    g, by_id, keep = _ref_graph_from_records(ref, recs)
+    sched = ref.lancius_ir_schedule(g)
+    arena = ref.lancius_arena_create(64 << 20)
+    ref.lancius_schedule_execute(sched, arena)
+    out["cifar_logits"] = _node_values(by_id[20])
+    out["cifar_loss"] = _node_values(by_id[22]).ravel()
+    print("cifar loss", out["cifar_loss"])
+    ref.lancius_schedule_destroy(sched)
+    ref.lancius_arena_destroy(arena)
+    np.savez_compressed(OUT / "model_io.npz", **out)
 
 
 def ref_op(ref, shapes: dict[str, tuple], build, feeds: dict[str, np.ndarray]) -> np.ndarray:
@@ -467,4 +583,10 @@ def train_feeds(t, seed: int) -> dict[str, np.ndarray]:
 
 
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["models"]:  # only the model-file fixtures
+        _ref = oracle.ref_lib()
+        if _ref is None:
+            raise SystemExit("oracle/_ref/liblancius_ref.so not built (needs /root/reference)")
+        model_vectors(_ref)
+    else:
+        main()
