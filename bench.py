@@ -28,7 +28,9 @@ import ctypes as C
 import json
 import os
 import platform
+import shutil
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -159,6 +161,90 @@ def decode_cases(dev, steps, warmup) -> dict:
     for b in (x, g, y):
         b.free()
     return out
+
+
+LOAD_LAYERS, LOAD_DIM = 4, 4096  # stored weights: 4 x 4096 x 4096 fp64 = 512 MiB in a v10 file
+
+
+def write_load_models(tmpdir: Path) -> tuple[Path, Path]:
+    """An MLP whose weights are stored in the file, saved as v10 (fp64) and as
+    a v2 container with fp32 weights."""
+    lib = graph_lib()
+    bg = graphs.BuiltGraph(lib, lib.lancius_graph_create())
+    h = graphs._inp(bg, "x", 64, LOAD_DIM)
+    for i in range(LOAD_LAYERS):
+        w = graphs._inp(bg, f"W{i}", LOAD_DIM, LOAD_DIM)
+        graphs._bind(bg, f"W{i}", prng.normal(800 + i, (LOAD_DIM, LOAD_DIM), 0, 0.02))
+        h = lib.lancius_matmul(bg.g, h, w)
+    v10, v2 = tmpdir / "mlp.lancius", tmpdir / "mlp_fp32.lancius2"
+    lib.lancius_graph_save(bg.g, str(v10).encode())
+    if lib.lancius_graph_save_v2(bg.g, str(v2).encode(), abi.DTYPE_FP32) != 0:
+        raise RuntimeError("lancius_graph_save_v2 failed")
+    bg.destroy()
+    return v10, v2
+
+
+def model_load_cases(dev, v10: Path, v2: Path) -> dict:
+    """File -> HBM arena: lancius_graph_load_mapped (parse; the v2 CRC-32 over
+    the whole file), program creation, lancius_device_upload_weights (pread
+    into pinned buffers, H2D copies, fp64 -> fp32 on the device).  The files
+    were just written, so reads come from the page cache; best of 3."""
+    lib = graph_lib()
+    out = {}
+    for tag, path in (("v10_fp64", v10), ("v2_fp32", v2)):
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            wm = abi.WeightMap()
+            g = lib.lancius_graph_load_mapped(str(path).encode(), C.byref(wm))
+            t1 = time.perf_counter()
+            lib.lancius_graph_set_dtype(g, abi.DTYPE_FP32)
+            sched = lib.lancius_ir_schedule(g)
+            plan = lib.lancius_build_memory_plan(sched, g)
+            prog = DeviceProgram(dev, g, sched, plan)
+            t2 = time.perf_counter()
+            prog.upload_weights(path, wm)
+            t3 = time.perf_counter()
+            times = (t1 - t0, t2 - t1, t3 - t2, t3 - t0)
+            if best is None or times[3] < best[3]:
+                best = times
+            prog.close()
+            lib.lancius_memory_plan_destroy(plan)
+            lib.lancius_schedule_destroy(sched)
+            lib.lancius_weight_map_free(C.byref(wm))
+            lib.lancius_graph_destroy(g)
+        size = path.stat().st_size
+        out[f"model_load_{tag}_{LOAD_LAYERS}x{LOAD_DIM}x{LOAD_DIM}"] = {
+            "file_MiB": round(size / 2 ** 20, 1), "parse_ms": round(best[0] * 1e3, 2),
+            "program_ms": round(best[1] * 1e3, 2), "upload_ms": round(best[2] * 1e3, 2),
+            "total_ms": round(best[3] * 1e3, 2), "file_GB/s": round(size / best[3] / 1e9, 2),
+            "upload_GB/s": round(size / best[2] / 1e9, 2)}
+    return out
+
+
+def cpu_model_load(ref, v10: Path) -> dict:
+    """The reference's lancius_graph_load on the same v10 file (fread into
+    malloc'd fp64 buffers), page cache warm, best of 3."""
+    import ctypes.util
+
+    libc = C.CDLL(ctypes.util.find_library("c"))
+    best = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        g = ref.lancius_graph_load(str(v10).encode())
+        dt = time.perf_counter() - t0
+        if not g:
+            raise RuntimeError("reference lancius_graph_load failed")
+        best = dt if best is None else min(best, dt)
+        for i in range(g.contents.node_count):  # its graph_destroy leaves the weights to the caller
+            n = g.contents.nodes[i]
+            if n.contents.runtime_data:
+                libc.free(C.c_void_p(C.addressof(n.contents.runtime_data.contents)))
+                n.contents.runtime_data = None
+        ref.lancius_graph_destroy(g)
+    size = v10.stat().st_size
+    return {"ms": round(best * 1e3, 2), "GB/s": round(size / best / 1e9, 2), "file_MiB": round(size / 2 ** 20, 1),
+            "note": "reference lancius_graph_load (lancius_serialize.c:65-259) into host fp64, page cache warm"}
 
 
 def int8_cases(dev, steps, warmup) -> dict:
@@ -478,6 +564,7 @@ def main() -> int:
                             "hbm_copy_GBs_measured": round(measured_hbm, 1), "hbm_GBs_spec": PEAK_HBM},
     }
     extra = {}
+    load_dir, load_files = None, None
     if not args.quick:
         steps = max(5, args.steps)
         for name, (m, k, n) in (("gemm_1024", (1024, 1024, 1024)), ("gemm_2048", (2048, 2048, 2048)),
@@ -506,6 +593,10 @@ def main() -> int:
         extra.update(conv_bwd_cases(dev, steps, 3))
         log("row and elementwise kernels")
         extra.update(rowop_cases(dev, max(20, steps), 5))
+        log("model files to HBM")
+        load_dir = Path(tempfile.mkdtemp(prefix="lancius_load_"))
+        load_files = write_load_models(load_dir)
+        extra.update(model_load_cases(dev, *load_files))
         log("host-pointer bridge")
         extra["kernel_matmul_f32_host_bridge_4096"] = bridge_case(dev)
         log("mlp graph")
@@ -553,6 +644,13 @@ def main() -> int:
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(M, K, N)
+        if load_files and result["cpu_baseline"] and result["cpu_baseline"]["kind"] == "reference":
+            import oracle
+
+            result["cpu_baseline"]["other_configs"][f"model_load_v10_fp64_{LOAD_LAYERS}x{LOAD_DIM}x{LOAD_DIM}"] = \
+                cpu_model_load(oracle.ref_lib(), load_files[0])
+    if load_dir is not None:
+        shutil.rmtree(load_dir, ignore_errors=True)
     print(json.dumps(result))
     return 0
 

@@ -119,7 +119,7 @@ def build_graph() -> Path:
     out = PKG / "liblancius_graph.so"
     tmp = out.with_suffix(".so.tmp")
     _run(["gcc", *C_FLAGS, "-shared", "-o", str(tmp), *[str(CSRC / s) for s in HOST_C_SOURCES],
-          "-lm", "-Wl,--no-undefined"])
+          "-lm", "-pthread", "-Wl,--no-undefined"])
     os.replace(tmp, out)
     return out
 

@@ -171,6 +171,10 @@ void lancius_hip_ctx_destroy(lancius_hip_ctx* ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
     if (ctx->counters) (void)hipFree(ctx->counters);
+    for (int s = 0; s < 3; ++s) {
+        if (ctx->host_stage[s]) (void)hipHostFree(ctx->host_stage[s]);
+        if (ctx->stage_done[s]) (void)hipEventDestroy(ctx->stage_done[s]);
+    }
     (void)hipEventDestroy(ctx->ev_start);
     (void)hipEventDestroy(ctx->ev_stop);
     (void)hipEventDestroy(ctx->ev_order);

@@ -21,6 +21,8 @@ struct lancius_hip_ctx {
     int owns_stream;        // stream created by lancius_hip_ctx_create_own_stream
     int capturing;          // between lancius_hip_capture_begin and _end
     hipEvent_t ev_order;    // lancius_hip_stream_wait
+    void* host_stage[3];    // pinned staging of lancius_hip_upload_file, kept until destroy
+    hipEvent_t stage_done[3];
 };
 
 struct lancius_hip_graph {

@@ -13,6 +13,7 @@
  */
 #define _GNU_SOURCE
 #include <fcntl.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -48,7 +49,7 @@ __attribute__((constructor)) static void crc_init(void) {
         for (int t = 1; t < 8; t++) crc_tab[t][i] = (crc_tab[t - 1][i] >> 8) ^ crc_tab[0][crc_tab[t - 1][i] & 0xFFu];
 }
 
-uint32_t lancius_crc32(uint32_t crc, const void* data, size_t len) {
+static uint32_t crc32_serial(uint32_t crc, const void* data, size_t len) {
     const uint8_t* p = (const uint8_t*)data;
     crc = ~crc;
     while (len >= 8) {
@@ -62,6 +63,78 @@ uint32_t lancius_crc32(uint32_t crc, const void* data, size_t len) {
     }
     while (len--) crc = crc_tab[0][(crc ^ *p++) & 0xFFu] ^ (crc >> 8);
     return ~crc;
+}
+
+/* Polynomials over GF(2) modulo P in the reflected representation of the
+ * table above: bit k holds the coefficient of x^(31-k), so 1u << 31 is 1 and
+ * multiplying by x is a right shift that folds bit 0 (x^32) back in as the
+ * low terms of P. */
+static uint32_t gf2_mulmod(uint32_t a, uint32_t b) {
+    uint32_t prod = 0;
+    for (uint32_t m = 1u << 31; m; m >>= 1) {
+        if (a & m) prod ^= b;
+        b = (b & 1u) ? (b >> 1) ^ 0xEDB88320u : b >> 1;
+    }
+    return prod;
+}
+
+/* x^(8 n) mod P by squaring: x^(2^j) for every set bit j of 8n. */
+static uint32_t x_pow_8n(uint64_t n) {
+    uint32_t result = 1u << 31, sq = 1u << 30; /* 1 and x */
+    for (uint64_t e = n << 3; e; e >>= 1) {
+        if (e & 1u) result = gf2_mulmod(result, sq);
+        sq = gf2_mulmod(sq, sq);
+    }
+    return result;
+}
+
+/* CRC of A followed by B from crc(A), crc(B) and |B|: the bits of A move
+ * 8|B| places further from the end, i.e. crc(A) * x^(8|B|) mod P, and the
+ * pre/post-conditioning terms cancel (the combination used by zlib's
+ * crc32_combine, M. Adler). */
+static uint32_t crc32_combine_(uint32_t crc_a, uint32_t crc_b, uint64_t len_b) {
+    return gf2_mulmod(x_pow_8n(len_b), crc_a) ^ crc_b;
+}
+
+typedef struct {
+    const uint8_t* p;
+    size_t len;
+    uint32_t crc;
+} crc_job;
+
+static void* crc_worker(void* arg) {
+    crc_job* j = (crc_job*)arg;
+    j->crc = crc32_serial(0, j->p, j->len);
+    return NULL;
+}
+
+/* Large buffers are split over up to 16 threads (each chunk's CRC from 0)
+ * and the chunk CRCs combined in order; the result equals the serial CRC. */
+uint32_t lancius_crc32(uint32_t crc, const void* data, size_t len) {
+    enum { MAX_JOBS = 16 };
+    const size_t min_chunk = (size_t)4 << 20;
+    long cpus = sysconf(_SC_NPROCESSORS_ONLN);
+    size_t jobs = len / min_chunk;
+    if (jobs > MAX_JOBS) jobs = MAX_JOBS;
+    if (cpus > 0 && jobs > (size_t)cpus) jobs = (size_t)cpus;
+    if (jobs < 2) return crc32_serial(crc, data, len);
+    crc_job job[MAX_JOBS];
+    pthread_t tid[MAX_JOBS];
+    int started[MAX_JOBS] = {0};
+    const uint8_t* p = (const uint8_t*)data;
+    const size_t chunk = len / jobs;
+    for (size_t i = 0; i < jobs; i++) {
+        job[i].p = p + i * chunk;
+        job[i].len = i + 1 == jobs ? len - i * chunk : chunk;
+        started[i] = i > 0 && pthread_create(&tid[i], NULL, crc_worker, &job[i]) == 0;
+    }
+    for (size_t i = 0; i < jobs; i++)
+        if (!started[i]) crc_worker(&job[i]); /* the calling thread takes chunk 0 and any thread that failed */
+    for (size_t i = 0; i < jobs; i++) {
+        if (started[i]) pthread_join(tid[i], NULL);
+        crc = crc32_combine_(crc, job[i].crc, job[i].len);
+    }
+    return crc;
 }
 
 /* ---- reading ------------------------------------------------------------------ */

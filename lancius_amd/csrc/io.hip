@@ -1,8 +1,9 @@
-// Model-file tensors to HBM: the file is read with pread into two pinned host
-// buffers in turn; each filled buffer is copied to the device asynchronously
-// on the context's stream while the host reads the next piece, and fp64 or
-// int8 pieces are converted to fp32 by a kernel on the device.  An event per
-// buffer keeps the host from refilling a buffer whose copy has not finished.
+// Model-file tensors to HBM: the file is read with pread into three pinned
+// host pieces in turn (kept in the context); each filled piece is copied to
+// the device asynchronously on the context's stream while the host reads the
+// next, and fp64 or int8 pieces are converted to fp32 by a kernel on the
+// device from a staging slot of the context workspace.  An event per piece
+// keeps the host from refilling a piece whose copy has not finished.
 #include <errno.h>
 #include <fcntl.h>
 #include <sys/stat.h>
@@ -46,20 +47,16 @@ int read_fully(int fd, void* dst, size_t bytes, uint64_t offset) {
     return 0;
 }
 
-struct Staging {
-    void* host[2] = {nullptr, nullptr};
-    void* dev[2] = {nullptr, nullptr};
-    hipEvent_t done[2] = {nullptr, nullptr};
+constexpr int kStages = 3;
+
+// Waits for every staging piece still in flight (on an error path the
+// copies enqueued so far must finish before the caller reuses anything).
+struct Drain {
+    lancius_hip_ctx* ctx;
+    bool enqueued = false;
     int fd = -1;
-    hipStream_t stream = nullptr;
-    bool enqueued = false;  // copies may be in flight: drain before freeing
-    ~Staging() {
-        if (enqueued) (void)hipStreamSynchronize(stream);
-        for (int s = 0; s < 2; ++s) {
-            if (host[s]) (void)hipHostFree(host[s]);
-            if (dev[s]) (void)hipFree(dev[s]);
-            if (done[s]) (void)hipEventDestroy(done[s]);
-        }
+    ~Drain() {
+        if (enqueued) (void)hipStreamSynchronize(ctx->stream);
         if (fd >= 0) close(fd);
     }
 };
@@ -72,7 +69,8 @@ using namespace lancius;
 extern "C" int lancius_hip_upload_file(lancius_hip_ctx* ctx, const char* path, size_t count,
                                        const lancius_hip_file_tensor* tensors) {
     LANCIUS_REQUIRE(ctx && path && (count == 0 || tensors), LANCIUS_HIP_ERR_NULL_PTR, "upload_file: NULL argument");
-    Staging st;
+    LANCIUS_REQUIRE(!ctx->capturing, LANCIUS_HIP_ERR_UNSUPPORTED, "upload_file: the context is capturing a graph");
+    Drain st{ctx};
     st.fd = open(path, O_RDONLY | O_CLOEXEC);
     LANCIUS_REQUIRE(st.fd >= 0, LANCIUS_HIP_ERR_UNSUPPORTED, "upload_file: cannot open %s", path);
     struct stat sb;
@@ -98,14 +96,21 @@ extern "C" int lancius_hip_upload_file(lancius_hip_ctx* ctx, const char* path, s
                         (unsigned long long)file_size);
     }
     if (int rc = bind_device(ctx)) return rc;
-    for (int s = 0; s < 2; ++s) {
-        LANCIUS_HIP_TRY(hipHostMalloc(&st.host[s], kPiece, hipHostMallocDefault), "hipHostMalloc(staging)");
-        if (convert) LANCIUS_HIP_TRY(hipMalloc(&st.dev[s], kPiece), "hipMalloc(staging)");
-        LANCIUS_HIP_TRY(hipEventCreateWithFlags(&st.done[s], hipEventDisableTiming), "hipEventCreate");
+    // pinned pieces and their events live in the context (allocated once)
+    for (int s = 0; s < kStages; ++s) {
+        if (!ctx->host_stage[s])
+            LANCIUS_HIP_TRY(hipHostMalloc(&ctx->host_stage[s], kPiece, hipHostMallocDefault), "hipHostMalloc(staging)");
+        if (!ctx->stage_done[s])
+            LANCIUS_HIP_TRY(hipEventCreateWithFlags(&ctx->stage_done[s], hipEventDisableTiming), "hipEventCreate");
     }
-    st.stream = ctx->stream;
+    char* dev_stage = nullptr;  // conversions read their piece from the context workspace
+    if (convert) {
+        void* ws = nullptr;
+        if (int rc = workspace(ctx, kStages * kPiece, &ws)) return rc;
+        dev_stage = (char*)ws;
+    }
     int slot = 0;
-    bool used[2] = {false, false};
+    bool used[kStages] = {false, false, false};
     for (size_t t = 0; t < count; ++t) {
         const lancius_hip_file_tensor& x = tensors[t];
         const size_t eb = file_elem_bytes(x.file_dtype);
@@ -113,30 +118,32 @@ extern "C" int lancius_hip_upload_file(lancius_hip_ctx* ctx, const char* path, s
         for (uint64_t e0 = 0; e0 < x.elements; e0 += per_piece) {
             const size_t n = (size_t)std::min<uint64_t>(per_piece, x.elements - e0);
             const size_t bytes = n * eb;
-            if (used[slot]) LANCIUS_HIP_TRY(hipEventSynchronize(st.done[slot]), "hipEventSynchronize(staging)");
-            LANCIUS_REQUIRE(read_fully(st.fd, st.host[slot], bytes, x.file_offset + e0 * eb) == 0,
+            if (used[slot]) LANCIUS_HIP_TRY(hipEventSynchronize(ctx->stage_done[slot]), "hipEventSynchronize(staging)");
+            void* host = ctx->host_stage[slot];
+            LANCIUS_REQUIRE(read_fully(st.fd, host, bytes, x.file_offset + e0 * eb) == 0,
                             LANCIUS_HIP_ERR_UNSUPPORTED, "upload_file: read of %s failed", path);
             st.enqueued = true;
             if (x.dst_dtype == x.file_dtype) {
                 char* dst = (char*)x.dst + e0 * eb;
-                LANCIUS_HIP_TRY(hipMemcpyAsync(dst, st.host[slot], bytes, hipMemcpyHostToDevice, ctx->stream),
+                LANCIUS_HIP_TRY(hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, ctx->stream),
                                 "hipMemcpyAsync(upload_file)");
             } else {
-                LANCIUS_HIP_TRY(hipMemcpyAsync(st.dev[slot], st.host[slot], bytes, hipMemcpyHostToDevice, ctx->stream),
+                char* stage = dev_stage + (size_t)slot * kPiece;
+                LANCIUS_HIP_TRY(hipMemcpyAsync(stage, host, bytes, hipMemcpyHostToDevice, ctx->stream),
                                 "hipMemcpyAsync(upload_file)");
                 float* dst = (float*)x.dst + e0;
                 const unsigned grid = (unsigned)std::min<size_t>(4096, (n + 255) / 256);
                 if (x.file_dtype == LANCIUS_HIP_FILE_F64)
                     hipLaunchKernelGGL(f64_to_f32, dim3(grid), dim3(256), 0, ctx->stream, dst,
-                                       (const double*)st.dev[slot], n);
+                                       (const double*)stage, n);
                 else
                     hipLaunchKernelGGL(i8_to_f32, dim3(grid), dim3(256), 0, ctx->stream, dst,
-                                       (const int8_t*)st.dev[slot], x.scale, n);
+                                       (const int8_t*)stage, x.scale, n);
                 if (int rc = check_launch("upload_file convert")) return rc;
             }
-            LANCIUS_HIP_TRY(hipEventRecord(st.done[slot], ctx->stream), "hipEventRecord(staging)");
+            LANCIUS_HIP_TRY(hipEventRecord(ctx->stage_done[slot], ctx->stream), "hipEventRecord(staging)");
             used[slot] = true;
-            slot ^= 1;
+            slot = (slot + 1) % kStages;
         }
     }
     LANCIUS_HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(upload_file)");

@@ -85,11 +85,14 @@ def check_against_records(g, recs, weights_loaded=True):
 # ---- CRC-32 ---------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("n", [0, 1, 7, 8, 9, 63, 1000, 1 << 20])
+@pytest.mark.parametrize("n", [0, 1, 7, 8, 9, 63, 1000, 1 << 20, (40 << 20) + 7])
 def test_crc32_matches_zlib(n):
+    """Serial below 8 MiB; above, chunk CRCs on threads joined by the
+    x^(8 len) mod P combination."""
     lib = graph_lib()
     buf = np.random.default_rng(n).integers(0, 256, n, dtype=np.uint8).tobytes()
     assert lib.lancius_crc32(0, buf, n) == zlib.crc32(buf)
+    assert lib.lancius_crc32(0xDEADBEEF, buf, n) == zlib.crc32(buf, 0xDEADBEEF)
     # chained: crc(a + b) == crc(crc(a), b)
     h = n // 3
     assert lib.lancius_crc32(lib.lancius_crc32(0, buf[:h], h), buf[h:], n - h) == zlib.crc32(buf)
