@@ -528,6 +528,11 @@ def main() -> int:
     if device_count() < 1:
         print("bench.py: no GPU visible to HIP", file=sys.stderr)
         return 1
+    # stdout carries exactly one JSON line: everything else the libraries
+    # print (loader and pass messages) goes to stderr
+    sys.stdout.flush()
+    json_out = os.fdopen(os.dup(1), "w")
+    os.dup2(2, 1)
     dev = Device(0)
     M = N = K = 4096
     log("device ceilings")
@@ -651,7 +656,9 @@ def main() -> int:
                 cpu_model_load(oracle.ref_lib(), load_files[0])
     if load_dir is not None:
         shutil.rmtree(load_dir, ignore_errors=True)
-    print(json.dumps(result))
+    sys.stdout.flush()
+    json_out.write(json.dumps(result) + "\n")
+    json_out.flush()
     return 0
 
 
