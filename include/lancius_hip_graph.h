@@ -7,12 +7,19 @@
  * _static (bleeding/v11A1/src/runtime/lancius_scheduler.c:311-520) and their
  * dispatch execute_node_math (:61-309) for the ops of the device path:
  * INPUT, CONST, NOP, MATMUL, ADD, BROADCAST, RELU, GELU, SOFTMAX, LAYERNORM,
- * ATTENTION, CONV2D, CONV2D_RELU_FUSED, RESHAPE, FLATTEN.
+ * ATTENTION, CONV2D, CONV2D_RELU_FUSED, RESHAPE, FLATTEN; the training ops
+ * SUB, MUL, RELU_BWD, TRANSPOSE, SUM, SUM_AXIS0, SUM_AXIS1, SOFTMAX_BWD,
+ * CROSS_ENTROPY, CROSS_ENTROPY_BWD, CONV2D_BWD, CONV2D_BWD_W, MAXPOOL2D,
+ * MAXPOOL2D_BWD; and RMSNORM, SWIGLU, GQA, ROPE.  MATMUL and conv nodes whose
+ * weight operand is an int8 INPUT (dtype INT8 or an int8 copy bound) run on
+ * the int8 kernels.
  *
  * Compilation turns the waves into a launch list:
  *  - MATMUL -> ADD(BROADCAST bias) -> RELU|GELU -> ADD(residual) chains whose
  *    intermediates have one consumer become one GEMM with a fused epilogue;
  *  - RESHAPE / FLATTEN become aliases of their input (no copy);
+ *  - a TRANSPOSE whose only consumer is a MATMUL is folded into it (the GEMM
+ *    reads that operand transposed);
  *  - launches of one wave with the same shape are merged into one grouped
  *    launch (the branches of a batch).
  * Buffer lifetimes are recomputed over that launch list.  The caller's plan
