@@ -42,6 +42,7 @@ struct AttnParams {
     int causal;    // query i sees keys j <= i + (Skv - S)
     float qscale;  // scale * log2(e)
     int q_tiles;
+    int pair_tiles;  // causal grid small enough to be resident at once (see attention_d64)
     int Z;         // count * batch independent problems
 };
 
@@ -67,7 +68,14 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     const int z = rem / p.H;
     const int h = rem - z * p.H;
     const int g = z / p.batch, b = z % p.batch;
-    const int qt = p.causal ? (p.q_tiles - 1 - t_rank) : t_rank;
+    // Causal order: longest tiles first.  When every workgroup is resident at
+    // once (p.pair_tiles: two per CU), ranks T/2.. run the shortest tiles
+    // first instead, so the workgroup that shares a CU with the k-th longest
+    // tile gets the k-th shortest one (tile T-1-k with tile k).
+    const int half_t = p.q_tiles / 2;
+    const int qt = !p.causal                        ? t_rank
+                   : (p.pair_tiles && t_rank >= p.q_tiles - half_t) ? t_rank - (p.q_tiles - half_t)
+                                                                      : p.q_tiles - 1 - t_rank;
     const int S = p.S, H = p.H, Skv = p.Skv;
     const int off = Skv - S;  // causal offset of the query rows into the key sequence
     const int hk = h / (H / p.Hkv);
@@ -618,6 +626,7 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
         p.q_tiles = (int)((S + kBQ - 1) / kBQ);
         const size_t tasks = (size_t)p.q_tiles * H * z;
         LANCIUS_REQUIRE(tasks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention: too many tiles");
+        p.pair_tiles = causal && tasks <= 2 * (size_t)cu_count(ctx) && tune("attn_pair", 1);
         hipLaunchKernelGGL(attention_d64, dim3((unsigned)tasks), dim3(256), 0, ctx->stream, p);
         if (int rc = check_launch("attention_d64")) return rc;
     } else {

@@ -52,6 +52,16 @@ int tune(const char* key, int fallback) {
     return fallback;
 }
 
+int cu_count(lancius_hip_ctx* ctx) {
+    if (ctx->cus <= 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, ctx->device) != hipSuccess || n <= 0)
+            n = 256;  // MI355X
+        ctx->cus = n;
+    }
+    return ctx->cus;
+}
+
 int workspace(lancius_hip_ctx* ctx, size_t bytes, void** out) {
     *out = nullptr;
     if (bytes <= ctx->workspace_bytes && ctx->workspace) {

@@ -23,6 +23,7 @@ struct lancius_hip_ctx {
     hipEvent_t ev_order;    // lancius_hip_stream_wait
     void* host_stage[3];    // pinned staging of lancius_hip_upload_file, kept until destroy
     hipEvent_t stage_done[3];
+    int cus;                // compute units of the device (0 until first asked)
 };
 
 struct lancius_hip_graph {
@@ -55,6 +56,9 @@ int tune(const char* key, int fallback);
 // kept until the context is destroyed.  Calls on one context are ordered by
 // its stream, so one buffer serves every kernel of the context.
 int workspace(lancius_hip_ctx* ctx, size_t bytes, void** out);
+
+// Compute units of the context's device (cached in the context).
+int cu_count(lancius_hip_ctx* ctx);
 
 // At least n zero-initialised arrival counters (see counters in the context);
 // every kernel that increments a counter returns it to zero before exiting.
