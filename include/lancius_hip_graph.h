@@ -21,7 +21,9 @@
  *  - a TRANSPOSE whose only consumer is a MATMUL is folded into it (the GEMM
  *    reads that operand transposed);
  *  - launches of one wave with the same shape are merged into one grouped
- *    launch (the branches of a batch).
+ *    launch (the branches of a batch);
+ *  - a small-batch GEMM -> GEMM [-> SOFTMAX] chain (M <= 64 rows, <= 64
+ *    outputs) becomes one lancius_hip_mlp2_f32 call (two kernels).
  * Buffer lifetimes are recomputed over that launch list.  The caller's plan
  * offsets are used unchanged (buffer = arena + plan->offsets[id]) when they
  * keep every pair of simultaneously live buffers apart; otherwise the program
@@ -51,6 +53,8 @@ typedef struct lancius_device_program lancius_device_program;
 #define LANCIUS_DEVICE_NO_FUSION 0x1u /* one launch per node, no grouping */
 #define LANCIUS_DEVICE_KEEP_ALL  0x2u /* every node keeps its own buffer (readable after run) */
 #define LANCIUS_DEVICE_NO_GROUP  0x4u /* fuse epilogues but do not merge branches */
+#define LANCIUS_DEVICE_NO_CHAIN 0x10u /* keep a small GEMM -> GEMM -> SOFTMAX chain as separate
+                                         launches (default: one lancius_hip_mlp2_f32 call) */
 #define LANCIUS_DEVICE_GRAPH     0x8u /* first run: eager + capture into a HIP graph; later runs
                                          replay it on the context's stream (on a null-stream
                                          context: on a private stream, ordered after and before

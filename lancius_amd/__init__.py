@@ -8,10 +8,10 @@ Native libraries (built in-tree by `python -m lancius_amd.build`):
 This Python package only loads and wraps them; it computes nothing itself.
 """
 from . import abi, prng
-from .runtime import (ACT_GELU, ACT_NONE, ACT_RELU, DEVICE_GRAPH, DEVICE_KEEP_ALL, DEVICE_NO_FUSION, DEVICE_NO_GROUP, Device,
+from .runtime import (ACT_GELU, ACT_NONE, ACT_RELU, DEVICE_GRAPH, DEVICE_KEEP_ALL, DEVICE_NO_CHAIN, DEVICE_NO_FUSION, DEVICE_NO_GROUP, Device,
                       DeviceProgram, HipError, device_count, graph_lib, hip_lib)
 
 __all__ = [
     "abi", "prng", "Device", "DeviceProgram", "HipError", "device_count", "graph_lib", "hip_lib",
-    "ACT_NONE", "ACT_RELU", "ACT_GELU", "DEVICE_GRAPH", "DEVICE_NO_FUSION", "DEVICE_KEEP_ALL", "DEVICE_NO_GROUP",
+    "ACT_NONE", "ACT_RELU", "ACT_GELU", "DEVICE_GRAPH", "DEVICE_NO_CHAIN", "DEVICE_NO_FUSION", "DEVICE_KEEP_ALL", "DEVICE_NO_GROUP",
 ]

@@ -36,7 +36,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip", "reduce.hip", "pool.hip",
-               "int8.hip", "io.hip", "probe.hip"]
+               "int8.hip", "io.hip", "chain.hip", "probe.hip"]
 HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c", "host/graph_autodiff.c", "host/graph_io.c"]
 DEVICE_C_SOURCES = ["host/device_exec.c"]
 

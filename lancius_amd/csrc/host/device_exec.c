@@ -18,14 +18,14 @@
 typedef enum {
     L_GEMM, L_CONV, L_ATTN, L_LN, L_SOFTMAX, L_ADD, L_RELU, L_GELU, L_BCAST,
     L_SUB, L_MUL, L_RELU_BWD, L_TRANSPOSE, L_SUM, L_SUM0, L_SUM1, L_SOFTMAX_BWD, L_CE, L_CE_BWD,
-    L_CONV_BWD_IN, L_CONV_BWD_W, L_POOL, L_POOL_BWD, L_RMSNORM, L_SWIGLU, L_GQA, L_ROPE
+    L_CONV_BWD_IN, L_CONV_BWD_W, L_POOL, L_POOL_BWD, L_RMSNORM, L_SWIGLU, L_GQA, L_ROPE, L_MLP2
 } lkind;
 
 enum { ROLE_NONE = 0, ROLE_INPUT, ROLE_CONST, ROLE_POOLED, ROLE_ALIAS, ROLE_FUSED };
 
 typedef struct {
     uint32_t out;   /* node id written */
-    uint32_t in[4]; /* node ids read (alias roots), NONE when unused */
+    uint32_t in[6]; /* node ids read (alias roots), NONE when unused */
 } member_t;
 
 typedef struct {
@@ -236,7 +236,7 @@ static int make_launch(cstate* c, const lancius_node* n, launch_t* L) {
     L->count = 1;
     member_t* m = &L->m[0];
     m->out = n->id;
-    for (int j = 0; j < 4; j++) m->in[j] = NONE;
+    for (int j = 0; j < 6; j++) m->in[j] = NONE;
     for (uint32_t j = 0; j < n->input_count; j++)
         if (!n->inputs[j]) return fail(LANCIUS_HIP_ERR_NULL_PTR, "node with a NULL input");
     const size_t e = elems(n);
@@ -689,6 +689,50 @@ int lancius_device_program_info_get(const lancius_device_program* p, lancius_dev
 
 #define CALLOC(ptr, n) ((ptr) = calloc((n) ? (n) : 1, sizeof(*(ptr))))
 
+/* GEMM(+bias, act) -> GEMM(+bias) [-> SOFTMAX] on adjacent launches, the
+ * hidden and logit tensors each read once by the next launch, small enough
+ * for lancius_hip_mlp2_f32 (M <= 64, N2 <= 64, M*N1 <= 16384,
+ * N1*N2 <= 8192): one launch instead of up to three dependent ones. */
+static uint32_t fuse_mlp2(lancius_device_program* p, const cstate* c, uint32_t nl) {
+    for (uint32_t s = 0; s + 1 < nl; s++) {
+        launch_t* A = &p->launches[s];
+        launch_t* B = &p->launches[s + 1];
+        if (A->kind != L_GEMM || B->kind != L_GEMM || A->count != 1 || B->count != 1) continue;
+        if (A->ta || A->tb || A->i8 || A->has_res || B->ta || B->tb || B->i8 || B->has_res || B->act) continue;
+        const uint32_t h = A->m[0].out, y = B->m[0].out;
+        if (B->m[0].in[0] != h || B->m[0].in[1] == h || c->consumers[h] != 1) continue;
+        const size_t M = A->d[0], K1 = A->d[1], N1 = A->d[2], N2 = B->d[2];
+        if (B->d[0] != M || B->d[1] != N1 || M > 64 || N2 > 64 || M * N1 > 16384 || N1 * N2 > 8192) continue;
+        int sm = 0;
+        if (s + 2 < nl) {
+            const launch_t* S = &p->launches[s + 2];
+            sm = S->kind == L_SOFTMAX && S->count == 1 && S->m[0].in[0] == y && c->consumers[y] == 1 &&
+                 S->d[0] == M && S->d[1] == N2;
+        }
+        launch_t F = *A;
+        F.kind = L_MLP2;
+        F.m[0].out = sm ? p->launches[s + 2].m[0].out : y;
+        F.m[0].in[3] = B->m[0].in[1]; /* W2 */
+        F.m[0].in[4] = B->m[0].in[2]; /* b2 */
+        F.d[0] = M;
+        F.d[1] = K1;
+        F.d[2] = N1;
+        F.d[3] = N2;
+        F.d[4] = (size_t)sm;
+        p->role[h] = ROLE_FUSED;
+        p->info.fused_nodes++;
+        if (sm) {
+            p->role[y] = ROLE_FUSED;
+            p->info.fused_nodes++;
+        }
+        const uint32_t drop = sm ? 2 : 1;
+        p->launches[s] = F;
+        for (uint32_t k = s + 1; k + drop < nl; k++) p->launches[k] = p->launches[k + drop];
+        nl -= drop;
+    }
+    return nl;
+}
+
 int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, const lancius_schedule* sched,
                                   const lancius_memory_plan* plan, uint32_t flags, lancius_device_program** out) {
     if (!ctx || !g || !sched || !out) return LANCIUS_HIP_ERR_NULL_PTR;
@@ -860,6 +904,8 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         }
         nl = k;
     }
+    if (!(flags & (LANCIUS_DEVICE_NO_FUSION | LANCIUS_DEVICE_KEEP_ALL | LANCIUS_DEVICE_NO_CHAIN)))
+        nl = fuse_mlp2(p, &c, nl);
     p->n_launches = nl;
     p->info.launches = nl;
 
@@ -869,7 +915,7 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         for (uint32_t k = 0; k < L->count; k++) {
             birth[L->m[k].out] = s;
             if (last[L->m[k].out] < s) last[L->m[k].out] = s;
-            for (int j = 0; j < 4; j++) {
+            for (int j = 0; j < 6; j++) {
                 const uint32_t r = L->m[k].in[j];
                 if (r != NONE && last[r] < s) last[r] = s;
             }
@@ -1103,6 +1149,10 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
                                                  (float)(1.0 / sqrt((double)L->d[3])));
         case L_ROPE:
             return lancius_hip_rope_f32(ctx, P(m->out), P(m->in[0]), 2, 1, L->d[0], L->d[1], L->d[2], 0);
+        case L_MLP2:
+            return lancius_hip_mlp2_f32(ctx, P(m->out), L->d[4] ? prog->argmax[m->out] : NULL, P(m->in[0]),
+                                        P(m->in[1]), P(m->in[2]), L->act, P(m->in[3]), P(m->in[4]), L->d[0], L->d[1],
+                                        L->d[2], L->d[3], (int)L->d[4]);
         case L_POOL_BWD:
             return lancius_hip_maxpool2d_bwd_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), L->d[0], L->d[1],
                                                  L->d[2], L->d[3], L->d[4], L->d[5], L->d[6], L->d[7]);

@@ -8,6 +8,7 @@
 namespace lancius {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // MI355X: 256 CUs in 8 XCDs.  Consecutive workgroup ids are dealt round-robin

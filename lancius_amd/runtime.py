@@ -21,7 +21,7 @@ ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
 MAX_GROUP = 16
 
 # LANCIUS_DEVICE_* flags (include/lancius_hip_graph.h)
-DEVICE_NO_FUSION, DEVICE_KEEP_ALL, DEVICE_NO_GROUP, DEVICE_GRAPH = 0x1, 0x2, 0x4, 0x8
+DEVICE_NO_FUSION, DEVICE_KEEP_ALL, DEVICE_NO_GROUP, DEVICE_GRAPH, DEVICE_NO_CHAIN = 0x1, 0x2, 0x4, 0x8, 0x10
 
 
 class HipError(RuntimeError):
@@ -76,6 +76,7 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_attention_grouped_f32.argtypes = [vp, sz, vpp, vpp, vpp, vpp, sz, sz, sz, i32, f32]
     lib.lancius_hip_layernorm_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, f32]
     lib.lancius_hip_softmax_f32.argtypes = [vp, vp, vp, vp, sz, sz]
+    lib.lancius_hip_mlp2_f32.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, vp, sz, sz, sz, sz, i32]
     lib.lancius_hip_add_f32.argtypes = [vp, vp, vp, vp, sz]
     lib.lancius_hip_relu_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_gelu_f32.argtypes = [vp, vp, vp, sz]
@@ -293,6 +294,10 @@ class Device:
 
     def softmax(self, probs, argmax, x, rows, cols) -> None:
         _check(self.lib.lancius_hip_softmax_f32(self.ctx, _vp(probs), _vp(argmax), _vp(x), rows, cols))
+
+    def mlp2(self, out, argmax, x, w1, b1, act1, w2, b2, M, K1, N1, N2, softmax=True) -> None:
+        _check(self.lib.lancius_hip_mlp2_f32(self.ctx, _vp(out), _vp(argmax), _vp(x), _vp(w1), _vp(b1), act1,
+                                             _vp(w2), _vp(b2), M, K1, N1, N2, int(bool(softmax))))
 
     def add(self, out, a, b, n) -> None:
         _check(self.lib.lancius_hip_add_f32(self.ctx, _vp(out), _vp(a), _vp(b), n))

@@ -8,8 +8,8 @@ import numpy as np
 import pytest
 
 import oracle
-from lancius_amd import (DEVICE_GRAPH, DEVICE_KEEP_ALL, DEVICE_NO_FUSION, DeviceProgram, HipError, abi, graph_lib, graphs,
-                         prng)
+from lancius_amd import (DEVICE_GRAPH, DEVICE_KEEP_ALL, DEVICE_NO_CHAIN, DEVICE_NO_FUSION, DeviceProgram, HipError, abi,
+                         graph_lib, graphs, prng)
 from tests.conftest import case
 
 pytestmark = pytest.mark.gpu
@@ -74,19 +74,26 @@ def _feed(prog, bg, feeds):
 # ---- MLP ----------------------------------------------------------------------------
 
 
-def test_mlp_fused_matches_reference(dev):
+@pytest.mark.parametrize("chain", [True, False])
+def test_mlp_fused_matches_reference(dev, chain):
+    """Default: the whole MLP is one lancius_hip_mlp2_f32 launch; with
+    DEVICE_NO_CHAIN it is GEMM+bias+ReLU, GEMM+bias, softmax."""
     pl = Planned(graphs.build_mlp(graph_lib()))
     feeds = {n: GO[f"mlp_{n}"] for n in pl.bg.inputs}
-    case("mlp fused")
-    prog = pl.program(dev)
-    _feed(prog, pl.bg, feeds)
-    prog.run()
+    case(f"mlp fused, chain={chain}")
+    prog = pl.program(dev, flags=0 if chain else DEVICE_NO_CHAIN)
     sm = pl.bg.node("softmax")
-    got = prog.download(sm)
-    assert oracle.normwise_error(got, GO["mlp_softmax"]) <= oracle.tolerance(784)
-    assert np.array_equal(prog.argmax(sm), oracle.argmax(GO["mlp_softmax"]))
+    for _ in range(3):  # the chain's arrival counters must come back to zero
+        _feed(prog, pl.bg, feeds)
+        prog.run()
+        got = prog.download(sm)
+        assert oracle.normwise_error(got, GO["mlp_softmax"]) <= oracle.tolerance(784)
+        assert np.array_equal(prog.argmax(sm), oracle.argmax(GO["mlp_softmax"]))
     info = prog.info()
-    assert info["launches"] == 3 and info["fused_nodes"] == 5
+    if chain:
+        assert info["launches"] == 1 and info["fused_nodes"] == 7
+    else:
+        assert info["launches"] == 3 and info["fused_nodes"] == 5
     prog.close()
     pl.close()
 
