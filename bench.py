@@ -39,7 +39,7 @@ import numpy as np
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-from lancius_amd import (DEVICE_GRAPH, Device, DeviceProgram, abi, device_count, graph_lib,  # noqa: E402
+from lancius_amd import (DEVICE_GRAPH, DEVICE_NO_CHAIN, Device, DeviceProgram, abi, device_count, graph_lib,  # noqa: E402
                          graphs, prng)
 
 PEAK_FP32_MFMA = 157.3  # TFLOP/s, MI355X dense fp32 matrix
@@ -613,10 +613,13 @@ def main() -> int:
                  "b2": np.zeros((1, 10), np.float32)}
         t, info = graph_case(dev, bg, feeds, max(20, steps), 5)
         tg, _ = graph_case(sdev, bg, feeds, max(20, steps), 5, DEVICE_GRAPH)
+        tu, info_u = graph_case(dev, bg, feeds, max(20, steps), 5, DEVICE_NO_CHAIN)
         bg.destroy()
         extra["mlp_graph_64x784x256x10"] = {"fwd_latency_ms": round(t, 4), "launches": info["launches"],
                                             "GFLOP/s": round(26.02e6 / t / 1e6, 1),
-                                            "fwd_latency_ms_hipgraph": round(tg, 4)}
+                                            "fwd_latency_ms_hipgraph": round(tg, 4),
+                                            "fwd_latency_ms_unchained": round(tu, 4),
+                                            "launches_unchained": info_u["launches"]}
         log("transformer block graph")
         bg = graphs.build_block(lib)
         feeds = {}
