@@ -32,67 +32,98 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int kMaxBlocks = 1024;
+constexpr int kMaxBlocks = 512;
 
 // ---- quantization ------------------------------------------------------------
 
+// Per-workgroup max|x| (order-independent, so the result does not depend on
+// the grid).  vec: x is 16-byte aligned; four float4 loads per thread are in
+// flight per step.
 __global__ void __launch_bounds__(kThreads) absmax_partials(float* __restrict__ part, const float* __restrict__ x,
-                                                            size_t n) {
-    __shared__ float s[kThreads];
+                                                            size_t n, int vec) {
+    __shared__ float s[kThreads / 64];
     float m = 0.0f;
-    const size_t step = (size_t)gridDim.x * kThreads;
-    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += step) m = fmaxf(m, fabsf(x[i]));
-    s[threadIdx.x] = m;
-    __syncthreads();
-    for (int w = kThreads / 2; w >= 1; w >>= 1) {
-        if ((int)threadIdx.x < w) s[threadIdx.x] = fmaxf(s[threadIdx.x], s[threadIdx.x + w]);
-        __syncthreads();
+    const size_t T = (size_t)gridDim.x * kThreads, t0 = (size_t)blockIdx.x * kThreads + threadIdx.x;
+    size_t tail = 0;
+    if (vec) {
+        const size_t n4 = n / 4;
+        const f32x4* __restrict__ x4 = (const f32x4*)x;
+        size_t i = t0;
+        for (; i + 3 * T < n4; i += 4 * T) {
+            const f32x4 a = x4[i], b = x4[i + T], c = x4[i + 2 * T], d = x4[i + 3 * T];
+            m = fmaxf(m, fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                               fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w)))));
+            m = fmaxf(m, fmaxf(fmaxf(fmaxf(fabsf(c.x), fabsf(c.y)), fmaxf(fabsf(c.z), fabsf(c.w))),
+                               fmaxf(fmaxf(fabsf(d.x), fabsf(d.y)), fmaxf(fabsf(d.z), fabsf(d.w)))));
+        }
+        for (; i < n4; i += T) {
+            const f32x4 a = x4[i];
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
+        }
+        tail = 4 * n4;
     }
-    if (threadIdx.x == 0) part[blockIdx.x] = s[0];
+    for (size_t i = tail + t0; i < n; i += T) m = fmaxf(m, fabsf(x[i]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
 }
 
+// The per-tensor scale from the partial maxima, computed by every
+// workgroup of the consuming kernel (all threads must call it):
 // scale = max|x| / 127, or 1e-8 for an all-zero tensor (fp64, as the
-// reference); also stores the other operand's host-given scale at scale[1]
-// when `other` is >= 0 (one launch for both).
-__global__ void __launch_bounds__(kThreads) absmax_scale(double* __restrict__ scale, const float* __restrict__ part,
-                                                         int count, double other) {
-    __shared__ float s[kThreads];
+// reference).  Workgroup 0 also stores it at scale_out[0], and the other
+// operand's host-given scale at scale_out[1] when `other` >= 0, for the
+// GEMM epilogue and the caller.
+__device__ double scale_from_partials(const float* __restrict__ part, int parts, double* __restrict__ scale_out,
+                                      double other) {
+    __shared__ float s[kThreads / 64];
     float m = 0.0f;
-    for (int i = threadIdx.x; i < count; i += kThreads) m = fmaxf(m, part[i]);
-    s[threadIdx.x] = m;
+    for (int i = threadIdx.x; i < parts; i += kThreads) m = fmaxf(m, part[i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = m;
     __syncthreads();
-    for (int w = kThreads / 2; w >= 1; w >>= 1) {
-        if ((int)threadIdx.x < w) s[threadIdx.x] = fmaxf(s[threadIdx.x], s[threadIdx.x + w]);
-        __syncthreads();
+    m = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    const double sc = m > 0.0f ? (double)m / 127.0 : 1e-8;
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        scale_out[0] = sc;
+        if (other >= 0.0) scale_out[1] = other;
     }
-    if (threadIdx.x == 0) {
-        scale[0] = s[0] > 0.0f ? (double)s[0] / 127.0 : 1e-8;
-        if (other >= 0.0) scale[1] = other;
-    }
+    return sc;
 }
 
 __device__ __forceinline__ int8_t quant(float v, double scale) { return (int8_t)(int)round((double)v / scale); }
 
+__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, double sc) {
+    return (uint32_t)(uint8_t)quant(a, sc) | (uint32_t)(uint8_t)quant(b, sc) << 8 |
+           (uint32_t)(uint8_t)quant(c, sc) << 16 | (uint32_t)(uint8_t)quant(d, sc) << 24;
+}
+
 // Row-major copy: q[i] = quant(x[i]).
 __global__ void __launch_bounds__(kThreads) quantize_flat(int8_t* __restrict__ q, const float* __restrict__ x,
-                                                          const double* __restrict__ scale, size_t n) {
-    const double sc = scale[0];
+                                                          const float* __restrict__ part, int parts,
+                                                          double* __restrict__ scale_out, size_t n) {
+    const double sc = scale_from_partials(part, parts, scale_out, -1.0);
     const size_t step = (size_t)gridDim.x * kThreads;
     for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += step) q[i] = quant(x[i], sc);
 }
 
 // NCHW fp32 -> NHWC int8 with Cp >= C channels per pixel (padding bytes 0),
 // through a 64 (channels) x 64 (pixels) LDS tile: reads coalesce along the
-// pixels of a channel plane, writes along the channels of a pixel.
+// pixels of a channel plane; each write is 4 channels of one pixel packed
+// into 32 bits, 16 lanes covering 64 channels of a pixel.
 __global__ void __launch_bounds__(kThreads) quantize_nchw_to_nhwc(int8_t* __restrict__ q, const float* __restrict__ x,
-                                                                  const double* __restrict__ scale, int N, int C,
-                                                                  int HW, int Cp, int tiles_p, int tiles_c) {
+                                                                  const float* __restrict__ part, int parts,
+                                                                  double* __restrict__ scale_out, double other, int N,
+                                                                  int C, int HW, int Cp, int tiles_p, int tiles_c) {
     __shared__ int8_t t[64][65];
+    const double sc = scale_from_partials(part, parts, scale_out, other);
     const int tile = blockIdx.x;
     const int n = tile / (tiles_p * tiles_c);
     const int rem = tile - n * tiles_p * tiles_c;
     const int c0 = (rem / tiles_p) * 64, p0 = (rem % tiles_p) * 64;
-    const double sc = scale[0];
     const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const float* xn = x + (size_t)n * C * HW;
 #pragma unroll
@@ -103,56 +134,101 @@ __global__ void __launch_bounds__(kThreads) quantize_nchw_to_nhwc(int8_t* __rest
     __syncthreads();
     int8_t* qn = q + (size_t)n * HW * Cp;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int p = p0 + ty + 4 * i, c = c0 + tx;
-        if (p < HW && c < Cp) qn[(size_t)p * Cp + c] = t[tx][ty + 4 * i];
+    for (int i = 0; i < 4; ++i) {
+        const int idx = threadIdx.x + kThreads * i;
+        const int pl = idx >> 4, cq = idx & 15;
+        const int p = p0 + pl, c = c0 + 4 * cq;
+        if (p < HW && c < Cp) {
+            const uint32_t v = (uint32_t)(uint8_t)t[4 * cq][pl] | (uint32_t)(uint8_t)t[4 * cq + 1][pl] << 8 |
+                               (uint32_t)(uint8_t)t[4 * cq + 2][pl] << 16 | (uint32_t)(uint8_t)t[4 * cq + 3][pl] << 24;
+            *(uint32_t*)(qn + (size_t)p * Cp + c) = v;
+        }
     }
 }
 
-// B [K][N] int8 -> B^T [N][Kp] int8 (k padded with zeros to Kp).
+// B [K][N] int8 -> B^T [N][Kp] int8 (k zero-padded to Kp, a multiple of
+// 128), one 128 (k) x 128 (n) tile per workgroup.  Reads: 16-byte runs of a
+// k-row (vec: N % 16 == 0 and B 16-byte aligned; otherwise byte loads with
+// bounds), kept in LDS as T[n/4][k] words of 4 n-bytes.  Writes: a thread
+// takes 4 columns n x 16 rows k, transposes the 16 x 4 bytes in registers and
+// stores four 16-byte runs of B^T rows; 8 lanes cover 128 contiguous bytes.
 __global__ void __launch_bounds__(kThreads) transpose_i8(int8_t* __restrict__ bt, const int8_t* __restrict__ b, int K,
-                                                         int N, int Kp, int tiles_n) {
-    __shared__ int8_t t[64][65];
-    const int k0 = (blockIdx.x / tiles_n) * 64, n0 = (blockIdx.x % tiles_n) * 64;
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+                                                         int N, int Kp, int tiles_n, int vec) {
+    constexpr int P = 130;  // words per T row (2-way bank aliasing on the writes)
+    __shared__ uint32_t T[32 * P];
+    const int k0 = (blockIdx.x / tiles_n) * 128, n0 = (blockIdx.x % tiles_n) * 128;
+    const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int k = k0 + ty + 4 * i, n = n0 + tx;
-        t[ty + 4 * i][tx] = (k < K && n < N) ? b[(size_t)k * N + n] : (int8_t)0;
+    for (int i = 0; i < 4; ++i) {
+        const int idx = tid + kThreads * i;
+        const int k = idx >> 3, c = idx & 7;
+        const int gk = k0 + k, gn = n0 + 16 * c;
+        v4i w = {0, 0, 0, 0};
+        if (gk < K) {
+            if (vec) {
+                if (gn < N) w = *(const v4i*)(b + (size_t)gk * N + gn);
+            } else {
+                uint32_t u[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    if (gn + e < N) u[e >> 2] |= (uint32_t)(uint8_t)b[(size_t)gk * N + gn + e] << (8 * (e & 3));
+                w = v4i{(int)u[0], (int)u[1], (int)u[2], (int)u[3]};
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) T[(4 * c + d) * P + k] = (uint32_t)w[d];
     }
     __syncthreads();
+    const int nq = tid >> 3, kb = tid & 7;
+    uint32_t w[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int n = n0 + ty + 4 * i, k = k0 + tx;
-        if (n < N && k < Kp) bt[(size_t)n * Kp + k] = t[tx][ty + 4 * i];
+    for (int i = 0; i < 16; ++i) w[i] = T[nq * P + 16 * kb + i];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + 4 * nq + j;
+        if (n >= N) break;
+        v4i o;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            o[m] = (int)(((w[4 * m] >> (8 * j)) & 0xffu) | ((w[4 * m + 1] >> (8 * j)) & 0xffu) << 8 |
+                         ((w[4 * m + 2] >> (8 * j)) & 0xffu) << 16 | ((w[4 * m + 3] >> (8 * j)) & 0xffu) << 24);
+        *(v4i*)(bt + (size_t)n * Kp + k0 + 16 * kb) = o;
     }
 }
 
-// A [M][K] fp32 -> [M][Kp] int8, zeros past K.  One row per blockIdx.y;
-// with K % 4 == 0 each thread converts a float4 into one 32-bit store.
+// A [M][K] fp32 -> [M][Kp] int8, zeros past K (Kp a multiple of 128, so a
+// row is D = Kp/4 words).  Each thread writes whole 32-bit words (vec: K % 4
+// == 0 and A 16-byte aligned, one float4 per word); rows shorter than the
+// workgroup share it, 256/D rows at a time.
 __global__ void __launch_bounds__(kThreads) quantize_rows_padded(int8_t* __restrict__ q, const float* __restrict__ x,
-                                                                 const double* __restrict__ scale, size_t M, int K,
-                                                                 int Kp, int vec) {
-    const double sc = scale[0];
-    const int step = gridDim.x * kThreads;
-    for (size_t r = blockIdx.y; r < M; r += gridDim.y) {
-    const float* xr = x + r * K;
-    int8_t* qr = q + r * Kp;
-    if (vec) {
-        for (int k4 = blockIdx.x * kThreads + threadIdx.x; 4 * k4 < Kp; k4 += step) {
-            const int k = 4 * k4;
+                                                                 const float* __restrict__ part, int parts,
+                                                                 double* __restrict__ scale_out, double other,
+                                                                 size_t M, int K, int Kp, int vec) {
+    const double sc = scale_from_partials(part, parts, scale_out, other);
+    const int D = Kp / 4;
+    const int rows_per = D >= kThreads ? 1 : kThreads / D;
+    const int sub = D >= kThreads ? 0 : (int)threadIdx.x / D;
+    const int d0 = D >= kThreads ? (int)threadIdx.x : (int)threadIdx.x % D;
+    const int dstep = D >= kThreads ? kThreads : D;
+    if (sub >= rows_per) return;
+    for (size_t r = (size_t)blockIdx.x * rows_per + sub; r < M; r += (size_t)gridDim.x * rows_per) {
+        const float* __restrict__ xr = x + r * K;
+        uint32_t* __restrict__ qr = (uint32_t*)(q + r * Kp);
+        for (int d = d0; d < D; d += dstep) {
+            const int k = 4 * d;
             uint32_t packed = 0;
-            if (k < K) {
-                const f32x4 v = *(const f32x4*)(xr + k);
-                packed = (uint32_t)(uint8_t)quant(v.x, sc) | (uint32_t)(uint8_t)quant(v.y, sc) << 8 |
-                         (uint32_t)(uint8_t)quant(v.z, sc) << 16 | (uint32_t)(uint8_t)quant(v.w, sc) << 24;
+            if (vec) {
+                if (k < K) {
+                    const f32x4 v = *(const f32x4*)(xr + k);
+                    packed = quant4(v.x, v.y, v.z, v.w, sc);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (k + e < K) packed |= (uint32_t)(uint8_t)quant(xr[k + e], sc) << (8 * e);
             }
-            *(uint32_t*)(qr + k) = packed;
+            qr[d] = packed;
         }
-    } else {
-        for (int k = blockIdx.x * kThreads + threadIdx.x; k < Kp; k += step)
-            qr[k] = k < K ? quant(xr[k], sc) : (int8_t)0;
-    }
     }
 }
 
@@ -347,15 +423,13 @@ unsigned grid_for(size_t work) {
     return (unsigned)std::max<size_t>(1, std::min<size_t>((work + kThreads - 1) / kThreads, 4096));
 }
 
-// Per-tensor scale of x into scale_dev (two small launches; max is
-// order-independent, so the result does not depend on the grid).
-int absmax_to_scale(lancius_hip_ctx* ctx, double* scale_dev, float* part, const float* x, size_t n,
-                    double other = -1.0) {
-    const unsigned blocks = (unsigned)std::max<size_t>(1, std::min<size_t>((n + 4095) / 4096, kMaxBlocks));
-    hipLaunchKernelGGL(absmax_partials, dim3(blocks), dim3(kThreads), 0, ctx->stream, part, x, n);
-    if (int rc = check_launch("absmax_partials")) return rc;
-    hipLaunchKernelGGL(absmax_scale, dim3(1), dim3(kThreads), 0, ctx->stream, scale_dev, part, (int)blocks, other);
-    return check_launch("absmax_scale");
+// Partial maxima of |x| into part (at most kMaxBlocks); returns their count.
+int absmax_partials_launch(lancius_hip_ctx* ctx, float* part, const float* x, size_t n, int* parts) {
+    const unsigned blocks = (unsigned)std::max<size_t>(1, std::min<size_t>((n + 8191) / 8192, kMaxBlocks));
+    const int vec = ((uintptr_t)x & 15u) == 0;
+    hipLaunchKernelGGL(absmax_partials, dim3(blocks), dim3(kThreads), 0, ctx->stream, part, x, n, vec);
+    *parts = (int)blocks;
+    return check_launch("absmax_partials");
 }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -372,10 +446,11 @@ int lancius_hip_quantize_i8(lancius_hip_ctx* ctx, int8_t* q, double* scale, cons
     if (int rc = bind_device(ctx)) return rc;
     void* ws = nullptr;
     if (int rc = workspace(ctx, kMaxBlocks * sizeof(float), &ws)) return rc;
-    if (int rc = absmax_to_scale(ctx, scale, (float*)ws, x, n)) return rc;
-    if (n == 0) return ok();
-    hipLaunchKernelGGL(quantize_flat, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, q, x, (const double*)scale,
-                       n);
+    int parts = 0;
+    if (int rc = absmax_partials_launch(ctx, (float*)ws, x, n, &parts)) return rc;
+    // one workgroup at least: it stores the scale even for n == 0
+    hipLaunchKernelGGL(quantize_flat, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, q, x, (const float*)ws, parts,
+                       scale, n);
     return check_launch("quantize_flat");
 }
 
@@ -401,17 +476,22 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     int8_t* bt = (int8_t*)(ws + off_b);
     // scale_b is a host value; the kernel reads both scales from device memory
     LANCIUS_REQUIRE(scale_b >= 0.0, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: negative scale");
-    if (int rc = absmax_to_scale(ctx, scales, (float*)(ws + off_part), A, M * K, scale_b)) return rc;
-    // A_q [M][Kp]: row r holds quant(A[r][k]) for k < K, zeros after
-    const bool vec4 = K % 4 == 0 && ((uintptr_t)A & 15u) == 0;
-    const unsigned row_blocks = (unsigned)std::min<size_t>((Kp / (vec4 ? 4 : 1) + kThreads - 1) / kThreads, 64);
-    hipLaunchKernelGGL(quantize_rows_padded, dim3(row_blocks, (unsigned)std::min<size_t>(M, 65535)), dim3(kThreads),
-                       0, ctx->stream, aq, A, (const double*)scales, M, (int)K, (int)Kp, (int)vec4);
+    float* part = (float*)(ws + off_part);
+    int parts = 0;
+    if (int rc = absmax_partials_launch(ctx, part, A, M * K, &parts)) return rc;
+    // A_q [M][Kp]: row r holds quant(A[r][k]) for k < K, zeros after; the
+    // kernel also stores scale_a (and scale_b) for the GEMM epilogue
+    const int vec4 = K % 4 == 0 && ((uintptr_t)A & 15u) == 0;
+    const size_t D = Kp / 4, rows_per = D >= (size_t)kThreads ? 1 : kThreads / D;
+    const unsigned qblocks = (unsigned)std::min<size_t>((M + rows_per - 1) / rows_per, 2048);
+    hipLaunchKernelGGL(quantize_rows_padded, dim3(qblocks), dim3(kThreads), 0, ctx->stream, aq, A, (const float*)part,
+                       parts, scales, scale_b, M, (int)K, (int)Kp, vec4);
     if (int rc = check_launch("quantize_rows_padded")) return rc;
-    const int tiles_k = (int)((Kp + 63) / 64), tiles_n = (int)((N + 63) / 64);
+    const int tiles_k = (int)(Kp / 128), tiles_n = (int)((N + 127) / 128);
     LANCIUS_REQUIRE((size_t)tiles_k * tiles_n < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: B too large");
+    const int bvec = N % 16 == 0 && ((uintptr_t)B & 15u) == 0;
     hipLaunchKernelGGL(transpose_i8, dim3((unsigned)(tiles_k * tiles_n)), dim3(kThreads), 0, ctx->stream, bt, B,
-                       (int)K, (int)N, (int)Kp, tiles_n);
+                       (int)K, (int)N, (int)Kp, tiles_n, bvec);
     if (int rc = check_launch("transpose_i8")) return rc;
     I8Params p{};
     p.C = C;
@@ -462,12 +542,15 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     int8_t* wq = (int8_t*)(ws + off_w);
     int8_t* xq = (int8_t*)(ws + off_x);
     LANCIUS_REQUIRE(scale_w >= 0.0, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: negative scale");
-    if (int rc = absmax_to_scale(ctx, scales, (float*)(ws + off_part), in, N * C_in * H * W, scale_w)) return rc;
+    float* part = (float*)(ws + off_part);
+    int parts = 0;
+    if (int rc = absmax_partials_launch(ctx, part, in, N * C_in * H * W, &parts)) return rc;
     const int HW = (int)(H * W);
     const int tiles_p = (HW + 63) / 64, tiles_c = (int)((Cp + 63) / 64);
     LANCIUS_REQUIRE((size_t)N * tiles_p * tiles_c < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: input too large");
     hipLaunchKernelGGL(quantize_nchw_to_nhwc, dim3((unsigned)(N * tiles_p * tiles_c)), dim3(kThreads), 0, ctx->stream,
-                       xq, in, (const double*)scales, (int)N, (int)C_in, HW, (int)Cp, tiles_p, tiles_c);
+                       xq, in, (const float*)part, parts, scales, scale_w, (int)N, (int)C_in, HW, (int)Cp, tiles_p,
+                       tiles_c);
     if (int rc = check_launch("quantize_nchw_to_nhwc")) return rc;
     // weights re-laid k = (kh, kw, ci) and zero-padded to Kp
     hipLaunchKernelGGL(conv_weights_i8_padded, dim3(grid_for(C_out * Kp)), dim3(kThreads), 0, ctx->stream, wq, w,
