@@ -49,18 +49,29 @@ constexpr int kThreads = 256;
 // TB: B is given transposed, stored [N][K] (element (k,n) at B[n*K + k]).
 // The LDS tiles are the same k-major tiles either way; only the global-load
 // pattern changes (a transposed operand is read along its contiguous axis).
+// KG > 1: the workgroup has KG groups of 4 waves over the same C tile; group
+// g takes k-pairs g, g + KG, g + 2 KG, ... of every k-tile, and at the end
+// groups 1 .. KG-1 pass their accumulators through LDS to group 0, which adds
+// them in group order (fixed, so run-to-run identical) and runs the epilogue.
+// It puts 8 or 16 waves on a CU when the grid has only one workgroup per CU.
 template <int BM, int BN, int BK, int WGM, int WGN, bool VEC, bool SPLIT, int OCC = 1, bool TA = false,
-          bool TB = false>
-__global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams p) {
-    static_assert(WGM * WGN == 4, "4 waves per workgroup");
+          bool TB = false, int KG = 1>
+__global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmParams p) {
+    static_assert(WGM * WGN == 4, "4 waves per k-group");
+    constexpr int NT = kThreads * KG;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
     static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "wave tile is a multiple of 32");
     static_assert(BK % 4 == 0, "BK multiple of 4");
+    constexpr int KPG = BK / 2 / KG;  // k-pairs per group per k-tile
+    static_assert(KPG >= 1 && KPG * KG * 2 == BK, "k-pairs split evenly over the groups");
     constexpr int LDA = BM + 4;  // As[k][m]
     constexpr int LDB = BN + 4;  // Bs[k][n]
-    __shared__ __attribute__((aligned(16))) float As[2][BK][LDA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LDB];
+    constexpr int STAGE = 2 * BK * (LDA + LDB);
+    constexpr int RED = KG > 1 ? 4 * TM * TN * 16 * 64 : 0;  // one group's accumulators
+    __shared__ __attribute__((aligned(16))) float smem[STAGE > RED ? STAGE : RED];
+    float(*As)[BK][LDA] = reinterpret_cast<float(*)[BK][LDA]>(smem);
+    float(*Bs)[BK][LDB] = reinterpret_cast<float(*)[BK][LDB]>(smem + 2 * BK * LDA);
 
     const int g = blockIdx.z;
     const float* __restrict__ A = p.A[g];
@@ -88,16 +99,17 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    const int wm = wave / WGN, wn = wave % WGN;
+    const int kg = KG > 1 ? wave >> 2 : 0, wl = wave & 3;
+    const int wm = wl / WGN, wn = wl % WGN;
     const int lr = lane & 31, lk = lane >> 5;
 
     // ---- global -> register staging -------------------------------------
-    constexpr int A_VEC = VEC ? (BM * BK / 4) / kThreads : 0;
-    constexpr int B_VEC = VEC ? (BK * BN / 4) / kThreads : 0;
-    constexpr int A_SCL = VEC ? 0 : (BM * BK) / kThreads;
-    constexpr int B_SCL = VEC ? 0 : (BK * BN) / kThreads;
-    static_assert(!VEC || (A_VEC * kThreads * 4 == BM * BK && B_VEC * kThreads * 4 == BK * BN), "even split");
-    static_assert(VEC || (A_SCL * kThreads == BM * BK && B_SCL * kThreads == BK * BN), "even split");
+    constexpr int A_VEC = VEC ? (BM * BK / 4) / NT : 0;
+    constexpr int B_VEC = VEC ? (BK * BN / 4) / NT : 0;
+    constexpr int A_SCL = VEC ? 0 : (BM * BK) / NT;
+    constexpr int B_SCL = VEC ? 0 : (BK * BN) / NT;
+    static_assert(!VEC || (A_VEC * NT * 4 == BM * BK && B_VEC * NT * 4 == BK * BN), "even split");
+    static_assert(VEC || (A_SCL * NT == BM * BK && B_SCL * NT == BK * BN), "even split");
     f32x4 a_v[A_VEC > 0 ? A_VEC : 1];
     f32x4 b_v[B_VEC > 0 ? B_VEC : 1];
     float a_s[A_SCL > 0 ? A_SCL : 1];
@@ -109,7 +121,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TA) {
                     const int r = idx / (BK / 4), kq = idx % (BK / 4);
                     const int gm = m0 + r, gk = k0 + 4 * kq;
@@ -124,7 +136,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
             }
 #pragma unroll
             for (int i = 0; i < B_VEC; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TB) {
                     const int kr = idx / (BN / 4), nq = idx % (BN / 4);
                     const int gk = k0 + kr, gn = n0 + 4 * nq;
@@ -140,7 +152,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
         } else {
 #pragma unroll
             for (int i = 0; i < A_SCL; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TA) {
                     const int r = idx / BK, kk = idx % BK;
                     const int gm = m0 + r, gk = k0 + kk;
@@ -153,7 +165,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
             }
 #pragma unroll
             for (int i = 0; i < B_SCL; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TB) {
                     const int kr = idx / BN, n = idx % BN;
                     const int gk = k0 + kr, gn = n0 + n;
@@ -171,7 +183,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TA) {
                     const int r = idx / (BK / 4), kq = idx % (BK / 4);
                     As[buf][4 * kq + 0][r] = a_v[i].x;
@@ -185,7 +197,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
             }
 #pragma unroll
             for (int i = 0; i < B_VEC; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TB) {
                     const int kr = idx / (BN / 4), nq = idx % (BN / 4);
                     *(f32x4*)&Bs[buf][kr][4 * nq] = b_v[i];
@@ -200,7 +212,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
         } else {
 #pragma unroll
             for (int i = 0; i < A_SCL; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TA)
                     As[buf][idx % BK][idx / BK] = a_s[i];
                 else
@@ -208,7 +220,7 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
             }
 #pragma unroll
             for (int i = 0; i < B_SCL; ++i) {
-                const int idx = tid + i * kThreads;
+                const int idx = tid + i * NT;
                 if constexpr (!TB)
                     Bs[buf][idx / BN][idx % BN] = b_s[i];
                 else
@@ -240,19 +252,22 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
         if (more) load_tile((kt + 1) * BK);
         // Fragments of k-pair kp+1 are read from LDS before the MFMAs of kp are
         // issued (register double buffer), so no MFMA waits on its own reads.
+        // group kg: k rows 2 (kg + KG j) + lk, j = 0 .. KPG-1
         float af[2][TM], bf[2][TN];
+        const int kf = 2 * kg + lk;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) af[0][i] = As[cur][lk][wm * WM + i * 32 + lr];
+        for (int i = 0; i < TM; ++i) af[0][i] = As[cur][kf][wm * WM + i * 32 + lr];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bf[0][j] = Bs[cur][lk][wn * WN + j * 32 + lr];
+        for (int j = 0; j < TN; ++j) bf[0][j] = Bs[cur][kf][wn * WN + j * 32 + lr];
 #pragma unroll
-        for (int kp = 0; kp < BK / 2; ++kp) {
+        for (int kp = 0; kp < KPG; ++kp) {
             const int c = kp & 1;
-            if (kp + 1 < BK / 2) {
+            if (kp + 1 < KPG) {
+                const int kr = kf + 2 * KG * (kp + 1);
 #pragma unroll
-                for (int i = 0; i < TM; ++i) af[c ^ 1][i] = As[cur][2 * kp + 2 + lk][wm * WM + i * 32 + lr];
+                for (int i = 0; i < TM; ++i) af[c ^ 1][i] = As[cur][kr][wm * WM + i * 32 + lr];
 #pragma unroll
-                for (int j = 0; j < TN; ++j) bf[c ^ 1][j] = Bs[cur][2 * kp + 2 + lk][wn * WN + j * 32 + lr];
+                for (int j = 0; j < TN; ++j) bf[c ^ 1][j] = Bs[cur][kr][wn * WN + j * 32 + lr];
             }
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -262,6 +277,32 @@ __global__ void __launch_bounds__(kThreads, OCC) gemm_f32_mfma(const GemmParams 
         }
         if (more) store_tile(cur ^ 1);
         __syncthreads();
+    }
+
+    if constexpr (KG > 1) {
+        // groups 1 .. KG-1 hand their sums to group 0 one at a time (the
+        // staging buffers are free after the last barrier of the k loop)
+        for (int s = 1; s < KG; ++s) {
+            if (kg == s) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) smem[(((wl * TM + i) * TN + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+            }
+            __syncthreads();
+            if (kg == 0) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] += smem[(((wl * TM + i) * TN + j) * 16 + r) * 64 + lane];
+            }
+            if (s + 1 < KG) __syncthreads();
+        }
+        if (kg != 0) return;
     }
 
     // ---- epilogue: bias, activation, residual, one store -----------------
@@ -495,24 +536,26 @@ __global__ void __launch_bounds__(256) splitk_reduce(const GemmParams p, int cou
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int OCC = 1, bool TA = false, bool TB = false>
+template <int BM, int BN, int BK, int WGM, int WGN, int OCC = 1, bool TA = false, bool TB = false, int KG = 1>
 int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
+    constexpr int SOCC = KG > 1 ? OCC : 1;  // occupancy hint of the split and scalar variants
     p.tiles_m = (uint32_t)((p.M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((p.N + BN - 1) / BN);
     p.map2d = tune("gemm_map", 0) == 1 && p.tiles_m % 2 == 0 && p.tiles_n % 4 == 0;
     dim3 grid(p.tiles_m * p.tiles_n, (unsigned)p.splits, (unsigned)count);
     const bool split = p.splits > 1;
+    const dim3 block(kThreads * KG);
     if (vec && split)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true, 1, TA, TB>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true, SOCC, TA, TB, KG>), grid, block, 0,
                            ctx->stream, p);
     else if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false, OCC, TA, TB>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false, OCC, TA, TB, KG>), grid, block, 0,
                            ctx->stream, p);
     else if (split)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true, 1, TA, TB>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true, SOCC, TA, TB, KG>), grid, block, 0,
                            ctx->stream, p);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, false, 1, TA, TB>), grid, dim3(kThreads), 0,
+        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, false, SOCC, TA, TB, KG>), grid, block, 0,
                            ctx->stream, p);
     if (int rc = check_launch("gemm_f32_mfma")) return rc;
     if (split) {
@@ -537,6 +580,10 @@ int launch_by_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec, int 
             case 4: return launch_cfg<128, 128, 32, 2, 2>(ctx, p, count, vec);
             case 5: return launch_cfg<128, 256, 16, 2, 2>(ctx, p, count, vec);
             case 6: return launch_cfg<128, 128, 16, 2, 2, 4>(ctx, p, count, vec);
+            case 7: return launch_cfg<128, 128, 32, 2, 2, 2, false, false, 2>(ctx, p, count, vec);
+            case 8: return launch_cfg<128, 128, 32, 2, 2, 1, false, false, 4>(ctx, p, count, vec);
+            case 9: return launch_cfg<64, 64, 64, 2, 2, 1, false, false, 4>(ctx, p, count, vec);
+            case 10: return launch_cfg<64, 64, 32, 2, 2, 2, false, false, 2>(ctx, p, count, vec);
             default: return launch_cfg<128, 128, 16, 2, 2>(ctx, p, count, vec);
         }
     }
@@ -628,20 +675,41 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         }
     }
 
-    // Tile: 128x128 when that alone gives >= 256 workgroups (one per CU),
-    // else 64x64.  Split-K when the 64x64 grid still leaves CUs idle and K is
-    // long enough: enough K ranges for ~512 workgroups, each >= 128 deep.
-    // Configurations (BM x BN / BK): 1 = 128x128/16, 2 = 64x64/16,
-    // 3 = 256x128/16, 4 = 128x128/32, 5 = 128x256/16.
+    // Configurations (BM x BN / BK, k-groups): 1 = 128x128/16, 2 = 64x64/16,
+    // 3 = 256x128/16, 4 = 128x128/32, 5 = 128x256/16, 6 = 128x128/16 built
+    // for 4 workgroups per CU, 7 = 128x128/32 x2, 8 = 128x128/32 x4,
+    // 9 = 64x64/64 x4, 10 = 64x64/32 x2.  Default by the number of 128x128
+    // tiles (one per CU fills the chip once), measured on MI355X:
+    //  * >= 768: 6 (4096^3: 112 TFLOP/s);
+    //  * 384 .. 767: 7 (two 8-wave workgroups per CU);
+    //  * 256 .. 383: 8, 16 waves on the CU's one tile (2048^3: 205 -> 190
+    //    us; 4096x1024x1024: 110 -> 103 us);
+    //  * fewer, K >= 2048: 7 with split-K (1024x4096x1024: 137 -> 103 us);
+    //  * fewer, shorter K: 9 (1024^3: 38.9 -> 34.0 us), or 2 for small
+    //    grids and transposed operands.
+    // Split-K when the grid still leaves CUs idle and K is long enough:
+    // enough K ranges for ~512 workgroups, each >= 128 deep.
     const size_t big_tiles = count * ((M + 127) / 128) * ((N + 127) / 128);
-    // Default: 6 (128x128/16 built for 4 workgroups per CU, 112 VGPRs) when
-    // that gives >= 256 workgroups, else 64x64.  Measured on MI355X: 115
-    // TFLOP/s at 4096^3 (84% of the measured 137 TFLOP/s fp32 MFMA ceiling).
+    const size_t t64 = count * ((M + 63) / 64) * ((N + 63) / 64);
+    const bool plain = !ta && !tb;
     int cfg = tune("gemm_tile", 0);
-    if (cfg < 1 || cfg > 6 || ((ta || tb) && cfg != 2 && cfg != 6)) cfg = big_tiles >= 256 ? 6 : 2;
-    const size_t bm = cfg == 2 ? 64 : cfg == 3 ? 256 : 128;
-    const size_t bn = cfg == 2 ? 64 : cfg == 5 ? 256 : 128;
-    const size_t bk = cfg == 4 ? 32 : kBK;
+    if (cfg < 1 || cfg > 10 || ((ta || tb) && cfg != 2 && cfg != 6)) {
+        if (big_tiles >= 768)
+            cfg = 6;
+        else if (big_tiles >= 384)
+            cfg = plain ? 7 : 6;
+        else if (big_tiles >= 256)
+            cfg = plain ? 8 : 6;
+        else if (plain && K >= 2048 && big_tiles >= 16)
+            cfg = 7;
+        else if (plain && t64 >= 64)
+            cfg = 9;
+        else
+            cfg = 2;
+    }
+    const size_t bm = cfg == 2 || cfg >= 9 ? 64 : cfg == 3 ? 256 : 128;
+    const size_t bn = cfg == 2 || cfg >= 9 ? 64 : cfg == 5 ? 256 : 128;
+    const size_t bk = cfg == 9 ? 64 : cfg == 4 || cfg == 7 || cfg == 8 || cfg == 10 ? 32 : kBK;
     const size_t tiles = count * ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const size_t ktiles = (K + bk - 1) / bk;
     size_t splits = (size_t)tune("gemm_split", 0);
