@@ -117,6 +117,13 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
 
     // A tile (rows m0.., k0..): along k from A[M][K], along m from A^T[K][M].
     // B tile (k0.., cols n0..): along n from B[K][N], along k from B^T[N][K].
+    // Branch-free: every load reads a clamped, in-bounds address, so one
+    // k-tile is one basic block and a load past the last k-tile is harmless.
+    // Rows of A past M and columns of B past N then hold copies of the last
+    // row / column; they only reach rows and columns of C that are never
+    // stored.  Elements past K must be zero: store_tile clears them in the
+    // one k-tile that crosses K (a uniform branch), so no select waits on a
+    // load in the other tiles.
     auto load_tile = [&](int k0) {
         if constexpr (VEC) {
 #pragma unroll
@@ -125,13 +132,11 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
                 if constexpr (!TA) {
                     const int r = idx / (BK / 4), kq = idx % (BK / 4);
                     const int gm = m0 + r, gk = k0 + 4 * kq;
-                    a_v[i] = (gm < M && gk < K) ? *(const f32x4*)(A + (size_t)gm * K + gk)
-                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                    a_v[i] = *(const f32x4*)(A + (size_t)min(gm, M - 1) * K + min(gk, K - 4));
                 } else {
                     const int kr = idx / (BM / 4), mq = idx % (BM / 4);
                     const int gk = k0 + kr, gm = m0 + 4 * mq;
-                    a_v[i] = (gk < K && gm < M) ? *(const f32x4*)(A + (size_t)gk * M + gm)
-                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                    a_v[i] = *(const f32x4*)(A + (size_t)min(gk, K - 1) * M + min(gm, M - 4));
                 }
             }
 #pragma unroll
@@ -140,13 +145,11 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
                 if constexpr (!TB) {
                     const int kr = idx / (BN / 4), nq = idx % (BN / 4);
                     const int gk = k0 + kr, gn = n0 + 4 * nq;
-                    b_v[i] = (gk < K && gn < N) ? *(const f32x4*)(B + (size_t)gk * N + gn)
-                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                    b_v[i] = *(const f32x4*)(B + (size_t)min(gk, K - 1) * N + min(gn, N - 4));
                 } else {
                     const int c = idx / (BK / 4), kq = idx % (BK / 4);
                     const int gn = n0 + c, gk = k0 + 4 * kq;
-                    b_v[i] = (gn < N && gk < K) ? *(const f32x4*)(B + (size_t)gn * K + gk)
-                                                : f32x4{0.f, 0.f, 0.f, 0.f};
+                    b_v[i] = *(const f32x4*)(B + (size_t)min(gn, N - 1) * K + min(gk, K - 4));
                 }
             }
         } else {
@@ -156,11 +159,11 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
                 if constexpr (!TA) {
                     const int r = idx / BK, kk = idx % BK;
                     const int gm = m0 + r, gk = k0 + kk;
-                    a_s[i] = (gm < M && gk < K) ? A[(size_t)gm * K + gk] : 0.0f;
+                    a_s[i] = A[(size_t)min(gm, M - 1) * K + min(gk, K - 1)];
                 } else {
                     const int kr = idx / BM, r = idx % BM;
                     const int gk = k0 + kr, gm = m0 + r;
-                    a_s[i] = (gk < K && gm < M) ? A[(size_t)gk * M + gm] : 0.0f;
+                    a_s[i] = A[(size_t)min(gk, K - 1) * M + min(gm, M - 1)];
                 }
             }
 #pragma unroll
@@ -169,17 +172,46 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
                 if constexpr (!TB) {
                     const int kr = idx / BN, n = idx % BN;
                     const int gk = k0 + kr, gn = n0 + n;
-                    b_s[i] = (gk < K && gn < N) ? B[(size_t)gk * N + gn] : 0.0f;
+                    b_s[i] = B[(size_t)min(gk, K - 1) * N + min(gn, N - 1)];
                 } else {
                     const int c = idx / BK, kk = idx % BK;
                     const int gn = n0 + c, gk = k0 + kk;
-                    b_s[i] = (gn < N && gk < K) ? B[(size_t)gn * K + gk] : 0.0f;
+                    b_s[i] = B[(size_t)min(gn, N - 1) * K + min(gk, K - 1)];
                 }
             }
         }
     };
 
-    auto store_tile = [&](int buf) {
+    auto clear_past_k = [&](int k0) {
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < A_VEC; ++i) {
+            const int idx = tid + i * NT;
+            const int gk = !TA ? k0 + 4 * (idx % (BK / 4)) : k0 + idx / (BM / 4);
+            if (gk >= K) a_v[i] = z4;
+        }
+#pragma unroll
+        for (int i = 0; i < B_VEC; ++i) {
+            const int idx = tid + i * NT;
+            const int gk = !TB ? k0 + idx / (BN / 4) : k0 + 4 * (idx % (BK / 4));
+            if (gk >= K) b_v[i] = z4;
+        }
+#pragma unroll
+        for (int i = 0; i < A_SCL; ++i) {
+            const int idx = tid + i * NT;
+            const int gk = !TA ? k0 + idx % BK : k0 + idx / BM;
+            if (gk >= K) a_s[i] = 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < B_SCL; ++i) {
+            const int idx = tid + i * NT;
+            const int gk = !TB ? k0 + idx / BN : k0 + idx % BK;
+            if (gk >= K) b_s[i] = 0.0f;
+        }
+    };
+
+    auto store_tile = [&](int buf, int k0) {
+        if (k0 + BK > K) clear_past_k(k0);
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
@@ -243,15 +275,18 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
         kt1 = min(kt1, kt0 + p.kchunk / BK);
     }
     load_tile(kt0 * BK);
-    store_tile(0);
+    store_tile(0, kt0 * BK);
     __syncthreads();
 
     for (int kt = kt0; kt < kt1; ++kt) {
         const int cur = (kt - kt0) & 1;
-        const bool more = kt + 1 < kt1;
-        if (more) load_tile((kt + 1) * BK);
-        // Fragments of k-pair kp+1 are read from LDS before the MFMAs of kp are
-        // issued (register double buffer), so no MFMA waits on its own reads.
+        load_tile((kt + 1) * BK);  // past the end on the last tile: clamped, unused
+        // keep the global loads first: they have the whole k-tile to land
+        __builtin_amdgcn_sched_barrier(0);
+        // Fragments of k-pair kp+1 are read from LDS before the MFMAs of kp in
+        // program order (the compiler may sink the reads after them; the
+        // other waves on the SIMD cover that latency - pinning the order
+        // measured no faster).
         // group kg: k rows 2 (kg + KG j) + lk, j = 0 .. KPG-1
         float af[2][TM], bf[2][TN];
         const int kf = 2 * kg + lk;
@@ -275,7 +310,7 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[c][i], bf[c][j], acc[i][j], 0, 0, 0);
         }
-        if (more) store_tile(cur ^ 1);
+        store_tile(cur ^ 1, (kt + 1) * BK);  // the other buffer: nobody reads it before the barrier
         __syncthreads();
     }
 
@@ -707,8 +742,9 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         else
             cfg = 2;
     }
-    const size_t bm = cfg == 2 || cfg >= 9 ? 64 : cfg == 3 ? 256 : 128;
-    const size_t bn = cfg == 2 || cfg >= 9 ? 64 : cfg == 5 ? 256 : 128;
+    const bool small = cfg == 2 || cfg == 9 || cfg == 10;
+    const size_t bm = small ? 64 : cfg == 3 ? 256 : 128;
+    const size_t bn = small ? 64 : cfg == 5 ? 256 : 128;
     const size_t bk = cfg == 9 ? 64 : cfg == 4 || cfg == 7 || cfg == 8 || cfg == 10 ? 32 : kBK;
     const size_t tiles = count * ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const size_t ktiles = (K + bk - 1) / bk;
