@@ -75,6 +75,23 @@ def test_gemm_config_sampled_rows(dev, n):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(n)
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (2048, 1000, 2048),  # 256 tiles of 128^2: 4 k-groups, K crosses a 32-deep k-tile
+    (2048, 72, 3072),    # 384 tiles: 2 k-groups
+    (2000, 40, 2990),    # 384 tiles, N % 4 != 0: scalar loads
+    (520, 2100, 500),    # 20 tiles, K >= 2048: 2 k-groups with split K, ragged edges
+    (600, 300, 700),     # 64x64 tiles with 4 k-groups, ragged edges
+    (601, 301, 703),     # same, K % 4 != 0: scalar loads
+])
+def test_gemm_tile_paths(dev, M, K, N):
+    """Each default tile path of the GEMM dispatch (k-groups reduce their
+    accumulators through LDS before the epilogue), with bias, GELU and a
+    residual; 96 sampled rows for the two largest products."""
+    rows = (M - 96, M) if M * N >= 4_000_000 else None
+    got, ref = _gemm_case(dev, M, K, N, seed=120 + M + N, bias=True, act=ACT_GELU, residual=True, rows=rows)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
 @pytest.mark.parametrize("M,K,N,act", [(100, 2000, 120, ACT_NONE), (33, 1500, 64, ACT_GELU),
                                        (16, 4096, 260, ACT_RELU), (5, 777, 9, ACT_NONE),
                                        (24, 1024, 200, ACT_GELU), (8, 200, 64, ACT_RELU), (32, 2052, 4100, ACT_NONE),
