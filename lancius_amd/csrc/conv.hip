@@ -319,9 +319,11 @@ struct WgradParams {
     uint32_t tiles_m, tiles_n;
 };
 
-template <int BM, int BN>
+// BK pixels per k-tile: lanes run along BK consecutive pixels of a row, so
+// BK = 64 makes each load instruction one 256-byte run per row.
+template <int BM, int BN, int BK>
 __global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
-    constexpr int BK = 16, WGM = 2, WGN = 2;
+    constexpr int WGM = 2, WGN = 2;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int LDA = BM + 4, LDB = BN + 4;
@@ -342,15 +344,16 @@ __global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
 
     // Loader mapping: lanes along the pixel index (contiguous in memory).
     const int kk = tid % BK;
-    const int row0 = tid / BK;                      // 0..15
-    constexpr int A_PER = BM / (256 / BK);          // channels per thread
-    constexpr int B_PER = BN / (256 / BK);          // j per thread
+    const int row0 = tid / BK;                      // 0 .. 256/BK - 1
+    constexpr int RSTEP = 256 / BK;                 // rows covered per pass
+    constexpr int A_PER = BM / RSTEP;               // channels per thread
+    constexpr int B_PER = BN / RSTEP;               // j per thread
     const int HWo = p.Ho * p.Wo, KHW = p.KH * p.KW;
     // The (ci, kh, kw) of each j this thread loads never changes.
     int b_off[B_PER], b_dh[B_PER], b_dw[B_PER];
 #pragma unroll
     for (int i = 0; i < B_PER; ++i) {
-        const int j = j0 + row0 + 16 * i;
+        const int j = j0 + row0 + RSTEP * i;
         if (j < p.J) {
             const int ci = j / KHW, t = j - (j / KHW) * KHW;
             const int kh = t / p.KW, kw = t - (t / p.KW) * p.KW;
@@ -376,7 +379,7 @@ __global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
         const float* g = p.dy + ((size_t)n * p.C_out) * HWo + (size_t)ho * p.Wo + wo;
 #pragma unroll
         for (int i = 0; i < A_PER; ++i) {
-            const int co = m0 + row0 + 16 * i;
+            const int co = m0 + row0 + RSTEP * i;
             a_s[i] = (valid && co < p.C_out) ? g[(size_t)co * HWo] : 0.0f;
         }
         const float* xi = p.x + (size_t)n * p.C_in * p.H * p.W;
@@ -391,9 +394,9 @@ __global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < A_PER; ++i) As[buf][kk][row0 + 16 * i] = a_s[i];
+        for (int i = 0; i < A_PER; ++i) As[buf][kk][row0 + RSTEP * i] = a_s[i];
 #pragma unroll
-        for (int i = 0; i < B_PER; ++i) Bs[buf][kk][row0 + 16 * i] = b_s[i];
+        for (int i = 0; i < B_PER; ++i) Bs[buf][kk][row0 + RSTEP * i] = b_s[i];
     };
 
     f32x16 acc[TM][TN];
@@ -491,6 +494,8 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
     return check_launch("conv2d_implicit_gemm");
 }
 
+int default_tile(size_t C_out) { return C_out > 64 ? 1 : C_out > 32 ? 2 : 3; }
+
 template <int KH_T, int KW_T>
 int launch_tile(lancius_hip_ctx* ctx, ConvParams& p, int tile) {
     switch (tile) {
@@ -539,10 +544,12 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     p.Kdim = (int)(C_in * K_h * K_w);
     p.Ptotal = (long long)N * p.Ho * p.Wo;
     p.act = act;
-    // Tiles (C_out x pixels): 0 = 128x128, 1 = 128x64, 2 = 64x64, 3 = 32x128.
+    // Tiles (C_out x pixels): 0 = 128x128, 1 = 128x64, 2 = 64x64, 3 = 32x128,
+    // the one whose channel extent covers C_out with the least padding.
     // 128x64 measured best on the N32 64->128 56x56 config (78.6 TFLOP/s vs
-    // 72.3 for 128x128): twice the workgroups, a shorter tail.
-    const int tile = tune("conv_tile", C_out > 64 ? 1 : 3);
+    // 72.3 for 128x128): twice the workgroups, a shorter tail; 64x64 for its
+    // dgrad (64 output channels: 238 -> 204 us against 32x128).
+    const int tile = tune("conv_tile", default_tile(C_out));
     const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
     return rc ? rc : ok();
 }
@@ -600,7 +607,7 @@ extern "C" int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx,
         p.wt = (const float*)ws;
     else
         p.w = (const float*)ws;
-    const int tile = tune("conv_tile", p.C_out > 64 ? 1 : 3);
+    const int tile = tune("conv_tile", default_tile((size_t)p.C_out));
     const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
     return rc ? rc : ok();
 }
@@ -642,21 +649,33 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     const size_t tiles = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(tiles < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: too many tiles");
     // Split the pixel reduction for ~1024 workgroups, each >= 256 pixels deep.
-    const long long ktiles = (p.Ptotal + 15) / 16;
+    // k-tiles of 32 pixels: 296 -> 264 us at the N32 64->128 56x56 config
+    // (16: 64-byte runs per load; 64: 70 KB of LDS, fewer workgroups per CU,
+    // 360 us).
+    int bk = tune("conv_wgrad_bk", 32);
+    if (bk != 16 && bk != 64) bk = 32;
+    const long long ktiles = (p.Ptotal + bk - 1) / bk;
     long long splits = tune("conv_wgrad_split", 0);
-    if (splits <= 0) splits = std::max<long long>(1, std::min<long long>((1024 + tiles - 1) / tiles, ktiles / 16));
+    if (splits <= 0) splits = std::max<long long>(1, std::min<long long>((1024 + tiles - 1) / tiles, ktiles * bk / 256));
     splits = std::max<long long>(1, std::min<long long>({splits, std::max<long long>(ktiles, 1), 65535}));
     while (splits > 1 && (size_t)splits * C_out * J * sizeof(float) > ((size_t)1 << 28)) splits = (splits + 1) / 2;
     const long long chunk_tiles = (std::max<long long>(ktiles, 1) + splits - 1) / splits;
-    p.pchunk = chunk_tiles * 16;
+    p.pchunk = chunk_tiles * bk;
     p.splits = (int)((std::max<long long>(ktiles, 1) + chunk_tiles - 1) / chunk_tiles);
     if (p.splits > 1) {
         void* ws = nullptr;
         if (int rc = workspace(ctx, (size_t)p.splits * C_out * J * sizeof(float), &ws)) return rc;
         p.ws = (float*)ws;
     }
-    hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
-                       ctx->stream, p);
+    if (bk == 64)
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN, 64>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
+                           ctx->stream, p);
+    else if (bk == 32)
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN, 32>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
+                           ctx->stream, p);
+    else
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN, 16>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
+                           ctx->stream, p);
     if (int rc = check_launch("conv2d_wgrad_mfma")) return rc;
     if (p.splits > 1) {
         const size_t n = C_out * J;
