@@ -9,7 +9,10 @@ namespace {
 constexpr int kChains = 8;  // independent accumulators per wave
 
 // Every wave issues `iters` rounds of kChains independent
-// v_mfma_f32_32x32x2_f32; the operands change each round so nothing folds.
+// v_mfma_f32_32x32x2_f32.  The accumulators carry from round to round, so
+// nothing folds; the A/B operands stay fixed, so no VALU instruction sits
+// between the MFMAs (changing them every round - a VALU write of an MFMA
+// source each round - measured 135 TFLOP/s against 144-154 without).
 __global__ void __launch_bounds__(256) mfma_rate(float* out, int iters) {
     f32x16 acc[kChains];
 #pragma unroll
@@ -20,8 +23,6 @@ __global__ void __launch_bounds__(256) mfma_rate(float* out, int iters) {
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
         for (int c = 0; c < kChains; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[c], 0, 0, 0);
-        a += 1e-9f;
-        b -= 1e-9f;
     }
     float s = 0.0f;
 #pragma unroll
@@ -66,12 +67,18 @@ extern "C" int lancius_hip_peak_probe(lancius_hip_ctx* ctx, int which, double* r
         float* out = nullptr;
         hipError_t e = hipMalloc(&out, (size_t)blocks * 256 * sizeof(float));
         if (e == hipSuccess) {
-            hipLaunchKernelGGL(mfma_rate, dim3(blocks), dim3(256), 0, ctx->stream, out, 64);  // warm-up
-            (void)hipEventRecord(e0, ctx->stream);
+            // The clock settles over the first milliseconds of MFMA load: one
+            // untimed launch, then the fastest of three timed ones.
             hipLaunchKernelGGL(mfma_rate, dim3(blocks), dim3(256), 0, ctx->stream, out, iters);
-            (void)hipEventRecord(e1, ctx->stream);
-            e = hipEventSynchronize(e1);
-            if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+            for (int rep = 0; rep < 3 && e == hipSuccess; ++rep) {
+                float t = 0.0f;
+                (void)hipEventRecord(e0, ctx->stream);
+                hipLaunchKernelGGL(mfma_rate, dim3(blocks), dim3(256), 0, ctx->stream, out, iters);
+                (void)hipEventRecord(e1, ctx->stream);
+                e = hipEventSynchronize(e1);
+                if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+                if (e == hipSuccess && (rep == 0 || t < ms)) ms = t;
+            }
             (void)hipFree(out);
         }
         if (e != hipSuccess) rc = from_hip(e, "mfma probe");
