@@ -516,7 +516,10 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # The GPU clock settles over the first ~50 ms of MFMA load (4096^3 launches
+    # shorten from 1.27 to 1.10 ms); 50 untimed launches put the timed ones
+    # in the steady state.
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--quick", action="store_true", help="headline only (no other configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
