@@ -44,6 +44,7 @@ extern "C" {
 #define LANCIUS_HIP_ACT_NONE 0
 #define LANCIUS_HIP_ACT_RELU 1   /* max(x, 0): lancius_scheduler.c:305-308       */
 #define LANCIUS_HIP_ACT_GELU 2   /* tanh GELU with +-100 clamp: lancius_kernels.c:238-246 */
+#define LANCIUS_HIP_ACT_TANH 3   /* tanh(x): BASIS_OP_TANH (include/basis/stage6_ir/graph.h:12) */
 
 typedef struct lancius_hip_ctx lancius_hip_ctx;
 
@@ -72,10 +73,11 @@ LANCIUS_HIP_EXPORT int lancius_hip_timer_stop(lancius_hip_ctx* ctx, float* elaps
 /* ---- kernels (device pointers, fp32, row-major) --------------------- */
 
 /* C[M,N] = epilogue(A[M,K] . B[K,N]).
- * Epilogue order: y = acc + bias[n] (bias may be NULL); y = act(y);
- * y = y + residual[m,n] (residual may be NULL; it may alias C).
- * Replaces the MATMUL branch (lancius_scheduler.c:222-234) plus the
- * BROADCAST/ADD/RELU/GELU nodes that follow it in a graph. */
+ * Epilogue order: y = acc + bias[n] (bias may be NULL); y = act(y) with act
+ * any LANCIUS_HIP_ACT_*; y = y + residual[m,n] (residual may be NULL; it
+ * may alias C).  Replaces the MATMUL branch (lancius_scheduler.c:222-234)
+ * plus the BROADCAST/ADD/RELU/GELU nodes that follow it in a graph (and the
+ * BASIS graph's BROADCAST_ADD/RELU/TANH/ADD, include/lancius_basis.h). */
 LANCIUS_HIP_EXPORT int lancius_hip_gemm_f32(lancius_hip_ctx* ctx, float* C, const float* A, const float* B,
                                             size_t M, size_t K, size_t N,
                                             const float* bias, int act, const float* residual);
@@ -150,6 +152,12 @@ LANCIUS_HIP_EXPORT int lancius_hip_softmax_f32(lancius_hip_ctx* ctx, float* prob
 LANCIUS_HIP_EXPORT int lancius_hip_add_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n);
 LANCIUS_HIP_EXPORT int lancius_hip_relu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n);
 LANCIUS_HIP_EXPORT int lancius_hip_gelu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n);
+/* out = tanh(a) over n elements (BASIS_OP_TANH). */
+LANCIUS_HIP_EXPORT int lancius_hip_tanh_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n);
+/* out[r,c] = act(a[r,c] + bias[c]) for a rows x cols matrix: BASIS_OP_BROADCAST_ADD
+ * with the activation of a following RELU / TANH (act: LANCIUS_HIP_ACT_*). */
+LANCIUS_HIP_EXPORT int lancius_hip_bias_act_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* bias,
+                                                size_t rows, size_t cols, int act);
 /* out[r,c] = row[c] for r < rows (row has `cols` values); with cols_in == 1
  * every element is row[0] (the scalar branch, lancius_scheduler.c:271-273). */
 LANCIUS_HIP_EXPORT int lancius_hip_broadcast_f32(lancius_hip_ctx* ctx, float* out, const float* row,

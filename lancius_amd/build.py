@@ -8,10 +8,9 @@ Products (next to this file):
                        names (a drop-in for the reference host library on the
                        graph path).
 
-Test infrastructure (never loaded by the product):
-  oracle/liboracle.so           fp64 CPU restatement of the reference path.
-  oracle/_ref/liblancius_ref.so the reference's own C sources compiled from
-                                /root/reference when that tree is present.
+The test infrastructure (oracle/liboracle.so and, from /root/reference,
+oracle/_ref/*) has its own recipe, oracle/Makefile; __graft_entry__.build()
+runs both.
 
 Usage: python -m lancius_amd.build  (or __graft_entry__.build()).
 """
@@ -29,16 +28,16 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 BUILD = PKG / "_build"
-ORACLE = ROOT / "oracle"
 
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["capi.hip", "gemm.hip", "attention.hip", "conv.hip", "rowops.hip", "reduce.hip", "pool.hip",
-               "int8.hip", "io.hip", "chain.hip", "probe.hip"]
-HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c", "host/graph_autodiff.c", "host/graph_io.c"]
-DEVICE_C_SOURCES = ["host/device_exec.c"]
+               "int8.hip", "io.hip", "chain.hip", "probe.hip", "basis.hip"]
+HOST_C_SOURCES = ["host/graph_ir.c", "host/graph_plan.c", "host/graph_autodiff.c", "host/graph_io.c",
+                  "host/basis_graph.c"]
+DEVICE_C_SOURCES = ["host/device_exec.c", "host/basis_exec.c"]
 
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -55,26 +54,6 @@ HIP_FLAGS = [
     f"-I{CSRC}",
 ]
 C_FLAGS = ["-O2", "-std=gnu11", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter", f"-I{INCLUDE}"]
-
-# Reference sources on the hot path (B/ = bleeding/v11A1/), compiled with the
-# reference's own flags (B/makefile:2) into oracle/_ref for fixtures and the
-# CPU baseline.
-REF_ROOT = Path("/root/reference/bleeding/v11A1")
-REF_SOURCES = [
-    "src/core/lancius_arena.c",
-    "src/core/lancius_error.c",
-    "src/ir/lancius_ir.c",
-    "src/math/lancius_kernels.c",
-    "src/math/lancius_autodiff.c",
-    "src/runtime/lancius_scheduler.c",
-    "src/runtime/lancius_memory_planner.c",
-    "src/runtime/lancius_vision_ops.c",
-    "src/runtime/lancius_threadpool.c",
-    "src/compiler/lancius_optimizer.c",
-    "src/compiler/lancius_quantize.c",
-    "src/core/lancius_serialize.c",
-]
-
 
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
@@ -124,45 +103,15 @@ def build_graph() -> Path:
     return out
 
 
-def build_oracle() -> Path:
-    out = ORACLE / "liboracle.so"
-    tmp = out.with_suffix(".so.tmp")
-    _run(["gcc", "-O3", "-mavx2", "-mfma", "-fopenmp", "-fPIC", "-shared", "-std=gnu11", f"-I{INCLUDE}",
-          "-o", str(tmp), str(ORACLE / "lancius_oracle.c"), "-lm"])
-    os.replace(tmp, out)
-    return out
-
-
-def build_ref() -> Path | None:
-    """Compile the reference's hot-path C sources where they lie (test oracle)."""
-    if not REF_ROOT.is_dir():
-        return None
-    out_dir = ORACLE / "_ref"
-    out_dir.mkdir(exist_ok=True)
-    out = out_dir / "liblancius_ref.so"
-    tmp = out.with_suffix(".so.tmp")
-    _run(["gcc", "-O3", "-mavx2", "-mfma", "-fopenmp", "-fPIC", "-shared", f"-I{REF_ROOT / 'include'}",
-          "-o", str(tmp), *[str(REF_ROOT / s) for s in REF_SOURCES], "-lm", "-lpthread"])
-    os.replace(tmp, out)
-    return out
-
-
 def build_all(verbose: bool = True) -> dict[str, Path | None]:
     if shutil.which("gcc") is None:
         raise RuntimeError("gcc not found")
     if not Path(HIPCC).exists():
         raise RuntimeError(f"hipcc not found at {HIPCC}")
-    with cf.ThreadPoolExecutor(max_workers=4) as ex:
+    with cf.ThreadPoolExecutor(max_workers=2) as ex:
         f_hip = ex.submit(build_hip)
         f_graph = ex.submit(build_graph)
-        f_oracle = ex.submit(build_oracle)
-        f_ref = ex.submit(build_ref)
-        res = {
-            "liblancius_hip": f_hip.result(),
-            "liblancius_graph": f_graph.result(),
-            "liboracle": f_oracle.result(),
-            "liblancius_ref": f_ref.result(),
-        }
+        res = {"liblancius_hip": f_hip.result(), "liblancius_graph": f_graph.result()}
     if verbose:
         for k, v in res.items():
             print(f"[build] {k}: {v}")

@@ -189,7 +189,7 @@ extern "C" int lancius_hip_mlp2_f32(lancius_hip_ctx* ctx, float* out, int32_t* a
                         M * N1 <= (size_t)kMaxH && N1 * N2 <= (size_t)kMaxW2 && K1 < (1u << 30),
                     LANCIUS_HIP_ERR_SHAPE, "mlp2: M=%zu K1=%zu N1=%zu N2=%zu outside the fused chain's limits", M, K1,
                     N1, N2);
-    LANCIUS_REQUIRE(act1 >= LANCIUS_HIP_ACT_NONE && act1 <= LANCIUS_HIP_ACT_GELU, LANCIUS_HIP_ERR_UNSUPPORTED,
+    LANCIUS_REQUIRE(act1 >= LANCIUS_HIP_ACT_NONE && act1 <= LANCIUS_HIP_ACT_TANH, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "mlp2: activation %d", act1);
     if (int rc = bind_device(ctx)) return rc;
     ChainParams p{};

@@ -655,7 +655,7 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     LANCIUS_REQUIRE(M > 0 && N > 0 && K > 0, LANCIUS_HIP_ERR_SHAPE, "gemm: empty shape M=%zu K=%zu N=%zu", M, K, N);
     LANCIUS_REQUIRE(M < (1u << 30) && N < (1u << 30) && K < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
                     "gemm: dimension too large");
-    LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_GELU, LANCIUS_HIP_ERR_UNSUPPORTED,
+    LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_TANH, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "gemm: activation %d", act);
     if (int rc = bind_device(ctx)) return rc;
     ta = ta != 0;

@@ -459,7 +459,7 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm_i8: NULL argument");
     LANCIUS_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1u << 30) && N < (1u << 30) && K < (1u << 30),
                     LANCIUS_HIP_ERR_SHAPE, "gemm_i8: shape M=%zu K=%zu N=%zu", M, K, N);
-    LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_GELU, LANCIUS_HIP_ERR_UNSUPPORTED,
+    LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_TANH, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "gemm_i8: activation %d", act);
     if (int rc = bind_device(ctx)) return rc;
     constexpr int BM = 128, BN = 128, BK = 128;

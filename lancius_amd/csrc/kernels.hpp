@@ -36,7 +36,7 @@ __device__ __forceinline__ void grouped_tile(uint32_t id, uint32_t tiles_m, uint
 }
 
 // Activation codes match LANCIUS_HIP_ACT_* in lancius_hip.h.
-enum : int { kActNone = 0, kActRelu = 1, kActGelu = 2 };
+enum : int { kActNone = 0, kActRelu = 1, kActGelu = 2, kActTanh = 3 };
 
 // max(x, 0) written as the reference's comparison (NaN maps to 0):
 // bleeding/v11A1/src/runtime/lancius_scheduler.c:307.
@@ -55,6 +55,7 @@ __device__ __forceinline__ float gelu_ref(float x) {
 __device__ __forceinline__ float apply_act(float x, int act) {
     if (act == kActRelu) return relu_ref(x);
     if (act == kActGelu) return gelu_ref(x);
+    if (act == kActTanh) return tanhf(x);
     return x;
 }
 

@@ -417,7 +417,7 @@ __global__ void __launch_bounds__(256) rope_kernel(float* __restrict__ out, cons
 
 // ---- elementwise --------------------------------------------------------
 
-enum EwOp : int { kAdd = 0, kRelu = 1, kGelu = 2, kCopy = 3, kSub = 4, kMul = 5, kReluBwd = 6 };
+enum EwOp : int { kAdd = 0, kRelu = 1, kGelu = 2, kCopy = 3, kSub = 4, kMul = 5, kReluBwd = 6, kTanh = 7 };
 
 constexpr bool binary_op(int op) { return op == kAdd || op == kSub || op == kMul || op == kReluBwd; }
 
@@ -431,6 +431,7 @@ __device__ __forceinline__ float ew(float a, float b) {
     if constexpr (OP == kReluBwd) return b > 0.0f ? a : 0.0f;
     if constexpr (OP == kRelu) return relu_ref(a);
     if constexpr (OP == kGelu) return gelu_ref(a);
+    if constexpr (OP == kTanh) return tanhf(a);
     return a;
 }
 
@@ -464,6 +465,30 @@ __global__ void __launch_bounds__(256) broadcast_rows(float* __restrict__ out, c
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
         out[i] = cols_in == 1 ? row[0] : row[i % cols];
+}
+
+// out[r][c] = act(a[r][c] + bias[c]); float4 along the row when cols % 4 == 0
+// and the pointers are 16-byte aligned (vec).
+__global__ void __launch_bounds__(256) bias_act_rows(float* __restrict__ out, const float* __restrict__ a,
+                                                     const float* __restrict__ bias, size_t rows, size_t cols,
+                                                     int act, int vec) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    if (vec) {
+        const size_t c4 = cols / 4, n4 = rows * c4;
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+            const f32x4 x = ((const f32x4*)a)[i], b = ((const f32x4*)bias)[i % c4];
+            f32x4 o;
+            o.x = apply_act(x.x + b.x, act);
+            o.y = apply_act(x.y + b.y, act);
+            o.z = apply_act(x.z + b.z, act);
+            o.w = apply_act(x.w + b.w, act);
+            ((f32x4*)out)[i] = o;
+        }
+        return;
+    }
+    const size_t n = rows * cols;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = apply_act(a[i] + bias[i % cols], act);
 }
 
 __global__ void __launch_bounds__(256) fill_kernel(float* __restrict__ out, float value, size_t n) {
@@ -557,6 +582,25 @@ int lancius_hip_softmax_f32(lancius_hip_ctx* ctx, float* probs, int32_t* argmax,
 
 int lancius_hip_add_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* b, size_t n) {
     return run_elementwise<kAdd>(ctx, out, a, b, n, "add");
+}
+
+int lancius_hip_tanh_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n) {
+    return run_elementwise<kTanh>(ctx, out, a, nullptr, n, "tanh");
+}
+
+int lancius_hip_bias_act_f32(lancius_hip_ctx* ctx, float* out, const float* a, const float* bias, size_t rows,
+                             size_t cols, int act) {
+    LANCIUS_REQUIRE(ctx && out && a && bias, LANCIUS_HIP_ERR_NULL_PTR, "bias_act: NULL argument");
+    LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_TANH, LANCIUS_HIP_ERR_UNSUPPORTED,
+                    "bias_act: activation %d", act);
+    LANCIUS_REQUIRE(cols == 0 || rows <= ((size_t)1 << 40) / cols, LANCIUS_HIP_ERR_SHAPE, "bias_act: %zu x %zu",
+                    rows, cols);
+    if (rows == 0 || cols == 0) return ok();
+    if (int rc = bind_device(ctx)) return rc;
+    const int vec = cols % 4 == 0 && aligned16(out) && aligned16(a) && aligned16(bias);
+    hipLaunchKernelGGL(bias_act_rows, dim3(ew_grid(rows * cols / (vec ? 4 : 1))), dim3(256), 0, ctx->stream, out, a,
+                       bias, rows, cols, act, vec);
+    return check_launch("bias_act");
 }
 
 int lancius_hip_relu_f32(lancius_hip_ctx* ctx, float* out, const float* a, size_t n) {

@@ -17,7 +17,7 @@ PKG = Path(__file__).resolve().parent
 HIP_LIB = PKG / "liblancius_hip.so"
 GRAPH_LIB = PKG / "liblancius_graph.so"
 
-ACT_NONE, ACT_RELU, ACT_GELU = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_GELU, ACT_TANH = 0, 1, 2, 3
 MAX_GROUP = 16
 
 # LANCIUS_DEVICE_* flags (include/lancius_hip_graph.h)
@@ -78,6 +78,8 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_softmax_f32.argtypes = [vp, vp, vp, vp, sz, sz]
     lib.lancius_hip_mlp2_f32.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, vp, sz, sz, sz, sz, i32]
     lib.lancius_hip_add_f32.argtypes = [vp, vp, vp, vp, sz]
+    lib.lancius_hip_tanh_f32.argtypes = [vp, vp, vp, sz]
+    lib.lancius_hip_bias_act_f32.argtypes = [vp, vp, vp, vp, sz, sz, i32]
     lib.lancius_hip_relu_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_gelu_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_copy_f32.argtypes = [vp, vp, vp, sz]
@@ -304,6 +306,12 @@ class Device:
 
     def relu(self, out, a, n) -> None:
         _check(self.lib.lancius_hip_relu_f32(self.ctx, _vp(out), _vp(a), n))
+
+    def tanh(self, out, a, n) -> None:
+        _check(self.lib.lancius_hip_tanh_f32(self.ctx, _vp(out), _vp(a), n))
+
+    def bias_act(self, out, a, bias, rows, cols, act=ACT_NONE) -> None:
+        _check(self.lib.lancius_hip_bias_act_f32(self.ctx, _vp(out), _vp(a), _vp(bias), rows, cols, act))
 
     def gelu(self, out, a, n) -> None:
         _check(self.lib.lancius_hip_gelu_f32(self.ctx, _vp(out), _vp(a), n))

@@ -19,7 +19,8 @@ def _declared(header: Path, marker: str | None = None) -> set[str]:
     text = header.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     names = set()
-    for m in re.finditer(r"(?:^|\n)\s*(?:LANCIUS_HIP_EXPORT\s+)?[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text):
+    for m in re.finditer(r"(?:^|\n)\s*(?:LANCIUS_(?:HIP|BASIS)_EXPORT\s+)?[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(",
+                         text):
         line = m.group(0)
         if "typedef" in line or "#define" in line or "static inline" in line:
             continue
@@ -29,12 +30,18 @@ def _declared(header: Path, marker: str | None = None) -> set[str]:
     return names
 
 
+def _hip_declared() -> set[str]:
+    return (_declared(INCLUDE / "lancius_hip.h", "LANCIUS_HIP_EXPORT")
+            | _declared(INCLUDE / "lancius_hip_graph.h", "LANCIUS_HIP_EXPORT")
+            | _declared(INCLUDE / "lancius_basis.h", "LANCIUS_BASIS_EXPORT"))
+
+
 def test_hip_library_exports_every_declared_symbol():
     lib = C.CDLL(str(runtime.HIP_LIB))
-    names = _declared(INCLUDE / "lancius_hip.h", "LANCIUS_HIP_EXPORT") | _declared(
-        INCLUDE / "lancius_hip_graph.h", "LANCIUS_HIP_EXPORT")
+    names = _hip_declared()
     assert {"lancius_hip_gemm_f32", "lancius_hip_attention_f32", "lancius_hip_conv2d_f32", "kernel_matmul_f32",
-            "lancius_device_program_create", "lancius_schedule_execute_device"} <= names
+            "lancius_device_program_create", "lancius_schedule_execute_device", "basis_arena_create",
+            "basis_pool_free", "lancius_basis_program_run"} <= names
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert missing == []
 
@@ -43,9 +50,7 @@ def test_hip_library_exports_nothing_else():
     out = subprocess.run(["nm", "-D", "--defined-only", str(runtime.HIP_LIB)], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
-    declared = _declared(INCLUDE / "lancius_hip.h", "LANCIUS_HIP_EXPORT") | _declared(
-        INCLUDE / "lancius_hip_graph.h", "LANCIUS_HIP_EXPORT")
-    assert sorted(n for n in exported if n not in declared and not n.startswith("_")) == []
+    assert sorted(n for n in exported if n not in _hip_declared() and not n.startswith("_")) == []
 
 
 def test_graph_library_exports_every_declared_symbol():
@@ -53,6 +58,10 @@ def test_graph_library_exports_every_declared_symbol():
     names = _declared(INCLUDE / "lancius_graph.h")
     assert "lancius_build_memory_plan" in names and "lancius_ir_schedule" in names
     assert [n for n in sorted(names) if not hasattr(lib, n)] == []
+    # the BASIS builders (the lancius_basis.h declarations without the export marker)
+    basis = _declared(INCLUDE / "lancius_basis.h") - _declared(INCLUDE / "lancius_basis.h", "LANCIUS_BASIS_EXPORT")
+    assert {"basis_graph_new", "basis_graph_matmul", "basis_graph_print", "basis_graph_free"} <= basis
+    assert [n for n in sorted(basis) if not hasattr(lib, n)] == []
 
 
 def test_no_gpu_call_needed_to_load():
@@ -60,7 +69,8 @@ def test_no_gpu_call_needed_to_load():
     assert isinstance(lib.lancius_hip_device_count(), int)
 
 
-@pytest.mark.parametrize("header", ["lancius_hip.h", "lancius_hip_graph.h", "lancius_graph.h", "lancius_abi.h"])
+@pytest.mark.parametrize("header", ["lancius_hip.h", "lancius_hip_graph.h", "lancius_graph.h", "lancius_abi.h",
+                                    "lancius_basis.h"])
 def test_public_headers_are_c(tmp_path, header):
     src = tmp_path / "t.c"
     src.write_text(f'#include "{header}"\nint main(void) {{ return 0; }}\n')
@@ -142,3 +152,44 @@ def test_python_mirror_matches_c_layout(tmp_path):
     sizes = [int(x) for x in text.split("sizes")[1].split()[:5]]
     assert sizes == [C.sizeof(abi.Node), C.sizeof(abi.Graph), C.sizeof(abi.RuntimeState), C.sizeof(abi.Schedule),
                      C.sizeof(abi.MemoryPlan)]
+
+
+BASIS_INCLUDE = Path("/root/reference/include")
+
+BASIS_PROBE = r"""
+#include <stdio.h>
+#include <stddef.h>
+%(includes)s
+#define F(T, f) printf(#T "." #f " %%zu %%zu\n", offsetof(T, f), sizeof(((T*)0)->f))
+int main(void) {
+    F(basis_node, id); F(basis_node, op); F(basis_node, input_ids); F(basis_node, rows); F(basis_node, cols);
+    F(basis_node, name); F(basis_graph, nodes); F(basis_graph, node_count); F(basis_graph, node_cap);
+    printf("sizes %%zu %%zu\n", sizeof(basis_node), sizeof(basis_graph));
+    printf("ops %%d %%d %%d %%d %%d %%d\n", BASIS_OP_INPUT, BASIS_OP_MATMUL, BASIS_OP_ADD, BASIS_OP_RELU, BASIS_OP_TANH,
+           BASIS_OP_BROADCAST_ADD);
+    return 0;
+}
+"""
+
+
+def _basis_layout(tmp_path, includes: str, incdirs: list[Path], tag: str) -> str:
+    src = tmp_path / f"{tag}.c"
+    src.write_text(BASIS_PROBE % {"includes": includes})
+    exe = tmp_path / tag
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", *[f"-I{d}" for d in incdirs], str(src), "-o", str(exe)],
+                   check=True)
+    return subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout
+
+
+@pytest.mark.skipif(not BASIS_INCLUDE.is_dir(), reason="reference headers are only present in the build container")
+def test_basis_layout_matches_reference_headers(tmp_path):
+    """include/basis/stage6_ir/graph.h:7-39 and include/basis/core/memory.h:
+    same layouts and enum values, and either header order compiles."""
+    ref = _basis_layout(tmp_path, '#include "basis/stage6_ir/graph.h"\n#include "basis/core/memory.h"',
+                        [BASIS_INCLUDE], "ref")
+    ours = _basis_layout(tmp_path, '#include "lancius_basis.h"', [INCLUDE], "ours")
+    assert ours == ref
+    for order, tag in ((('"lancius_basis.h"', '"basis/stage6_ir/graph.h"', '"basis/core/memory.h"'), "a"),
+                       (('"basis/stage6_ir/graph.h"', '"basis/core/memory.h"', '"lancius_basis.h"'), "b")):
+        both = _basis_layout(tmp_path, "\n".join(f"#include {h}" for h in order), [INCLUDE, BASIS_INCLUDE], tag)
+        assert both == ref
