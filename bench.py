@@ -413,6 +413,29 @@ def bridge_case(dev, n=4096) -> dict:
             "note": "host-pointer bridge, PCIe copies of A, B and C included (wall clock)"}
 
 
+def basis_case(dev, steps, warmup) -> dict:
+    """The MLP as a BASIS static graph (include/basis/stage6_ir/graph.h):
+    x . W1 + b1 -> tanh -> . W2 + b2 -> relu through lancius_basis_program_*
+    (one fused two-layer launch)."""
+    from lancius_amd.basis import Graph, Program
+
+    g = Graph(graph_lib())
+    x, w1, b1 = g.input("x", 64, 784), g.input("W1", 784, 256), g.input("b1", 1, 256)
+    h = g.tanh(g.broadcast_add(g.matmul(x, w1), b1))
+    w2, b2 = g.input("W2", 256, 10), g.input("b2", 1, 10)
+    g.relu(g.broadcast_add(g.matmul(h, w2), b2))
+    prog = Program(dev, g)
+    for i, seed in ((x, 42), (w1, 142), (b1, 242), (w2, 342), (b2, 442)):
+        n = g.node(i)
+        prog.upload(i, prng.normal(seed, (n.rows, n.cols), 0, 0.02 if i != x else 1.0))
+    t = time_steps(dev, prog.run, steps, warmup)
+    info = prog.info()
+    prog.close()
+    g.close()
+    return {"fwd_latency_ms": round(t, 4), "launches": info["launches"], "GFLOP/s": round(26.02e6 / t / 1e6, 1),
+            "arena_KiB": round(info["arena_bytes"] / 1024, 1)}
+
+
 def graph_case(dev, bg, feeds, steps, warmup, flags=0):
     lib = graph_lib()
     lib.lancius_graph_set_dtype(bg.g, abi.DTYPE_FP32)
@@ -634,6 +657,8 @@ def main() -> int:
                                             "fwd_latency_ms_hipgraph": round(tg, 4),
                                             "fwd_latency_ms_unchained": round(tu, 4),
                                             "launches_unchained": info_u["launches"]}
+        log("basis graph")
+        extra["basis_mlp_graph_64x784x256x10_tanh"] = basis_case(dev, max(20, steps), 5)
         log("transformer block graph")
         bg = graphs.build_block(lib)
         feeds = {}

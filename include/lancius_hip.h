@@ -321,7 +321,7 @@ LANCIUS_HIP_EXPORT void lancius_hip_graph_destroy(lancius_hip_graph* graph);
 /* out = softmax(act1(x . W1 + b1) . W2 + b2) row by row (softmax != 0, with
  * the first-maximum argmax when argmax != NULL), or the logits y when
  * softmax == 0, in two launches (a split-K GEMM for the first layer, then
- * one workgroup for the rest): the MATMUL -> BROADCAST+ADD -> RELU|GELU ->
+ * one workgroup for the rest): the MATMUL -> BROADCAST+ADD -> RELU|GELU|TANH ->
  * MATMUL -> BROADCAST+ADD -> SOFTMAX chain of lancius_scheduler.c:169-233,
  * 284-308 for small batches, whose unfused form (five launches) is bound by
  * its launch count.  x [M][K1], W1 [K1][N1], W2 [N1][N2], out [M][N2]; b1,
@@ -332,6 +332,13 @@ LANCIUS_HIP_EXPORT void lancius_hip_graph_destroy(lancius_hip_graph* graph);
 LANCIUS_HIP_EXPORT int lancius_hip_mlp2_f32(lancius_hip_ctx* ctx, float* out, int32_t* argmax, const float* x,
                                             const float* w1, const float* b1, int act1, const float* w2,
                                             const float* b2, size_t M, size_t K1, size_t N1, size_t N2, int softmax);
+/* The same with an activation on the second layer too: y = act2(h . W2 +
+ * b2) before the softmax or the store (the BASIS graph's MATMUL ->
+ * BROADCAST_ADD -> RELU|TANH -> MATMUL -> BROADCAST_ADD -> RELU|TANH). */
+LANCIUS_HIP_EXPORT int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t* argmax, const float* x,
+                                               const float* w1, const float* b1, int act1, const float* w2,
+                                               const float* b2, int act2, size_t M, size_t K1, size_t N1, size_t N2,
+                                               int softmax);
 
 /* ---- model-file tensors to HBM -------------------------------------- */
 

@@ -34,7 +34,7 @@ struct ChainParams {
     float* out;       // [M][N2]: probabilities (softmax) or y
     int32_t* argmax;  // [M] or null
     float* part;      // [splits][M][N1]
-    int M, K1, N1, N2, act1, softmax;
+    int M, K1, N1, N2, act1, act2, softmax;
     int splits, kchunk, tiles_n;
 };
 
@@ -144,7 +144,7 @@ __global__ void __launch_bounds__(256) mlp2_tail(const ChainParams p) {
     __syncthreads();
     if (q != 0) return;
     float v = -INFINITY;
-    if (lane < N2) v = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) + (p.b2 ? p.b2[lane] : 0.0f);
+    if (lane < N2) v = apply_act(((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) + (p.b2 ? p.b2[lane] : 0.0f), p.act2);
     float* o = p.out + (size_t)r * N2;
     if (!p.softmax) {
         if (lane < N2) o[lane] = v;
@@ -184,13 +184,21 @@ using namespace lancius;
 extern "C" int lancius_hip_mlp2_f32(lancius_hip_ctx* ctx, float* out, int32_t* argmax, const float* x,
                                     const float* w1, const float* b1, int act1, const float* w2, const float* b2,
                                     size_t M, size_t K1, size_t N1, size_t N2, int softmax) {
+    return lancius_hip_mlp2_ex_f32(ctx, out, argmax, x, w1, b1, act1, w2, b2, LANCIUS_HIP_ACT_NONE, M, K1, N1, N2,
+                                   softmax);
+}
+
+extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t* argmax, const float* x,
+                                       const float* w1, const float* b1, int act1, const float* w2, const float* b2,
+                                       int act2, size_t M, size_t K1, size_t N1, size_t N2, int softmax) {
     LANCIUS_REQUIRE(ctx && out && x && w1 && w2, LANCIUS_HIP_ERR_NULL_PTR, "mlp2: NULL argument");
     LANCIUS_REQUIRE(M >= 1 && M <= (size_t)kT && N2 >= 1 && N2 <= (size_t)kT && N1 >= 1 && K1 >= 1 &&
                         M * N1 <= (size_t)kMaxH && N1 * N2 <= (size_t)kMaxW2 && K1 < (1u << 30),
                     LANCIUS_HIP_ERR_SHAPE, "mlp2: M=%zu K1=%zu N1=%zu N2=%zu outside the fused chain's limits", M, K1,
                     N1, N2);
-    LANCIUS_REQUIRE(act1 >= LANCIUS_HIP_ACT_NONE && act1 <= LANCIUS_HIP_ACT_TANH, LANCIUS_HIP_ERR_UNSUPPORTED,
-                    "mlp2: activation %d", act1);
+    LANCIUS_REQUIRE(act1 >= LANCIUS_HIP_ACT_NONE && act1 <= LANCIUS_HIP_ACT_TANH && act2 >= LANCIUS_HIP_ACT_NONE &&
+                        act2 <= LANCIUS_HIP_ACT_TANH,
+                    LANCIUS_HIP_ERR_UNSUPPORTED, "mlp2: activations %d, %d", act1, act2);
     if (int rc = bind_device(ctx)) return rc;
     ChainParams p{};
     p.x = x;
@@ -205,6 +213,7 @@ extern "C" int lancius_hip_mlp2_f32(lancius_hip_ctx* ctx, float* out, int32_t* a
     p.N1 = (int)N1;
     p.N2 = (int)N2;
     p.act1 = act1;
+    p.act2 = act2;
     p.softmax = softmax ? 1 : 0;
     p.tiles_n = (int)((N1 + kT - 1) / kT);
     // K ranges of whole k-tiles, about 128 deep, at most 8: the tail

@@ -9,6 +9,8 @@
  *    step taken only while the running result has exactly one consumer,
  *    becomes one lancius_hip_gemm_f32 with that epilogue (bias, activation,
  *    residual: the GEMM's own order);
+ *  - two such chains back to back with a small batch (one hidden layer of
+ *    an MLP) become one lancius_hip_mlp2_ex_f32 (try_mlp2);
  *  - BROADCAST_ADD -> RELU|TANH becomes one lancius_hip_bias_act_f32;
  *  - ADD, RELU, TANH run elementwise.
  * Nodes that are not absorbed get a 256-byte aligned buffer in one HBM
@@ -23,14 +25,15 @@
 #include "lancius_basis.h"
 #include "lancius_hip.h"
 
-enum { K_GEMM, K_BIAS_ACT, K_ADD, K_RELU, K_TANH };
+enum { K_GEMM, K_BIAS_ACT, K_ADD, K_RELU, K_TANH, K_MLP2 };
 
 typedef struct {
     int kind;
     int out;                 /* node whose buffer receives the result */
     int a, b;                /* operand nodes (-1: none) */
     int bias, residual, act; /* GEMM / bias_act epilogue */
-    size_t m, k, n;
+    int w2, bias2, act2;     /* second layer of K_MLP2 */
+    size_t m, k, n, n2;
 } basis_launch;
 
 struct lancius_basis_program {
@@ -106,6 +109,61 @@ static int act_of(basis_op_type op) {
     return op == BASIS_OP_RELU ? LANCIUS_HIP_ACT_RELU : op == BASIS_OP_TANH ? LANCIUS_HIP_ACT_TANH : -1;
 }
 
+/* MATMUL(x, W1) [-> BROADCAST_ADD(b1)] [-> RELU|TANH] -> MATMUL(., W2)
+ * [-> BROADCAST_ADD(b2)] [-> RELU|TANH] with single consumers, within
+ * lancius_hip_mlp2_ex_f32's limits (M <= 64, N2 <= 64, M*N1 <= 16384,
+ * N1*N2 <= 8192): one launch of two kernels instead of two split-K GEMMs
+ * with their reduces.  Fills L and marks the chain's inner nodes absorbed;
+ * returns 0 when the pattern does not match. */
+static int try_mlp2(const basis_graph* g, const int* uses, int head, basis_launch* L, char* absorbed) {
+    const basis_node* nd = g->nodes;
+    int chain[6], len = 0;
+    int t = head, c = sole_consumer(g, uses, t);
+    int b1 = -1, act1 = LANCIUS_HIP_ACT_NONE, b2 = -1, act2 = LANCIUS_HIP_ACT_NONE;
+    chain[len++] = t;
+    if (c >= 0 && nd[c].op == BASIS_OP_BROADCAST_ADD && nd[c].input_ids[0] == t && ready_before(g, nd[c].input_ids[1], head)) {
+        b1 = nd[c].input_ids[1];
+        chain[len++] = t = c;
+        c = sole_consumer(g, uses, t);
+    }
+    if (c >= 0 && act_of(nd[c].op) >= 0) {
+        act1 = act_of(nd[c].op);
+        chain[len++] = t = c;
+        c = sole_consumer(g, uses, t);
+    }
+    if (c < 0 || nd[c].op != BASIS_OP_MATMUL || nd[c].input_ids[0] != t || !ready_before(g, nd[c].input_ids[1], head))
+        return 0;
+    const int mm2 = c;
+    chain[len++] = t = c;
+    c = sole_consumer(g, uses, t);
+    if (c >= 0 && nd[c].op == BASIS_OP_BROADCAST_ADD && nd[c].input_ids[0] == t && ready_before(g, nd[c].input_ids[1], head)) {
+        b2 = nd[c].input_ids[1];
+        chain[len++] = t = c;
+        c = sole_consumer(g, uses, t);
+    }
+    if (c >= 0 && act_of(nd[c].op) >= 0) {
+        act2 = act_of(nd[c].op);
+        chain[len++] = t = c;
+    }
+    const size_t M = nd[head].rows, N1 = nd[head].cols, N2 = nd[mm2].cols;
+    if (M > 64 || N2 > 64 || M * N1 > 16384 || N1 * N2 > 8192) return 0;
+    for (int j = 0; j + 1 < len; j++) absorbed[chain[j]] = 1;
+    L->kind = K_MLP2;
+    L->a = nd[head].input_ids[0];
+    L->b = nd[head].input_ids[1];
+    L->bias = b1;
+    L->act = act1;
+    L->w2 = nd[mm2].input_ids[1];
+    L->bias2 = b2;
+    L->act2 = act2;
+    L->m = M;
+    L->k = nd[L->a].cols;
+    L->n = N1;
+    L->n2 = N2;
+    L->out = t;
+    return 1;
+}
+
 int lancius_basis_program_create(lancius_hip_ctx* ctx, const basis_graph* g, unsigned flags,
                                  lancius_basis_program** out) {
     if (!ctx || !g || !out) return LANCIUS_HIP_ERR_NULL_PTR;
@@ -147,7 +205,9 @@ int lancius_basis_program_create(lancius_hip_ctx* ctx, const basis_graph* g, uns
         L.bias = L.residual = -1;
         L.act = LANCIUS_HIP_ACT_NONE;
         int tail = (int)i; /* the node whose value the launch produces */
-        if (n->op == BASIS_OP_MATMUL) {
+        if (n->op == BASIS_OP_MATMUL && !keep_all && try_mlp2(g, uses, (int)i, &L, absorbed)) {
+            tail = L.out;
+        } else if (n->op == BASIS_OP_MATMUL) {
             L.kind = K_GEMM;
             L.m = n->rows;
             L.k = g->nodes[L.a].cols;
@@ -245,6 +305,12 @@ int lancius_basis_program_run(lancius_basis_program* p) {
                 break;
             case K_BIAS_ACT:
                 rc = lancius_hip_bias_act_f32(p->ctx, out, p->buf[L->a], p->buf[L->bias], L->m, L->n, L->act);
+                break;
+            case K_MLP2:
+                rc = lancius_hip_mlp2_ex_f32(p->ctx, out, NULL, p->buf[L->a], p->buf[L->b],
+                                             L->bias >= 0 ? p->buf[L->bias] : NULL, L->act, p->buf[L->w2],
+                                             L->bias2 >= 0 ? p->buf[L->bias2] : NULL, L->act2, L->m, L->k, L->n,
+                                             L->n2, 0);
                 break;
             case K_ADD:
                 rc = lancius_hip_add_f32(p->ctx, out, p->buf[L->a], p->buf[L->b], o->rows * o->cols);

@@ -77,6 +77,7 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_layernorm_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, f32]
     lib.lancius_hip_softmax_f32.argtypes = [vp, vp, vp, vp, sz, sz]
     lib.lancius_hip_mlp2_f32.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, vp, sz, sz, sz, sz, i32]
+    lib.lancius_hip_mlp2_ex_f32.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, vp, i32, sz, sz, sz, sz, i32]
     lib.lancius_hip_add_f32.argtypes = [vp, vp, vp, vp, sz]
     lib.lancius_hip_tanh_f32.argtypes = [vp, vp, vp, sz]
     lib.lancius_hip_bias_act_f32.argtypes = [vp, vp, vp, vp, sz, sz, i32]
@@ -297,9 +298,13 @@ class Device:
     def softmax(self, probs, argmax, x, rows, cols) -> None:
         _check(self.lib.lancius_hip_softmax_f32(self.ctx, _vp(probs), _vp(argmax), _vp(x), rows, cols))
 
-    def mlp2(self, out, argmax, x, w1, b1, act1, w2, b2, M, K1, N1, N2, softmax=True) -> None:
-        _check(self.lib.lancius_hip_mlp2_f32(self.ctx, _vp(out), _vp(argmax), _vp(x), _vp(w1), _vp(b1), act1,
-                                             _vp(w2), _vp(b2), M, K1, N1, N2, int(bool(softmax))))
+    def mlp2(self, out, argmax, x, w1, b1, act1, w2, b2, M, K1, N1, N2, softmax=True, act2=None) -> None:
+        if act2 is None:
+            _check(self.lib.lancius_hip_mlp2_f32(self.ctx, _vp(out), _vp(argmax), _vp(x), _vp(w1), _vp(b1), act1,
+                                                 _vp(w2), _vp(b2), M, K1, N1, N2, int(bool(softmax))))
+        else:
+            _check(self.lib.lancius_hip_mlp2_ex_f32(self.ctx, _vp(out), _vp(argmax), _vp(x), _vp(w1), _vp(b1), act1,
+                                                    _vp(w2), _vp(b2), act2, M, K1, N1, N2, int(bool(softmax))))
 
     def add(self, out, a, b, n) -> None:
         _check(self.lib.lancius_hip_add_f32(self.ctx, _vp(out), _vp(a), _vp(b), n))

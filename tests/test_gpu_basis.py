@@ -141,14 +141,18 @@ def _mlp_ref(f):
     return ht, np.maximum(oracle.matmul(ht, f["W2"]) + d["b2"], 0.0)
 
 
-@pytest.mark.parametrize("flags,launches", [(0, 2), (KEEP_ALL, 6)])
-def test_mlp_graph(dev, flags, launches):
-    g, ids = _mlp_graph()
+@pytest.mark.parametrize("M,flags,launches", [
+    (64, 0, 1),         # the whole MLP in one lancius_hip_mlp2_ex_f32 call
+    (96, 0, 2),         # batch above the chain kernel's limit: two fused GEMMs
+    (64, KEEP_ALL, 6),  # every node its own launch and buffer
+])
+def test_mlp_graph(dev, M, flags, launches):
+    g, ids = _mlp_graph(M=M)
     f = _feeds(g, ids, 300)
     prog = Program(dev, g, flags)
     for name, arr in f.items():
         prog.upload(ids[name], arr)
-    case(f"basis mlp flags={flags}")
+    case(f"basis mlp M={M} flags={flags}")
     prog.run()
     ht_ref, out_ref = _mlp_ref(f)
     got = prog.download(ids["out"])
@@ -158,7 +162,7 @@ def test_mlp_graph(dev, flags, launches):
         assert oracle.normwise_error(prog.download(ids["ht"]), ht_ref) <= oracle.tolerance(784)
         assert prog.buffer(ids["h"]) is not None
     else:
-        assert prog.buffer(ids["h"]) is None  # absorbed into the GEMM epilogue
+        assert prog.buffer(ids["h"]) is None  # absorbed into a fused launch
         with pytest.raises(HipError) as e:
             prog.download(ids["h"])
         assert e.value.code == -4
@@ -194,6 +198,29 @@ def test_residual_and_unfused_ops(dev):
     assert oracle.normwise_error(prog.download(bt), np.tanh(d[u] + d[b])) <= TOL_ELEMENTWISE
     # GEMM(+bias, ReLU, residual), ADD, TANH, RELU, bias+TANH
     assert prog.info()["launches"] == 5
+    prog.close()
+    g.close()
+
+
+def test_hidden_layer_read_twice_is_not_one_mlp_launch(dev):
+    """The hidden activation feeds both the second MATMUL and a residual ADD,
+    so it must be materialised: two GEMM chains, the second with the
+    residual in its epilogue, not one MLP launch."""
+    g = Graph(graph_lib())
+    x, W1, W2 = g.input("x", 32, 48), g.input("W1", 48, 64), g.input("W2", 64, 64)
+    h = g.tanh(g.matmul(x, W1))
+    out = g.add(g.relu(g.matmul(h, W2)), h)
+    f = {i: prng.normal(800 + i, (g.node(i).rows, g.node(i).cols), std=0.2) for i in (x, W1, W2)}
+    prog = Program(dev, g)
+    for i, arr in f.items():
+        prog.upload(i, arr)
+    case("basis mlp with a shared hidden layer")
+    prog.run()
+    ht = np.tanh(oracle.matmul(f[x], f[W1]))
+    ref = np.maximum(oracle.matmul(ht, f[W2]), 0.0) + ht
+    assert oracle.normwise_error(prog.download(out), ref) <= oracle.tolerance(64)
+    assert oracle.normwise_error(prog.download(h), ht) <= oracle.tolerance(48)
+    assert prog.info()["launches"] == 2
     prog.close()
     g.close()
 

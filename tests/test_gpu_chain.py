@@ -1,32 +1,40 @@
-"""lancius_hip_mlp2_f32: two dense layers and a row softmax in one launch,
-against the fp64 oracle of the unfused chain (MATMUL, bias, activation,
-MATMUL, bias, SOFTMAX, first-maximum argmax).  Tolerance as for the GEMM of
+"""lancius_hip_mlp2_f32 / lancius_hip_mlp2_ex_f32: two dense layers (each
+with bias and activation) and a row softmax in one launch, against the fp64
+oracle of the unfused chain (MATMUL, bias, activation, MATMUL, bias,
+activation, SOFTMAX, first-maximum argmax).  Tolerance as for the GEMM of
 the longest reduction, 1e-4 * max(1, sqrt(K1)/32); argmax bit-exact."""
 import numpy as np
 import pytest
 
 import oracle
-from lancius_amd import ACT_GELU, ACT_NONE, ACT_RELU, HipError, prng
+from lancius_amd import ACT_GELU, ACT_NONE, ACT_RELU, ACT_TANH, HipError, prng
 from tests.conftest import case
 
 pytestmark = pytest.mark.gpu
 
 
-def reference(x, w1, b1, act, w2, b2, softmax):
+def _act(h, act):
+    if act == ACT_RELU:
+        return oracle.relu(h)
+    if act == ACT_GELU:
+        return oracle.gelu(h)
+    if act == ACT_TANH:
+        return np.tanh(h)
+    return h
+
+
+def reference(x, w1, b1, act, w2, b2, softmax, act2=ACT_NONE):
     h = oracle.matmul(x, w1)
     if b1 is not None:
         h = h + b1.astype(np.float64)[None, :]
-    if act == ACT_RELU:
-        h = oracle.relu(h)
-    elif act == ACT_GELU:
-        h = oracle.gelu(h)
-    y = oracle.matmul(h, w2)
+    y = oracle.matmul(_act(h, act), w2)
     if b2 is not None:
         y = y + b2.astype(np.float64)[None, :]
+    y = _act(y, act2)
     return oracle.softmax(y) if softmax else y
 
 
-def run(dev, M, K1, N1, N2, act, bias, softmax, seed):
+def run(dev, M, K1, N1, N2, act, bias, softmax, seed, act2=None):
     x = prng.uniform(seed, (M, K1), -1.0, 1.0)
     w1 = prng.normal(seed + 1, (K1, N1), 0, 0.05)
     w2 = prng.normal(seed + 2, (N1, N2), 0, 0.1)
@@ -36,14 +44,14 @@ def run(dev, M, K1, N1, N2, act, bias, softmax, seed):
     db1 = dev.upload(b1) if bias else None
     db2 = dev.upload(b2) if bias else None
     out, am = dev.alloc(M * N2 * 4), dev.alloc(M * 4)
-    case(f"mlp2 M={M} K1={K1} N1={N1} N2={N2} act={act} bias={bias} softmax={softmax}")
-    dev.mlp2(out, am, bufs["x"], bufs["w1"], db1, act, bufs["w2"], db2, M, K1, N1, N2, softmax)
+    case(f"mlp2 M={M} K1={K1} N1={N1} N2={N2} act={act},{act2} bias={bias} softmax={softmax}")
+    dev.mlp2(out, am, bufs["x"], bufs["w1"], db1, act, bufs["w2"], db2, M, K1, N1, N2, softmax, act2)
     got = dev.download(out, (M, N2))
     idx = dev.download(am, (M,), np.int32) if softmax else None
     for b in list(bufs.values()) + [db1, db2, out, am]:
         if b is not None:
             b.free()
-    return got, idx, reference(x, w1, b1, act, w2, b2, softmax)
+    return got, idx, reference(x, w1, b1, act, w2, b2, softmax, ACT_NONE if act2 is None else act2)
 
 
 @pytest.mark.parametrize("M,K1,N1,N2,act,bias,softmax", [
@@ -63,6 +71,19 @@ def test_mlp2_matches_unfused_chain(dev, M, K1, N1, N2, act, bias, softmax):
         assert np.array_equal(idx, oracle.argmax(ref))
 
 
+@pytest.mark.parametrize("M,K1,N1,N2,act,act2,bias,softmax", [
+    (64, 784, 256, 10, ACT_TANH, ACT_RELU, True, False),  # the BASIS example MLP
+    (64, 784, 256, 10, ACT_TANH, ACT_TANH, True, True),
+    (5, 33, 64, 64, ACT_GELU, ACT_GELU, False, False),
+    (64, 128, 128, 64, ACT_NONE, ACT_RELU, True, True),
+])
+def test_mlp2_second_activation(dev, M, K1, N1, N2, act, act2, bias, softmax):
+    got, idx, ref = run(dev, M, K1, N1, N2, act, bias, softmax, 90 + N1 + act2, act2)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(max(K1, N1))
+    if softmax:
+        assert np.array_equal(idx, oracle.argmax(ref))
+
+
 def test_mlp2_repeatable(dev):
     """Fixed reduction orders and counters that return to zero: repeated
     calls give identical bits."""
@@ -76,3 +97,6 @@ def test_mlp2_limits(dev):
         with pytest.raises(HipError) as e:
             dev.mlp2(1, None, 1, 1, None, ACT_NONE, 1, None, M, K1, N1, N2)
         assert e.value.code == -3
+    with pytest.raises(HipError) as e:
+        dev.mlp2(1, None, 1, 1, None, ACT_NONE, 1, None, 8, 8, 8, 8, act2=7)
+    assert e.value.code != 0
