@@ -265,13 +265,24 @@ struct I8Params {
 };
 
 // CONV selects the B-operand gather (im2col over NHWC) and the NCHW store;
-// otherwise B rows come from B^T and C is row-major [M][N].
-template <int BM, int BN, bool CONV>
-__global__ void __launch_bounds__(kThreads, 2) gemm_i8_mfma(const I8Params p) {
-    constexpr int BK = 128;  // int8 of k per tile
+// otherwise B rows come from B^T and C is row-major [M][N].  WGM x WGN waves
+// each own a (BM/WGM) x (BN/WGN) sub-tile; BK int8 of k per tile.
+//
+// A k-tile's global loads are issued two tiles ahead of its use (two
+// register sets, even and odd tiles, and an LDS double buffer): at the LDS
+// store of tile t+1 the loads of tile t+2 stay in flight.  256 x 256 tiles
+// (8 waves of 128 x 64, one workgroup per CU) halve the bytes per MFMA
+// against 128 x 128.  Together these took 4096^3 from 106 to ~83 us; the
+// int8 pipes are still busy only about a third of the time (a pure-MFMA
+// loop reaches 0.9 of peak), the LDS fragment reads, the barrier-aligned
+// phases of the 8 waves and the loads not overlapping well enough.
+template <int BM, int BN, int WGM, int WGN, int BK, bool CONV>
+__global__ void __launch_bounds__(64 * WGM * WGN, 8 / (WGM * WGN)) gemm_i8_mfma(const I8Params p) {
     constexpr int LDK = BK + 16;
-    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int NT = 64 * WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int TM = WM / 32, TN = WN / 32;
+    static_assert(BK % 32 == 0, "k-tile of whole MFMA steps");
     __shared__ __attribute__((aligned(16))) int8_t As[2][BM][LDK];
     __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN][LDK];
 
@@ -280,22 +291,36 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_mfma(const I8Params p) {
     grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
     const int m0 = (int)tm_id * BM, n0 = (int)tn_id * BN;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = wave / 2, wn = wave % 2;
+    const int wm = wave / WGN, wn = wave % WGN;
     const int lr = lane & 31, lh = lane >> 5;
 
     // Each thread moves 16-byte chunks: chunk c of a tile row is k bytes
-    // [16c, 16c+16).  A tile: BM rows x 8 chunks, B tile: BN rows x 8 chunks.
+    // [16c, 16c+16).  A tile: BM rows x CH chunks, B tile: BN rows x CH chunks.
     constexpr int CH = BK / 16;
-    constexpr int A_LD = BM * CH / kThreads, B_LD = BN * CH / kThreads;
-    static_assert(A_LD * kThreads == BM * CH && B_LD * kThreads == BN * CH, "even split");
-    v4i a_v[A_LD], b_v[B_LD];
+    constexpr int A_LD = BM * CH / NT, B_LD = BN * CH / NT;
+    static_assert(A_LD * NT == BM * CH && B_LD * NT == BN * CH, "even split");
+    v4i a0[A_LD], b0[B_LD], a1[A_LD], b1[B_LD];
 
+    // Rows past M (A) or N (B) are loaded from row M-1 / N-1 instead of
+    // being zeroed: they only reach accumulator rows / columns that the
+    // epilogue never stores, and the loads need no branch.  k is padded
+    // with zeros to Kp in both operands.
+    const int8_t* a_row[A_LD];
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+        const int idx = tid + i * NT;
+        a_row[i] = p.A + (size_t)min(m0 + idx / CH, p.M - 1) * p.Kp + 16 * (idx % CH);
+    }
+    const int8_t* b_row[B_LD];
     // conv: the pixel of each B row this thread loads (fixed for the k loop)
     int pix_n[B_LD], pix_h[B_LD], pix_w[B_LD];
-    if constexpr (CONV) {
 #pragma unroll
-        for (int i = 0; i < B_LD; ++i) {
-            const int row = (tid + i * kThreads) / CH;
+    for (int i = 0; i < B_LD; ++i) {
+        const int idx = tid + i * NT;
+        const int row = idx / CH;
+        if constexpr (!CONV) {
+            b_row[i] = p.B + (size_t)min(n0 + row, p.N - 1) * p.Kp + 16 * (idx % CH);
+        } else {
             const int P = n0 + row;
             if (P < p.N) {
                 const int img = P / p.HWo, rem = P - (P / p.HWo) * p.HWo;
@@ -310,43 +335,46 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_mfma(const I8Params p) {
         }
     }
 
-    auto load_tile = [&](int k0) {
+    // Every load is unconditional, so the compiler's wait counts see one
+    // path: a load skipped on some path made it wait for all outstanding
+    // loads at the LDS store, the look-ahead tile included.  The conv gather
+    // loads the image's first pixel for taps outside the image and zeroes
+    // them at the store (bit i of *bin).
+    auto load_tile = [&](int k0, v4i* av, v4i* bv, unsigned* bin) {
 #pragma unroll
-        for (int i = 0; i < A_LD; ++i) {
-            const int idx = tid + i * kThreads;
-            const int row = idx / CH, ch = idx % CH;
-            const int gm = m0 + row;
-            a_v[i] = gm < p.M ? *(const v4i*)(p.A + (size_t)gm * p.Kp + k0 + 16 * ch) : v4i{0, 0, 0, 0};
-        }
+        for (int i = 0; i < A_LD; ++i) av[i] = *(const v4i*)(a_row[i] + k0);
+        if constexpr (CONV) *bin = 0;
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
-            const int idx = tid + i * kThreads;
-            const int row = idx / CH, ch = idx % CH;
             if constexpr (!CONV) {
-                const int gn = n0 + row;
-                b_v[i] = gn < p.N ? *(const v4i*)(p.B + (size_t)gn * p.Kp + k0 + 16 * ch) : v4i{0, 0, 0, 0};
+                bv[i] = *(const v4i*)(b_row[i] + k0);
             } else {
                 // k = (tap, channel run): 16 channels of one tap at one pixel
-                const int k = k0 + 16 * ch;
+                const int k = k0 + 16 * ((tid + i * NT) % CH);
                 const int tap = k / p.Cp, c = k - (k / p.Cp) * p.Cp;
                 const int kh = tap / p.KW, kw = tap - (tap / p.KW) * p.KW;
                 const int hi = pix_h[i] + kh, wi = pix_w[i] + kw;
                 const bool in = pix_n[i] >= 0 && tap < p.KHW && hi >= 0 && hi < p.H && wi >= 0 && wi < p.W;
-                b_v[i] = in ? *(const v4i*)(p.B + (((size_t)pix_n[i] * p.H + hi) * p.W + wi) * p.Cp + c)
-                            : v4i{0, 0, 0, 0};
+                const size_t off = in ? (((size_t)pix_n[i] * p.H + hi) * p.W + wi) * p.Cp + c : 0;
+                bv[i] = *(const v4i*)(p.B + off);
+                *bin |= (unsigned)in << i;
             }
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int buf, const v4i* av, const v4i* bv, unsigned bin) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
-            const int idx = tid + i * kThreads;
-            *(v4i*)&As[buf][idx / CH][16 * (idx % CH)] = a_v[i];
+            const int idx = tid + i * NT;
+            *(v4i*)&As[buf][idx / CH][16 * (idx % CH)] = av[i];
         }
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
-            const int idx = tid + i * kThreads;
-            *(v4i*)&Bs[buf][idx / CH][16 * (idx % CH)] = b_v[i];
+            const int idx = tid + i * NT;
+            v4i v = bv[i];
+            if constexpr (CONV) {
+                if (!((bin >> i) & 1u)) v = v4i{0, 0, 0, 0};
+            }
+            *(v4i*)&Bs[buf][idx / CH][16 * (idx % CH)] = v;
         }
     };
 
@@ -358,31 +386,49 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_i8_mfma(const I8Params p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-    const int ktiles = p.Kp / BK;
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int cur = kt & 1;
-        const bool more = kt + 1 < ktiles;
-        if (more) load_tile((kt + 1) * BK);
+    auto compute = [&](int buf) {
 #pragma unroll
         for (int ks = 0; ks < BK / 32; ++ks) {
             // lane half h holds k bytes [32ks + 16h, +16) of its row / column
             v4i af[TM], bf[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = *(const v4i*)&As[cur][wm * WM + i * 32 + lr][32 * ks + 16 * lh];
+            for (int i = 0; i < TM; ++i) af[i] = *(const v4i*)&As[buf][wm * WM + i * 32 + lr][32 * ks + 16 * lh];
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bf[j] = *(const v4i*)&Bs[cur][wn * WN + j * 32 + lr][32 * ks + 16 * lh];
+            for (int j = 0; j < TN; ++j) bf[j] = *(const v4i*)&Bs[buf][wn * WN + j * 32 + lr][32 * ks + 16 * lh];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (more) store_tile(cur ^ 1);
+    };
+
+    // Even tiles live in (a0, b0) and LDS buffer 0, odd tiles in (a1, b1)
+    // and buffer 1.
+    // Past the last tile the loads re-read the last tile (never stored).
+    const int ktiles = p.Kp / BK;
+    unsigned in0 = 0, in1 = 0;
+    load_tile(0, a0, b0, &in0);
+    load_tile(min(1, ktiles - 1) * BK, a1, b1, &in1);
+    store_tile(0, a0, b0, in0);
+    __syncthreads();
+    // Pairs of tiles per trip, the odd last tile after the loop (an exit in
+    // the middle of the trip made the compiler rotate the loop and keep two
+    // copies of the accumulators).
+    int kt = 0;
+    for (; kt + 1 < ktiles; kt += 2) {
+        load_tile(min(kt + 2, ktiles - 1) * BK, a0, b0, &in0);
+        compute(0);
+        __builtin_amdgcn_sched_barrier(0);
+        store_tile(1, a1, b1, in1);  // waits for tile kt+1 only
+        __syncthreads();
+        load_tile(min(kt + 3, ktiles - 1) * BK, a1, b1, &in1);
+        compute(1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 2 < ktiles) store_tile(0, a0, b0, in0);
         __syncthreads();
     }
+    if (kt < ktiles) compute(0);
 
     // int32 -> (double) * scale_a * scale_b -> fp32, then bias / act / residual.
     // Register r of lane l: row 8(r/4) + 4(l/32) + r%4, column l%32.
@@ -462,7 +508,7 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_TANH, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "gemm_i8: activation %d", act);
     if (int rc = bind_device(ctx)) return rc;
-    constexpr int BM = 128, BN = 128, BK = 128;
+    constexpr int BK = 128;
     const size_t Kp = align_up(K, BK);
     // workspace: scales (2 doubles) | absmax partials | A_q [M][Kp] | B^T [N][Kp]
     const size_t off_part = 64, off_a = align_up(off_part + kMaxBlocks * sizeof(float), 256);
@@ -505,11 +551,24 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     p.N = (int)N;
     p.Kp = (int)Kp;
     p.act = act;
+    // 256 x 256 tiles when they still give every CU one (fewer bytes per
+    // MFMA), else 128 x 128 (more workgroups for small products)
+    const int big = tune("gemm_i8_big", ((M + 255) / 256) * ((N + 255) / 256) >= 240 ? 1 : 0);
+    const int bk = tune("gemm_i8_bk", 128);
+    const int BM = big ? 256 : 128, BN = BM;
     p.tiles_m = (uint32_t)((M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((N + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: too many tiles");
-    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, false>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
+    if (big && bk == 128)
+        hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 128, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,
+                           p);
+    else if (big)
+        hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 64, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,
+                           p);
+    else
+        hipLaunchKernelGGL((gemm_i8_mfma<128, 128, 2, 2, 128, false>), dim3((unsigned)grid), dim3(256), 0, ctx->stream,
+                           p);
     if (int rc = check_launch("gemm_i8_mfma")) return rc;
     return ok();
 }
@@ -583,7 +642,8 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     p.tiles_n = (uint32_t)((P + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: too many tiles");
-    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, true>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
+    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, 2, 2, 128, true>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream,
+                       p);
     return check_launch("conv2d_i8_mfma");
 }
 

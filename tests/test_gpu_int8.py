@@ -72,7 +72,9 @@ def test_gemm_i8_golden(dev):
 
 
 @pytest.mark.parametrize("M,Kd,N", [(1, 1, 1), (64, 784, 128), (130, 70, 201), (257, 300, 129), (1024, 1024, 1024),
-                                    (33, 4096, 50)])
+                                    (33, 4096, 50),
+                                    # 256 x 256 tiles (one per CU or more): exact and ragged edges
+                                    (4096, 128, 4096), (3900, 130, 3950)])
 def test_gemm_i8_shapes(dev, M, Kd, N):
     a = prng.normal(80 + M, (M, Kd))
     bq = np.round(prng.uniform(81 + N, (Kd, N), -127.4, 127.4)).astype(np.int8)
@@ -80,8 +82,8 @@ def test_gemm_i8_shapes(dev, M, Kd, N):
     assert oracle.normwise_error(got, oracle.matmul_i8(f64(a), bq, 0.0123)) <= TOL
 
 
-def test_gemm_i8_epilogue(dev):
-    M, Kd, N = 96, 200, 72
+@pytest.mark.parametrize("M,Kd,N", [(96, 200, 72), (3850, 40, 4000)])
+def test_gemm_i8_epilogue(dev, M, Kd, N):
     a = prng.normal(90, (M, Kd))
     bq = np.round(prng.uniform(91, (Kd, N), -127.4, 127.4)).astype(np.int8)
     bias, res = prng.normal(92, (N,)), prng.normal(93, (M, N))
