@@ -65,13 +65,25 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
     static_assert(BK % 4 == 0, "BK multiple of 4");
     constexpr int KPG = BK / 2 / KG;  // k-pairs per group per k-tile
     static_assert(KPG >= 1 && KPG * KG * 2 == BK, "k-pairs split evenly over the groups");
+    // AMK: A[M][K] loaded along k is kept m-major in LDS (Am[m][k], a
+    // 16-byte store per float4); k-group g takes k in [g*BK/KG, (g+1)*BK/KG)
+    // and lane half h of its MFMAs the h-th half of that range: a lane's A
+    // operands for a whole k-tile are BK/(8 KG) 16-byte reads instead of
+    // BK/(2 KG) 4-byte reads, and the k-major transpose on the store (four
+    // 4-byte writes per float4) goes away.  Any pairing of k between A and B
+    // is valid as long as both use the same one.  The pitch BK+4 keeps 16
+    // consecutive rows on distinct 16-byte bank groups.
+    constexpr bool AMK = VEC && !TA && (BK / KG) % 8 == 0;
     constexpr int LDA = BM + 4;  // As[k][m]
     constexpr int LDB = BN + 4;  // Bs[k][n]
-    constexpr int STAGE = 2 * BK * (LDA + LDB);
+    constexpr int LDK = BK + 4;  // Am[m][k]
+    constexpr int A_STAGE = AMK ? BM * LDK : BK * LDA;
+    constexpr int STAGE = 2 * (A_STAGE + BK * LDB);
     constexpr int RED = KG > 1 ? 4 * TM * TN * 16 * 64 : 0;  // one group's accumulators
     __shared__ __attribute__((aligned(16))) float smem[STAGE > RED ? STAGE : RED];
     float(*As)[BK][LDA] = reinterpret_cast<float(*)[BK][LDA]>(smem);
-    float(*Bs)[BK][LDB] = reinterpret_cast<float(*)[BK][LDB]>(smem + 2 * BK * LDA);
+    float(*Am)[BM][LDK] = reinterpret_cast<float(*)[BM][LDK]>(smem);
+    float(*Bs)[BK][LDB] = reinterpret_cast<float(*)[BK][LDB]>(smem + 2 * A_STAGE);
 
     const int g = blockIdx.z;
     const float* __restrict__ A = p.A[g];
@@ -216,7 +228,9 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
                 const int idx = tid + i * NT;
-                if constexpr (!TA) {
+                if constexpr (AMK) {
+                    *(f32x4*)&Am[buf][idx / (BK / 4)][4 * (idx % (BK / 4))] = a_v[i];
+                } else if constexpr (!TA) {
                     const int r = idx / (BK / 4), kq = idx % (BK / 4);
                     As[buf][4 * kq + 0][r] = a_v[i].x;
                     As[buf][4 * kq + 1][r] = a_v[i].y;
@@ -287,6 +301,40 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
         // program order (the compiler may sink the reads after them; the
         // other waves on the SIMD cover that latency - pinning the order
         // measured no faster).
+        if constexpr (AMK) {
+            // group kg, lane half lk: k = kb + kp, kp = 0 .. KH-1
+            constexpr int KH = BK / KG / 2;
+            const int kb = kg * (BK / KG) + lk * KH;
+            f32x4 av[TM][KH / 4];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int h = 0; h < KH / 4; ++h) av[i][h] = *(const f32x4*)&Am[cur][wm * WM + i * 32 + lr][kb + 4 * h];
+            float bf[2][TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[0][j] = Bs[cur][kb][wn * WN + j * 32 + lr];
+#pragma unroll
+            for (int kp = 0; kp < KH; ++kp) {
+                const int c = kp & 1;
+                if (kp + 1 < KH) {
+#pragma unroll
+                    for (int j = 0; j < TN; ++j) bf[c ^ 1][j] = Bs[cur][kb + kp + 1][wn * WN + j * 32 + lr];
+                }
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[c][j], acc[i][j],
+                                                                         0, 0, 0);
+                if (kp == (KH > 1 ? KH / 2 - 1 : 0)) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    store_tile(cur ^ 1, (kt + 1) * BK);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            __syncthreads();
+            continue;
+        }
         // group kg: k rows 2 (kg + KG j) + lk, j = 0 .. KPG-1
         float af[2][TM], bf[2][TN];
         const int kf = 2 * kg + lk;
