@@ -13,7 +13,7 @@
 // B operand is never materialised: each k-tile of the im2col matrix is
 // gathered from the NCHW input straight into LDS (zero outside the padded
 // image), consecutive threads taking consecutive pixels so the gathers
-// coalesce along W.  The MFMA tiling, double-buffered LDS and k-major layout
+// coalesce along W.  The MFMA tiling, double-buffered LDS and LDS layouts
 // are those of the GEMM kernel; the epilogue writes Out[n][co][ho][wo], where
 // lanes 0..31 of a register cover 32 consecutive pixels of one channel.
 #include <algorithm>
@@ -28,7 +28,7 @@ struct ConvParams {
     float* out;
     const float* in;
     const float* w;
-    const float* wt;   // weights re-laid k-major: wt[(tap*C_in + ci)*C_out + co] (CI_INNER path)
+    const float* wt;   // weights re-laid per output channel: wt[(co*KH*KW + tap)*C_in + ci] (CI_INNER path)
     const float* bias;
     int N, C_in, H, W, C_out, KH, KW, stride, pad, Ho, Wo;
     int Kdim;          // C_in * KH * KW
@@ -47,8 +47,18 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int LDA = BM + 4;
     constexpr int LDB = BN + 4;
-    __shared__ __attribute__((aligned(16))) float As[2][BK][LDA];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LDB];
+    // CI_INNER stages the filter tile m-major (Am[co][k], pitch BK+4: 16
+    // consecutive rows on distinct 16-byte bank groups) and lane half h of
+    // every MFMA takes k in [h*BK/2, (h+1)*BK/2), so a lane reads its A
+    // operands for a whole k-tile with BK/8 16-byte reads; B reads the
+    // matching rows.  Otherwise the filter tile is k-major (As[k][co]).
+    constexpr int LDK = BK + 4;
+    constexpr int A_STAGE = CI_INNER ? BM * LDK : BK * LDA;
+    static_assert(!CI_INNER || BK % 8 == 0, "k halves of whole float4");
+    __shared__ __attribute__((aligned(16))) float smem[2 * A_STAGE + 2 * BK * LDB];
+    float(*As)[BK][LDA] = reinterpret_cast<float(*)[BK][LDA]>(smem);
+    float(*Am)[BM][LDK] = reinterpret_cast<float(*)[BM][LDK]>(smem);
+    float(*Bs)[BK][LDB] = reinterpret_cast<float(*)[BK][LDB]>(smem + 2 * A_STAGE);
 
     const int KH = KH_T > 0 ? KH_T : p.KH;
     const int KW = KW_T > 0 ? KW_T : p.KW;
@@ -107,14 +117,17 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
             const int tap = kt / ctiles;
             const int ci0 = (kt - tap * ctiles) * BK;
             const int kh = tap / KW, kw = tap - (tap / KW) * KW;
-            // A tile straight from the k-major weights: rows k, float4 along co.
-            const float* wrow = p.wt + (size_t)(tap * p.C_in + ci0) * C_out + m0;
+            // A tile straight from the per-channel weights: rows co, float4
+            // along ci.  Rows past C_out re-read the last row (they only
+            // reach output channels that are never stored); threads past
+            // the tile re-read its last float4 and store nothing.
+            const float* wrow = p.wt + (size_t)tap * p.C_in + ci0;
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
-                const int idx = tid + i * kThreads;
-                const int c = idx / (BM / 4), rq = idx % (BM / 4);
-                a_v[i] = (idx < A4 && m0 + 4 * rq < C_out) ? *(const f32x4*)(wrow + (size_t)c * C_out + 4 * rq)
-                                                          : f32x4{0.f, 0.f, 0.f, 0.f};
+                const int idx = min(tid + i * kThreads, A4 - 1);
+                const int r = idx / (BK / 4), kq = idx % (BK / 4);
+                const int co = min(m0 + r, C_out - 1);
+                a_v[i] = *(const f32x4*)(wrow + (size_t)co * KHW * p.C_in + 4 * kq);
             }
             const int hi = hi0 + kh, wi = wi0 + kw;
             const bool inside = p_valid && hi >= 0 && hi < H && wi >= 0 && wi < W;
@@ -150,7 +163,7 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
                 const int idx = tid + i * kThreads;
-                if (idx < A4) *(f32x4*)&As[buf][idx / (BM / 4)][4 * (idx % (BM / 4))] = a_v[i];
+                if (idx < A4) *(f32x4*)&Am[buf][idx / (BK / 4)][4 * (idx % (BK / 4))] = a_v[i];
             }
         } else {
 #pragma unroll
@@ -179,6 +192,29 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
         const int cur = kt & 1;
         const bool more = kt + 1 < ktiles;
         if (more) load_tile(kt + 1);
+        if constexpr (CI_INNER) {
+            // lane half lk: k = lk*KH + kp
+            constexpr int KH2 = BK / 2;
+            f32x4 av[TM][KH2 / 4];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int h = 0; h < KH2 / 4; ++h) av[i][h] = *(const f32x4*)&Am[cur][wm * WM + i * 32 + lr][lk * KH2 + 4 * h];
+#pragma unroll
+            for (int kp = 0; kp < KH2; ++kp) {
+                float bf[TN];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) bf[j] = Bs[cur][lk * KH2 + kp][wn * WN + j * 32 + lr];
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
+            }
+            if (more) store_tile(cur ^ 1);
+            __syncthreads();
+            continue;
+        }
 #pragma unroll
         for (int kp = 0; kp < BK / 2; ++kp) {
             float af[TM], bf[TN];
@@ -222,17 +258,17 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
     }
 }
 
-// wt[(tap*C_in + ci)*C_out + co] = w[(co*C_in + ci)*KHW + tap]: the OIHW
+// wt[(co*KHW + tap)*C_in + ci] = w[(co*C_in + ci)*KHW + tap]: the OIHW
 // weights re-laid with the reduction index (tap, ci) major and C_out
 // contiguous, so the conv's A tiles are plain float4 row copies.
-__global__ void __launch_bounds__(256) conv_weights_kmajor(float* __restrict__ wt, const float* __restrict__ w,
+__global__ void __launch_bounds__(256) conv_weights_per_co(float* __restrict__ wt, const float* __restrict__ w,
                                                            int C_out, int C_in, int KHW) {
     const size_t total = (size_t)C_out * C_in * KHW;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t d = (size_t)blockIdx.x * blockDim.x + threadIdx.x; d < total; d += stride) {
-        const int co = (int)(d % C_out);
-        const size_t kk = d / C_out;
-        const int ci = (int)(kk % C_in), tap = (int)(kk / C_in);
+        const int ci = (int)(d % C_in);
+        const size_t r = d / C_in;
+        const int tap = (int)(r % KHW), co = (int)(r / KHW);
         wt[d] = w[((size_t)co * C_in + ci) * KHW + tap];
     }
 }
@@ -242,11 +278,11 @@ __global__ void __launch_bounds__(256) conv_weights_kmajor(float* __restrict__ w
 // Input gradient at stride 1 is itself a convolution: dx = conv(dy, w') with
 // w'[ci][co][kh][kw] = w[co][ci][K_h-1-kh][K_w-1-kw] and padding K-1-pad,
 // since dx[ih] = sum_kh dy[ih + pad - kh] w[kh].  The flipped weights are
-// written straight into the layout the forward kernel reads: k-major
-// ((tap, co) rows, C_in contiguous) when the forward kernel takes that path,
-// OIHW otherwise.
+// written straight into the layout the forward kernel reads: per output
+// channel ((ci, tap) rows, C_out contiguous) when the forward kernel takes
+// that path, OIHW otherwise.
 __global__ void __launch_bounds__(256) dgrad_weights(float* __restrict__ wt, const float* __restrict__ w, int C_out,
-                                                     int C_in, int KH, int KW, int kmajor) {
+                                                     int C_in, int KH, int KW, int per_co) {
     const int KHW = KH * KW;
     const size_t total = (size_t)C_out * C_in * KHW;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -258,8 +294,8 @@ __global__ void __launch_bounds__(256) dgrad_weights(float* __restrict__ wt, con
         const int ftap = (KH - 1 - kh) * KW + (KW - 1 - kw);  // tap of the flipped filter
         const float v = w[s];
         // flipped conv: output channel ci, input channel co
-        if (kmajor)
-            wt[((size_t)ftap * C_out + co) * C_in + ci] = v;
+        if (per_co)
+            wt[((size_t)ci * KHW + ftap) * C_out + co] = v;
         else
             wt[((size_t)ci * C_out + co) * KHW + ftap] = v;
     }
@@ -481,9 +517,9 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
         if (int rc = workspace(ctx, wbytes, &ws)) return rc;
         p.wt = (const float*)ws;
         const size_t total = (size_t)p.C_out * p.Kdim;
-        hipLaunchKernelGGL(conv_weights_kmajor, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)),
+        hipLaunchKernelGGL(conv_weights_per_co, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)),
                            dim3(256), 0, ctx->stream, (float*)ws, p.w, p.C_out, p.C_in, p.KH * p.KW);
-        if (int rc = check_launch("conv_weights_kmajor")) return rc;
+        if (int rc = check_launch("conv_weights_per_co")) return rc;
     }
     if (p.wt)
         hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
@@ -596,14 +632,14 @@ extern "C" int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx,
     p.Kdim = (int)(C_out * K_h * K_w);
     p.Ptotal = (long long)N * H * W;
     p.act = LANCIUS_HIP_ACT_NONE;
-    const bool kmajor = p.C_in % 16 == 0 && p.C_out % 4 == 0;
+    const bool per_co = p.C_in % 16 == 0 && p.C_out % 4 == 0;
     void* ws = nullptr;
     if (int rc = workspace(ctx, C_out * C_in * K_h * K_w * sizeof(float), &ws)) return rc;
     const size_t wn = C_out * C_in * K_h * K_w;
     hipLaunchKernelGGL(dgrad_weights, dim3((unsigned)std::min<size_t>((wn + 255) / 256, 2048)), dim3(256), 0,
-                       ctx->stream, (float*)ws, w, (int)C_out, (int)C_in, (int)K_h, (int)K_w, (int)kmajor);
+                       ctx->stream, (float*)ws, w, (int)C_out, (int)C_in, (int)K_h, (int)K_w, (int)per_co);
     if (int rc = check_launch("conv2d_dgrad_weights")) return rc;
-    if (kmajor)
+    if (per_co)
         p.wt = (const float*)ws;
     else
         p.w = (const float*)ws;
