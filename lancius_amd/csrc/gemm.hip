@@ -136,13 +136,31 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
     // stored.  Elements past K must be zero: store_tile clears them in the
     // one k-tile that crosses K (a uniform branch), so no select waits on a
     // load in the other tiles.
+    // AMK: float4 idx of the A tile -> (row, k chunk).  A wave's 64 float4
+    // cover 64/KQ rows x all KQ chunks, as with row-major order, but lanes
+    // of one chunk take consecutive rows, so a 16-lane group stores 16 rows
+    // of one chunk: the same distinct 16-byte bank slots as the operand
+    // reads (row-major order put 4 lanes on one 64-byte row segment and
+    // conflicted 2-way at the BK+4 pitch).
+    constexpr int KQ = BK / 4, RPW = 64 / KQ;
+    static_assert(!AMK || (64 % KQ == 0 && (BM * KQ) % 64 == 0), "whole waves of A rows");
+    auto a_rk = [&](int idx, int& r, int& kq) {
+        if constexpr (AMK) {
+            r = (idx / 64) * RPW + (idx % 64) % RPW;
+            kq = (idx % 64) / RPW;
+        } else {
+            r = idx / KQ;
+            kq = idx % KQ;
+        }
+    };
     auto load_tile = [&](int k0) {
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < A_VEC; ++i) {
                 const int idx = tid + i * NT;
                 if constexpr (!TA) {
-                    const int r = idx / (BK / 4), kq = idx % (BK / 4);
+                    int r, kq;
+                    a_rk(idx, r, kq);
                     const int gm = m0 + r, gk = k0 + 4 * kq;
                     a_v[i] = *(const f32x4*)(A + (size_t)min(gm, M - 1) * K + min(gk, K - 4));
                 } else {
@@ -199,7 +217,9 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
 #pragma unroll
         for (int i = 0; i < A_VEC; ++i) {
             const int idx = tid + i * NT;
-            const int gk = !TA ? k0 + 4 * (idx % (BK / 4)) : k0 + idx / (BM / 4);
+            int r, kq;
+            a_rk(idx, r, kq);
+            const int gk = !TA ? k0 + 4 * kq : k0 + idx / (BM / 4);
             if (gk >= K) a_v[i] = z4;
         }
 #pragma unroll
@@ -229,9 +249,12 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
             for (int i = 0; i < A_VEC; ++i) {
                 const int idx = tid + i * NT;
                 if constexpr (AMK) {
-                    *(f32x4*)&Am[buf][idx / (BK / 4)][4 * (idx % (BK / 4))] = a_v[i];
+                    int r, kq;
+                    a_rk(idx, r, kq);
+                    *(f32x4*)&Am[buf][r][4 * kq] = a_v[i];
                 } else if constexpr (!TA) {
-                    const int r = idx / (BK / 4), kq = idx % (BK / 4);
+                    int r, kq;
+                    a_rk(idx, r, kq);
                     As[buf][4 * kq + 0][r] = a_v[i].x;
                     As[buf][4 * kq + 1][r] = a_v[i].y;
                     As[buf][4 * kq + 2][r] = a_v[i].z;
