@@ -662,7 +662,9 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     const size_t J = C_in * K_h * K_w;
     if (C_out * J == 0) return ok();
     if (int rc = bind_device(ctx)) return rc;
-    constexpr int BM = 64, BN = 64;
+    // 128 x 64 tiles (two 32 x 32 MFMA blocks per wave) when C_out > 64,
+    // else 64 x 64 (one)
+    const int BM = tune("conv_wgrad_bm", C_out > 64 ? 128 : 64) == 128 ? 128 : 64, BN = 64;
     WgradParams p{};
     p.dw = dw;
     p.dy = dy;
@@ -684,15 +686,25 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     p.tiles_n = (uint32_t)((J + BN - 1) / BN);
     const size_t tiles = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(tiles < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: too many tiles");
-    // Split the pixel reduction for ~1024 workgroups, each >= 256 pixels deep.
-    // k-tiles of 32 pixels: 296 -> 264 us at the N32 64->128 56x56 config
-    // (16: 64-byte runs per load; 64: 70 KB of LDS, fewer workgroups per CU,
-    // 360 us).
+    // Split the pixel reduction so the grid is one full round of resident
+    // workgroups (CUs x workgroups per CU by LDS), each >= 256 pixels deep:
+    // a partial second round costs the time of a whole one.  k-tiles of 32
+    // pixels (16: 64-byte runs per load; 64: 70 KB of LDS, fewer workgroups
+    // per CU).  At the N32 64->128 56x56 config: 64 x 64 tiles, 57 splits
+    // (1026 workgroups for 1024 slots) 0.239 ms; 128 x 64 tiles, 85 splits
+    // (765 for 768) 0.216 ms.
     int bk = tune("conv_wgrad_bk", 32);
     if (bk != 16 && bk != 64) bk = 32;
+    if (BM == 128 && bk == 64) bk = 32;
     const long long ktiles = (p.Ptotal + bk - 1) / bk;
     long long splits = tune("conv_wgrad_split", 0);
-    if (splits <= 0) splits = std::max<long long>(1, std::min<long long>((1024 + tiles - 1) / tiles, ktiles * bk / 256));
+    if (splits <= 0) {
+        const size_t lds = (size_t)2 * bk * ((BM + 4) + (BN + 4)) * sizeof(float);
+        const size_t per_cu = std::max<size_t>(1, std::min<size_t>(8, 163840 / lds));
+        const size_t slots = (size_t)cu_count(ctx) * per_cu;
+        splits = std::max<long long>(1, std::min<long long>((long long)std::max<size_t>(1, slots / tiles),
+                                                            ktiles * bk / 256));
+    }
     splits = std::max<long long>(1, std::min<long long>({splits, std::max<long long>(ktiles, 1), 65535}));
     while (splits > 1 && (size_t)splits * C_out * J * sizeof(float) > ((size_t)1 << 28)) splits = (splits + 1) / 2;
     const long long chunk_tiles = (std::max<long long>(ktiles, 1) + splits - 1) / splits;
@@ -703,15 +715,17 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
         if (int rc = workspace(ctx, (size_t)p.splits * C_out * J * sizeof(float), &ws)) return rc;
         p.ws = (float*)ws;
     }
-    if (bk == 64)
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN, 64>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
-                           ctx->stream, p);
+    const dim3 grid((unsigned)tiles, (unsigned)p.splits);
+    if (BM == 128 && bk == 32)
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<128, 64, 32>), grid, dim3(256), 0, ctx->stream, p);
+    else if (BM == 128)
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<128, 64, 16>), grid, dim3(256), 0, ctx->stream, p);
+    else if (bk == 64)
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<64, 64, 64>), grid, dim3(256), 0, ctx->stream, p);
     else if (bk == 32)
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN, 32>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
-                           ctx->stream, p);
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<64, 64, 32>), grid, dim3(256), 0, ctx->stream, p);
     else
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<BM, BN, 16>), dim3((unsigned)tiles, (unsigned)p.splits), dim3(256), 0,
-                           ctx->stream, p);
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<64, 64, 16>), grid, dim3(256), 0, ctx->stream, p);
     if (int rc = check_launch("conv2d_wgrad_mfma")) return rc;
     if (p.splits > 1) {
         const size_t n = C_out * J;
