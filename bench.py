@@ -280,8 +280,15 @@ def int8_cases(dev, steps, warmup) -> dict:
     t = time_steps(dev, lambda: dev.conv2d_i8(o, x, w, 0.001, None, N, C_in, H, W, C_out, 3, 3, 1, 1, 1), steps,
                    warmup)
     ops = 2.0 * N * C_out * H * W * C_in * 9
+    # 14.8 G ops over >= 77 MB (fp32 activation in, fp32 output out, int8
+    # filter) is ~190 ops per byte, below the int8 MFMA ridge (5.0 P / 8 TB/s
+    # = 625): HBM is this call's roofline, so both fractions are reported.
+    nbytes = 4.0 * (N * C_in * H * W + N * C_out * H * W) + C_out * C_in * 9
     out["conv3x3_N32_64to128_56x56_relu_i8"] = {"ms": round(t, 4), "TOPS": round(ops / t / 1e9, 1),
-                                                "frac_int8_mfma": round(ops / t / 1e9 / PEAK_INT8_MFMA, 4)}
+                                                "frac_int8_mfma": round(ops / t / 1e9 / PEAK_INT8_MFMA, 4),
+                                                "GB/s": round(nbytes / t / 1e6, 1),
+                                                "frac_hbm": round(nbytes / t / 1e6 / PEAK_HBM, 4),
+                                                "bound": "hbm"}
     for buf in (x, w, o):
         buf.free()
     return out
