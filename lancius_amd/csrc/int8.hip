@@ -276,8 +276,8 @@ struct I8Params {
 // int8 pipes are still busy only about a third of the time (a pure-MFMA
 // loop reaches 0.9 of peak), the LDS fragment reads, the barrier-aligned
 // phases of the 8 waves and the loads not overlapping well enough.
-template <int BM, int BN, int WGM, int WGN, int BK, bool CONV>
-__global__ void __launch_bounds__(64 * WGM * WGN, 8 / (WGM * WGN)) gemm_i8_mfma(const I8Params p) {
+template <int BM, int BN, int WGM, int WGN, int BK, bool CONV, int MINW = 8 / (WGM * WGN)>
+__global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Params p) {
     constexpr int LDK = BK + 16;
     constexpr int NT = 64 * WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -585,7 +585,13 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
                     "conv2d_i8: activation %d", act);
     const size_t Cp = align_up(C_in, 16);
     const size_t KHW = K_h * K_w;
-    const size_t Kp = align_up(KHW * Cp, 128);
+    // k-tiles of 64 (k padded to 64, not 128) at 3 waves per SIMD: 40 KB of
+    // LDS and <= 168 VGPRs per 128 x 128 workgroup, 3 per CU.  The bench
+    // conv's 784 tiles then take one round plus 16 tiles instead of 1.5
+    // rounds at 2 per CU (k-tiles of 128): 55.0 -> 51.3 us per call.  4 per
+    // CU (one round) needs <= 128 VGPRs and spilled: 85 us.
+    constexpr size_t BK = 64;
+    const size_t Kp = align_up(KHW * Cp, BK);
     const size_t Ho = (H + 2 * pad - K_h) / stride + 1, Wo = (W + 2 * pad - K_w) / stride + 1;
     const size_t P = N * Ho * Wo;
     LANCIUS_REQUIRE(Kp < (1u << 30) && P < (1u << 31) && N * H * W * Cp < ((size_t)1 << 40) && C_out < (1u << 30),
@@ -642,8 +648,8 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     p.tiles_n = (uint32_t)((P + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: too many tiles");
-    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, 2, 2, 128, true>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream,
-                       p);
+    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, 2, 2, (int)BK, true, 3>), dim3((unsigned)grid), dim3(kThreads), 0,
+                       ctx->stream, p);
     return check_launch("conv2d_i8_mfma");
 }
 
