@@ -352,9 +352,10 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
                 // The next tile's LDS store (see the k-major path below for
                 // why mid-tile): a quarter in with one k-group (4096^3:
                 // 133.5 -> 134.7 TFLOP/s against halfway; three quarters in
-                // measured 132.4), halfway with k-groups (a quarter in cost
-                // 1024^3 6%).
-                if (kp == (KG == 1 && KH >= 8 ? KH / 4 - 1 : KH > 1 ? KH / 2 - 1 : 0)) {
+                // measured 132.4); with k-groups after the first k-pair of
+                // four (2048^3: 115.3 -> 117.7) and halfway through eight (a
+                // quarter in cost 1024^3 6%).
+                if (kp == (KG == 1 && KH >= 8 ? KH / 4 - 1 : KH == 4 ? 0 : KH > 1 ? KH / 2 - 1 : 0)) {
                     __builtin_amdgcn_sched_barrier(0);
                     store_tile(cur ^ 1, (kt + 1) * BK);
                     __builtin_amdgcn_sched_barrier(0);
