@@ -341,7 +341,7 @@ __global__ void __launch_bounds__(256) dgrad_direct(float* __restrict__ dx, cons
 // with dY[co][P] = dy[n][co][ho][wo] and X[j][P] the im2col value
 // x[n][ci][ho*stride-pad+kh][wo*stride-pad+kw] (0 outside the image).  The
 // reduction over P (N*H_out*W_out, ~10^5 at the conv config) is split across
-// blockIdx.y; partials are added in split order by wgrad_reduce.
+// blockIdx.y; wgrad_reduce adds the partials in a fixed order.
 struct WgradParams {
     float* dw;
     float* ws;
@@ -488,19 +488,23 @@ __global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
     }
 }
 
-// One wave per weight: lane l adds splits l, l+64, ... in order, then a fixed
-// butterfly over the lanes (deterministic, and the split partials of one
-// weight are read by 64 lanes at once instead of one thread).
+// A workgroup per 64 consecutive weights: lane l of wave g adds splits g,
+// g+4, g+8, ... of weight l in order (a wave reads 256 contiguous bytes of a
+// split's partials), then wave 0 adds the four sums in wave order: a fixed
+// order, so results are identical from run to run.  (One wave per weight,
+// its lanes on 64 splits a whole partial array apart, read a cache line per
+// 4-byte value: 29.7 us for 85 splits of 73728 weights.)
 __global__ void __launch_bounds__(256) wgrad_reduce(float* __restrict__ dw, const float* __restrict__ ws, size_t n,
                                                     int splits) {
-    const size_t i = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (i >= n) return;
+    __shared__ float part[4][64];
+    const int lane = threadIdx.x & 63, g = threadIdx.x >> 6;
+    const size_t i = (size_t)blockIdx.x * 64 + lane;
     float s = 0.0f;
-    for (int k = lane; k < splits; k += 64) s += ws[(size_t)k * n + i];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
-    if (lane == 0) dw[i] = s;
+    if (i < n)
+        for (int k = g; k < splits; k += 4) s += ws[(size_t)k * n + i];
+    part[g][lane] = s;
+    __syncthreads();
+    if (g == 0 && i < n) dw[i] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
 }
 
 template <int BM, int BN, int KH_T, int KW_T>
@@ -729,8 +733,8 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     if (int rc = check_launch("conv2d_wgrad_mfma")) return rc;
     if (p.splits > 1) {
         const size_t n = C_out * J;
-        LANCIUS_REQUIRE((n + 3) / 4 < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: %zu weights", n);
-        hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, ctx->stream, dw,
+        LANCIUS_REQUIRE((n + 63) / 64 < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_bwd_weight: %zu weights", n);
+        hipLaunchKernelGGL(wgrad_reduce, dim3((unsigned)((n + 63) / 64)), dim3(256), 0, ctx->stream, dw,
                            (const float*)p.ws, n, p.splits);
         if (int rc = check_launch("conv2d_wgrad_reduce")) return rc;
     }
