@@ -60,22 +60,27 @@ def log(msg: str) -> None:
     sys.stderr.flush()
 
 
-def time_steps(dev: Device, fn, steps: int, warmup: int, settle_ms: float = 40.0) -> float:
+def time_steps(dev: Device, fn, steps: int, warmup: int, settle_ms: float = 40.0, info: dict | None = None) -> float:
     """Average ms per call of fn over `steps` calls, HIP events on the
     context stream, after `warmup` untimed calls and, with settle_ms > 0,
     enough further untimed calls for about settle_ms of GPU work (at most
     500): the clock drops while the host prepares a case and settles again
-    over tens of milliseconds of load."""
+    over tens of milliseconds of load.  info["settle_launches"] receives the
+    number of those further calls."""
     for _ in range(warmup):
         fn()
     dev.synchronize()
+    settled = 0
     if settle_ms > 0:
         dev.timer_start()
         fn()
         one = max(dev.timer_stop(), 1e-3)
-        for _ in range(min(500, int(settle_ms / one))):
+        settled = 1 + min(500, int(settle_ms / one))
+        for _ in range(settled - 1):
             fn()
         dev.synchronize()
+    if info is not None:
+        info["settle_launches"] = settled
     dev.timer_start()
     for _ in range(steps):
         fn()
@@ -84,11 +89,11 @@ def time_steps(dev: Device, fn, steps: int, warmup: int, settle_ms: float = 40.0
     return ms / steps
 
 
-def gemm_case(dev, M, K, N, seed, steps, warmup, settle_ms=40.0):
+def gemm_case(dev, M, K, N, seed, steps, warmup, settle_ms=40.0, info=None):
     A = dev.upload(prng.normal(seed, (M, K)))
     B = dev.upload(prng.normal(seed + 1000, (K, N)))
     Cb = dev.alloc(M * N * 4)
-    ms = time_steps(dev, lambda: dev.gemm(Cb, A, B, M, K, N), steps, warmup, settle_ms)
+    ms = time_steps(dev, lambda: dev.gemm(Cb, A, B, M, K, N), steps, warmup, settle_ms, info)
     for b in (A, B, Cb):
         b.free()
     flops = 2.0 * M * N * K
@@ -557,9 +562,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     # The GPU clock settles over the first ~50 ms of MFMA load (4096^3 launches
-    # shorten from 1.27 to 1.10 ms); 50 untimed launches put the timed ones
-    # in the steady state.
-    ap.add_argument("--warmup", type=int, default=50)
+    # shorten from 1.27 to 1.02 ms); the headline adds untimed launches for
+    # about 60 ms of load after the warm-up, so the timed ones run in the
+    # steady state whatever --warmup is.
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no other configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     args = ap.parse_args()
@@ -582,8 +588,12 @@ def main() -> int:
     measured_mfma = dev.peak_probe("mfma")
     measured_hbm = dev.peak_probe("hbm")
     log("headline gemm 4096^3")
-    # the headline does exactly args.warmup untimed launches before the timed ones
-    ms, flops, nbytes = gemm_case(dev, M, K, N, 43, args.steps, args.warmup, settle_ms=0.0)
+    # args.warmup untimed launches, then further untimed launches for about
+    # 60 ms of MFMA load (counted in the JSON as settle_launches): with few
+    # warm-up launches the timed ones would otherwise run during the clock
+    # ramp (1.3 ms per launch at the start against 1.02 ms settled).
+    head_info: dict = {}
+    ms, flops, nbytes = gemm_case(dev, M, K, N, 43, args.steps, args.warmup, settle_ms=60.0, info=head_info)
     gflops = flops / (ms * 1e-3) / 1e9
     traffic = None
     if TRAFFIC_FILE.exists():
@@ -596,6 +606,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "settle_launches": head_info.get("settle_launches", 0),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -29,6 +29,10 @@ int ok() {
 }
 
 int from_hip(hipError_t e, const char* what) {
+    // HIP keeps the failure as the thread's pending "last error"; reset it so
+    // the launch check of the next, unrelated call (hipGetLastError after
+    // <<<>>>) does not report it again.
+    (void)hipGetLastError();
     int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? LANCIUS_HIP_ERR_OOM
                                                                            : LANCIUS_HIP_ERR_INTERNAL;
     return set_error(code, "%s: %s", what, hipGetErrorString(e));
@@ -112,6 +116,9 @@ int counters(lancius_hip_ctx* ctx, size_t n, unsigned** out) {
 }
 
 int bind_device(lancius_hip_ctx* ctx) {
+    // A failure of a HIP call whose status was ignored (cleanup paths) must
+    // not surface in this call's launch checks.
+    (void)hipGetLastError();
     int cur = -1;
     LANCIUS_HIP_TRY(hipGetDevice(&cur), "hipGetDevice");
     if (cur != ctx->device) LANCIUS_HIP_TRY(hipSetDevice(ctx->device), "hipSetDevice");

@@ -693,6 +693,32 @@ int lancius_device_program_info_get(const lancius_device_program* p, lancius_dev
  * hidden and logit tensors each read once by the next launch, small enough
  * for lancius_hip_mlp2_f32 (M <= 64, N2 <= 64, M*N1 <= 16384,
  * N1*N2 <= 8192): one launch instead of up to three dependent ones. */
+/* Launches read tensors through their buffer owner (RESHAPE/FLATTEN
+ * aliases resolved), so a node with one direct consumer can still be read
+ * by several launches: h -> FLATTEN -> {GEMM, RELU}.  The buffer of `r` may
+ * only be fused away when exactly one operand slot of the whole launch list
+ * reads it, that slot is in launch `reader`, and no alias of `r` is a sink
+ * (a caller may download sinks). */
+static int sole_reader(const lancius_device_program* p, const cstate* c, uint32_t nl, uint32_t r,
+                       uint32_t reader) {
+    uint32_t reads = 0;
+    for (uint32_t s = 0; s < nl; s++) {
+        const launch_t* L = &p->launches[s];
+        for (uint32_t k = 0; k < L->count; k++)
+            for (int j = 0; j < 6; j++)
+                if (L->m[k].in[j] == r) {
+                    if (s != reader) return 0;
+                    reads++;
+                }
+    }
+    if (reads != 1) return 0;
+    for (uint32_t i = 0; i < c->g->node_count; i++) {
+        const lancius_node* n = c->g->nodes[i];
+        if (n->id != r && c->root[n->id] == r && c->consumers[n->id] == 0) return 0;
+    }
+    return 1;
+}
+
 static uint32_t fuse_mlp2(lancius_device_program* p, const cstate* c, uint32_t nl) {
     for (uint32_t s = 0; s + 1 < nl; s++) {
         launch_t* A = &p->launches[s];
@@ -700,14 +726,15 @@ static uint32_t fuse_mlp2(lancius_device_program* p, const cstate* c, uint32_t n
         if (A->kind != L_GEMM || B->kind != L_GEMM || A->count != 1 || B->count != 1) continue;
         if (A->ta || A->tb || A->i8 || A->has_res || B->ta || B->tb || B->i8 || B->has_res || B->act) continue;
         const uint32_t h = A->m[0].out, y = B->m[0].out;
-        if (B->m[0].in[0] != h || B->m[0].in[1] == h || c->consumers[h] != 1) continue;
+        if (B->m[0].in[0] != h || B->m[0].in[1] == h || c->consumers[h] != 1 || !sole_reader(p, c, nl, h, s + 1))
+            continue;
         const size_t M = A->d[0], K1 = A->d[1], N1 = A->d[2], N2 = B->d[2];
         if (B->d[0] != M || B->d[1] != N1 || M > 64 || N2 > 64 || M * N1 > 16384 || N1 * N2 > 8192) continue;
         int sm = 0;
         if (s + 2 < nl) {
             const launch_t* S = &p->launches[s + 2];
             sm = S->kind == L_SOFTMAX && S->count == 1 && S->m[0].in[0] == y && c->consumers[y] == 1 &&
-                 S->d[0] == M && S->d[1] == N2;
+                 S->d[0] == M && S->d[1] == N2 && sole_reader(p, c, nl, y, s + 2);
         }
         launch_t F = *A;
         F.kind = L_MLP2;

@@ -303,6 +303,20 @@ static void attempt_drop(attempt* a) {
 
 static size_t enc_size(lancius_dtype enc) { return enc == LANCIUS_DTYPE_INT8 ? 1 : enc == LANCIUS_DTYPE_FP32 ? 4 : 8; }
 
+/* A node's element count must be representable: the product of its dims,
+ * formed with overflow checks, at most 2^40 (so byte counts of any dtype
+ * stay far inside size_t).  A crafted shape such as [2^32, 2^32], recorded
+ * or derived by a builder from such inputs, would otherwise wrap to a small
+ * count that passes every later size check. */
+#define MAX_NODE_ELEMS ((uint64_t)1 << 40)
+static int shape_ok(const lancius_node* n) {
+    uint64_t e = 1;
+    if (n->ndim > 4) return 0;
+    for (uint8_t d = 0; d < n->ndim; d++)
+        if (__builtin_mul_overflow(e, (uint64_t)n->shape[d], &e)) return 0;
+    return e <= MAX_NODE_ELEMS;
+}
+
 /* Payload of a weighted node: host copy (lazy == 0) or a map entry. */
 static int take_weights(attempt* a, lancius_node* n, lancius_dtype node_dtype, double scale, lancius_dtype enc,
                         const uint8_t* src, uint64_t file_offset, uint64_t e, int lazy) {
@@ -368,6 +382,7 @@ static int parse_records(const uint8_t* base, size_t file_size, size_t rec_begin
         int skipped = 0;
         lancius_node* n = build(a->g, &r, id_map, &skipped);
         if (!n && !skipped) goto bad;
+        if (n && !shape_ok(n)) goto bad;
         if (n) {
             n->kernel_h = r.meta[0];
             n->kernel_w = r.meta[1];

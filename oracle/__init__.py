@@ -160,16 +160,20 @@ def conv2d(x, w, stride=1, pad=0, relu=False, images: tuple[int, int] | None = N
 
 
 def attention(q, k, v, causal=True, scale=None, batches: tuple[int, int] | None = None,
-              rows: tuple[int, int] | None = None) -> np.ndarray:
-    """q, k, v: [B, S, H, D] (or [S, H, D] for batch 1)."""
+              rows: tuple[int, int] | None = None, row_list=None) -> np.ndarray:
+    """q, k, v: [B, S, H, D] (or [S, H, D] for batch 1).  Query rows [i0, i1)
+    (all by default), or the rows listed in row_list, of batches [b0, b1);
+    other rows are 0."""
     squeeze = q.ndim == 3
     q, k, v = (_d(t)[None] if squeeze else _d(t) for t in (q, k, v))
     B, S, H, D = q.shape
     scale = 1.0 / np.sqrt(D) if scale is None else scale
     b0, b1 = batches if batches else (0, B)
-    i0, i1 = rows if rows else (0, S)
+    ranges = [(int(r), int(r) + 1) for r in row_list] if row_list is not None else [rows if rows else (0, S)]
     out = np.zeros_like(q)
-    lib().oracle_attention(_p(out), _p(q), _p(k), _p(v), B, S, H, D, int(bool(causal)), float(scale), b0, b1, i0, i1)
+    for i0, i1 in ranges:
+        lib().oracle_attention(_p(out), _p(q), _p(k), _p(v), B, S, H, D, int(bool(causal)), float(scale), b0, b1,
+                               i0, i1)
     return out[0] if squeeze else out
 
 

@@ -312,10 +312,11 @@ def test_block_small_every_node(dev):
 
 
 @pytest.mark.parametrize("noncausal", [False, True])
-def test_block_config_branch0(dev, noncausal):
-    """Full config block (B=4, S=1024, d=1024, H=16, F=4096) on the device;
-    sequence 0 checked against the fp64 oracle executor on a batch-1 graph
-    with the same weights."""
+def test_block_config_first_and_last_sequence(dev, noncausal):
+    """Full config block (B=4, S=1024, d=1024, H=16, F=4096) on the device.
+    Sequences 0 and 3 (member 0 and the last member of every grouped
+    launch) are checked against the fp64 oracle executor on a batch-1 graph
+    with the same weights; every sink is NaN-free."""
     lib = graph_lib()
     pl = Planned(graphs.build_block(lib, noncausal=noncausal))
     feeds = _block_feeds(pl.bg)
@@ -323,13 +324,59 @@ def test_block_config_branch0(dev, noncausal):
     prog = pl.program(dev)
     _feed(prog, pl.bg, feeds)
     prog.run()
-    got = prog.download(pl.bg.node("y0"))
+    got = {name: prog.download(pl.bg.node(name)) for name in pl.bg.outputs}
     info = prog.info()
     prog.close()
     pl.close()
-    one = Planned(graphs.build_block(lib, batch=1, noncausal=noncausal), plan=False)
-    f1 = {n: feeds[n] for n in one.bg.inputs}
-    ref = one.oracle_run(f1)[one.bg.node("y0").contents.id]
-    one.close()
-    assert oracle.normwise_error(got.ravel(), ref) <= oracle.tolerance(4096)
     assert info["launches"] == 13, info
+    for name, y in got.items():
+        assert np.isfinite(y).all(), name
+    one = Planned(graphs.build_block(lib, batch=1, noncausal=noncausal), plan=False)
+    for seq in (0, 3):
+        f1 = {n: feeds[n] for n in one.bg.inputs if n != "x0"}
+        f1["x0"] = feeds[f"x{seq}"]
+        ref = one.oracle_run(f1)[one.bg.node("y0").contents.id]
+        assert oracle.normwise_error(got[f"y{seq}"].ravel(), ref) <= oracle.tolerance(4096), seq
+    one.close()
+
+
+# ---- aliases between fused launches ------------------------------------------------
+
+
+@pytest.mark.parametrize("second", ["relu", "sink_alias"])
+def test_mlp_chain_not_fused_through_shared_alias(dev, second):
+    """h = ReLU(x.W1 + b1) reaches the second MATMUL through a RESHAPE that a
+    second node also reads (a RELU, or a RESHAPE left as a sink).  h's
+    buffer is read by more than the second GEMM, so the two-layer chain must
+    not be fused into one launch: every sink comes back right."""
+    lib = graph_lib()
+    bg = graphs.BuiltGraph(lib, lib.lancius_graph_create())
+    M, K1, N1, N2 = 8, 32, 64, 10
+    shapes = {"x": (M, K1), "W1": (K1, N1), "b1": (1, N1), "W2": (N1, N2), "b2": (1, N2)}
+    for name, shp in shapes.items():
+        bg.nodes[name] = lib.lancius_input(bg.g, *shp)
+        bg.inputs.append(name)
+    n = bg.nodes
+    a1 = lib.lancius_add(bg.g, lib.lancius_matmul(bg.g, n["x"], n["W1"]), lib.lancius_broadcast(bg.g, n["b1"], M, N1))
+    h = lib.lancius_relu(bg.g, a1)
+    hr = lib.lancius_reshape(bg.g, h, 2, M, N1, 0, 0)
+    a2 = lib.lancius_add(bg.g, lib.lancius_matmul(bg.g, hr, n["W2"]), lib.lancius_broadcast(bg.g, n["b2"], M, N2))
+    sm = lib.lancius_softmax(bg.g, a2)
+    other = lib.lancius_relu(bg.g, hr) if second == "relu" else lib.lancius_reshape(bg.g, hr, 2, M, N1, 0, 0)
+    n.update(softmax=sm, other=other)
+    bg.outputs = ["softmax", "other"]
+    pl = Planned(bg)
+    feeds = {"x": prng.uniform(71, (M, K1), -1.0, 1.0), "W1": prng.normal(72, (K1, N1), 0, 0.2),
+             "b1": prng.normal(73, (1, N1), 0, 0.2), "W2": prng.normal(74, (N1, N2), 0, 0.2),
+             "b2": prng.normal(75, (1, N2), 0, 0.2)}
+    case(f"mlp chain with a shared alias of h, second reader {second}")
+    prog = pl.program(dev)
+    _feed(prog, pl.bg, feeds)
+    prog.run()
+    hid = oracle.relu(oracle.matmul(feeds["x"], feeds["W1"]) + feeds["b1"].astype(np.float64))
+    ref_sm = oracle.softmax(oracle.matmul(hid, feeds["W2"]) + feeds["b2"].astype(np.float64))
+    assert oracle.normwise_error(prog.download(sm).reshape(M, N2), ref_sm) <= oracle.tolerance(K1)
+    assert oracle.normwise_error(prog.download(other).reshape(M, N1), hid) <= oracle.tolerance(K1)
+    assert prog.info()["launches"] >= 2
+    prog.close()
+    pl.close()

@@ -20,7 +20,11 @@ def _upload(dev, *arrs):
     return [dev.upload(np.ascontiguousarray(a, dtype=np.float32)) for a in arrs]
 
 
-def _gemm_case(dev, M, K, N, seed, bias=False, act=ACT_NONE, residual=False, rows=None):
+def _gemm_case(dev, M, K, N, seed, bias=False, act=ACT_NONE, residual=False, rows=None, row_list=None):
+    """C is filled with NaN before the call, so an element the kernel never
+    writes shows up in the finite check of the caller.  rows = (r0, r1) or
+    row_list = [r, ...] restricts the fp64 oracle (and the returned pair) to
+    those rows of the full product."""
     A = prng.normal(seed, (M, K))
     B = prng.normal(seed + 1000, (K, N))
     bv = prng.normal(seed + 2000, (N,)) if bias else None
@@ -29,10 +33,20 @@ def _gemm_case(dev, M, K, N, seed, bias=False, act=ACT_NONE, residual=False, row
     dbias = dev.upload(bv) if bias else None
     dR = dev.upload(R) if residual else None
     dC = dev.alloc(M * N * 4)
+    dev.fill(dC, float("nan"), M * N)
     case(f"gemm M={M} K={K} N={N} bias={bias} act={act} res={residual}")
     dev.gemm(dC, dA, dB, M, K, N, bias=dbias, act=act, residual=dR)
     got = dev.download(dC, (M, N))
-    ref = oracle.matmul(A, B, rows=rows)
+    assert np.isfinite(got).all(), f"{np.count_nonzero(~np.isfinite(got))} elements of C not written"
+    if row_list is not None:
+        sel = np.asarray(row_list)
+        ref = oracle.matmul(A[sel], B)
+        Rs = R[sel] if residual else None
+    else:
+        ref = oracle.matmul(A, B, rows=rows)
+        sel = slice(*rows) if rows else slice(None)
+        ref = ref[sel]
+        Rs = R[sel] if residual else None
     if bias:
         ref = ref + bv.astype(np.float64)[None, :]
     if act == ACT_RELU:
@@ -40,12 +54,21 @@ def _gemm_case(dev, M, K, N, seed, bias=False, act=ACT_NONE, residual=False, row
     elif act == ACT_GELU:
         ref = oracle.gelu(ref)
     if residual:
-        ref = ref + R.astype(np.float64)
-    sel = slice(*rows) if rows else slice(None)
+        ref = ref + Rs.astype(np.float64)
     for b in (dA, dB, dC, dbias, dR):
         if b is not None:
             b.free()
-    return got[sel], ref[sel]
+    return got[sel], ref
+
+
+def band_rows(M, band=128, per_band=2):
+    """per_band rows of every band-row tile band of an M-row output, at
+    offsets that differ from band to band, plus the first and last row."""
+    rows = {0, M - 1}
+    for b in range((M + band - 1) // band):
+        for j in range(per_band):
+            rows.add(min(M - 1, b * band + (37 * b + 61 * j + 5) % band))
+    return sorted(rows)
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 1, 1), (7, 13, 5), (64, 784, 256), (64, 256, 10), (130, 70, 200),
@@ -69,9 +92,12 @@ def test_gemm_config_full(dev, M, K, N):
 
 
 @pytest.mark.parametrize("n", [2048, 4096])
-def test_gemm_config_sampled_rows(dev, n):
-    # Rows [n-96, n) are exact fp64 oracle rows of the full product.
-    got, ref = _gemm_case(dev, n, n, n, seed=43, rows=(n - 96, n))
+def test_gemm_config_every_band(dev, n):
+    """Every element is written (NaN-filled C comes back finite), and two
+    rows of every 128-row tile band, across all columns (so every 128x128
+    tile), are exact fp64 oracle rows of the full product: the XCD
+    renumbering and raster of the tiles cannot drop or misplace a tile."""
+    got, ref = _gemm_case(dev, n, n, n, seed=43, row_list=band_rows(n))
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(n)
 
 
@@ -86,9 +112,9 @@ def test_gemm_config_sampled_rows(dev, n):
 def test_gemm_tile_paths(dev, M, K, N):
     """Each default tile path of the GEMM dispatch (k-groups reduce their
     accumulators through LDS before the epilogue), with bias, GELU and a
-    residual; 96 sampled rows for the two largest products."""
-    rows = (M - 96, M) if M * N >= 4_000_000 else None
-    got, ref = _gemm_case(dev, M, K, N, seed=120 + M + N, bias=True, act=ACT_GELU, residual=True, rows=rows)
+    residual; rows of every 128-row band for the two largest products."""
+    rows = band_rows(M) if M * N >= 4_000_000 else None
+    got, ref = _gemm_case(dev, M, K, N, seed=120 + M + N, bias=True, act=ACT_GELU, residual=True, row_list=rows)
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
 
 
@@ -214,21 +240,26 @@ def test_kernel_matmul_f32_bridge(dev):
 # ---- attention ---------------------------------------------------------------
 
 
-def _attn_case(dev, B, S, H, D, causal, seed, batches=None, rows=None):
+def _attn_case(dev, B, S, H, D, causal, seed, batches=None, rows=None, row_list=None):
+    """The output is NaN-filled before the call and must come back finite
+    everywhere; the oracle covers batches [b0, b1) and rows (r0, r1) or the
+    rows in row_list (all by default)."""
     q = prng.normal(seed, (B, S, H, D))
     k = prng.normal(seed + 1, (B, S, H, D))
     v = prng.normal(seed + 2, (B, S, H, D))
     dq, dk, dv = _upload(dev, q, k, v)
     do = dev.alloc(q.nbytes)
+    dev.fill(do, float("nan"), q.size)
     case(f"attention B={B} S={S} H={H} D={D} causal={causal}")
     dev.attention(do, dq, dk, dv, B, S, H, D, causal=causal)
     got = dev.download(do, q.shape)
-    ref = oracle.attention(q, k, v, causal=causal, batches=batches, rows=rows)
+    assert np.isfinite(got).all(), f"{np.count_nonzero(~np.isfinite(got))} output elements not written"
+    ref = oracle.attention(q, k, v, causal=causal, batches=batches, rows=rows, row_list=row_list)
     for b in (dq, dk, dv, do):
         b.free()
     bs = slice(*batches) if batches else slice(None)
-    rs = slice(*rows) if rows else slice(None)
-    return got[bs, rs], ref[bs, rs]
+    rs = np.asarray(row_list) if row_list is not None else slice(*rows) if rows else slice(None)
+    return got[bs][:, rs], ref[bs][:, rs]
 
 
 @pytest.mark.parametrize("causal", [True, False])
@@ -241,13 +272,26 @@ def test_attention_shapes(dev, B, S, H, D, causal):
 
 @pytest.mark.parametrize("causal", [True, False])
 def test_attention_config_s512(dev, causal):
-    got, ref = _attn_case(dev, 8, 512, 16, 64, causal, seed=44, batches=(0, 1))
+    """The whole S=512 config (every batch, head and row) against the oracle."""
+    got, ref = _attn_case(dev, 8, 512, 16, 64, causal, seed=44)
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(512)
 
 
+def tile_rows(S, tile=128):
+    """First, last and one varying row of every tile-row query tile."""
+    rows = set()
+    for t in range((S + tile - 1) // tile):
+        lo, hi = t * tile, min(S, (t + 1) * tile) - 1
+        rows.update((lo, hi, min(hi, lo + (29 * t + 11) % tile)))
+    return sorted(rows)
+
+
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention_config_s2048_sampled(dev, causal):
-    got, ref = _attn_case(dev, 8, 2048, 16, 64, causal, seed=44, batches=(7, 8), rows=(1792, 2048))
+def test_attention_config_s2048_every_tile(dev, causal):
+    """S=2048: every element written, and three rows of every 128-query tile
+    of every (batch, head) against the oracle, so the causal task order
+    (long and short tiles paired, XCD-spread) cannot drop a tile."""
+    got, ref = _attn_case(dev, 8, 2048, 16, 64, causal, seed=44, row_list=tile_rows(2048))
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(2048)
 
 
@@ -289,14 +333,17 @@ def test_attention_grouped(dev):
 
 
 def _conv_case(dev, N, C_in, H, W, C_out, KH, KW, stride, pad, relu, seed, images=None):
+    """The output is NaN-filled before the call and must come back finite."""
     x = prng.normal(seed, (N, C_in, H, W))
     w = prng.normal(seed + 1, (C_out, C_in, KH, KW), std=float(np.sqrt(2.0 / (KH * KW * C_in))))
     dx, dw = _upload(dev, x, w)
     Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
     do = dev.alloc(N * C_out * Ho * Wo * 4)
+    dev.fill(do, float("nan"), N * C_out * Ho * Wo)
     case(f"conv N={N} C_in={C_in} {H}x{W} C_out={C_out} k={KH}x{KW} s={stride} p={pad} relu={relu}")
     dev.conv2d(do, dx, dw, None, N, C_in, H, W, C_out, KH, KW, stride, pad, ACT_RELU if relu else ACT_NONE)
     got = dev.download(do, (N, C_out, Ho, Wo))
+    assert np.isfinite(got).all(), f"{np.count_nonzero(~np.isfinite(got))} output elements not written"
     ref = oracle.conv2d(x, w, stride, pad, relu, images=images)
     for b in (dx, dw, do):
         b.free()
@@ -318,8 +365,9 @@ def test_conv_shapes(dev, N, C_in, H, W, C_out, KH, KW, stride, pad, relu):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(C_in * KH * KW)
 
 
-def test_conv_config_sampled(dev):
-    got, ref = _conv_case(dev, 32, 64, 56, 56, 128, 3, 3, 1, 1, True, seed=45, images=(30, 32))
+def test_conv_config_full(dev):
+    """The whole conv config (all 32 images, every channel and pixel)."""
+    got, ref = _conv_case(dev, 32, 64, 56, 56, 128, 3, 3, 1, 1, True, seed=45)
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(64 * 9)
 
 

@@ -357,6 +357,48 @@ def test_malformed_headers_and_records(tmp_path):
     assert lib.lancius_get_error() == -8  # LANCIUS_ERROR_IO
 
 
+def test_overflowing_shapes_fail(tmp_path):
+    """Element counts are formed with overflow checks: a record of shape
+    [2^32, 2^32] (whose product wraps to 0 in 64 bits) and a MATMUL whose
+    derived shape overflows both fail the load, with or without a payload."""
+    lib = graph_lib()
+    recs = mf.read_records(data_of("test_model"), 9)
+    # test_model: x, W (weights), MATMUL(x, W), RELU(MATMUL)
+
+    def fails(r) -> bool:
+        """The loader refuses the v10 file, or (the layout is found by
+        parsing) reads it as some other v9 record stream in which every node
+        has a representable element count and none has the crafted dims."""
+        p = tmp_path / "o.lancius"
+        p.write_bytes(mf.write_records(r, 10))
+        g = load(p)
+        if not g:
+            return True
+        ok = True
+        for i in range(g.contents.node_count):
+            n = g.contents.nodes[i].contents
+            dims = [int(d) for d in n.shape[:n.ndim]]
+            ok = ok and float(np.prod([float(d) for d in dims])) <= 2.0 ** 40 and max(dims, default=0) < 1 << 32
+        lib.lancius_graph_destroy(g)
+        return ok
+
+    r = [dict(x) for x in recs]
+    r[0]["shape"] = (1 << 32, 1 << 32, 0, 0)  # x, no payload
+    assert fails(r)
+    r = [dict(x) for x in recs]
+    r[1].update(shape=(1 << 32, 1 << 32, 0, 0), weights=np.zeros(0))  # W: wrapped count 0 would match 0 bytes
+    assert fails(r)
+    r = [dict(x) for x in recs]
+    r[0]["shape"] = (1 << 33, 20, 0, 0)  # x [2^33, 20] and W [20, 2^33] are representable ...
+    r[1].update(shape=(20, 1 << 33, 0, 0), weights=None)
+    assert fails(r)  # ... the MATMUL the builder derives, [2^33, 2^33], is not
+    p = tmp_path / "ok.lancius"
+    p.write_bytes(mf.write_records([dict(x) for x in recs], 10))
+    g = load(p)
+    assert g and g.contents.node_count == len(recs)
+    lib.lancius_graph_destroy(g)
+
+
 def test_unknown_op_is_skipped_and_its_readers_fail(tmp_path):
     recs = mf.read_records(data_of("test_model"), 9)
     # test_model: x, W (weights), MATMUL(x, W), RELU(MATMUL)
