@@ -82,6 +82,21 @@ LANCIUS_HIP_EXPORT int lancius_hip_gemm_f32(lancius_hip_ctx* ctx, float* C, cons
                                             size_t M, size_t K, size_t N,
                                             const float* bias, int act, const float* residual);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc): lancius_hip_gemm_f32 with its split-K partial sums in a
+ * fixed scratch array of LANCIUS_HIP_NOALLOC_SCRATCH_BYTES inside the
+ * library, one per GPU, held until the process ends; it never grows the
+ * context workspace and calls no hipMalloc or hipFree.  Same kernels and same
+ * split choice as lancius_hip_gemm_f32, hence the same bits.  A shape whose
+ * partial sums would exceed the scratch returns -3 before anything is
+ * launched.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (two streams or two host threads) race, so order them. */
+#define LANCIUS_HIP_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+LANCIUS_HIP_EXPORT int lancius_hip_gemm_f32_noalloc(lancius_hip_ctx* ctx, float* C, const float* A, const float* B,
+                                                    size_t M, size_t K, size_t N,
+                                                    const float* bias, int act, const float* residual);
+
 /* `count` independent GEMMs of one shape in a single launch (the branches of
  * one scheduler wave).  Every array is a host array of `count` device
  * pointers; B[g] and bias[g] may repeat; bias and residual may be NULL (the

@@ -17,6 +17,7 @@
 //  * Workgroup ids are renumbered XCD-contiguously and rastered in groups of
 //    tile-rows so that each XCD's L2 sees a compact set of A/B panels.
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -720,12 +721,56 @@ void launch_skinny(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
+// Split-K partial sums of lancius_hip_gemm_f32_noalloc.  Each GPU the library
+// runs on holds its own copy of this array until the process ends.  Host code
+// never uses the name itself (on the host it only stands for the symbol):
+// the per-device address comes from hipGetSymbolAddress, below.
+constexpr size_t kNoallocScratchBytes = LANCIUS_HIP_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, by device index
+
+// Address of the calling device's scratch; resolved once per device, with
+// that device current (the caller has bound ctx->device).
+int noalloc_scratch(lancius_hip_ctx* ctx, void** out) {
+    *out = nullptr;
+    LANCIUS_REQUIRE(ctx->device >= 0 && ctx->device < kMaxScratchDevices, LANCIUS_HIP_ERR_UNSUPPORTED,
+                    "gemm_f32_noalloc: device index %d beyond %d", ctx->device, kMaxScratchDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[ctx->device]) {
+        void* p = nullptr;
+        LANCIUS_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        LANCIUS_REQUIRE(p != nullptr, LANCIUS_HIP_ERR_INTERNAL, "gemm_f32_noalloc: no address for the scratch");
+        g_scratch_ptr[ctx->device] = p;
+    }
+    *out = g_scratch_ptr[ctx->device];
+    return 0;
+}
+
+// Device memory for `bytes` of split-K partials: the context workspace (grown
+// on demand), or, when `fixed` is given, that buffer of `fixed_bytes`, with
+// a clear error when the shape needs more.
+int partials(lancius_hip_ctx* ctx, void* fixed, size_t fixed_bytes, size_t bytes, void** out) {
+    if (!fixed) return workspace(ctx, bytes, out);
+    *out = nullptr;
+    LANCIUS_REQUIRE(bytes <= fixed_bytes, LANCIUS_HIP_ERR_SHAPE,
+                    "gemm_f32_noalloc: this shape splits K into partial sums of %zu bytes, more than the %zu-byte "
+                    "scratch (use lancius_hip_gemm_f32)",
+                    bytes, fixed_bytes);
+    *out = fixed;
+    return 0;
+}
+
 constexpr int kBK = 16;
 constexpr size_t kMaxSplitBytes = (size_t)256 << 20;
 
+// fixed_ws: when not null, split-K partials go there (fixed_bytes long)
+// instead of the context workspace, and nothing is allocated.
 int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
                   const float* const* B, size_t M, size_t K, size_t N, int ta, int tb, const float* const* bias,
-                  int act, const float* const* residual) {
+                  int act, const float* const* residual, void* fixed_ws = nullptr, size_t fixed_bytes = 0) {
     LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm: NULL argument");
     LANCIUS_REQUIRE(count >= 1 && count <= LANCIUS_HIP_MAX_GROUP, LANCIUS_HIP_ERR_SHAPE, "gemm: group count %zu",
                     count);
@@ -769,7 +814,7 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         if (ws_bytes <= kMaxSplitBytes && splits < 65536 && col_blocks < kMaxGridX) {
             if (splits > 1) {
                 void* ws = nullptr;
-                if (int rc = workspace(ctx, ws_bytes, &ws)) return rc;
+                if (int rc = partials(ctx, fixed_ws, fixed_bytes, ws_bytes, &ws)) return rc;
                 p.ws = (float*)ws;
             }
             p.splits = (int)splits;
@@ -852,7 +897,7 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     p.kchunk = (int)(chunk_tiles * bk);
     if (splits > 1) {
         void* ws = nullptr;
-        if (int rc = workspace(ctx, count * splits * M * N * sizeof(float), &ws)) return rc;
+        if (int rc = partials(ctx, fixed_ws, fixed_bytes, count * splits * M * N * sizeof(float), &ws)) return rc;
         p.ws = (float*)ws;
     }
     int rc;
@@ -882,6 +927,20 @@ int lancius_hip_gemm_f32(lancius_hip_ctx* ctx, float* C, const float* A, const f
     const float* s1[1] = {bias};
     const float* r1[1] = {residual};
     return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, 0, 0, s1, act, r1);
+}
+
+int lancius_hip_gemm_f32_noalloc(lancius_hip_ctx* ctx, float* C, const float* A, const float* B, size_t M,
+                                 size_t K, size_t N, const float* bias, int act, const float* residual) {
+    LANCIUS_REQUIRE(ctx != nullptr, LANCIUS_HIP_ERR_NULL_PTR, "gemm_f32_noalloc: NULL context");
+    if (int rc = bind_device(ctx)) return rc;
+    void* ws = nullptr;
+    if (int rc = noalloc_scratch(ctx, &ws)) return rc;
+    float* c1[1] = {C};
+    const float* a1[1] = {A};
+    const float* b1[1] = {B};
+    const float* s1[1] = {bias};
+    const float* r1[1] = {residual};
+    return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, 0, 0, s1, act, r1, ws, kNoallocScratchBytes);
 }
 
 int lancius_hip_gemm_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,

@@ -71,6 +71,7 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_timer_stop.argtypes = [vp, C.POINTER(f32)]
     lib.lancius_hip_gemm_f32.argtypes = [vp, vp, vp, vp, sz, sz, sz, vp, i32, vp]
     lib.lancius_hip_gemm_grouped_f32.argtypes = [vp, sz, vpp, vpp, vpp, sz, sz, sz, vpp, i32, vpp]
+    lib.lancius_hip_gemm_f32_noalloc.argtypes = [vp, vp, vp, vp, sz, sz, sz, vp, i32, vp]
     lib.lancius_hip_conv2d_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, sz, sz, i32]
     lib.lancius_hip_attention_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, sz, sz, i32, f32]
     lib.lancius_hip_attention_grouped_f32.argtypes = [vp, sz, vpp, vpp, vpp, vpp, sz, sz, sz, i32, f32]
