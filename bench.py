@@ -518,6 +518,7 @@ def cpu_baseline(M, K, N, target_s: float = 12.0) -> dict | None:
         pass
     other = {}
     if ref is not None:
+        other.update(cpu_config_baselines(ref))
         for name, builder in (("train_step_mnist_mlp_B64_784x128x10", lambda l: graphs.build_mlp_ce(l)),
                               ("train_step_cifar_cnn_B32", lambda l: graphs.build_cnn_ce(l, batch=32))):
             other[name] = {"step_latency_ms": round(cpu_train_step_ms(ref, builder), 3),
@@ -527,6 +528,118 @@ def cpu_baseline(M, K, N, target_s: float = 12.0) -> dict | None:
             "sample": f"rows 0-{rows - 1} of the {M}x{K}x{N} fp64 product through the "
                       f"{'reference' if kind == 'reference' else 'oracle'} graph MATMUL node (IKJ, 1 thread), "
                       f"{dt:.1f} s on {cpu} ({os.cpu_count()} logical CPUs visible)"}
+
+
+def _omp_threads() -> int:
+    """OpenMP threads the reference's parallel kernels run with here (the
+    reference library and this process share one libgomp)."""
+    try:
+        return int(C.CDLL("libgomp.so.1").omp_get_max_threads())
+    except OSError:
+        return int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+
+
+def _ref_graph_ms(ref, bg, feeds: dict, reps: int) -> float:
+    """Median wall time of lancius_schedule_execute (the reference's scratch
+    arena executor, B/src/runtime/lancius_scheduler.c:311-362) on a graph the
+    reference library built, fresh intermediates each run."""
+    keep = {k: np.ascontiguousarray(v, dtype=np.float64) for k, v in feeds.items()}
+    for name in bg.inputs:
+        bg.node(name).contents.runtime_data = keep[name].ctypes.data_as(C.POINTER(C.c_double))
+    sched = ref.lancius_ir_schedule(bg.g)
+    arena = ref.lancius_arena_create(512 << 20)
+    times = []
+    for _ in range(reps):
+        g = bg.g.contents
+        for i in range(g.node_count):
+            n = g.nodes[i]
+            if n.contents.op not in (abi.OP["INPUT"], abi.OP["CONST"]):
+                n.contents.runtime_data = None
+        t0 = time.perf_counter()
+        ref.lancius_schedule_execute(sched, arena)
+        times.append(time.perf_counter() - t0)
+        ref.lancius_arena_reset(arena)
+    ref.lancius_arena_destroy(arena)
+    ref.lancius_schedule_destroy(sched)
+    for name in bg.inputs:
+        bg.node(name).contents.runtime_data = None
+    return sorted(times)[len(times) // 2] * 1e3
+
+
+def cpu_config_baselines(ref) -> dict:
+    """The reference's own CPU path for every other config, on this host:
+    graph MATMUL nodes (one thread by construction, lancius_scheduler.c:226-233),
+    kernel_attention and kernel_conv2d_relu_fwd (OpenMP, all threads this
+    process has), and the MLP and transformer-block graphs through the
+    reference's executor.  Sizes that would take tens of seconds run on a
+    stated sample; the extrapolation is stated with them."""
+    threads = _omp_threads()
+    D = C.POINTER(C.c_double)
+    out = {}
+    for name, (m, k, n) in (("gemm_1024", (1024, 1024, 1024)), ("gemm_2048", (2048, 2048, 2048)),
+                            ("gemm_16x4096x4096", (16, 4096, 4096))):
+        log(f"cpu {name}")
+        bg = graphs.BuiltGraph(ref, ref.lancius_graph_create())
+        a, b = bg.nodes["a"], bg.nodes["b"] = ref.lancius_input(bg.g, m, k), ref.lancius_input(bg.g, k, n)
+        bg.inputs = ["a", "b"]
+        ref.lancius_matmul(bg.g, a, b)
+        ms = _ref_graph_ms(ref, bg, {"a": prng.normal(43, (m, k)), "b": prng.normal(1043, (k, n))},
+                           1 if m * n * k >= 1 << 33 else 3)
+        bg.destroy()
+        out[name] = {"ms": round(ms, 2), "GFLOP/s": round(2.0 * m * n * k / ms / 1e6, 3), "cores": 1,
+                     "note": "reference graph MATMUL node (IKJ, one thread), whole product"}
+    for S in (512, 2048):
+        log(f"cpu attention S={S}")
+        B, H, Dh = 8, 16, 64
+        seqs = B if S == 512 else 1
+        q, k, v = (np.ascontiguousarray(prng.normal(44 + j, (seqs, S, H, Dh)), dtype=np.float64) for j in range(3))
+        o = np.zeros_like(q)
+        t0 = time.perf_counter()
+        for b in range(seqs):
+            ref.kernel_attention(o[b].ctypes.data_as(D), q[b].ctypes.data_as(D), k[b].ctypes.data_as(D),
+                                 v[b].ctypes.data_as(D), S, H, Dh)
+        dt = (time.perf_counter() - t0) * B / seqs
+        flops = 4.0 * B * H * Dh * S * (S + 1) / 2
+        out[f"attention_B8_H16_D64_S{S}_causal"] = {
+            "ms": round(dt * 1e3, 1), "GFLOP/s": round(flops / dt / 1e9, 3), "cores": threads,
+            "note": ("kernel_attention (causal; masked keys still computed, so the non-causal variant, "
+                     "which has no reference kernel, costs the same), one call per sequence, "
+                     + ("all 8 sequences" if seqs == B else "1 of the 8 sequences timed, x8"))}
+    log("cpu conv")
+    x = np.ascontiguousarray(prng.normal(45, (32, 64, 56, 56)), dtype=np.float64)
+    w = np.ascontiguousarray(prng.normal(145, (128, 64, 3, 3), std=float(np.sqrt(2.0 / 576))), dtype=np.float64)
+    y = np.zeros((32, 128, 56, 56))
+    t0 = time.perf_counter()
+    ref.kernel_conv2d_relu_fwd(y.ctypes.data_as(D), x.ctypes.data_as(D), w.ctypes.data_as(D), 32, 64, 56, 56, 128,
+                               3, 3, 1, 1)
+    dt = time.perf_counter() - t0
+    out["conv3x3_N32_64to128_56x56_relu"] = {
+        "ms": round(dt * 1e3, 1), "GFLOP/s": round(2.0 * 32 * 128 * 56 * 56 * 64 * 9 / dt / 1e9, 3),
+        "cores": threads, "note": "kernel_conv2d_relu_fwd, whole batch"}
+    log("cpu mlp graph")
+    bg = graphs.build_mlp(ref)
+    feeds = {"x": prng.uniform(1, (64, 784), -1.0, 1.0), "W1": prng.normal(2, (784, 256), 0, 0.02),
+             "b1": np.zeros((1, 256)), "W2": prng.normal(3, (256, 10), 0, 0.02), "b2": np.zeros((1, 10))}
+    ms = _ref_graph_ms(ref, bg, feeds, 7)
+    bg.destroy()
+    out["mlp_graph_64x784x256x10"] = {"fwd_latency_ms": round(ms, 3), "cores": threads,
+                                      "note": "reference executor on the reference-built graph, median of 7"}
+    log("cpu transformer block (one sequence)")
+    bg = graphs.build_block(ref, batch=1)
+    feeds = {}
+    for i, name in enumerate(bg.inputs):
+        shape = abi.node_shape(bg.node(name))
+        feeds[name] = (prng.normal(1000 + i, shape) if name.startswith("x")
+                       else 1.0 + prng.normal(1000 + i, shape, 0, 0.02) if name in ("g1", "g2")
+                       else prng.normal(1000 + i, shape, 0, 0.02))
+    ms = _ref_graph_ms(ref, bg, feeds, 1)
+    bg.destroy()
+    out["transformer_block_B4_S1024_d1024_H16_F4096"] = {
+        "fwd_latency_ms": round(4 * ms, 1), "one_sequence_ms": round(ms, 1), "cores": threads,
+        "GFLOP/s": round(27.925 / ms * 1e3, 3),
+        "note": ("reference executor on the reference-built block graph with batch 1 (one of the 4 "
+                 "sequences, which share only the weights), x4; MATMUL nodes one thread, attention OpenMP")}
+    return out
 
 
 def cpu_train_step_ms(ref, builder) -> float:
@@ -587,6 +700,7 @@ def main() -> int:
     log("device ceilings")
     measured_mfma = dev.peak_probe("mfma")
     measured_hbm = dev.peak_probe("hbm")
+    measured_hbm_read = dev.peak_probe("hbm_read")
     log("headline gemm 4096^3")
     # args.warmup untimed launches, then further untimed launches for about
     # 60 ms of MFMA load (counted in the JSON as settle_launches): with few
@@ -621,7 +735,8 @@ def main() -> int:
                      "frac_of_measured_peak": round(flops / (ms * 1e-3) / 1e12 / measured_mfma, 4)},
         "device_ceilings": {"fp32_mfma_TFLOPs_measured": round(measured_mfma, 2),
                             "fp32_mfma_TFLOPs_spec": PEAK_FP32_MFMA,
-                            "hbm_copy_GBs_measured": round(measured_hbm, 1), "hbm_GBs_spec": PEAK_HBM},
+                            "hbm_copy_GBs_measured": round(measured_hbm, 1),
+                            "hbm_read_GBs_measured": round(measured_hbm_read, 1), "hbm_GBs_spec": PEAK_HBM},
     }
     extra = {}
     load_dir, load_files = None, None

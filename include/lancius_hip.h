@@ -392,8 +392,9 @@ LANCIUS_HIP_EXPORT int lancius_hip_upload_file(lancius_hip_ctx* ctx, const char*
 /* Measured ceilings of this device, for roofline reporting:
  *   which = 0: fp32 matrix rate, TFLOP/s (independent back-to-back
  *              v_mfma_f32_32x32x2_f32 on every SIMD, no memory traffic);
- *   which = 1: HBM copy bandwidth, GB/s (float4 copy of 2 x 1 GiB,
- *              bytes read + written).
+ *   which = 1: HBM copy bandwidth, GB/s (float4 copy of 1 GiB into another
+ *              1 GiB, bytes read + written);
+ *   which = 2: HBM read bandwidth, GB/s (float4 reads of 1 GiB).
  * Allocates and frees its own buffers; takes a few hundred milliseconds. */
 LANCIUS_HIP_EXPORT int lancius_hip_peak_probe(lancius_hip_ctx* ctx, int which, double* result);
 

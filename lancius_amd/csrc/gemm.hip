@@ -35,12 +35,21 @@ struct GemmParams {
     int act;
     uint32_t tiles_m, tiles_n;
     float* ws;   // split-K partials [count][splits][M][N]
+    unsigned* counters;  // fused skinny split-K: one arrival counter per (group, column block), zero between launches
     int splits;  // K ranges (blockIdx.y), 1 = no split
     int kchunk;  // K per split, a multiple of the k-tile
     int map2d;   // 1: each XCD owns a 2-D block of tiles (tiles_m % 2 == 0, tiles_n % 4 == 0)
 };
 
 constexpr int kThreads = 256;
+// s_waitcnt operand that waits for vmcnt 0 and leaves expcnt / lgkmcnt alone.
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
+// Cache-policy operand of the raw buffer load/store builtins on gfx950: sc1,
+// device scope (the access is coherent across the XCDs' L2 caches).
+constexpr int kCachePolicySc1 = 16;
+// Fourth word of a raw buffer resource on gfx9 (32-bit data format).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // SPLIT: the workgroup reduces K range [y*kchunk, (y+1)*kchunk) and stores its
 // raw partial sums; splitk_reduce adds the partials in order y = 0, 1, ...
@@ -476,48 +485,89 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
 // Skinny GEMM (M <= 16*MT): the product is bound by reading B once from
 // HBM (or, for tiny problems, by latency), so the kernel is organised around
 // that stream.
-//  * A workgroup owns 64 columns and a K slice of 256 rows; each wave takes
-//    64 of those rows and issues all 16 of its B loads before the first MFMA.
-//  * VB: every B load is a float4: lane l reads row k0 + 4s + l/16, columns
-//    c0 + 4(l%16) .. +3, so 16 lanes stream 256 contiguous bytes of a row and
-//    a wave keeps 16 KB in flight.  Otherwise (N % 4 != 0 or unaligned B) the
-//    same four columns are four bounds-checked scalar loads.  Component j
-//    feeds its own v_mfma_f32_16x16x4_f32, whose column index l%16 then stands
-//    for column c0 + 4(l%16) + j; the four MFMAs cover the 64 columns.
-//  * TA: A is given transposed ([K][M]); the staging loop then walks m fastest.
-//  * The four waves' partial sums are added through LDS in wave order (the
-//    buffer that held the A slice is reused).  With several K slices each
-//    workgroup stores its partial and a reduce kernel adds them in slice order
-//    (deterministic).  An in-kernel "last workgroup reduces" scheme would need
-//    agent-scope fences, which on this part write back and invalidate the
-//    per-XCD L2 - measured 4x slower.
-template <int MT, bool VB, bool TA>
-__global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
-    constexpr int KS = 256;         // K rows per workgroup
-    constexpr int KW = KS / 4;      // per wave
-    constexpr int STEPS = KW / 4;   // MFMA k-steps per wave
+//  * A workgroup of WAVES waves owns 64 columns and a K slice of 64*WAVES
+//    rows; each wave takes 64 of those rows.  Lane l's MFMA k index l/16
+//    stands for rows k0 + 16(l/16) + s of step s = 0..15 (any bijection of k
+//    serves, as long as A and B use the same one), so a lane's A operands
+//    for the whole slice are 16 consecutive floats of one A row: four float4
+//    loads from L2 (A is small and shared), no LDS staging, no barrier.
+//  * A loads are issued first, then all 16 B loads, and step s waits only
+//    for its own B rows: the MFMAs run while later rows are in flight
+//    instead of after the whole slice has arrived (the grid is one round of
+//    workgroups, so there is nothing else to overlap them with).
+//  * VB: every B load is a float4: lane l reads row k0 + 16(l/16) + s,
+//    columns c0 + 4(l%16) .. +3, so 16 lanes stream 256 contiguous bytes of a
+//    row and a wave keeps 16 KB in flight.  Otherwise (N % 4 != 0 or
+//    unaligned B) the same four columns are four bounds-checked scalar loads.
+//    Component j feeds its own v_mfma_f32_16x16x4_f32, whose column index
+//    l%16 then stands for column c0 + 4(l%16) + j; the four MFMAs cover the
+//    64 columns.
+//  * VA: A rows are float4-loadable (K % 4 == 0, A 16-byte aligned, not
+//    transposed); otherwise the 16 values are scalar loads (TA: A given
+//    transposed, [K][M]).
+//  * The waves' partial sums are added through LDS in wave order.  With
+//    several K slices each workgroup stores its partial sums, and the K
+//    slices are added in slice order y = 0, 1, ... (fixed, so results are
+//    run-to-run identical):
+//    - FUSED: in this launch, by the workgroup that arrives last at its
+//      column block's counter.  An agent-scope release/acquire pair would
+//      write back and invalidate the XCD's whole L2 (measured 4x slower), so
+//      the partials instead go through the point of coherence: stored with
+//      the device-scope cache policy (sc1: written through), the wave waits
+//      for the stores to complete before the counter's atomic add, and the
+//      last workgroup reads them back with sc1 loads (which miss in L2).
+//      Workgroup-scope fences order the accesses; the sc1 accesses carry the
+//      coherence.  The last workgroup resets the counter to zero, so
+//      counters are zero between launches.
+//    - otherwise a separate reduce kernel adds them (splitk_reduce*).
+template <int MT, bool VB, bool TA, bool FUSED, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) gemm_skinny_f32(const GemmParams p) {
+    constexpr int KW = 64;           // K rows per wave
+    constexpr int KS = KW * WAVES;   // K rows per workgroup
+    constexpr int STEPS = 16;        // MFMA k-steps per wave
     constexpr int ROWS = 16 * MT;
-    constexpr int A_FLOATS = ROWS * (KS + 1);
-    constexpr int RED_FLOATS = 4 * ROWS * 64;
-    __shared__ __attribute__((aligned(16))) float smem[A_FLOATS > RED_FLOATS ? A_FLOATS : RED_FLOATS];
-    float(*As)[KS + 1] = (float(*)[KS + 1])smem;
-    float(*red)[ROWS][64] = (float(*)[ROWS][64])smem;
+    constexpr int NT = 64 * WAVES;   // threads
+    __shared__ __attribute__((aligned(16))) float red[WAVES][ROWS][64];
 
     const int g = blockIdx.z, split = blockIdx.y, cb = blockIdx.x;
     const int M = p.M, N = p.N, K = p.K;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int kl = lane >> 4, cq = lane & 15;
+    const int kq = lane >> 4, cq = lane & 15;
     const int c0 = cb * 64;
     const int col4 = c0 + 4 * cq;
-    const int kslice = split * KS;
-    const int kw0 = kslice + wave * KW;
+    const int kbase = split * KS + wave * KW + 16 * kq;  // this lane's 16 rows: kbase .. kbase + 15
     const float* __restrict__ A = p.A[g];
     const float* __restrict__ B = p.B[g];
 
+    // A operands first: av[t][s] = A[16t + cq][kbase + s]
+    float av[MT][STEPS];
+    const bool va = !TA && (K % 4 == 0) && (((uintptr_t)A & 15u) == 0);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int m = 16 * t + cq;
+        if (va) {
+#pragma unroll
+            for (int q = 0; q < STEPS / 4; ++q) {
+                const int k = kbase + 4 * q;
+                const f32x4 x = (m < M && k < K) ? *(const f32x4*)(A + (size_t)m * K + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+                av[t][4 * q] = x.x;
+                av[t][4 * q + 1] = x.y;
+                av[t][4 * q + 2] = x.z;
+                av[t][4 * q + 3] = x.w;
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                const int k = kbase + s;
+                av[t][s] = (m < M && k < K) ? (TA ? A[(size_t)k * M + m] : A[(size_t)m * K + k]) : 0.0f;
+            }
+        }
+    }
+    // then every B load of the slice
     f32x4 bv[STEPS];
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
-        const int k = kw0 + 4 * s + kl;
+        const int k = kbase + s;
         if constexpr (VB) {
             bv[s] = (k < K && col4 < N) ? *(const f32x4*)(B + (size_t)k * N + col4) : f32x4{0.f, 0.f, 0.f, 0.f};
         } else {
@@ -527,28 +577,6 @@ __global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
                           (kin && col4 + 2 < N) ? row[col4 + 2] : 0.f, (kin && col4 + 3 < N) ? row[col4 + 3] : 0.f};
         }
     }
-    constexpr int A_PER = ROWS * KS / 256;
-    float as[A_PER];
-#pragma unroll
-    for (int i = 0; i < A_PER; ++i) {
-        const int idx = tid + 256 * i;
-        if constexpr (!TA) {
-            const int r = idx / KS, c = idx % KS;
-            as[i] = (r < M && kslice + c < K) ? A[(size_t)r * K + kslice + c] : 0.0f;
-        } else {
-            const int c = idx / ROWS, r = idx % ROWS;
-            as[i] = (r < M && kslice + c < K) ? A[(size_t)(kslice + c) * M + r] : 0.0f;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < A_PER; ++i) {
-        const int idx = tid + 256 * i;
-        if constexpr (!TA)
-            As[idx / KS][idx % KS] = as[i];
-        else
-            As[idx % ROWS][idx / ROWS] = as[i];
-    }
-    __syncthreads();
 
     f32x4 acc[MT][4];
 #pragma unroll
@@ -559,58 +587,133 @@ __global__ void __launch_bounds__(256) gemm_skinny_f32(const GemmParams p) {
     for (int s = 0; s < STEPS; ++s) {
 #pragma unroll
         for (int t = 0; t < MT; ++t) {
-            const float av = As[16 * t + cq][wave * KW + 4 * s + kl];
-            acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].x, acc[t][0], 0, 0, 0);
-            acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].y, acc[t][1], 0, 0, 0);
-            acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].z, acc[t][2], 0, 0, 0);
-            acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[s].w, acc[t][3], 0, 0, 0);
+            acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t][s], bv[s].x, acc[t][0], 0, 0, 0);
+            acc[t][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t][s], bv[s].y, acc[t][1], 0, 0, 0);
+            acc[t][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t][s], bv[s].z, acc[t][2], 0, 0, 0);
+            acc[t][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[t][s], bv[s].w, acc[t][3], 0, 0, 0);
         }
     }
-    __syncthreads();  // the A slice is no longer read: its LDS becomes red
     // Accumulator (t, j), register r of lane l: row 16t + 4(l/16) + r,
     // column c0 + 4(l%16) + j.
 #pragma unroll
     for (int t = 0; t < MT; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-            *(f32x4*)&red[wave][16 * t + 4 * kl + r][4 * cq] =
+            *(f32x4*)&red[wave][16 * t + 4 * kq + r][4 * cq] =
                 f32x4{acc[t][0][r], acc[t][1][r], acc[t][2][r], acc[t][3][r]};
     __syncthreads();
+
+    // ROWS x 16 float4 groups of the tile; thread e4 < ROWS*16 owns group e4
+    // (row e4 / 16, columns c0 + 4 (e4 % 16) .. +3); the waves' sums are
+    // added in wave order.
+    constexpr int GROUPS = ROWS * 16;
+    static_assert(GROUPS <= NT, "one float4 group per thread");
+    const int e4 = tid;
+    const int row = e4 / 16, col = c0 + 4 * (e4 % 16), cc = 4 * (e4 % 16);
+    const bool mine = e4 < GROUPS && row < M && col < N;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (mine) {
+        v = *(const f32x4*)&red[0][row][cc];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) v += *(const f32x4*)&red[w][row][cc];
+    }
 
     const float* __restrict__ bias = p.bias[g];
     const float* __restrict__ R = p.R[g];
     float* __restrict__ C = p.C[g];
     const size_t MN = (size_t)M * N;
+    if constexpr (FUSED) {
+        if (p.splits > 1) {
+            // This group's partials as a raw buffer: 16-byte loads and stores
+            // with the device-scope cache policy (sc1) the coherence needs.
+            const __amdgpu_buffer_rsrc_t part = __builtin_amdgcn_make_buffer_rsrc(
+                p.ws + (size_t)g * p.splits * MN, 0, (int)(p.splits * MN * sizeof(float)), kBufferRsrcWord3);
+            // 1. this K slice's partial sums, written through to the point of coherence
+            if (mine) {
+                const int off = (int)(((size_t)split * MN + (size_t)row * N + col) * sizeof(float));
+                if constexpr (VB) {
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), part, off, 0, kCachePolicySc1);
+                } else {
+                    const float o[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-        const int e4 = tid + 256 * i;
-        const int row = e4 / 16, col = c0 + 4 * (e4 % 16);
-        if (row >= M || col >= N) continue;
-        const int cc = 4 * (e4 % 16);
-        f32x4 v = *(const f32x4*)&red[0][row][cc];
-        v += *(const f32x4*)&red[1][row][cc];
-        v += *(const f32x4*)&red[2][row][cc];
-        v += *(const f32x4*)&red[3][row][cc];
-        float o[4] = {v.x, v.y, v.z, v.w};
-        float* dst = p.splits == 1 ? C + (size_t)row * N + col
-                                   : p.ws + ((size_t)g * p.splits + split) * MN + (size_t)row * N + col;
-        if (p.splits == 1) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (!VB && col + j >= N) break;
-                float y = o[j] + (bias ? bias[col + j] : 0.0f);
-                y = apply_act(y, p.act);
-                if (R) y += R[(size_t)row * N + col + j];
-                o[j] = y;
+                    for (int j = 0; j < 4; ++j)
+                        if (col + j < N)
+                            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, o[j]), part,
+                                                                  off + 4 * j, 0, kCachePolicySc1);
+                }
             }
-        }
-        if constexpr (VB) {
-            *(f32x4*)dst = f32x4{o[0], o[1], o[2], o[3]};
-        } else {
+            // 2. arrival: the stores have completed before the counter moves
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            __shared__ int s_last;
+            __syncthreads();
+            unsigned* ctr = p.counters + (size_t)g * gridDim.x + cb;
+            if (tid == 0)
+                s_last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                         (unsigned)(p.splits - 1);
+            __syncthreads();
+            if (!s_last) return;
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            // 3. the last workgroup adds the slices in order y = 0, 1, ... and
+            //    runs the epilogue; the loads of up to kLoadsInFlight slices
+            //    are issued before the first add
+            if (mine) {
+                constexpr int kLoadsInFlight = 16;
+                const int off = (int)(((size_t)row * N + col) * sizeof(float));
+                const int step = (int)(MN * sizeof(float));
+                f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int y0 = 0; y0 < p.splits; y0 += kLoadsInFlight) {
+                    f32x4 pv[kLoadsInFlight];
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (col + j < N) dst[j] = o[j];
+                    for (int t = 0; t < kLoadsInFlight; ++t) {
+                        if (y0 + t >= p.splits) break;
+                        if constexpr (VB) {
+                            pv[t] = __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(part, off + (y0 + t) * step, 0,
+                                                                             kCachePolicySc1));
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                pv[t][j] = col + j < N ? __builtin_bit_cast(
+                                                             float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                        part, off + (y0 + t) * step + 4 * j, 0,
+                                                                        kCachePolicySc1))
+                                                       : 0.0f;
+                        }
+                    }
+#pragma unroll
+                    for (int t = 0; t < kLoadsInFlight; ++t) {
+                        if (y0 + t >= p.splits) break;
+                        sum = (y0 + t == 0) ? pv[t] : sum + pv[t];
+                    }
+                }
+                v = sum;
+            }
+            if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+    }
+    if (!mine) return;
+    float o[4] = {v.x, v.y, v.z, v.w};
+    const bool direct = p.splits == 1 || FUSED;
+    float* dst = direct ? C + (size_t)row * N + col
+                        : p.ws + ((size_t)g * p.splits + split) * MN + (size_t)row * N + col;
+    if (direct) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (!VB && col + j >= N) break;
+            float y = o[j] + (bias ? bias[col + j] : 0.0f);
+            y = apply_act(y, p.act);
+            if (R) y += R[(size_t)row * N + col + j];
+            o[j] = y;
+        }
+    }
+    if constexpr (VB) {
+        *(f32x4*)dst = f32x4{o[0], o[1], o[2], o[3]};
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (col + j < N) dst[j] = o[j];
     }
 }
 
@@ -711,31 +814,65 @@ int launch_by_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec, int 
     }
 }
 
-template <int MT, bool TA>
-void launch_skinny(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb) {
-    if (vb)
-        hipLaunchKernelGGL((gemm_skinny_f32<MT, true, TA>), grid, dim3(256), 0, ctx->stream, p);
+template <int MT, bool TA, int WAVES>
+void launch_skinny(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb, bool fused) {
+    const dim3 block(64 * WAVES);
+    if (vb && fused)
+        hipLaunchKernelGGL((gemm_skinny_f32<MT, true, TA, true, WAVES>), grid, block, 0, ctx->stream, p);
+    else if (fused)
+        hipLaunchKernelGGL((gemm_skinny_f32<MT, false, TA, true, WAVES>), grid, block, 0, ctx->stream, p);
+    else if (vb)
+        hipLaunchKernelGGL((gemm_skinny_f32<MT, true, TA, false, WAVES>), grid, block, 0, ctx->stream, p);
     else
-        hipLaunchKernelGGL((gemm_skinny_f32<MT, false, TA>), grid, dim3(256), 0, ctx->stream, p);
+        hipLaunchKernelGGL((gemm_skinny_f32<MT, false, TA, false, WAVES>), grid, block, 0, ctx->stream, p);
+}
+
+// Waves per workgroup of the skinny kernel (K rows per workgroup = 64 x waves).
+template <bool TA>
+void launch_skinny_waves(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb, bool fused, int mt,
+                         int waves) {
+    if (mt == 1) {
+        if (waves == 16) return launch_skinny<1, TA, 16>(ctx, p, grid, vb, fused);
+        if (waves == 8) return launch_skinny<1, TA, 8>(ctx, p, grid, vb, fused);
+        return launch_skinny<1, TA, 4>(ctx, p, grid, vb, fused);
+    }
+    return launch_skinny<2, TA, 8>(ctx, p, grid, vb, fused);  // 32 rows x 16 float4 groups: 512 threads
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
 
-// Split-K partial sums of lancius_hip_gemm_f32_noalloc.  Each GPU the library
-// runs on holds its own copy of this array until the process ends.  Host code
-// never uses the name itself (on the host it only stands for the symbol):
-// the per-device address comes from hipGetSymbolAddress, below.
+// Scratch of lancius_hip_gemm_f32_noalloc: split-K partial sums, then
+// kScratchCounters arrival counters (zero between launches).  Each GPU the
+// library runs on holds its own copy of this array until the process ends.
+// Host code never uses the name itself (on the host it only stands for the
+// symbol): the per-device address comes from hipGetSymbolAddress, below.
 constexpr size_t kNoallocScratchBytes = LANCIUS_HIP_NOALLOC_SCRATCH_BYTES;
+constexpr size_t kScratchCounters = 16384;
+constexpr size_t kScratchPartialBytes = kNoallocScratchBytes - kScratchCounters * sizeof(unsigned);
 static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
 
 constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch`, by device index
 
-// Address of the calling device's scratch; resolved once per device, with
-// that device current (the caller has bound ctx->device).
-int noalloc_scratch(lancius_hip_ctx* ctx, void** out) {
-    *out = nullptr;
+__global__ void zero_words(unsigned* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// Where a GEMM puts split-K partial sums and arrival counters: the context's
+// workspace and counters (grown on demand), or a fixed buffer.
+struct SplitStore {
+    void* partials = nullptr;  // null: the context workspace
+    size_t partial_bytes = 0;
+    unsigned* counters = nullptr;
+    size_t n_counters = 0;
+};
+
+// The calling device's scratch; its address is resolved (and its counters
+// cleared by a kernel, not a memset, so a caller may capture the call) once
+// per device, with that device current (the caller has bound ctx->device).
+int noalloc_scratch(lancius_hip_ctx* ctx, SplitStore* out) {
     LANCIUS_REQUIRE(ctx->device >= 0 && ctx->device < kMaxScratchDevices, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "gemm_f32_noalloc: device index %d beyond %d", ctx->device, kMaxScratchDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -743,34 +880,50 @@ int noalloc_scratch(lancius_hip_ctx* ctx, void** out) {
         void* p = nullptr;
         LANCIUS_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
         LANCIUS_REQUIRE(p != nullptr, LANCIUS_HIP_ERR_INTERNAL, "gemm_f32_noalloc: no address for the scratch");
+        hipLaunchKernelGGL(zero_words, dim3(16), dim3(256), 0, ctx->stream,
+                           (unsigned*)((char*)p + kScratchPartialBytes), kScratchCounters);
+        if (int rc = check_launch("zero_words")) return rc;
         g_scratch_ptr[ctx->device] = p;
     }
-    *out = g_scratch_ptr[ctx->device];
+    out->partials = g_scratch_ptr[ctx->device];
+    out->partial_bytes = kScratchPartialBytes;
+    out->counters = (unsigned*)((char*)out->partials + kScratchPartialBytes);
+    out->n_counters = kScratchCounters;
     return 0;
 }
 
-// Device memory for `bytes` of split-K partials: the context workspace (grown
-// on demand), or, when `fixed` is given, that buffer of `fixed_bytes`, with
-// a clear error when the shape needs more.
-int partials(lancius_hip_ctx* ctx, void* fixed, size_t fixed_bytes, size_t bytes, void** out) {
-    if (!fixed) return workspace(ctx, bytes, out);
+// Device memory for `bytes` of split-K partials: the context workspace, or
+// the fixed buffer of `st`, with a clear error when the shape needs more.
+int partials(lancius_hip_ctx* ctx, const SplitStore* st, size_t bytes, void** out) {
+    if (!st || !st->partials) return workspace(ctx, bytes, out);
     *out = nullptr;
-    LANCIUS_REQUIRE(bytes <= fixed_bytes, LANCIUS_HIP_ERR_SHAPE,
+    LANCIUS_REQUIRE(bytes <= st->partial_bytes, LANCIUS_HIP_ERR_SHAPE,
                     "gemm_f32_noalloc: this shape splits K into partial sums of %zu bytes, more than the %zu-byte "
                     "scratch (use lancius_hip_gemm_f32)",
-                    bytes, fixed_bytes);
-    *out = fixed;
+                    bytes, st->partial_bytes);
+    *out = st->partials;
+    return 0;
+}
+
+// `n` zero arrival counters: the context's, or those of `st`.
+int arrival_counters(lancius_hip_ctx* ctx, const SplitStore* st, size_t n, unsigned** out) {
+    if (!st || !st->partials) return counters(ctx, n, out);
+    *out = nullptr;
+    LANCIUS_REQUIRE(n <= st->n_counters, LANCIUS_HIP_ERR_SHAPE,
+                    "gemm_f32_noalloc: %zu column blocks need more than the scratch's %zu counters", n,
+                    st->n_counters);
+    *out = st->counters;
     return 0;
 }
 
 constexpr int kBK = 16;
 constexpr size_t kMaxSplitBytes = (size_t)256 << 20;
 
-// fixed_ws: when not null, split-K partials go there (fixed_bytes long)
-// instead of the context workspace, and nothing is allocated.
+// fixed: when not null, split-K partials and arrival counters go to its
+// buffers instead of the context's, and nothing is allocated.
 int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,
                   const float* const* B, size_t M, size_t K, size_t N, int ta, int tb, const float* const* bias,
-                  int act, const float* const* residual, void* fixed_ws = nullptr, size_t fixed_bytes = 0) {
+                  int act, const float* const* residual, const SplitStore* fixed = nullptr) {
     LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm: NULL argument");
     LANCIUS_REQUIRE(count >= 1 && count <= LANCIUS_HIP_MAX_GROUP, LANCIUS_HIP_ERR_SHAPE, "gemm: group count %zu",
                     count);
@@ -803,28 +956,40 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     p.act = act;
 
     // M <= 32 (B not transposed): the B-streaming skinny kernel, one
-    // workgroup per (64 columns, 256-row K slice).  Measured on MI355X it
-    // beats the tiled kernel up to M = 32 (16x4096x4096: 22 vs 34 us;
+    // workgroup per (64 columns, 64 x waves K rows), the K slices added
+    // inside the launch.  Measured on MI355X it beats the tiled kernel up to
+    // M = 32 (16x4096x4096: 22 vs 34 us with the first skinny design;
     // 32x2048x120: 10.6 vs 13.6 us) and loses at M = 64 with four row tiles
     // (64x4096x4096: 43 vs 38 us; 64x784x256: 13.0 vs 11.8 us).
     if (M <= 32 && !tb && tune("gemm_skinny", 1)) {
-        const size_t splits = (K + 255) / 256;
+        const int mt = M <= 16 ? 1 : 2;
+        // 8 waves (512-row K slices) measured best on MI355X: 16x4096x4096
+        // 15.9 us as 4 or 16 waves 16.4 / 15.9, 16x8192x8192 51.5 against
+        // 57.3 / 53.1, 8x1024x768 7.8 against 8.7 / 8.6
+        int waves = tune("gemm_skinny_waves", 8);
+        waves = mt == 2 ? 8 : waves >= 16 ? 16 : waves >= 8 ? 8 : 4;
+        const size_t splits = (K + 64 * waves - 1) / (64 * waves);
         const size_t col_blocks = (N + 63) / 64;
         const size_t ws_bytes = splits > 1 ? count * splits * M * N * sizeof(float) : 0;
         if (ws_bytes <= kMaxSplitBytes && splits < 65536 && col_blocks < kMaxGridX) {
+            // the K slices are added inside the launch (see gemm_skinny_f32);
+            // LANCIUS_HIP_TUNE=gemm_skinny_fused=0 keeps the separate reduce
+            const bool fused = splits > 1 && tune("gemm_skinny_fused", 1);
             if (splits > 1) {
                 void* ws = nullptr;
-                if (int rc = partials(ctx, fixed_ws, fixed_bytes, ws_bytes, &ws)) return rc;
+                if (int rc = partials(ctx, fixed, ws_bytes, &ws)) return rc;
                 p.ws = (float*)ws;
+                if (fused)
+                    if (int rc = arrival_counters(ctx, fixed, count * col_blocks, &p.counters)) return rc;
             }
             p.splits = (int)splits;
             const dim3 grid((unsigned)col_blocks, (unsigned)splits, (unsigned)count);
-            if (M <= 16)
-                ta ? launch_skinny<1, true>(ctx, p, grid, vb) : launch_skinny<1, false>(ctx, p, grid, vb);
+            if (ta)
+                launch_skinny_waves<true>(ctx, p, grid, vb, fused, mt, waves);
             else
-                ta ? launch_skinny<2, true>(ctx, p, grid, vb) : launch_skinny<2, false>(ctx, p, grid, vb);
+                launch_skinny_waves<false>(ctx, p, grid, vb, fused, mt, waves);
             if (int rc = check_launch("gemm_skinny_f32")) return rc;
-            if (splits > 1) {
+            if (splits > 1 && !fused) {
                 if (vb) {
                     const size_t total4 = count * M * N / 4;
                     hipLaunchKernelGGL(splitk_reduce_vec4,
@@ -897,7 +1062,7 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     p.kchunk = (int)(chunk_tiles * bk);
     if (splits > 1) {
         void* ws = nullptr;
-        if (int rc = partials(ctx, fixed_ws, fixed_bytes, count * splits * M * N * sizeof(float), &ws)) return rc;
+        if (int rc = partials(ctx, fixed, count * splits * M * N * sizeof(float), &ws)) return rc;
         p.ws = (float*)ws;
     }
     int rc;
@@ -933,14 +1098,14 @@ int lancius_hip_gemm_f32_noalloc(lancius_hip_ctx* ctx, float* C, const float* A,
                                  size_t K, size_t N, const float* bias, int act, const float* residual) {
     LANCIUS_REQUIRE(ctx != nullptr, LANCIUS_HIP_ERR_NULL_PTR, "gemm_f32_noalloc: NULL context");
     if (int rc = bind_device(ctx)) return rc;
-    void* ws = nullptr;
-    if (int rc = noalloc_scratch(ctx, &ws)) return rc;
+    SplitStore st;
+    if (int rc = noalloc_scratch(ctx, &st)) return rc;
     float* c1[1] = {C};
     const float* a1[1] = {A};
     const float* b1[1] = {B};
     const float* s1[1] = {bias};
     const float* r1[1] = {residual};
-    return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, 0, 0, s1, act, r1, ws, kNoallocScratchBytes);
+    return gemm_dispatch(ctx, 1, c1, a1, b1, M, K, N, 0, 0, s1, act, r1, &st);
 }
 
 int lancius_hip_gemm_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* C, const float* const* A,

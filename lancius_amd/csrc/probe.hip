@@ -1,5 +1,5 @@
 // Device ceilings for roofline reporting: the sustained fp32 MFMA rate and
-// the HBM copy bandwidth of this GPU (lancius_hip_peak_probe).
+// the HBM copy and read bandwidths of this GPU (lancius_hip_peak_probe).
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -32,16 +32,38 @@ __global__ void __launch_bounds__(256) mfma_rate(float* out, int iters) {
     if (s == 1234.5f) out[blockIdx.x * blockDim.x + threadIdx.x] = s;  // keeps the loop alive
 }
 
-// Four float4 loads in flight per thread before the stores; n4 % (4 * grid) == 0.
-__global__ void __launch_bounds__(256) copy_f4(f32x4* __restrict__ dst, const f32x4* __restrict__ src, size_t n4) {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i + 3 * stride < n4; i += 4 * stride) {
-        const f32x4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
-        dst[i] = a;
-        dst[i + stride] = b;
-        dst[i + 2 * stride] = c;
-        dst[i + 3 * stride] = d;
+// Streaming probes: every workgroup walks its own contiguous chunk of
+// per_wg float4s with kInFlight loads in flight per thread (per_wg is a
+// multiple of kInFlight * 256).  Measured on MI355X this pattern beats a
+// grid-stride walk (1 GiB read 6.1 against 5.0 TB/s; the grid-stride copy
+// with 4 loads in flight read 4.4 TB/s).
+constexpr int kInFlight = 8;
+
+__global__ void __launch_bounds__(256) copy_f4(f32x4* __restrict__ dst, const f32x4* __restrict__ src,
+                                               size_t per_wg) {
+    const size_t base = (size_t)blockIdx.x * per_wg + threadIdx.x;
+    for (size_t i = 0; i < per_wg; i += kInFlight * 256) {
+        f32x4 v[kInFlight];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) v[u] = src[base + i + u * 256];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) __builtin_nontemporal_store(v[u], dst + base + i + u * 256);
     }
+}
+
+// Read-only stream; one float per thread is stored so the loads stay live.
+__global__ void __launch_bounds__(256) read_f4(float* __restrict__ out, const f32x4* __restrict__ src,
+                                               size_t per_wg) {
+    const size_t base = (size_t)blockIdx.x * per_wg + threadIdx.x;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    for (size_t i = 0; i < per_wg; i += kInFlight * 256) {
+        f32x4 v[kInFlight];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) v[u] = src[base + i + u * 256];
+#pragma unroll
+        for (int u = 0; u < kInFlight; ++u) a += v[u];
+    }
+    out[(size_t)blockIdx.x * 256 + threadIdx.x] = a.x + a.y + a.z + a.w;
 }
 
 }  // namespace
@@ -51,7 +73,7 @@ using namespace lancius;
 
 extern "C" int lancius_hip_peak_probe(lancius_hip_ctx* ctx, int which, double* result) {
     LANCIUS_REQUIRE(ctx && result, LANCIUS_HIP_ERR_NULL_PTR, "peak_probe: NULL argument");
-    LANCIUS_REQUIRE(which == 0 || which == 1, LANCIUS_HIP_ERR_UNSUPPORTED, "peak_probe: which=%d", which);
+    LANCIUS_REQUIRE(which >= 0 && which <= 2, LANCIUS_HIP_ERR_UNSUPPORTED, "peak_probe: which=%d", which);
     if (int rc = bind_device(ctx)) return rc;
     hipDeviceProp_t prop;
     LANCIUS_HIP_TRY(hipGetDeviceProperties(&prop, ctx->device), "hipGetDeviceProperties");
@@ -85,25 +107,35 @@ extern "C" int lancius_hip_peak_probe(lancius_hip_ctx* ctx, int which, double* r
         const double flops = (double)blocks * 4 /*waves*/ * iters * kChains * 32.0 * 32.0 * 2.0 * 2.0;
         if (!rc) *result = flops / (ms * 1e-3) / 1e12;
     } else {
+        // 1 GiB, four times the 256 MB last-level cache: HBM, not cache, bandwidth
         const size_t bytes = (size_t)1 << 30;
+        const unsigned blocks = 2048;
+        const size_t per_wg = bytes / 16 / blocks;  // 32768 float4s, a multiple of kInFlight * 256
         void *a = nullptr, *b = nullptr;
         hipError_t e = hipMalloc(&a, bytes);
-        if (e == hipSuccess) e = hipMalloc(&b, bytes);
+        if (e == hipSuccess) e = hipMalloc(&b, which == 1 ? bytes : (size_t)blocks * 256 * sizeof(float));
+        if (e == hipSuccess) e = hipMemsetAsync(a, 0, bytes, ctx->stream);
+        auto launch = [&] {
+            if (which == 1)
+                hipLaunchKernelGGL(copy_f4, dim3(blocks), dim3(256), 0, ctx->stream, (f32x4*)b, (const f32x4*)a,
+                                   per_wg);
+            else
+                hipLaunchKernelGGL(read_f4, dim3(blocks), dim3(256), 0, ctx->stream, (float*)b, (const f32x4*)a,
+                                   per_wg);
+        };
         if (e == hipSuccess) {
-            const size_t n4 = bytes / 16;
-            const unsigned blocks = 4096;  // n4 = 2^26 is a multiple of 4 * 4096 * 256
-            hipLaunchKernelGGL(copy_f4, dim3(blocks), dim3(256), 0, ctx->stream, (f32x4*)b, (const f32x4*)a, n4);
+            launch();
+            launch();
             (void)hipEventRecord(e0, ctx->stream);
-            for (int r = 0; r < 5; ++r)
-                hipLaunchKernelGGL(copy_f4, dim3(blocks), dim3(256), 0, ctx->stream, (f32x4*)b, (const f32x4*)a, n4);
+            for (int r = 0; r < 5; ++r) launch();
             (void)hipEventRecord(e1, ctx->stream);
             e = hipEventSynchronize(e1);
             if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
         }
         if (a) (void)hipFree(a);
         if (b) (void)hipFree(b);
-        if (e != hipSuccess) rc = from_hip(e, "copy probe");
-        if (!rc) *result = 5.0 * 2.0 * (double)bytes / (ms * 1e-3) / 1e9;
+        if (e != hipSuccess) rc = from_hip(e, which == 1 ? "copy probe" : "read probe");
+        if (!rc) *result = 5.0 * (which == 1 ? 2.0 : 1.0) * (double)bytes / (ms * 1e-3) / 1e9;
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);

@@ -248,9 +248,9 @@ class Device:
         return float(ms.value)
 
     def peak_probe(self, which: str) -> float:
-        """Measured fp32 MFMA TFLOP/s ("mfma") or HBM copy GB/s ("hbm")."""
+        """Measured fp32 MFMA TFLOP/s ("mfma"), HBM copy GB/s ("hbm") or HBM read GB/s ("hbm_read")."""
         out = C.c_double()
-        _check(self.lib.lancius_hip_peak_probe(self.ctx, {"mfma": 0, "hbm": 1}[which], C.byref(out)))
+        _check(self.lib.lancius_hip_peak_probe(self.ctx, {"mfma": 0, "hbm": 1, "hbm_read": 2}[which], C.byref(out)))
         return float(out.value)
 
     def close(self) -> None:

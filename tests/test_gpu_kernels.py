@@ -128,6 +128,29 @@ def test_gemm_split_k(dev, M, K, N, act):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
 
 
+@pytest.mark.parametrize("M,K,N", [(16, 4096, 4096), (32, 8192, 1000), (5, 3000, 77)])
+def test_gemm_skinny_fused_split_repeatable(dev, M, K, N):
+    """The skinny kernel adds its K slices inside the launch (partials through
+    the point of coherence, the last-arriving workgroup reduces in slice
+    order): eight calls in a row give the same bits, and the oracle's values."""
+    A, B = prng.normal(31 + M, (M, K)), prng.normal(32 + N, (K, N))
+    bv, R = prng.normal(33, (N,)), prng.normal(34, (M, N))
+    dA, dB, db, dR = _upload(dev, A, B, bv, R)
+    dC = dev.alloc(M * N * 4)
+    case(f"skinny fused split M={M} K={K} N={N} x8")
+    outs = []
+    for _ in range(8):
+        dev.fill(dC, float("nan"), M * N)
+        dev.gemm(dC, dA, dB, M, K, N, bias=db, act=ACT_RELU, residual=dR)
+        outs.append(dev.download(dC, (M, N)))
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    ref = oracle.relu(oracle.matmul(A, B) + bv.astype(np.float64)[None, :]) + R.astype(np.float64)
+    assert oracle.normwise_error(outs[0], ref) <= oracle.tolerance(K)
+    for b in (dA, dB, db, dR, dC):
+        b.free()
+
+
 @pytest.mark.parametrize("M,K,N", [(32, 784, 128), (32, 128, 10), (17, 300, 77), (3, 1000, 1), (64, 784, 128),
                                    (64, 128, 10), (48, 300, 77), (40, 4096, 4096)])
 def test_gemm_small_m_and_ragged_n(dev, M, K, N):
