@@ -140,19 +140,26 @@ def decode_cases(dev, steps, warmup) -> dict:
         "ms": round(t, 4), "GB/s": round(nb / t / 1e6, 1), "frac_hbm": round(nb / t / 1e6 / PEAK_HBM, 4)}
     for b in (q, k, v, o):
         b.free()
-    B, Sq, Skv, Hq, Hkv, D = 4, 1024, 2048, 32, 8, 64
-    q = dev.upload(prng.uniform(63, (B, Sq, Hq, D), -1.0, 1.0))
-    k = dev.upload(prng.uniform(64, (B, Skv, Hkv, D), -1.0, 1.0))
-    v = dev.upload(prng.uniform(65, (B, Skv, Hkv, D), -1.0, 1.0))
-    o = dev.alloc(B * Sq * Hq * D * 4)
-    t = time_steps(dev, lambda: dev.attention_gqa(o, q, k, v, B, Sq, Skv, Hq, Hkv, D, True), steps, warmup)
-    # causal with a 1024-token history: query i sees 1024 + i + 1 keys
-    flops = 4.0 * B * Hq * D * sum(Skv - Sq + i + 1 for i in range(Sq))
-    out[f"attention_gqa_prefill_B{B}_q{Sq}_kv{Skv}_Hq{Hq}_Hkv{Hkv}_D{D}"] = {
-        "ms": round(t, 4), "GFLOP/s": round(flops / t / 1e6, 1),
-        "frac_fp32_mfma": round(flops / t / 1e9 / PEAK_FP32_MFMA, 4)}
-    for b in (q, k, v, o):
-        b.free()
+    for D in (64, 128):
+        B, Sq, Skv, Hq, Hkv = 4, 1024, 2048, 32, 8
+        q = dev.upload(prng.uniform(63, (B, Sq, Hq, D), -1.0, 1.0))
+        k = dev.upload(prng.uniform(64, (B, Skv, Hkv, D), -1.0, 1.0))
+        v = dev.upload(prng.uniform(65, (B, Skv, Hkv, D), -1.0, 1.0))
+        o = dev.alloc(B * Sq * Hq * D * 4)
+        t = time_steps(dev, lambda: dev.attention_gqa(o, q, k, v, B, Sq, Skv, Hq, Hkv, D, True), steps, warmup)
+        # causal with a 1024-token history: query i sees 1024 + i + 1 keys
+        flops = 4.0 * B * Hq * D * sum(Skv - Sq + i + 1 for i in range(Sq))
+        out[f"attention_gqa_prefill_B{B}_q{Sq}_kv{Skv}_Hq{Hq}_Hkv{Hkv}_D{D}"] = {
+            "ms": round(t, 4), "GFLOP/s": round(flops / t / 1e6, 1),
+            "frac_fp32_mfma": round(flops / t / 1e9 / PEAK_FP32_MFMA, 4)}
+        for b in (q, k, v, o):
+            b.free()
+    for D in (32, 128):  # the SDPA config at other head dims (same B, S, H)
+        for causal in (True, False):
+            name = f"attention_B8_H16_D{D}_S2048_{'causal' if causal else 'noncausal'}"
+            t, f, _ = attention_case(dev, 8, 2048, 16, D, causal, 44, steps, warmup)
+            out[name] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
+                         "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
     rows, hid = 4096, 4096
     x = dev.upload(prng.normal(66, (rows, hid)))
     g = dev.upload(np.ones((hid,), np.float32))

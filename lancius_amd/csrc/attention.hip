@@ -8,8 +8,8 @@
 // Skipping key blocks that lie entirely above the diagonal is exactly the
 // reference's masking: exp(-1e9 - m) is 0 and the correction factor is 1.
 //
-// Fast kernel (D = 64), "transposed" formulation so that every softmax
-// statistic is lane-local:
+// Fast kernel (D = 32, 64, 96, 128), "transposed" formulation so that every
+// softmax statistic is lane-local:
 //   S^T[key][q] = K . Q^T    MFMA A = K tile (LDS), B = Q^T (registers)
 //   O^T[d][q]  += V^T . P^T  MFMA A = V^T (LDS),    B = P^T (the S^T registers)
 // With v_mfma_f32_32x32x2_f32, lane l holds query l%32 in both accumulators,
@@ -18,9 +18,9 @@
 // any data movement: step s of the PV product uses register s, whose key index
 // 8*(s/4) + 4*(l/32) + s%4 is matched by the V^T operand address.
 // The score tile never leaves registers.  Each workgroup (4 waves) owns 128
-// queries of one (batch, head); K/V blocks of 64 keys are double-buffered in
-// LDS and shared by the 4 waves.  Q is pre-scaled by scale*log2(e) so the
-// exponentials are exp2.
+// queries of one (batch, head); K/V blocks of 64 keys (32 for D > 64) are
+// double-buffered in LDS and shared by the 4 waves.  Q is pre-scaled by
+// scale*log2(e) so the exponentials are exp2.
 #include <math.h>
 
 #include <algorithm>
@@ -42,19 +42,26 @@ struct AttnParams {
     int causal;    // query i sees keys j <= i + (Skv - S)
     float qscale;  // scale * log2(e)
     int q_tiles;
-    int pair_tiles;  // causal grid small enough to be resident at once (see attention_d64)
+    int pair_tiles;  // causal grid small enough to be resident at once (see attention_mfma)
     int Z;         // count * batch independent problems
 };
 
-constexpr int kD = 64;
 constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
-constexpr int kBKV = 64;   // keys per LDS block
-constexpr int kLDK = kD + 1;  // K rows padded: lanes read 32 different keys at one d
-constexpr int kLDV = kD + 4;  // V rows: lanes read 32 consecutive d of one key
 
-__global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
-    __shared__ __attribute__((aligned(16))) float Ks[2][kBKV][kLDK];
-    __shared__ __attribute__((aligned(16))) float Vs[2][kBKV][kLDV];
+// D = head dim (a multiple of 32, at most 128); BKV = keys per LDS block
+// (64 for D <= 64, 32 above, so the double-buffered K/V blocks of two
+// workgroups fit a CU's LDS).
+template <int D, int BKV>
+__global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
+    static_assert(D % 32 == 0 && D <= 128 && BKV % 32 == 0, "tile shape");
+    constexpr int LDK = D + 1;  // K rows padded: lanes read 32 different keys at one d
+    constexpr int LDV = D + 4;  // V rows: lanes read 32 consecutive d of one key
+    constexpr int QSTEPS = D / 2;        // K.Q^T MFMA steps (2 d each)
+    constexpr int DB = D / 32;           // O^T d-blocks
+    constexpr int SB = BKV / 32;         // S^T key blocks
+    constexpr int NKV = BKV * D / 1024;  // float4 of each K/V block per thread
+    __shared__ __attribute__((aligned(16))) float Ks[2][BKV][LDK];
+    __shared__ __attribute__((aligned(16))) float Vs[2][BKV][LDV];
 
     // 1-D task order, query-tile major: consecutive ids (which the hardware
     // deals round-robin to the 8 XCDs) are different (batch, head) problems of
@@ -79,10 +86,10 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     const int S = p.S, H = p.H, Skv = p.Skv;
     const int off = Skv - S;  // causal offset of the query rows into the key sequence
     const int hk = h / (H / p.Hkv);
-    const size_t row_stride = (size_t)H * kD;
-    const size_t kv_stride = (size_t)p.Hkv * kD;
-    const size_t base = ((size_t)b * S * H + h) * kD;
-    const size_t kv_base = ((size_t)b * Skv * p.Hkv + hk) * kD;
+    const size_t row_stride = (size_t)H * D;
+    const size_t kv_stride = (size_t)p.Hkv * D;
+    const size_t base = ((size_t)b * S * H + h) * D;
+    const size_t kv_base = ((size_t)b * Skv * p.Hkv + hk) * D;
     const float* __restrict__ Qg = p.Q[g] + base;
     const float* __restrict__ Kg = p.K[g] + kv_base;
     const float* __restrict__ Vg = p.V[g] + kv_base;
@@ -96,12 +103,12 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     const int q = qw0 + lq;           // this lane's query
     const bool q_valid = q < S;
 
-    // Q^T operand: step s uses d = s + 32*(l/32); the K operand uses the same d.
-    float qf[32];
+    // Q^T operand: step s uses d = s + (D/2)*(l/32); the K operand uses the same d.
+    float qf[QSTEPS];
     if (q_valid) {
-        const f32x4* src = (const f32x4*)(Qg + (size_t)q * row_stride + 32 * lk);
+        const f32x4* src = (const f32x4*)(Qg + (size_t)q * row_stride + QSTEPS * lk);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < QSTEPS / 4; ++i) {
             const f32x4 v = src[i];
             qf[4 * i + 0] = v.x * p.qscale;
             qf[4 * i + 1] = v.y * p.qscale;
@@ -110,20 +117,20 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 32; ++i) qf[i] = 0.0f;
+        for (int i = 0; i < QSTEPS; ++i) qf[i] = 0.0f;
     }
 
     // Key range of this workgroup.
     const int kv_end = p.causal ? max(0, min(Skv, q0 + kBQ + off)) : Skv;
-    const int nblocks = (kv_end + kBKV - 1) / kBKV;
+    const int nblocks = (kv_end + BKV - 1) / BKV;
 
-    // K/V global -> register staging: 64 keys x 64 d = 1024 float4 per tensor.
-    f32x4 kreg[4], vreg[4];
+    // K/V global -> register staging: BKV keys x D floats per tensor.
+    f32x4 kreg[NKV], vreg[NKV];
     auto load_kv = [&](int kb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NKV; ++i) {
             const int idx = tid + 256 * i;
-            const int key = idx >> 4, dq = idx & 15;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
             const int gk = kb + key;
             if (gk < Skv) {
                 kreg[i] = *(const f32x4*)(Kg + (size_t)gk * kv_stride + 4 * dq);
@@ -136,9 +143,9 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     };
     auto store_kv = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NKV; ++i) {
             const int idx = tid + 256 * i;
-            const int key = idx >> 4, dq = idx & 15;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
             float* kd = &Ks[buf][key][4 * dq];
             kd[0] = kreg[i].x;
             kd[1] = kreg[i].y;
@@ -148,12 +155,11 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
         }
     };
 
-    f32x16 o_acc[2];  // O^T for d-blocks 0..31 and 32..63
+    f32x16 o_acc[DB];  // O^T, d-block db holds d = 32*db .. 32*db + 31
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        o_acc[0][r] = 0.0f;
-        o_acc[1][r] = 0.0f;
-    }
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[db][r] = 0.0f;
     float m_run = -1e30f;  // running max (log2 domain); finite so exp2 never sees inf - inf
     float l_part = 0.0f;   // this lane's share of the running sum
 
@@ -165,32 +171,31 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
 
     for (int blk = 0; blk < nblocks; ++blk) {
         const int cur = blk & 1;
-        const int kb = blk * kBKV;
+        const int kb = blk * BKV;
         const bool more = blk + 1 < nblocks;
-        if (more) load_kv(kb + kBKV);
+        if (more) load_kv(kb + BKV);
 
         // Wave-uniform skip of blocks entirely above this wave's diagonal.
         const bool active = !p.causal || kb <= qw0 + 31 + off;
         if (active) {
-            f32x16 s_acc[2];
+            f32x16 s_acc[SB];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s_acc[0][r] = 0.0f;
-                s_acc[1][r] = 0.0f;
-            }
+            for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-            for (int s = 0; s < 32; ++s) {
-                const int d = s + 32 * lk;
-                const float k0 = Ks[cur][lq][d];
-                const float k1 = Ks[cur][32 + lq][d];
-                s_acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(k0, qf[s], s_acc[0], 0, 0, 0);
-                s_acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(k1, qf[s], s_acc[1], 0, 0, 0);
+                for (int r = 0; r < 16; ++r) s_acc[sb][r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < QSTEPS; ++s) {
+                const int d = s + QSTEPS * lk;
+#pragma unroll
+                for (int sb = 0; sb < SB; ++sb)
+                    s_acc[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[cur][32 * sb + lq][d], qf[s], s_acc[sb], 0,
+                                                                     0, 0);
             }
             // Register r of lane l holds key kb + 32*sb + 8*(r/4) + 4*(l/32) + r%4.
-            const bool need_mask = (p.causal && kb + kBKV - 1 > qw0 + off) || (kb + kBKV > Skv);
+            const bool need_mask = (p.causal && kb + BKV - 1 > qw0 + off) || (kb + BKV > Skv);
             if (need_mask) {
 #pragma unroll
-                for (int sb = 0; sb < 2; ++sb)
+                for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
                         const int key = kb + 32 * sb + 8 * (r >> 2) + 4 * lk + (r & 3);
@@ -199,14 +204,16 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
             }
             float mx = -INFINITY;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s_acc[0][r], s_acc[1][r]));
+            for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_acc[sb][r]);
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float m_new = fmaxf(m_run, mx);
             const float corr = exp2f(m_run - m_new);
             m_run = m_new;
             float psum = 0.0f;
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
+            for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const float pv = exp2f(s_acc[sb][r] - m_new);
@@ -215,20 +222,19 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
                 }
             l_part = l_part * corr + psum;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                o_acc[0][r] *= corr;
-                o_acc[1][r] *= corr;
-            }
-            // O^T += V^T . P^T over the 64 keys of this block.
+            for (int db = 0; db < DB; ++db)
 #pragma unroll
-            for (int sb = 0; sb < 2; ++sb)
+                for (int r = 0; r < 16; ++r) o_acc[db][r] *= corr;
+            // O^T += V^T . P^T over the BKV keys of this block.
+#pragma unroll
+            for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
                 for (int s = 0; s < 16; ++s) {
                     const int key = 32 * sb + 8 * (s >> 2) + 4 * lk + (s & 3);
-                    const float v0 = Vs[cur][key][lq];
-                    const float v1 = Vs[cur][key][32 + lq];
-                    o_acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(v0, s_acc[sb][s], o_acc[0], 0, 0, 0);
-                    o_acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(v1, s_acc[sb][s], o_acc[1], 0, 0, 0);
+#pragma unroll
+                    for (int db = 0; db < DB; ++db)
+                        o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[cur][key][32 * db + lq], s_acc[sb][s],
+                                                                         o_acc[db], 0, 0, 0);
                 }
         }
         if (more) store_kv(cur ^ 1);
@@ -241,7 +247,7 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
     float* dst = Og + (size_t)q * row_stride;
     // O^T register r of lane l: d = 32*db + 8*(r/4) + 4*(l/32) + r%4.
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             f32x4 o;
@@ -253,9 +259,12 @@ __global__ void __launch_bounds__(256, 2) attention_d64(const AttnParams p) {
         }
 }
 
-// Any head_dim: one thread per (query row, head), the reference's online loop
-// in fp32 with the output row as the accumulator.  Used for shapes the fast
-// kernel does not cover.
+// Head dims the MFMA kernel does not take (not a multiple of 32, or above
+// 128) and operands that are not 16-byte aligned: one thread per (query
+// row, head), the reference's online loop in fp32.  Up to DMAX values the
+// output row is accumulated in registers and written once; beyond that
+// (DMAX = 0) the output row in memory is the accumulator.
+template <int DMAX>
 __global__ void __launch_bounds__(256) attention_rowwise(const AttnParams p) {
     const size_t rows = (size_t)p.S * p.H;
     const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -272,24 +281,49 @@ __global__ void __launch_bounds__(256) attention_rowwise(const AttnParams p) {
     const float* K = p.K[g] + kv_base;
     const float* V = p.V[g] + kv_base;
     float* o = p.O[g] + base + (size_t)i * rs;
-    for (int d = 0; d < D; ++d) o[d] = 0.0f;
     float m = -1e30f, l = 0.0f;
     const int jend = p.causal ? min(p.Skv, max(0, i + 1 + p.Skv - p.S)) : p.Skv;
-    for (int j = 0; j < jend; ++j) {
-        const float* k = K + (size_t)j * rkv;
-        float s = 0.0f;
-        for (int d = 0; d < D; ++d) s += q[d] * k[d];
-        s *= p.qscale;
-        const float m_new = fmaxf(m, s);
-        const float c = exp2f(m - m_new);
-        const float pj = exp2f(s - m_new);
-        l = l * c + pj;
-        const float* v = V + (size_t)j * rkv;
-        for (int d = 0; d < D; ++d) o[d] = o[d] * c + pj * v[d];
-        m = m_new;
+    if constexpr (DMAX > 0) {
+        float acc[DMAX];
+#pragma unroll
+        for (int d = 0; d < DMAX; ++d) acc[d] = 0.0f;
+        for (int j = 0; j < jend; ++j) {
+            const float* k = K + (size_t)j * rkv;
+            float s = 0.0f;
+            for (int d = 0; d < D; ++d) s += q[d] * k[d];
+            s *= p.qscale;
+            const float m_new = fmaxf(m, s);
+            const float c = exp2f(m - m_new);
+            const float pj = exp2f(s - m_new);
+            l = l * c + pj;
+            const float* v = V + (size_t)j * rkv;
+#pragma unroll
+            for (int d = 0; d < DMAX; ++d)
+                if (d < D) acc[d] = acc[d] * c + pj * v[d];
+            m = m_new;
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int d = 0; d < DMAX; ++d)
+            if (d < D) o[d] = acc[d] * inv;
+    } else {
+        for (int d = 0; d < D; ++d) o[d] = 0.0f;
+        for (int j = 0; j < jend; ++j) {
+            const float* k = K + (size_t)j * rkv;
+            float s = 0.0f;
+            for (int d = 0; d < D; ++d) s += q[d] * k[d];
+            s *= p.qscale;
+            const float m_new = fmaxf(m, s);
+            const float c = exp2f(m - m_new);
+            const float pj = exp2f(s - m_new);
+            l = l * c + pj;
+            const float* v = V + (size_t)j * rkv;
+            for (int d = 0; d < D; ++d) o[d] = o[d] * c + pj * v[d];
+            m = m_new;
+        }
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        for (int d = 0; d < D; ++d) o[d] *= inv;
     }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    for (int d = 0; d < D; ++d) o[d] *= inv;
 }
 
 // ---- decode: one query token per sequence against a K/V cache --------------
@@ -622,15 +656,27 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
     p.qscale = scale * 1.4426950408889634f;  // log2(e)
     const unsigned z = (unsigned)(count * batch);
     p.Z = (int)z;
-    if (D == kD && vec) {
+    if (vec && D % 32 == 0 && D <= 128) {
         p.q_tiles = (int)((S + kBQ - 1) / kBQ);
         const size_t tasks = (size_t)p.q_tiles * H * z;
         LANCIUS_REQUIRE(tasks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention: too many tiles");
         p.pair_tiles = causal && tasks <= 2 * (size_t)cu_count(ctx) && tune("attn_pair", 1);
-        hipLaunchKernelGGL(attention_d64, dim3((unsigned)tasks), dim3(256), 0, ctx->stream, p);
-        if (int rc = check_launch("attention_d64")) return rc;
+        const dim3 grid((unsigned)tasks);
+        switch (D) {
+            case 32: hipLaunchKernelGGL((attention_mfma<32, 64>), grid, dim3(256), 0, ctx->stream, p); break;
+            case 64: hipLaunchKernelGGL((attention_mfma<64, 64>), grid, dim3(256), 0, ctx->stream, p); break;
+            case 96: hipLaunchKernelGGL((attention_mfma<96, 32>), grid, dim3(256), 0, ctx->stream, p); break;
+            default: hipLaunchKernelGGL((attention_mfma<128, 32>), grid, dim3(256), 0, ctx->stream, p); break;
+        }
+        if (int rc = check_launch("attention_mfma")) return rc;
     } else {
-        hipLaunchKernelGGL(attention_rowwise, dim3(ceil_div(S * H, 256), 1, z), dim3(256), 0, ctx->stream, p);
+        const dim3 grid(ceil_div(S * H, 256), 1, z);
+        if (D <= 32)
+            hipLaunchKernelGGL(attention_rowwise<32>, grid, dim3(256), 0, ctx->stream, p);
+        else if (D <= 128)
+            hipLaunchKernelGGL(attention_rowwise<128>, grid, dim3(256), 0, ctx->stream, p);
+        else
+            hipLaunchKernelGGL(attention_rowwise<0>, grid, dim3(256), 0, ctx->stream, p);
         if (int rc = check_launch("attention_rowwise")) return rc;
     }
     return ok();

@@ -97,6 +97,11 @@ def test_gqa_golden(dev):
     (2, 65, 190, 8, 8, 64, False),      # non-causal, ragged lengths
     (1, 50, 80, 6, 3, 40, True),        # other head dim: row kernel
     (1, 1, 513, 4, 1, 64, True),        # one query over a cache (MQA)
+    (2, 300, 300, 16, 4, 128, True),    # GQA prefill at D = 128: the fused kernel, 32-key blocks
+    (2, 128, 1000, 8, 2, 128, True),    # D = 128 after an 872-token history
+    (1, 77, 200, 8, 4, 128, False),     # D = 128 non-causal, ragged
+    (2, 96, 500, 8, 2, 32, True),       # D = 32 with history
+    (1, 130, 130, 6, 2, 96, True),      # D = 96
 ])
 def test_gqa_shapes(dev, B, Sq, Skv, Hq, Hkv, D, causal):
     q, k, v, got = _gqa(dev, B, Sq, Skv, Hq, Hkv, D, causal, 230 + Sq + Skv)

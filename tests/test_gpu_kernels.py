@@ -294,6 +294,38 @@ def test_attention_shapes(dev, B, S, H, D, causal):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("D", [32, 96, 128])
+@pytest.mark.parametrize("B,S,H", [(1, 1, 2), (2, 77, 3), (1, 300, 2), (2, 129, 1)])
+def test_attention_head_dims(dev, B, S, H, D, causal):
+    """The MFMA kernel at head dims other than 64 (32 and 96/128 use 64- and
+    32-key blocks), ragged query tiles included."""
+    got, ref = _attn_case(dev, B, S, H, D, causal, seed=950 + S + D)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(max(S, D))
+
+
+@pytest.mark.parametrize("D", [20, 64, 128, 160])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_misaligned_and_odd_dims(dev, D, causal):
+    """Operands 4 bytes past a 16-byte boundary (and D = 20, 160) take the
+    row kernel: the output row in registers up to D = 128, in memory above."""
+    B, S, H = 2, 70, 3
+    q, k, v = (prng.normal(960 + j + D, (B, S, H, D)) for j in range(3))
+    n = q.size
+    dq, dk, dv, do = (dev.alloc(4 * (n + 1)) for _ in range(4))
+    for buf, a in ((dq, q), (dk, k), (dv, v)):
+        dev.write(int(buf) + 4, np.ascontiguousarray(a, np.float32))
+    dev.fill(int(do) + 4, float("nan"), n)
+    case(f"attention misaligned D={D} causal={causal}")
+    dev.attention(int(do) + 4, int(dq) + 4, int(dk) + 4, int(dv) + 4, B, S, H, D, causal=causal)
+    got = dev.download(int(do) + 4, q.shape)
+    assert np.isfinite(got).all()
+    ref = oracle.attention(q, k, v, causal=causal)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(max(S, D))
+    for b in (dq, dk, dv, do):
+        b.free()
+
+
+@pytest.mark.parametrize("causal", [True, False])
 def test_attention_config_s512(dev, causal):
     """The whole S=512 config (every batch, head and row) against the oracle."""
     got, ref = _attn_case(dev, 8, 512, 16, 64, causal, seed=44)
