@@ -677,6 +677,35 @@ def cpu_train_step_ms(ref, builder) -> float:
     return sorted(times)[1] * 1e3
 
 
+PROFILE_CASES = {
+    # name: (what it runs, callable(dev, reps) -> ms per call)
+    "gemm4096": "fp32 GEMM 4096^3 (the headline)",
+    "gemm_skinny": "fp32 GEMM 16x4096x4096",
+    "conv": "conv 3x3 N32 64->128 56x56 + ReLU",
+    "attn_s512_causal": "SDPA B8 H16 D64 S512 causal",
+    "attn_s2048_causal": "SDPA B8 H16 D64 S2048 causal",
+    "attn_s2048_noncausal": "SDPA B8 H16 D64 S2048 non-causal",
+    "copy": "HBM copy probe (1 GiB read + 1 GiB written per launch)",
+}
+
+
+def profile_case(dev, name: str, reps: int) -> float:
+    """One config on its own, `reps` timed calls after a settle period, for
+    rocprofv3 passes whose dispatches are the kernel of interest; the "copy"
+    case (the HBM copy probe) calibrates the byte counters."""
+    if name == "copy":
+        dev.peak_probe("hbm")
+        return 0.0
+    if name == "gemm4096":
+        return gemm_case(dev, 4096, 4096, 4096, 43, reps, 2, settle_ms=60.0)[0]
+    if name == "gemm_skinny":
+        return gemm_case(dev, 16, 4096, 4096, 43, reps, 2)[0]
+    if name == "conv":
+        return conv_case(dev, reps, 2)[0]
+    S = 512 if "s512" in name else 2048
+    return attention_case(dev, 8, S, 16, 64, name.endswith("_causal"), 44, reps, 2)[0]
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -688,6 +717,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--quick", action="store_true", help="headline only (no other configs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--profile-case", choices=sorted(PROFILE_CASES),
+                    help="run one config only (for rocprofv3 passes): " +
+                         "; ".join(f"{k}: {v}" for k, v in PROFILE_CASES.items()))
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
@@ -703,6 +735,12 @@ def main() -> int:
     json_out = os.fdopen(os.dup(1), "w")
     os.dup2(2, 1)
     dev = Device(0)
+    if args.profile_case:
+        ms = profile_case(dev, args.profile_case, args.steps)
+        dev.close()
+        json_out.write(json.dumps({"profile_case": args.profile_case, "ms": round(ms, 4)}) + "\n")
+        json_out.flush()
+        return 0
     M = N = K = 4096
     log("device ceilings")
     measured_mfma = dev.peak_probe("mfma")

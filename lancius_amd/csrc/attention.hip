@@ -54,12 +54,16 @@ constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
 template <int D, int BKV>
 __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
     static_assert(D % 32 == 0 && D <= 128 && BKV % 32 == 0, "tile shape");
+    constexpr int NT = 256;
     constexpr int LDK = D + 1;  // K rows padded: lanes read 32 different keys at one d
-    constexpr int LDV = D + 4;  // V rows: lanes read 32 consecutive d of one key
+    // V rows: lanes read 32 consecutive d of one key, the two lane halves
+    // keys 4 rows apart; D + 8 puts those 32 banks apart (64 banks).
+    constexpr int LDV = D + 8;
     constexpr int QSTEPS = D / 2;        // K.Q^T MFMA steps (2 d each)
     constexpr int DB = D / 32;           // O^T d-blocks
     constexpr int SB = BKV / 32;         // S^T key blocks
-    constexpr int NKV = BKV * D / 1024;  // float4 of each K/V block per thread
+    constexpr int NKV = BKV * D / (4 * NT);  // float4 of each K/V block per thread
+    static_assert(NKV * 4 * NT == BKV * D, "staging covers the block");
     __shared__ __attribute__((aligned(16))) float Ks[2][BKV][LDK];
     __shared__ __attribute__((aligned(16))) float Vs[2][BKV][LDV];
 
@@ -126,12 +130,12 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
 
     // K/V global -> register staging: BKV keys x D floats per tensor.
     f32x4 kreg[NKV], vreg[NKV];
-    auto load_kv = [&](int kb) {
+    auto load_kv = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < NKV; ++i) {
-            const int idx = tid + 256 * i;
+            const int idx = tid + NT * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
-            const int gk = kb + key;
+            const int gk = k0 + key;
             if (gk < Skv) {
                 kreg[i] = *(const f32x4*)(Kg + (size_t)gk * kv_stride + 4 * dq);
                 vreg[i] = *(const f32x4*)(Vg + (size_t)gk * kv_stride + 4 * dq);
@@ -144,7 +148,7 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
     auto store_kv = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < NKV; ++i) {
-            const int idx = tid + 256 * i;
+            const int idx = tid + NT * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
             float* kd = &Ks[buf][key][4 * dq];
             kd[0] = kreg[i].x;
