@@ -335,15 +335,17 @@ LANCIUS_HIP_EXPORT void lancius_hip_graph_destroy(lancius_hip_graph* graph);
 
 /* out = softmax(act1(x . W1 + b1) . W2 + b2) row by row (softmax != 0, with
  * the first-maximum argmax when argmax != NULL), or the logits y when
- * softmax == 0, in two launches (a split-K GEMM for the first layer, then
- * one workgroup for the rest): the MATMUL -> BROADCAST+ADD -> RELU|GELU|TANH ->
- * MATMUL -> BROADCAST+ADD -> SOFTMAX chain of lancius_scheduler.c:169-233,
- * 284-308 for small batches, whose unfused form (five launches) is bound by
- * its launch count.  x [M][K1], W1 [K1][N1], W2 [N1][N2], out [M][N2]; b1,
- * b2 may be NULL.  Limits: M <= 64, N2 <= 64, M*N1 <= 16384,
- * N1*N2 <= 8192 (else -3).  Results equal the unfused launches up to fp32
- * summation order; repeated calls give identical bits.  Uses the context's
- * workspace, so calls on one context are ordered by its stream. */
+ * softmax == 0, in one launch (workgroups own 16x16 tiles of the hidden
+ * layer over the whole K1 and hand their share of the second layer to the
+ * last-arriving workgroup of each 16-row block): the MATMUL -> BROADCAST+ADD
+ * -> RELU|GELU|TANH -> MATMUL -> BROADCAST+ADD -> SOFTMAX chain of
+ * lancius_scheduler.c:169-233, 284-308 for small batches, whose unfused form
+ * (five launches) is bound by its launch count.  x [M][K1], W1 [K1][N1],
+ * W2 [N1][N2], out [M][N2]; b1, b2 may be NULL.  Limits: M <= 64, N2 <= 64,
+ * M*N1 <= 16384, N1*N2 <= 8192 (else -3).  Results equal the unfused
+ * launches up to fp32 summation order; repeated calls give identical bits.
+ * Uses the context's workspace and arrival counters, so calls on one context
+ * are ordered by its stream. */
 LANCIUS_HIP_EXPORT int lancius_hip_mlp2_f32(lancius_hip_ctx* ctx, float* out, int32_t* argmax, const float* x,
                                             const float* w1, const float* b1, int act1, const float* w2,
                                             const float* b2, size_t M, size_t K1, size_t N1, size_t N2, int softmax);

@@ -1,20 +1,9 @@
-// Two dense layers and a row softmax in two launches, for the small-batch MLP
+// Two dense layers and a row softmax in one launch, for the small-batch MLP
 // graphs (B/examples/train_mnist.c:149-158 builds x -> MATMUL -> +b -> RELU ->
 // MATMUL -> +b -> SOFTMAX with 64 rows).  At that size every kernel of the
 // unfused chain (split-K GEMM, its reduce, GEMM, reduce, softmax) is a few
-// microseconds of work behind a fixed ~9 us launch cost, so the chain is
-// bound by its number of dependent launches.
-//  * mlp2_partials: workgroup (column tile t, K range s) computes the
-//    64 x 64 tile of x . W1 over its K range with 32x32x2 MFMAs and stores
-//    the partial.
-//  * mlp2_tail (one workgroup per row): adds the row's partials in K-range
-//    order, applies b1 and the activation into LDS, computes y = h . W2 + b2
-//    (W2 staged in LDS), then the row's softmax with the first-maximum
-//    argmax, exactly as softmax_rows does.
-// The kernel boundary orders the two phases.  (Joining them in one launch
-// with "last workgroup continues" arrival counters needs device-scope
-// release/acquire fences, which write back and invalidate the XCD's L2 on
-// this part: measured 91 us against 26 us for the unfused chain.)
+// microseconds of work behind a fixed launch cost, so the chain is bound by
+// its number of dependent launches.  See mlp2_fused for the design.
 #include <math.h>
 
 #include <algorithm>
@@ -33,146 +22,200 @@ struct ChainParams {
     const float* b2;  // [N2] or null
     float* out;       // [M][N2]: probabilities (softmax) or y
     int32_t* argmax;  // [M] or null
-    float* part;      // [splits][M][N1]
+    float* ypart;     // [tiles_n][M][N2]: each column tile's share of y
+    unsigned* counters;  // one arrival counter per row block, zero between launches
     int M, K1, N1, N2, act1, act2, softmax;
-    int splits, kchunk, tiles_n;
+    int vec;  // K1 and N1 multiples of 4, x and W1 16-byte aligned: float4 loads
+    int tiles_n;
 };
 
-constexpr int kT = 64;   // phase-1 tile: up to 64 rows x 64 columns
-constexpr int kK = 16;   // k-tile
-constexpr int kMaxH = 16384;  // M * N1 floats of h in LDS
-constexpr int kMaxW2 = 8192;  // N1 * N2 floats of W2 in LDS
+// Workgroup (column tile t of 16 columns of h, row block b of 16 rows):
+//  1. h[b, t] = act1(x[b] . W1[:, t] + b1[t]) over the whole K1: the x row
+//     block and the W1 column slab are staged in LDS (in K chunks of kFKC),
+//     the 4 waves take a quarter of each chunk's k-steps with
+//     v_mfma_f32_16x16x4_f32 and add their accumulators through LDS in wave
+//     order;
+//  2. y_t = h[b, t] . W2[t rows, :], the tile's share of the second layer,
+//     stored for the row block's reducer;
+//  3. the workgroup that arrives last at row block b's counter adds the
+//     tiles' shares in tile order, adds b2, applies act2, and runs each row's
+//     softmax and first-maximum argmax (one thread per row).
+// One hand-off between workgroups (through the point of coherence,
+// kernels.hpp); every sum runs in a fixed order, so repeated calls give
+// identical bits.
+// Limits of the chain (the small-batch regime it is for; lancius_hip.h):
+// rows, outputs, hidden values M * N1 and second-layer weights N1 * N2.
+constexpr int kMaxRows = 64;
+constexpr int kMaxOut = 64;
+constexpr int kMaxH = 16384;
+constexpr int kMaxW2 = 8192;
+constexpr int kFR = 16;     // rows of h per workgroup
+constexpr int kFC = 16;     // columns of h per workgroup
+constexpr int kFKC = 1024;  // K staged per chunk
+constexpr int kXP = kFKC + 4;  // x rows in LDS: lanes read rows r at k-steps (r*kXP + k) mod 64 distinct
 
-__global__ void __launch_bounds__(256) mlp2_partials(const ChainParams p) {
-    __shared__ __attribute__((aligned(16))) float As[2][kK][kT + 4];
-    __shared__ __attribute__((aligned(16))) float Bs[2][kK][kT + 4];
+__global__ void __launch_bounds__(256) mlp2_fused(const ChainParams p) {
+    __shared__ __attribute__((aligned(16))) float Xs[kFR][kXP];    // x rows of the block, current K chunk
+    __shared__ __attribute__((aligned(16))) float Wsl[kFKC][kFC];  // W1 columns of the tile, current K chunk
+    __shared__ float red[4][kFR][kFC + 1];
+    __shared__ float Hs[kFR][kFC + 1];
+    __shared__ float W2s[kFC][64];
+    __shared__ float Ys[kFR][64];
+    __shared__ int s_flag;
 
-    const int tn = (int)blockIdx.x % p.tiles_n, sp = (int)blockIdx.x / p.tiles_n;
-    const int n0 = tn * kT;
-    const int M = p.M, K1 = p.K1, N1 = p.N1;
+    const int tn = (int)blockIdx.x % p.tiles_n, rb = (int)blockIdx.x / p.tiles_n;
+    const int n0 = tn * kFC, m0 = rb * kFR;
+    const int M = p.M, K1 = p.K1, N1 = p.N1, N2 = p.N2;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int wm = wave >> 1, wn = wave & 1, lr = lane & 31, lk = lane >> 5;
-    const int kb = sp * p.kchunk, ke = min(K1, kb + p.kchunk);
+    const int li = lane & 15, lq = lane >> 4;
 
-    // staging: thread -> 4 consecutive k of row tid/4 (A), 4 consecutive
-    // columns of k-row tid/16 (B); bounds-checked scalar loads.
-    float ar[4], br[4];
-    auto load = [&](int k0) {
-        const int r = tid >> 2, ka = k0 + 4 * (tid & 3);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ar[j] = (r < M && ka + j < ke) ? p.x[(size_t)r * K1 + ka + j] : 0.0f;
-        const int kr = k0 + (tid >> 4), c = n0 + 4 * (tid & 15);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) br[j] = (kr < ke && c + j < N1) ? p.w1[(size_t)kr * N1 + c + j] : 0.0f;
-    };
-    auto store = [&](int buf) {
-        const int r = tid >> 2, ka = 4 * (tid & 3);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) As[buf][ka + j][r] = ar[j];
-        const int kr = tid >> 4, c = 4 * (tid & 15);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Bs[buf][kr][c + j] = br[j];
-    };
-    f32x16 acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-    const int nk = (ke - kb + kK - 1) / kK;
-    if (nk > 0) {
-        load(kb);
-        store(0);
+    // W2 rows of this tile, needed after phase 1: loaded first
+    for (int i = tid; i < kFC * N2; i += 256) {
+        const int k = i / N2, j = i % N2;
+        W2s[k][j] = n0 + k < N1 ? p.w2[(size_t)(n0 + k) * N2 + j] : 0.0f;
     }
-    __syncthreads();
-    for (int t = 0; t < nk; ++t) {
-        const int cur = t & 1;
-        const bool more = t + 1 < nk;
-        if (more) load(kb + (t + 1) * kK);
-#pragma unroll
-        for (int kp = 0; kp < kK / 2; ++kp) {
-            const float a = As[cur][2 * kp + lk][wm * 32 + lr];
-            const float b = Bs[cur][2 * kp + lk][wn * 32 + lr];
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc, 0, 0, 0);
-        }
-        if (more) store(cur ^ 1);
-        __syncthreads();
-    }
-    // register r of lane l: row 8(r/4) + 4(l/32) + r%4, column l%32 of the wave's 32x32 block
-    float* dst = p.part + (size_t)sp * M * N1;
-    const int col = n0 + wn * 32 + lr;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int row = wm * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
-        if (row < M && col < N1) dst[(size_t)row * N1 + col] = acc[r];
-    }
-}
 
-constexpr int kMaxSplits = 8;
-
-// One workgroup per row r: h[r] = act(sum of the K-range partials in order
-// + b1) in LDS, y[r] = h[r] . W2 + b2 with W2 staged in LDS (four k-quarters
-// per output column added in order), then the row's softmax and argmax.
-__global__ void __launch_bounds__(256) mlp2_tail(const ChainParams p) {
-    __shared__ float Hs[kMaxH];
-    __shared__ float Ws[kMaxW2];
-    __shared__ float red[4][kT];
-    const int r = (int)blockIdx.x;
-    const int M = p.M, N1 = p.N1, N2 = p.N2;
-    const int tid = threadIdx.x, lane = tid & 63, q = tid >> 6;
-
-    for (int k = tid; k < N1; k += 256) {
-        float t[kMaxSplits];
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kc = 0; kc < K1; kc += kFKC) {
+        const int kn = min(kFKC, K1 - kc);  // k of this chunk
+        if (kc > 0) __syncthreads();        // the previous chunk's reads are done
+        // x rows m0.. of the chunk (float4 along k) and W1 columns n0.. (one
+        // float4 per k and quarter of the 16 columns): every load of the
+        // chunk is issued before the first LDS store.
+        constexpr int kPer = kFR * kFKC / 4 / 256;  // float4 of each operand per thread
+        const int xq = (kn + 3) / 4;
+        f32x4 xv[kPer], wv[kPer];
 #pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s) t[s] = s < p.splits ? p.part[((size_t)s * M + r) * N1 + k] : 0.0f;
-        float v = 0.0f;
+        for (int u = 0; u < kPer; ++u) {
+            const int i = tid + 256 * u;
+            const int r = i / xq, k = 4 * (i % xq);
+            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (i < kFR * xq && m0 + r < M) {
+                const float* src = p.x + (size_t)(m0 + r) * K1 + kc + k;
+                if (p.vec && k + 4 <= kn) {
+                    v = *(const f32x4*)src;
+                } else {
 #pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s) v += t[s];
-        if (p.b1) v += p.b1[k];
-        Hs[k] = apply_act(v, p.act1);
-    }
-    for (int i = tid; i < N1 * N2; i += 256) Ws[i] = p.w2[i];
-    __syncthreads();
-    const int kq = (N1 + 3) / 4, k0 = q * kq, k1 = min(N1, k0 + kq);
-    if (lane < N2) {
-        float a0 = 0.0f, a1 = 0.0f;
-        int k = k0;
-        for (; k + 1 < k1; k += 2) {
-            a0 += Hs[k] * Ws[k * N2 + lane];
-            a1 += Hs[k + 1] * Ws[(k + 1) * N2 + lane];
-        }
-        if (k < k1) a0 += Hs[k] * Ws[k * N2 + lane];
-        red[q][lane] = a0 + a1;
-    }
-    __syncthreads();
-    if (q != 0) return;
-    float v = -INFINITY;
-    if (lane < N2) v = apply_act(((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) + (p.b2 ? p.b2[lane] : 0.0f), p.act2);
-    float* o = p.out + (size_t)r * N2;
-    if (!p.softmax) {
-        if (lane < N2) o[lane] = v;
-        return;
-    }
-    float m = v;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    const float e = lane < N2 ? expf(v - m) : 0.0f;
-    float sum = e;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-    const float pv = e / sum;
-    if (lane < N2) o[lane] = pv;
-    if (p.argmax) {
-        // first index of the largest probability, scanning with '>' from -1e9
-        float best = lane < N2 && pv > -1e9f ? pv : -1e9f;
-        int bi = lane < N2 && pv > -1e9f ? lane : 0x7fffffff;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const float ob = __shfl_xor(best, off);
-            const int oi = __shfl_xor(bi, off);
-            if (ob > best || (ob == best && oi < bi)) {
-                best = ob;
-                bi = oi;
+                    for (int j = 0; j < 4; ++j)
+                        if (k + j < kn) v[j] = src[j];
+                }
             }
+            xv[u] = v;
+            const int kw = i >> 2, c = 4 * (i & 3);
+            f32x4 w = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (kw < kn) {
+                const float* src = p.w1 + (size_t)(kc + kw) * N1 + n0 + c;
+                if (p.vec && n0 + c + 4 <= N1) {
+                    w = *(const f32x4*)src;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (n0 + c + j < N1) w[j] = src[j];
+                }
+            }
+            wv[u] = w;
         }
-        if (lane == 0) p.argmax[r] = bi == 0x7fffffff ? 0 : bi;
+#pragma unroll
+        for (int u = 0; u < kPer; ++u) {
+            const int i = tid + 256 * u;
+            if (i < kFR * xq) {
+                const int r = i / xq, k = 4 * (i % xq);
+                Xs[r][k] = xv[u].x, Xs[r][k + 1] = xv[u].y, Xs[r][k + 2] = xv[u].z, Xs[r][k + 3] = xv[u].w;
+            }
+            if ((i >> 2) < kn) *(f32x4*)&Wsl[i >> 2][4 * (i & 3)] = wv[u];
+        }
+        __syncthreads();
+        // wave w takes k-steps w, w + 4, ...; lane l holds A[row l%16][k + l/16]
+        // and B[k + l/16][column l%16]; eight steps' LDS reads are issued
+        // before their MFMAs
+        const int steps = (kn + 3) / 4;
+        for (int s0 = wave; s0 < steps; s0 += 32) {
+            float a[8], b[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int k = 4 * (s0 + 4 * u) + lq;
+                a[u] = k < kn ? Xs[li][k] : 0.0f;
+                b[u] = k < kn ? Wsl[k][li] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+        }
+    }
+    // register r of lane l: row 4(l/16) + r, column l%16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = acc[r];
+    __syncthreads();
+    {
+        const int r = tid >> 4, c = tid & 15;  // 256 threads = 16 x 16
+        const float v = ((red[0][r][c] + red[1][r][c]) + red[2][r][c]) + red[3][r][c];
+        float h = 0.0f;
+        if (m0 + r < M && n0 + c < N1) h = apply_act(v + (p.b1 ? p.b1[n0 + c] : 0.0f), p.act1);
+        Hs[r][c] = h;  // rows past M and columns past N1 hold 0
+    }
+    __syncthreads();
+    // this tile's share of y for the block's rows
+    const size_t MN2 = (size_t)M * N2;
+    const __amdgpu_buffer_rsrc_t ypart = coherent_buffer(p.ypart, (size_t)p.tiles_n * MN2 * sizeof(float));
+    for (int i = tid; i < kFR * N2; i += 256) {
+        const int r = i / N2, j = i % N2;
+        if (m0 + r >= M) continue;
+        float a = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kFC; ++k) a += Hs[r][k] * W2s[k][j];
+        store_coherent(ypart, (int)(((size_t)tn * MN2 + (size_t)(m0 + r) * N2 + j) * sizeof(float)), a);
+    }
+    if (!arrive_last(p.counters + rb, (unsigned)p.tiles_n, &s_flag)) return;
+    reset_arrival(p.counters + rb);
+
+    // the block's rows: y = sum of the tiles' shares in tile order + b2
+    {
+        constexpr int kChunk = 16;
+        for (int i = tid; i < kFR * N2; i += 256) {
+            const int r = i / N2, j = i % N2;
+            if (m0 + r >= M) continue;
+            const int off = (int)(((size_t)(m0 + r) * N2 + j) * sizeof(float));
+            float y = 0.0f;
+            for (int t0 = 0; t0 < p.tiles_n; t0 += kChunk) {
+                float t[kChunk];
+#pragma unroll
+                for (int c = 0; c < kChunk; ++c)
+                    t[c] = t0 + c < p.tiles_n
+                               ? load_coherent(ypart, off + (int)((size_t)(t0 + c) * MN2 * sizeof(float)))
+                               : 0.0f;
+#pragma unroll
+                for (int c = 0; c < kChunk; ++c)
+                    if (t0 + c < p.tiles_n) y = (t0 + c == 0) ? t[c] : y + t[c];
+            }
+            Ys[r][j] = apply_act(y + (p.b2 ? p.b2[j] : 0.0f), p.act2);
+        }
+    }
+    __syncthreads();
+    // One thread per row: the reference's serial loops, max, exp, sum,
+    // divide (lancius_scheduler.c:284-294), then the first maximum scanning
+    // with '>' from -1e9 (B/examples/train_mnist.c:206-209).
+    if (tid < kFR && m0 + tid < M) {
+        const int r = m0 + tid;
+        const float* yr = Ys[tid];
+        float* o = p.out + (size_t)r * N2;
+        if (!p.softmax) {
+            for (int j = 0; j < N2; ++j) o[j] = yr[j];
+        } else {
+            float m = yr[0];
+            for (int j = 1; j < N2; ++j) m = fmaxf(m, yr[j]);
+            float sum = 0.0f;
+            for (int j = 0; j < N2; ++j) sum += expf(yr[j] - m);
+            float best = -1e9f;
+            int bi = 0;
+            for (int j = 0; j < N2; ++j) {
+                const float pv = expf(yr[j] - m) / sum;
+                o[j] = pv;
+                if (pv > best) {
+                    best = pv;
+                    bi = j;
+                }
+            }
+            if (p.argmax) p.argmax[r] = bi;
+        }
     }
 }
 
@@ -192,7 +235,7 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
                                        const float* w1, const float* b1, int act1, const float* w2, const float* b2,
                                        int act2, size_t M, size_t K1, size_t N1, size_t N2, int softmax) {
     LANCIUS_REQUIRE(ctx && out && x && w1 && w2, LANCIUS_HIP_ERR_NULL_PTR, "mlp2: NULL argument");
-    LANCIUS_REQUIRE(M >= 1 && M <= (size_t)kT && N2 >= 1 && N2 <= (size_t)kT && N1 >= 1 && K1 >= 1 &&
+    LANCIUS_REQUIRE(M >= 1 && M <= (size_t)kMaxRows && N2 >= 1 && N2 <= (size_t)kMaxOut && N1 >= 1 && K1 >= 1 &&
                         M * N1 <= (size_t)kMaxH && N1 * N2 <= (size_t)kMaxW2 && K1 < (1u << 30),
                     LANCIUS_HIP_ERR_SHAPE, "mlp2: M=%zu K1=%zu N1=%zu N2=%zu outside the fused chain's limits", M, K1,
                     N1, N2);
@@ -215,21 +258,14 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
     p.act1 = act1;
     p.act2 = act2;
     p.softmax = softmax ? 1 : 0;
-    p.tiles_n = (int)((N1 + kT - 1) / kT);
-    // K ranges of whole k-tiles, about 128 deep, at most 8: the tail
-    // workgroup reads splits * M * N1 partials, the first launch wants
-    // enough workgroups to finish quickly.
-    size_t splits = std::max<size_t>(1, std::min<size_t>(kMaxSplits, (K1 + 127) / 128));
-    const size_t kchunk = ((K1 + splits - 1) / splits + kK - 1) / kK * kK;
-    splits = (K1 + kchunk - 1) / kchunk;
-    p.splits = (int)splits;
-    p.kchunk = (int)kchunk;
+    p.vec = K1 % 4 == 0 && N1 % 4 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)w1 & 15u) == 0;
+    p.tiles_n = (int)((N1 + kFC - 1) / kFC);
+    const size_t row_blocks = (M + kFR - 1) / kFR;
     void* ws = nullptr;
-    if (int rc = workspace(ctx, splits * M * N1 * sizeof(float), &ws)) return rc;
-    p.part = (float*)ws;
-    hipLaunchKernelGGL(mlp2_partials, dim3((unsigned)(p.tiles_n * splits)), dim3(256), 0, ctx->stream, p);
-    if (int rc = check_launch("mlp2_partials")) return rc;
-    hipLaunchKernelGGL(mlp2_tail, dim3((unsigned)M), dim3(256), 0, ctx->stream, p);
-    if (int rc = check_launch("mlp2_tail")) return rc;
+    if (int rc = workspace(ctx, (size_t)p.tiles_n * M * N2 * sizeof(float), &ws)) return rc;
+    p.ypart = (float*)ws;
+    if (int rc = counters(ctx, row_blocks, &p.counters)) return rc;
+    hipLaunchKernelGGL(mlp2_fused, dim3((unsigned)(p.tiles_n * row_blocks)), dim3(256), 0, ctx->stream, p);
+    if (int rc = check_launch("mlp2_fused")) return rc;
     return ok();
 }

@@ -42,14 +42,6 @@ struct GemmParams {
 };
 
 constexpr int kThreads = 256;
-// s_waitcnt operand that waits for vmcnt 0 and leaves expcnt / lgkmcnt alone.
-constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
-// Cache-policy operand of the raw buffer load/store builtins on gfx950: sc1,
-// device scope (the access is coherent across the XCDs' L2 caches).
-constexpr int kCachePolicySc1 = 16;
-// Fourth word of a raw buffer resource on gfx9 (32-bit data format).
-constexpr int kBufferRsrcWord3 = 0x00020000;
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // SPLIT: the workgroup reduces K range [y*kchunk, (y+1)*kchunk) and stores its
 // raw partial sums; splitk_reduce adds the partials in order y = 0, 1, ...

@@ -35,6 +35,65 @@ __device__ __forceinline__ void grouped_tile(uint32_t id, uint32_t tiles_m, uint
     tn = in_group / gm;
 }
 
+// ---- passing data between workgroups of one launch -------------------------
+// The 8 XCDs each have their own L2, and an agent-scope release/acquire
+// fence writes back and invalidates an XCD's whole L2 (measured 4x slower
+// than a second launch).  Data handed from one workgroup to another instead
+// goes through the point of coherence: stored and loaded with the
+// device-scope cache policy (sc1: stores written through, loads missing in
+// L2), the storing wave waits for its stores to complete (vmcnt 0) before the
+// arrival counter's atomic add, and workgroup-scope fences order the rest.
+// The workgroup that arrives last (counter == expected - 1) resets the
+// counter, so counters are zero between launches.
+
+// s_waitcnt operand that waits for vmcnt 0 and leaves expcnt / lgkmcnt alone.
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
+// Cache-policy operand of the raw buffer load/store builtins on gfx950: sc1,
+// device scope (the access is coherent across the XCDs' L2 caches).
+constexpr int kCachePolicySc1 = 16;
+// Fourth word of a raw buffer resource on gfx9 (32-bit data format).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer over `bytes` bytes at `base` (bytes < 2^31).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_buffer(const void* base, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferRsrcWord3);
+}
+__device__ __forceinline__ void store_coherent(__amdgpu_buffer_rsrc_t buf, int byte_off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), buf, byte_off, 0, kCachePolicySc1);
+}
+__device__ __forceinline__ void store_coherent4(__amdgpu_buffer_rsrc_t buf, int byte_off, f32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), buf, byte_off, 0, kCachePolicySc1);
+}
+__device__ __forceinline__ float load_coherent(__amdgpu_buffer_rsrc_t buf, int byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(buf, byte_off, 0, kCachePolicySc1));
+}
+__device__ __forceinline__ f32x4 load_coherent4(__amdgpu_buffer_rsrc_t buf, int byte_off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(buf, byte_off, 0, kCachePolicySc1));
+}
+
+// Called by every thread of the workgroup after its coherent stores: true in
+// the workgroup that arrives last of `expected` at `*ctr` (which it then owns
+// and must reset with reset_arrival once done reading).  s_flag is a
+// __shared__ int of the caller.
+__device__ __forceinline__ bool arrive_last(unsigned* ctr, unsigned expected, int* s_flag) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *s_flag = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
+    __syncthreads();
+    const bool last = *s_flag != 0;
+    if (last) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
+    return last;
+}
+__device__ __forceinline__ void reset_arrival(unsigned* ctr) {
+    if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Activation codes match LANCIUS_HIP_ACT_* in lancius_hip.h.
 enum : int { kActNone = 0, kActRelu = 1, kActGelu = 2, kActTanh = 3 };
 
