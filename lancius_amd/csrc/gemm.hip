@@ -474,6 +474,173 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
     }
 }
 
+// 128x128 tiles, k-tiles of 16, 4 waves of 64x64, with both operand tiles
+// loaded straight from global memory into LDS (16-byte buffer loads with the
+// LDS as destination, gfx950): no register staging and no LDS store
+// instructions, and the next k-tile's loads have a whole k-tile of MFMAs to
+// land before the barrier that precedes their first read.  The two LDS
+// buffers are separate arrays and the loop is unrolled by two, so every
+// access names its buffer statically.
+//  * A (rows m0.., float4 chunks c of 4 k) lives m-major, 64 bytes per row;
+//    chunk c of row r sits at chunk c ^ ((r >> 2) & 3), so the 16-byte
+//    operand reads of 16 consecutive rows hit 16 different bank groups.
+//  * B (rows k, columns n0..) lives k-major, 512 bytes per row; chunk c of
+//    row k sits at chunk c ^ (8 * ((k >> 3) & 1)): the two lane halves, which
+//    read rows 8 apart, land on disjoint banks.
+//  * Elements past K are zero because their loads use an offset past the
+//    buffer's end (which returns 0); rows past M and columns past N read the
+//    last row / column and only reach entries of C that are never stored.
+// Requires A, B non-transposed and float4-aligned (K, N multiples of 4) and
+// both operands under 2 GiB.  A and B use the same k pairing as the AMK
+// path: lane half h of the MFMAs takes k in [8h, 8h + 8).
+template <int OCC>
+__global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) {
+    constexpr int BM = 128, BN = 128, BK = 16;
+    constexpr int WM = 64, WN = 64, TM = 2, TN = 2;
+    typedef __attribute__((address_space(3))) void lds_void;
+    __shared__ __attribute__((aligned(16))) float As0[BM * BK];
+    __shared__ __attribute__((aligned(16))) float As1[BM * BK];
+    __shared__ __attribute__((aligned(16))) float Bs0[BK * BN];
+    __shared__ __attribute__((aligned(16))) float Bs1[BK * BN];
+
+    const int g = blockIdx.z;
+    const float* __restrict__ A = p.A[g];
+    const float* __restrict__ B = p.B[g];
+    float* __restrict__ C = p.C[g];
+    const float* __restrict__ R = p.R[g];
+    const int M = p.M, N = p.N, K = p.K;
+    const uint32_t ntiles = p.tiles_m * p.tiles_n;
+    uint32_t tm_id, tn_id;
+    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
+    const int m0 = (int)tm_id * BM;
+    const int n0 = (int)tn_id * BN;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(A), 0, (int)((size_t)M * K * sizeof(float)), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(B), 0, (int)((size_t)K * N * sizeof(float)), kBufferRsrcWord3);
+    constexpr int kOut = 0x7ffffff0;  // an offset past the end of any operand: the load returns 0
+
+    // This lane's two chunks of each tile (instruction i of wave w fills LDS
+    // chunks (2w + i) * 64 + lane).  Byte offsets at k0 = 0; per k-tile A
+    // moves 64 bytes and B 16 rows.
+    int a_row[2], a_k[2], b_kr[2];
+    int a_off0[2], b_off0[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = (2 * wave + i) * 64 + lane;
+        const int row = q >> 2, c = (q & 3) ^ ((row >> 2) & 3);
+        a_row[i] = row;
+        a_k[i] = 4 * c;
+        a_off0[i] = (min(m0 + row, M - 1) * K + 4 * c) * (int)sizeof(float);
+        const int kr = q >> 5, lc = (q & 31) ^ (((kr >> 3) & 1) << 3);
+        b_kr[i] = kr;
+        b_off0[i] = (kr * N + min(n0 + 4 * lc, N - 4)) * (int)sizeof(float);
+    }
+    auto load_tile = [&](float* As, float* Bs, int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ao = k0 + a_k[i] < K ? a_off0[i] + k0 * (int)sizeof(float) : kOut;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(As + (2 * wave + i) * 256), 16, ao, 0, 0, 0);
+            const int bo = k0 + b_kr[i] < K ? b_off0[i] + k0 * N * (int)sizeof(float) : kOut;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (2 * wave + i) * 256), 16, bo, 0, 0, 0);
+        }
+        // keep the loads ahead of the MFMAs that follow (the scheduler would
+        // otherwise sink them to the wait before the barrier)
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // operand addresses (floats) of this lane, fixed over the k loop
+    int a_rd[TM][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = wm * WM + i * 32 + lr, c = 2 * lk + h;
+            a_rd[i][h] = row * BK + 4 * (c ^ ((row >> 2) & 3));
+        }
+    int b_rd[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = wn * WN + j * 32 + lr;
+        b_rd[j] = 8 * lk * BN + 4 * ((n >> 2) ^ (lk << 3)) + (n & 3);
+    }
+    auto compute = [&](const float* As, const float* Bs) {
+        f32x4 av[TM][2];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) av[i][h] = *(const f32x4*)(As + a_rd[i][h]);
+#pragma unroll
+        for (int kp = 0; kp < 8; ++kp) {
+            float bf[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = Bs[b_rd[j] + kp * BN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // k-tiles in pairs; when their count is odd the last pair's second tile
+    // lies wholly past K, loads as zeros and adds nothing.
+    const int pairs = (K + 2 * BK - 1) / (2 * BK);
+    load_tile(As0, Bs0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    for (int pr = 0; pr < pairs; ++pr) {
+        load_tile(As1, Bs1, 2 * pr + 1);
+        compute(As0, Bs0);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);
+        compute(As1, Bs1);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+    }
+
+    // ---- epilogue: bias, activation, residual, one store -----------------
+    const float* __restrict__ bias = p.bias[g];
+    const int act = p.act;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lr;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + 8 * (r >> 2) + (r & 3);
+                if (row < M) {
+                    float v = acc[i][j][r] + bv;
+                    v = apply_act(v, act);
+                    const size_t o = (size_t)row * N + col;
+                    if (R) v += R[o];
+                    C[o] = v;
+                }
+            }
+        }
+    }
+}
+
 // Skinny GEMM (M <= 16*MT): the product is bound by reading B once from
 // HBM (or, for tiny problems, by latency), so the kernel is organised around
 // that stream.
@@ -1052,6 +1219,16 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     }
     p.splits = (int)splits;
     p.kchunk = (int)(chunk_tiles * bk);
+    // 128x128 tiles loaded straight into LDS (gemm_f32_direct)
+    if (cfg == 6 && splits == 1 && vec && !ta && !tb && tune("gemm_direct", 1) &&
+        M * K * sizeof(float) < ((size_t)1 << 31) && K * N * sizeof(float) < ((size_t)1 << 31)) {
+        p.tiles_m = (uint32_t)((M + 127) / 128);
+        p.tiles_n = (uint32_t)((N + 127) / 128);
+        hipLaunchKernelGGL((gemm_f32_direct<4>), dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256), 0,
+                           ctx->stream, p);
+        if (int rc = check_launch("gemm_f32_direct")) return rc;
+        return ok();
+    }
     if (splits > 1) {
         void* ws = nullptr;
         if (int rc = partials(ctx, fixed, count * splits * M * N * sizeof(float), &ws)) return rc;
