@@ -270,12 +270,9 @@ struct I8Params {
 //
 // A k-tile's global loads are issued two tiles ahead of its use (two
 // register sets, even and odd tiles, and an LDS double buffer): at the LDS
-// store of tile t+1 the loads of tile t+2 stay in flight.  256 x 256 tiles
-// (8 waves of 128 x 64, one workgroup per CU) halve the bytes per MFMA
-// against 128 x 128.  Together these took 4096^3 from 106 to ~83 us; the
-// int8 pipes are still busy only about a third of the time (a pure-MFMA
-// loop reaches 0.9 of peak), the LDS fragment reads, the barrier-aligned
-// phases of the 8 waves and the loads not overlapping well enough.
+// store of tile t+1 the loads of tile t+2 stay in flight.  The implicit-GEMM
+// conv and GEMMs with fewer than ~240 256 x 256 tiles use this kernel; large
+// GEMMs use gemm_i8_direct.
 template <int BM, int BN, int WGM, int WGN, int BK, bool CONV, int MINW = 8 / (WGM * WGN)>
 __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Params p) {
     constexpr int LDK = BK + 16;
@@ -465,6 +462,214 @@ __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Par
     }
 }
 
+// GEMM only: 256 x 256 tiles, one workgroup of 4 waves per CU, each wave
+// a 128 x 128 block (16 accumulators of 32 x 32, so every 16-byte fragment
+// read from LDS feeds 4 MFMAs).  Both operands are k-contiguous ([M][Kp]
+// and B^T [N][Kp]) and are loaded straight into LDS with 16-byte buffer
+// loads (LDS destination): k-tiles of 128 bytes, two static buffers, the
+// next tile's loads issued ahead of the current tile's MFMAs.  In LDS a row
+// is 8 chunks of 16 bytes, chunk c stored at slot c ^ ((row >> 1) & 7): the
+// 16 rows one fragment read touches in a cycle fall on 16 distinct bank
+// groups.  Fragments of k-step s + 1 are read while the MFMAs of step s run.
+// Rows past M / N load as zeros (an offset past the buffer's end) and are
+// never stored; an odd last k-tile is paired with an all-zero one.
+// Requires (M + 1) * Kp and (N + 1) * Kp below 2^31 - 16.
+__global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
+    constexpr int BM = 256, BN = 256, BK = 128, TM = 4, TN = 4;
+    constexpr int kTileBytes = BM * BK;  // one operand's k-tile (BM == BN)
+    typedef __attribute__((address_space(3))) void lds_void;
+    __shared__ __attribute__((aligned(16))) int8_t As0[kTileBytes];
+    __shared__ __attribute__((aligned(16))) int8_t As1[kTileBytes];
+    __shared__ __attribute__((aligned(16))) int8_t Bs0[kTileBytes];
+    __shared__ __attribute__((aligned(16))) int8_t Bs1[kTileBytes];
+
+    const uint32_t ntiles = p.tiles_m * p.tiles_n;
+    uint32_t tm_id, tn_id;
+    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
+    const int m0 = (int)tm_id * BM, n0 = (int)tn_id * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lh = lane >> 5;
+    const int Kp = p.Kp;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.A), 0, (int)((size_t)p.M * Kp), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t*>(p.B), 0, (int)((size_t)p.N * Kp), kBufferRsrcWord3);
+    // Offsets are 32-bit unsigned.  A row past M (N) starts at M * Kp, the
+    // buffer's end, so it reads zeros at every k0 < Kp; the all-zero tail
+    // tile adds kOut = 2^31 - 16 to in-range offsets (< 2^31 - Kp), which
+    // lands past the end without wrapping (the host checks (M + 1) * Kp <
+    // 2^31 - 16, and the same for N).
+    constexpr unsigned kOut = 0x7ffffff0u;
+
+    // Instruction i of wave w fills LDS chunks (4i + w) * 64 + lane: tile row
+    // (4i + w) * 8 + lane / 8, slot lane % 8.  The slot's logical chunk is
+    // the same for every i.
+    const int sub_row = wave * 8 + (lane >> 3);
+    const int chunk = (lane & 7) ^ (((wave & 1) * 4 + (lane >> 4)) & 7);
+    unsigned a_off[8], b_off[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        a_off[i] = (unsigned)min(m0 + 32 * i + sub_row, p.M) * (unsigned)Kp + 16u * chunk;
+        b_off[i] = (unsigned)min(n0 + 32 * i + sub_row, p.N) * (unsigned)Kp + 16u * chunk;
+    }
+    auto load_tile = [&](int8_t* As, int8_t* Bs, int kt) {
+        const unsigned k0 = kt * BK < Kp ? (unsigned)(kt * BK) : kOut;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(As + (4 * i + wave) * 1024), 16,
+                                                     (int)(a_off[i] + k0), 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (4 * i + wave) * 1024), 16,
+                                                     (int)(b_off[i] + k0), 0, 0, 0);
+        // keep the loads ahead of the MFMAs that follow
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // fragment addresses (bytes) at k-step 0; step s reads chunk 2s + lh
+    int a_rd[TM], b_rd[TN], a_sw[TM], b_sw[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int row = wm * 128 + i * 32 + lr;
+        a_rd[i] = row * BK;
+        a_sw[i] = (row >> 1) & 7;
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int row = wn * 128 + j * 32 + lr;
+        b_rd[j] = row * BK;
+        b_sw[j] = (row >> 1) & 7;
+    }
+
+    v16i acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    auto read_frags = [&](const int8_t* As, const int8_t* Bs, int s, v4i* af, v4i* bf) {
+        const int c = 2 * s + lh;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = *(const v4i*)(As + a_rd[i] + 16 * (c ^ a_sw[i]));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[j] = *(const v4i*)(Bs + b_rd[j] + 16 * (c ^ b_sw[j]));
+    };
+    auto mfmas = [&](const v4i* af, const v4i* bf) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+    // One k-step: its 16 MFMAs with the next step's 8 fragment reads placed
+    // one after each of the first 8 (the reads land while MFMAs run).
+    auto step = [&](const v4i* af, const v4i* bf, const int8_t* As, const int8_t* Bs, int s_next, v4i* an,
+                    v4i* bn) {
+        read_frags(As, Bs, s_next, an, bn);
+        mfmas(af, bf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // One k-tile in buffer X (fragments of its step 0 already in f0), with
+    // tile kt + 1 landing in Y.  The barrier sits before the last step: by
+    // then every wave holds all of X's fragments, so X can take tile kt + 2
+    // and the last step's MFMAs cover the first reads of Y.
+    v4i fa0[TM], fb0[TN], fa1[TM], fb1[TN];
+    auto tile = [&](int8_t* Xa, int8_t* Xb, const int8_t* Ya, const int8_t* Yb, int kt) {
+        step(fa0, fb0, Xa, Xb, 1, fa1, fb1);
+        step(fa1, fb1, Xa, Xb, 2, fa0, fb0);
+        step(fa0, fb0, Xa, Xb, 3, fa1, fb1);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        load_tile(Xa, Xb, kt + 2);
+        step(fa1, fb1, Ya, Yb, 0, fa0, fb0);
+    };
+
+    // k-tiles in pairs; tiles at or past Kp load as zeros (an odd count's
+    // last pair adds nothing; the look-ahead past the end is never used).
+    const int pairs = (Kp / BK + 1) / 2;
+    load_tile(As0, Bs0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    load_tile(As1, Bs1, 1);
+    read_frags(As0, Bs0, 0, fa0, fb0);
+    for (int pr = 0; pr < pairs; ++pr) {
+        tile(As0, Bs0, As1, Bs1, 2 * pr);
+        tile(As1, Bs1, As0, Bs0, 2 * pr + 1);
+    }
+    // the last look-ahead loads land before the workgroup ends
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+
+    // int32 -> (double) * scale_a * scale_b -> fp32, then bias / act / residual.
+    // Register r of lane l: row 8(r/4) + 4(l/32) + r%4, column l%32.
+    // Epilogue staged through LDS (free now): each wave takes one of the four
+    // 32 KB arrays and, per half of its block (64 rows x 128 columns), writes
+    // the scaled values there, then reads whole rows back as float4 and
+    // stores them with bias, activation and residual: 64 row-contiguous
+    // 16-byte stores per lane instead of 256 scattered 4-byte ones.  Column
+    // c of row r sits at c ^ (32 * ((r >> 2) & 1)), so the two lane halves
+    // (rows 4 apart) write disjoint banks.
+    __syncthreads();
+    float* st = (float*)(wave == 0 ? As0 : wave == 1 ? As1 : wave == 2 ? Bs0 : Bs1);
+    const double scale = p.scale_a[0] * p.scale_b[0];
+    const bool vec = (p.N & 3) == 0 && ((uintptr_t)p.C & 15) == 0 && ((uintptr_t)p.R & 15) == 0 &&
+                     ((uintptr_t)p.bias & 15) == 0;
+    with_act(p.act, [&](auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int lrow = ii * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                        const int col = j * 32 + lr;
+                        st[lrow * 128 + (col ^ (((lrow >> 2) & 1) << 5))] =
+                            (float)((double)acc[2 * h + ii][j][r] * scale);
+                    }
+            // the wave reads back only what it wrote: LDS order within a wave
+#pragma unroll 4
+            for (int t = 0; t < 32; ++t) {
+                const int idx = t * 64 + lane, lrow = idx >> 5, c4 = 4 * (idx & 31);
+                const f32x4 v0 = *(const f32x4*)&st[lrow * 128 + (c4 ^ (((lrow >> 2) & 1) << 5))];
+                const int row = m0 + wm * 128 + h * 64 + lrow, col = n0 + wn * 128 + c4;
+                if (row >= p.M || col >= p.N) continue;
+                const size_t o = (size_t)row * p.N + col;
+                if (vec) {
+                    f32x4 v = v0;
+                    if (p.bias) v += *(const f32x4*)(p.bias + col);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = act_fixed<ACT>(v[e]);
+                    if (p.R) v += *(const f32x4*)(p.R + o);
+                    *(f32x4*)(p.C + o) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (col + e >= p.N) break;
+                        float v = v0[e];
+                        if (p.bias) v += p.bias[col + e];
+                        v = act_fixed<ACT>(v);
+                        if (p.R) v += p.R[o + e];
+                        p.C[o + e] = v;
+                    }
+                }
+            }
+        }
+    });
+}
+
 unsigned grid_for(size_t work) {
     return (unsigned)std::max<size_t>(1, std::min<size_t>((work + kThreads - 1) / kThreads, 4096));
 }
@@ -560,7 +765,10 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     p.tiles_n = (uint32_t)((N + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: too many tiles");
-    if (big && bk == 128)
+    if (big && bk == 128 && tune("gemm_i8_direct", 1) && (M + 1) * Kp < ((size_t)1 << 31) - 16 &&
+        (N + 1) * Kp < ((size_t)1 << 31) - 16)
+        hipLaunchKernelGGL(gemm_i8_direct, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p);
+    else if (big && bk == 128)
         hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 128, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,
                            p);
     else if (big)

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace lancius {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -116,6 +118,29 @@ __device__ __forceinline__ float apply_act(float x, int act) {
     if (act == kActGelu) return gelu_ref(x);
     if (act == kActTanh) return tanhf(x);
     return x;
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_fixed(float x) {
+    if constexpr (ACT == kActRelu) return relu_ref(x);
+    if constexpr (ACT == kActGelu) return gelu_ref(x);
+    if constexpr (ACT == kActTanh) return tanhf(x);
+    return x;
+}
+
+// Calls f(std::integral_constant<int, ACT>) for the activation code act.  A
+// fully unrolled epilogue written against the constant holds one
+// activation's code per element instead of all four: with hundreds of
+// outputs per lane the four-way version is tens of thousands of
+// instructions, and fetching them costs more than the stores.
+template <typename F>
+__device__ __forceinline__ void with_act(int act, F&& f) {
+    switch (act) {
+        case kActRelu: f(std::integral_constant<int, kActRelu>{}); break;
+        case kActGelu: f(std::integral_constant<int, kActGelu>{}); break;
+        case kActTanh: f(std::integral_constant<int, kActTanh>{}); break;
+        default: f(std::integral_constant<int, kActNone>{}); break;
+    }
 }
 
 }  // namespace lancius

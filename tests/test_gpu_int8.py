@@ -92,6 +92,27 @@ def test_gemm_i8_epilogue(dev, M, Kd, N):
     assert oracle.normwise_error(got, ref) <= TOL
 
 
+def test_gemm_i8_big_tiles_every_element(dev):
+    """256 x 256 tiles (240 of them) over 11 k-tiles of 128: an odd count,
+    ragged M and N; C starts as NaN, so an unwritten element fails."""
+    M, Kd, N = 4000, 1400, 3790
+    a = prng.normal(94, (M, Kd))
+    bq = np.round(prng.uniform(95, (Kd, N), -127.4, 127.4)).astype(np.int8)
+    da, db = dev.upload(a), dev.upload(bq)
+    dc = dev.upload(np.full((M, N), np.nan, np.float32))
+    case(f"gemm_i8 M={M} K={Kd} N={N} NaN-filled")
+    dev.gemm_i8(dc, da, db, 0.0021, M, Kd, N)
+    got = dev.download(dc, (M, N))
+    for b in (da, db, dc):
+        b.free()
+    assert np.isfinite(got).all()
+    # the oracle's quantizer, then the integer product through float64 BLAS:
+    # every partial sum is an integer below 2^53, so it is exact in any order
+    qa, sa = oracle.quantize_i8(f64(a).ravel())
+    ref = (qa.reshape(M, Kd).astype(np.float64) @ bq.astype(np.float64)) * (sa * 0.0021)
+    assert oracle.normwise_error(got, ref) <= TOL
+
+
 def _conv_i8(dev, x, wq, sw, stride, pad, act=ACT_NONE):
     N, Ci, H, W = x.shape
     Co, _, KH, KW = wq.shape
