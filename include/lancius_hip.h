@@ -297,6 +297,20 @@ LANCIUS_HIP_EXPORT int lancius_hip_quantize_i8(lancius_hip_ctx* ctx, int8_t* q, 
 LANCIUS_HIP_EXPORT int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, const int8_t* B,
                                                double scale_b, size_t M, size_t K, size_t N,
                                                const float* bias, int act, const float* residual);
+/* The same product split in two for a weight used many times: the reference
+ * walks b_int8 [K,N] column by column inside the product
+ * (lancius_scheduler.c:210-215); the device re-lays it once into the
+ * k-contiguous layout its int8 matrix cores read (B^T [N, Kp], k zero-padded
+ * to a multiple of 128: lancius_hip_i8_packed_bytes(K, N) bytes), and
+ * lancius_hip_gemm_i8p_f32 takes that packed copy in place of B.  Results are
+ * bit-identical to lancius_hip_gemm_i8_f32.  The device executor keeps one
+ * packed copy per int8 weight and re-packs it after an upload. */
+LANCIUS_HIP_EXPORT size_t lancius_hip_i8_packed_bytes(size_t K, size_t N);
+LANCIUS_HIP_EXPORT int lancius_hip_i8_pack_weight(lancius_hip_ctx* ctx, int8_t* packed, const int8_t* B, size_t K,
+                                                  size_t N);
+LANCIUS_HIP_EXPORT int lancius_hip_gemm_i8p_f32(lancius_hip_ctx* ctx, float* C, const float* A,
+                                                const int8_t* packed, double scale_b, size_t M, size_t K, size_t N,
+                                                const float* bias, int act, const float* residual);
 /* conv2d with int8 OIHW weights of scale scale_w and the fp32 NCHW input
  * quantized per tensor on the fly: kernel_conv2d_int8_fwd
  * (lancius_kernels.c:177-210) as routed by lancius_vision_ops.c:16-57;

@@ -258,6 +258,175 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
     }
 }
 
+// The per-channel path (C_in % 16 == 0, weights re-laid as wt) with both
+// operand tiles loaded straight from global memory into LDS (buffer loads
+// with LDS destination, gfx950), as the GEMM's direct kernel: no register
+// staging, the next k-tile's loads issued ahead of the current one's MFMAs.
+// 128 output channels x BN pixels per workgroup, 4 waves of 64 x BN/2,
+// k-tiles of 16 channels of one filter tap.
+//  * A: rows co of wt (16 floats of the tap's channel run), 16-byte loads,
+//    m-major in LDS with chunk c of row r at c ^ ((r >> 2) & 3).
+//  * B: the im2col tile, k-major: one wave instruction fills 64 pixels of
+//    one k-row with 4-byte loads.  A lane's pixel is fixed, so per filter tap
+//    it computes one base offset; a tap outside the (padded) image, a pixel
+//    past the batch and every load of a k-tile past the end use an offset
+//    past the input's end and read 0.
+// Requires the input and wt below 2 GiB.
+template <int BN, int KH_T, int KW_T>
+__global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p) {
+    constexpr int BM = 128, BK = 16, WM = 64, WN = BN / 2, TM = 2, TN = WN / 32;
+    constexpr int B_INSTR = BK * BN / 256;  // 4-byte instructions per wave per k-tile
+    typedef __attribute__((address_space(3))) void lds_void;
+    __shared__ __attribute__((aligned(16))) float As0[BM * BK];
+    __shared__ __attribute__((aligned(16))) float As1[BM * BK];
+    __shared__ __attribute__((aligned(16))) float Bs0[BK * BN];
+    __shared__ __attribute__((aligned(16))) float Bs1[BK * BN];
+
+    const int KH = KH_T > 0 ? KH_T : p.KH;
+    const int KW = KW_T > 0 ? KW_T : p.KW;
+    const int KHW = KH * KW;
+    const int H = p.H, W = p.W, Ho = p.Ho, Wo = p.Wo;
+    const int HWo = Ho * Wo;
+    const int C_in = p.C_in, C_out = p.C_out;
+    const unsigned HW4 = (unsigned)(H * W) * 4u;
+
+    const uint32_t ntiles = p.tiles_m * p.tiles_n;
+    uint32_t tm_id, tn_id;
+    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 2, tm_id, tn_id);
+    const int m0 = (int)tm_id * BM;
+    const long long P0 = (long long)tn_id * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.in), 0, (int)((size_t)p.N * C_in * H * W * sizeof(float)), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.wt), 0, (int)((size_t)C_out * KHW * C_in * sizeof(float)), kBufferRsrcWord3);
+    constexpr unsigned kOut = 0x7ffffff0u;  // past the end of either operand: the load returns 0
+
+    // B: instruction j of wave w fills k-row ((4j + w) * 64) / BN, pixels
+    // ((4j + w) * 64) % BN + lane; the pixel is the same for every j.
+    const int b_pix = BN == 64 ? lane : (wave & 1) * 64 + lane;
+    const long long P = P0 + b_pix;
+    const bool p_valid = P < p.Ptotal;
+    int n_img = 0, hi0 = 0, wi0 = 0;
+    if (p_valid) {
+        n_img = (int)(P / HWo);
+        const int rem = (int)(P - (long long)n_img * HWo);
+        const int ho = rem / Wo, wo = rem - (rem / Wo) * Wo;
+        hi0 = ho * p.stride - p.pad;
+        wi0 = wo * p.stride - p.pad;
+    }
+    const unsigned img_base = (unsigned)n_img * (unsigned)C_in * HW4;
+    // A: instruction i of wave w fills chunks (2w + i) * 64 + lane
+    int a_row[2], a_c[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int q = (2 * wave + i) * 64 + lane;
+        a_row[i] = min(m0 + (q >> 2), C_out - 1);
+        a_c[i] = (q & 3) ^ (((q >> 2) >> 2) & 3);
+    }
+    const int ctiles = C_in / BK;
+    const int ktiles = KHW * ctiles;
+    auto load_tile = [&](float* As, float* Bs, int kt) {
+        const bool live = kt < ktiles;
+        const int tap = live ? kt / ctiles : 0;
+        const int ci0 = (kt - tap * ctiles) * BK;
+        const int kh = tap / KW, kw = tap - (tap / KW) * KW;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const unsigned ao =
+                live ? (unsigned)(((a_row[i] * KHW + tap) * C_in + ci0 + 4 * a_c[i]) * (int)sizeof(float)) : kOut;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(As + (2 * wave + i) * 256), 16, (int)ao, 0, 0, 0);
+        }
+        const int hi = hi0 + kh, wi = wi0 + kw;
+        const bool inside = live && p_valid && hi >= 0 && hi < H && wi >= 0 && wi < W;
+        const unsigned pix = img_base + (unsigned)(hi * W + wi) * 4u + (unsigned)ci0 * HW4;
+#pragma unroll
+        for (int j = 0; j < B_INSTR; ++j) {
+            const int row = ((4 * j + wave) * 64) / BN;
+            const unsigned bo = inside ? pix + (unsigned)row * HW4 : kOut;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(Bs + (4 * j + wave) * 64), 4, (int)bo, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    int a_rd[TM][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = wm * WM + i * 32 + lr, c = 2 * lk + h;
+            a_rd[i][h] = row * BK + 4 * (c ^ ((row >> 2) & 3));
+        }
+    auto compute = [&](const float* As, const float* Bs) {
+        f32x4 av[TM][2];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) av[i][h] = *(const f32x4*)(As + a_rd[i][h]);
+#pragma unroll
+        for (int kp = 0; kp < 8; ++kp) {
+            float bf[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = Bs[(8 * lk + kp) * BN + wn * WN + j * 32 + lr];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    const int pairs = (ktiles + 1) / 2;
+    load_tile(As0, Bs0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    for (int pr = 0; pr < pairs; ++pr) {
+        load_tile(As1, Bs1, 2 * pr + 1);
+        compute(As0, Bs0);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);
+        compute(As1, Bs1);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+    }
+
+    // register r of lane l: channel row 8(r/4) + 4(l/32) + r%4, pixel l%32
+    const float* __restrict__ bias = p.bias;
+    with_act(p.act, [&](auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const long long Pc = P0 + wn * WN + j * 32 + lr;
+            if (Pc >= p.Ptotal) continue;
+            const int n_o = (int)(Pc / HWo);
+            const int pix = (int)(Pc - (long long)n_o * HWo);
+            float* obase = p.out + (size_t)n_o * C_out * HWo + pix;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int cbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int co = cbase + 8 * (r >> 2) + (r & 3);
+                    if (co < C_out) obase[(size_t)co * HWo] = act_fixed<ACT>(acc[i][j][r] + (bias ? bias[co] : 0.0f));
+                }
+            }
+        }
+    });
+}
+
 // wt[(co*KHW + tap)*C_in + ci] = w[(co*C_in + ci)*KHW + tap]: the OIHW
 // weights re-laid with the reduction index (tap, ci) major and C_out
 // contiguous, so the conv's A tiles are plain float4 row copies.
@@ -525,7 +694,12 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
                            dim3(256), 0, ctx->stream, (float*)ws, p.w, p.C_out, p.C_in, p.KH * p.KW);
         if (int rc = check_launch("conv_weights_per_co")) return rc;
     }
-    if (p.wt)
+    const int direct = tune("conv_direct", 1);
+    if (p.wt && BM == 128 && (BN == 64 || BN == 128) && direct &&
+        (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < ((size_t)1 << 31) - 64 &&
+        (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64)
+        hipLaunchKernelGGL((conv2d_direct<BN, KH_T, KW_T>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
+    else if (p.wt)
         hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
                            dim3(kThreads), 0, ctx->stream, p);
     else
@@ -586,9 +760,10 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     p.act = act;
     // Tiles (C_out x pixels): 0 = 128x128, 1 = 128x64, 2 = 64x64, 3 = 32x128,
     // the one whose channel extent covers C_out with the least padding.
-    // 128x64 measured best on the N32 64->128 56x56 config (78.6 TFLOP/s vs
-    // 72.3 for 128x128): twice the workgroups, a shorter tail; 64x64 for its
-    // dgrad (64 output channels: 238 -> 204 us against 32x128).
+    // 128x64 measured best on the N32 64->128 56x56 config (with the direct
+    // loads 100.9 TFLOP/s against 89.6 for 128x128): twice the workgroups, a
+    // shorter tail; 64x64 for its dgrad (64 output channels: 238 -> 204 us
+    // against 32x128).
     const int tile = tune("conv_tile", default_tile(C_out));
     const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
     return rc ? rc : ok();

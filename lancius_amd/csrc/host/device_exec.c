@@ -52,6 +52,14 @@ struct lancius_device_program {
     size_t* bytes;
     uint8_t* role;
     uint8_t* is_i8;  /* by id: INPUT holding int8 weights (1 byte per element) */
+    /* by id: an int8 GEMM weight's copy in the layout the int8 product reads
+     * (lancius_hip_i8_pack_weight), its [K, N], and whether the weight
+     * changed since it was packed (set by uploads and by handing out the
+     * buffer; lancius_device_run re-packs first) */
+    char** packed;
+    size_t* packed_k;
+    size_t* packed_n;
+    uint8_t* packed_stale;
     uint8_t* readable;
     int32_t** argmax;
     size_t* rows;
@@ -670,6 +678,13 @@ void lancius_device_program_destroy(lancius_device_program* p) {
     if (p->graph) lancius_hip_graph_destroy(p->graph);
     if (p->private_ctx) lancius_hip_ctx_destroy(p->private_ctx);
     if (p->arena) lancius_hip_free(p->ctx, p->arena);
+    if (p->packed)
+        for (uint32_t i = 0; i < p->n_ids; i++)
+            if (p->packed[i]) lancius_hip_free(p->ctx, p->packed[i]);
+    free(p->packed);
+    free(p->packed_k);
+    free(p->packed_n);
+    free(p->packed_stale);
     free(p->ptr);
     free(p->bytes);
     free(p->role);
@@ -786,7 +801,8 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         !CALLOC(c.chain_bias, ids) || !CALLOC(c.chain_res, ids) || !CALLOC(c.chain_act, ids) ||
         !CALLOC(c.mm_src, ids2) ||
         !CALLOC(p->ptr, ids) || !CALLOC(p->bytes, ids) || !CALLOC(p->role, ids) || !CALLOC(p->readable, ids) ||
-        !CALLOC(p->is_i8, ids) ||
+        !CALLOC(p->is_i8, ids) || !CALLOC(p->packed, ids) || !CALLOC(p->packed_k, ids) ||
+        !CALLOC(p->packed_n, ids) || !CALLOC(p->packed_stale, ids) ||
         !CALLOC(p->argmax, ids) || !CALLOC(p->rows, ids) || !CALLOC(birth, ids) || !CALLOC(last, ids) ||
         !CALLOC(pinned, ids)) {
         rc = LANCIUS_HIP_ERR_OOM;
@@ -1047,6 +1063,19 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         rc = lancius_hip_fill_f32(ctx, (float*)p->ptr[n->id], (float)n->attr_val, elems(n));
         if (rc) goto out;
     }
+    /* one packed copy per int8 GEMM weight, filled by the first run */
+    for (uint32_t i = 0; i < p->n_launches && !rc; i++) {
+        const launch_t* L = &p->launches[i];
+        const uint32_t w = L->m[0].in[1];
+        if (L->kind != L_GEMM || !L->i8 || p->packed[w]) continue;
+        void* buf = NULL;
+        rc = lancius_hip_malloc(ctx, &buf, lancius_hip_i8_packed_bytes(L->d[1], L->d[2]));
+        p->packed[w] = (char*)buf;
+        p->packed_k[w] = L->d[1];
+        p->packed_n[w] = L->d[2];
+        p->packed_stale[w] = 1;
+    }
+    if (rc) goto out;
     rc = lancius_hip_synchronize(ctx);
     if (!rc && (flags & LANCIUS_DEVICE_GRAPH)) {
         /* A private context keeps the workspace the graph captures away from
@@ -1087,9 +1116,9 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
     switch (L->kind) {
         case L_GEMM: {
             if (L->i8)
-                return lancius_hip_gemm_i8_f32(ctx, P(m->out), P(m->in[0]), (const int8_t*)prog->ptr[m->in[1]],
-                                               L->scale_w, L->d[0], L->d[1], L->d[2], P(m->in[2]), L->act,
-                                               P(m->in[3]));
+                return lancius_hip_gemm_i8p_f32(ctx, P(m->out), P(m->in[0]), (const int8_t*)prog->packed[m->in[1]],
+                                                L->scale_w, L->d[0], L->d[1], L->d[2], P(m->in[2]), L->act,
+                                                P(m->in[3]));
             float* C[MAXG];
             const float *A[MAXG], *B[MAXG], *bias[MAXG], *res[MAXG];
             for (uint32_t k = 0; k < L->count; k++) {
@@ -1195,8 +1224,23 @@ static int run_all(lancius_device_program* prog) {
     return 0;
 }
 
+/* Re-lay every int8 GEMM weight that changed since it was last packed, on
+ * the caller's stream (after its uploads, before the launches). */
+static int repack_stale(lancius_device_program* prog) {
+    for (uint32_t i = 0; i < prog->n_ids; i++) {
+        if (!prog->packed_stale[i]) continue;
+        const int rc = lancius_hip_i8_pack_weight(prog->ctx, (int8_t*)prog->packed[i], (const int8_t*)prog->ptr[i],
+                                                  prog->packed_k[i], prog->packed_n[i]);
+        if (rc) return rc;
+        prog->packed_stale[i] = 0;
+    }
+    return 0;
+}
+
 int lancius_device_run(lancius_device_program* prog) {
     if (!prog) return LANCIUS_HIP_ERR_NULL_PTR;
+    const int rc_pack = repack_stale(prog);
+    if (rc_pack) return rc_pack;
     if (!prog->private_ctx) return run_all(prog);
     /* graph mode.  On a stream of its own, the replay starts after the
      * caller's work and the caller's stream continues after it. */
@@ -1224,6 +1268,7 @@ int lancius_device_run(lancius_device_program* prog) {
 
 void* lancius_device_buffer(lancius_device_program* prog, const lancius_node* n) {
     if (!prog || !n || n->id >= prog->n_ids) return NULL;
+    if (prog->packed[n->id]) prog->packed_stale[n->id] = 1; /* the caller may write through it */
     return prog->ptr[n->id];
 }
 
@@ -1233,9 +1278,11 @@ int lancius_device_upload(lancius_device_program* prog, const lancius_node* n, c
     if (n->id >= prog->n_ids || (prog->role[n->id] != ROLE_INPUT && prog->role[n->id] != ROLE_CONST))
         return LANCIUS_HIP_ERR_UNSUPPORTED;
     const size_t e = elems(n);
-    if (prog->is_i8[n->id]) /* int8 weights take their int8 bytes */
-        return host_dtype == LANCIUS_DTYPE_INT8 ? lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e)
-                                                : LANCIUS_HIP_ERR_DTYPE;
+    if (prog->is_i8[n->id]) { /* int8 weights take their int8 bytes */
+        if (host_dtype != LANCIUS_DTYPE_INT8) return LANCIUS_HIP_ERR_DTYPE;
+        if (prog->packed[n->id]) prog->packed_stale[n->id] = 1;
+        return lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e);
+    }
     if (host_dtype == LANCIUS_DTYPE_FP32) return lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e * 4);
     if (host_dtype != LANCIUS_DTYPE_FP64) return LANCIUS_HIP_ERR_DTYPE;
     float* tmp = (float*)malloc(e * sizeof(float) + 1);
@@ -1266,6 +1313,7 @@ int lancius_device_upload_weights(lancius_device_program* prog, const char* path
             rc = fail(LANCIUS_HIP_ERR_DTYPE, "int8 weight stored as floating point");
         } else {
             t[i].dst = prog->ptr[n->id];
+            if (prog->packed[n->id]) prog->packed_stale[n->id] = 1;
             t[i].dst_dtype = prog->is_i8[n->id] ? LANCIUS_HIP_FILE_I8 : LANCIUS_HIP_FILE_F32;
             t[i].file_dtype = r->file_dtype == LANCIUS_DTYPE_INT8   ? LANCIUS_HIP_FILE_I8
                               : r->file_dtype == LANCIUS_DTYPE_FP32 ? LANCIUS_HIP_FILE_F32

@@ -94,20 +94,39 @@ __device__ double scale_from_partials(const float* __restrict__ part, int parts,
     return sc;
 }
 
-__device__ __forceinline__ int8_t quant(float v, double scale) { return (int8_t)(int)round((double)v / scale); }
-
-__device__ __forceinline__ uint32_t quant4(float a, float b, float c, float d, double sc) {
-    return (uint32_t)(uint8_t)quant(a, sc) | (uint32_t)(uint8_t)quant(b, sc) << 8 |
-           (uint32_t)(uint8_t)quant(c, sc) << 16 | (uint32_t)(uint8_t)quant(d, sc) << 24;
-}
+// The reference's quantized value: (int8) round(x / scale), the quotient
+// rounded to fp64 first, halves away from zero.  Fast path in fp32:
+// r = x * fl32(1 / scale) is within 1.5e-5 of x / scale (|x / scale| <=
+// 127.5, two roundings of 2^-24 relative), so when r's fraction is farther
+// than 1e-4 from one half, round(r) is the reference's integer.  The rest -
+// values near a half, NaN, and scales below 1e-30 whose reciprocal would
+// overflow fp32 - take the fp64 division.
+struct Quantizer {
+    double scale;
+    float inv;
+    bool fast;
+    __device__ explicit Quantizer(double s) : scale(s), inv((float)(1.0 / s)), fast(s >= 1e-30) {}
+    __device__ __forceinline__ int8_t operator()(float v) const {
+        if (fast) {
+            const float r = v * inv;
+            const float a = fabsf(r);
+            if (fabsf(a - floorf(a) - 0.5f) >= 1e-4f) return (int8_t)(int)roundf(r);
+        }
+        return (int8_t)(int)round((double)v / scale);
+    }
+    __device__ __forceinline__ uint32_t pack4(float a, float b, float c, float d) const {
+        return (uint32_t)(uint8_t)(*this)(a) | (uint32_t)(uint8_t)(*this)(b) << 8 |
+               (uint32_t)(uint8_t)(*this)(c) << 16 | (uint32_t)(uint8_t)(*this)(d) << 24;
+    }
+};
 
 // Row-major copy: q[i] = quant(x[i]).
 __global__ void __launch_bounds__(kThreads) quantize_flat(int8_t* __restrict__ q, const float* __restrict__ x,
                                                           const float* __restrict__ part, int parts,
                                                           double* __restrict__ scale_out, size_t n) {
-    const double sc = scale_from_partials(part, parts, scale_out, -1.0);
+    const Quantizer quant(scale_from_partials(part, parts, scale_out, -1.0));
     const size_t step = (size_t)gridDim.x * kThreads;
-    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += step) q[i] = quant(x[i], sc);
+    for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += step) q[i] = quant(x[i]);
 }
 
 // NCHW fp32 -> NHWC int8 with Cp >= C channels per pixel (padding bytes 0),
@@ -119,7 +138,7 @@ __global__ void __launch_bounds__(kThreads) quantize_nchw_to_nhwc(int8_t* __rest
                                                                   double* __restrict__ scale_out, double other, int N,
                                                                   int C, int HW, int Cp, int tiles_p, int tiles_c) {
     __shared__ int8_t t[64][65];
-    const double sc = scale_from_partials(part, parts, scale_out, other);
+    const Quantizer quant(scale_from_partials(part, parts, scale_out, other));
     const int tile = blockIdx.x;
     const int n = tile / (tiles_p * tiles_c);
     const int rem = tile - n * tiles_p * tiles_c;
@@ -129,7 +148,7 @@ __global__ void __launch_bounds__(kThreads) quantize_nchw_to_nhwc(int8_t* __rest
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int c = c0 + ty + 4 * i, p = p0 + tx;
-        t[ty + 4 * i][tx] = (c < C && p < HW) ? quant(xn[(size_t)c * HW + p], sc) : (int8_t)0;
+        t[ty + 4 * i][tx] = (c < C && p < HW) ? quant(xn[(size_t)c * HW + p]) : (int8_t)0;
     }
     __syncthreads();
     int8_t* qn = q + (size_t)n * HW * Cp;
@@ -198,13 +217,14 @@ __global__ void __launch_bounds__(kThreads) transpose_i8(int8_t* __restrict__ bt
 
 // A [M][K] fp32 -> [M][Kp] int8, zeros past K (Kp a multiple of 128, so a
 // row is D = Kp/4 words).  Each thread writes whole 32-bit words (vec: K % 4
-// == 0 and A 16-byte aligned, one float4 per word); rows shorter than the
-// workgroup share it, 256/D rows at a time.
+// == 0 and A 16-byte aligned, one float4 per word), four words per trip with
+// their loads issued together; rows shorter than the workgroup share it,
+// 256/D rows at a time.
 __global__ void __launch_bounds__(kThreads) quantize_rows_padded(int8_t* __restrict__ q, const float* __restrict__ x,
                                                                  const float* __restrict__ part, int parts,
                                                                  double* __restrict__ scale_out, double other,
                                                                  size_t M, int K, int Kp, int vec) {
-    const double sc = scale_from_partials(part, parts, scale_out, other);
+    const Quantizer quant(scale_from_partials(part, parts, scale_out, other));
     const int D = Kp / 4;
     const int rows_per = D >= kThreads ? 1 : kThreads / D;
     const int sub = D >= kThreads ? 0 : (int)threadIdx.x / D;
@@ -214,20 +234,27 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_padded(int8_t* __restr
     for (size_t r = (size_t)blockIdx.x * rows_per + sub; r < M; r += (size_t)gridDim.x * rows_per) {
         const float* __restrict__ xr = x + r * K;
         uint32_t* __restrict__ qr = (uint32_t*)(q + r * Kp);
-        for (int d = d0; d < D; d += dstep) {
-            const int k = 4 * d;
-            uint32_t packed = 0;
+        for (int d = d0; d < D; d += 4 * dstep) {
             if (vec) {
-                if (k < K) {
-                    const f32x4 v = *(const f32x4*)(xr + k);
-                    packed = quant4(v.x, v.y, v.z, v.w, sc);
-                }
-            } else {
+                f32x4 v[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (k + e < K) packed |= (uint32_t)(uint8_t)quant(xr[k + e], sc) << (8 * e);
+                for (int u = 0; u < 4; ++u) {
+                    const int k = 4 * (d + u * dstep);
+                    v[u] = k < K ? *(const f32x4*)(xr + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (d + u * dstep < D) qr[d + u * dstep] = quant.pack4(v[u].x, v[u].y, v[u].z, v[u].w);
+            } else {
+                for (int u = 0; u < 4 && d + u * dstep < D; ++u) {
+                    const int k = 4 * (d + u * dstep);
+                    uint32_t packed = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (k + e < K) packed |= (uint32_t)(uint8_t)quant(xr[k + e]) << (8 * e);
+                    qr[d + u * dstep] = packed;
+                }
             }
-            qr[d] = packed;
         }
     }
 }
@@ -474,6 +501,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Par
 // Rows past M / N load as zeros (an offset past the buffer's end) and are
 // never stored; an odd last k-tile is paired with an all-zero one.
 // Requires (M + 1) * Kp and (N + 1) * Kp below 2^31 - 16.
+template <bool MIXED_LOADS>
 __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
     constexpr int BM = 256, BN = 256, BK = 128, TM = 4, TN = 4;
     constexpr int kTileBytes = BM * BK;  // one operand's k-tile (BM == BN)
@@ -526,7 +554,7 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (4 * i + wave) * 1024), 16,
                                                      (int)(b_off[i] + k0), 0, 0, 0);
         // keep the loads ahead of the MFMAs that follow
-        __builtin_amdgcn_sched_barrier(0);
+        if (!MIXED_LOADS) __builtin_amdgcn_sched_barrier(0);
     };
 
     // fragment addresses (bytes) at k-step 0; step s reads chunk 2s + lh
@@ -567,15 +595,17 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
     };
     // One k-step: its 16 MFMAs with the next step's 8 fragment reads placed
-    // one after each of the first 8 (the reads land while MFMAs run).
+    // one after each of the first 8 (the reads land while MFMAs run), and,
+    // with `loads`, the 16 loads of a k-tile two after each MFMA.
     auto step = [&](const v4i* af, const v4i* bf, const int8_t* As, const int8_t* Bs, int s_next, v4i* an,
-                    v4i* bn) {
+                    v4i* bn, bool loads = false) {
         read_frags(As, Bs, s_next, an, bn);
         mfmas(af, bf);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            if (MIXED_LOADS && loads) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // global loads
         }
         __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -592,7 +622,7 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
         load_tile(Xa, Xb, kt + 2);
-        step(fa1, fb1, Ya, Yb, 0, fa0, fb0);
+        step(fa1, fb1, Ya, Yb, 0, fa0, fb0, true);
     };
 
     // k-tiles in pairs; tiles at or past Kp load as zeros (an odd count's
@@ -685,49 +715,44 @@ int absmax_partials_launch(lancius_hip_ctx* ctx, float* part, const float* x, si
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-}  // namespace
-}  // namespace lancius
+// k-tile of the int8 GEMMs: both operands are zero-padded in k to a
+// multiple of it.
+constexpr size_t kGemmBK = 128;
 
-using namespace lancius;
-
-extern "C" {
-
-int lancius_hip_quantize_i8(lancius_hip_ctx* ctx, int8_t* q, double* scale, const float* x, size_t n) {
-    LANCIUS_REQUIRE(ctx && q && scale && x, LANCIUS_HIP_ERR_NULL_PTR, "quantize_i8: NULL argument");
-    if (int rc = bind_device(ctx)) return rc;
-    void* ws = nullptr;
-    if (int rc = workspace(ctx, kMaxBlocks * sizeof(float), &ws)) return rc;
-    int parts = 0;
-    if (int rc = absmax_partials_launch(ctx, (float*)ws, x, n, &parts)) return rc;
-    // one workgroup at least: it stores the scale even for n == 0
-    hipLaunchKernelGGL(quantize_flat, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, q, x, (const float*)ws, parts,
-                       scale, n);
-    return check_launch("quantize_flat");
+// B [K][N] int8 -> B^T [N][Kp] (the layout both int8 GEMM kernels read).
+int pack_weight(lancius_hip_ctx* ctx, int8_t* bt, const int8_t* B, size_t K, size_t N) {
+    const size_t Kp = align_up(K, kGemmBK);
+    const int tiles_k = (int)(Kp / 128), tiles_n = (int)((N + 127) / 128);
+    LANCIUS_REQUIRE((size_t)tiles_k * tiles_n < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: B too large");
+    const int bvec = N % 16 == 0 && ((uintptr_t)B & 15u) == 0;
+    hipLaunchKernelGGL(transpose_i8, dim3((unsigned)(tiles_k * tiles_n)), dim3(kThreads), 0, ctx->stream, bt, B,
+                       (int)K, (int)N, (int)Kp, tiles_n, bvec);
+    return check_launch("transpose_i8");
 }
 
-int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, const int8_t* B, double scale_b,
-                            size_t M, size_t K, size_t N, const float* bias, int act, const float* residual) {
-    LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm_i8: NULL argument");
+int gemm_i8_check(size_t M, size_t K, size_t N, int act, double scale_b) {
     LANCIUS_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1u << 30) && N < (1u << 30) && K < (1u << 30),
                     LANCIUS_HIP_ERR_SHAPE, "gemm_i8: shape M=%zu K=%zu N=%zu", M, K, N);
     LANCIUS_REQUIRE(act >= LANCIUS_HIP_ACT_NONE && act <= LANCIUS_HIP_ACT_TANH, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "gemm_i8: activation %d", act);
-    if (int rc = bind_device(ctx)) return rc;
-    constexpr int BK = 128;
-    const size_t Kp = align_up(K, BK);
-    // workspace: scales (2 doubles) | absmax partials | A_q [M][Kp] | B^T [N][Kp]
-    const size_t off_part = 64, off_a = align_up(off_part + kMaxBlocks * sizeof(float), 256);
-    const size_t off_b = align_up(off_a + M * Kp, 256);
-    const size_t bytes = off_b + N * Kp;
-    LANCIUS_REQUIRE(bytes < ((size_t)1 << 36), LANCIUS_HIP_ERR_SHAPE, "gemm_i8: operands too large");
-    char* ws = nullptr;
-    if (int rc = workspace(ctx, bytes, (void**)&ws)) return rc;
-    double* scales = (double*)ws;
-    int8_t* aq = (int8_t*)(ws + off_a);
-    int8_t* bt = (int8_t*)(ws + off_b);
     // scale_b is a host value; the kernel reads both scales from device memory
     LANCIUS_REQUIRE(scale_b >= 0.0, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: negative scale");
-    float* part = (float*)(ws + off_part);
+    LANCIUS_REQUIRE(align_up(K, kGemmBK) * (M > N ? M : N) < ((size_t)1 << 36), LANCIUS_HIP_ERR_SHAPE,
+                    "gemm_i8: operands too large");
+    return 0;
+}
+
+// Workspace head: the two scales (doubles) and the absmax partials; A_q
+// [M][Kp] starts at this offset.
+size_t gemm_i8_a_offset() { return align_up(64 + kMaxBlocks * sizeof(float), 256); }
+
+// Quantize A into the workspace, then the int8 product with B^T [N][Kp].
+int gemm_i8_core(lancius_hip_ctx* ctx, char* ws, float* C, const float* A, const int8_t* bt, double scale_b,
+                 size_t M, size_t K, size_t N, const float* bias, int act, const float* residual) {
+    const size_t Kp = align_up(K, kGemmBK);
+    double* scales = (double*)ws;
+    float* part = (float*)(ws + 64);
+    int8_t* aq = (int8_t*)(ws + gemm_i8_a_offset());
     int parts = 0;
     if (int rc = absmax_partials_launch(ctx, part, A, M * K, &parts)) return rc;
     // A_q [M][Kp]: row r holds quant(A[r][k]) for k < K, zeros after; the
@@ -738,12 +763,6 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     hipLaunchKernelGGL(quantize_rows_padded, dim3(qblocks), dim3(kThreads), 0, ctx->stream, aq, A, (const float*)part,
                        parts, scales, scale_b, M, (int)K, (int)Kp, vec4);
     if (int rc = check_launch("quantize_rows_padded")) return rc;
-    const int tiles_k = (int)(Kp / 128), tiles_n = (int)((N + 127) / 128);
-    LANCIUS_REQUIRE((size_t)tiles_k * tiles_n < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: B too large");
-    const int bvec = N % 16 == 0 && ((uintptr_t)B & 15u) == 0;
-    hipLaunchKernelGGL(transpose_i8, dim3((unsigned)(tiles_k * tiles_n)), dim3(kThreads), 0, ctx->stream, bt, B,
-                       (int)K, (int)N, (int)Kp, tiles_n, bvec);
-    if (int rc = check_launch("transpose_i8")) return rc;
     I8Params p{};
     p.C = C;
     p.A = aq;
@@ -767,7 +786,8 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: too many tiles");
     if (big && bk == 128 && tune("gemm_i8_direct", 1) && (M + 1) * Kp < ((size_t)1 << 31) - 16 &&
         (N + 1) * Kp < ((size_t)1 << 31) - 16)
-        hipLaunchKernelGGL(gemm_i8_direct, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p);
+        hipLaunchKernelGGL(tune("gemm_i8_mixed", 0) ? gemm_i8_direct<true> : gemm_i8_direct<false>,
+                           dim3((unsigned)grid), dim3(256), 0, ctx->stream, p);
     else if (big && bk == 128)
         hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 128, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,
                            p);
@@ -777,7 +797,67 @@ int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, cons
     else
         hipLaunchKernelGGL((gemm_i8_mfma<128, 128, 2, 2, 128, false>), dim3((unsigned)grid), dim3(256), 0, ctx->stream,
                            p);
-    if (int rc = check_launch("gemm_i8_mfma")) return rc;
+    return check_launch("gemm_i8_mfma");
+}
+
+}  // namespace
+}  // namespace lancius
+
+using namespace lancius;
+
+extern "C" {
+
+int lancius_hip_quantize_i8(lancius_hip_ctx* ctx, int8_t* q, double* scale, const float* x, size_t n) {
+    LANCIUS_REQUIRE(ctx && q && scale && x, LANCIUS_HIP_ERR_NULL_PTR, "quantize_i8: NULL argument");
+    if (int rc = bind_device(ctx)) return rc;
+    void* ws = nullptr;
+    if (int rc = workspace(ctx, kMaxBlocks * sizeof(float), &ws)) return rc;
+    int parts = 0;
+    if (int rc = absmax_partials_launch(ctx, (float*)ws, x, n, &parts)) return rc;
+    // one workgroup at least: it stores the scale even for n == 0
+    hipLaunchKernelGGL(quantize_flat, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, q, x, (const float*)ws, parts,
+                       scale, n);
+    return check_launch("quantize_flat");
+}
+
+size_t lancius_hip_i8_packed_bytes(size_t K, size_t N) { return N * align_up(K, kGemmBK); }
+
+int lancius_hip_i8_pack_weight(lancius_hip_ctx* ctx, int8_t* packed, const int8_t* B, size_t K, size_t N) {
+    LANCIUS_REQUIRE(ctx && packed && B, LANCIUS_HIP_ERR_NULL_PTR, "i8_pack_weight: NULL argument");
+    LANCIUS_REQUIRE(N > 0 && K > 0 && N < (1u << 30) && K < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
+                    "i8_pack_weight: shape K=%zu N=%zu", K, N);
+    if (int rc = bind_device(ctx)) return rc;
+    if (int rc = pack_weight(ctx, packed, B, K, N)) return rc;
+    return ok();
+}
+
+int lancius_hip_gemm_i8p_f32(lancius_hip_ctx* ctx, float* C, const float* A, const int8_t* packed, double scale_b,
+                             size_t M, size_t K, size_t N, const float* bias, int act, const float* residual) {
+    LANCIUS_REQUIRE(ctx && C && A && packed, LANCIUS_HIP_ERR_NULL_PTR, "gemm_i8p: NULL argument");
+    if (int rc = gemm_i8_check(M, K, N, act, scale_b)) return rc;
+    if (int rc = bind_device(ctx)) return rc;
+    const size_t Kp = align_up(K, kGemmBK);
+    char* ws = nullptr;
+    if (int rc = workspace(ctx, gemm_i8_a_offset() + M * Kp, (void**)&ws)) return rc;
+    if (int rc = gemm_i8_core(ctx, ws, C, A, packed, scale_b, M, K, N, bias, act, residual)) return rc;
+    return ok();
+}
+
+int lancius_hip_gemm_i8_f32(lancius_hip_ctx* ctx, float* C, const float* A, const int8_t* B, double scale_b,
+                            size_t M, size_t K, size_t N, const float* bias, int act, const float* residual) {
+    LANCIUS_REQUIRE(ctx && C && A && B, LANCIUS_HIP_ERR_NULL_PTR, "gemm_i8: NULL argument");
+    if (int rc = gemm_i8_check(M, K, N, act, scale_b)) return rc;
+    if (int rc = bind_device(ctx)) return rc;
+    // workspace: scales | absmax partials | A_q [M][Kp] | B^T [N][Kp]
+    const size_t Kp = align_up(K, kGemmBK);
+    const size_t off_b = align_up(gemm_i8_a_offset() + M * Kp, 256);
+    const size_t bytes = off_b + N * Kp;
+    LANCIUS_REQUIRE(bytes < ((size_t)1 << 36), LANCIUS_HIP_ERR_SHAPE, "gemm_i8: operands too large");
+    char* ws = nullptr;
+    if (int rc = workspace(ctx, bytes, (void**)&ws)) return rc;
+    int8_t* bt = (int8_t*)(ws + off_b);
+    if (int rc = pack_weight(ctx, bt, B, K, N)) return rc;
+    if (int rc = gemm_i8_core(ctx, ws, C, A, bt, scale_b, M, K, N, bias, act, residual)) return rc;
     return ok();
 }
 

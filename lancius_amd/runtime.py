@@ -94,6 +94,10 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_rope_f32.argtypes = [vp, vp, vp] + [sz] * 5 + [i32]
     lib.lancius_hip_quantize_i8.argtypes = [vp, vp, vp, vp, sz]
     lib.lancius_hip_gemm_i8_f32.argtypes = [vp, vp, vp, vp, C.c_double, sz, sz, sz, vp, i32, vp]
+    lib.lancius_hip_gemm_i8p_f32.argtypes = [vp, vp, vp, vp, C.c_double, sz, sz, sz, vp, i32, vp]
+    lib.lancius_hip_i8_pack_weight.argtypes = [vp, vp, vp, sz, sz]
+    lib.lancius_hip_i8_packed_bytes.argtypes = [sz, sz]
+    lib.lancius_hip_i8_packed_bytes.restype = sz
     lib.lancius_hip_conv2d_i8_f32.argtypes = [vp, vp, vp, vp, C.c_double, vp] + [sz] * 9 + [i32]
     lib.lancius_hip_gemm_ex_f32.argtypes = [vp, vp, vp, vp, sz, sz, sz, i32, i32, vp, i32, vp]
     lib.lancius_hip_gemm_grouped_ex_f32.argtypes = [vp, sz, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp), sz, sz, sz,
@@ -360,6 +364,16 @@ class Device:
     def gemm_i8(self, C_, A, B_i8, scale_b, M, K, N, bias=None, act=ACT_NONE, residual=None) -> None:
         _check(self.lib.lancius_hip_gemm_i8_f32(self.ctx, _vp(C_), _vp(A), _vp(B_i8), float(scale_b), M, K, N,
                                                 _vp(bias), act, _vp(residual)))
+
+    def i8_packed_bytes(self, K, N) -> int:
+        return int(self.lib.lancius_hip_i8_packed_bytes(K, N))
+
+    def i8_pack_weight(self, packed, B_i8, K, N) -> None:
+        _check(self.lib.lancius_hip_i8_pack_weight(self.ctx, _vp(packed), _vp(B_i8), K, N))
+
+    def gemm_i8p(self, C_, A, packed, scale_b, M, K, N, bias=None, act=ACT_NONE, residual=None) -> None:
+        _check(self.lib.lancius_hip_gemm_i8p_f32(self.ctx, _vp(C_), _vp(A), _vp(packed), float(scale_b), M, K, N,
+                                                 _vp(bias), act, _vp(residual)))
 
     def conv2d_i8(self, out, x, w_i8, scale_w, bias, N, C_in, H, W, C_out, K_h, K_w, stride, pad,
                   act=ACT_NONE) -> None:

@@ -41,6 +41,28 @@ def test_quantize_bit_exact(dev, n):
         b.free()
 
 
+@pytest.mark.parametrize("top", [381.0, 127.0 / 8, 100.0])
+def test_quantize_exact_halves(dev, top):
+    """x / scale exactly k + 0.5 (scale = top / 127 is 3, 1/8 or 100/127):
+    the reference rounds the fp64 quotient half away from zero, so a
+    multiply by 1 / scale that lands a hair below the half must not decide
+    these.  The remaining entries sit one float step either side of them."""
+    sc = top / 127.0
+    halves = np.array([(k + 0.5) * sc for k in range(-127, 127)], np.float64)
+    x = np.concatenate([[top], halves.astype(np.float32), np.nextafter(halves.astype(np.float32), np.float32(np.inf)),
+                        np.nextafter(halves.astype(np.float32), np.float32(-np.inf))]).astype(np.float32)
+    n = x.size
+    dx, dq, ds = dev.upload(x), dev.alloc(n), dev.alloc(8)
+    case(f"quantize_i8 exact halves top={top}")
+    dev.quantize_i8(dq, ds, dx, n)
+    q = dev.download(dq, (n,), np.int8)
+    rq, rs = oracle.quantize_i8(f64(x))
+    assert float(dev.download(ds, (1,), np.float64)[0]) == rs
+    np.testing.assert_array_equal(q, rq)
+    for b in (dx, dq, ds):
+        b.free()
+
+
 def test_quantize_all_zero(dev):
     dx, dq, ds = dev.upload(np.zeros(100, np.float32)), dev.alloc(100), dev.alloc(8)
     case("quantize_i8 zeros")
@@ -111,6 +133,26 @@ def test_gemm_i8_big_tiles_every_element(dev):
     qa, sa = oracle.quantize_i8(f64(a).ravel())
     ref = (qa.reshape(M, Kd).astype(np.float64) @ bq.astype(np.float64)) * (sa * 0.0021)
     assert oracle.normwise_error(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,Kd,N", [(130, 70, 201), (4000, 1400, 3790), (33, 4096, 50)])
+def test_gemm_i8_packed_weight_bit_identical(dev, M, Kd, N):
+    """lancius_hip_i8_pack_weight once + lancius_hip_gemm_i8p_f32 gives the
+    bits of lancius_hip_gemm_i8_f32 (which packs on every call)."""
+    a = prng.normal(96 + M, (M, Kd))
+    bq = np.round(prng.uniform(97 + N, (Kd, N), -127.4, 127.4)).astype(np.int8)
+    bias = prng.normal(98, (N,))
+    da, db, dbias = dev.upload(a), dev.upload(bq), dev.upload(bias)
+    dpk = dev.alloc(dev.i8_packed_bytes(Kd, N))
+    c1, c2 = dev.alloc(4 * M * N), dev.alloc(4 * M * N)
+    case(f"gemm_i8p M={M} K={Kd} N={N}")
+    dev.i8_pack_weight(dpk, db, Kd, N)
+    dev.gemm_i8(c1, da, db, 0.0031, M, Kd, N, bias=dbias, act=ACT_RELU)
+    for _ in range(2):
+        dev.gemm_i8p(c2, da, dpk, 0.0031, M, Kd, N, bias=dbias, act=ACT_RELU)
+        np.testing.assert_array_equal(dev.download(c2, (M, N)), dev.download(c1, (M, N)))
+    for b in (da, db, dbias, dpk, c1, c2):
+        b.free()
 
 
 def _conv_i8(dev, x, wq, sw, stride, pad, act=ACT_NONE):
@@ -215,5 +257,36 @@ def test_int8_matmul_drop_in(dev):
     mm.contents.runtime_data = None
     na.contents.runtime_data = nb.contents.runtime_data = None
     nb.contents.runtime_data_int8 = None
+    lib.lancius_schedule_destroy(sched)
+    lib.lancius_graph_destroy(g)
+
+
+def test_int8_matmul_program_repacks_changed_weights(dev):
+    """A program keeps one packed copy of an int8 MATMUL weight.  A new
+    upload, and a write through lancius_device_buffer, must both reach the
+    next run."""
+    lib = graph_lib()
+    M, Kd, N = 96, 300, 130
+    g = lib.lancius_graph_create()
+    na, nb = lib.lancius_input(g, M, Kd), lib.lancius_input(g, Kd, N)
+    mm = lib.lancius_matmul(g, na, nb)
+    lib.lancius_graph_set_dtype(g, abi.DTYPE_FP32)
+    nb.contents.dtype = abi.DTYPE_INT8
+    nb.contents.scale = 0.004
+    sched = lib.lancius_ir_schedule(g)
+    case("int8 matmul program, weight re-uploaded")
+    prog = DeviceProgram(dev, g, sched)
+    a = prng.normal(99, (M, Kd))
+    prog.upload(na, a)
+    for seed, how in ((1, "upload"), (2, "upload"), (3, "buffer")):
+        bq = np.round(prng.uniform(200 + seed, (Kd, N), -127.4, 127.4)).astype(np.int8)
+        if how == "upload":
+            prog.upload(nb, bq)
+        else:
+            dev.write(prog.buffer(nb), bq)
+        prog.run()
+        got = prog.download(mm).reshape(M, N)
+        assert oracle.normwise_error(got, oracle.matmul_i8(f64(a), bq, 0.004)) <= TOL, (seed, how)
+    prog.close()
     lib.lancius_schedule_destroy(sched)
     lib.lancius_graph_destroy(g)
