@@ -786,7 +786,7 @@ int gemm_i8_core(lancius_hip_ctx* ctx, char* ws, float* C, const float* A, const
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: too many tiles");
     if (big && bk == 128 && tune("gemm_i8_direct", 1) && (M + 1) * Kp < ((size_t)1 << 31) - 16 &&
         (N + 1) * Kp < ((size_t)1 << 31) - 16)
-        hipLaunchKernelGGL(tune("gemm_i8_mixed", 0) ? gemm_i8_direct<true> : gemm_i8_direct<false>,
+        hipLaunchKernelGGL(tune("gemm_i8_mixed", 1) ? gemm_i8_direct<true> : gemm_i8_direct<false>,
                            dim3((unsigned)grid), dim3(256), 0, ctx->stream, p);
     else if (big && bk == 128)
         hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 128, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,
