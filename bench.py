@@ -773,7 +773,7 @@ def main() -> int:
     gflops = flops / (ms * 1e-3) / 1e9
     traffic = None
     if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("gemm_f32_mfma 4096^3")
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("gemm_f32_direct 4096^3")
     result = {
         "metric": METRIC,
         "value": round(gflops, 1),
