@@ -272,7 +272,7 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
 //    past the batch and every load of a k-tile past the end use an offset
 //    past the input's end and read 0.
 // Requires the input and wt below 2 GiB.
-template <int BN, int KH_T, int KW_T>
+template <int BN, int KH_T, int KW_T, bool MIX>
 __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p) {
     constexpr int BM = 128, BK = 16, WM = 64, WN = BN / 2, TM = 2, TN = WN / 32;
     constexpr int B_INSTR = BK * BN / 256;  // 4-byte instructions per wave per k-tile
@@ -351,7 +351,7 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
             const unsigned bo = inside ? pix + (unsigned)row * HW4 : kOut;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(Bs + (4 * j + wave) * 64), 4, (int)bo, 0, 0, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
+        if (!MIX) __builtin_amdgcn_sched_barrier(0);
     };
 
     f32x16 acc[TM][TN];
@@ -386,6 +386,16 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
         }
+        if (MIX) {
+            // the k-tile's loads one after each of the first MFMAs
+#pragma unroll
+            for (int i = 0; i < 2 + B_INSTR; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - 2 - B_INSTR, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     const int pairs = (ktiles + 1) / 2;
@@ -397,7 +407,7 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
         compute(As0, Bs0);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
-        if (pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);
+        if (MIX || pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);  // past the end: zeros
         compute(As1, Bs1);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
@@ -697,9 +707,11 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
     const int direct = tune("conv_direct", 1);
     if (p.wt && BM == 128 && (BN == 64 || BN == 128) && direct &&
         (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < ((size_t)1 << 31) - 64 &&
-        (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64)
-        hipLaunchKernelGGL((conv2d_direct<BN, KH_T, KW_T>), dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
-    else if (p.wt)
+        (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64) {
+        void (*kern)(const ConvParams) =
+            tune("conv_mix", 1) ? conv2d_direct<BN, KH_T, KW_T, true> : conv2d_direct<BN, KH_T, KW_T, false>;
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
+    } else if (p.wt)
         hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
                            dim3(kThreads), 0, ctx->stream, p);
     else

@@ -493,7 +493,7 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
 // Requires A, B non-transposed and float4-aligned (K, N multiples of 4) and
 // both operands under 2 GiB.  A and B use the same k pairing as the AMK
 // path: lane half h of the MFMAs takes k in [8h, 8h + 8).
-template <int OCC>
+template <int OCC, int MIX>
 __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) {
     constexpr int BM = 128, BN = 128, BK = 16;
     constexpr int WM = 64, WN = 64, TM = 2, TN = 2;
@@ -552,8 +552,9 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (2 * wave + i) * 256), 16, bo, 0, 0, 0);
         }
         // keep the loads ahead of the MFMAs that follow (the scheduler would
-        // otherwise sink them to the wait before the barrier)
-        __builtin_amdgcn_sched_barrier(0);
+        // otherwise sink them to the wait before the barrier); with MIX they
+        // go between the first MFMAs instead (see compute)
+        if (!MIX) __builtin_amdgcn_sched_barrier(0);
     };
 
     f32x16 acc[TM][TN];
@@ -596,6 +597,15 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
         }
+        if (MIX) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, MIX, 0);  // MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // global load
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - 4 * MIX, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     // k-tiles in pairs; when their count is odd the last pair's second tile
@@ -609,7 +619,9 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
         compute(As0, Bs0);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
-        if (pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);
+        // (with MIX unconditional, so the loads share the MFMAs' block: past
+        // K they read zeros, and the wait below covers them)
+        if (MIX || pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);
         compute(As1, Bs1);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
@@ -1224,8 +1236,16 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         M * K * sizeof(float) < ((size_t)1 << 31) && K * N * sizeof(float) < ((size_t)1 << 31)) {
         p.tiles_m = (uint32_t)((M + 127) / 128);
         p.tiles_n = (uint32_t)((N + 127) / 128);
-        hipLaunchKernelGGL((gemm_f32_direct<4>), dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256), 0,
-                           ctx->stream, p);
+        // the k-tile's four loads one after each of the first four MFMAs
+        // (measured 143.0 -> 144.4 TFLOP/s at 4096^3; a burst before the
+        // MFMAs, or one load per 2, 4 or 7 MFMAs, ran slower)
+        const int mix = tune("gemm_direct_mix", 1);
+        void (*kern)(const GemmParams) = mix == 1   ? gemm_f32_direct<4, 1>
+                                         : mix == 2 ? gemm_f32_direct<4, 2>
+                                         : mix == 4 ? gemm_f32_direct<4, 4>
+                                         : mix == 7 ? gemm_f32_direct<4, 7>
+                                                    : gemm_f32_direct<4, 0>;
+        hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256), 0, ctx->stream, p);
         if (int rc = check_launch("gemm_f32_direct")) return rc;
         return ok();
     }
