@@ -596,18 +596,27 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
     };
     // One k-step: its 16 MFMAs with the next step's 8 fragment reads placed
     // one after each of the first 8 (the reads land while MFMAs run), and,
-    // with `loads`, the 16 loads of a k-tile two after each MFMA.
+    // with `loads`, the 16 loads of a k-tile one after each MFMA.
     auto step = [&](const v4i* af, const v4i* bf, const int8_t* As, const int8_t* Bs, int s_next, v4i* an,
                     v4i* bn, bool loads = false) {
         read_frags(As, Bs, s_next, an, bn);
         mfmas(af, bf);
+        if (MIXED_LOADS && loads) {
+            // one global load after each of the 16 MFMAs
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            if (MIXED_LOADS && loads) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // global loads
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA
+                if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);             // global load
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
         __builtin_amdgcn_sched_barrier(0);
     };
     // One k-tile in buffer X (fragments of its step 0 already in f0), with
