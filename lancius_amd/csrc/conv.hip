@@ -262,8 +262,8 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
 // operand tiles loaded straight from global memory into LDS (buffer loads
 // with LDS destination, gfx950), as the GEMM's direct kernel: no register
 // staging, the next k-tile's loads issued ahead of the current one's MFMAs.
-// 128 output channels x BN pixels per workgroup, 4 waves of 64 x BN/2,
-// k-tiles of 16 channels of one filter tap.
+// BM (64 or 128) output channels x BN pixels per workgroup, 4 waves of
+// BM/2 x BN/2, k-tiles of 16 channels of one filter tap.
 //  * A: rows co of wt (16 floats of the tap's channel run), 16-byte loads,
 //    m-major in LDS with chunk c of row r at c ^ ((r >> 2) & 3).
 //  * B: the im2col tile, k-major: one wave instruction fills 64 pixels of
@@ -272,10 +272,11 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
 //    past the batch and every load of a k-tile past the end use an offset
 //    past the input's end and read 0.
 // Requires the input and wt below 2 GiB.
-template <int BN, int KH_T, int KW_T, bool MIX>
+template <int BM, int BN, int KH_T, int KW_T, bool MIX>
 __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p) {
-    constexpr int BM = 128, BK = 16, WM = 64, WN = BN / 2, TM = 2, TN = WN / 32;
-    constexpr int B_INSTR = BK * BN / 256;  // 4-byte instructions per wave per k-tile
+    constexpr int BK = 16, WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    constexpr int A_INSTR = BM * BK / 4 / 256;  // 16-byte instructions per wave per k-tile
+    constexpr int B_INSTR = BK * BN / 256;      // 4-byte instructions per wave per k-tile
     typedef __attribute__((address_space(3))) void lds_void;
     __shared__ __attribute__((aligned(16))) float As0[BM * BK];
     __shared__ __attribute__((aligned(16))) float As1[BM * BK];
@@ -321,11 +322,11 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
         wi0 = wo * p.stride - p.pad;
     }
     const unsigned img_base = (unsigned)n_img * (unsigned)C_in * HW4;
-    // A: instruction i of wave w fills chunks (2w + i) * 64 + lane
-    int a_row[2], a_c[2];
+    // A: instruction i of wave w fills chunks (A_INSTR * w + i) * 64 + lane
+    int a_row[A_INSTR], a_c[A_INSTR];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int q = (2 * wave + i) * 64 + lane;
+    for (int i = 0; i < A_INSTR; ++i) {
+        const int q = (A_INSTR * wave + i) * 64 + lane;
         a_row[i] = min(m0 + (q >> 2), C_out - 1);
         a_c[i] = (q & 3) ^ (((q >> 2) >> 2) & 3);
     }
@@ -337,10 +338,11 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
         const int ci0 = (kt - tap * ctiles) * BK;
         const int kh = tap / KW, kw = tap - (tap / KW) * KW;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < A_INSTR; ++i) {
             const unsigned ao =
                 live ? (unsigned)(((a_row[i] * KHW + tap) * C_in + ci0 + 4 * a_c[i]) * (int)sizeof(float)) : kOut;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(As + (2 * wave + i) * 256), 16, (int)ao, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_void*)(As + (A_INSTR * wave + i) * 256), 16, (int)ao, 0,
+                                                     0, 0);
         }
         const int hi = hi0 + kh, wi = wi0 + kw;
         const bool inside = live && p_valid && hi >= 0 && hi < H && wi >= 0 && wi < W;
@@ -389,11 +391,11 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
         if (MIX) {
             // the k-tile's loads one after each of the first MFMAs
 #pragma unroll
-            for (int i = 0; i < 2 + B_INSTR; ++i) {
+            for (int i = 0; i < A_INSTR + B_INSTR; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - 2 - B_INSTR, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - A_INSTR - B_INSTR, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -704,14 +706,17 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
                            dim3(256), 0, ctx->stream, (float*)ws, p.w, p.C_out, p.C_in, p.KH * p.KW);
         if (int rc = check_launch("conv_weights_per_co")) return rc;
     }
-    const int direct = tune("conv_direct", 1);
-    if (p.wt && BM == 128 && (BN == 64 || BN == 128) && direct &&
-        (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < ((size_t)1 << 31) - 64 &&
-        (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64) {
-        void (*kern)(const ConvParams) =
-            tune("conv_mix", 1) ? conv2d_direct<BN, KH_T, KW_T, true> : conv2d_direct<BN, KH_T, KW_T, false>;
-        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
-    } else if (p.wt)
+    if constexpr ((BM == 64 || BM == 128) && (BN == 64 || BN == 128)) {
+        if (p.wt && tune("conv_direct", 1) &&
+            (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < ((size_t)1 << 31) - 64 &&
+            (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64) {
+            void (*kern)(const ConvParams) = tune("conv_mix", 1) ? conv2d_direct<BM, BN, KH_T, KW_T, true>
+                                                                 : conv2d_direct<BM, BN, KH_T, KW_T, false>;
+            hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
+            return check_launch("conv2d_direct");
+        }
+    }
+    if (p.wt)
         hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
                            dim3(kThreads), 0, ctx->stream, p);
     else
