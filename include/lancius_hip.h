@@ -356,7 +356,8 @@ LANCIUS_HIP_EXPORT void lancius_hip_graph_destroy(lancius_hip_graph* graph);
  * lancius_scheduler.c:169-233, 284-308 for small batches, whose unfused form
  * (five launches) is bound by its launch count.  x [M][K1], W1 [K1][N1],
  * W2 [N1][N2], out [M][N2]; b1, b2 may be NULL.  Limits: M <= 64, N2 <= 64,
- * M*N1 <= 16384, N1*N2 <= 8192 (else -3).  Results equal the unfused
+ * M*N1 <= 16384, N1*N2 <= 8192, K1*max(M, N1) <= 2^28 (else -3).  Results
+ * equal the unfused
  * launches up to fp32 summation order; repeated calls give identical bits.
  * Uses the context's workspace and arrival counters, so calls on one context
  * are ordered by its stream. */

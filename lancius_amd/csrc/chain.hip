@@ -3,7 +3,8 @@
 // MATMUL -> +b -> SOFTMAX with 64 rows).  At that size every kernel of the
 // unfused chain (split-K GEMM, its reduce, GEMM, reduce, softmax) is a few
 // microseconds of work behind a fixed launch cost, so the chain is bound by
-// its number of dependent launches.  See mlp2_fused for the design.
+// its number of dependent launches.  See mlp2_split and mlp2_tiles for the
+// two designs.
 #include <math.h>
 
 #include <algorithm>
@@ -22,201 +23,457 @@ struct ChainParams {
     const float* b2;  // [N2] or null
     float* out;       // [M][N2]: probabilities (softmax) or y
     int32_t* argmax;  // [M] or null
-    float* ypart;     // [tiles_n][M][N2]: each column tile's share of y
+    float* part;      // mlp2_split: [row_blocks][ks][16][16 tiles_n] partial h; mlp2_tiles: [tiles_n][M][N2] y shares
     unsigned* counters;  // one arrival counter per row block, zero between launches
     int M, K1, N1, N2, act1, act2, softmax;
-    int vec;  // K1 and N1 multiples of 4, x and W1 16-byte aligned: float4 loads
-    int tiles_n;
+    int tiles_n;  // 16-column tiles of h
+    int ks;       // mlp2_split: K ranges per tile
+    int kchunk;   // mlp2_split: K per range, a multiple of 4
 };
 
-// Workgroup (column tile t of 16 columns of h, row block b of 16 rows):
-//  1. h[b, t] = act1(x[b] . W1[:, t] + b1[t]) over the whole K1: the x row
-//     block and the W1 column slab are staged in LDS (in K chunks of kFKC),
-//     the 4 waves take a quarter of each chunk's k-steps with
-//     v_mfma_f32_16x16x4_f32 and add their accumulators through LDS in wave
-//     order;
-//  2. y_t = h[b, t] . W2[t rows, :], the tile's share of the second layer,
-//     stored for the row block's reducer;
-//  3. the workgroup that arrives last at row block b's counter adds the
-//     tiles' shares in tile order, adds b2, applies act2, and runs each row's
-//     softmax and first-maximum argmax (one thread per row).
-// One hand-off between workgroups (through the point of coherence,
-// kernels.hpp); every sum runs in a fixed order, so repeated calls give
-// identical bits.
 // Limits of the chain (the small-batch regime it is for; lancius_hip.h):
-// rows, outputs, hidden values M * N1 and second-layer weights N1 * N2.
+// rows, outputs, hidden values M * N1, second-layer weights N1 * N2, and
+// x and W1 each within kMaxOperand values (32-bit buffer offsets).
 constexpr int kMaxRows = 64;
 constexpr int kMaxOut = 64;
 constexpr int kMaxH = 16384;
 constexpr int kMaxW2 = 8192;
+constexpr size_t kMaxOperand = size_t(1) << 28;
 constexpr int kFR = 16;     // rows of h per workgroup
 constexpr int kFC = 16;     // columns of h per workgroup
 constexpr int kFKC = 1024;  // K staged per chunk
 constexpr int kXP = kFKC + 4;  // x rows in LDS: lanes read rows r at k-steps (r*kXP + k) mod 64 distinct
+constexpr int kSplitMaxN1 = 256;  // mlp2_split: the reducer holds the block's whole h
+constexpr int kMaxSplit = 4;      // mlp2_split: K ranges per tile
+constexpr int kSplitMaxTiles = 16;  // mlp2_split by default: at most 16 * kMaxSplit arrivals per row block
+constexpr int kSplitMinK = 2048;    // and at least 256 KiB per workgroup of mlp2_tiles
+constexpr int kOut = 0x7ffffff0;  // a byte offset past the end of any operand: the load returns 0
+constexpr int kYPer = kFR * kMaxOut / 256;  // (row, output) pairs of a block per thread
 
-__global__ void __launch_bounds__(256) mlp2_fused(const ChainParams p) {
-    __shared__ __attribute__((aligned(16))) float Xs[kFR][kXP];    // x rows of the block, current K chunk
-    __shared__ __attribute__((aligned(16))) float Wsl[kFKC][kFC];  // W1 columns of the tile, current K chunk
-    __shared__ float red[4][kFR][kFC + 1];
-    __shared__ float Hs[kFR][kFC + 1];
-    __shared__ float W2s[kFC][64];
-    __shared__ float Ys[kFR][64];
-    __shared__ int s_flag;
+// Every global read is a buffer load whose offset is pushed past the end of
+// its operand where the element does not exist, so no load sits behind a
+// branch: the launch is a few microseconds long, and per-load exec-mask
+// branches cost as much as the loads themselves.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t operand(const float* base, size_t count) {
+    // a null operand gets no records: every load from it returns 0
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, base ? (int)(count * sizeof(float)) : 0,
+                                             kBufferRsrcWord3);
+}
+__device__ __forceinline__ float load1(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
 
-    const int tn = (int)blockIdx.x % p.tiles_n, rb = (int)blockIdx.x / p.tiles_n;
-    const int n0 = tn * kFC, m0 = rb * kFR;
-    const int M = p.M, K1 = p.K1, N1 = p.N1, N2 = p.N2;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int li = lane & 15, lq = lane >> 4;
+struct NoPrefetch {
+    __device__ void operator()() const {}
+};
 
-    // W2 rows of this tile, needed after phase 1: loaded first
-    for (int i = tid; i < kFC * N2; i += 256) {
-        const int k = i / N2, j = i % N2;
-        W2s[k][j] = n0 + k < N1 ? p.w2[(size_t)(n0 + k) * N2 + j] : 0.0f;
-    }
-
+// The 16 x 16 tile of x . W1 at rows m0.., columns n0.. over k in
+// [kbeg, kend), one f32x4 of partial sums per wave (register r of lane l:
+// row 4(l/16) + r, column l%16; the four waves' sums add up to the tile).
+// x and W1 are staged in LDS a kFKC chunk at a time: x with wave w loading
+// rows 4w .. 4w+3 with its lanes along k; W1 with four threads per k row, a
+// float4 of the 16 columns each.  Every LDS position the MFMA loop reads is
+// written (zeros past kend, M and N1), so the loop has no bounds checks.
+// prefetch() runs once, after the first chunk's loads are issued, so loads
+// of its own share their trip to memory.
+// VEC: K1 and N1 multiples of 4 (x and W1 rows hold whole float4s).
+template <bool VEC, class Prefetch>
+__device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float (*Xs)[kXP], float (*Wsl)[kFC], int m0,
+                                             int n0, int kbeg, int kend, int wave, int lane, Prefetch prefetch) {
+    const int tid = threadIdx.x, li = lane & 15, lq = lane >> 4;
+    const int M = p.M, K1 = p.K1, N1 = p.N1;
+    const __amdgpu_buffer_rsrc_t xb = operand(p.x, (size_t)M * K1), wb = operand(p.w1, (size_t)K1 * N1);
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kc = 0; kc < K1; kc += kFKC) {
-        const int kn = min(kFKC, K1 - kc);  // k of this chunk
-        if (kc > 0) __syncthreads();        // the previous chunk's reads are done
-        // x rows m0.. of the chunk (float4 along k) and W1 columns n0.. (one
-        // float4 per k and quarter of the 16 columns): every load of the
-        // chunk is issued before the first LDS store.
-        constexpr int kPer = kFR * kFKC / 4 / 256;  // float4 of each operand per thread
-        const int xq = (kn + 3) / 4;
-        f32x4 xv[kPer], wv[kPer];
+    for (int kc = kbeg; kc < kend; kc += kFKC) {
+        const int kn = min(kFKC, kend - kc);  // k of this chunk
+        const int trips = (kn + 127) / 128;   // MFMA trips of 128 k
+        const int kpad = 128 * trips;          // LDS k the trips read
+        if (kc > kbeg) __syncthreads();        // the previous chunk's reads are done
+        constexpr int kXT = kFKC / 4 / 64;         // float4 per x row per lane
+        constexpr int kWT = kFKC * kFC / 4 / 256;  // float4 of W1 per thread (64 k rows each)
+        f32x4 xv[4][kXT], wv[kWT];
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int i = tid + 256 * u;
-            const int r = i / xq, k = 4 * (i % xq);
-            f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (i < kFR * xq && m0 + r < M) {
-                const float* src = p.x + (size_t)(m0 + r) * K1 + kc + k;
-                if (p.vec && k + 4 <= kn) {
-                    v = *(const f32x4*)src;
+        for (int rr = 0; rr < 4; ++rr) {
+            const int r = 4 * wave + rr;
+            const bool row = m0 + r < M;
+            const unsigned base = ((unsigned)(m0 + r) * (unsigned)K1 + (unsigned)kc) * 4u;
+#pragma unroll
+            for (int t = 0; t < kXT; ++t) {
+                if (256 * t >= kpad) continue;
+                const int k = 4 * (lane + 64 * t);
+                if constexpr (VEC) {
+                    const unsigned off = row && k < kn ? base + 4u * k : (unsigned)kOut;
+                    xv[rr][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xb, (int)off, 0, 0));
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (k + j < kn) v[j] = src[j];
+                    for (int e = 0; e < 4; ++e)
+                        xv[rr][t][e] = load1(xb, row && k + e < kn ? base + 4u * (k + e) : (unsigned)kOut);
                 }
             }
-            xv[u] = v;
-            const int kw = i >> 2, c = 4 * (i & 3);
-            f32x4 w = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (kw < kn) {
-                const float* src = p.w1 + (size_t)(kc + kw) * N1 + n0 + c;
-                if (p.vec && n0 + c + 4 <= N1) {
-                    w = *(const f32x4*)src;
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (n0 + c + j < N1) w[j] = src[j];
-                }
-            }
-            wv[u] = w;
         }
 #pragma unroll
-        for (int u = 0; u < kPer; ++u) {
-            const int i = tid + 256 * u;
-            if (i < kFR * xq) {
-                const int r = i / xq, k = 4 * (i % xq);
-                Xs[r][k] = xv[u].x, Xs[r][k + 1] = xv[u].y, Xs[r][k + 2] = xv[u].z, Xs[r][k + 3] = xv[u].w;
+        for (int u = 0; u < kWT; ++u) {
+            if (64 * u >= kpad) continue;
+            const int i = tid + 256 * u, kw = i >> 2, c = n0 + 4 * (i & 3);
+            const unsigned base = ((unsigned)(kc + kw) * (unsigned)N1 + (unsigned)c) * 4u;
+            if constexpr (VEC) {
+                const unsigned off = kw < kn && c < N1 ? base : (unsigned)kOut;
+                wv[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wb, (int)off, 0, 0));
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    wv[u][e] = load1(wb, kw < kn && c + e < N1 ? base + 4u * e : (unsigned)kOut);
             }
-            if ((i >> 2) < kn) *(f32x4*)&Wsl[i >> 2][4 * (i & 3)] = wv[u];
+        }
+        if (kc == kbeg) prefetch();
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+            for (int t = 0; t < kXT; ++t) {
+                if (256 * t >= kpad) continue;
+                *(f32x4*)&Xs[4 * wave + rr][4 * (lane + 64 * t)] = xv[rr][t];  // kXP * 4 bytes is a multiple of 16
+            }
+#pragma unroll
+        for (int u = 0; u < kWT; ++u) {
+            if (64 * u >= kpad) continue;
+            const int i = tid + 256 * u;
+            *(f32x4*)&Wsl[i >> 2][4 * (i & 3)] = wv[u];
         }
         __syncthreads();
-        // wave w takes k-steps w, w + 4, ...; lane l holds A[row l%16][k + l/16]
-        // and B[k + l/16][column l%16]; eight steps' LDS reads are issued
-        // before their MFMAs
-        const int steps = (kn + 3) / 4;
-        for (int s0 = wave; s0 < steps; s0 += 32) {
+        // wave w takes k-steps w, w + 4, ...; lane l holds A[row l%16][k +
+        // l/16] and B[k + l/16][column l%16]; a trip's 16 LDS reads are
+        // issued before its 8 MFMAs
+        for (int tr = 0; tr < trips; ++tr) {
             float a[8], b[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int k = 4 * (s0 + 4 * u) + lq;
-                a[u] = k < kn ? Xs[li][k] : 0.0f;
-                b[u] = k < kn ? Wsl[k][li] : 0.0f;
+                const int k = 4 * (wave + 32 * tr + 4 * u) + lq;
+                a[u] = Xs[li][k];
+                b[u] = Wsl[k][li];
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
         }
     }
-    // register r of lane l: row 4(l/16) + r, column l%16
+    return acc;
+}
+
+// This thread's (row, output) pairs of a 16-row block: i = tid + 256 u is
+// row i / N2, output i % N2; valid when the pair exists and its row < M.
+struct RowPairs {
+    int r[kYPer], j[kYPer];
+    bool ok[kYPer];
+    __device__ RowPairs(int m0, int M, int N2) {
+#pragma unroll
+        for (int u = 0; u < kYPer; ++u) {
+            const int i = (int)threadIdx.x + 256 * u;
+            r[u] = i / N2;
+            j[u] = i - r[u] * N2;
+            ok[u] = i < kFR * N2 && m0 + r[u] < M;
+        }
+    }
+};
+
+// The block's outputs from Ys (y after b2 and act2, all rows written, the
+// caller has synchronised): the logits, or the reference's softmax
+// (lancius_scheduler.c:284-294) with one (row, output) pair per thread and
+// the same arithmetic (m = the row's maximum, e = expf(y - m), sum = the
+// e's added in output order, p = e / sum), then the first maximum of each
+// row's p scanning with '>' from -1e9 (B/examples/train_mnist.c:206-209).
+__device__ __forceinline__ void finish_rows(const ChainParams& p, const RowPairs& q, int m0, float (*Ys)[kMaxOut],
+                                            float (*Es)[kMaxOut]) {
+    const int M = p.M, N2 = p.N2, tid = threadIdx.x;
+    if (!p.softmax) {
+#pragma unroll
+        for (int u = 0; u < kYPer; ++u)
+            if (q.ok[u]) p.out[(m0 + q.r[u]) * N2 + q.j[u]] = Ys[q.r[u]][q.j[u]];
+        return;
+    }
+#pragma unroll
+    for (int u = 0; u < kYPer; ++u) {
+        if (!q.ok[u]) continue;
+        const float* yr = Ys[q.r[u]];
+        float m = yr[0];
+        for (int c = 1; c < N2; ++c) m = fmaxf(m, yr[c]);
+        Es[q.r[u]][q.j[u]] = expf(yr[q.j[u]] - m);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kYPer; ++u) {
+        if (!q.ok[u]) continue;
+        const float* er = Es[q.r[u]];
+        float sum = 0.0f;
+        for (int c = 0; c < N2; ++c) sum += er[c];
+        const float prob = er[q.j[u]] / sum;
+        p.out[(m0 + q.r[u]) * N2 + q.j[u]] = prob;
+        Ys[q.r[u]][q.j[u]] = prob;
+    }
+    if (!p.argmax) return;
+    __syncthreads();
+    if (tid < kFR && m0 + tid < M) {
+        float best = -1e9f;
+        int bi = 0;
+        for (int j = 0; j < N2; ++j) {
+            if (Ys[tid][j] > best) {
+                best = Ys[tid][j];
+                bi = j;
+            }
+        }
+        p.argmax[m0 + tid] = bi;
+    }
+}
+
+// mlp2_split, for N1 <= kSplitMaxN1.  Workgroup (row block b of 16 rows,
+// column tile t of 16 columns of h, K range q):
+//  1. the tile's partial x[b] . W1[q range, t] (hidden_tile; the four waves'
+//     sums added in wave order), stored for the row block's reducer;
+//  2. the workgroup that arrives last at row block b's counter (of
+//     tiles_n * ks) loads the block's partials together with W2, b1 and b2,
+//     forms h = act1(sum of the ks partials in range order + b1) in LDS,
+//     multiplies it by W2 with MFMAs (the waves split the output tiles, and
+//     K where there are fewer than four output tiles, and their sums add in
+//     wave order), adds b2, applies act2 and finishes the rows.
+// The K split spreads the first layer, nearly all of the work and of the
+// loaded bytes, over tiles_n * row_blocks * ks workgroups instead of
+// tiles_n * row_blocks, and the second layer needs no hand-off of its own.
+// It pays where there are few tiles and a long K (each workgroup of
+// mlp2_tiles would stream 128 * K1 bytes): the reducer's loads bypass the
+// caches (about 30 GB/s for one workgroup, measured) and arrivals at one
+// counter serialise (about 45 ns each), so with many tiles (the
+// 64 x 784 -> 256 MLP: 64 tiles, 256 arrivals) mlp2_tiles is faster (8.7
+// against 13.1 us).  One hand-off between workgroups (through the point of
+// coherence, kernels.hpp); every sum runs in a fixed order, so repeated
+// calls give identical bits.
+template <bool VEC>
+__global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
+    constexpr int kStage = kFR * kXP + kFKC * kFC;
+    __shared__ __attribute__((aligned(16))) float smem[kStage];
+    __shared__ float red[4][kFR][kFC + 1];
+    __shared__ float Ys[kFR][kMaxOut];
+    __shared__ float Es[kFR][kMaxOut];
+    __shared__ float B2s[kMaxOut];
+    __shared__ int s_flag;
+
+    const int ks = p.ks, kq = (int)blockIdx.x % ks, rest = (int)blockIdx.x / ks;
+    const int tn = rest % p.tiles_n, rb = rest / p.tiles_n;
+    const int n0 = tn * kFC, m0 = rb * kFR;
+    const int M = p.M, N1 = p.N1, N2 = p.N2;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15, lq = lane >> 4;
+    const int kbeg = kq * p.kchunk, kend = min(p.K1, kbeg + p.kchunk);
+
+    const f32x4 acc = hidden_tile<VEC>(p, reinterpret_cast<float(*)[kXP]>(smem),
+                                       reinterpret_cast<float(*)[kFC]>(smem + kFR * kXP), m0, n0, kbeg, kend, wave,
+                                       lane, NoPrefetch{});
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = acc[r];
+    __syncthreads();
+    const int N1p = p.tiles_n * kFC;  // h columns, padded to the tiles
+    const int blk = kFR * N1p;        // one range's partials of a block
+    const __amdgpu_buffer_rsrc_t part = coherent_buffer(p.part, (size_t)(M + kFR - 1) / kFR * ks * blk * sizeof(float));
+    {
+        const int r = tid >> 4, c = tid & 15;  // 256 threads = 16 x 16
+        const float v = ((red[0][r][c] + red[1][r][c]) + red[2][r][c]) + red[3][r][c];
+        store_coherent(part, ((rb * ks + kq) * blk + r * N1p + n0 + c) * (int)sizeof(float), v);
+    }
+    if (!arrive_last(p.counters + rb, (unsigned)(p.tiles_n * ks), &s_flag)) return;
+    reset_arrival(p.counters + rb);
+
+    // The reducer.  Thread tid holds h elements e = 4 (tid + 256 g), g <
+    // N1p / 64: row e / N1p, columns e % N1p .. +3.
+    constexpr int kHG = kFR * kSplitMaxN1 / 4 / 256;  // float4 groups per thread
+    constexpr int kW2T = kMaxW2 / 256;                // W2 values per thread
+    f32x4 hp[kMaxSplit][kHG];
+#pragma unroll
+    for (int s = 0; s < kMaxSplit; ++s)
+#pragma unroll
+        for (int g = 0; g < kHG; ++g) {
+            const int e = 4 * (tid + 256 * g);
+            const bool in = s < ks && e < blk;
+            hp[s][g] = load_coherent4(part, in ? ((rb * ks + s) * blk + e) * (int)sizeof(float) : kOut);
+        }
+    float w2v[kW2T];
+    const __amdgpu_buffer_rsrc_t w2b = operand(p.w2, (size_t)N1 * N2);
+#pragma unroll
+    for (int u = 0; u < kW2T; ++u) {
+        const int i = tid + 256 * u;
+        w2v[u] = load1(w2b, i < N1 * N2 ? 4u * i : (unsigned)kOut);
+    }
+    const __amdgpu_buffer_rsrc_t b1b = operand(p.b1, (size_t)N1);
+    f32x4 b1v[kHG];
+#pragma unroll
+    for (int g = 0; g < kHG; ++g) {
+        const int e = 4 * (tid + 256 * g), c = e % N1p;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) b1v[g][x] = load1(b1b, e < blk && c + x < N1 ? 4u * (c + x) : (unsigned)kOut);
+    }
+    const float b2r = load1(operand(p.b2, (size_t)N2), tid < N2 ? 4u * tid : (unsigned)kOut);
+
+    // h and W2 in LDS (the staging area is free: every wave has passed the
+    // arrival barrier).  Hs rows have pitch N1p + 4; W2s keeps W2's layout.
+    const int ldh = N1p + 4;
+    float* Hs = smem;
+    float* W2s = smem + kFR * ldh;
+    with_act(p.act1, [&](auto A) {
+#pragma unroll
+        for (int g = 0; g < kHG; ++g) {
+            const int e = 4 * (tid + 256 * g);
+            if (e >= blk) continue;
+            const int r = e / N1p, c = e % N1p;
+            f32x4 v = hp[0][g];
+#pragma unroll
+            for (int s = 1; s < kMaxSplit; ++s)
+                if (s < ks) v += hp[s][g];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) Hs[r * ldh + c + x] = act_fixed<decltype(A)::value>(v[x] + b1v[g][x]);
+        }
+    });
+#pragma unroll
+    for (int u = 0; u < kW2T; ++u) {
+        const int i = tid + 256 * u;
+        if (i < N1 * N2) W2s[i] = w2v[u];
+    }
+    if (tid < kMaxOut) B2s[tid] = b2r;
+    __syncthreads();
+
+    // y = h . W2: output tile t = w / parts of 16 outputs, K part w % parts
+    const int ytiles = (N2 + 15) / 16;
+    const int parts = ytiles == 1 ? 4 : ytiles == 2 ? 2 : 1;
+    const int yt = wave / parts, part_k = wave % parts;
+    const int steps = N1 / 4 + (N1 % 4 != 0);  // k-steps of 4 over N1
+    const int per = (steps + parts - 1) / parts;
+    f32x4 ya = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (yt < ytiles) {
+        const int col = 16 * yt + li;
+        const int s1 = min(steps, (part_k + 1) * per);
+        for (int s = part_k * per; s < s1; s += 4) {
+            // four steps' LDS reads ahead of their MFMAs (addresses past
+            // N1 stay inside the staging area and are masked)
+            float a[4], b[4];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const int k = 4 * (s + x) + lq;
+                const bool in = s + x < s1 && k < N1;
+                a[x] = in ? Hs[li * ldh + k] : 0.0f;
+                b[x] = in && col < N2 ? W2s[k * N2 + col] : 0.0f;
+            }
+#pragma unroll
+            for (int x = 0; x < 4; ++x) ya = __builtin_amdgcn_mfma_f32_16x16x4f32(a[x], b[x], ya, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = ya[r];
+    __syncthreads();
+    const RowPairs q(m0, M, N2);
+#pragma unroll
+    for (int u = 0; u < kYPer; ++u) {
+        if (!q.ok[u]) continue;
+        const int t = q.j[u] / 16, c = q.j[u] % 16;
+        float y = red[t * parts][q.r[u]][c];
+        for (int k = 1; k < parts; ++k) y += red[t * parts + k][q.r[u]][c];
+        Ys[q.r[u]][q.j[u]] = apply_act(y + B2s[q.j[u]], p.act2);
+    }
+    __syncthreads();
+    finish_rows(p, q, m0, Ys, Es);
+}
+
+// mlp2_tiles, for any N1 within the limits.  Workgroup (column tile t of 16
+// columns of h, row block b of 16 rows):
+//  1. h[b, t] = act1(x[b] . W1[:, t] + b1[t]) over the whole K1
+//     (hidden_tile; the four waves' sums added in wave order);
+//  2. y_t = h[b, t] . W2[t rows, :], the tile's share of the second layer,
+//     stored for the row block's reducer;
+//  3. the workgroup that arrives last at row block b's counter adds the
+//     tiles' shares in tile order, adds b2, applies act2 and finishes the
+//     rows.
+// One hand-off between workgroups; every sum runs in a fixed order, so
+// repeated calls give identical bits.
+template <bool VEC>
+__global__ void __launch_bounds__(256) mlp2_tiles(const ChainParams p) {
+    __shared__ __attribute__((aligned(16))) float Xs[kFR][kXP];    // x rows of the block, current K chunk
+    __shared__ __attribute__((aligned(16))) float Wsl[kFKC][kFC];  // W1 columns of the tile, current K chunk
+    __shared__ float red[4][kFR][kFC + 1];
+    __shared__ float Hs[kFR][kFC + 1];
+    __shared__ float W2s[kFC * kMaxOut];  // W2 rows of the tile, row pitch N2
+    __shared__ float B2s[kMaxOut];
+    __shared__ float Ys[kFR][kMaxOut];
+    __shared__ float Es[kFR][kMaxOut];
+    __shared__ int s_flag;
+
+    const int tn = (int)blockIdx.x % p.tiles_n, rb = (int)blockIdx.x / p.tiles_n;
+    const int n0 = tn * kFC, m0 = rb * kFR;
+    const int M = p.M, N1 = p.N1, N2 = p.N2;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15, lq = lane >> 4;
+
+    // W2 rows n0.. (one contiguous run of kFC * N2 values), this thread's
+    // b1 column and b2 output: loaded with the first K chunk, so the launch
+    // makes one trip to memory for its inputs
+    constexpr int kW2Per = kFC * kMaxOut / 256;
+    float w2r[kW2Per], b1r = 0.0f, b2r = 0.0f;
+    const f32x4 acc = hidden_tile<VEC>(p, Xs, Wsl, m0, n0, 0, p.K1, wave, lane, [&] {
+        const __amdgpu_buffer_rsrc_t w2b = operand(p.w2, (size_t)N1 * N2);
+        const int run = min(kFC, N1 - n0) * N2;  // W2 values of the tile
+#pragma unroll
+        for (int u = 0; u < kW2Per; ++u) {
+            const int i = tid + 256 * u;
+            w2r[u] = load1(w2b, i < run ? (unsigned)(n0 * N2 + i) * 4u : (unsigned)kOut);
+        }
+        const int c = n0 + (tid & 15);
+        b1r = load1(operand(p.b1, (size_t)N1), c < N1 ? 4u * c : (unsigned)kOut);
+        b2r = load1(operand(p.b2, (size_t)N2), tid < N2 ? 4u * tid : (unsigned)kOut);
+    });
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = acc[r];
+#pragma unroll
+    for (int u = 0; u < kW2Per; ++u) W2s[tid + 256 * u] = w2r[u];  // zeros past the tile's rows
+    if (tid < kMaxOut) B2s[tid] = b2r;
     __syncthreads();
     {
         const int r = tid >> 4, c = tid & 15;  // 256 threads = 16 x 16
         const float v = ((red[0][r][c] + red[1][r][c]) + red[2][r][c]) + red[3][r][c];
         float h = 0.0f;
-        if (m0 + r < M && n0 + c < N1) h = apply_act(v + (p.b1 ? p.b1[n0 + c] : 0.0f), p.act1);
+        if (m0 + r < M && n0 + c < N1) h = apply_act(v + b1r, p.act1);
         Hs[r][c] = h;  // rows past M and columns past N1 hold 0
     }
     __syncthreads();
     // this tile's share of y for the block's rows
-    const size_t MN2 = (size_t)M * N2;
-    const __amdgpu_buffer_rsrc_t ypart = coherent_buffer(p.ypart, (size_t)p.tiles_n * MN2 * sizeof(float));
-    for (int i = tid; i < kFR * N2; i += 256) {
-        const int r = i / N2, j = i % N2;
-        if (m0 + r >= M) continue;
+    const RowPairs q(m0, M, N2);
+    const int MN2 = M * N2;
+    const __amdgpu_buffer_rsrc_t ypart = coherent_buffer(p.part, (size_t)p.tiles_n * MN2 * sizeof(float));
+#pragma unroll
+    for (int u = 0; u < kYPer; ++u) {
+        if (!q.ok[u]) continue;
         float a = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kFC; ++k) a += Hs[r][k] * W2s[k][j];
-        store_coherent(ypart, (int)(((size_t)tn * MN2 + (size_t)(m0 + r) * N2 + j) * sizeof(float)), a);
+        for (int k = 0; k < kFC; ++k) a += Hs[q.r[u]][k] * W2s[k * N2 + q.j[u]];
+        store_coherent(ypart, (tn * MN2 + (m0 + q.r[u]) * N2 + q.j[u]) * (int)sizeof(float), a);
     }
     if (!arrive_last(p.counters + rb, (unsigned)p.tiles_n, &s_flag)) return;
     reset_arrival(p.counters + rb);
 
     // the block's rows: y = sum of the tiles' shares in tile order + b2
-    {
+    // (loads past the last tile fall outside the buffer and return 0)
+#pragma unroll
+    for (int u = 0; u < kYPer; ++u) {
+        if (!q.ok[u]) continue;
         constexpr int kChunk = 16;
-        for (int i = tid; i < kFR * N2; i += 256) {
-            const int r = i / N2, j = i % N2;
-            if (m0 + r >= M) continue;
-            const int off = (int)(((size_t)(m0 + r) * N2 + j) * sizeof(float));
-            float y = 0.0f;
-            for (int t0 = 0; t0 < p.tiles_n; t0 += kChunk) {
-                float t[kChunk];
+        const int off = ((m0 + q.r[u]) * N2 + q.j[u]) * (int)sizeof(float);
+        float y = 0.0f;
+        for (int t0 = 0; t0 < p.tiles_n; t0 += kChunk) {
+            float t[kChunk];
 #pragma unroll
-                for (int c = 0; c < kChunk; ++c)
-                    t[c] = t0 + c < p.tiles_n
-                               ? load_coherent(ypart, off + (int)((size_t)(t0 + c) * MN2 * sizeof(float)))
-                               : 0.0f;
+            for (int c = 0; c < kChunk; ++c) t[c] = load_coherent(ypart, off + (t0 + c) * MN2 * (int)sizeof(float));
 #pragma unroll
-                for (int c = 0; c < kChunk; ++c)
-                    if (t0 + c < p.tiles_n) y = (t0 + c == 0) ? t[c] : y + t[c];
-            }
-            Ys[r][j] = apply_act(y + (p.b2 ? p.b2[j] : 0.0f), p.act2);
+            for (int c = 0; c < kChunk; ++c)
+                if (t0 + c < p.tiles_n) y = (t0 + c == 0) ? t[c] : y + t[c];
         }
+        Ys[q.r[u]][q.j[u]] = apply_act(y + B2s[q.j[u]], p.act2);
     }
     __syncthreads();
-    // One thread per row: the reference's serial loops, max, exp, sum,
-    // divide (lancius_scheduler.c:284-294), then the first maximum scanning
-    // with '>' from -1e9 (B/examples/train_mnist.c:206-209).
-    if (tid < kFR && m0 + tid < M) {
-        const int r = m0 + tid;
-        const float* yr = Ys[tid];
-        float* o = p.out + (size_t)r * N2;
-        if (!p.softmax) {
-            for (int j = 0; j < N2; ++j) o[j] = yr[j];
-        } else {
-            float m = yr[0];
-            for (int j = 1; j < N2; ++j) m = fmaxf(m, yr[j]);
-            float sum = 0.0f;
-            for (int j = 0; j < N2; ++j) sum += expf(yr[j] - m);
-            float best = -1e9f;
-            int bi = 0;
-            for (int j = 0; j < N2; ++j) {
-                const float pv = expf(yr[j] - m) / sum;
-                o[j] = pv;
-                if (pv > best) {
-                    best = pv;
-                    bi = j;
-                }
-            }
-            if (p.argmax) p.argmax[r] = bi;
-        }
-    }
+    finish_rows(p, q, m0, Ys, Es);
 }
 
 }  // namespace
@@ -236,7 +493,7 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
                                        int act2, size_t M, size_t K1, size_t N1, size_t N2, int softmax) {
     LANCIUS_REQUIRE(ctx && out && x && w1 && w2, LANCIUS_HIP_ERR_NULL_PTR, "mlp2: NULL argument");
     LANCIUS_REQUIRE(M >= 1 && M <= (size_t)kMaxRows && N2 >= 1 && N2 <= (size_t)kMaxOut && N1 >= 1 && K1 >= 1 &&
-                        M * N1 <= (size_t)kMaxH && N1 * N2 <= (size_t)kMaxW2 && K1 < (1u << 30),
+                        M * N1 <= (size_t)kMaxH && N1 * N2 <= (size_t)kMaxW2 && K1 * std::max(M, N1) <= kMaxOperand,
                     LANCIUS_HIP_ERR_SHAPE, "mlp2: M=%zu K1=%zu N1=%zu N2=%zu outside the fused chain's limits", M, K1,
                     N1, N2);
     LANCIUS_REQUIRE(act1 >= LANCIUS_HIP_ACT_NONE && act1 <= LANCIUS_HIP_ACT_TANH && act2 >= LANCIUS_HIP_ACT_NONE &&
@@ -258,14 +515,32 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
     p.act1 = act1;
     p.act2 = act2;
     p.softmax = softmax ? 1 : 0;
-    p.vec = K1 % 4 == 0 && N1 % 4 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)w1 & 15u) == 0;
+    const bool vec = K1 % 4 == 0 && N1 % 4 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)w1 & 15u) == 0;
     p.tiles_n = (int)((N1 + kFC - 1) / kFC);
     const size_t row_blocks = (M + kFR - 1) / kFR;
-    void* ws = nullptr;
-    if (int rc = workspace(ctx, (size_t)p.tiles_n * M * N2 * sizeof(float), &ws)) return rc;
-    p.ypart = (float*)ws;
+    const size_t tiles = row_blocks * (size_t)p.tiles_n;
     if (int rc = counters(ctx, row_blocks, &p.counters)) return rc;
-    hipLaunchKernelGGL(mlp2_fused, dim3((unsigned)(p.tiles_n * row_blocks)), dim3(256), 0, ctx->stream, p);
-    if (int rc = check_launch("mlp2_fused")) return rc;
+    void* ws = nullptr;
+    const int split = tune("mlp2_split", -1);  // 0: never, 1: whenever N1 allows, -1: few tiles with a long K
+    if ((size_t)p.tiles_n * kFC <= (size_t)kSplitMaxN1 &&
+        (split == 1 || (split < 0 && tiles <= kSplitMaxTiles && K1 >= kSplitMinK))) {
+        // K ranges of at least 64 that bring the grid to about one
+        // workgroup per CU
+        int ks = (int)std::max<size_t>(1, std::min<size_t>(kMaxSplit, 256 / tiles));
+        while (ks > 1 && K1 < (size_t)ks * 64) --ks;
+        p.kchunk = (int)((K1 + ks - 1) / ks + 3) / 4 * 4;
+        p.ks = (int)((K1 + p.kchunk - 1) / p.kchunk);
+        if (int rc = workspace(ctx, row_blocks * p.ks * kFR * p.tiles_n * kFC * sizeof(float), &ws)) return rc;
+        p.part = (float*)ws;
+        hipLaunchKernelGGL(vec ? mlp2_split<true> : mlp2_split<false>, dim3((unsigned)(tiles * p.ks)), dim3(256), 0,
+                           ctx->stream, p);
+        if (int rc = check_launch("mlp2_split")) return rc;
+        return ok();
+    }
+    if (int rc = workspace(ctx, (size_t)p.tiles_n * M * N2 * sizeof(float), &ws)) return rc;
+    p.part = (float*)ws;
+    hipLaunchKernelGGL(vec ? mlp2_tiles<true> : mlp2_tiles<false>, dim3((unsigned)tiles), dim3(256), 0, ctx->stream,
+                       p);
+    if (int rc = check_launch("mlp2_tiles")) return rc;
     return ok();
 }

@@ -112,9 +112,9 @@ static int act_of(basis_op_type op) {
 /* MATMUL(x, W1) [-> BROADCAST_ADD(b1)] [-> RELU|TANH] -> MATMUL(., W2)
  * [-> BROADCAST_ADD(b2)] [-> RELU|TANH] with single consumers, within
  * lancius_hip_mlp2_ex_f32's limits (M <= 64, N2 <= 64, M*N1 <= 16384,
- * N1*N2 <= 8192): one launch of two kernels instead of two split-K GEMMs
- * with their reduces.  Fills L and marks the chain's inner nodes absorbed;
- * returns 0 when the pattern does not match. */
+ * N1*N2 <= 8192, K1*max(M, N1) <= 2^28): one launch instead of two
+ * split-K GEMMs with their reduces.  Fills L and marks the chain's inner
+ * nodes absorbed; returns 0 when the pattern does not match. */
 static int try_mlp2(const basis_graph* g, const int* uses, int head, basis_launch* L, char* absorbed) {
     const basis_node* nd = g->nodes;
     int chain[6], len = 0;
@@ -145,8 +145,8 @@ static int try_mlp2(const basis_graph* g, const int* uses, int head, basis_launc
         act2 = act_of(nd[c].op);
         chain[len++] = t = c;
     }
-    const size_t M = nd[head].rows, N1 = nd[head].cols, N2 = nd[mm2].cols;
-    if (M > 64 || N2 > 64 || M * N1 > 16384 || N1 * N2 > 8192) return 0;
+    const size_t M = nd[head].rows, N1 = nd[head].cols, N2 = nd[mm2].cols, K1 = nd[nd[head].input_ids[0]].cols;
+    if (M > 64 || N2 > 64 || M * N1 > 16384 || N1 * N2 > 8192 || K1 * (M > N1 ? M : N1) > ((size_t)1 << 28)) return 0;
     for (int j = 0; j + 1 < len; j++) absorbed[chain[j]] = 1;
     L->kind = K_MLP2;
     L->a = nd[head].input_ids[0];

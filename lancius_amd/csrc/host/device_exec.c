@@ -707,7 +707,8 @@ int lancius_device_program_info_get(const lancius_device_program* p, lancius_dev
 /* GEMM(+bias, act) -> GEMM(+bias) [-> SOFTMAX] on adjacent launches, the
  * hidden and logit tensors each read once by the next launch, small enough
  * for lancius_hip_mlp2_f32 (M <= 64, N2 <= 64, M*N1 <= 16384,
- * N1*N2 <= 8192): one launch instead of up to three dependent ones. */
+ * N1*N2 <= 8192, K1*max(M, N1) <= 2^28): one launch instead of up to three
+ * dependent ones. */
 /* Launches read tensors through their buffer owner (RESHAPE/FLATTEN
  * aliases resolved), so a node with one direct consumer can still be read
  * by several launches: h -> FLATTEN -> {GEMM, RELU}.  The buffer of `r` may
@@ -744,7 +745,9 @@ static uint32_t fuse_mlp2(lancius_device_program* p, const cstate* c, uint32_t n
         if (B->m[0].in[0] != h || B->m[0].in[1] == h || c->consumers[h] != 1 || !sole_reader(p, c, nl, h, s + 1))
             continue;
         const size_t M = A->d[0], K1 = A->d[1], N1 = A->d[2], N2 = B->d[2];
-        if (B->d[0] != M || B->d[1] != N1 || M > 64 || N2 > 64 || M * N1 > 16384 || N1 * N2 > 8192) continue;
+        if (B->d[0] != M || B->d[1] != N1 || M > 64 || N2 > 64 || M * N1 > 16384 || N1 * N2 > 8192 ||
+            K1 * (M > N1 ? M : N1) > ((size_t)1 << 28))
+            continue;
         int sm = 0;
         if (s + 2 < nl) {
             const launch_t* S = &p->launches[s + 2];

@@ -63,6 +63,13 @@ def run(dev, M, K1, N1, N2, act, bias, softmax, seed, act2=None):
     (64, 17, 100, 7, ACT_NONE, True, False),
     (50, 1000, 96, 33, ACT_GELU, False, False),
     (64, 4096, 64, 64, ACT_RELU, True, True),
+    (16, 9000, 64, 10, ACT_RELU, True, True),    # K ranges of several staged chunks
+    (13, 301, 250, 9, ACT_TANH, True, True),     # K ranges and N1 not multiples of 4
+    # hidden layers wider than 256: one workgroup per 16-column tile, no K split
+    (16, 300, 512, 16, ACT_RELU, True, True),
+    (4, 2000, 2048, 4, ACT_GELU, True, True),
+    (3, 77, 1000, 8, ACT_RELU, False, False),
+    (1, 100, 8192, 1, ACT_RELU, True, False),
 ])
 def test_mlp2_matches_unfused_chain(dev, M, K1, N1, N2, act, bias, softmax):
     got, idx, ref = run(dev, M, K1, N1, N2, act, bias, softmax, 40 + M + K1)
@@ -93,7 +100,8 @@ def test_mlp2_repeatable(dev):
 
 def test_mlp2_limits(dev):
     case("mlp2 limits")
-    for M, K1, N1, N2 in ((65, 8, 8, 8), (8, 8, 8, 65), (64, 8, 257, 8), (8, 8, 200, 64)):
+    for M, K1, N1, N2 in ((65, 8, 8, 8), (8, 8, 8, 65), (64, 8, 257, 8), (8, 8, 200, 64), (64, (1 << 22) + 1, 8, 8),
+                          (8, 1 << 25, 16, 8)):
         with pytest.raises(HipError) as e:
             dev.mlp2(1, None, 1, 1, None, ACT_NONE, 1, None, M, K1, N1, N2)
         assert e.value.code == -3
