@@ -345,12 +345,12 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
                                                      0, 0);
         }
         const int hi = hi0 + kh, wi = wi0 + kw;
-        const bool inside = live && p_valid && hi >= 0 && hi < H && wi >= 0 && wi < W;
+        const bool inside = live & p_valid & ((unsigned)hi < (unsigned)H) & ((unsigned)wi < (unsigned)W);
         const unsigned pix = img_base + (unsigned)(hi * W + wi) * 4u + (unsigned)ci0 * HW4;
 #pragma unroll
         for (int j = 0; j < B_INSTR; ++j) {
             const int row = ((4 * j + wave) * 64) / BN;
-            const unsigned bo = inside ? pix + (unsigned)row * HW4 : kOut;
+            const unsigned bo = (unsigned)pick(inside, (int)(pix + (unsigned)row * HW4), (int)kOut);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(Bs + (4 * j + wave) * 64), 4, (int)bo, 0, 0, 0);
         }
         if (!MIX) __builtin_amdgcn_sched_barrier(0);
@@ -669,6 +669,215 @@ __global__ void __launch_bounds__(256) conv2d_wgrad_mfma(const WgradParams p) {
     }
 }
 
+// Weight gradient with both operand tiles loaded straight from global memory
+// into LDS (buffer loads with the LDS as destination), the forward direct
+// GEMM's pipeline (gemm.hip, gemm_f32_direct): BM x 64 tiles (BM = 128 or
+// 64), k-tiles of 16 pixels, 4 waves of (BM/2) x 32, two separate LDS
+// buffers and the k loop unrolled by two.  Both operands run along the
+// pixel index, so both live m-major, 64 bytes per row, chunk c (4 pixels)
+// of row r at chunk c ^ ((r >> 2) & 3): the 16-byte operand reads of 16
+// consecutive rows hit 16 different bank groups.  Lane half h of the MFMAs
+// takes pixels [8h, 8h + 8) of the k-tile, the same for both operands.
+//  * dY rows (channels m0..) load as 16-byte chunks: HWo % 4 == 0 keeps a
+//    chunk of 4 pixels inside one image and 16-byte aligned.  Instruction i
+//    of wave w fills LDS chunks (A_INSTR w + i) * 64 + lane; every
+//    instruction of a lane reads the same pixel chunk (rows 16 apart share
+//    the swizzle), so the lane tracks one (image, pixel) pair.
+//  * X im2col rows (j = (ci, kh, kw) from j0) load 4 bytes per lane:
+//    instruction t = w + 4 i writes words 64 t + lane, rows 4 t + lane/16,
+//    whose swizzle is (4 t + ...) >> 2 & 3 = w: the lane's pixel is again
+//    one per k-tile, tracked as (image, ho, wo) and advanced by 16 pixels a
+//    k-tile without a division.  Taps outside the image, pixels past the
+//    split's range and j past J use an offset past the buffer's end (the
+//    load returns 0); channel rows past C_out read the last row and reach
+//    only entries that are never stored.
+// Requires HWo % 4 == 0, HWo >= 16 and dY, X under 2 GiB.
+template <int BM>
+__global__ void __launch_bounds__(256, 2) conv2d_wgrad_direct(const WgradParams p) {
+    constexpr int BN = 64, BK = 16;
+    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    constexpr int A_INSTR = BM * BK / 4 / 64 / 4;  // 16-byte loads of dY per wave per k-tile
+    constexpr int B_INSTR = BN * BK / 64 / 4;      // 4-byte loads of X per wave per k-tile
+    static_assert(A_INSTR >= 1 && B_INSTR == 4 && TN == 1, "tile shape");
+    typedef __attribute__((address_space(3))) void lds_void;
+    __shared__ __attribute__((aligned(16))) float As0[BM * BK];
+    __shared__ __attribute__((aligned(16))) float As1[BM * BK];
+    __shared__ __attribute__((aligned(16))) float Bs0[BN * BK];
+    __shared__ __attribute__((aligned(16))) float Bs1[BN * BK];
+
+    const uint32_t tile = blockIdx.x;
+    const int m0 = (int)(tile / p.tiles_n) * BM;  // first output channel
+    const int j0 = (int)(tile % p.tiles_n) * BN;  // first (ci, kh, kw)
+    const long long pbeg = (long long)blockIdx.y * p.pchunk;
+    const int prange = (int)((pbeg + p.pchunk < p.Ptotal ? pbeg + p.pchunk : p.Ptotal) - pbeg);
+    const int HWo = p.Ho * p.Wo, HW = p.H * p.W, KHW = p.KH * p.KW;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.dy), 0, (int)((size_t)p.N * p.C_out * HWo * sizeof(float)), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.x), 0, (int)((size_t)p.N * p.C_in * HW * sizeof(float)), kBufferRsrcWord3);
+    constexpr int kOut = 0x7ffffff0;  // an offset past the end of any operand: the load returns 0
+
+    // dY: this lane's rows and pixel chunk
+    int a_rowoff[A_INSTR];
+    const int qa = A_INSTR * wave * 64 + lane;
+    const int a_c = (qa & 3) ^ ((qa >> 4) & 3);
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) a_rowoff[i] = min(m0 + ((qa >> 2) + 16 * i), p.C_out - 1) * HWo;
+    int a_rel = 4 * a_c;  // pixel of the chunk, relative to pbeg
+    int a_n, a_pix;
+    {
+        const long long P = pbeg + a_rel;
+        a_n = (int)(P / HWo);
+        a_pix = (int)(P - (long long)a_n * HWo);
+    }
+    // X: this lane's four rows j and its pixel
+    int b_cioff[B_INSTR], b_dh[B_INSTR], b_dw[B_INSTR];
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i) {
+        const int j = j0 + 16 * i + 4 * wave + (lane >> 4);
+        if (j < p.J) {
+            const int ci = j / KHW, t = j - ci * KHW;
+            const int kh = t / p.KW, kw = t - kh * p.KW;
+            b_cioff[i] = ci * HW;
+            b_dh[i] = kh - p.pad;
+            b_dw[i] = kw - p.pad;
+        } else {
+            b_cioff[i] = -1;
+            b_dh[i] = b_dw[i] = 0;
+        }
+    }
+    int b_rel = 4 * (((lane & 15) >> 2) ^ wave) + (lane & 3);
+    int b_n, b_ho, b_wo;
+    {
+        const long long P = pbeg + b_rel;
+        b_n = (int)(P / HWo);
+        const int pix = (int)(P - (long long)b_n * HWo);
+        b_ho = pix / p.Wo;
+        b_wo = pix - b_ho * p.Wo;
+    }
+
+    // Issues the loads of the next k-tile into (As, Bs) and advances the
+    // lane's pixels by one k-tile.
+    auto load_tile = [&](float* As, float* Bs) {
+        const bool a_in = a_rel < prange;
+#pragma unroll
+        for (int i = 0; i < A_INSTR; ++i) {
+            const int ao = pick(a_in, ((a_n * p.C_out) * HWo + a_rowoff[i] + a_pix) * (int)sizeof(float), kOut);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(As + (A_INSTR * wave + i) * 256), 16, ao, 0, 0,
+                                                     0);
+        }
+        const bool b_in = b_rel < prange;
+        const int hb = b_ho * p.stride, wb = b_wo * p.stride, xbase = b_n * p.C_in * HW;
+#pragma unroll
+        for (int i = 0; i < B_INSTR; ++i) {
+            const int hi = hb + b_dh[i], wi = wb + b_dw[i];
+            const bool in = b_in & (b_cioff[i] >= 0) & ((unsigned)hi < (unsigned)p.H) & ((unsigned)wi < (unsigned)p.W);
+            const int bo = pick(in, (xbase + b_cioff[i] + hi * p.W + wi) * (int)sizeof(float), kOut);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (wave + 4 * i) * 64), 4, bo, 0, 0, 0);
+        }
+        // keep the loads ahead of the MFMAs that follow
+        __builtin_amdgcn_sched_barrier(0);
+        a_rel += BK;
+        a_pix += BK;
+        if (a_pix >= HWo) {
+            a_pix -= HWo;
+            ++a_n;
+        }
+        b_rel += BK;
+        b_wo += BK;
+        while (b_wo >= p.Wo) {
+            b_wo -= p.Wo;
+            if (++b_ho == p.Ho) {
+                b_ho = 0;
+                ++b_n;
+            }
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // operand addresses (floats) of this lane, fixed over the k loop
+    int a_rd[TM][2], b_rd[TN][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = 2 * lk + h;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int row = wm * WM + i * 32 + lr;
+            a_rd[i][h] = row * BK + 4 * (c ^ ((row >> 2) & 3));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int row = wn * WN + j * 32 + lr;
+            b_rd[j][h] = row * BK + 4 * (c ^ ((row >> 2) & 3));
+        }
+    }
+    auto compute = [&](const float* As, const float* Bs) {
+        f32x4 av[TM][2], bv[TN][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i) av[i][h] = *(const f32x4*)(As + a_rd[i][h]);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bv[j][h] = *(const f32x4*)(Bs + b_rd[j][h]);
+        }
+#pragma unroll
+        for (int kp = 0; kp < 8; ++kp)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bv[j][kp / 4][kp % 4],
+                                                                     acc[i][j], 0, 0, 0);
+    };
+
+    // k-tiles in pairs; when their count is odd the last pair's second tile
+    // lies wholly past the range, loads as zeros and adds nothing.
+    const int pairs = (prange + 2 * BK - 1) / (2 * BK);
+    load_tile(As0, Bs0);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    for (int pr = 0; pr < pairs; ++pr) {
+        load_tile(As1, Bs1);
+        compute(As0, Bs0);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        if (pr + 1 < pairs) load_tile(As0, Bs0);
+        compute(As1, Bs1);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+    }
+
+    // Register r of lane l: channel row 8(r/4) + 4(l/32) + r%4, column l%32.
+    float* dst = p.splits == 1 ? p.dw : p.ws + (size_t)blockIdx.y * p.C_out * p.J;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = j0 + wn * WN + j * 32 + lr;
+        if (col >= p.J) continue;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int cbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int co = cbase + 8 * (r >> 2) + (r & 3);
+                if (co < p.C_out) dst[(size_t)co * p.J + col] = acc[i][j][r];
+            }
+        }
+    }
+}
+
 // A workgroup per 64 consecutive weights: lane l of wave g adds splits g,
 // g+4, g+8, ... of weight l in order (a wave reads 256 contiguous bytes of a
 // split's partials), then wave 0 adds the four sums in wave order: a fixed
@@ -889,14 +1098,23 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     // per CU).  At the N32 64->128 56x56 config: 64 x 64 tiles, 57 splits
     // (1026 workgroups for 1024 slots) 0.239 ms; 128 x 64 tiles, 85 splits
     // (765 for 768) 0.216 ms.
-    int bk = tune("conv_wgrad_bk", 32);
+    // conv2d_wgrad_direct: k-tiles of 16 pixels taken in pairs (so the
+    // split length is a multiple of 32), splits for three workgroups per CU
+    // (N32 64->128 56x56: 0.1477 ms at two, 0.1450 at three, 0.1461 at four;
+    // the staged kernel 0.1939)
+    const size_t HWo = H_out * W_out;
+    const bool direct = tune("conv_wgrad_direct", 1) && HWo % 4 == 0 && HWo >= 16 &&
+                        N * C_out * HWo * sizeof(float) < ((size_t)1 << 31) - 64 &&
+                        N * C_in * H * W * sizeof(float) < ((size_t)1 << 31) - 64;
+    int bk = direct ? 32 : tune("conv_wgrad_bk", 32);
     if (bk != 16 && bk != 64) bk = 32;
     if (BM == 128 && bk == 64) bk = 32;
     const long long ktiles = (p.Ptotal + bk - 1) / bk;
     long long splits = tune("conv_wgrad_split", 0);
     if (splits <= 0) {
         const size_t lds = (size_t)2 * bk * ((BM + 4) + (BN + 4)) * sizeof(float);
-        const size_t per_cu = std::max<size_t>(1, std::min<size_t>(8, 163840 / lds));
+        const size_t per_cu = direct ? (size_t)std::max(1, tune("conv_wgrad_direct_occ", 3))
+                                     : std::max<size_t>(1, std::min<size_t>(8, 163840 / lds));
         const size_t slots = (size_t)cu_count(ctx) * per_cu;
         splits = std::max<long long>(1, std::min<long long>((long long)std::max<size_t>(1, slots / tiles),
                                                             ktiles * bk / 256));
@@ -912,7 +1130,11 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
         p.ws = (float*)ws;
     }
     const dim3 grid((unsigned)tiles, (unsigned)p.splits);
-    if (BM == 128 && bk == 32)
+    if (direct && BM == 128)
+        hipLaunchKernelGGL(conv2d_wgrad_direct<128>, grid, dim3(256), 0, ctx->stream, p);
+    else if (direct)
+        hipLaunchKernelGGL(conv2d_wgrad_direct<64>, grid, dim3(256), 0, ctx->stream, p);
+    else if (BM == 128 && bk == 32)
         hipLaunchKernelGGL((conv2d_wgrad_mfma<128, 64, 32>), grid, dim3(256), 0, ctx->stream, p);
     else if (BM == 128)
         hipLaunchKernelGGL((conv2d_wgrad_mfma<128, 64, 16>), grid, dim3(256), 0, ctx->stream, p);

@@ -58,6 +58,14 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 // Raw buffer over `bytes` bytes at `base` (bytes < 2^31).
+// c ? a : b without a branch.  hipcc tends to turn a select between a
+// computed load offset and a constant (the past-the-end offset of a buffer
+// load) into an exec-mask branch around the computation, once per load.
+__device__ __forceinline__ int pick(bool c, int a, int b) {
+    const int m = -(int)c;
+    return (a & m) | (b & ~m);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_buffer(const void* base, size_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferRsrcWord3);
 }

@@ -221,6 +221,8 @@ def test_conv_backward_golden(dev, tag, stride, pad):
     (1, 4, 10, 12, 6, 3, 5, 1, 1),     # non-square filter: direct dgrad
     (1, 2, 6, 6, 3, 3, 3, 1, 3),       # pad > K - 1: direct dgrad
     (3, 8, 7, 7, 5, 1, 1, 1, 0),       # 1x1
+    (2, 6, 16, 16, 8, 3, 3, 2, 1),     # stride 2, H_out * W_out % 4 == 0: direct-load wgrad
+    (2, 20, 12, 12, 130, 3, 3, 1, 1),  # two channel tiles of 128, J = 180 (a partial column tile)
 ])
 def test_conv_backward_shapes(dev, shape):
     N, Ci, H, W, Co, KH, KW, st, pd = shape
