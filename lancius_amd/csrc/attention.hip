@@ -366,14 +366,19 @@ struct DecodeParams {
 
 constexpr int kDecMaxD = 128;
 
+constexpr int kDecOut = 0x7ffffff0;  // a byte offset past the end of any operand: the load returns 0
+
+// This lane's NV values of the row at byte offset `row` of buffer r; values
+// past D come from a past-the-end offset (0) instead of a branch around the
+// load.
 template <int NV, bool VEC>
-__device__ __forceinline__ void load_piece(const float* __restrict__ row, int l16, int D, float (&x)[NV]) {
+__device__ __forceinline__ void load_piece(__amdgpu_buffer_rsrc_t r, int row, int l16, int D, float (&x)[NV]) {
     if constexpr (VEC) {
 #pragma unroll
         for (int j = 0; j < NV / 4; ++j) {
             const int d = 4 * l16 + 64 * j;
-            float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (d < D) t = *reinterpret_cast<const float4*>(row + d);
+            const f32x4 t = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, pick(d < D, row + 4 * d, kDecOut), 0, 0));
             x[4 * j] = t.x;
             x[4 * j + 1] = t.y;
             x[4 * j + 2] = t.z;
@@ -383,7 +388,8 @@ __device__ __forceinline__ void load_piece(const float* __restrict__ row, int l1
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int d = l16 + 16 * i;
-            x[i] = d < D ? row[d] : 0.0f;
+            x[i] = __builtin_bit_cast(float,
+                                      __builtin_amdgcn_raw_buffer_load_b32(r, pick(d < D, row + 4 * d, kDecOut), 0, 0));
         }
     }
 }
@@ -442,16 +448,25 @@ __global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
     const int k0 = split * p.chunk, k1 = min(len, k0 + p.chunk);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int l16 = lane & 15, stream = wave * 4 + (lane >> 4);
-    const size_t kv_row = (size_t)p.Hkv * D;
-    const float* kb = p.k + ((size_t)b * p.Skv * p.Hkv + hk) * D;
-    const float* vb = p.v + ((size_t)b * p.Skv * p.Hkv + hk) * D;
+    const int kv_row = p.Hkv * D;
+    // K and V rows of this key range as buffers (the host keeps a range
+    // under 1 GiB); key k is at byte (k - k0) * kv_row * 4
+    const size_t kv0 = ((size_t)b * p.Skv + k0) * kv_row + (size_t)hk * D;
+    const int kv_bytes = ((max(k1 - k0, 1) - 1) * kv_row + D) * (int)sizeof(float);
+    const __amdgpu_buffer_rsrc_t kr_buf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.k + kv0), 0, kv_bytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vr_buf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.v + kv0), 0, kv_bytes, kBufferRsrcWord3);
     const int h0 = hc * GT;
+    const __amdgpu_buffer_rsrc_t q_buf = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(p.q + ((size_t)b * p.Hq + (size_t)hk * G + h0) * D), 0,
+        min(GT, G - h0) * D * (int)sizeof(float), kBufferRsrcWord3);
 
     float qv[GT][NV], o[GT][NV], m[GT], l[GT];
 #pragma unroll
     for (int h = 0; h < GT; ++h) {
         if (h0 + h < G) {
-            load_piece<NV, VEC>(p.q + ((size_t)b * p.Hq + (size_t)hk * G + h0 + h) * D, l16, D, qv[h]);
+            load_piece<NV, VEC>(q_buf, h * D * (int)sizeof(float), l16, D, qv[h]);
         } else {
 #pragma unroll
             for (int i = 0; i < NV; ++i) qv[h][i] = 0.0f;
@@ -472,9 +487,9 @@ __global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
         for (int u = 0; u < UNR; ++u) {
             const int key = base + 16 * u + stream;
             valid[u] = key < k1;
-            const size_t row = (size_t)(valid[u] ? key : k1 - 1) * kv_row;
-            load_piece<NV, VEC>(kb + row, l16, D, kr[u]);
-            load_piece<NV, VEC>(vb + row, l16, D, vr[u]);
+            const int row = ((valid[u] ? key : k1 - 1) - k0) * kv_row * (int)sizeof(float);
+            load_piece<NV, VEC>(kr_buf, row, l16, D, kr[u]);
+            load_piece<NV, VEC>(vr_buf, row, l16, D, vr[u]);
         }
     };
     auto consume = [&](const float (&kr)[UNR][NV], const float (&vr)[UNR][NV], const bool (&valid)[UNR]) {
@@ -748,6 +763,10 @@ int lancius_hip_attention_decode_f32(lancius_hip_ctx* ctx, float* out, const flo
     const size_t seqs = batch * H_kv;
     const size_t tasks = seqs * hchunks;
     size_t splits = std::max<size_t>(1, std::min<size_t>((512 + tasks - 1) / tasks, (S_kv + 255) / 256));
+    // a key range's K and V rows are addressed with 32-bit buffer offsets:
+    // at most 1 GiB per range
+    const size_t max_chunk = std::max<size_t>(1, ((size_t)1 << 30) / (H_kv * D * sizeof(float)));
+    splits = std::max(splits, (S_kv + max_chunk - 1) / max_chunk);
     const size_t chunk = (S_kv + splits - 1) / splits;
     splits = (S_kv + chunk - 1) / chunk;
     LANCIUS_REQUIRE(tasks * splits < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention_decode: too many heads");
