@@ -710,9 +710,16 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_skinny_f32(const GemmParams p
     const float* __restrict__ A = p.A[g];
     const float* __restrict__ B = p.B[g];
 
-    // A operands first: av[t][s] = A[16t + cq][kbase + s]
+    // A operands first: av[t][s] = A[16t + cq][kbase + s].  The float4 loads
+    // go through buffer resources with past-the-end offsets for elements
+    // that do not exist (the load returns 0): a branch around each load, as
+    // hipcc compiles a plain guarded load, costs as much as the load.
+    constexpr int kOut = 0x7ffffff0;
     float av[MT][STEPS];
-    const bool va = !TA && (K % 4 == 0) && (((uintptr_t)A & 15u) == 0);
+    const bool va = !TA && (K % 4 == 0) && (((uintptr_t)A & 15u) == 0) && (size_t)M * K < ((size_t)1 << 29);
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), 0, va ? M * K * (int)sizeof(float) : 0,
+                                          kBufferRsrcWord3);
 #pragma unroll
     for (int t = 0; t < MT; ++t) {
         const int m = 16 * t + cq;
@@ -720,7 +727,9 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_skinny_f32(const GemmParams p
 #pragma unroll
             for (int q = 0; q < STEPS / 4; ++q) {
                 const int k = kbase + 4 * q;
-                const f32x4 x = (m < M && k < K) ? *(const f32x4*)(A + (size_t)m * K + k) : f32x4{0.f, 0.f, 0.f, 0.f};
+                const f32x4 x = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               ra, pick((m < M) & (k < K), (m * K + k) * (int)sizeof(float), kOut), 0, 0));
                 av[t][4 * q] = x.x;
                 av[t][4 * q + 1] = x.y;
                 av[t][4 * q + 2] = x.z;
@@ -734,13 +743,20 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_skinny_f32(const GemmParams p
             }
         }
     }
-    // then every B load of the slice
+    // then every B load of the slice (VB: a buffer over the slice's rows,
+    // rows past K past its end)
     f32x4 bv[STEPS];
+    const int k_slice = split * KS;
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(B + (size_t)k_slice * N), 0, VB ? min(KS, K - k_slice) * N * (int)sizeof(float) : 0,
+        kBufferRsrcWord3);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
         const int k = kbase + s;
         if constexpr (VB) {
-            bv[s] = (k < K && col4 < N) ? *(const f32x4*)(B + (size_t)k * N + col4) : f32x4{0.f, 0.f, 0.f, 0.f};
+            bv[s] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           rb, pick(col4 < N, ((k - k_slice) * N + col4) * (int)sizeof(float), kOut), 0, 0));
         } else {
             const float* row = B + (size_t)k * N;
             const bool kin = k < K;
@@ -748,6 +764,9 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_skinny_f32(const GemmParams p
                           (kin && col4 + 2 < N) ? row[col4 + 2] : 0.f, (kin && col4 + 3 < N) ? row[col4 + 3] : 0.f};
         }
     }
+    // every load of the slice is in flight before the first MFMA (the
+    // scheduler would otherwise place each load next to its MFMA)
+    __builtin_amdgcn_sched_barrier(0);
 
     f32x4 acc[MT][4];
 #pragma unroll
@@ -1110,7 +1129,9 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     GemmParams p{};
     // float4 global loads run along each operand's contiguous axis
     bool vec = ((ta ? M : K) % 4 == 0) && ((tb ? K : N) % 4 == 0);
-    bool vb = N % 4 == 0;  // skinny: float4 B rows and float4 C / partial stores
+    // skinny: float4 B rows (a K slice of up to 1024 rows within 32-bit
+    // buffer offsets) and float4 C / partial stores
+    bool vb = N % 4 == 0 && N < ((size_t)1 << 19);
     for (size_t g = 0; g < count; ++g) {
         LANCIUS_REQUIRE(C[g] && A[g] && B[g], LANCIUS_HIP_ERR_NULL_PTR, "gemm: NULL operand in group %zu", g);
         p.C[g] = C[g];
