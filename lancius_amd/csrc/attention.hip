@@ -128,7 +128,16 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
     const int kv_end = p.causal ? max(0, min(Skv, q0 + kBQ + off)) : Skv;
     const int nblocks = (kv_end + BKV - 1) / BKV;
 
-    // K/V global -> register staging: BKV keys x D floats per tensor.
+    // K/V global -> register staging: BKV keys x D floats per tensor, as
+    // buffer loads (the sequence's K and V rows, under 2 GiB: the host
+    // checks) whose keys past Skv use a past-the-end offset and read 0; a
+    // guarded plain load would be a branch per load.
+    constexpr int kOut = 0x7ffffff0;
+    const int kv_bytes = ((Skv - 1) * (int)kv_stride + D) * (int)sizeof(float);
+    const __amdgpu_buffer_rsrc_t kbuf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Kg), 0, kv_bytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vbuf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Vg), 0, kv_bytes, kBufferRsrcWord3);
     f32x4 kreg[NKV], vreg[NKV];
     auto load_kv = [&](int k0) {
 #pragma unroll
@@ -136,14 +145,13 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
             const int idx = tid + NT * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
             const int gk = k0 + key;
-            if (gk < Skv) {
-                kreg[i] = *(const f32x4*)(Kg + (size_t)gk * kv_stride + 4 * dq);
-                vreg[i] = *(const f32x4*)(Vg + (size_t)gk * kv_stride + 4 * dq);
-            } else {
-                kreg[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-                vreg[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+            const int off = pick(gk < Skv, (gk * (int)kv_stride + 4 * dq) * (int)sizeof(float), kOut);
+            kreg[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(kbuf, off, 0, 0));
+            vreg[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(vbuf, off, 0, 0));
         }
+        // the loads leave before the block's MFMAs (the scheduler would
+        // otherwise move them down to the LDS stores they feed)
+        __builtin_amdgcn_sched_barrier(0);
     };
     auto store_kv = [&](int buf) {
 #pragma unroll
@@ -675,7 +683,8 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
     p.qscale = scale * 1.4426950408889634f;  // log2(e)
     const unsigned z = (unsigned)(count * batch);
     p.Z = (int)z;
-    if (vec && D % 32 == 0 && D <= 128) {
+    // the MFMA kernel addresses a sequence's K and V rows with 32-bit buffer offsets
+    if (vec && D % 32 == 0 && D <= 128 && Skv * Hkv * D * sizeof(float) < ((size_t)1 << 31) - 64) {
         p.q_tiles = (int)((S + kBQ - 1) / kBQ);
         const size_t tasks = (size_t)p.q_tiles * H * z;
         LANCIUS_REQUIRE(tasks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention: too many tiles");
