@@ -653,6 +653,221 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
     }
 }
 
+// The direct-load pipeline of gemm_f32_direct for grids too small to give
+// every CU several tiles: BM x BM tiles (BM = 128, or 64 for the smallest
+// products) and KG k-groups of 4 waves in one workgroup.  Group g takes
+// k-tiles g, g + KG, g + 2 KG, ... with its own pair of LDS buffers (same
+// layouts and swizzles as gemm_f32_direct, scaled to BM), so a CU runs 4 KG
+// waves on its tile instead of 4.  At the end the groups' sums are added
+// through LDS in the fixed order (g0 + g1) + (g2 + g3) and group 0 runs the
+// epilogue: results are run-to-run identical.
+template <int BM, int KG>
+__global__ void __launch_bounds__(256 * KG, 1) gemm_f32_direct_kg(const GemmParams p) {
+    constexpr int BN = BM, BK = 16;
+    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    constexpr int AI = BM / 64, BI = BN / 64;  // 16-byte loads per wave per k-tile
+    constexpr int ASZ = BM * BK, BSZ = BK * BN;
+    constexpr int STAGE = KG * 2 * (ASZ + BSZ);
+    constexpr int RED = (KG > 2 ? 2 : 1) * BM * BN;  // partial tiles in LDS at once
+    static_assert(KG == 1 || KG == 2 || KG == 4, "k-groups");
+    typedef __attribute__((address_space(3))) void lds_void;
+    __shared__ __attribute__((aligned(16))) float smem[STAGE > RED ? STAGE : RED];
+
+    const int g = blockIdx.z;
+    const float* __restrict__ A = p.A[g];
+    const float* __restrict__ B = p.B[g];
+    float* __restrict__ C = p.C[g];
+    const float* __restrict__ R = p.R[g];
+    const int M = p.M, N = p.N, K = p.K;
+    const uint32_t ntiles = p.tiles_m * p.tiles_n;
+    uint32_t tm_id, tn_id;
+    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
+    const int m0 = (int)tm_id * BM;
+    const int n0 = (int)tn_id * BN;
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int grp = wave >> 2, gw = wave & 3;
+    const int wm = gw >> 1, wn = gw & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+    float* const As0 = smem + grp * 2 * (ASZ + BSZ);
+    float* const As1 = As0 + ASZ;
+    float* const Bs0 = As1 + ASZ;
+    float* const Bs1 = Bs0 + BSZ;
+
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(A), 0, (int)((size_t)M * K * sizeof(float)), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(B), 0, (int)((size_t)K * N * sizeof(float)), kBufferRsrcWord3);
+    constexpr int kOut = 0x7ffffff0;  // an offset past the end of any operand: the load returns 0
+
+    // A chunks: instruction i of wave gw fills chunks (AI gw + i) * 64 + lane
+    // (row q >> 2, chunk (q & 3) ^ ((row >> 2) & 3)); B chunks likewise
+    // (row q / (BN / 4), chunk swizzled by 8 ((row >> 3) & 1)).
+    int a_k[AI], a_off0[AI], b_kr[BI], b_off0[BI];
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+        const int q = (AI * gw + i) * 64 + lane;
+        const int row = q >> 2, c = (q & 3) ^ ((row >> 2) & 3);
+        a_k[i] = 4 * c;
+        a_off0[i] = (min(m0 + row, M - 1) * K + 4 * c) * (int)sizeof(float);
+    }
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+        const int q = (BI * gw + i) * 64 + lane;
+        const int kr = q / (BN / 4), lc = (q % (BN / 4)) ^ (((kr >> 3) & 1) << 3);
+        b_kr[i] = kr;
+        b_off0[i] = (kr * N + min(n0 + 4 * lc, N - 4)) * (int)sizeof(float);
+    }
+    auto load_tile = [&](float* As, float* Bs, int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int i = 0; i < AI; ++i) {
+            const int ao = pick(k0 + a_k[i] < K, a_off0[i] + k0 * (int)sizeof(float), kOut);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(As + (AI * gw + i) * 256), 16, ao, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < BI; ++i) {
+            const int bo = pick(k0 + b_kr[i] < K, b_off0[i] + k0 * N * (int)sizeof(float), kOut);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (BI * gw + i) * 256), 16, bo, 0, 0, 0);
+        }
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    int a_rd[TM][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int row = wm * WM + i * 32 + lr, c = 2 * lk + h;
+            a_rd[i][h] = row * BK + 4 * (c ^ ((row >> 2) & 3));
+        }
+    int b_rd[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int n = wn * WN + j * 32 + lr;
+        b_rd[j] = 8 * lk * BN + 4 * ((n >> 2) ^ (lk << 3)) + (n & 3);
+    }
+    // one global load after each of the k-tile's first MFMAs
+    auto compute = [&](const float* As, const float* Bs) {
+        f32x4 av[TM][2];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) av[i][h] = *(const f32x4*)(As + a_rd[i][h]);
+#pragma unroll
+        for (int kp = 0; kp < 8; ++kp) {
+            float bf[TN];
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bf[j] = Bs[b_rd[j] + kp * BN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < AI + BI; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - (AI + BI), 0);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // this group's k-tiles grp, grp + KG, ... in pairs; the groups run the
+    // same number of steps, k-tiles past K load as zeros and add nothing
+    const int ktiles = (K + BK - 1) / BK;
+    const int steps = (ktiles + KG - 1) / KG;
+    const int pairs = (steps + 1) / 2;
+    load_tile(As0, Bs0, grp);
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+    __syncthreads();
+    for (int pr = 0; pr < pairs; ++pr) {
+        load_tile(As1, Bs1, grp + KG * (2 * pr + 1));
+        compute(As0, Bs0);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+        load_tile(As0, Bs0, grp + KG * (2 * pr + 2));
+        compute(As1, Bs1);
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
+    }
+
+    // (g0 + g1) + (g2 + g3) through LDS: a group's sums are BM x BN floats,
+    // stored per (wave, register quad, lane) as 16-byte pieces
+    if constexpr (KG > 1) {
+        constexpr int QUADS = TM * TN * 4;
+        auto put = [&](int slot) {
+            float* dst = smem + slot * BM * BN + gw * QUADS * 256;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        *(f32x4*)(dst + (((i * TN + j) * 4 + q) * 64 + lane) * 4) =
+                            f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        };
+        auto add = [&](int slot) {
+            const float* src = smem + slot * BM * BN + gw * QUADS * 256;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x4 v = *(const f32x4*)(src + (((i * TN + j) * 4 + q) * 64 + lane) * 4);
+                        acc[i][j][4 * q] += v.x;
+                        acc[i][j][4 * q + 1] += v.y;
+                        acc[i][j][4 * q + 2] += v.z;
+                        acc[i][j][4 * q + 3] += v.w;
+                    }
+        };
+        if (grp & 1) put(grp >> 1);
+        __syncthreads();
+        if (!(grp & 1)) add(grp >> 1);
+        if constexpr (KG == 4) {
+            __syncthreads();
+            if (grp == 2) put(0);
+            __syncthreads();
+            if (grp == 0) add(0);
+        }
+        if (grp != 0) return;
+    }
+
+    const float* __restrict__ bias = p.bias[g];
+    const int act = p.act;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = n0 + wn * WN + j * 32 + lr;
+        if (col >= N) continue;
+        const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+            const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = rbase + 8 * (r >> 2) + (r & 3);
+                if (row < M) {
+                    float v = acc[i][j][r] + bv;
+                    v = apply_act(v, act);
+                    const size_t o = (size_t)row * N + col;
+                    if (R) v += R[o];
+                    C[o] = v;
+                }
+            }
+        }
+    }
+}
+
 // Skinny GEMM (M <= 16*MT): the product is bound by reading B once from
 // HBM (or, for tiny problems, by latency), so the kernel is organised around
 // that stream.
@@ -1269,6 +1484,35 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256), 0, ctx->stream, p);
         if (int rc = check_launch("gemm_f32_direct")) return rc;
         return ok();
+    }
+    // Grids that give a CU about one 128 x 128 tile (or one 64 x 64 tile):
+    // the direct-load pipeline with the K loop spread over k-groups of
+    // 4 waves inside the workgroup (gemm_f32_direct_kg)
+    const int kgd = tune("gemm_direct_kg", 1);
+    if (kgd && vec && plain && M * K * sizeof(float) < ((size_t)1 << 31) &&
+        K * N * sizeof(float) < ((size_t)1 << 31) && K >= 256 && (big_tiles < 768 || kgd > 1)) {
+        // 64 x 64 tiles, with 4 k-groups when that gives about one tile per
+        // CU and 2 otherwise; 128 x 128 tiles (2 k-groups: 4 would leave 128
+        // registers a wave and spill) for K >= 4096 with >= 192 of them.
+        // Measured on MI355X (old dispatch -> this): 1024^3 27.0 -> 23.7 us,
+        // 2048^3 146.0 -> 135.6, 4096x1024x1024 82.4 -> 71.3,
+        // 1024x4096x1024 84.4 -> 76.4, 4096x4096x1024 275.2 -> 257.3,
+        // 3000x1000x2000 145.8 -> 104.3.
+        const int bm_kg = tune("gemm_direct_kg_bm", K >= 4096 && big_tiles >= 192 ? 128 : 64);
+        const int kg = tune("gemm_direct_kg_groups", bm_kg == 128 || t64 > 384 ? 2 : 4);
+        const size_t kg_tiles = count * ((M + bm_kg - 1) / bm_kg) * ((N + bm_kg - 1) / bm_kg);
+        if (kg_tiles >= 128 || kgd > 1) {
+            p.tiles_m = (uint32_t)((M + bm_kg - 1) / bm_kg);
+            p.tiles_n = (uint32_t)((N + bm_kg - 1) / bm_kg);
+            void (*kern)(const GemmParams) = bm_kg == 128 ? (kg == 2 ? gemm_f32_direct_kg<128, 2>
+                                                                     : gemm_f32_direct_kg<128, 4>)
+                                                          : (kg == 2 ? gemm_f32_direct_kg<64, 2>
+                                                                     : gemm_f32_direct_kg<64, 4>);
+            hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256 * (kg == 2 ? 2 : 4)), 0,
+                               ctx->stream, p);
+            if (int rc = check_launch("gemm_f32_direct_kg")) return rc;
+            return ok();
+        }
     }
     if (splits > 1) {
         void* ws = nullptr;

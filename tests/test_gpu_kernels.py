@@ -102,11 +102,13 @@ def test_gemm_config_every_band(dev, n):
 
 
 @pytest.mark.parametrize("M,K,N", [
-    (2048, 1000, 2048),  # 256 tiles of 128^2: 4 k-groups, K crosses a 32-deep k-tile
-    (2048, 72, 3072),    # 384 tiles: 2 k-groups
+    (2048, 1000, 2048),  # direct loads, 64x64 tiles, 2 k-groups; K crosses a 16-deep k-tile
+    (1000, 1028, 1100),  # direct loads, 64x64 tiles, 4 k-groups, ragged edges
+    (3000, 4096, 1500),  # direct loads, 128x128 tiles, 2 k-groups, ragged edges
+    (2048, 72, 3072),    # K < 256: staged, 384 tiles of 128^2 with 2 k-groups
     (2000, 40, 2990),    # 384 tiles, N % 4 != 0: scalar loads
     (520, 2100, 500),    # 20 tiles, K >= 2048: 2 k-groups with split K, ragged edges
-    (600, 300, 700),     # 64x64 tiles with 4 k-groups, ragged edges
+    (600, 300, 700),     # 64x64 tiles with 4 k-groups (staged), ragged edges
     (601, 301, 703),     # same, K % 4 != 0: scalar loads
 ])
 def test_gemm_tile_paths(dev, M, K, N):
@@ -215,6 +217,32 @@ def test_gemm_grouped(dev):
         ref = oracle.relu(oracle.matmul(As[g], Bs[g]) + bs[g].astype(np.float64)) + Rs[g]
         got = dev.download(dC[g], (M, N))
         assert oracle.normwise_error(got, ref) <= oracle.tolerance(K), g
+
+
+def test_gemm_grouped_direct_kgroups(dev):
+    """A grouped launch through the direct-load k-group kernel (64x64
+    tiles, 4 k-groups; grid.z = member) with each member's own B, bias and
+    residual, NaN-filled outputs, and repeat calls bit-identical."""
+    M, K, N, G = 520, 300, 600, 3
+    As = [prng.normal(900 + g, (M, K)) for g in range(G)]
+    Bs = [prng.normal(910 + g, (K, N)) for g in range(G)]
+    bs = [prng.normal(920 + g, (N,)) for g in range(G)]
+    Rs = [prng.normal(930 + g, (M, N)) for g in range(G)]
+    dA, dB, db, dR = _upload(dev, *As), _upload(dev, *Bs), _upload(dev, *bs), _upload(dev, *Rs)
+    dC = [dev.alloc(M * N * 4) for _ in range(G)]
+    for c in dC:
+        dev.fill(c, float("nan"), M * N)
+    case("gemm grouped, direct k-groups")
+    dev.gemm_grouped(dC, dA, dB, M, K, N, biases=db, act=ACT_GELU, residuals=dR)
+    first = [dev.download(dC[g], (M, N)) for g in range(G)]
+    dev.gemm_grouped(dC, dA, dB, M, K, N, biases=db, act=ACT_GELU, residuals=dR)
+    for g in range(G):
+        assert np.isfinite(first[g]).all(), g
+        ref = oracle.gelu(oracle.matmul(As[g], Bs[g]) + bs[g].astype(np.float64)) + Rs[g]
+        assert oracle.normwise_error(first[g], ref) <= oracle.tolerance(K), g
+        assert np.array_equal(first[g].view(np.uint32), dev.download(dC[g], (M, N)).view(np.uint32)), g
+    for b in dA + dB + db + dR + dC:
+        b.free()
 
 
 def test_gemm_deterministic(dev):
