@@ -17,6 +17,7 @@
 // are those of the GEMM kernel; the epilogue writes Out[n][co][ho][wo], where
 // lanes 0..31 of a register cover 32 consecutive pixels of one channel.
 #include <algorithm>
+#include <atomic>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -35,6 +36,17 @@ struct ConvParams {
     long long Ptotal;  // N * Ho * Wo
     int act;
     uint32_t tiles_m, tiles_n;
+    // conv2d_direct's split of the tiles: workgroups [0, sk_dp) take whole
+    // tiles [0, sk_dp); sk_wgs more share the rest by (tile, k-tile) units
+    int sk_dp, sk_wgs;
+    float* sk_part;       // 2 * sk_wgs slots of one tile's sums
+    unsigned* sk_ctr;     // one arrival counter per shared tile, zero between launches
+    // weights the launch lays out in the workspace first: 0 none (wt or w
+    // ready), 1 the forward per-channel layout of w, 2 dgrad's flipped
+    // weights of w_src (the conv being differentiated has C_in and C_out
+    // swapped against this one)
+    int prep;
+    const float* w_src;
 };
 
 constexpr int kThreads = 256;
@@ -282,6 +294,7 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
     __shared__ __attribute__((aligned(16))) float As1[BM * BK];
     __shared__ __attribute__((aligned(16))) float Bs0[BK * BN];
     __shared__ __attribute__((aligned(16))) float Bs1[BK * BN];
+    __shared__ int s_flag;
 
     const int KH = KH_T > 0 ? KH_T : p.KH;
     const int KW = KW_T > 0 ? KW_T : p.KW;
@@ -290,12 +303,7 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
     const int HWo = Ho * Wo;
     const int C_in = p.C_in, C_out = p.C_out;
     const unsigned HW4 = (unsigned)(H * W) * 4u;
-
     const uint32_t ntiles = p.tiles_m * p.tiles_n;
-    uint32_t tm_id, tn_id;
-    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 2, tm_id, tn_id);
-    const int m0 = (int)tm_id * BM;
-    const long long P0 = (long long)tn_id * BN;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -308,32 +316,45 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
         const_cast<float*>(p.wt), 0, (int)((size_t)C_out * KHW * C_in * sizeof(float)), kBufferRsrcWord3);
     constexpr unsigned kOut = 0x7ffffff0u;  // past the end of either operand: the load returns 0
 
-    // B: instruction j of wave w fills k-row ((4j + w) * 64) / BN, pixels
-    // ((4j + w) * 64) % BN + lane; the pixel is the same for every j.
+    // Per-tile lane state (setup): B instruction j of wave w fills k-row
+    // ((4j + w) * 64) / BN, pixels ((4j + w) * 64) % BN + lane, so a lane's
+    // pixel is the same for every j; A instruction i of wave w fills chunks
+    // (A_INSTR * w + i) * 64 + lane.
     const int b_pix = BN == 64 ? lane : (wave & 1) * 64 + lane;
-    const long long P = P0 + b_pix;
-    const bool p_valid = P < p.Ptotal;
-    int n_img = 0, hi0 = 0, wi0 = 0;
-    if (p_valid) {
-        n_img = (int)(P / HWo);
-        const int rem = (int)(P - (long long)n_img * HWo);
-        const int ho = rem / Wo, wo = rem - (rem / Wo) * Wo;
-        hi0 = ho * p.stride - p.pad;
-        wi0 = wo * p.stride - p.pad;
-    }
-    const unsigned img_base = (unsigned)n_img * (unsigned)C_in * HW4;
-    // A: instruction i of wave w fills chunks (A_INSTR * w + i) * 64 + lane
-    int a_row[A_INSTR], a_c[A_INSTR];
+    int a_c[A_INSTR];
 #pragma unroll
     for (int i = 0; i < A_INSTR; ++i) {
         const int q = (A_INSTR * wave + i) * 64 + lane;
-        a_row[i] = min(m0 + (q >> 2), C_out - 1);
         a_c[i] = (q & 3) ^ (((q >> 2) >> 2) & 3);
     }
+    int m0 = 0, hi0 = 0, wi0 = 0, a_row[A_INSTR];
+    long long P0 = 0;
+    bool p_valid = false;
+    unsigned img_base = 0;
+    auto setup = [&](uint32_t t) {
+        uint32_t tm_id, tn_id;
+        grouped_tile(t, p.tiles_m, p.tiles_n, 2, tm_id, tn_id);
+        m0 = (int)tm_id * BM;
+        P0 = (long long)tn_id * BN;
+        const long long P = P0 + b_pix;
+        p_valid = P < p.Ptotal;
+        int n_img = 0;
+        hi0 = wi0 = 0;
+        if (p_valid) {
+            n_img = (int)(P / HWo);
+            const int rem = (int)(P - (long long)n_img * HWo);
+            const int ho = rem / Wo, wo = rem - (rem / Wo) * Wo;
+            hi0 = ho * p.stride - p.pad;
+            wi0 = wo * p.stride - p.pad;
+        }
+        img_base = (unsigned)n_img * (unsigned)C_in * HW4;
+#pragma unroll
+        for (int i = 0; i < A_INSTR; ++i) a_row[i] = min(m0 + (((A_INSTR * wave + i) * 64 + lane) >> 2), C_out - 1);
+    };
     const int ctiles = C_in / BK;
     const int ktiles = KHW * ctiles;
-    auto load_tile = [&](float* As, float* Bs, int kt) {
-        const bool live = kt < ktiles;
+    auto load_tile = [&](float* As, float* Bs, int kt, int kend) {
+        const bool live = kt < kend;
         const int tap = live ? kt / ctiles : 0;
         const int ci0 = (kt - tap * ctiles) * BK;
         const int kh = tap / KW, kw = tap - (tap / KW) * KW;
@@ -357,12 +378,6 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
     };
 
     f32x16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     int a_rd[TM][2];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -399,44 +414,143 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-
-    const int pairs = (ktiles + 1) / 2;
-    load_tile(As0, Bs0, 0);
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-    __syncthreads();
-    for (int pr = 0; pr < pairs; ++pr) {
-        load_tile(As1, Bs1, 2 * pr + 1);
-        compute(As0, Bs0);
+    // acc = the tile's sums over k-tiles [kbeg, kend), in pairs (a pair's
+    // second tile past kend loads zeros)
+    auto run = [&](int kbeg, int kend) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        const int pairs = (kend - kbeg + 1) / 2;
+        load_tile(As0, Bs0, kbeg, kend);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
-        if (MIX || pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);  // past the end: zeros
-        compute(As1, Bs1);
-        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-        __syncthreads();
-    }
+        for (int pr = 0; pr < pairs; ++pr) {
+            load_tile(As1, Bs1, kbeg + 2 * pr + 1, kend);
+            compute(As0, Bs0);
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            __syncthreads();
+            if (MIX || pr + 1 < pairs) load_tile(As0, Bs0, kbeg + 2 * pr + 2, kend);  // past the end: zeros
+            compute(As1, Bs1);
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            __syncthreads();
+        }
+    };
 
     // register r of lane l: channel row 8(r/4) + 4(l/32) + r%4, pixel l%32
-    const float* __restrict__ bias = p.bias;
-    with_act(p.act, [&](auto act_c) {
-        constexpr int ACT = decltype(act_c)::value;
+    auto store = [&]() {
+        const float* __restrict__ bias = p.bias;
+        with_act(p.act, [&](auto act_c) {
+            constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const long long Pc = P0 + wn * WN + j * 32 + lr;
-            if (Pc >= p.Ptotal) continue;
-            const int n_o = (int)(Pc / HWo);
-            const int pix = (int)(Pc - (long long)n_o * HWo);
-            float* obase = p.out + (size_t)n_o * C_out * HWo + pix;
+            for (int j = 0; j < TN; ++j) {
+                const long long Pc = P0 + wn * WN + j * 32 + lr;
+                if (Pc >= p.Ptotal) continue;
+                const int n_o = (int)(Pc / HWo);
+                const int pix = (int)(Pc - (long long)n_o * HWo);
+                float* obase = p.out + (size_t)n_o * C_out * HWo + pix;
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int cbase = m0 + wm * WM + i * 32 + 4 * lk;
+                for (int i = 0; i < TM; ++i) {
+                    const int cbase = m0 + wm * WM + i * 32 + 4 * lk;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int co = cbase + 8 * (r >> 2) + (r & 3);
-                    if (co < C_out) obase[(size_t)co * HWo] = act_fixed<ACT>(acc[i][j][r] + (bias ? bias[co] : 0.0f));
+                    for (int r = 0; r < 16; ++r) {
+                        const int co = cbase + 8 * (r >> 2) + (r & 3);
+                        if (co < C_out)
+                            obase[(size_t)co * HWo] = act_fixed<ACT>(acc[i][j][r] + (bias ? bias[co] : 0.0f));
+                    }
+                }
+            }
+        });
+    };
+
+    // Whole tiles: workgroups [0, sk_dp) take tiles [0, sk_dp) (each XCD a
+    // contiguous run).
+    // Stream-K: workgroup s of sk_wgs takes the s-th equal share of the
+    // remaining tiles' (tile, k-tile) units, in tile order.  A tile split
+    // between workgroups is finished by the one that arrives last at its
+    // counter: each share's sums go to its workgroup's slot (2s for the
+    // first tile of its range, 2s + 1 for the last) through the point of
+    // coherence, and the last re-reads all shares, its own included, and
+    // adds them in k order, so the sum does not depend on which came last;
+    // then it runs the epilogue.  Every workgroup of the launch is resident
+    // at once (the host sizes the grid to the CUs), and none waits for
+    // another.  Unit counts are 32-bit (the host checks U * sk_wgs).
+    // One loop body serves both kinds of workgroup (a whole tile is one
+    // pass), so the kernel holds one copy of the k loop and the epilogue.
+    const int S = p.sk_wgs, s = (int)blockIdx.x - p.sk_dp;
+    const int U = ((int)ntiles - p.sk_dp) * ktiles;
+    int t_rel, kbeg, kend, u = 0, uend = 0;
+    if (s < 0) {
+        t_rel = (int)xcd_contiguous_id(blockIdx.x, (uint32_t)p.sk_dp) - p.sk_dp;
+        kbeg = 0;
+        kend = ktiles;
+    } else {
+        u = s * U / S;
+        uend = (s + 1) * U / S;
+        t_rel = u / ktiles;
+        kbeg = u - t_rel * ktiles;
+        kend = min(ktiles, uend - t_rel * ktiles);
+        u = t_rel * ktiles + kend;
+    }
+    constexpr int QUADS = TM * TN * 4;  // 16-byte pieces of a lane's sums
+    for (;;) {
+        setup((uint32_t)(p.sk_dp + t_rel));
+        run(kbeg, kend);
+        bool out = true;
+        if (kbeg != 0 || kend != ktiles) {
+            // slot: 4 waves x QUADS x 64 lanes x 16 bytes = QUADS * 4096 bytes
+            const __amdgpu_buffer_rsrc_t part = coherent_buffer(p.sk_part, (size_t)2 * S * QUADS * 4096);
+            auto owner = [&](int v) { return ((v + 1) * S - 1) / U; };
+            auto slot_off = [&](int w) {
+                const int first = w * U / S / ktiles;
+                return ((2 * w + (t_rel == first ? 0 : 1)) * QUADS * 256 + wave * QUADS * 64 + lane) * 16;
+            };
+            const int mine = slot_off(s);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        store_coherent4(part, mine + ((i * TN + j) * 4 + q) * 64 * 16,
+                                        f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                              acc[i][j][4 * q + 3]});
+            const int w_lo = owner(t_rel * ktiles), w_hi = owner((t_rel + 1) * ktiles - 1);
+            out = arrive_last(p.sk_ctr + t_rel, (unsigned)(w_hi - w_lo + 1), &s_flag);
+            if (out) {
+                reset_arrival(p.sk_ctr + t_rel);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+                for (int w = w_lo; w <= w_hi; ++w) {
+                    const int off = slot_off(w);
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int j = 0; j < TN; ++j)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const f32x4 v = load_coherent4(part, off + ((i * TN + j) * 4 + q) * 64 * 16);
+                                acc[i][j][4 * q] += v.x;
+                                acc[i][j][4 * q + 1] += v.y;
+                                acc[i][j][4 * q + 2] += v.z;
+                                acc[i][j][4 * q + 3] += v.w;
+                            }
                 }
             }
         }
-    });
+        if (out) store();
+        if (u >= uend) break;
+        t_rel = u / ktiles;
+        kbeg = 0;
+        kend = min(ktiles, uend - t_rel * ktiles);
+        u = t_rel * ktiles + kend;
+    }
 }
 
 // wt[(co*KHW + tap)*C_in + ci] = w[(co*C_in + ci)*KHW + tap]: the OIHW
@@ -905,25 +1019,75 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d: too many tiles");
     constexpr int WGM = BM >= 64 ? 2 : 1;
     constexpr int WGN = 4 / WGM;
-    if (!p.wt && p.C_in % 16 == 0 && p.C_out % 4 == 0) {
-        const size_t wbytes = (size_t)p.C_out * p.Kdim * sizeof(float);
-        void* ws = nullptr;
-        if (int rc = workspace(ctx, wbytes, &ws)) return rc;
-        p.wt = (const float*)ws;
-        const size_t total = (size_t)p.C_out * p.Kdim;
-        hipLaunchKernelGGL(conv_weights_per_co, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)),
-                           dim3(256), 0, ctx->stream, (float*)ws, p.w, p.C_out, p.C_in, p.KH * p.KW);
-        if (int rc = check_launch("conv_weights_per_co")) return rc;
-    }
+    // conv2d_direct: whole tiles, plus a stream-K share of the rest when
+    // the tiles are not a multiple of the CUs (see conv2d_direct)
+    bool direct = false;
+    void (*kern)(const ConvParams) = nullptr;
     if constexpr ((BM == 64 || BM == 128) && (BN == 64 || BN == 128)) {
-        if (p.wt && tune("conv_direct", 1) &&
-            (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < ((size_t)1 << 31) - 64 &&
-            (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64) {
-            void (*kern)(const ConvParams) = tune("conv_mix", 1) ? conv2d_direct<BM, BN, KH_T, KW_T, true>
-                                                                 : conv2d_direct<BM, BN, KH_T, KW_T, false>;
-            hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kThreads), 0, ctx->stream, p);
-            return check_launch("conv2d_direct");
+        direct = p.C_in % 16 == 0 && p.C_out % 4 == 0 && tune("conv_direct", 1) &&
+                 (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < ((size_t)1 << 31) - 64 &&
+                 (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64;
+        kern = tune("conv_mix", 1) ? conv2d_direct<BM, BN, KH_T, KW_T, true> : conv2d_direct<BM, BN, KH_T, KW_T, false>;
+    }
+    p.sk_dp = (int)grid;
+    p.sk_wgs = 0;
+    size_t part_bytes = 0;
+    if (direct && tune("conv_stream_k", 1)) {
+        // resident workgroups per CU, per instantiation (host threads may
+        // race to fill it in: they all store the same value)
+        static std::atomic<int> occupancy[2];
+        std::atomic<int>& slot = occupancy[tune("conv_mix", 1) ? 1 : 0];
+        int occ = slot.load(std::memory_order_relaxed);
+        if (occ == 0) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kThreads, 0) != hipSuccess || occ < 1) occ = 1;
+            slot.store(occ, std::memory_order_relaxed);
         }
+        // When tiles / CUs is a little above an integer n (at most n + 1/4)
+        // and every workgroup is resident at once, whole tiles alone would
+        // leave some CUs n + 1 tiles and the rest n: instead (n - 1) * CUs
+        // workgroups take whole tiles and one per CU shares the rest, about
+        // 1 + (tiles - n CUs) / CUs tiles each.  Measured at N32 64->128 56^2:
+        // forward 140.4 -> 135.8 us, dgrad 150.3 -> 143.6 us; with 2, 3 or 6
+        // sharing workgroups per CU it ran slower (each shared tile costs a
+        // hand-off through the point of coherence), and larger remainders
+        // are faster as whole tiles (N33: 6.32 tiles per CU 141.0 against
+        // 143.7 us; N31: 5.93, 122.7 against 141.3).
+        const size_t cus = (size_t)cu_count(ctx), per = grid / cus, rem = grid % cus;
+        const size_t units = (grid - (per > 0 ? per - 1 : 0) * cus) * (size_t)p.Kdim / 16;
+        if (per >= 1 && per <= (size_t)occ && rem != 0 && rem <= cus / 4 && units * cus < ((size_t)1 << 31)) {
+            p.sk_dp = (int)((per - 1) * cus);
+            p.sk_wgs = (int)cus;
+            part_bytes = 2 * cus * BM * BN * sizeof(float);
+        }
+    }
+    const bool per_co = p.C_in % 16 == 0 && p.C_out % 4 == 0;
+    const size_t wcount = (size_t)p.C_out * p.Kdim;
+    const size_t wbytes = (p.prep == 1 && per_co) || p.prep == 2 ? (wcount * sizeof(float) + 255) / 256 * 256 : 0;
+    if (wbytes + part_bytes > 0) {
+        void* ws = nullptr;
+        if (int rc = workspace(ctx, wbytes + part_bytes, &ws)) return rc;
+        p.sk_part = (float*)((char*)ws + wbytes);
+        const unsigned wgrid = (unsigned)std::min<size_t>((wcount + 255) / 256, 2048);
+        if (p.prep == 1 && per_co) {
+            p.wt = (const float*)ws;
+            hipLaunchKernelGGL(conv_weights_per_co, dim3(wgrid), dim3(256), 0, ctx->stream, (float*)ws, p.w, p.C_out,
+                               p.C_in, p.KH * p.KW);
+            if (int rc = check_launch("conv_weights_per_co")) return rc;
+        } else if (p.prep == 2) {
+            hipLaunchKernelGGL(dgrad_weights, dim3(wgrid), dim3(256), 0, ctx->stream, (float*)ws, p.w_src, p.C_in,
+                               p.C_out, p.KH, p.KW, (int)per_co);
+            if (int rc = check_launch("conv2d_dgrad_weights")) return rc;
+            if (per_co)
+                p.wt = (const float*)ws;
+            else
+                p.w = (const float*)ws;
+        }
+    }
+    if (direct && p.wt) {
+        if (p.sk_wgs > 0)
+            if (int rc = counters(ctx, grid - (size_t)p.sk_dp, &p.sk_ctr)) return rc;
+        hipLaunchKernelGGL(kern, dim3((unsigned)(p.sk_dp + p.sk_wgs)), dim3(kThreads), 0, ctx->stream, p);
+        return check_launch("conv2d_direct");
     }
     if (p.wt)
         hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
@@ -984,6 +1148,7 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     p.Kdim = (int)(C_in * K_h * K_w);
     p.Ptotal = (long long)N * p.Ho * p.Wo;
     p.act = act;
+    p.prep = 1;
     // Tiles (C_out x pixels): 0 = 128x128, 1 = 128x64, 2 = 64x64, 3 = 32x128,
     // the one whose channel extent covers C_out with the least padding.
     // 128x64 measured best on the N32 64->128 56x56 config (with the direct
@@ -1037,17 +1202,8 @@ extern "C" int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx,
     p.Kdim = (int)(C_out * K_h * K_w);
     p.Ptotal = (long long)N * H * W;
     p.act = LANCIUS_HIP_ACT_NONE;
-    const bool per_co = p.C_in % 16 == 0 && p.C_out % 4 == 0;
-    void* ws = nullptr;
-    if (int rc = workspace(ctx, C_out * C_in * K_h * K_w * sizeof(float), &ws)) return rc;
-    const size_t wn = C_out * C_in * K_h * K_w;
-    hipLaunchKernelGGL(dgrad_weights, dim3((unsigned)std::min<size_t>((wn + 255) / 256, 2048)), dim3(256), 0,
-                       ctx->stream, (float*)ws, w, (int)C_out, (int)C_in, (int)K_h, (int)K_w, (int)per_co);
-    if (int rc = check_launch("conv2d_dgrad_weights")) return rc;
-    if (per_co)
-        p.wt = (const float*)ws;
-    else
-        p.w = (const float*)ws;
+    p.prep = 2;  // the launch lays out the flipped weights of w
+    p.w_src = w;
     const int tile = tune("conv_tile", default_tile((size_t)p.C_out));
     const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
     return rc ? rc : ok();
