@@ -454,6 +454,32 @@ def test_conv_config_full(dev):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(64 * 9)
 
 
+@pytest.mark.parametrize("N,C_in,H,W,C_out", [(32, 64, 56, 56, 128), (6, 16, 56, 56, 128), (23, 32, 28, 28, 64)])
+def test_conv_stream_k_repeatable(dev, N, C_in, H, W, C_out):
+    """Grids a little over a whole number of tiles per CU share their last
+    tiles between workgroups (1568, 294 and 282 tiles here); whichever
+    workgroup arrives last adds the shares in k order, so repeat calls give
+    identical bits, and the result matches the oracle."""
+    x = prng.normal(460 + N, (N, C_in, H, W))
+    w = prng.normal(461 + N, (C_out, C_in, 3, 3), std=float(np.sqrt(2.0 / (9 * C_in))))
+    dx, dw = _upload(dev, x, w)
+    do = dev.alloc(N * C_out * H * W * 4)
+    dev.fill(do, float("nan"), N * C_out * H * W)
+    case(f"conv stream-K N={N} C_in={C_in} {H}x{W} C_out={C_out}")
+    outs = []
+    for _ in range(3):
+        dev.conv2d(do, dx, dw, None, N, C_in, H, W, C_out, 3, 3, 1, 1, ACT_RELU)
+        outs.append(dev.download(do, (N, C_out, H, W)))
+    assert np.isfinite(outs[0]).all()
+    for o in outs[1:]:
+        assert np.array_equal(outs[0].view(np.uint32), o.view(np.uint32))
+    img = (N - 2, N)
+    ref = oracle.conv2d(x, w, 1, 1, True, images=img)
+    assert oracle.normwise_error(outs[0][slice(*img)], ref[slice(*img)]) <= oracle.tolerance(9 * C_in)
+    for b in (dx, dw, do):
+        b.free()
+
+
 def test_conv_bias(dev):
     N, C_in, H, W, C_out = 2, 4, 9, 9, 6
     x = prng.normal(71, (N, C_in, H, W))
