@@ -130,6 +130,25 @@ LANCIUS_HIP_EXPORT int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, 
                                               size_t N, size_t C_in, size_t H, size_t W,
                                               size_t C_out, size_t K_h, size_t K_w,
                                               size_t stride, size_t pad, int act);
+/* The same conv split in two for a weight used many times (an inference
+ * graph's constant filters): the reference reads w in OIHW inside its loops
+ * (lancius_kernels.c:147-165); the device kernels read the filter per
+ * output channel with taps outer and input channels inner, and
+ * lancius_hip_conv2d_f32 re-lays w into that order on every call.
+ * lancius_hip_conv2d_pack_weight does it once into `packed`
+ * (lancius_hip_conv2d_packed_bytes(...) bytes), and
+ * lancius_hip_conv2d_packed_f32 takes the packed copy in place of w; results
+ * are bit-identical to lancius_hip_conv2d_f32.  Both require C_in % 16 == 0
+ * and C_out % 4 == 0 (else -3); other convs read OIHW directly and have
+ * nothing to pack.  The device executor keeps one packed copy per such
+ * filter and re-packs it after an upload. */
+LANCIUS_HIP_EXPORT size_t lancius_hip_conv2d_packed_bytes(size_t C_out, size_t C_in, size_t K_h, size_t K_w);
+LANCIUS_HIP_EXPORT int lancius_hip_conv2d_pack_weight(lancius_hip_ctx* ctx, float* packed, const float* w,
+                                                      size_t C_out, size_t C_in, size_t K_h, size_t K_w);
+LANCIUS_HIP_EXPORT int lancius_hip_conv2d_packed_f32(lancius_hip_ctx* ctx, float* out, const float* in,
+                                                     const float* packed, const float* bias, size_t N, size_t C_in,
+                                                     size_t H, size_t W, size_t C_out, size_t K_h, size_t K_w,
+                                                     size_t stride, size_t pad, int act);
 
 /* Scaled-dot-product attention over [batch, S, H, D] row-major tensors
  * (row (b,i,h) starts at ((b*S + i)*H + h)*D).  causal != 0 masks keys

@@ -1115,10 +1115,14 @@ int launch_tile(lancius_hip_ctx* ctx, ConvParams& p, int tile) {
 
 using namespace lancius;
 
-extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* w,
-                                      const float* bias, size_t N, size_t C_in, size_t H, size_t W, size_t C_out,
-                                      size_t K_h, size_t K_w, size_t stride, size_t pad, int act) {
-    LANCIUS_REQUIRE(ctx && out && in && w, LANCIUS_HIP_ERR_NULL_PTR, "conv2d: NULL argument");
+namespace {
+
+// The forward conv with the filter as OIHW w (re-laid per call when the
+// kernels want it per output channel) or, with w null, already packed.
+int conv2d_entry(lancius_hip_ctx* ctx, float* out, const float* in, const float* w, const float* packed,
+                 const float* bias, size_t N, size_t C_in, size_t H, size_t W, size_t C_out, size_t K_h, size_t K_w,
+                 size_t stride, size_t pad, int act) {
+    LANCIUS_REQUIRE(ctx && out && in && (w || packed), LANCIUS_HIP_ERR_NULL_PTR, "conv2d: NULL argument");
     LANCIUS_REQUIRE(N && C_in && H && W && C_out && K_h && K_w && stride, LANCIUS_HIP_ERR_SHAPE,
                     "conv2d: empty shape");
     LANCIUS_REQUIRE(H + 2 * pad >= K_h && W + 2 * pad >= K_w, LANCIUS_HIP_ERR_SHAPE,
@@ -1133,6 +1137,7 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     p.out = out;
     p.in = in;
     p.w = w;
+    p.wt = packed;
     p.bias = bias;
     p.N = (int)N;
     p.C_in = (int)C_in;
@@ -1148,7 +1153,7 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     p.Kdim = (int)(C_in * K_h * K_w);
     p.Ptotal = (long long)N * p.Ho * p.Wo;
     p.act = act;
-    p.prep = 1;
+    p.prep = packed ? 0 : 1;
     // Tiles (C_out x pixels): 0 = 128x128, 1 = 128x64, 2 = 64x64, 3 = 32x128,
     // the one whose channel extent covers C_out with the least padding.
     // 128x64 measured best on the N32 64->128 56x56 config (with the direct
@@ -1158,6 +1163,44 @@ extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const fl
     const int tile = tune("conv_tile", default_tile(C_out));
     const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
     return rc ? rc : ok();
+}
+
+}  // namespace
+
+extern "C" int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* w,
+                                      const float* bias, size_t N, size_t C_in, size_t H, size_t W, size_t C_out,
+                                      size_t K_h, size_t K_w, size_t stride, size_t pad, int act) {
+    LANCIUS_REQUIRE(w, LANCIUS_HIP_ERR_NULL_PTR, "conv2d: NULL weights");
+    return conv2d_entry(ctx, out, in, w, nullptr, bias, N, C_in, H, W, C_out, K_h, K_w, stride, pad, act);
+}
+
+extern "C" size_t lancius_hip_conv2d_packed_bytes(size_t C_out, size_t C_in, size_t K_h, size_t K_w) {
+    return C_out * C_in * K_h * K_w * sizeof(float);
+}
+
+extern "C" int lancius_hip_conv2d_pack_weight(lancius_hip_ctx* ctx, float* packed, const float* w, size_t C_out,
+                                              size_t C_in, size_t K_h, size_t K_w) {
+    LANCIUS_REQUIRE(ctx && packed && w, LANCIUS_HIP_ERR_NULL_PTR, "conv2d_pack_weight: NULL argument");
+    LANCIUS_REQUIRE(C_out && C_in && K_h && K_w && C_in % 16 == 0 && C_out % 4 == 0 &&
+                        C_out * C_in * K_h * K_w < ((size_t)1 << 31),
+                    LANCIUS_HIP_ERR_SHAPE, "conv2d_pack_weight: C_out=%zu C_in=%zu (need C_in %% 16 == 0, C_out %% 4 == 0)",
+                    C_out, C_in);
+    if (int rc = bind_device(ctx)) return rc;
+    const size_t total = C_out * C_in * K_h * K_w;
+    hipLaunchKernelGGL(conv_weights_per_co, dim3((unsigned)std::min<size_t>((total + 255) / 256, 2048)), dim3(256), 0,
+                       ctx->stream, packed, w, (int)C_out, (int)C_in, (int)(K_h * K_w));
+    if (int rc = check_launch("conv_weights_per_co")) return rc;
+    return ok();
+}
+
+extern "C" int lancius_hip_conv2d_packed_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* packed,
+                                             const float* bias, size_t N, size_t C_in, size_t H, size_t W,
+                                             size_t C_out, size_t K_h, size_t K_w, size_t stride, size_t pad,
+                                             int act) {
+    LANCIUS_REQUIRE(packed, LANCIUS_HIP_ERR_NULL_PTR, "conv2d_packed: NULL weights");
+    LANCIUS_REQUIRE(C_in % 16 == 0 && C_out % 4 == 0, LANCIUS_HIP_ERR_SHAPE,
+                    "conv2d_packed: C_out=%zu C_in=%zu (need C_in %% 16 == 0, C_out %% 4 == 0)", C_out, C_in);
+    return conv2d_entry(ctx, out, in, nullptr, packed, bias, N, C_in, H, W, C_out, K_h, K_w, stride, pad, act);
 }
 
 extern "C" int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx, const float* dy, const float* w,

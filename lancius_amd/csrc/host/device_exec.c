@@ -22,6 +22,7 @@ typedef enum {
 } lkind;
 
 enum { ROLE_NONE = 0, ROLE_INPUT, ROLE_CONST, ROLE_POOLED, ROLE_ALIAS, ROLE_FUSED };
+enum { PACK_NONE = 0, PACK_I8, PACK_CONV };
 
 typedef struct {
     uint32_t out;   /* node id written */
@@ -52,13 +53,16 @@ struct lancius_device_program {
     size_t* bytes;
     uint8_t* role;
     uint8_t* is_i8;  /* by id: INPUT holding int8 weights (1 byte per element) */
-    /* by id: an int8 GEMM weight's copy in the layout the int8 product reads
-     * (lancius_hip_i8_pack_weight), its [K, N], and whether the weight
-     * changed since it was packed (set by uploads and by handing out the
-     * buffer; lancius_device_run re-packs first) */
+    /* by id: a weight's copy in the layout its kernel reads, what it is, its
+     * dimensions, and whether the weight changed since it was packed (set by
+     * uploads and by handing out the buffer; lancius_device_run re-packs
+     * first):
+     *   PACK_I8:   an int8 GEMM B [K, N] (lancius_hip_i8_pack_weight);
+     *   PACK_CONV: an fp32 conv filter OIHW [C_out, C_in, K_h, K_w]
+     *              (lancius_hip_conv2d_pack_weight) */
     char** packed;
-    size_t* packed_k;
-    size_t* packed_n;
+    uint8_t* packed_kind;
+    size_t* packed_dims; /* 4 per id */
     uint8_t* packed_stale;
     uint8_t* readable;
     int32_t** argmax;
@@ -682,8 +686,8 @@ void lancius_device_program_destroy(lancius_device_program* p) {
         for (uint32_t i = 0; i < p->n_ids; i++)
             if (p->packed[i]) lancius_hip_free(p->ctx, p->packed[i]);
     free(p->packed);
-    free(p->packed_k);
-    free(p->packed_n);
+    free(p->packed_kind);
+    free(p->packed_dims);
     free(p->packed_stale);
     free(p->ptr);
     free(p->bytes);
@@ -798,14 +802,14 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
     p->ctx = ctx;
     p->exec = ctx;
     p->n_ids = ids;
-    const size_t ids2 = 2 * (size_t)ids;
+    const size_t ids2 = 2 * (size_t)ids, ids4 = 4 * (size_t)ids;
     if (!CALLOC(c.node, ids) || !CALLOC(c.wave, ids) || !CALLOC(c.order, ids) || !CALLOC(c.consumers, ids) ||
         !CALLOC(c.sole, ids) || !CALLOC(c.root, ids) || !CALLOC(c.absorbed, ids) || !CALLOC(c.chain_head, ids) ||
         !CALLOC(c.chain_bias, ids) || !CALLOC(c.chain_res, ids) || !CALLOC(c.chain_act, ids) ||
         !CALLOC(c.mm_src, ids2) ||
         !CALLOC(p->ptr, ids) || !CALLOC(p->bytes, ids) || !CALLOC(p->role, ids) || !CALLOC(p->readable, ids) ||
-        !CALLOC(p->is_i8, ids) || !CALLOC(p->packed, ids) || !CALLOC(p->packed_k, ids) ||
-        !CALLOC(p->packed_n, ids) || !CALLOC(p->packed_stale, ids) ||
+        !CALLOC(p->is_i8, ids) || !CALLOC(p->packed, ids) || !CALLOC(p->packed_kind, ids) ||
+        !CALLOC(p->packed_dims, ids4) || !CALLOC(p->packed_stale, ids) ||
         !CALLOC(p->argmax, ids) || !CALLOC(p->rows, ids) || !CALLOC(birth, ids) || !CALLOC(last, ids) ||
         !CALLOC(pinned, ids)) {
         rc = LANCIUS_HIP_ERR_OOM;
@@ -1066,16 +1070,36 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         rc = lancius_hip_fill_f32(ctx, (float*)p->ptr[n->id], (float)n->attr_val, elems(n));
         if (rc) goto out;
     }
-    /* one packed copy per int8 GEMM weight, filled by the first run */
+    /* one packed copy per int8 GEMM weight, and per fp32 conv filter that
+     * the caller or a CONST fills (not one a launch computes), filled by the
+     * first run */
     for (uint32_t i = 0; i < p->n_launches && !rc; i++) {
         const launch_t* L = &p->launches[i];
         const uint32_t w = L->m[0].in[1];
-        if (L->kind != L_GEMM || !L->i8 || p->packed[w]) continue;
+        /* only these two launch kinds read a weight in slot 1; other kinds
+         * may leave it NONE */
+        if ((L->kind != L_GEMM && L->kind != L_CONV) || w == NONE || p->packed[w]) continue;
+        size_t* d = p->packed_dims + 4 * (size_t)w;
+        size_t bytes = 0;
+        if (L->kind == L_GEMM && L->i8) {
+            p->packed_kind[w] = PACK_I8;
+            d[0] = L->d[1];
+            d[1] = L->d[2];
+            bytes = lancius_hip_i8_packed_bytes(d[0], d[1]);
+        } else if (L->kind == L_CONV && !L->i8 && L->d[1] % 16 == 0 && L->d[4] % 4 == 0 &&
+                   (p->role[w] == ROLE_INPUT || p->role[w] == ROLE_CONST)) {
+            p->packed_kind[w] = PACK_CONV;
+            d[0] = L->d[4];
+            d[1] = L->d[1];
+            d[2] = L->d[5];
+            d[3] = L->d[6];
+            bytes = lancius_hip_conv2d_packed_bytes(d[0], d[1], d[2], d[3]);
+        } else {
+            continue;
+        }
         void* buf = NULL;
-        rc = lancius_hip_malloc(ctx, &buf, lancius_hip_i8_packed_bytes(L->d[1], L->d[2]));
+        rc = lancius_hip_malloc(ctx, &buf, bytes);
         p->packed[w] = (char*)buf;
-        p->packed_k[w] = L->d[1];
-        p->packed_n[w] = L->d[2];
         p->packed_stale[w] = 1;
     }
     if (rc) goto out;
@@ -1151,6 +1175,10 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
                 return lancius_hip_conv2d_i8_f32(ctx, P(m->out), P(m->in[0]), (const int8_t*)prog->ptr[m->in[1]],
                                                  L->scale_w, NULL, L->d[0], L->d[1], L->d[2], L->d[3], L->d[4],
                                                  L->d[5], L->d[6], L->d[7], L->d[8], L->act);
+            if (prog->packed[m->in[1]])
+                return lancius_hip_conv2d_packed_f32(ctx, P(m->out), P(m->in[0]), (const float*)prog->packed[m->in[1]],
+                                                     NULL, L->d[0], L->d[1], L->d[2], L->d[3], L->d[4], L->d[5],
+                                                     L->d[6], L->d[7], L->d[8], L->act);
             return lancius_hip_conv2d_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), NULL, L->d[0], L->d[1], L->d[2],
                                           L->d[3], L->d[4], L->d[5], L->d[6], L->d[7], L->d[8], L->act);
         case L_LN:
@@ -1227,13 +1255,17 @@ static int run_all(lancius_device_program* prog) {
     return 0;
 }
 
-/* Re-lay every int8 GEMM weight that changed since it was last packed, on
- * the caller's stream (after its uploads, before the launches). */
+/* Re-lay every packed weight that changed since it was last packed, on the
+ * caller's stream (after its uploads, before the launches). */
 static int repack_stale(lancius_device_program* prog) {
     for (uint32_t i = 0; i < prog->n_ids; i++) {
         if (!prog->packed_stale[i]) continue;
-        const int rc = lancius_hip_i8_pack_weight(prog->ctx, (int8_t*)prog->packed[i], (const int8_t*)prog->ptr[i],
-                                                  prog->packed_k[i], prog->packed_n[i]);
+        const size_t* d = prog->packed_dims + 4 * (size_t)i;
+        const int rc = prog->packed_kind[i] == PACK_I8
+                           ? lancius_hip_i8_pack_weight(prog->ctx, (int8_t*)prog->packed[i],
+                                                        (const int8_t*)prog->ptr[i], d[0], d[1])
+                           : lancius_hip_conv2d_pack_weight(prog->ctx, (float*)prog->packed[i],
+                                                            (const float*)prog->ptr[i], d[0], d[1], d[2], d[3]);
         if (rc) return rc;
         prog->packed_stale[i] = 0;
     }
@@ -1281,9 +1313,9 @@ int lancius_device_upload(lancius_device_program* prog, const lancius_node* n, c
     if (n->id >= prog->n_ids || (prog->role[n->id] != ROLE_INPUT && prog->role[n->id] != ROLE_CONST))
         return LANCIUS_HIP_ERR_UNSUPPORTED;
     const size_t e = elems(n);
+    if (prog->packed[n->id]) prog->packed_stale[n->id] = 1; /* re-packed by the next run */
     if (prog->is_i8[n->id]) { /* int8 weights take their int8 bytes */
         if (host_dtype != LANCIUS_DTYPE_INT8) return LANCIUS_HIP_ERR_DTYPE;
-        if (prog->packed[n->id]) prog->packed_stale[n->id] = 1;
         return lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e);
     }
     if (host_dtype == LANCIUS_DTYPE_FP32) return lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e * 4);

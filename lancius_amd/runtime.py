@@ -73,6 +73,10 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_gemm_grouped_f32.argtypes = [vp, sz, vpp, vpp, vpp, sz, sz, sz, vpp, i32, vpp]
     lib.lancius_hip_gemm_f32_noalloc.argtypes = [vp, vp, vp, vp, sz, sz, sz, vp, i32, vp]
     lib.lancius_hip_conv2d_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, sz, sz, i32]
+    lib.lancius_hip_conv2d_packed_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, sz, sz, i32]
+    lib.lancius_hip_conv2d_pack_weight.argtypes = [vp, vp, vp, sz, sz, sz, sz]
+    lib.lancius_hip_conv2d_packed_bytes.argtypes = [sz, sz, sz, sz]
+    lib.lancius_hip_conv2d_packed_bytes.restype = sz
     lib.lancius_hip_attention_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, sz, sz, i32, f32]
     lib.lancius_hip_attention_grouped_f32.argtypes = [vp, sz, vpp, vpp, vpp, vpp, sz, sz, sz, i32, f32]
     lib.lancius_hip_layernorm_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, f32]
@@ -364,6 +368,16 @@ class Device:
     def gemm_i8(self, C_, A, B_i8, scale_b, M, K, N, bias=None, act=ACT_NONE, residual=None) -> None:
         _check(self.lib.lancius_hip_gemm_i8_f32(self.ctx, _vp(C_), _vp(A), _vp(B_i8), float(scale_b), M, K, N,
                                                 _vp(bias), act, _vp(residual)))
+
+    def conv2d_packed_bytes(self, C_out, C_in, K_h, K_w) -> int:
+        return int(self.lib.lancius_hip_conv2d_packed_bytes(C_out, C_in, K_h, K_w))
+
+    def conv2d_pack_weight(self, packed, w, C_out, C_in, K_h, K_w) -> None:
+        _check(self.lib.lancius_hip_conv2d_pack_weight(self.ctx, _vp(packed), _vp(w), C_out, C_in, K_h, K_w))
+
+    def conv2d_packed(self, out, x, packed, bias, N, C_in, H, W, C_out, K_h, K_w, stride, pad, act=ACT_NONE) -> None:
+        _check(self.lib.lancius_hip_conv2d_packed_f32(self.ctx, _vp(out), _vp(x), _vp(packed), _vp(bias), N, C_in, H,
+                                                      W, C_out, K_h, K_w, stride, pad, act))
 
     def i8_packed_bytes(self, K, N) -> int:
         return int(self.lib.lancius_hip_i8_packed_bytes(K, N))

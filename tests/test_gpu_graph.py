@@ -259,6 +259,29 @@ def test_conv_graph_config(dev):
     pl.close()
 
 
+def test_conv_graph_repacks_changed_filter(dev):
+    """The executor keeps one packed copy of a conv filter the caller
+    uploads (C_in % 16 == 0); a new upload and a write through
+    lancius_device_buffer must both reach the next run."""
+    N, C_in, H, W, C_out = 2, 16, 12, 12, 32
+    pl = Planned(graphs.build_conv(graph_lib(), N=N, C_in=C_in, H=H, W=W, C_out=C_out))
+    case("conv graph, filter re-uploaded")
+    prog = pl.program(dev)
+    x = prng.normal(700, (N, C_in, H, W))
+    prog.upload(pl.bg.node("x"), x)
+    for seed, how in ((1, "upload"), (2, "upload"), (3, "buffer")):
+        w = prng.normal(710 + seed, (C_out, C_in, 3, 3), std=0.1)
+        if how == "upload":
+            prog.upload(pl.bg.node("w"), w)
+        else:
+            dev.write(prog.buffer(pl.bg.node("w")), w)
+        prog.run()
+        got = prog.download(pl.bg.node("relu"))
+        assert oracle.normwise_error(got, oracle.conv2d(x, w, 1, 1, True)) <= oracle.tolerance(9 * C_in), (seed, how)
+    prog.close()
+    pl.close()
+
+
 # ---- transformer block ----------------------------------------------------------------
 
 

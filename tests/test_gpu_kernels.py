@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 import oracle
-from lancius_amd import ACT_GELU, ACT_NONE, ACT_RELU, prng
+from lancius_amd import ACT_GELU, ACT_NONE, ACT_RELU, HipError, prng
 from tests.conftest import case
 
 pytestmark = pytest.mark.gpu
@@ -478,6 +478,43 @@ def test_conv_stream_k_repeatable(dev, N, C_in, H, W, C_out):
     assert oracle.normwise_error(outs[0][slice(*img)], ref[slice(*img)]) <= oracle.tolerance(9 * C_in)
     for b in (dx, dw, do):
         b.free()
+
+
+@pytest.mark.parametrize("N,C_in,H,W,C_out,KH,KW,stride,pad,act", [
+    (4, 32, 28, 28, 64, 3, 3, 1, 1, ACT_RELU),   # direct kernel
+    (2, 16, 15, 13, 36, 5, 5, 2, 2, ACT_NONE),   # 5x5, stride 2, runtime filter size
+    (32, 64, 56, 56, 128, 3, 3, 1, 1, ACT_RELU),  # the config (stream-K grid)
+])
+def test_conv_packed_weight_bit_identical(dev, N, C_in, H, W, C_out, KH, KW, stride, pad, act):
+    """lancius_hip_conv2d_pack_weight once + lancius_hip_conv2d_packed_f32
+    gives the bits of lancius_hip_conv2d_f32 (which re-lays w every call)."""
+    Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    x = prng.normal(470 + C_in, (N, C_in, H, W))
+    w = prng.normal(471 + C_in, (C_out, C_in, KH, KW), std=float(np.sqrt(2.0 / (KH * KW * C_in))))
+    b = prng.normal(472 + C_in, (C_out,))
+    dx, dw, db = _upload(dev, x, w, b)
+    packed = dev.alloc(dev.conv2d_packed_bytes(C_out, C_in, KH, KW))
+    o1, o2 = dev.alloc(N * C_out * Ho * Wo * 4), dev.alloc(N * C_out * Ho * Wo * 4)
+    case(f"conv packed N={N} C_in={C_in} {H}x{W} C_out={C_out} k={KH}x{KW} s={stride}")
+    dev.conv2d(o1, dx, dw, db, N, C_in, H, W, C_out, KH, KW, stride, pad, act)
+    dev.conv2d_pack_weight(packed, dw, C_out, C_in, KH, KW)
+    dev.conv2d_packed(o2, dx, packed, db, N, C_in, H, W, C_out, KH, KW, stride, pad, act)
+    a, c = dev.download(o1, (N, C_out, Ho, Wo)), dev.download(o2, (N, C_out, Ho, Wo))
+    assert np.isfinite(a).all()
+    assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+    for buf in (dx, dw, db, packed, o1, o2):
+        buf.free()
+
+
+def test_conv_packed_weight_shape_limits(dev):
+    case("conv packed limits")
+    for C_out, C_in in ((4, 3), (6, 16)):  # C_in % 16 != 0, C_out % 4 != 0
+        with pytest.raises(HipError) as e:
+            dev.conv2d_pack_weight(1, 1, C_out, C_in, 3, 3)
+        assert e.value.code == -3
+        with pytest.raises(HipError) as e:
+            dev.conv2d_packed(1, 1, 1, None, 1, C_in, 8, 8, C_out, 3, 3, 1, 1)
+        assert e.value.code == -3
 
 
 def test_conv_bias(dev):
