@@ -48,7 +48,6 @@ constexpr int kMaxSplit = 4;      // mlp2_split: K ranges per tile
 constexpr int kSplitMaxTiles = 16;  // mlp2_split by default: at most 16 * kMaxSplit arrivals per row block
 constexpr int kSplitMinK = 2048;    // and at least 256 KiB per workgroup of mlp2_tiles
 constexpr int kOut = 0x7ffffff0;  // a byte offset past the end of any operand: the load returns 0
-constexpr int kYPer = kFR * kMaxOut / 256;  // (row, output) pairs of a block per thread
 
 // Every global read is a buffer load whose offset is pushed past the end of
 // its operand where the element does not exist, so no load sits behind a
@@ -158,69 +157,102 @@ __device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float (*Xs)[k
     return acc;
 }
 
-// This thread's (row, output) pairs of a 16-row block: i = tid + 256 u is
-// row i / N2, output i % N2; valid when the pair exists and its row < M.
-struct RowPairs {
-    int r[kYPer], j[kYPer];
-    bool ok[kYPer];
-    __device__ RowPairs(int m0, int M, int N2) {
-#pragma unroll
-        for (int u = 0; u < kYPer; ++u) {
-            const int i = (int)threadIdx.x + 256 * u;
-            r[u] = i / N2;
-            j[u] = i - r[u] * N2;
-            ok[u] = i < kFR * N2 && m0 + r[u] < M;
-        }
-    }
-};
+// Outputs of a 16-row block: row 4 w + g belongs to lanes 16 g .. 16 g + 15
+// of wave w, and lane 16 g + c holds outputs c + 16 q, q < kOutPerLane
+// (N2 <= 64), so every reduction over a row stays inside one DPP row of 16
+// lanes and the four rows of a wave reduce together.
+constexpr int kOutPerLane = kMaxOut / 16;
 
-// The block's outputs from Ys (y after b2 and act2, all rows written, the
-// caller has synchronised): the logits, or the reference's softmax
-// (lancius_scheduler.c:284-294) with one (row, output) pair per thread and
-// the same arithmetic (m = the row's maximum, e = expf(y - m), sum = the
-// e's added in output order, p = e / sum), then the first maximum of each
-// row's p scanning with '>' from -1e9 (B/examples/train_mnist.c:206-209).
-__device__ __forceinline__ void finish_rows(const ChainParams& p, const RowPairs& q, int m0, float (*Ys)[kMaxOut],
-                                            float (*Es)[kMaxOut]) {
-    const int M = p.M, N2 = p.N2, tid = threadIdx.x;
+template <int kCtrl>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xf, 0xf, false);
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, dpp_i<kCtrl>(__builtin_bit_cast(int, v)));
+}
+// DPP controls: lane ^ 1 and lane ^ 2 within a quad, lane 7 - i within a
+// half row of 8, lane 15 - i within a row of 16.  Once the quads agree, the
+// half-row mirror pairs every lane with a lane of the other quad, and once
+// the half rows agree the row mirror pairs it with the other half: both
+// partners combine the same two values, so all 16 lanes end with identical
+// bits.
+constexpr int kQuadXor1 = 0xb1, kQuadXor2 = 0x4e, kHalfRowMirror = 0x141, kRowMirror = 0x140;
+
+template <class Op>
+__device__ __forceinline__ float row16(float v, Op op) {
+    v = op(v, dpp_f<kQuadXor1>(v));
+    v = op(v, dpp_f<kQuadXor2>(v));
+    v = op(v, dpp_f<kHalfRowMirror>(v));
+    return op(v, dpp_f<kRowMirror>(v));
+}
+
+// The first maximum of a row's values (the larger value, the smaller output
+// index among equal ones): the same winner whichever of two lanes combines.
+template <int kCtrl>
+__device__ __forceinline__ void argmax_step(float& best, int& bi) {
+    const float ob = dpp_f<kCtrl>(best);
+    const int oi = dpp_i<kCtrl>(bi);
+    const bool take = ob > best || (ob == best && oi < bi);
+    best = take ? ob : best;
+    bi = take ? oi : bi;
+}
+
+// The block's outputs from y (after b2 and act2; y[q] is output c + 16 q of
+// this lane's row): the logits, or the reference's softmax
+// (lancius_scheduler.c:284-294: m = the row's maximum, p = exp(y - m) /
+// sum of exp(y - m)), then the first maximum of each row's p, as scanning
+// with '>' from -1e9 finds it (B/examples/train_mnist.c:206-209): the
+// largest p, the smallest output among equal ones, output 0 when no p
+// exceeds -1e9.  Every lane runs the reductions (DPP reads no lane outside
+// its row); only the stores are masked.  No LDS, no barrier.
+__device__ __forceinline__ void finish_rows(const ChainParams& p, int m0, int wave, int lane,
+                                            const float (&y)[kOutPerLane]) {
+    const int N2 = p.N2, c = lane & 15;
+    const int r = m0 + 4 * wave + (lane >> 4);
+    const bool row_on = r < p.M;
+    float* o = p.out + (size_t)r * N2;
     if (!p.softmax) {
 #pragma unroll
-        for (int u = 0; u < kYPer; ++u)
-            if (q.ok[u]) p.out[(m0 + q.r[u]) * N2 + q.j[u]] = Ys[q.r[u]][q.j[u]];
+        for (int q = 0; q < kOutPerLane; ++q)
+            if (row_on && c + 16 * q < N2) o[c + 16 * q] = y[q];
         return;
     }
+    // output groups q with 16 q >= N2 hold no output of any lane: skipped
+    // (uniformly), so N2 <= 16 costs one exponential and one division
+    float m = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < kYPer; ++u) {
-        if (!q.ok[u]) continue;
-        const float* yr = Ys[q.r[u]];
-        float m = yr[0];
-        for (int c = 1; c < N2; ++c) m = fmaxf(m, yr[c]);
-        Es[q.r[u]][q.j[u]] = expf(yr[q.j[u]] - m);
+    for (int q = 0; q < kOutPerLane; ++q)
+        if (16 * q < N2 && c + 16 * q < N2) m = fmaxf(m, y[q]);
+    m = row16(m, [](float a, float b) { return fmaxf(a, b); });
+    float e[kOutPerLane], s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kOutPerLane; ++q) {
+        e[q] = 0.0f;
+        if (16 * q >= N2) continue;
+        if (c + 16 * q < N2) e[q] = expf(y[q] - m);
+        s += e[q];
     }
-    __syncthreads();
+    s = row16(s, [](float a, float b) { return a + b; });
+    float best = -1e9f;
+    int bi = 0;
 #pragma unroll
-    for (int u = 0; u < kYPer; ++u) {
-        if (!q.ok[u]) continue;
-        const float* er = Es[q.r[u]];
-        float sum = 0.0f;
-        for (int c = 0; c < N2; ++c) sum += er[c];
-        const float prob = er[q.j[u]] / sum;
-        p.out[(m0 + q.r[u]) * N2 + q.j[u]] = prob;
-        Ys[q.r[u]][q.j[u]] = prob;
+    for (int q = 0; q < kOutPerLane; ++q) {
+        if (16 * q >= N2) continue;
+        const int j = c + 16 * q;
+        const float prob = e[q] / s;
+        if (row_on && j < N2) o[j] = prob;
+        if (j < N2 && prob > best) {  // q ascending: the lane's first maximum
+            best = prob;
+            bi = j;
+        }
     }
     if (!p.argmax) return;
-    __syncthreads();
-    if (tid < kFR && m0 + tid < M) {
-        float best = -1e9f;
-        int bi = 0;
-        for (int j = 0; j < N2; ++j) {
-            if (Ys[tid][j] > best) {
-                best = Ys[tid][j];
-                bi = j;
-            }
-        }
-        p.argmax[m0 + tid] = bi;
-    }
+    argmax_step<kQuadXor1>(best, bi);
+    argmax_step<kQuadXor2>(best, bi);
+    argmax_step<kHalfRowMirror>(best, bi);
+    argmax_step<kRowMirror>(best, bi);
+    if (row_on && c == 0) p.argmax[r] = bi;
 }
 
 // mlp2_split, for N1 <= kSplitMaxN1.  Workgroup (row block b of 16 rows,
@@ -249,8 +281,6 @@ __global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
     constexpr int kStage = kFR * kXP + kFKC * kFC;
     __shared__ __attribute__((aligned(16))) float smem[kStage];
     __shared__ float red[4][kFR][kFC + 1];
-    __shared__ float Ys[kFR][kMaxOut];
-    __shared__ float Es[kFR][kMaxOut];
     __shared__ float B2s[kMaxOut];
     __shared__ int s_flag;
 
@@ -365,17 +395,25 @@ __global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = ya[r];
     __syncthreads();
-    const RowPairs q(m0, M, N2);
+    // y of this lane's row and outputs c + 16 q: the waves' K parts of the
+    // output tile q added in wave order
+    float y[kOutPerLane];
+    {
+        const int r = 4 * wave + lq;
 #pragma unroll
-    for (int u = 0; u < kYPer; ++u) {
-        if (!q.ok[u]) continue;
-        const int t = q.j[u] / 16, c = q.j[u] % 16;
-        float y = red[t * parts][q.r[u]][c];
-        for (int k = 1; k < parts; ++k) y += red[t * parts + k][q.r[u]][c];
-        Ys[q.r[u]][q.j[u]] = apply_act(y + B2s[q.j[u]], p.act2);
+        for (int q = 0; q < kOutPerLane; ++q) {
+            y[q] = 0.0f;
+            if (16 * q >= N2) continue;  // uniform
+            const int j = li + 16 * q;
+            float v = 0.0f;
+            if (j < N2) {
+                v = red[q * parts][r][li];
+                for (int k = 1; k < parts; ++k) v += red[q * parts + k][r][li];
+            }
+            y[q] = apply_act(v + B2s[j], p.act2);
+        }
     }
-    __syncthreads();
-    finish_rows(p, q, m0, Ys, Es);
+    finish_rows(p, m0, wave, lane, y);
 }
 
 // mlp2_tiles, for any N1 within the limits.  Workgroup (column tile t of 16
@@ -397,8 +435,6 @@ __global__ void __launch_bounds__(256) mlp2_tiles(const ChainParams p) {
     __shared__ float Hs[kFR][kFC + 1];
     __shared__ float W2s[kFC * kMaxOut];  // W2 rows of the tile, row pitch N2
     __shared__ float B2s[kMaxOut];
-    __shared__ float Ys[kFR][kMaxOut];
-    __shared__ float Es[kFR][kMaxOut];
     __shared__ int s_flag;
 
     const int tn = (int)blockIdx.x % p.tiles_n, rb = (int)blockIdx.x / p.tiles_n;
@@ -439,41 +475,58 @@ __global__ void __launch_bounds__(256) mlp2_tiles(const ChainParams p) {
         Hs[r][c] = h;  // rows past M and columns past N1 hold 0
     }
     __syncthreads();
-    // this tile's share of y for the block's rows
-    const RowPairs q(m0, M, N2);
+    // this tile's share of y for the lane's row and outputs c + 16 q
     const int MN2 = M * N2;
+    const int r = 4 * wave + lq;  // of the block
+    const bool row_on = m0 + r < M;
     const __amdgpu_buffer_rsrc_t ypart = coherent_buffer(p.part, (size_t)p.tiles_n * MN2 * sizeof(float));
 #pragma unroll
-    for (int u = 0; u < kYPer; ++u) {
-        if (!q.ok[u]) continue;
+    for (int q = 0; q < kOutPerLane; ++q) {
+        if (16 * q >= N2) continue;  // uniform
+        const int j = li + 16 * q;
         float a = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kFC; ++k) a += Hs[q.r[u]][k] * W2s[k * N2 + q.j[u]];
-        store_coherent(ypart, (tn * MN2 + (m0 + q.r[u]) * N2 + q.j[u]) * (int)sizeof(float), a);
+        for (int k = 0; k < kFC; ++k) a += Hs[r][k] * W2s[k * N2 + j];  // within W2s: j < 64
+        store_coherent(ypart, row_on && j < N2 ? (tn * MN2 + (m0 + r) * N2 + j) * (int)sizeof(float) : kOut, a);
     }
     if (!arrive_last(p.counters + rb, (unsigned)p.tiles_n, &s_flag)) return;
     reset_arrival(p.counters + rb);
 
     // the block's rows: y = sum of the tiles' shares in tile order + b2
-    // (loads past the last tile fall outside the buffer and return 0)
+    // (loads past the last tile or outside the block fall outside the
+    // buffer and return 0)
+    constexpr int kChunk = 16;
+    float y[kOutPerLane];
+    int off[kOutPerLane];
 #pragma unroll
-    for (int u = 0; u < kYPer; ++u) {
-        if (!q.ok[u]) continue;
-        constexpr int kChunk = 16;
-        const int off = ((m0 + q.r[u]) * N2 + q.j[u]) * (int)sizeof(float);
-        float y = 0.0f;
-        for (int t0 = 0; t0 < p.tiles_n; t0 += kChunk) {
-            float t[kChunk];
+    for (int q = 0; q < kOutPerLane; ++q) {
+        const int j = li + 16 * q;
+        y[q] = 0.0f;
+        off[q] = row_on && j < N2 ? ((m0 + r) * N2 + j) * (int)sizeof(float) : kOut;
+    }
+    for (int t0 = 0; t0 < p.tiles_n; t0 += kChunk) {
+        // every output group's loads of the chunk before any sum
+        float t[kOutPerLane][kChunk];
 #pragma unroll
-            for (int c = 0; c < kChunk; ++c) t[c] = load_coherent(ypart, off + (t0 + c) * MN2 * (int)sizeof(float));
+        for (int q = 0; q < kOutPerLane; ++q) {
+            if (16 * q >= N2) continue;  // uniform
 #pragma unroll
             for (int c = 0; c < kChunk; ++c)
-                if (t0 + c < p.tiles_n) y = (t0 + c == 0) ? t[c] : y + t[c];
+                t[q][c] = load_coherent(
+                    ypart, off[q] != kOut && t0 + c < p.tiles_n ? off[q] + (t0 + c) * MN2 * (int)sizeof(float) : kOut);
         }
-        Ys[q.r[u]][q.j[u]] = apply_act(y + B2s[q.j[u]], p.act2);
+#pragma unroll
+        for (int q = 0; q < kOutPerLane; ++q) {
+            if (16 * q >= N2) continue;
+#pragma unroll
+            for (int c = 0; c < kChunk; ++c)
+                if (t0 + c < p.tiles_n) y[q] = (t0 + c == 0) ? t[q][c] : y[q] + t[q][c];
+        }
     }
-    __syncthreads();
-    finish_rows(p, q, m0, Ys, Es);
+#pragma unroll
+    for (int q = 0; q < kOutPerLane; ++q)
+        if (16 * q < N2) y[q] = apply_act(y[q] + B2s[li + 16 * q], p.act2);
+    finish_rows(p, m0, wave, lane, y);
 }
 
 }  // namespace
