@@ -24,11 +24,12 @@ struct ChainParams {
     float* out;       // [M][N2]: probabilities (softmax) or y
     int32_t* argmax;  // [M] or null
     float* part;      // mlp2_split: [row_blocks][ks][16][16 tiles_n] partial h; mlp2_tiles: [tiles_n][M][N2] y shares
-    unsigned* counters;  // one arrival counter per row block, zero between launches
+    float* hpart;     // mlp2_tiles with ks > 1: [row_blocks][tiles_n][ks][16 x 16] partial h tiles
+    unsigned* counters;  // one arrival counter per row block (mlp2_tiles with ks > 1: then one per tile), zero between launches
     int M, K1, N1, N2, act1, act2, softmax;
     int tiles_n;  // 16-column tiles of h
-    int ks;       // mlp2_split: K ranges per tile
-    int kchunk;   // mlp2_split: K per range, a multiple of 4
+    int ks;       // K ranges per tile
+    int kchunk;   // K per range, a multiple of 4
 };
 
 // Limits of the chain (the small-batch regime it is for; lancius_hip.h):
@@ -41,12 +42,11 @@ constexpr int kMaxW2 = 8192;
 constexpr size_t kMaxOperand = size_t(1) << 28;
 constexpr int kFR = 16;     // rows of h per workgroup
 constexpr int kFC = 16;     // columns of h per workgroup
-constexpr int kFKC = 1024;  // K staged per chunk
-constexpr int kXP = kFKC + 4;  // x rows in LDS: lanes read rows r at k-steps (r*kXP + k) mod 64 distinct
 constexpr int kSplitMaxN1 = 256;  // mlp2_split: the reducer holds the block's whole h
-constexpr int kMaxSplit = 4;      // mlp2_split: K ranges per tile
+constexpr int kMaxSplit = 4;      // K ranges per tile
 constexpr int kSplitMaxTiles = 16;  // mlp2_split by default: at most 16 * kMaxSplit arrivals per row block
 constexpr int kSplitMinK = 2048;    // and at least 256 KiB per workgroup of mlp2_tiles
+constexpr int kTilesMinK = 128;     // mlp2_tiles: K per range (one MFMA trip of the four waves)
 constexpr int kOut = 0x7ffffff0;  // a byte offset past the end of any operand: the load returns 0
 
 // Every global read is a buffer load whose offset is pushed past the end of
@@ -61,6 +61,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t operand(const float* base, siz
 __device__ __forceinline__ float load1(__amdgpu_buffer_rsrc_t r, unsigned off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
+// A buffer over `count` values at `base` (count <= 0 or a null base: no
+// records).  Built from wave-uniform values it lives in scalar registers,
+// and its range does the bounds checks of every load from it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t range(const float* base, int count) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0,
+                                             base && count > 0 ? count * (int)sizeof(float) : 0, kBufferRsrcWord3);
+}
+__device__ __forceinline__ f32x4 load4(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
 
 struct NoPrefetch {
     __device__ void operator()() const {}
@@ -69,90 +79,92 @@ struct NoPrefetch {
 // The 16 x 16 tile of x . W1 at rows m0.., columns n0.. over k in
 // [kbeg, kend), one f32x4 of partial sums per wave (register r of lane l:
 // row 4(l/16) + r, column l%16; the four waves' sums add up to the tile).
-// x and W1 are staged in LDS a kFKC chunk at a time: x with wave w loading
-// rows 4w .. 4w+3 with its lanes along k; W1 with four threads per k row, a
-// float4 of the 16 columns each.  Every LDS position the MFMA loop reads is
-// written (zeros past kend, M and N1), so the loop has no bounds checks.
-// prefetch() runs once, after the first chunk's loads are issued, so loads
-// of its own share their trip to memory.
+// The range is cut into blocks of 16 k and wave w takes a contiguous quarter
+// of the blocks, so no operand is shared between waves and the loop has no
+// workgroup barrier.  Per block, lane l = 16 q + i loads
+//   x[m0 + i][k + 4q .. k + 4q + 3]        (one float4: the A operand of four
+//                                          MFMAs, MFMA j taking k + 4q + j)
+//   W1[k + l/4][n0 + 4(l%4) .. + 3]        (one float4: the block's 16 rows)
+// and W1 goes through the wave's own 1 KB of LDS, rows permuted so that MFMA
+// j's B operand, W1[k + 4q + j][n0 + i], is the 64 consecutive floats j*64
+// + l: a conflict-free read, ordered after the write by the wave alone.  A
+// group of kGroup blocks is loaded at once (no load is conditional: past
+// the range or the operand they read zeros past the end of their buffer,
+// so the compiler's wait counts stay exact and block 0's MFMAs run while
+// the later blocks arrive).  prefetch() issues right behind the first
+// group's loads, so loads of its own share the trip to memory.
 // VEC: K1 and N1 multiples of 4 (x and W1 rows hold whole float4s).
+constexpr int kKB = 16;     // k per block
+constexpr int kGroup = 16;  // blocks in flight per wave
+constexpr int kSlot = kKB * kFC;  // one W1 block in LDS (floats)
+constexpr int kFKC = 4 * kGroup * kKB;  // K that the four waves load in one group each
+
 template <bool VEC, class Prefetch>
-__device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float (*Xs)[kXP], float (*Wsl)[kFC], int m0,
-                                             int n0, int kbeg, int kend, int wave, int lane, Prefetch prefetch) {
-    const int tid = threadIdx.x, li = lane & 15, lq = lane >> 4;
+__device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float* wl, int m0, int n0, int kbeg, int kend,
+                                             int wave, int lane, Prefetch prefetch) {
+    const int li = lane & 15, lq = lane >> 4;
     const int M = p.M, K1 = p.K1, N1 = p.N1;
-    const __amdgpu_buffer_rsrc_t xb = operand(p.x, (size_t)M * K1), wb = operand(p.w1, (size_t)K1 * N1);
+    const int nb = (kend - kbeg + kKB - 1) / kKB;
+    const int b0 = wave * nb / 4, b1 = (wave + 1) * nb / 4;  // this wave's blocks
+    const int kend_w = min(kend, kbeg + kKB * b1);          // and the end of their k
+    const __amdgpu_buffer_rsrc_t xr = range(p.x, M * K1);
+    const __amdgpu_buffer_rsrc_t wr = range(p.w1, kend_w * N1);  // W1 rows below the wave's end: zeros past it
+    const bool row = m0 + li < M;
+    const int c = n0 + 4 * (lane & 3);
+    unsigned woff[VEC ? 1 : 4];
+#pragma unroll
+    for (int e = 0; e < (VEC ? 1 : 4); ++e)
+        woff[e] = c + e < N1 ? ((unsigned)(lane >> 2) * (unsigned)N1 + (unsigned)(c + e)) * 4u : (unsigned)kOut;
+    const int wpos = ((lane >> 2) & 3) * 64 + (lane >> 4) * 16 + 4 * (lane & 3);  // row l/4 permuted, column 4(l%4)
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kc = kbeg; kc < kend; kc += kFKC) {
-        const int kn = min(kFKC, kend - kc);  // k of this chunk
-        const int trips = (kn + 127) / 128;   // MFMA trips of 128 k
-        const int kpad = 128 * trips;          // LDS k the trips read
-        if (kc > kbeg) __syncthreads();        // the previous chunk's reads are done
-        constexpr int kXT = kFKC / 4 / 64;         // float4 per x row per lane
-        constexpr int kWT = kFKC * kFC / 4 / 256;  // float4 of W1 per thread (64 k rows each)
-        f32x4 xv[4][kXT], wv[kWT];
+    f32x4 xv[kGroup], wv[kGroup];
+    // block j of a group at g0: x at k = kbeg + 16 (g0 + j) + 4q, in range
+    // while 16 j < lim (lim < 0 for rows past M); W1 rows 16 (g0 + j) on
+    auto load_group = [&](int g0) {
+        const int kq = kbeg + kKB * g0 + 4 * lq;
+        const int lim = row ? kend_w - kq : -1;
+        const unsigned xo = ((unsigned)(m0 + li) * (unsigned)K1 + (unsigned)kq) * 4u;
+        const unsigned wstep = (unsigned)kKB * (unsigned)N1 * 4u;
+        const unsigned wbase = (unsigned)(kbeg + kKB * g0) * (unsigned)N1 * 4u;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int r = 4 * wave + rr;
-            const bool row = m0 + r < M;
-            const unsigned base = ((unsigned)(m0 + r) * (unsigned)K1 + (unsigned)kc) * 4u;
-#pragma unroll
-            for (int t = 0; t < kXT; ++t) {
-                if (256 * t >= kpad) continue;
-                const int k = 4 * (lane + 64 * t);
-                if constexpr (VEC) {
-                    const unsigned off = row && k < kn ? base + 4u * k : (unsigned)kOut;
-                    xv[rr][t] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xb, (int)off, 0, 0));
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        xv[rr][t][e] = load1(xb, row && k + e < kn ? base + 4u * (k + e) : (unsigned)kOut);
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kWT; ++u) {
-            if (64 * u >= kpad) continue;
-            const int i = tid + 256 * u, kw = i >> 2, c = n0 + 4 * (i & 3);
-            const unsigned base = ((unsigned)(kc + kw) * (unsigned)N1 + (unsigned)c) * 4u;
+        for (int j = 0; j < kGroup; ++j) {
             if constexpr (VEC) {
-                const unsigned off = kw < kn && c < N1 ? base : (unsigned)kOut;
-                wv[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wb, (int)off, 0, 0));
+                xv[j] = load4(xr, (unsigned)pick(kKB * j < lim, (int)xo, kOut) + 64u * j);
+                wv[j] = load4(wr, woff[0] + wbase + wstep * j);
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    wv[u][e] = load1(wb, kw < kn && c + e < N1 ? base + 4u * e : (unsigned)kOut);
+                for (int e = 0; e < 4; ++e) {
+                    xv[j][e] = load1(xr, (unsigned)pick(kKB * j + e < lim, (int)xo, kOut) + 64u * j + 4u * e);
+                    wv[j][e] = load1(wr, woff[e] + wbase + wstep * j);
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);  // issue in block order (block 0 lands first)
         }
-        if (kc == kbeg) prefetch();
+    };
+    auto run_group = [&](int g0) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
+        for (int j = 0; j < kGroup; ++j) {
+            if (g0 + j >= b1) continue;  // uniform; no loads follow
+            float* slot = wl + (j & 1) * kSlot;
+            *(f32x4*)&slot[wpos] = wv[j];
+            __builtin_amdgcn_wave_barrier();
+            float b[4];
 #pragma unroll
-            for (int t = 0; t < kXT; ++t) {
-                if (256 * t >= kpad) continue;
-                *(f32x4*)&Xs[4 * wave + rr][4 * (lane + 64 * t)] = xv[rr][t];  // kXP * 4 bytes is a multiple of 16
-            }
+            for (int jj = 0; jj < 4; ++jj) b[jj] = slot[jj * 64 + lane];
 #pragma unroll
-        for (int u = 0; u < kWT; ++u) {
-            if (64 * u >= kpad) continue;
-            const int i = tid + 256 * u;
-            *(f32x4*)&Wsl[i >> 2][4 * (i & 3)] = wv[u];
+            for (int jj = 0; jj < 4; ++jj) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[j][jj], b[jj], acc, 0, 0, 0);
         }
-        __syncthreads();
-        // wave w takes k-steps w, w + 4, ...; lane l holds A[row l%16][k +
-        // l/16] and B[k + l/16][column l%16]; a trip's 16 LDS reads are
-        // issued before its 8 MFMAs
-        for (int tr = 0; tr < trips; ++tr) {
-            float a[8], b[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int k = 4 * (wave + 32 * tr + 4 * u) + lq;
-                a[u] = Xs[li][k];
-                b[u] = Wsl[k][li];
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
-        }
+    };
+    // the first group, then prefetch() behind its loads (a K of up to kFKC
+    // is one group per wave), then the rest
+    load_group(b0);
+    prefetch();
+    __builtin_amdgcn_sched_barrier(0);  // the group's loads are all in flight before block 0's LDS write
+    run_group(b0);
+    for (int g0 = b0 + kGroup; g0 < b1; g0 += kGroup) {
+        load_group(g0);
+        __builtin_amdgcn_sched_barrier(0);
+        run_group(g0);
     }
     return acc;
 }
@@ -278,7 +290,9 @@ __device__ __forceinline__ void finish_rows(const ChainParams& p, int m0, int wa
 // calls give identical bits.
 template <bool VEC>
 __global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
-    constexpr int kStage = kFR * kXP + kFKC * kFC;
+    // the waves' W1 slots, then the reducer's h and W2
+    constexpr int kStage = kFR * (kSplitMaxN1 + 4) + kMaxW2;
+    static_assert(kStage >= 4 * 2 * kSlot, "slots fit the staging area");
     __shared__ __attribute__((aligned(16))) float smem[kStage];
     __shared__ float red[4][kFR][kFC + 1];
     __shared__ float B2s[kMaxOut];
@@ -293,9 +307,7 @@ __global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
     const int li = lane & 15, lq = lane >> 4;
     const int kbeg = kq * p.kchunk, kend = min(p.K1, kbeg + p.kchunk);
 
-    const f32x4 acc = hidden_tile<VEC>(p, reinterpret_cast<float(*)[kXP]>(smem),
-                                       reinterpret_cast<float(*)[kFC]>(smem + kFR * kXP), m0, n0, kbeg, kend, wave,
-                                       lane, NoPrefetch{});
+    const f32x4 acc = hidden_tile<VEC>(p, smem + wave * 2 * kSlot, m0, n0, kbeg, kend, wave, lane, NoPrefetch{});
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = acc[r];
     __syncthreads();
@@ -416,50 +428,52 @@ __global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
     finish_rows(p, m0, wave, lane, y);
 }
 
-// mlp2_tiles, for any N1 within the limits.  Workgroup (column tile t of 16
-// columns of h, row block b of 16 rows):
-//  1. h[b, t] = act1(x[b] . W1[:, t] + b1[t]) over the whole K1
-//     (hidden_tile; the four waves' sums added in wave order);
-//  2. y_t = h[b, t] . W2[t rows, :], the tile's share of the second layer,
-//     stored for the row block's reducer;
+// mlp2_tiles, for any N1 within the limits.  Workgroup (K range q of ks,
+// column tile t of 16 columns of h, row block b of 16 rows):
+//  1. the range's part of x[b] . W1[:, t] (hidden_tile; the four waves'
+//     sums added in wave order); with ks > 1, stored, and the workgroup
+//     that arrives last at tile (b, t)'s counter adds the ranges' parts in
+//     range order;
+//  2. h[b, t] = act1(that + b1[t]) and y_t = h[b, t] . W2[t rows, :], the
+//     tile's share of the second layer, stored for the row block's reducer;
 //  3. the workgroup that arrives last at row block b's counter adds the
 //     tiles' shares in tile order, adds b2, applies act2 and finishes the
 //     rows.
-// One hand-off between workgroups; every sum runs in a fixed order, so
-// repeated calls give identical bits.
+// The K ranges put ks workgroups on each tile, for a long K: a workgroup's
+// loads arrive at about 80 GB/s after a first trip of over a microsecond,
+// so a long K is faster spread over more CUs, at the price of one more
+// hand-off (three more trips to memory).  Every sum runs in a fixed order,
+// so repeated calls give identical bits.
 template <bool VEC>
 __global__ void __launch_bounds__(256) mlp2_tiles(const ChainParams p) {
-    __shared__ __attribute__((aligned(16))) float Xs[kFR][kXP];    // x rows of the block, current K chunk
-    __shared__ __attribute__((aligned(16))) float Wsl[kFKC][kFC];  // W1 columns of the tile, current K chunk
+    __shared__ __attribute__((aligned(16))) float Wl[4][2 * kSlot];  // each wave's W1 slots
     __shared__ float red[4][kFR][kFC + 1];
     __shared__ float Hs[kFR][kFC + 1];
     __shared__ float W2s[kFC * kMaxOut];  // W2 rows of the tile, row pitch N2
     __shared__ float B2s[kMaxOut];
     __shared__ int s_flag;
 
-    const int tn = (int)blockIdx.x % p.tiles_n, rb = (int)blockIdx.x / p.tiles_n;
+    const int ks = p.ks, kq = (int)blockIdx.x % ks, tile = (int)blockIdx.x / ks;
+    const int tn = tile % p.tiles_n, rb = tile / p.tiles_n;
     const int n0 = tn * kFC, m0 = rb * kFR;
     const int M = p.M, N1 = p.N1, N2 = p.N2;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lq = lane >> 4;
+    const int kbeg = kq * p.kchunk, kend = min(p.K1, kbeg + p.kchunk);
 
     // W2 rows n0.. (one contiguous run of kFC * N2 values), this thread's
     // b1 column and b2 output: loaded with the first K chunk, so the launch
     // makes one trip to memory for its inputs
     constexpr int kW2Per = kFC * kMaxOut / 256;
     float w2r[kW2Per], b1r = 0.0f, b2r = 0.0f;
-    const f32x4 acc = hidden_tile<VEC>(p, Xs, Wsl, m0, n0, 0, p.K1, wave, lane, [&] {
-        const __amdgpu_buffer_rsrc_t w2b = operand(p.w2, (size_t)N1 * N2);
-        const int run = min(kFC, N1 - n0) * N2;  // W2 values of the tile
+    const f32x4 acc = hidden_tile<VEC>(p, Wl[wave], m0, n0, kbeg, kend, wave, lane, [&] {
+        const int cols = min(kFC, N1 - n0);  // h columns of the tile
+        const __amdgpu_buffer_rsrc_t w2b = range(p.w2 + (size_t)n0 * N2, cols * N2);  // its W2 rows
 #pragma unroll
-        for (int u = 0; u < kW2Per; ++u) {
-            const int i = tid + 256 * u;
-            w2r[u] = load1(w2b, i < run ? (unsigned)(n0 * N2 + i) * 4u : (unsigned)kOut);
-        }
-        const int c = n0 + (tid & 15);
-        b1r = load1(operand(p.b1, (size_t)N1), c < N1 ? 4u * c : (unsigned)kOut);
-        b2r = load1(operand(p.b2, (size_t)N2), tid < N2 ? 4u * tid : (unsigned)kOut);
+        for (int u = 0; u < kW2Per; ++u) w2r[u] = load1(w2b, 4u * tid + 1024u * u);
+        b1r = load1(range(p.b1 + n0, cols), 4u * (tid & 15));
+        b2r = load1(range(p.b2, N2), 4u * tid);
     });
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = acc[r];
@@ -469,7 +483,23 @@ __global__ void __launch_bounds__(256) mlp2_tiles(const ChainParams p) {
     __syncthreads();
     {
         const int r = tid >> 4, c = tid & 15;  // 256 threads = 16 x 16
-        const float v = ((red[0][r][c] + red[1][r][c]) + red[2][r][c]) + red[3][r][c];
+        float v = ((red[0][r][c] + red[1][r][c]) + red[2][r][c]) + red[3][r][c];
+        if (ks > 1) {
+            const int row_blocks = (M + kFR - 1) / kFR;
+            const __amdgpu_buffer_rsrc_t hp =
+                coherent_buffer(p.hpart, (size_t)row_blocks * p.tiles_n * ks * kFR * kFC * sizeof(float));
+            store_coherent(hp, ((tile * ks + kq) * (kFR * kFC) + tid) * (int)sizeof(float), v);
+            if (!arrive_last(p.counters + row_blocks + tile, (unsigned)ks, &s_flag)) return;
+            reset_arrival(p.counters + row_blocks + tile);
+            float t[kMaxSplit];
+#pragma unroll
+            for (int q = 0; q < kMaxSplit; ++q)
+                t[q] = load_coherent(hp, q < ks ? ((tile * ks + q) * (kFR * kFC) + tid) * (int)sizeof(float) : kOut);
+            v = t[0];
+#pragma unroll
+            for (int q = 1; q < kMaxSplit; ++q)
+                if (q < ks) v += t[q];
+        }
         float h = 0.0f;
         if (m0 + r < M && n0 + c < N1) h = apply_act(v + b1r, p.act1);
         Hs[r][c] = h;  // rows past M and columns past N1 hold 0
@@ -590,10 +620,25 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
         if (int rc = check_launch("mlp2_split")) return rc;
         return ok();
     }
-    if (int rc = workspace(ctx, (size_t)p.tiles_n * M * N2 * sizeof(float), &ws)) return rc;
+    // For K beyond one staged chunk, K ranges of at least kTilesMinK that
+    // bring the grid to about one workgroup per CU (measured, 64 rows, 256
+    // hidden: K 784 is fastest whole, 8.2 against 8.5 us with four ranges;
+    // K 1500 and 4096 split four ways, 10.9 -> 9.1 and 17.9 -> 10.6 us)
+    int ks = tune("mlp2_tiles_ks", -1);
+    if (ks < 0) ks = K1 <= (size_t)kFKC ? 1 : (int)std::max<size_t>(1, std::min<size_t>(kMaxSplit, 256 / tiles));
+    ks = std::max(1, std::min(ks, kMaxSplit));
+    while (ks > 1 && K1 < (size_t)ks * kTilesMinK) --ks;
+    p.kchunk = (int)((K1 + ks - 1) / ks + 3) / 4 * 4;
+    p.ks = (int)((K1 + p.kchunk - 1) / p.kchunk);
+    const size_t ybytes = ((size_t)p.tiles_n * M * N2 * sizeof(float) + 255) & ~(size_t)255;
+    const size_t hbytes = p.ks > 1 ? tiles * p.ks * kFR * kFC * sizeof(float) : 0;
+    if (p.ks > 1)
+        if (int rc = counters(ctx, row_blocks + tiles, &p.counters)) return rc;
+    if (int rc = workspace(ctx, ybytes + hbytes, &ws)) return rc;
     p.part = (float*)ws;
-    hipLaunchKernelGGL(vec ? mlp2_tiles<true> : mlp2_tiles<false>, dim3((unsigned)tiles), dim3(256), 0, ctx->stream,
-                       p);
+    p.hpart = p.ks > 1 ? (float*)((char*)ws + ybytes) : nullptr;
+    hipLaunchKernelGGL(vec ? mlp2_tiles<true> : mlp2_tiles<false>, dim3((unsigned)(tiles * p.ks)), dim3(256), 0,
+                       ctx->stream, p);
     if (int rc = check_launch("mlp2_tiles")) return rc;
     return ok();
 }

@@ -65,11 +65,13 @@ def run(dev, M, K1, N1, N2, act, bias, softmax, seed, act2=None):
     (64, 4096, 64, 64, ACT_RELU, True, True),
     (16, 9000, 64, 10, ACT_RELU, True, True),    # K ranges of several staged chunks
     (13, 301, 250, 9, ACT_TANH, True, True),     # K ranges and N1 not multiples of 4
-    # hidden layers wider than 256: one workgroup per 16-column tile, no K split
+    (64, 400, 256, 10, ACT_RELU, True, True),    # three K ranges per tile
+    # hidden layers wider than 256: 16-column tiles, K split while the grid
+    # is under 256 workgroups and K allows
     (16, 300, 512, 16, ACT_RELU, True, True),
     (4, 2000, 2048, 4, ACT_GELU, True, True),
-    (3, 77, 1000, 8, ACT_RELU, False, False),
-    (1, 100, 8192, 1, ACT_RELU, True, False),
+    (3, 77, 1000, 8, ACT_RELU, False, False),   # K too short to split
+    (1, 100, 8192, 1, ACT_RELU, True, False),   # 512 tiles: no split
 ])
 def test_mlp2_matches_unfused_chain(dev, M, K1, N1, N2, act, bias, softmax):
     got, idx, ref = run(dev, M, K1, N1, N2, act, bias, softmax, 40 + M + K1)
