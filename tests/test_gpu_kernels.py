@@ -153,6 +153,44 @@ def test_gemm_skinny_fused_split_repeatable(dev, M, K, N):
         b.free()
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (16, 4096, 4096),   # the skinny config: 64 column blocks x 8 K slices
+    (1, 100, 4096),     # one row; one K slice of 100 rows (two waves)
+    (17, 1000, 4100),   # two row tiles (rows 17..31 absent); N % 64 = 4: a partial last column block
+    (32, 16, 8192),     # K = 16: seven of the eight waves hold no rows
+    (24, 8200, 4096),   # 17 K slices: the reducer adds them in two batches of loads
+])
+def test_gemm_skinny_wide(dev, M, K, N):
+    """M <= 32 and N >= 4096 through the B-streaming skinny kernel.  C is
+    NaN-filled, so every element must be written; bias, GELU and a
+    residual; every row is checked against the fp64 oracle, and two calls
+    give the same bits."""
+    got, ref = _gemm_case(dev, M, K, N, seed=150 + M + K, bias=True, act=ACT_GELU, residual=True)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+    again, _ = _gemm_case(dev, M, K, N, seed=150 + M + K, bias=True, act=ACT_GELU, residual=True)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_gemm_skinny_grouped(dev):
+    """A grouped call (blockIdx.z = member) through the skinny kernel: each
+    member against its own oracle product."""
+    M, K, N, n = 8, 512, 4096, 3
+    As = [prng.normal(170 + i, (M, K)) for i in range(n)]
+    Bs = [prng.normal(180 + i, (K, N)) for i in range(n)]
+    dAs, dBs = [dev.upload(a) for a in As], [dev.upload(b) for b in Bs]
+    dCs = [dev.alloc(M * N * 4) for _ in range(n)]
+    for c in dCs:
+        dev.fill(c, float("nan"), M * N)
+    case(f"skinny grouped x{n} M={M} K={K} N={N}")
+    dev.gemm_grouped(dCs, dAs, dBs, M, K, N)
+    for i in range(n):
+        got = dev.download(dCs[i], (M, N))
+        assert np.isfinite(got).all()
+        assert oracle.normwise_error(got, oracle.matmul(As[i], Bs[i])) <= oracle.tolerance(K)
+    for b in dAs + dBs + dCs:
+        b.free()
+
+
 @pytest.mark.parametrize("M,K,N", [(32, 784, 128), (32, 128, 10), (17, 300, 77), (3, 1000, 1), (64, 784, 128),
                                    (64, 128, 10), (48, 300, 77), (40, 4096, 4096)])
 def test_gemm_small_m_and_ragged_n(dev, M, K, N):
