@@ -859,17 +859,22 @@ def main() -> int:
         feeds = {"x": prng.uniform(42, (64, 784), -1.0, 1.0), "W1": prng.normal(142, (784, 256), 0, 0.02),
                  "b1": np.zeros((1, 256), np.float32), "W2": prng.normal(342, (256, 10), 0, 0.02),
                  "b2": np.zeros((1, 10), np.float32)}
-        t, info = graph_case(dev, bg, feeds, max(20, steps), 5)
-        tg, _ = graph_case(sdev, bg, feeds, max(20, steps), 5, DEVICE_GRAPH)
-        tu, info_u = graph_case(dev, bg, feeds, max(20, steps), 5, DEVICE_NO_CHAIN)
+        # a forward is a few microseconds: 200 timed forwards (each a whole
+        # run of the program) keep the stream's start-up latency out of the
+        # per-forward figure (at 20 it adds about 0.4 us)
+        small = max(200, steps)
+        t, info = graph_case(dev, bg, feeds, small, 5)
+        tg, _ = graph_case(sdev, bg, feeds, small, 5, DEVICE_GRAPH)
+        tu, info_u = graph_case(dev, bg, feeds, small, 5, DEVICE_NO_CHAIN)
         bg.destroy()
         extra["mlp_graph_64x784x256x10"] = {"fwd_latency_ms": round(t, 4), "launches": info["launches"],
+                                            "timed_forwards": small,
                                             "GFLOP/s": round(26.02e6 / t / 1e6, 1),
                                             "fwd_latency_ms_hipgraph": round(tg, 4),
                                             "fwd_latency_ms_unchained": round(tu, 4),
                                             "launches_unchained": info_u["launches"]}
         log("basis graph")
-        extra["basis_mlp_graph_64x784x256x10_tanh"] = basis_case(dev, max(20, steps), 5)
+        extra["basis_mlp_graph_64x784x256x10_tanh"] = basis_case(dev, small, 5)
         log("transformer block graph")
         bg = graphs.build_block(lib)
         feeds = {}
