@@ -88,18 +88,18 @@ struct NoPrefetch {
 // and W1 goes through the wave's own 1 KB of LDS, rows permuted so that MFMA
 // j's B operand, W1[k + 4q + j][n0 + i], is the 64 consecutive floats j*64
 // + l: a conflict-free read, ordered after the write by the wave alone.  A
-// group of kGroup blocks is loaded at once (no load is conditional: past
+// group of G blocks is loaded at once (no load is conditional: past
 // the range or the operand they read zeros past the end of their buffer,
 // so the compiler's wait counts stay exact and block 0's MFMAs run while
 // the later blocks arrive).  prefetch() issues right behind the first
 // group's loads, so loads of its own share the trip to memory.
 // VEC: K1 and N1 multiples of 4 (x and W1 rows hold whole float4s).
 constexpr int kKB = 16;     // k per block
-constexpr int kGroup = 16;  // blocks in flight per wave
+constexpr int kGroup = 16;  // blocks in flight per wave (the largest group)
 constexpr int kSlot = kKB * kFC;  // one W1 block in LDS (floats)
 constexpr int kFKC = 4 * kGroup * kKB;  // K that the four waves load in one group each
 
-template <bool VEC, class Prefetch>
+template <bool VEC, int G, class Prefetch>
 __device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float* wl, int m0, int n0, int kbeg, int kend,
                                              int wave, int lane, Prefetch prefetch) {
     const int li = lane & 15, lq = lane >> 4;
@@ -117,7 +117,7 @@ __device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float* wl, in
         woff[e] = c + e < N1 ? ((unsigned)(lane >> 2) * (unsigned)N1 + (unsigned)(c + e)) * 4u : (unsigned)kOut;
     const int wpos = ((lane >> 2) & 3) * 64 + (lane >> 4) * 16 + 4 * (lane & 3);  // row l/4 permuted, column 4(l%4)
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4 xv[kGroup], wv[kGroup];
+    f32x4 xv[G], wv[G];
     // block j of a group at g0: x at k = kbeg + 16 (g0 + j) + 4q, in range
     // while 16 j < lim (lim < 0 for rows past M); W1 rows 16 (g0 + j) on
     auto load_group = [&](int g0) {
@@ -127,7 +127,7 @@ __device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float* wl, in
         const unsigned wstep = (unsigned)kKB * (unsigned)N1 * 4u;
         const unsigned wbase = (unsigned)(kbeg + kKB * g0) * (unsigned)N1 * 4u;
 #pragma unroll
-        for (int j = 0; j < kGroup; ++j) {
+        for (int j = 0; j < G; ++j) {
             if constexpr (VEC) {
                 xv[j] = load4(xr, (unsigned)pick(kKB * j < lim, (int)xo, kOut) + 64u * j);
                 wv[j] = load4(wr, woff[0] + wbase + wstep * j);
@@ -143,7 +143,7 @@ __device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float* wl, in
     };
     auto run_group = [&](int g0) {
 #pragma unroll
-        for (int j = 0; j < kGroup; ++j) {
+        for (int j = 0; j < G; ++j) {
             if (g0 + j >= b1) continue;  // uniform; no loads follow
             float* slot = wl + (j & 1) * kSlot;
             *(f32x4*)&slot[wpos] = wv[j];
@@ -161,7 +161,7 @@ __device__ __forceinline__ f32x4 hidden_tile(const ChainParams& p, float* wl, in
     prefetch();
     __builtin_amdgcn_sched_barrier(0);  // the group's loads are all in flight before block 0's LDS write
     run_group(b0);
-    for (int g0 = b0 + kGroup; g0 < b1; g0 += kGroup) {
+    for (int g0 = b0 + G; g0 < b1; g0 += G) {
         load_group(g0);
         __builtin_amdgcn_sched_barrier(0);
         run_group(g0);
@@ -307,7 +307,7 @@ __global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
     const int li = lane & 15, lq = lane >> 4;
     const int kbeg = kq * p.kchunk, kend = min(p.K1, kbeg + p.kchunk);
 
-    const f32x4 acc = hidden_tile<VEC>(p, smem + wave * 2 * kSlot, m0, n0, kbeg, kend, wave, lane, NoPrefetch{});
+    const f32x4 acc = hidden_tile<VEC, kGroup>(p, smem + wave * 2 * kSlot, m0, n0, kbeg, kend, wave, lane, NoPrefetch{});
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][4 * lq + r][li] = acc[r];
     __syncthreads();
@@ -444,7 +444,7 @@ __global__ void __launch_bounds__(256) mlp2_split(const ChainParams p) {
 // so a long K is faster spread over more CUs, at the price of one more
 // hand-off (three more trips to memory).  Every sum runs in a fixed order,
 // so repeated calls give identical bits.
-template <bool VEC>
+template <bool VEC, int G>
 __global__ void __launch_bounds__(256) mlp2_tiles(const ChainParams p) {
     __shared__ __attribute__((aligned(16))) float Wl[4][2 * kSlot];  // each wave's W1 slots
     __shared__ float red[4][kFR][kFC + 1];
@@ -467,7 +467,7 @@ __global__ void __launch_bounds__(256) mlp2_tiles(const ChainParams p) {
     // makes one trip to memory for its inputs
     constexpr int kW2Per = kFC * kMaxOut / 256;
     float w2r[kW2Per], b1r = 0.0f, b2r = 0.0f;
-    const f32x4 acc = hidden_tile<VEC>(p, Wl[wave], m0, n0, kbeg, kend, wave, lane, [&] {
+    const f32x4 acc = hidden_tile<VEC, G>(p, Wl[wave], m0, n0, kbeg, kend, wave, lane, [&] {
         const int cols = min(kFC, N1 - n0);  // h columns of the tile
         const __amdgpu_buffer_rsrc_t w2b = range(p.w2 + (size_t)n0 * N2, cols * N2);  // its W2 rows
 #pragma unroll
@@ -637,8 +637,19 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
     if (int rc = workspace(ctx, ybytes + hbytes, &ws)) return rc;
     p.part = (float*)ws;
     p.hpart = p.ks > 1 ? (float*)((char*)ws + ybytes) : nullptr;
-    hipLaunchKernelGGL(vec ? mlp2_tiles<true> : mlp2_tiles<false>, dim3((unsigned)(tiles * p.ks)), dim3(256), 0,
-                       ctx->stream, p);
+    // the group size that leaves the fewest empty blocks in a wave's last
+    // group (empty blocks still cost their loads: at K 784, 13 blocks per
+    // wave, groups of 13 measured 7.63 against 7.84 us with groups of 16)
+    const int per_wave = ((p.kchunk + kKB - 1) / kKB + 3) / 4;  // most blocks of a wave
+    int group = kGroup;
+    for (int cand : {kGroup, 13, 8}) {
+        auto waste = [&](int g) { return (per_wave + g - 1) / g * g - per_wave; };
+        if (waste(cand) < waste(group)) group = cand;
+    }
+    auto kernel = group == 13 ? (vec ? mlp2_tiles<true, 13> : mlp2_tiles<false, 13>)
+                  : group == 8 ? (vec ? mlp2_tiles<true, 8> : mlp2_tiles<false, 8>)
+                               : (vec ? mlp2_tiles<true, kGroup> : mlp2_tiles<false, kGroup>);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)(tiles * p.ks)), dim3(256), 0, ctx->stream, p);
     if (int rc = check_launch("mlp2_tiles")) return rc;
     return ok();
 }
