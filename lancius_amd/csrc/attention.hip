@@ -356,8 +356,12 @@ __global__ void __launch_bounds__(256) attention_rowwise(const AttnParams p) {
 //    softmax (m, l, o) per head in the log2 domain;
 //  * the 16 streams merge in a fixed order (xor butterfly over the 4 streams
 //    of a wave, then the 4 waves in order through LDS), so results do not
-//    depend on timing; one split writes the normalised output directly, more
-//    splits write (o, m, l) partials that decode_combine merges in split order.
+//    depend on timing; one split writes the normalised output directly; with
+//    more, each split writes its (o, m, l) partial through the point of
+//    coherence and the workgroup that arrives last at its (sequence, K/V
+//    head, head chunk) counter merges the splits in split order (one launch:
+//    a separate merge kernel cost 8.6 us of launch and latency, the hand-off
+//    about 2 us at the end of the last ranges).
 // kernel_attention_kv_cache (lancius_kernels.c:338-379) is batch = 1,
 // Hq = Hkv, no mask, scale 1/sqrt(D).
 struct DecodeParams {
@@ -367,6 +371,7 @@ struct DecodeParams {
     const float* v;
     const int32_t* lens;    // per-sequence cache length (<= Skv) or null
     float* part;            // [B*Hkv][splits][G][D + 2]
+    unsigned* counters;     // one arrival counter per (sequence, K/V head, head chunk), zero between launches
     int B, Skv, Hq, Hkv, D, G;
     int splits, chunk, hchunks;
     float qscale;           // softmax scale * log2(e)
@@ -440,6 +445,7 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float (&o)[NV], 
 template <int NV, bool VEC, int GT, int UNR>
 __global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
     __shared__ float red[4][GT][kDecMaxD + 2];
+    __shared__ int s_flag;
     // XCD-aware order: consecutive workgroups go to different XCDs, so logical
     // ids are dealt out in contiguous runs per XCD (the head chunks of one
     // key range then share that XCD's L2).
@@ -574,6 +580,8 @@ __global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
     }
     __syncthreads();
     const int nh = min(GT, G - h0);
+    const size_t part_floats = (size_t)p.B * p.Hkv * p.splits * G * (D + 2);
+    const __amdgpu_buffer_rsrc_t part = coherent_buffer(p.part, p.splits > 1 ? part_floats * sizeof(float) : 0);
     for (int idx = tid; idx < nh * D; idx += 256) {
         const int h = idx / D, d = idx - (idx / D) * D;
         float mm = -INFINITY;
@@ -593,44 +601,38 @@ __global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
         if (p.splits == 1) {
             p.out[((size_t)b * p.Hq + hq) * D + d] = ll > 0.0f ? oo / ll : 0.0f;
         } else {
-            float* pr = p.part + (((size_t)bh * p.splits + split) * G + h0 + h) * (D + 2);
-            pr[d] = oo;
+            const int pr = (int)((((size_t)bh * p.splits + split) * G + h0 + h) * (D + 2));
+            store_coherent(part, (pr + d) * (int)sizeof(float), oo);
             if (d == 0) {
-                pr[D] = mm;
-                pr[D + 1] = ll;
+                store_coherent(part, (pr + D) * (int)sizeof(float), mm);
+                store_coherent(part, (pr + D + 1) * (int)sizeof(float), ll);
             }
         }
     }
-}
-
-// out = sum_s o_s 2^(m_s - m) / sum_s l_s 2^(m_s - m), m = max_s m_s; one
-// wave per (sequence, query head), splits in order.  A sequence with no keys
-// gets zeros.
-__global__ void __launch_bounds__(256) decode_combine(const DecodeParams p) {
-    const int row_id = blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, hq)
-    const int lane = threadIdx.x & 63;
-    if (row_id >= p.B * p.Hq) return;
-    const int b = row_id / p.Hq, hq = row_id - (row_id / p.Hq) * p.Hq;
-    const int hk = hq / p.G, row = hq - (hq / p.G) * p.G;
-    const int D = p.D;
-    const float* base = p.part + (((size_t)(b * p.Hkv + hk) * p.splits) * p.G + row) * (D + 2);
-    const size_t sstride = (size_t)p.G * (D + 2);
-    float m = -INFINITY;
-    for (int s = 0; s < p.splits; ++s) m = fmaxf(m, base[s * sstride + D]);
-    float l = 0.0f;
-    for (int s = 0; s < p.splits; ++s) {
-        const float ms = base[s * sstride + D];
-        if (ms > -INFINITY) l += base[s * sstride + D + 1] * exp2f(ms - m);
-    }
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    float* o = p.out + ((size_t)b * p.Hq + hq) * D;
-    for (int d = lane; d < D; d += 64) {
-        float acc = 0.0f;
-        for (int s = 0; s < p.splits; ++s) {
-            const float ms = base[s * sstride + D];
-            if (ms > -INFINITY) acc += base[s * sstride + d] * exp2f(ms - m);
+    if (p.splits == 1) return;
+    unsigned* ctr = p.counters + (size_t)bh * p.hchunks + hc;
+    if (!arrive_last(ctr, (unsigned)p.splits, &s_flag)) return;
+    reset_arrival(ctr);
+    // out = sum_s o_s 2^(m_s - m) / sum_s l_s 2^(m_s - m), m = max_s m_s, the
+    // splits in order; a sequence with no keys gets zeros
+    const int sstride = G * (D + 2);
+    for (int idx = tid; idx < nh * D; idx += 256) {
+        const int h = idx / D, d = idx - (idx / D) * D;
+        const int base = (int)((((size_t)bh * p.splits) * G + h0 + h) * (D + 2));
+        float m = -INFINITY;
+        for (int sp = 0; sp < p.splits; ++sp)
+            m = fmaxf(m, load_coherent(part, (base + sp * sstride + D) * (int)sizeof(float)));
+        float l = 0.0f, acc = 0.0f;
+        for (int sp = 0; sp < p.splits; ++sp) {
+            const float ms = load_coherent(part, (base + sp * sstride + D) * (int)sizeof(float));
+            if (ms > -INFINITY) {
+                const float w = exp2f(ms - m);
+                l += load_coherent(part, (base + sp * sstride + D + 1) * (int)sizeof(float)) * w;
+                acc += load_coherent(part, (base + sp * sstride + d) * (int)sizeof(float)) * w;
+            }
         }
-        o[d] = acc * inv;
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+        p.out[((size_t)b * p.Hq + hk * G + h0 + h) * D + d] = acc * inv;
     }
 }
 
@@ -783,9 +785,13 @@ int lancius_hip_attention_decode_f32(lancius_hip_ctx* ctx, float* out, const flo
     p.chunk = (int)chunk;
     p.hchunks = (int)hchunks;
     if (splits > 1) {
+        const size_t part_bytes = seqs * splits * p.G * (D + 2) * sizeof(float);
+        LANCIUS_REQUIRE(part_bytes < ((size_t)1 << 31), LANCIUS_HIP_ERR_SHAPE,
+                        "attention_decode: %zu bytes of split partials (32-bit offsets)", part_bytes);
         void* ws = nullptr;
-        if (int rc = workspace(ctx, seqs * splits * p.G * (D + 2) * sizeof(float), &ws)) return rc;
+        if (int rc = workspace(ctx, part_bytes, &ws)) return rc;
         p.part = (float*)ws;
+        if (int rc = counters(ctx, tasks, &p.counters)) return rc;
     }
     const bool vec = D % 4 == 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache);
     const unsigned grid = (unsigned)(tasks * splits);
@@ -794,12 +800,6 @@ int lancius_hip_attention_decode_f32(lancius_hip_ctx* ctx, float* out, const flo
     else if (D > 64) launch_decode<8, false>(p, grid, ctx->stream, gt);
     else launch_decode<4, false>(p, grid, ctx->stream, gt);
     if (int rc = check_launch("attention_decode")) return rc;
-    if (splits > 1) {
-        const size_t rows = batch * H_q;
-        LANCIUS_REQUIRE((rows + 3) / 4 < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention_decode: too many heads");
-        hipLaunchKernelGGL(decode_combine, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, ctx->stream, p);
-        if (int rc = check_launch("decode_combine")) return rc;
-    }
     return ok();
 }
 

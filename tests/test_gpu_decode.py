@@ -115,9 +115,11 @@ def _decode(dev, B, Skv, Hq, Hkv, D, lens, seed, q=None, k=None, v=None):
     v = prng.uniform(seed + 2, (B, Skv, Hkv, D), -1.0, 1.0) if v is None else v
     dq, dk, dv, do = up(dev, q), up(dev, k), up(dev, v), dev.alloc(4 * q.size)
     dl = dev.upload(np.asarray(lens, np.int32)) if lens is not None else None
+    dev.fill(do, float("nan"), q.size)  # every output element must be written
     case(f"attention_decode B={B} Skv={Skv} Hq={Hq} Hkv={Hkv} D={D} lens={lens is not None}")
     dev.attention_decode(do, dq, dk, dv, dl, B, Skv, Hq, Hkv, D)
     got = dev.download(do, q.shape)
+    assert np.isfinite(got).all(), f"{np.count_nonzero(~np.isfinite(got))} outputs not written"
     for b in (dq, dk, dv, do, dl):
         if b is not None:
             b.free()
