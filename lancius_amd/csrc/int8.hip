@@ -129,26 +129,77 @@ __global__ void __launch_bounds__(kThreads) quantize_flat(int8_t* __restrict__ q
     for (size_t i = (size_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += step) q[i] = quant(x[i]);
 }
 
+// Conv weights for the implicit GEMM: OIHW int8 -> [C_out][Kp] with
+// k = (kh, kw, ci), Cp channels per tap; zero for ci >= C_in and for
+// k >= KHW * Cp.  Element d of wblocks * kThreads per step.
+struct ConvWeightsI8 {
+    int8_t* wt;
+    const int8_t* w;
+    int C_out, C_in, KHW, Cp, Kp, blocks;
+};
+__device__ __forceinline__ void conv_weights_i8_part(const ConvWeightsI8& cw, int block) {
+    const size_t total = (size_t)cw.C_out * cw.Kp;
+    const size_t step = (size_t)cw.blocks * kThreads;
+    for (size_t d = (size_t)block * kThreads + threadIdx.x; d < total; d += step) {
+        const int k = (int)(d % cw.Kp), co = (int)(d / cw.Kp);
+        const int tap = k / cw.Cp, ci = k - (k / cw.Cp) * cw.Cp;
+        cw.wt[d] = (tap < cw.KHW && ci < cw.C_in) ? cw.w[((size_t)co * cw.C_in + ci) * cw.KHW + tap] : (int8_t)0;
+    }
+}
+
 // NCHW fp32 -> NHWC int8 with Cp >= C channels per pixel (padding bytes 0),
 // through a 64 (channels) x 64 (pixels) LDS tile: reads coalesce along the
-// pixels of a channel plane; each write is 4 channels of one pixel packed
-// into 32 bits, 16 lanes covering 64 channels of a pixel.
+// pixels of a channel plane (VEC, H*W % 4 == 0 and x 16-byte aligned: one
+// float4 of 4 pixels per load, through a buffer whose past-the-end offset
+// stands for channels and pixels that do not exist, so no load sits behind
+// a branch); each write is 4 channels of one pixel packed into 32 bits, 16
+// lanes covering 64 channels of a pixel.  Workgroups past the activation's
+// tiles re-lay the conv weights (the two are independent: one launch).
+template <bool VEC>
 __global__ void __launch_bounds__(kThreads) quantize_nchw_to_nhwc(int8_t* __restrict__ q, const float* __restrict__ x,
                                                                   const float* __restrict__ part, int parts,
                                                                   double* __restrict__ scale_out, double other, int N,
-                                                                  int C, int HW, int Cp, int tiles_p, int tiles_c) {
+                                                                  int C, int HW, int Cp, int tiles_p, int tiles_c,
+                                                                  const ConvWeightsI8 cw) {
+    const int qblocks = N * tiles_p * tiles_c;
+    if ((int)blockIdx.x >= qblocks) {
+        conv_weights_i8_part(cw, (int)blockIdx.x - qblocks);
+        return;
+    }
     __shared__ int8_t t[64][65];
     const Quantizer quant(scale_from_partials(part, parts, scale_out, other));
     const int tile = blockIdx.x;
     const int n = tile / (tiles_p * tiles_c);
     const int rem = tile - n * tiles_p * tiles_c;
     const int c0 = (rem / tiles_p) * 64, p0 = (rem % tiles_p) * 64;
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
     const float* xn = x + (size_t)n * C * HW;
+    if constexpr (VEC) {
+        constexpr int kOut = 0x7ffffff0;
+        const __amdgpu_buffer_rsrc_t xb = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(xn), 0, C * HW * (int)sizeof(float), kBufferRsrcWord3);
+        f32x4 v[4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int c = c0 + ty + 4 * i, p = p0 + tx;
-        t[ty + 4 * i][tx] = (c < C && p < HW) ? quant(xn[(size_t)c * HW + p]) : (int8_t)0;
+        for (int i = 0; i < 4; ++i) {
+            const int idx = threadIdx.x + kThreads * i;
+            const int cl = idx >> 4, p = p0 + 4 * (idx & 15), c = c0 + cl;
+            v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 xb, pick((c < C) & (p < HW), (c * HW + p) * (int)sizeof(float), kOut),
+                                                 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int idx = threadIdx.x + kThreads * i;
+            const int cl = idx >> 4, pl = 4 * (idx & 15);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[cl][pl + e] = quant(v[i][e]);  // zeros past C and HW quantize to 0
+        }
+    } else {
+        const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int c = c0 + ty + 4 * i, p = p0 + tx;
+            t[ty + 4 * i][tx] = (c < C && p < HW) ? quant(xn[(size_t)c * HW + p]) : (int8_t)0;
+        }
     }
     __syncthreads();
     int8_t* qn = q + (size_t)n * HW * Cp;
@@ -256,20 +307,6 @@ __global__ void __launch_bounds__(kThreads) quantize_rows_padded(int8_t* __restr
                 }
             }
         }
-    }
-}
-
-// OIHW int8 weights -> [C_out][Kp] with k = (kh, kw, ci), Cp channels per
-// tap; zero for ci >= C_in and for k >= KHW * Cp.
-__global__ void __launch_bounds__(kThreads) conv_weights_i8_padded(int8_t* __restrict__ wt,
-                                                                   const int8_t* __restrict__ w, int C_out, int C_in,
-                                                                   int KHW, int Cp, int Kp) {
-    const size_t total = (size_t)C_out * Kp;
-    const size_t step = (size_t)gridDim.x * kThreads;
-    for (size_t d = (size_t)blockIdx.x * kThreads + threadIdx.x; d < total; d += step) {
-        const int k = (int)(d % Kp), co = (int)(d / Kp);
-        const int tap = k / Cp, ci = k - (k / Cp) * Cp;
-        wt[d] = (tap < KHW && ci < C_in) ? w[((size_t)co * C_in + ci) * KHW + tap] : (int8_t)0;
     }
 }
 
@@ -910,14 +947,18 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     const int HW = (int)(H * W);
     const int tiles_p = (HW + 63) / 64, tiles_c = (int)((Cp + 63) / 64);
     LANCIUS_REQUIRE((size_t)N * tiles_p * tiles_c < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: input too large");
-    hipLaunchKernelGGL(quantize_nchw_to_nhwc, dim3((unsigned)(N * tiles_p * tiles_c)), dim3(kThreads), 0, ctx->stream,
-                       xq, in, (const float*)part, parts, scales, scale_w, (int)N, (int)C_in, HW, (int)Cp, tiles_p,
-                       tiles_c);
+    // the activation quantized to NHWC and, in the same launch, the weights
+    // re-laid k = (kh, kw, ci) and zero-padded to Kp
+    ConvWeightsI8 cw{wq, w, (int)C_out, (int)C_in, (int)KHW, (int)Cp, (int)Kp, 0};
+    cw.blocks = (int)std::min<size_t>(grid_for(C_out * Kp), 1024);
+    const size_t qblocks = (size_t)N * tiles_p * tiles_c;
+    LANCIUS_REQUIRE(qblocks + cw.blocks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: input too large");
+    const bool xvec = HW % 4 == 0 && ((uintptr_t)in & 15u) == 0 && C_in * (size_t)HW * sizeof(float) < ((size_t)1 << 31);
+    hipLaunchKernelGGL(xvec ? quantize_nchw_to_nhwc<true> : quantize_nchw_to_nhwc<false>,
+                       dim3((unsigned)(qblocks + cw.blocks)), dim3(kThreads), 0, ctx->stream, xq, in,
+                       (const float*)part, parts, scales, scale_w, (int)N, (int)C_in, HW, (int)Cp, tiles_p, tiles_c,
+                       cw);
     if (int rc = check_launch("quantize_nchw_to_nhwc")) return rc;
-    // weights re-laid k = (kh, kw, ci) and zero-padded to Kp
-    hipLaunchKernelGGL(conv_weights_i8_padded, dim3(grid_for(C_out * Kp)), dim3(kThreads), 0, ctx->stream, wq, w,
-                       (int)C_out, (int)C_in, (int)KHW, (int)Cp, (int)Kp);
-    if (int rc = check_launch("conv_weights_i8")) return rc;
     constexpr int BM = 128, BN = 128;
     I8Params p{};
     p.C = out;
