@@ -65,11 +65,14 @@ def run(dev, M, K1, N1, N2, act, bias, softmax, seed, act2=None):
     (64, 4096, 64, 64, ACT_RELU, True, True),
     (16, 9000, 64, 10, ACT_RELU, True, True),    # K ranges of several staged chunks
     (13, 301, 250, 9, ACT_TANH, True, True),     # K ranges and N1 not multiples of 4
-    (64, 400, 256, 10, ACT_RELU, True, True),    # three K ranges per tile
-    # hidden layers wider than 256: 16-column tiles, K split while the grid
-    # is under 256 workgroups and K allows
+    (64, 400, 256, 10, ACT_RELU, True, True),    # 7 blocks of 16 k per wave: groups of 8
+    (64, 1500, 128, 32, ACT_RELU, True, True),   # 32 tiles, K > 1024: four K ranges per tile
+    (40, 1200, 352, 10, ACT_GELU, True, True),   # 66 tiles: three K ranges per tile
+    (20, 2001, 250, 9, ACT_TANH, True, True),    # four K ranges, K1 and N1 not multiples of 4 (scalar loads)
+    # hidden layers wider than 256: 16-column tiles, K split for K > 1024
+    # while the grid is under 256 workgroups
     (16, 300, 512, 16, ACT_RELU, True, True),
-    (4, 2000, 2048, 4, ACT_GELU, True, True),
+    (4, 2000, 2048, 4, ACT_GELU, True, True),    # 128 tiles: two K ranges
     (3, 77, 1000, 8, ACT_RELU, False, False),   # K too short to split
     (1, 100, 8192, 1, ACT_RELU, True, False),   # 512 tiles: no split
 ])
