@@ -531,14 +531,15 @@ __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Par
 // read from LDS feeds 4 MFMAs).  Both operands are k-contiguous ([M][Kp]
 // and B^T [N][Kp]) and are loaded straight into LDS with 16-byte buffer
 // loads (LDS destination): k-tiles of 128 bytes, two static buffers, the
-// next tile's loads issued ahead of the current tile's MFMAs.  In LDS a row
+// loads of tile kt + 2 issued from the last k-step of tile kt over SPREAD
+// k-steps (SPREAD 0: in one burst ahead of that step's MFMAs).  In LDS a row
 // is 8 chunks of 16 bytes, chunk c stored at slot c ^ ((row >> 1) & 7): the
 // 16 rows one fragment read touches in a cycle fall on 16 distinct bank
 // groups.  Fragments of k-step s + 1 are read while the MFMAs of step s run.
 // Rows past M / N load as zeros (an offset past the buffer's end) and are
 // never stored; an odd last k-tile is paired with an all-zero one.
 // Requires (M + 1) * Kp and (N + 1) * Kp below 2^31 - 16.
-template <bool MIXED_LOADS>
+template <int SPREAD>
 __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
     constexpr int BM = 256, BN = 256, BK = 128, TM = 4, TN = 4;
     constexpr int kTileBytes = BM * BK;  // one operand's k-tile (BM == BN)
@@ -580,19 +581,25 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
         a_off[i] = (unsigned)min(m0 + 32 * i + sub_row, p.M) * (unsigned)Kp + 16u * chunk;
         b_off[i] = (unsigned)min(n0 + 32 * i + sub_row, p.N) * (unsigned)Kp + 16u * chunk;
     }
-    auto load_tile = [&](int8_t* As, int8_t* Bs, int kt) {
+    // Load i (0..7 A, 8..15 B) of k-tile kt, for lo <= i < hi.
+    auto load_part = [&](int8_t* As, int8_t* Bs, int kt, int lo, int hi) {
         const unsigned k0 = kt * BK < Kp ? (unsigned)(kt * BK) : kOut;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(As + (4 * i + wave) * 1024), 16,
-                                                     (int)(a_off[i] + k0), 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (4 * i + wave) * 1024), 16,
-                                                     (int)(b_off[i] + k0), 0, 0, 0);
+        for (int i = 0; i < 16; ++i) {
+            if (i < lo || i >= hi) continue;
+            if (i < 8)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(As + (4 * i + wave) * 1024), 16,
+                                                         (int)(a_off[i] + k0), 0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (4 * (i - 8) + wave) * 1024), 16,
+                                                         (int)(b_off[i - 8] + k0), 0, 0, 0);
+        }
         // keep the loads ahead of the MFMAs that follow
-        if (!MIXED_LOADS) __builtin_amdgcn_sched_barrier(0);
+        if (SPREAD == 0) __builtin_amdgcn_sched_barrier(0);
     };
+    // part q of SPREAD (SPREAD 0: one part) holds loads [lo(q), lo(q + 1))
+    constexpr int kParts = SPREAD > 0 ? SPREAD : 1;
+    auto lo = [](int q) { return 16 * q / kParts; };
 
     // fragment addresses (bytes) at k-step 0; step s reads chunk 2s + lh
     int a_rd[TM], b_rd[TN], a_sw[TM], b_sw[TN];
@@ -632,52 +639,48 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
     };
     // One k-step: its 16 MFMAs with the next step's 8 fragment reads placed
-    // one after each of the first 8 (the reads land while MFMAs run), and,
-    // with `loads`, the 16 loads of a k-tile one after each MFMA.
+    // one after each of the first 8 (the reads land while MFMAs run), and the
+    // n global loads issued just before spread evenly over the 16 MFMAs.
     auto step = [&](const v4i* af, const v4i* bf, const int8_t* As, const int8_t* Bs, int s_next, v4i* an,
-                    v4i* bn, bool loads = false) {
+                    v4i* bn, int n = 0) {
         read_frags(As, Bs, s_next, an, bn);
         mfmas(af, bf);
-        if (MIXED_LOADS && loads) {
-            // one global load after each of the 16 MFMAs
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);             // MFMA
-                if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);             // global load
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                     // MFMA
+            if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // LDS read
+            if (SPREAD > 0 && (i + 1) * n / 16 > i * n / 16)
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                 // global load
         }
         __builtin_amdgcn_sched_barrier(0);
     };
     // One k-tile in buffer X (fragments of its step 0 already in f0), with
     // tile kt + 1 landing in Y.  The barrier sits before the last step: by
     // then every wave holds all of X's fragments, so X can take tile kt + 2
-    // and the last step's MFMAs cover the first reads of Y.
+    // and the last step's MFMAs cover the first reads of Y.  The loads of
+    // tile kt + 2 start in that step (part 0) and the rest go with the first
+    // steps of tile kt + 1, so no step issues more loads than the CU's
+    // address unit takes in the step's MFMA time.
     v4i fa0[TM], fb0[TN], fa1[TM], fb1[TN];
-    auto tile = [&](int8_t* Xa, int8_t* Xb, const int8_t* Ya, const int8_t* Yb, int kt) {
-        step(fa0, fb0, Xa, Xb, 1, fa1, fb1);
-        step(fa1, fb1, Xa, Xb, 2, fa0, fb0);
+    auto tile = [&](int8_t* Xa, int8_t* Xb, int8_t* Ya, int8_t* Yb, int kt) {
+        if (kParts > 1) load_part(Ya, Yb, kt + 1, lo(1), lo(2));
+        step(fa0, fb0, Xa, Xb, 1, fa1, fb1, kParts > 1 ? lo(2) - lo(1) : 0);
+        if (kParts > 2) load_part(Ya, Yb, kt + 1, lo(2), lo(3));
+        step(fa1, fb1, Xa, Xb, 2, fa0, fb0, kParts > 2 ? lo(3) - lo(2) : 0);
         step(fa0, fb0, Xa, Xb, 3, fa1, fb1);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
-        load_tile(Xa, Xb, kt + 2);
-        step(fa1, fb1, Ya, Yb, 0, fa0, fb0, true);
+        load_part(Xa, Xb, kt + 2, 0, lo(1));
+        step(fa1, fb1, Ya, Yb, 0, fa0, fb0, lo(1));
     };
 
     // k-tiles in pairs; tiles at or past Kp load as zeros (an odd count's
     // last pair adds nothing; the look-ahead past the end is never used).
     const int pairs = (Kp / BK + 1) / 2;
-    load_tile(As0, Bs0, 0);
+    load_part(As0, Bs0, 0, 0, 16);
     __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
-    load_tile(As1, Bs1, 1);
+    load_part(As1, Bs1, 1, 0, lo(1));  // the rest in tile 0's first steps
     read_frags(As0, Bs0, 0, fa0, fb0);
     for (int pr = 0; pr < pairs; ++pr) {
         tile(As0, Bs0, As1, Bs1, 2 * pr);
@@ -825,14 +828,19 @@ int gemm_i8_core(lancius_hip_ctx* ctx, char* ws, float* C, const float* A, const
     // MFMA), else 128 x 128 (more workgroups for small products)
     const int big = tune("gemm_i8_big", ((M + 255) / 256) * ((N + 255) / 256) >= 240 ? 1 : 0);
     const int bk = tune("gemm_i8_bk", 128);
+    const bool fits31 = (M + 1) * Kp < ((size_t)1 << 31) - 16 && (N + 1) * Kp < ((size_t)1 << 31) - 16;
     const int BM = big ? 256 : 128, BN = BM;
     p.tiles_m = (uint32_t)((M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((N + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: too many tiles");
-    if (big && bk == 128 && tune("gemm_i8_direct", 1) && (M + 1) * Kp < ((size_t)1 << 31) - 16 &&
-        (N + 1) * Kp < ((size_t)1 << 31) - 16)
-        hipLaunchKernelGGL(tune("gemm_i8_mixed", 1) ? gemm_i8_direct<true> : gemm_i8_direct<false>,
+    // the k-tile loads of gemm_i8_direct spread over this many k-steps (0: in one burst)
+    const int spread = tune("gemm_i8_spread", 3);
+    if (big && bk == 128 && tune("gemm_i8_direct", 1) && fits31)
+        hipLaunchKernelGGL(spread == 0   ? gemm_i8_direct<0>
+                           : spread == 1 ? gemm_i8_direct<1>
+                           : spread == 2 ? gemm_i8_direct<2>
+                                         : gemm_i8_direct<3>,
                            dim3((unsigned)grid), dim3(256), 0, ctx->stream, p);
     else if (big && bk == 128)
         hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 128, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,

@@ -135,7 +135,40 @@ def test_gemm_i8_big_tiles_every_element(dev):
     assert oracle.normwise_error(got, ref) <= TOL
 
 
-@pytest.mark.parametrize("M,Kd,N", [(130, 70, 201), (4000, 1400, 3790), (33, 4096, 50)])
+@pytest.mark.parametrize("M,Kd,N", [(4096, 4096, 4096), (4000, 2000, 3790), (4096, 512, 4096)])
+def test_gemm_i8_big_tiles_bit_exact(dev, M, Kd, N):
+    """256 x 256 tiles over 32, 16 and 4 k-tiles (ragged M, N and K at the
+    second).  C starts as NaN.  Every element must equal the exact integer
+    product scaled in fp64 and rounded once to fp32, bit for bit."""
+    a = prng.normal(120 + M, (M, Kd))
+    bq = np.round(prng.uniform(121 + N, (Kd, N), -127.4, 127.4)).astype(np.int8)
+    da, db = dev.upload(a), dev.upload(bq)
+    dc = dev.upload(np.full((M, N), np.nan, np.float32))
+    case(f"gemm_i8 M={M} K={Kd} N={N} NaN-filled, bits")
+    dev.gemm_i8(dc, da, db, 0.0021, M, Kd, N)
+    got = dev.download(dc, (M, N))
+    for b in (da, db, dc):
+        b.free()
+    # integer partial sums below 2^53 are exact in float64 in any order
+    qa, sa = oracle.quantize_i8(f64(a).ravel())
+    ref = ((qa.reshape(M, Kd).astype(np.float64) @ bq.astype(np.float64)) * (sa * 0.0021)).astype(np.float32)
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_gemm_i8_big_tiles_epilogue(dev):
+    """The 256 x 256 kernel's staged epilogue: bias, ReLU and residual on
+    ragged edges, with an even number of k-tiles."""
+    M, Kd, N = 3850, 1000, 4000
+    a = prng.normal(122, (M, Kd))
+    bq = np.round(prng.uniform(123, (Kd, N), -127.4, 127.4)).astype(np.int8)
+    bias, res = prng.normal(124, (N,)), prng.normal(125, (M, N))
+    got = _gemm_i8(dev, a, bq, 0.004, bias=bias, act=ACT_RELU, res=res)
+    ref = np.maximum(oracle.matmul_i8(f64(a), bq, 0.004) + f64(bias)[None, :], 0.0) + f64(res)
+    assert np.isfinite(got).all()
+    assert oracle.normwise_error(got, ref) <= TOL
+
+
+@pytest.mark.parametrize("M,Kd,N", [(130, 70, 201), (4000, 1400, 3790), (33, 4096, 50), (4000, 2000, 3790)])
 def test_gemm_i8_packed_weight_bit_identical(dev, M, Kd, N):
     """lancius_hip_i8_pack_weight once + lancius_hip_gemm_i8p_f32 gives the
     bits of lancius_hip_gemm_i8_f32 (which packs on every call)."""
