@@ -967,7 +967,8 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
                        (const float*)part, parts, scales, scale_w, (int)N, (int)C_in, HW, (int)Cp, tiles_p, tiles_c,
                        cw);
     if (int rc = check_launch("quantize_nchw_to_nhwc")) return rc;
-    constexpr int BM = 128, BN = 128;
+    constexpr int BM = 128;
+    const int BN = tune("conv_i8_bn", 64) == 128 ? 128 : 64;  // pixels per tile
     I8Params p{};
     p.C = out;
     p.A = wq;
@@ -994,8 +995,15 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     p.tiles_n = (uint32_t)((P + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: too many tiles");
-    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, 2, 2, (int)BK, true, 3>), dim3((unsigned)grid), dim3(kThreads), 0,
-                       ctx->stream, p);
+    // 128 x 64 tiles, 4 workgroups per CU: the bench conv's 1568 tiles run
+    // 40 us against 47 us for 784 tiles of 128 x 128 at 3 per CU (5 per CU
+    // spilled and measured 41-43 us)
+    if (BN == 64)
+        hipLaunchKernelGGL((gemm_i8_mfma<BM, 64, 2, 2, (int)BK, true, 4>), dim3((unsigned)grid), dim3(kThreads), 0,
+                           ctx->stream, p);
+    else
+        hipLaunchKernelGGL((gemm_i8_mfma<BM, 128, 2, 2, (int)BK, true, 3>), dim3((unsigned)grid), dim3(kThreads), 0,
+                           ctx->stream, p);
     return check_launch("conv2d_i8_mfma");
 }
 
