@@ -220,6 +220,35 @@ def test_conv_i8_shapes(dev, shape):
     assert oracle.normwise_error(got, oracle.conv2d_i8(f64(x), wq, 0.003, st, pd)) <= TOL
 
 
+def test_conv_i8_bench_shape_bit_exact(dev):
+    """The bench conv (N32, 64 -> 128, 56 x 56, 3 x 3, pad 1): 1568 tiles of
+    128 x 64 pixels.  The output starts as NaN; every element must equal the
+    exact integer sum over the quantized operands times scale_w * scale_x in
+    fp64, rounded once to fp32, bit for bit."""
+    N, Ci, H, W, Co = 32, 64, 56, 56, 128
+    x = prng.normal(130, (N, Ci, H, W))
+    wq = np.round(prng.uniform(131, (Co, Ci, 3, 3), -127.4, 127.4)).astype(np.int8)
+    sw = 0.0017
+    dx, dw = dev.upload(x.astype(np.float32)), dev.upload(wq)
+    do = dev.upload(np.full((N, Co, H, W), np.nan, np.float32))
+    case(f"conv2d_i8 N={N} Ci={Ci} {H}x{W} Co={Co} 3x3 p1 NaN-filled, bits")
+    dev.conv2d_i8(do, dx, dw, sw, None, N, Ci, H, W, Co, 3, 3, 1, 1, ACT_NONE)
+    got = dev.download(do, (N, Co, H, W))
+    for b in (dx, dw, do):
+        b.free()
+    assert np.isfinite(got).all()
+    qx, sx = oracle.quantize_i8(f64(x).ravel())
+    xp = np.zeros((N, H + 2, W + 2, Ci))
+    xp[:, 1:-1, 1:-1, :] = qx.reshape(N, Ci, H, W).transpose(0, 2, 3, 1)
+    acc = np.zeros((N * H * W, Co))
+    for kh in range(3):
+        for kw in range(3):
+            # integer sums below 2^53 are exact in float64 in any order
+            acc += xp[:, kh:kh + H, kw:kw + W, :].reshape(-1, Ci) @ wq[:, :, kh, kw].astype(np.float64).T
+    ref = (acc * (sw * sx)).astype(np.float32).reshape(N, H, W, Co).transpose(0, 3, 1, 2)
+    np.testing.assert_array_equal(got, ref)
+
+
 # ---- through the device executor ------------------------------------------------------
 
 
