@@ -544,6 +544,7 @@ def cpu_baseline(M, K, N, target_s: float = 12.0) -> dict | None:
     other = {}
     if ref is not None:
         other.update(cpu_config_baselines(ref))
+        other.update(cpu_next_row_baselines(ref))
         for name, builder in (("train_step_mnist_mlp_B64_784x128x10", lambda l: graphs.build_mlp_ce(l)),
                               ("train_step_cifar_cnn_B32", lambda l: graphs.build_cnn_ce(l, batch=32))):
             other[name] = {"step_latency_ms": round(cpu_train_step_ms(ref, builder), 3),
@@ -664,6 +665,132 @@ def cpu_config_baselines(ref) -> dict:
         "GFLOP/s": round(27.925 / ms * 1e3, 3),
         "note": ("reference executor on the reference-built block graph with batch 1 (one of the 4 "
                  "sequences, which share only the weights), x4; MATMUL nodes one thread, attention OpenMP")}
+    return out
+
+
+def cpu_next_row_baselines(ref) -> dict:
+    """The reference's own CPU kernels for the bench lines of the rows past
+    the hot path (conv backward, the int8 path, the decode-side family), on
+    this host, each at its bench shape or a stated sample extrapolated
+    linearly.  Threads: the reference's OpenMP kernels run with every thread
+    this process has; the int8 MATMUL branch and kernel_rope have no
+    parallel loop (one thread)."""
+    threads = _omp_threads()
+    D = C.POINTER(C.c_double)
+    I8 = C.POINTER(C.c_int8)
+    out = {}
+
+    def timed(fn) -> float:
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    # conv backward (B/src/math/lancius_kernels.c:62-136) on 4 of the 32 images
+    log("cpu conv backward")
+    N, Cin, H, W, Cout, n_s = 32, 64, 56, 56, 128, 4
+    x = np.ascontiguousarray(prng.normal(50, (n_s, Cin, H, W)), dtype=np.float64)
+    w = np.ascontiguousarray(prng.normal(150, (Cout, Cin, 3, 3), std=float(np.sqrt(2.0 / 576))), dtype=np.float64)
+    g = np.ascontiguousarray(prng.normal(250, (n_s, Cout, H, W)), dtype=np.float64)
+    dx, dw = np.zeros_like(x), np.zeros_like(w)
+    flops = 2.0 * N * Cout * H * W * Cin * 9
+    for name, fn in (("bwd_input", lambda: ref.kernel_conv2d_bwd_in(dx.ctypes.data_as(D), g.ctypes.data_as(D),
+                                                                     w.ctypes.data_as(D), n_s, Cin, H, W, Cout, H, W,
+                                                                     3, 3, 1, 1)),
+                     ("bwd_weight", lambda: ref.kernel_conv2d_bwd_w(dw.ctypes.data_as(D), g.ctypes.data_as(D),
+                                                                     x.ctypes.data_as(D), n_s, Cin, H, W, Cout, H, W,
+                                                                     3, 3, 1, 1))):
+        dt = timed(fn) * N / n_s
+        out[f"conv3x3_N32_64to128_56x56_{name}"] = {
+            "ms": round(dt * 1e3, 1), "GFLOP/s": round(flops / dt / 1e9, 3), "cores": threads,
+            "note": f"kernel_conv2d_{'bwd_in' if name == 'bwd_input' else 'bwd_w'}, {n_s} of the {N} images timed, "
+                    f"x{N // n_s}"}
+    # int8 MATMUL branch (lancius_scheduler.c:195-220): quantize A, int32
+    # sums, one thread, through the reference executor on a row sample of
+    # the 4096^3 product
+    log("cpu int8 matmul")
+    n, rows = 4096, 16  # its B walk strides N per k: ~0.13 s per row here
+    a = np.ascontiguousarray(prng.normal(43, (rows, n)), dtype=np.float64)
+    bq = np.round(prng.uniform(1043, (n, n), -127.4, 127.4)).astype(np.int8)
+    bg = graphs.BuiltGraph(ref, ref.lancius_graph_create())
+    na, nb = ref.lancius_input(bg.g, rows, n), ref.lancius_input(bg.g, n, n)
+    ref.lancius_matmul(bg.g, na, nb)
+    nb.contents.runtime_data_int8 = bq.ctypes.data_as(I8)
+    nb.contents.scale = 0.01
+    na.contents.runtime_data = a.ctypes.data_as(D)
+    sched = ref.lancius_ir_schedule(bg.g)
+    arena = ref.lancius_arena_create(rows * n * 8 + (1 << 20))
+    dt = timed(lambda: ref.lancius_schedule_execute(sched, arena)) * n / rows
+    ref.lancius_arena_destroy(arena)
+    ref.lancius_schedule_destroy(sched)
+    na.contents.runtime_data = None
+    nb.contents.runtime_data_int8 = None
+    bg.destroy()
+    out["gemm_i8_4096"] = {"ms": round(dt * 1e3, 1), "TOPS": round(2.0 * n ** 3 / dt / 1e12, 5), "cores": 1,
+                           "note": f"reference int8 MATMUL branch (executor), rows 0-{rows - 1} of 4096 timed, "
+                                   f"x{n // rows}"}
+    # kernel_conv2d_int8_fwd (lancius_kernels.c:177-210) on 8 of the 32 images
+    log("cpu int8 conv")
+    n_s = 8
+    xq = np.round(prng.uniform(45, (n_s, Cin, H, W), -127.4, 127.4)).astype(np.int8)
+    wq = np.round(prng.uniform(145, (Cout, Cin, 3, 3), -127.4, 127.4)).astype(np.int8)
+    y = np.zeros((n_s, Cout, H, W))
+    dt = timed(lambda: ref.kernel_conv2d_int8_fwd(y.ctypes.data_as(D), xq.ctypes.data_as(I8), wq.ctypes.data_as(I8),
+                                                  0.01, 0.001, n_s, Cin, H, W, Cout, 3, 3, 1, 1)) * N / n_s
+    out["conv3x3_N32_64to128_56x56_relu_i8"] = {
+        "ms": round(dt * 1e3, 1), "TOPS": round(flops / dt / 1e12, 5), "cores": threads,
+        "note": f"kernel_conv2d_int8_fwd on int8 tensors (the quantization pass not timed), {n_s} of the {N} "
+                f"images timed, x{N // n_s}"}
+    # kernel_attention_kv_cache (lancius_kernels.c:338-379): batch 1 and
+    # Hq = Hkv, so the B16 Hq32/Hkv8 decode runs as 16 calls with 32 K/V
+    # heads (the same flops, four times the cache bytes); 2 calls timed
+    log("cpu decode attention")
+    B, Skv, Hq, Dh, n_s = 16, 4096, 32, 128, 2
+    q = np.ascontiguousarray(prng.uniform(60, (Hq * Dh,), -1.0, 1.0), dtype=np.float64)
+    kc = np.ascontiguousarray(prng.uniform(61, (Skv, Hq * Dh), -1.0, 1.0), dtype=np.float64)
+    vc = np.ascontiguousarray(prng.uniform(62, (Skv, Hq * Dh), -1.0, 1.0), dtype=np.float64)
+    o = np.zeros(Hq * Dh)
+    dt = timed(lambda: [ref.kernel_attention_kv_cache(o.ctypes.data_as(D), q.ctypes.data_as(D), kc.ctypes.data_as(D),
+                                                      vc.ctypes.data_as(D), Skv, Hq, Dh) for _ in range(n_s)]) * B / n_s
+    out["attention_decode_B16_kv4096_Hq32_Hkv8_D128"] = {
+        "ms": round(dt * 1e3, 1), "GFLOP/s": round(4.0 * B * Hq * Skv * Dh / dt / 1e9, 3), "cores": 1,
+        "note": f"kernel_attention_kv_cache (one thread, fp64), Hkv = Hq = 32 (no grouped form), {n_s} of the "
+                f"{B} sequences timed, x{B // n_s}"}
+    # kernel_gqa (lancius_kernels.c:407-448): keys = queries (no history),
+    # so the prefill's 1024 queries run over 1024 keys; one sequence of 4
+    for Dh in (64, 128):
+        log(f"cpu gqa D={Dh}")
+        Bq, Sq, Hq, Hkv = 4, 1024, 32, 8
+        q = np.ascontiguousarray(prng.uniform(63, (Sq, Hq * Dh), -1.0, 1.0), dtype=np.float64)
+        k = np.ascontiguousarray(prng.uniform(64, (Sq, Hkv * Dh), -1.0, 1.0), dtype=np.float64)
+        v = np.ascontiguousarray(prng.uniform(65, (Sq, Hkv * Dh), -1.0, 1.0), dtype=np.float64)
+        o = np.zeros_like(q)
+        dt = timed(lambda: ref.kernel_gqa(o.ctypes.data_as(D), q.ctypes.data_as(D), k.ctypes.data_as(D),
+                                          v.ctypes.data_as(D), Sq, Hq, Hkv, Dh)) * Bq
+        fl = 4.0 * Bq * Hq * Dh * Sq * (Sq + 1) / 2
+        out[f"attention_gqa_prefill_B4_q1024_Hq32_Hkv8_D{Dh}"] = {
+            "ms": round(dt * 1e3, 1), "GFLOP/s": round(fl / dt / 1e9, 3), "cores": threads,
+            "note": "kernel_gqa, causal over the 1024 queries only (it has no key history: the GPU case's 1024 "
+                    "earlier keys are not in this figure), 1 of the 4 sequences timed, x4"}
+    # row ops at the bench shapes
+    log("cpu rmsnorm / swiglu / rope")
+    rows, hid = 4096, 4096
+    x = np.ascontiguousarray(prng.normal(66, (rows, hid)), dtype=np.float64)
+    u = np.ascontiguousarray(prng.normal(67, (rows, hid)), dtype=np.float64)
+    gm = np.ones(hid)
+    y = np.zeros_like(x)
+    dt = timed(lambda: ref.kernel_rmsnorm(y.ctypes.data_as(D), x.ctypes.data_as(D), gm.ctypes.data_as(D), rows, hid,
+                                          1e-5))
+    out["rmsnorm_4096x4096"] = {"ms": round(dt * 1e3, 2), "GB/s": round(16.0 * rows * hid / dt / 1e9, 2),
+                                "cores": threads, "note": "kernel_rmsnorm, fp64 (16 bytes per element read + written)"}
+    dt = timed(lambda: ref.kernel_swiglu(y.ctypes.data_as(D), x.ctypes.data_as(D), u.ctypes.data_as(D), rows * hid))
+    out["swiglu_4096x4096"] = {"ms": round(dt * 1e3, 2), "GB/s": round(24.0 * rows * hid / dt / 1e9, 2),
+                               "cores": threads, "note": "kernel_swiglu, fp64"}
+    S, H, hd, s_rows = 4096, 16, 128, 512
+    qk = np.ascontiguousarray(prng.normal(68, (2, s_rows, H, hd)), dtype=np.float64)
+    dt = timed(lambda: ref.kernel_rope(qk[0].ctypes.data_as(D), qk[1].ctypes.data_as(D), 1, s_rows, H, hd, 0)) * S / s_rows
+    out["rope_q_k_S4096_H16_hd128"] = {"ms": round(dt * 1e3, 1), "GB/s": round(16.0 * 2 * S * H * hd / dt / 1e9, 3),
+                                       "cores": 1, "note": f"kernel_rope (one thread, pow/cos/sin per element pair), "
+                                                           f"{s_rows} of the {S} positions timed, x{S // s_rows}"}
     return out
 
 

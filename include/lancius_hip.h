@@ -139,9 +139,12 @@ LANCIUS_HIP_EXPORT int lancius_hip_conv2d_f32(lancius_hip_ctx* ctx, float* out, 
  * (lancius_hip_conv2d_packed_bytes(...) bytes), and
  * lancius_hip_conv2d_packed_f32 takes the packed copy in place of w; results
  * are bit-identical to lancius_hip_conv2d_f32.  Both require C_in % 16 == 0
- * and C_out % 4 == 0 (else -3); other convs read OIHW directly and have
- * nothing to pack.  The device executor keeps one packed copy per such
- * filter and re-packs it after an upload. */
+ * and C_out % 4 == 0, and the packed conv also one image (C_in * H * W
+ * floats) and the filter each under LANCIUS_HIP_CONV_PACKED_MAX_BYTES
+ * (else -3); other convs read OIHW directly and have nothing to pack.  The
+ * device executor keeps one packed copy per such filter and re-packs it
+ * after an upload. */
+#define LANCIUS_HIP_CONV_PACKED_MAX_BYTES ((size_t)2147483584u) /* 2^31 - 64 */
 LANCIUS_HIP_EXPORT size_t lancius_hip_conv2d_packed_bytes(size_t C_out, size_t C_in, size_t K_h, size_t K_w);
 LANCIUS_HIP_EXPORT int lancius_hip_conv2d_pack_weight(lancius_hip_ctx* ctx, float* packed, const float* w,
                                                       size_t C_out, size_t C_in, size_t K_h, size_t K_w);

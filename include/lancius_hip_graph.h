@@ -101,7 +101,12 @@ LANCIUS_HIP_EXPORT int lancius_device_download_argmax(lancius_device_program* pr
  * weights into host fp64 buffers, lancius_serialize.c:221-240). */
 LANCIUS_HIP_EXPORT int lancius_device_upload_weights(lancius_device_program* prog, const char* path,
                                                      const lancius_weight_map* map);
-/* Device address of a node's buffer (NULL for fused intermediates). */
+/* Device address of a node's buffer (NULL for fused intermediates).  The
+ * caller may write through it between runs.  A weight the program keeps a
+ * packed copy of (an int8 MATMUL weight, a conv filter with C_in % 16 == 0)
+ * is re-packed at the start of every run once its address has been handed
+ * out, so writes through the pointer reach every later run (a few
+ * microseconds per weight and run). */
 LANCIUS_HIP_EXPORT void* lancius_device_buffer(lancius_device_program* prog, const lancius_node* n);
 
 /* Enqueue one forward pass on the context's stream (asynchronous). */

@@ -49,12 +49,19 @@ struct AttnParams {
 constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
 
 // D = head dim (a multiple of 32, at most 128); BKV = keys per LDS block
-// (64 for D <= 64, 32 above, so the double-buffered K/V blocks of two
-// workgroups fit a CU's LDS).
-template <int D, int BKV>
-__global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
+// (64 for D <= 64, 32 above, so the K/V blocks of two workgroups fit a
+// CU's LDS).  KS = key split: with KS = 2 the workgroup has 8 waves, and
+// each 32-query block is owned by two waves, one taking its even key
+// blocks and one its odd ones (each step stages one block for each); at
+// the end the odd-block waves hand their (O, m, l) to the even-block waves
+// through LDS, which merge them in that fixed order.  That puts four waves on a SIMD instead of two
+// (at most 128 registers each), each with half the key blocks.  KS = 1:
+// 4 waves, every key block.  The staged keys are double-buffered in LDS.
+template <int D, int BKV, int KS>
+__global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnParams p) {
     static_assert(D % 32 == 0 && D <= 128 && BKV % 32 == 0, "tile shape");
-    constexpr int NT = 256;
+    static_assert(KS == 1 || KS == 2, "key split");
+    constexpr int NT = 256 * KS;
     constexpr int LDK = D + 1;  // K rows padded: lanes read 32 different keys at one d
     // V rows: lanes read 32 consecutive d of one key, the two lane halves
     // keys 4 rows apart; D + 8 puts those 32 banks apart (64 banks).
@@ -62,10 +69,17 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
     constexpr int QSTEPS = D / 2;        // K.Q^T MFMA steps (2 d each)
     constexpr int DB = D / 32;           // O^T d-blocks
     constexpr int SB = BKV / 32;         // S^T key blocks
-    constexpr int NKV = BKV * D / (4 * NT);  // float4 of each K/V block per thread
-    static_assert(NKV * 4 * NT == BKV * D, "staging covers the block");
-    __shared__ __attribute__((aligned(16))) float Ks[2][BKV][LDK];
-    __shared__ __attribute__((aligned(16))) float Vs[2][BKV][LDV];
+    constexpr int KB = KS * BKV;         // keys staged per step
+    constexpr int NKV = KB * D / (4 * NT);  // float4 of each K/V step per thread
+    static_assert(NKV * 4 * NT == KB * D, "staging covers the step");
+    constexpr int K_FLOATS = 2 * KB * LDK, V_FLOATS = 2 * KB * LDV;
+    constexpr int PER = 16 * DB + 2;  // a lane's hand-off: O^T registers, m, l
+    constexpr int RED_FLOATS = KS > 1 ? 4 * PER * 64 : 0;
+    constexpr int SMEM = K_FLOATS + V_FLOATS > RED_FLOATS ? K_FLOATS + V_FLOATS : RED_FLOATS;
+    static_assert(K_FLOATS % 4 == 0, "V rows 16-byte aligned");
+    __shared__ __attribute__((aligned(16))) float smem[SMEM];
+    float(*Ks)[KB][LDK] = reinterpret_cast<float(*)[KB][LDK]>(smem);
+    float(*Vs)[KB][LDV] = reinterpret_cast<float(*)[KB][LDV]>(smem + K_FLOATS);
 
     // 1-D task order, query-tile major: consecutive ids (which the hardware
     // deals round-robin to the 8 XCDs) are different (batch, head) problems of
@@ -101,9 +115,17 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
+    // KS = 2: wave w < 4 takes the even key blocks of query block w, wave
+    // w + 4 the odd key blocks of query block 3 - w.  The hardware puts
+    // waves w and w + 4 of a workgroup on the same SIMD (measured on MI355X
+    // from the HW_ID register), so each SIMD gets half of a short and half
+    // of a long query block of a causal tile, and the four SIMDs of the CU
+    // finish together.
+    const int kh = wave >> 2;                 // key parity
+    const int wq = kh ? 7 - wave : wave;      // query block of the wave
     const int lq = lane & 31, lk = lane >> 5;
     const int q0 = qt * kBQ;
-    const int qw0 = q0 + wave * 32;   // first query of this wave
+    const int qw0 = q0 + wq * 32;     // first query of this wave
     const int q = qw0 + lq;           // this lane's query
     const bool q_valid = q < S;
 
@@ -124,11 +146,12 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
         for (int i = 0; i < QSTEPS; ++i) qf[i] = 0.0f;
     }
 
-    // Key range of this workgroup.
+    // Key range of this workgroup, in blocks of BKV and steps of KS blocks.
     const int kv_end = p.causal ? max(0, min(Skv, q0 + kBQ + off)) : Skv;
     const int nblocks = (kv_end + BKV - 1) / BKV;
+    const int nsteps = (nblocks + KS - 1) / KS;
 
-    // K/V global -> register staging: BKV keys x D floats per tensor, as
+    // K/V global -> register staging: KB keys x D floats per tensor, as
     // buffer loads (the sequence's K and V rows, under 2 GiB: the host
     // checks) whose keys past Skv use a past-the-end offset and read 0; a
     // guarded plain load would be a branch per load.
@@ -175,20 +198,23 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
     float m_run = -1e30f;  // running max (log2 domain); finite so exp2 never sees inf - inf
     float l_part = 0.0f;   // this lane's share of the running sum
 
-    if (nblocks > 0) {
+    if (nsteps > 0) {
         load_kv(0);
         store_kv(0);
     }
     __syncthreads();
 
-    for (int blk = 0; blk < nblocks; ++blk) {
-        const int cur = blk & 1;
+    for (int st = 0; st < nsteps; ++st) {
+        const int cur = st & 1;
+        const bool more = st + 1 < nsteps;
+        if (more) load_kv((st + 1) * KB);
+        const int blk = st * KS + kh;  // this wave's block
         const int kb = blk * BKV;
-        const bool more = blk + 1 < nblocks;
-        if (more) load_kv(kb + BKV);
+        const int kl = kh * BKV;       // its first row in the staged keys
 
-        // Wave-uniform skip of blocks entirely above this wave's diagonal.
-        const bool active = !p.causal || kb <= qw0 + 31 + off;
+        // Wave-uniform skip of blocks past the keys or entirely above this
+        // wave's diagonal.
+        const bool active = blk < nblocks && (!p.causal || kb <= qw0 + 31 + off);
         if (active) {
             f32x16 s_acc[SB];
 #pragma unroll
@@ -200,8 +226,8 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
                 const int d = s + QSTEPS * lk;
 #pragma unroll
                 for (int sb = 0; sb < SB; ++sb)
-                    s_acc[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[cur][32 * sb + lq][d], qf[s], s_acc[sb], 0,
-                                                                     0, 0);
+                    s_acc[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[cur][kl + 32 * sb + lq][d], qf[s], s_acc[sb],
+                                                                     0, 0, 0);
             }
             // Register r of lane l holds key kb + 32*sb + 8*(r/4) + 4*(l/32) + r%4.
             const bool need_mask = (p.causal && kb + BKV - 1 > qw0 + off) || (kb + BKV > Skv);
@@ -245,12 +271,38 @@ __global__ void __launch_bounds__(256, 2) attention_mfma(const AttnParams p) {
                     const int key = 32 * sb + 8 * (s >> 2) + 4 * lk + (s & 3);
 #pragma unroll
                     for (int db = 0; db < DB; ++db)
-                        o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[cur][key][32 * db + lq], s_acc[sb][s],
-                                                                         o_acc[db], 0, 0, 0);
+                        o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[cur][kl + key][32 * db + lq],
+                                                                         s_acc[sb][s], o_acc[db], 0, 0, 0);
                 }
         }
         if (more) store_kv(cur ^ 1);
         __syncthreads();
+    }
+
+    if constexpr (KS > 1) {
+        // Waves of the odd blocks hand their O^T, m and l to the waves of the
+        // even blocks (same queries, same lanes), which merge them:
+        // m = max(m0, m1), O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise.
+        // The loop's last barrier has retired every read of the staged keys.
+        float* red = smem + wq * PER * 64 + lane;  // [wq][PER][64 lanes]
+        if (kh == 1) {
+#pragma unroll
+            for (int db = 0; db < DB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) red[(16 * db + r) * 64] = o_acc[db][r];
+            red[16 * DB * 64] = m_run;
+            red[(16 * DB + 1) * 64] = l_part;
+        }
+        __syncthreads();
+        if (kh == 1) return;
+        const float m1 = red[16 * DB * 64], l1 = red[(16 * DB + 1) * 64];
+        const float m = fmaxf(m_run, m1);
+        const float c0 = exp2f(m_run - m), c1 = exp2f(m1 - m);
+        l_part = l_part * c0 + l1 * c1;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o_acc[db][r] = o_acc[db][r] * c0 + red[(16 * db + r) * 64] * c1;
     }
 
     const float l_tot = l_part + __shfl_xor(l_part, 32);
@@ -690,13 +742,20 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
         p.q_tiles = (int)((S + kBQ - 1) / kBQ);
         const size_t tasks = (size_t)p.q_tiles * H * z;
         LANCIUS_REQUIRE(tasks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention: too many tiles");
-        p.pair_tiles = causal && tasks <= 2 * (size_t)cu_count(ctx) && tune("attn_pair", 1);
+        p.pair_tiles = causal && tasks <= 2 * (size_t)cu_count(ctx);
         const dim3 grid((unsigned)tasks);
+        // D = 64 runs the key split (KS = 2, 32-key blocks, four waves a
+        // SIMD), measured against one wave per query block (64-key blocks,
+        // two waves a SIMD): B8 H16 S512 causal 55.7 -> 50.9 us, S2048
+        // causal 0.611 -> 0.585 ms, non-causal 1.136 -> 1.113 ms, B4 S1024
+        // causal 94.1 -> 89.2 us.  At D = 32 it measured slower (S2048
+        // causal 0.328 -> 0.337 ms); D = 96 and 128 do not fit four waves'
+        // registers.
         switch (D) {
-            case 32: hipLaunchKernelGGL((attention_mfma<32, 64>), grid, dim3(256), 0, ctx->stream, p); break;
-            case 64: hipLaunchKernelGGL((attention_mfma<64, 64>), grid, dim3(256), 0, ctx->stream, p); break;
-            case 96: hipLaunchKernelGGL((attention_mfma<96, 32>), grid, dim3(256), 0, ctx->stream, p); break;
-            default: hipLaunchKernelGGL((attention_mfma<128, 32>), grid, dim3(256), 0, ctx->stream, p); break;
+            case 32: hipLaunchKernelGGL((attention_mfma<32, 64, 1>), grid, dim3(256), 0, ctx->stream, p); break;
+            case 64: hipLaunchKernelGGL((attention_mfma<64, 32, 2>), grid, dim3(512), 0, ctx->stream, p); break;
+            case 96: hipLaunchKernelGGL((attention_mfma<96, 32, 1>), grid, dim3(256), 0, ctx->stream, p); break;
+            default: hipLaunchKernelGGL((attention_mfma<128, 32, 1>), grid, dim3(256), 0, ctx->stream, p); break;
         }
         if (int rc = check_launch("attention_mfma")) return rc;
     } else {

@@ -44,18 +44,6 @@ int check_launch(const char* kernel) {
     return 0;
 }
 
-int tune(const char* key, int fallback) {
-    static const char* env = getenv("LANCIUS_HIP_TUNE");
-    if (!env || !key) return fallback;
-    const size_t n = strlen(key);
-    for (const char* p = env; p && *p;) {
-        if (strncmp(p, key, n) == 0 && p[n] == '=') return atoi(p + n + 1);
-        p = strchr(p, ',');
-        if (p) ++p;
-    }
-    return fallback;
-}
-
 int cu_count(lancius_hip_ctx* ctx) {
     if (ctx->cus <= 0) {
         int n = 0;
@@ -160,6 +148,13 @@ int lancius_hip_ctx_create(int device, void* stream, lancius_hip_ctx** out) {
     if (e != hipSuccess) {
         free(c);
         return from_hip(e, "hipEventCreate");
+    }
+    if (int rc = noalloc_scratch_init(c)) {
+        (void)hipEventDestroy(c->ev_start);
+        (void)hipEventDestroy(c->ev_stop);
+        (void)hipEventDestroy(c->ev_order);
+        free(c);
+        return rc;
     }
     *out = c;
     return ok();

@@ -604,9 +604,8 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
     const size_t tiles = row_blocks * (size_t)p.tiles_n;
     if (int rc = counters(ctx, row_blocks, &p.counters)) return rc;
     void* ws = nullptr;
-    const int split = tune("mlp2_split", -1);  // 0: never, 1: whenever N1 allows, -1: few tiles with a long K
-    if ((size_t)p.tiles_n * kFC <= (size_t)kSplitMaxN1 &&
-        (split == 1 || (split < 0 && tiles <= kSplitMaxTiles && K1 >= kSplitMinK))) {
+    // mlp2_split for few tiles with a long K, mlp2_tiles otherwise
+    if ((size_t)p.tiles_n * kFC <= (size_t)kSplitMaxN1 && tiles <= kSplitMaxTiles && K1 >= kSplitMinK) {
         // K ranges of at least 64 that bring the grid to about one
         // workgroup per CU
         int ks = (int)std::max<size_t>(1, std::min<size_t>(kMaxSplit, 256 / tiles));
@@ -624,8 +623,7 @@ extern "C" int lancius_hip_mlp2_ex_f32(lancius_hip_ctx* ctx, float* out, int32_t
     // bring the grid to about one workgroup per CU (measured, 64 rows, 256
     // hidden: K 784 is fastest whole, 8.2 against 8.5 us with four ranges;
     // K 1500 and 4096 split four ways, 10.9 -> 9.1 and 17.9 -> 10.6 us)
-    int ks = tune("mlp2_tiles_ks", -1);
-    if (ks < 0) ks = K1 <= (size_t)kFKC ? 1 : (int)std::max<size_t>(1, std::min<size_t>(kMaxSplit, 256 / tiles));
+    int ks = K1 <= (size_t)kFKC ? 1 : (int)std::max<size_t>(1, std::min<size_t>(kMaxSplit, 256 / tiles));
     ks = std::max(1, std::min(ks, kMaxSplit));
     while (ks > 1 && K1 < (size_t)ks * kTilesMinK) --ks;
     p.kchunk = (int)((K1 + ks - 1) / ks + 3) / 4 * 4;

@@ -46,12 +46,6 @@ int check_launch(const char* kernel);
 // Makes `ctx->device` current for the calling thread.
 int bind_device(lancius_hip_ctx* ctx);
 
-// Tuning override read once from the environment variable LANCIUS_HIP_TUNE,
-// a comma-separated list of key=value integers (e.g. "conv_bn=64,gemm=2").
-// Returns `fallback` for keys that are not set.  Used to sweep launch shapes
-// on hardware; the defaults are the measured best.
-int tune(const char* key, int fallback);
-
 // Device scratch owned by the context, grown with hipMalloc on demand and
 // kept until the context is destroyed.  Calls on one context are ordered by
 // its stream, so one buffer serves every kernel of the context.
@@ -63,6 +57,11 @@ int cu_count(lancius_hip_ctx* ctx);
 // At least n zero-initialised arrival counters (see counters in the context);
 // every kernel that increments a counter returns it to zero before exiting.
 int counters(lancius_hip_ctx* ctx, size_t n, unsigned** out);
+
+// Device address of lancius_hip_gemm_f32_noalloc's scratch on the
+// context's device (current), resolved and its counters cleared once per
+// device; called by lancius_hip_ctx_create.
+int noalloc_scratch_init(lancius_hip_ctx* ctx);
 
 static inline unsigned int ceil_div(size_t a, size_t b) { return (unsigned int)((a + b - 1) / b); }
 

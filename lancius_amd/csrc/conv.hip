@@ -284,7 +284,7 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
 //    past the batch and every load of a k-tile past the end use an offset
 //    past the input's end and read 0.
 // Requires the input and wt below 2 GiB.
-template <int BM, int BN, int KH_T, int KW_T, bool MIX>
+template <int BM, int BN, int KH_T, int KW_T>
 __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p) {
     constexpr int BK = 16, WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
     constexpr int A_INSTR = BM * BK / 4 / 256;  // 16-byte instructions per wave per k-tile
@@ -374,7 +374,6 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
             const unsigned bo = (unsigned)pick(inside, (int)(pix + (unsigned)row * HW4), (int)kOut);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_void*)(Bs + (4 * j + wave) * 64), 4, (int)bo, 0, 0, 0);
         }
-        if (!MIX) __builtin_amdgcn_sched_barrier(0);
     };
 
     f32x16 acc[TM][TN];
@@ -403,16 +402,14 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (MIX) {
-            // the k-tile's loads one after each of the first MFMAs
+        // the k-tile's loads one after each of the first MFMAs
 #pragma unroll
-            for (int i = 0; i < A_INSTR + B_INSTR; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - A_INSTR - B_INSTR, 0);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < A_INSTR + B_INSTR; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - A_INSTR - B_INSTR, 0);
+        __builtin_amdgcn_sched_barrier(0);
     };
     // acc = the tile's sums over k-tiles [kbeg, kend), in pairs (a pair's
     // second tile past kend loads zeros)
@@ -432,7 +429,7 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
             compute(As0, Bs0);
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
             __syncthreads();
-            if (MIX || pr + 1 < pairs) load_tile(As0, Bs0, kbeg + 2 * pr + 2, kend);  // past the end: zeros
+            load_tile(As0, Bs0, kbeg + 2 * pr + 2, kend);  // past the end: zeros
             compute(As1, Bs1);
             __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
             __syncthreads();
@@ -1019,24 +1016,31 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d: too many tiles");
     constexpr int WGM = BM >= 64 ? 2 : 1;
     constexpr int WGN = 4 / WGM;
-    // conv2d_direct: whole tiles, plus a stream-K share of the rest when
-    // the tiles are not a multiple of the CUs (see conv2d_direct)
-    bool direct = false;
+    // The filter re-laid per output channel (taps outer, input channels
+    // inner) feeds conv2d_direct (64- and 128-channel tiles: whole tiles,
+    // plus a stream-K share of the rest when the tiles are not a multiple
+    // of the CUs) and the A loads of the 32 x 128 implicit GEMM; every other
+    // launch reads OIHW.  conv2d_direct addresses the input and the filter
+    // with 32-bit offsets: the callers split the batch so that a launch's
+    // input stays under 2 GiB (one image beyond that takes the OIHW path).
+    constexpr bool kDirect = (BM == 64 || BM == 128) && (BN == 64 || BN == 128);
+    const bool per_co = p.C_in % 16 == 0 && p.C_out % 4 == 0 &&
+                        (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < LANCIUS_HIP_CONV_PACKED_MAX_BYTES &&
+                        (size_t)p.C_out * p.Kdim * sizeof(float) < LANCIUS_HIP_CONV_PACKED_MAX_BYTES;
+    const bool direct = kDirect && per_co;
+    const bool wt_layout = per_co && (kDirect || BM == 32);
+    LANCIUS_REQUIRE(p.prep != 0 || wt_layout, LANCIUS_HIP_ERR_SHAPE,
+                    "conv2d_packed: an image of %d x %d x %d or the filter is beyond 2 GiB (use lancius_hip_conv2d_f32)",
+                    p.C_in, p.H, p.W);
     void (*kern)(const ConvParams) = nullptr;
-    if constexpr ((BM == 64 || BM == 128) && (BN == 64 || BN == 128)) {
-        direct = p.C_in % 16 == 0 && p.C_out % 4 == 0 && tune("conv_direct", 1) &&
-                 (size_t)p.N * p.C_in * p.H * p.W * sizeof(float) < ((size_t)1 << 31) - 64 &&
-                 (size_t)p.C_out * p.Kdim * sizeof(float) < ((size_t)1 << 31) - 64;
-        kern = tune("conv_mix", 1) ? conv2d_direct<BM, BN, KH_T, KW_T, true> : conv2d_direct<BM, BN, KH_T, KW_T, false>;
-    }
+    if constexpr (kDirect) kern = conv2d_direct<BM, BN, KH_T, KW_T>;
     p.sk_dp = (int)grid;
     p.sk_wgs = 0;
     size_t part_bytes = 0;
-    if (direct && tune("conv_stream_k", 1)) {
+    if (direct) {
         // resident workgroups per CU, per instantiation (host threads may
         // race to fill it in: they all store the same value)
-        static std::atomic<int> occupancy[2];
-        std::atomic<int>& slot = occupancy[tune("conv_mix", 1) ? 1 : 0];
+        static std::atomic<int> slot;
         int occ = slot.load(std::memory_order_relaxed);
         if (occ == 0) {
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, kThreads, 0) != hipSuccess || occ < 1) occ = 1;
@@ -1060,53 +1064,76 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
             part_bytes = 2 * cus * BM * BN * sizeof(float);
         }
     }
-    const bool per_co = p.C_in % 16 == 0 && p.C_out % 4 == 0;
     const size_t wcount = (size_t)p.C_out * p.Kdim;
-    const size_t wbytes = (p.prep == 1 && per_co) || p.prep == 2 ? (wcount * sizeof(float) + 255) / 256 * 256 : 0;
+    const size_t wbytes = (p.prep == 1 && wt_layout) || p.prep == 2 ? (wcount * sizeof(float) + 255) / 256 * 256 : 0;
     if (wbytes + part_bytes > 0) {
         void* ws = nullptr;
         if (int rc = workspace(ctx, wbytes + part_bytes, &ws)) return rc;
         p.sk_part = (float*)((char*)ws + wbytes);
         const unsigned wgrid = (unsigned)std::min<size_t>((wcount + 255) / 256, 2048);
-        if (p.prep == 1 && per_co) {
+        if (p.prep == 1 && wt_layout) {
             p.wt = (const float*)ws;
             hipLaunchKernelGGL(conv_weights_per_co, dim3(wgrid), dim3(256), 0, ctx->stream, (float*)ws, p.w, p.C_out,
                                p.C_in, p.KH * p.KW);
             if (int rc = check_launch("conv_weights_per_co")) return rc;
         } else if (p.prep == 2) {
             hipLaunchKernelGGL(dgrad_weights, dim3(wgrid), dim3(256), 0, ctx->stream, (float*)ws, p.w_src, p.C_in,
-                               p.C_out, p.KH, p.KW, (int)per_co);
+                               p.C_out, p.KH, p.KW, (int)wt_layout);
             if (int rc = check_launch("conv2d_dgrad_weights")) return rc;
-            if (per_co)
+            if (wt_layout)
                 p.wt = (const float*)ws;
             else
                 p.w = (const float*)ws;
         }
     }
-    if (direct && p.wt) {
+    if (direct) {
         if (p.sk_wgs > 0)
             if (int rc = counters(ctx, grid - (size_t)p.sk_dp, &p.sk_ctr)) return rc;
         hipLaunchKernelGGL(kern, dim3((unsigned)(p.sk_dp + p.sk_wgs)), dim3(kThreads), 0, ctx->stream, p);
         return check_launch("conv2d_direct");
     }
-    if (p.wt)
-        hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
-                           dim3(kThreads), 0, ctx->stream, p);
-    else
-        hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, false>), dim3((unsigned)grid),
-                           dim3(kThreads), 0, ctx->stream, p);
+    if constexpr (BM == 32) {
+        if (wt_layout) {
+            hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, true>), dim3((unsigned)grid),
+                               dim3(kThreads), 0, ctx->stream, p);
+            return check_launch("conv2d_implicit_gemm");
+        }
+    }
+    hipLaunchKernelGGL((conv2d_implicit_gemm<BM, BN, 16, WGM, WGN, KH_T, KW_T, false>), dim3((unsigned)grid),
+                       dim3(kThreads), 0, ctx->stream, p);
     return check_launch("conv2d_implicit_gemm");
 }
 
 int default_tile(size_t C_out) { return C_out > 64 ? 1 : C_out > 32 ? 2 : 3; }
 
 template <int KH_T, int KW_T>
+int launch_tile(lancius_hip_ctx* ctx, ConvParams& p, int tile);
+
+// One launch per run of images whose input stays under 2 GiB (the direct
+// kernel's 32-bit input offsets); the images of a conv are independent, so
+// the split changes no result.  p describes the whole batch.
+int launch_batches(lancius_hip_ctx* ctx, const ConvParams& p, int tile) {
+    const size_t img_in = (size_t)p.C_in * p.H * p.W, img_out = (size_t)p.C_out * p.Ho * p.Wo;
+    const size_t per = std::max<size_t>(1, std::min<size_t>((size_t)p.N, (LANCIUS_HIP_CONV_PACKED_MAX_BYTES - 1) /
+                                                                           (img_in * sizeof(float))));
+    for (size_t n0 = 0; n0 < (size_t)p.N; n0 += per) {
+        ConvParams q = p;
+        q.N = (int)std::min<size_t>(per, (size_t)p.N - n0);
+        q.in = p.in + n0 * img_in;
+        q.out = p.out + n0 * img_out;
+        q.Ptotal = (long long)q.N * p.Ho * p.Wo;
+        const int rc = (p.KH == 3 && p.KW == 3) ? launch_tile<3, 3>(ctx, q, tile) : launch_tile<0, 0>(ctx, q, tile);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+template <int KH_T, int KW_T>
 int launch_tile(lancius_hip_ctx* ctx, ConvParams& p, int tile) {
     switch (tile) {
         case 1: return launch<128, 64, KH_T, KW_T>(ctx, p);
         case 2: return launch<64, 64, KH_T, KW_T>(ctx, p);
-        case 3: return launch<32, 128, KH_T, KW_T>(ctx, p);
-        default: return launch<128, 128, KH_T, KW_T>(ctx, p);
+        default: return launch<32, 128, KH_T, KW_T>(ctx, p);
     }
 }
 
@@ -1160,8 +1187,7 @@ int conv2d_entry(lancius_hip_ctx* ctx, float* out, const float* in, const float*
     // loads 100.9 TFLOP/s against 89.6 for 128x128): twice the workgroups, a
     // shorter tail; 64x64 for its dgrad (64 output channels: 238 -> 204 us
     // against 32x128).
-    const int tile = tune("conv_tile", default_tile(C_out));
-    const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
+    const int rc = launch_batches(ctx, p, default_tile(C_out));
     return rc ? rc : ok();
 }
 
@@ -1220,7 +1246,7 @@ extern "C" int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx,
     // (H = H_out + K - 1 - 2 pad, pad <= K - 1): the forward implicit GEMM
     // over flipped weights.  Anything else: the direct kernel.
     const bool as_conv = stride == 1 && K_h == K_w && pad + 1 <= K_h && H_out > 0 && W_out > 0 &&
-                         H + 2 * pad + 1 == H_out + K_h && W + 2 * pad + 1 == W_out + K_w && tune("conv_dgrad", 1);
+                         H + 2 * pad + 1 == H_out + K_h && W + 2 * pad + 1 == W_out + K_w;
     if (!as_conv) {
         const unsigned grid = (unsigned)std::max<size_t>(1, std::min<size_t>((total + 255) / 256, 16384));
         hipLaunchKernelGGL(dgrad_direct, dim3(grid), dim3(256), 0, ctx->stream, dx, dy, w, (int)N, (int)C_in, (int)H,
@@ -1247,8 +1273,7 @@ extern "C" int lancius_hip_conv2d_bwd_input_f32(lancius_hip_ctx* ctx, float* dx,
     p.act = LANCIUS_HIP_ACT_NONE;
     p.prep = 2;  // the launch lays out the flipped weights of w
     p.w_src = w;
-    const int tile = tune("conv_tile", default_tile((size_t)p.C_out));
-    const int rc = (K_h == 3 && K_w == 3) ? launch_tile<3, 3>(ctx, p, tile) : launch_tile<0, 0>(ctx, p, tile);
+    const int rc = launch_batches(ctx, p, default_tile((size_t)p.C_out));
     return rc ? rc : ok();
 }
 
@@ -1268,7 +1293,7 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     if (int rc = bind_device(ctx)) return rc;
     // 128 x 64 tiles (two 32 x 32 MFMA blocks per wave) when C_out > 64,
     // else 64 x 64 (one)
-    const int BM = tune("conv_wgrad_bm", C_out > 64 ? 128 : 64) == 128 ? 128 : 64, BN = 64;
+    const int BM = C_out > 64 ? 128 : 64, BN = 64;
     WgradParams p{};
     p.dw = dw;
     p.dy = dy;
@@ -1302,18 +1327,15 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
     // (N32 64->128 56x56: 0.1477 ms at two, 0.1450 at three, 0.1461 at four;
     // the staged kernel 0.1939)
     const size_t HWo = H_out * W_out;
-    const bool direct = tune("conv_wgrad_direct", 1) && HWo % 4 == 0 && HWo >= 16 &&
+    const bool direct = HWo % 4 == 0 && HWo >= 16 &&
                         N * C_out * HWo * sizeof(float) < ((size_t)1 << 31) - 64 &&
                         N * C_in * H * W * sizeof(float) < ((size_t)1 << 31) - 64;
-    int bk = direct ? 32 : tune("conv_wgrad_bk", 32);
-    if (bk != 16 && bk != 64) bk = 32;
-    if (BM == 128 && bk == 64) bk = 32;
+    constexpr int bk = 32;
     const long long ktiles = (p.Ptotal + bk - 1) / bk;
-    long long splits = tune("conv_wgrad_split", 0);
-    if (splits <= 0) {
+    long long splits;
+    {
         const size_t lds = (size_t)2 * bk * ((BM + 4) + (BN + 4)) * sizeof(float);
-        const size_t per_cu = direct ? (size_t)std::max(1, tune("conv_wgrad_direct_occ", 3))
-                                     : std::max<size_t>(1, std::min<size_t>(8, 163840 / lds));
+        const size_t per_cu = direct ? 3 : std::max<size_t>(1, std::min<size_t>(8, 163840 / lds));
         const size_t slots = (size_t)cu_count(ctx) * per_cu;
         splits = std::max<long long>(1, std::min<long long>((long long)std::max<size_t>(1, slots / tiles),
                                                             ktiles * bk / 256));
@@ -1333,16 +1355,10 @@ extern "C" int lancius_hip_conv2d_bwd_weight_f32(lancius_hip_ctx* ctx, float* dw
         hipLaunchKernelGGL(conv2d_wgrad_direct<128>, grid, dim3(256), 0, ctx->stream, p);
     else if (direct)
         hipLaunchKernelGGL(conv2d_wgrad_direct<64>, grid, dim3(256), 0, ctx->stream, p);
-    else if (BM == 128 && bk == 32)
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<128, 64, 32>), grid, dim3(256), 0, ctx->stream, p);
     else if (BM == 128)
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<128, 64, 16>), grid, dim3(256), 0, ctx->stream, p);
-    else if (bk == 64)
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<64, 64, 64>), grid, dim3(256), 0, ctx->stream, p);
-    else if (bk == 32)
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<64, 64, 32>), grid, dim3(256), 0, ctx->stream, p);
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<128, 64, bk>), grid, dim3(256), 0, ctx->stream, p);
     else
-        hipLaunchKernelGGL((conv2d_wgrad_mfma<64, 64, 16>), grid, dim3(256), 0, ctx->stream, p);
+        hipLaunchKernelGGL((conv2d_wgrad_mfma<64, 64, bk>), grid, dim3(256), 0, ctx->stream, p);
     if (int rc = check_launch("conv2d_wgrad_mfma")) return rc;
     if (p.splits > 1) {
         const size_t n = C_out * J;

@@ -38,7 +38,6 @@ struct GemmParams {
     unsigned* counters;  // fused skinny split-K: one arrival counter per (group, column block), zero between launches
     int splits;  // K ranges (blockIdx.y), 1 = no split
     int kchunk;  // K per split, a multiple of the k-tile
-    int map2d;   // 1: each XCD owns a 2-D block of tiles (tiles_m % 2 == 0, tiles_n % 4 == 0)
 };
 
 constexpr int kThreads = 256;
@@ -96,18 +95,7 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
 
     const uint32_t ntiles = p.tiles_m * p.tiles_n;
     uint32_t tm_id, tn_id;
-    if (p.map2d) {
-        // XCD x = id % 8 owns the (x/4, x%4) block of a 2 x 4 partition of the
-        // tile grid, so it needs half of A and a quarter of B instead of all of B.
-        const uint32_t xcd = blockIdx.x % kNumXcd, local = blockIdx.x / kNumXcd;
-        const uint32_t rm = p.tiles_m / 2, rn = p.tiles_n / 4;
-        uint32_t lm, ln;
-        grouped_tile(local, rm, rn, 4, lm, ln);
-        tm_id = (xcd / 4) * rm + lm;
-        tn_id = (xcd % 4) * rn + ln;
-    } else {
-        grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
-    }
+    grouped_tile(xcd_contiguous_id(blockIdx.x, ntiles), p.tiles_m, p.tiles_n, 4, tm_id, tn_id);
     const int m0 = (int)tm_id * BM;
     const int n0 = (int)tn_id * BN;
 
@@ -493,7 +481,7 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
 // Requires A, B non-transposed and float4-aligned (K, N multiples of 4) and
 // both operands under 2 GiB.  A and B use the same k pairing as the AMK
 // path: lane half h of the MFMAs takes k in [8h, 8h + 8).
-template <int OCC, int MIX>
+template <int OCC>
 __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) {
     constexpr int BM = 128, BN = 128, BK = 16;
     constexpr int WM = 64, WN = 64, TM = 2, TN = 2;
@@ -551,10 +539,7 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
             const int bo = k0 + b_kr[i] < K ? b_off0[i] + k0 * N * (int)sizeof(float) : kOut;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (2 * wave + i) * 256), 16, bo, 0, 0, 0);
         }
-        // keep the loads ahead of the MFMAs that follow (the scheduler would
-        // otherwise sink them to the wait before the barrier); with MIX they
-        // go between the first MFMAs instead (see compute)
-        if (!MIX) __builtin_amdgcn_sched_barrier(0);
+        // (compute places them between its first MFMAs)
     };
 
     f32x16 acc[TM][TN];
@@ -597,15 +582,16 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][kp / 4][kp % 4], bf[j], acc[i][j], 0, 0, 0);
         }
-        if (MIX) {
+        // the k-tile's four loads one after each of the first four MFMAs
+        // (the scheduler would otherwise sink them to the wait before the
+        // barrier)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, MIX, 0);  // MFMAs
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // global load
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - 4 * MIX, 0);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
         }
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - 4, 0);
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     // k-tiles in pairs; when their count is odd the last pair's second tile
@@ -619,9 +605,9 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
         compute(As0, Bs0);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
-        // (with MIX unconditional, so the loads share the MFMAs' block: past
-        // K they read zeros, and the wait below covers them)
-        if (MIX || pr + 1 < pairs) load_tile(As0, Bs0, 2 * pr + 2);
+        // (unconditional, so the loads share the MFMAs' block: past K they
+        // read zeros, and the wait below covers them)
+        load_tile(As0, Bs0, 2 * pr + 2);
         compute(As1, Bs1);
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         __syncthreads();
@@ -1122,31 +1108,6 @@ __global__ void __launch_bounds__(64 * WAVES) gemm_skinny_f32(const GemmParams p
     }
 }
 
-// splitk_reduce over float4 groups (N % 4 == 0): same order, same epilogue.
-__global__ void __launch_bounds__(256) splitk_reduce_vec4(const GemmParams p, int count) {
-    const size_t MN = (size_t)p.M * p.N;
-    const size_t total4 = (size_t)count * MN / 4;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i4 = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i4 < total4; i4 += stride) {
-        const size_t idx = 4 * i4;
-        const int g = (int)(idx / MN);
-        const size_t e = idx - (size_t)g * MN;
-        const float* part = p.ws + (size_t)g * p.splits * MN + e;
-        f32x4 s = *(const f32x4*)part;
-        for (int y = 1; y < p.splits; ++y) s += *(const f32x4*)(part + (size_t)y * MN);
-        const int col = (int)(e % p.N);
-        float o[4] = {s.x, s.y, s.z, s.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float v = o[j] + (p.bias[g] ? p.bias[g][col + j] : 0.0f);
-            v = apply_act(v, p.act);
-            if (p.R[g]) v += p.R[g][e + j];
-            o[j] = v;
-        }
-        *(f32x4*)(p.C[g] + e) = f32x4{o[0], o[1], o[2], o[3]};
-    }
-}
-
 // Sums split-K partials in split order and applies the epilogue.
 __global__ void __launch_bounds__(256) splitk_reduce(const GemmParams p, int count) {
     const size_t MN = (size_t)p.M * p.N;
@@ -1166,27 +1127,46 @@ __global__ void __launch_bounds__(256) splitk_reduce(const GemmParams p, int cou
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int OCC = 1, bool TA = false, bool TB = false, int KG = 1>
+// SPLITS: the configuration can be chosen for a split K (grids under 256
+// tiles); VECS: with float4 operand loads (false where the dispatch sends
+// every float4-shaped case of the configuration to a direct kernel).  Only
+// the variants the dispatch can reach are built.
+template <int BM, int BN, int BK, int WGM, int WGN, int OCC = 1, bool TA = false, bool TB = false, int KG = 1,
+          bool SPLITS = true, bool VECS = true>
 int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
     constexpr int SOCC = KG > 1 ? OCC : 1;  // occupancy hint of the split and scalar variants
     p.tiles_m = (uint32_t)((p.M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((p.N + BN - 1) / BN);
-    p.map2d = tune("gemm_map", 0) == 1 && p.tiles_m % 2 == 0 && p.tiles_n % 4 == 0;
     dim3 grid(p.tiles_m * p.tiles_n, (unsigned)p.splits, (unsigned)count);
     const bool split = p.splits > 1;
+    LANCIUS_REQUIRE((SPLITS || !split) && (VECS || !vec), LANCIUS_HIP_ERR_INTERNAL,
+                    "gemm: configuration %dx%d/%d without this variant (split %d, vec %d)", BM, BN, BK, (int)split,
+                    (int)vec);
     const dim3 block(kThreads * KG);
-    if (vec && split)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true, SOCC, TA, TB, KG>), grid, block, 0,
-                           ctx->stream, p);
-    else if (vec)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false, OCC, TA, TB, KG>), grid, block, 0,
-                           ctx->stream, p);
-    else if (split)
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true, SOCC, TA, TB, KG>), grid, block, 0,
-                           ctx->stream, p);
-    else
-        hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, false, SOCC, TA, TB, KG>), grid, block, 0,
-                           ctx->stream, p);
+    if constexpr (SPLITS && VECS) {
+        if (vec && split) {
+            hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, true, SOCC, TA, TB, KG>), grid, block, 0,
+                               ctx->stream, p);
+            goto launched;
+        }
+    }
+    if constexpr (VECS) {
+        if (vec) {
+            hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, true, false, OCC, TA, TB, KG>), grid, block, 0,
+                               ctx->stream, p);
+            goto launched;
+        }
+    }
+    if constexpr (SPLITS) {
+        if (split) {
+            hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, true, SOCC, TA, TB, KG>), grid, block, 0,
+                               ctx->stream, p);
+            goto launched;
+        }
+    }
+    hipLaunchKernelGGL((gemm_f32_mfma<BM, BN, BK, WGM, WGN, false, false, SOCC, TA, TB, KG>), grid, block, 0,
+                       ctx->stream, p);
+launched:
     if (int rc = check_launch("gemm_f32_mfma")) return rc;
     if (split) {
         const size_t total = (size_t)count * p.M * p.N;
@@ -1198,26 +1178,31 @@ int launch_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec) {
 }
 
 // Transposed operands are built for the two default tile shapes only.
+// Configurations 6 and 8 run grids of at least 256 tiles, which never split
+// K; with plain operands, configuration 6's float4 case is the direct
+// kernel's (the dispatch sends operands beyond its 2 GiB offsets to the
+// scalar variant).
 template <bool TA, bool TB>
 int launch_by_cfg(lancius_hip_ctx* ctx, GemmParams& p, int count, bool vec, int cfg) {
     if constexpr (TA || TB) {
         if (cfg == 2) return launch_cfg<64, 64, 16, 2, 2, 1, TA, TB>(ctx, p, count, vec);
-        return launch_cfg<128, 128, 16, 2, 2, 4, TA, TB>(ctx, p, count, vec);
+        return launch_cfg<128, 128, 16, 2, 2, 4, TA, TB, 1, false>(ctx, p, count, vec);
     } else {
         switch (cfg) {
             case 2: return launch_cfg<64, 64, 16, 2, 2>(ctx, p, count, vec);
-            case 3: return launch_cfg<256, 128, 16, 2, 2>(ctx, p, count, vec);
-            case 4: return launch_cfg<128, 128, 32, 2, 2>(ctx, p, count, vec);
-            case 5: return launch_cfg<128, 256, 16, 2, 2>(ctx, p, count, vec);
-            case 6: return launch_cfg<128, 128, 16, 2, 2, 4>(ctx, p, count, vec);
             case 7: return launch_cfg<128, 128, 32, 2, 2, 2, false, false, 2>(ctx, p, count, vec);
-            case 8: return launch_cfg<128, 128, 32, 2, 2, 1, false, false, 4>(ctx, p, count, vec);
+            case 8: return launch_cfg<128, 128, 32, 2, 2, 1, false, false, 4, false>(ctx, p, count, vec);
             case 9: return launch_cfg<64, 64, 64, 2, 2, 1, false, false, 4>(ctx, p, count, vec);
-            case 10: return launch_cfg<64, 64, 32, 2, 2, 2, false, false, 2>(ctx, p, count, vec);
-            default: return launch_cfg<128, 128, 16, 2, 2>(ctx, p, count, vec);
+            default: return launch_cfg<128, 128, 16, 2, 2, 4, false, false, 1, false, false>(ctx, p, count, vec);  // 6
         }
     }
 }
+
+// Waves per workgroup of the skinny kernel (K rows per workgroup = 64 x
+// waves).  8 measured best on MI355X: 16x4096x4096 15.9 us against 16.4 /
+// 15.9 at 4 / 16 waves, 16x8192x8192 51.5 against 57.3 / 53.1, 8x1024x768
+// 7.8 against 8.7 / 8.6.
+constexpr int kSkinnyWaves = 8;
 
 template <int MT, bool TA, int WAVES>
 void launch_skinny(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb, bool fused) {
@@ -1232,16 +1217,10 @@ void launch_skinny(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb
         hipLaunchKernelGGL((gemm_skinny_f32<MT, false, TA, false, WAVES>), grid, block, 0, ctx->stream, p);
 }
 
-// Waves per workgroup of the skinny kernel (K rows per workgroup = 64 x waves).
 template <bool TA>
-void launch_skinny_waves(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb, bool fused, int mt,
-                         int waves) {
-    if (mt == 1) {
-        if (waves == 16) return launch_skinny<1, TA, 16>(ctx, p, grid, vb, fused);
-        if (waves == 8) return launch_skinny<1, TA, 8>(ctx, p, grid, vb, fused);
-        return launch_skinny<1, TA, 4>(ctx, p, grid, vb, fused);
-    }
-    return launch_skinny<2, TA, 8>(ctx, p, grid, vb, fused);  // 32 rows x 16 float4 groups: 512 threads
+void launch_skinny_rows(lancius_hip_ctx* ctx, const GemmParams& p, dim3 grid, bool vb, bool fused, int mt) {
+    if (mt == 1) return launch_skinny<1, TA, kSkinnyWaves>(ctx, p, grid, vb, fused);
+    return launch_skinny<2, TA, kSkinnyWaves>(ctx, p, grid, vb, fused);  // 32 rows x 16 float4 groups: 512 threads
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15u) == 0; }
@@ -1277,20 +1256,47 @@ struct SplitStore {
 // The calling device's scratch; its address is resolved (and its counters
 // cleared by a kernel, not a memset, so a caller may capture the call) once
 // per device, with that device current (the caller has bound ctx->device).
+}  // namespace
+
+// Resolves the scratch's address on the context's device (which is
+// current) and clears its counters, once per device; lancius_hip_ctx_create
+// calls it, so a lancius_hip_gemm_f32_noalloc call, under stream capture
+// or not, never does more than read the cached address.  The clearing runs
+// on a private stream and is waited for here, outside any capture.
+int noalloc_scratch_init(lancius_hip_ctx* ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxScratchDevices) return 0;  // the entry point reports it
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[ctx->device]) return 0;
+    void* p = nullptr;
+    LANCIUS_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    LANCIUS_REQUIRE(p != nullptr, LANCIUS_HIP_ERR_INTERNAL, "gemm_f32_noalloc: no address for the scratch");
+    hipStream_t s = nullptr;
+    LANCIUS_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    hipLaunchKernelGGL(zero_words, dim3(16), dim3(256), 0, s, (unsigned*)((char*)p + kScratchPartialBytes),
+                       kScratchCounters);
+    hipError_t e = hipGetLastError();
+    const hipError_t e2 = hipStreamSynchronize(s);
+    const hipError_t e3 = hipStreamDestroy(s);
+    if (e == hipSuccess) e = e2 != hipSuccess ? e2 : e3;
+    if (e != hipSuccess) return from_hip(e, "noalloc scratch init");
+    g_scratch_ptr[ctx->device] = p;
+    return 0;
+}
+
+namespace {
+
 int noalloc_scratch(lancius_hip_ctx* ctx, SplitStore* out) {
     LANCIUS_REQUIRE(ctx->device >= 0 && ctx->device < kMaxScratchDevices, LANCIUS_HIP_ERR_UNSUPPORTED,
                     "gemm_f32_noalloc: device index %d beyond %d", ctx->device, kMaxScratchDevices);
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[ctx->device]) {
-        void* p = nullptr;
-        LANCIUS_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
-        LANCIUS_REQUIRE(p != nullptr, LANCIUS_HIP_ERR_INTERNAL, "gemm_f32_noalloc: no address for the scratch");
-        hipLaunchKernelGGL(zero_words, dim3(16), dim3(256), 0, ctx->stream,
-                           (unsigned*)((char*)p + kScratchPartialBytes), kScratchCounters);
-        if (int rc = check_launch("zero_words")) return rc;
-        g_scratch_ptr[ctx->device] = p;
+    void* p;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_ptr[ctx->device];
     }
-    out->partials = g_scratch_ptr[ctx->device];
+    LANCIUS_REQUIRE(p != nullptr, LANCIUS_HIP_ERR_INTERNAL,
+                    "gemm_f32_noalloc: the scratch of device %d was not set up by lancius_hip_ctx_create",
+                    ctx->device);
+    out->partials = p;
     out->partial_bytes = kScratchPartialBytes;
     out->counters = (unsigned*)((char*)out->partials + kScratchPartialBytes);
     out->n_counters = kScratchCounters;
@@ -1368,20 +1374,14 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     // M = 32 (16x4096x4096: 22 vs 34 us with the first skinny design;
     // 32x2048x120: 10.6 vs 13.6 us) and loses at M = 64 with four row tiles
     // (64x4096x4096: 43 vs 38 us; 64x784x256: 13.0 vs 11.8 us).
-    if (M <= 32 && !tb && tune("gemm_skinny", 1)) {
+    if (M <= 32 && !tb) {
         const int mt = M <= 16 ? 1 : 2;
-        // 8 waves (512-row K slices) measured best on MI355X: 16x4096x4096
-        // 15.9 us as 4 or 16 waves 16.4 / 15.9, 16x8192x8192 51.5 against
-        // 57.3 / 53.1, 8x1024x768 7.8 against 8.7 / 8.6
-        int waves = tune("gemm_skinny_waves", 8);
-        waves = mt == 2 ? 8 : waves >= 16 ? 16 : waves >= 8 ? 8 : 4;
-        const size_t splits = (K + 64 * waves - 1) / (64 * waves);
+        const size_t splits = (K + 64 * kSkinnyWaves - 1) / (64 * kSkinnyWaves);
         const size_t col_blocks = (N + 63) / 64;
         const size_t ws_bytes = splits > 1 ? count * splits * M * N * sizeof(float) : 0;
         if (ws_bytes <= kMaxSplitBytes && splits < 65536 && col_blocks < kMaxGridX) {
-            // the K slices are added inside the launch (see gemm_skinny_f32);
-            // LANCIUS_HIP_TUNE=gemm_skinny_fused=0 keeps the separate reduce
-            const bool fused = splits > 1 && tune("gemm_skinny_fused", 1);
+            // the K slices are added inside the launch (see gemm_skinny_f32)
+            const bool fused = splits > 1;
             if (splits > 1) {
                 void* ws = nullptr;
                 if (int rc = partials(ctx, fixed, ws_bytes, &ws)) return rc;
@@ -1392,32 +1392,18 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
             p.splits = (int)splits;
             const dim3 grid((unsigned)col_blocks, (unsigned)splits, (unsigned)count);
             if (ta)
-                launch_skinny_waves<true>(ctx, p, grid, vb, fused, mt, waves);
+                launch_skinny_rows<true>(ctx, p, grid, vb, fused, mt);
             else
-                launch_skinny_waves<false>(ctx, p, grid, vb, fused, mt, waves);
+                launch_skinny_rows<false>(ctx, p, grid, vb, fused, mt);
             if (int rc = check_launch("gemm_skinny_f32")) return rc;
-            if (splits > 1 && !fused) {
-                if (vb) {
-                    const size_t total4 = count * M * N / 4;
-                    hipLaunchKernelGGL(splitk_reduce_vec4,
-                                       dim3((unsigned)std::min<size_t>((total4 + 255) / 256, 4096)), dim3(256), 0,
-                                       ctx->stream, p, (int)count);
-                } else {
-                    const size_t total = count * M * N;
-                    hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)std::min<size_t>((total + 255) / 256, 4096)),
-                                       dim3(256), 0, ctx->stream, p, (int)count);
-                }
-                if (int rc = check_launch("splitk_reduce")) return rc;
-            }
             return ok();
         }
     }
 
-    // Configurations (BM x BN / BK, k-groups): 1 = 128x128/16, 2 = 64x64/16,
-    // 3 = 256x128/16, 4 = 128x128/32, 5 = 128x256/16, 6 = 128x128/16 built
-    // for 4 workgroups per CU, 7 = 128x128/32 x2, 8 = 128x128/32 x4,
-    // 9 = 64x64/64 x4, 10 = 64x64/32 x2.  Default by the number of 128x128
-    // tiles (one per CU fills the chip once), measured on MI355X:
+    // Configurations (BM x BN / BK, k-groups): 2 = 64x64/16, 6 = 128x128/16
+    // built for 4 workgroups per CU, 7 = 128x128/32 x2, 8 = 128x128/32 x4,
+    // 9 = 64x64/64 x4.  Chosen by the number of 128x128 tiles (one per CU
+    // fills the chip once), measured on MI355X:
     //  * >= 768: 6 (4096^3: 112 TFLOP/s);
     //  * 384 .. 767: 7 (two 8-wave workgroups per CU);
     //  * 256 .. 383: 8, 16 waves on the CU's one tile (2048^3: 205 -> 190
@@ -1430,33 +1416,27 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     const size_t big_tiles = count * ((M + 127) / 128) * ((N + 127) / 128);
     const size_t t64 = count * ((M + 63) / 64) * ((N + 63) / 64);
     const bool plain = !ta && !tb;
-    int cfg = tune("gemm_tile", 0);
-    if (cfg < 1 || cfg > 10 || ((ta || tb) && cfg != 2 && cfg != 6)) {
-        if (big_tiles >= 768)
-            cfg = 6;
-        else if (big_tiles >= 384)
-            cfg = plain ? 7 : 6;
-        else if (big_tiles >= 256)
-            cfg = plain ? 8 : 6;
-        else if (plain && K >= 2048 && big_tiles >= 16)
-            cfg = 7;
-        else if (plain && t64 >= 64)
-            cfg = 9;
-        else
-            cfg = 2;
-    }
-    const bool small = cfg == 2 || cfg == 9 || cfg == 10;
-    const size_t bm = small ? 64 : cfg == 3 ? 256 : 128;
-    const size_t bn = small ? 64 : cfg == 5 ? 256 : 128;
-    const size_t bk = cfg == 9 ? 64 : cfg == 4 || cfg == 7 || cfg == 8 || cfg == 10 ? 32 : kBK;
+    int cfg;
+    if (big_tiles >= 768)
+        cfg = 6;
+    else if (big_tiles >= 384)
+        cfg = plain ? 7 : 6;
+    else if (big_tiles >= 256)
+        cfg = plain ? 8 : 6;
+    else if (plain && K >= 2048 && big_tiles >= 16)
+        cfg = 7;
+    else if (plain && t64 >= 64)
+        cfg = 9;
+    else
+        cfg = 2;
+    const bool small = cfg == 2 || cfg == 9;
+    const size_t bm = small ? 64 : 128;
+    const size_t bn = bm;
+    const size_t bk = cfg == 9 ? 64 : cfg == 7 || cfg == 8 ? 32 : kBK;
     const size_t tiles = count * ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const size_t ktiles = (K + bk - 1) / bk;
-    size_t splits = (size_t)tune("gemm_split", 0);
-    if (splits == 0) {
-        splits = 1;
-        if (tiles < 256 && K >= 256)
-            splits = std::min<size_t>({(512 + tiles - 1) / tiles, K / 128, 16});
-    }
+    size_t splits = 1;
+    if (tiles < 256 && K >= 256) splits = std::min<size_t>({(512 + tiles - 1) / tiles, K / 128, 16});
     splits = std::max<size_t>(1, std::min(splits, ktiles));
     size_t chunk_tiles = (ktiles + splits - 1) / splits;
     splits = (ktiles + chunk_tiles - 1) / chunk_tiles;  // no empty K range
@@ -1468,29 +1448,22 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     p.splits = (int)splits;
     p.kchunk = (int)(chunk_tiles * bk);
     // 128x128 tiles loaded straight into LDS (gemm_f32_direct)
-    if (cfg == 6 && splits == 1 && vec && !ta && !tb && tune("gemm_direct", 1) &&
+    if (cfg == 6 && splits == 1 && vec && !ta && !tb &&
         M * K * sizeof(float) < ((size_t)1 << 31) && K * N * sizeof(float) < ((size_t)1 << 31)) {
         p.tiles_m = (uint32_t)((M + 127) / 128);
         p.tiles_n = (uint32_t)((N + 127) / 128);
         // the k-tile's four loads one after each of the first four MFMAs
         // (measured 143.0 -> 144.4 TFLOP/s at 4096^3; a burst before the
         // MFMAs, or one load per 2, 4 or 7 MFMAs, ran slower)
-        const int mix = tune("gemm_direct_mix", 1);
-        void (*kern)(const GemmParams) = mix == 1   ? gemm_f32_direct<4, 1>
-                                         : mix == 2 ? gemm_f32_direct<4, 2>
-                                         : mix == 4 ? gemm_f32_direct<4, 4>
-                                         : mix == 7 ? gemm_f32_direct<4, 7>
-                                                    : gemm_f32_direct<4, 0>;
-        hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256), 0, ctx->stream, p);
+        hipLaunchKernelGGL(gemm_f32_direct<4>, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256), 0, ctx->stream, p);
         if (int rc = check_launch("gemm_f32_direct")) return rc;
         return ok();
     }
     // Grids that give a CU about one 128 x 128 tile (or one 64 x 64 tile):
     // the direct-load pipeline with the K loop spread over k-groups of
     // 4 waves inside the workgroup (gemm_f32_direct_kg)
-    const int kgd = tune("gemm_direct_kg", 1);
-    if (kgd && vec && plain && M * K * sizeof(float) < ((size_t)1 << 31) &&
-        K * N * sizeof(float) < ((size_t)1 << 31) && K >= 256 && (big_tiles < 768 || kgd > 1)) {
+    if (vec && plain && M * K * sizeof(float) < ((size_t)1 << 31) && K * N * sizeof(float) < ((size_t)1 << 31) &&
+        K >= 256 && big_tiles < 768) {
         // 64 x 64 tiles, with 4 k-groups when that gives about one tile per
         // CU and 2 otherwise; 128 x 128 tiles (2 k-groups: 4 would leave 128
         // registers a wave and spill) for K >= 4096 with >= 192 of them.
@@ -1498,14 +1471,13 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         // 2048^3 146.0 -> 135.6, 4096x1024x1024 82.4 -> 71.3,
         // 1024x4096x1024 84.4 -> 76.4, 4096x4096x1024 275.2 -> 257.3,
         // 3000x1000x2000 145.8 -> 104.3.
-        const int bm_kg = tune("gemm_direct_kg_bm", K >= 4096 && big_tiles >= 192 ? 128 : 64);
-        const int kg = tune("gemm_direct_kg_groups", bm_kg == 128 || t64 > 384 ? 2 : 4);
+        const int bm_kg = K >= 4096 && big_tiles >= 192 ? 128 : 64;
+        const int kg = bm_kg == 128 || t64 > 384 ? 2 : 4;
         const size_t kg_tiles = count * ((M + bm_kg - 1) / bm_kg) * ((N + bm_kg - 1) / bm_kg);
-        if (kg_tiles >= 128 || kgd > 1) {
+        if (kg_tiles >= 128) {
             p.tiles_m = (uint32_t)((M + bm_kg - 1) / bm_kg);
             p.tiles_n = (uint32_t)((N + bm_kg - 1) / bm_kg);
-            void (*kern)(const GemmParams) = bm_kg == 128 ? (kg == 2 ? gemm_f32_direct_kg<128, 2>
-                                                                     : gemm_f32_direct_kg<128, 4>)
+            void (*kern)(const GemmParams) = bm_kg == 128 ? gemm_f32_direct_kg<128, 2>
                                                           : (kg == 2 ? gemm_f32_direct_kg<64, 2>
                                                                      : gemm_f32_direct_kg<64, 4>);
             hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256 * (kg == 2 ? 2 : 4)), 0,
@@ -1519,6 +1491,8 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         if (int rc = partials(ctx, fixed, count * splits * M * N * sizeof(float), &ws)) return rc;
         p.ws = (float*)ws;
     }
+    // plain configuration-6 operands beyond the direct kernel's offsets: scalar loads
+    if (cfg == 6 && plain) vec = false;
     int rc;
     if (ta && tb)
         rc = launch_by_cfg<true, true>(ctx, p, (int)count, vec, cfg);

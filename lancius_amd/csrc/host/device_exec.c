@@ -23,6 +23,7 @@ typedef enum {
 
 enum { ROLE_NONE = 0, ROLE_INPUT, ROLE_CONST, ROLE_POOLED, ROLE_ALIAS, ROLE_FUSED };
 enum { PACK_NONE = 0, PACK_I8, PACK_CONV };
+enum { PACK_FRESH = 0, PACK_STALE = 1, PACK_EXPOSED = 2 };
 
 typedef struct {
     uint32_t out;   /* node id written */
@@ -54,9 +55,10 @@ struct lancius_device_program {
     uint8_t* role;
     uint8_t* is_i8;  /* by id: INPUT holding int8 weights (1 byte per element) */
     /* by id: a weight's copy in the layout its kernel reads, what it is, its
-     * dimensions, and whether the weight changed since it was packed (set by
-     * uploads and by handing out the buffer; lancius_device_run re-packs
-     * first):
+     * dimensions, and whether it must be re-packed before the next run
+     * (PACK_STALE after an upload; PACK_EXPOSED once lancius_device_buffer
+     * handed out the weight's address, through which the caller may write
+     * at any time: re-packed before every run from then on):
      *   PACK_I8:   an int8 GEMM B [K, N] (lancius_hip_i8_pack_weight);
      *   PACK_CONV: an fp32 conv filter OIHW [C_out, C_in, K_h, K_w]
      *              (lancius_hip_conv2d_pack_weight) */
@@ -1087,6 +1089,8 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
             d[1] = L->d[2];
             bytes = lancius_hip_i8_packed_bytes(d[0], d[1]);
         } else if (L->kind == L_CONV && !L->i8 && L->d[1] % 16 == 0 && L->d[4] % 4 == 0 &&
+                   L->d[1] * L->d[2] * L->d[3] * sizeof(float) < LANCIUS_HIP_CONV_PACKED_MAX_BYTES &&
+                   L->d[4] * L->d[1] * L->d[5] * L->d[6] * sizeof(float) < LANCIUS_HIP_CONV_PACKED_MAX_BYTES &&
                    (p->role[w] == ROLE_INPUT || p->role[w] == ROLE_CONST)) {
             p->packed_kind[w] = PACK_CONV;
             d[0] = L->d[4];
@@ -1100,7 +1104,7 @@ int lancius_device_program_create(lancius_hip_ctx* ctx, const lancius_graph* g, 
         void* buf = NULL;
         rc = lancius_hip_malloc(ctx, &buf, bytes);
         p->packed[w] = (char*)buf;
-        p->packed_stale[w] = 1;
+        p->packed_stale[w] = PACK_STALE;
     }
     if (rc) goto out;
     rc = lancius_hip_synchronize(ctx);
@@ -1255,8 +1259,9 @@ static int run_all(lancius_device_program* prog) {
     return 0;
 }
 
-/* Re-lay every packed weight that changed since it was last packed, on the
- * caller's stream (after its uploads, before the launches). */
+/* Re-lay every packed weight that changed since it was last packed, or
+ * whose address the caller holds, on the caller's stream (after its
+ * uploads, before the launches). */
 static int repack_stale(lancius_device_program* prog) {
     for (uint32_t i = 0; i < prog->n_ids; i++) {
         if (!prog->packed_stale[i]) continue;
@@ -1267,7 +1272,7 @@ static int repack_stale(lancius_device_program* prog) {
                            : lancius_hip_conv2d_pack_weight(prog->ctx, (float*)prog->packed[i],
                                                             (const float*)prog->ptr[i], d[0], d[1], d[2], d[3]);
         if (rc) return rc;
-        prog->packed_stale[i] = 0;
+        if (prog->packed_stale[i] == PACK_STALE) prog->packed_stale[i] = PACK_FRESH;
     }
     return 0;
 }
@@ -1303,7 +1308,7 @@ int lancius_device_run(lancius_device_program* prog) {
 
 void* lancius_device_buffer(lancius_device_program* prog, const lancius_node* n) {
     if (!prog || !n || n->id >= prog->n_ids) return NULL;
-    if (prog->packed[n->id]) prog->packed_stale[n->id] = 1; /* the caller may write through it */
+    if (prog->packed[n->id]) prog->packed_stale[n->id] = PACK_EXPOSED; /* the caller may write through it */
     return prog->ptr[n->id];
 }
 
@@ -1313,7 +1318,8 @@ int lancius_device_upload(lancius_device_program* prog, const lancius_node* n, c
     if (n->id >= prog->n_ids || (prog->role[n->id] != ROLE_INPUT && prog->role[n->id] != ROLE_CONST))
         return LANCIUS_HIP_ERR_UNSUPPORTED;
     const size_t e = elems(n);
-    if (prog->packed[n->id]) prog->packed_stale[n->id] = 1; /* re-packed by the next run */
+    if (prog->packed[n->id] && prog->packed_stale[n->id] != PACK_EXPOSED)
+        prog->packed_stale[n->id] = PACK_STALE; /* re-packed by the next run */
     if (prog->is_i8[n->id]) { /* int8 weights take their int8 bytes */
         if (host_dtype != LANCIUS_DTYPE_INT8) return LANCIUS_HIP_ERR_DTYPE;
         return lancius_hip_upload(prog->ctx, prog->ptr[n->id], host, e);
@@ -1348,7 +1354,8 @@ int lancius_device_upload_weights(lancius_device_program* prog, const char* path
             rc = fail(LANCIUS_HIP_ERR_DTYPE, "int8 weight stored as floating point");
         } else {
             t[i].dst = prog->ptr[n->id];
-            if (prog->packed[n->id]) prog->packed_stale[n->id] = 1;
+            if (prog->packed[n->id] && prog->packed_stale[n->id] != PACK_EXPOSED)
+                prog->packed_stale[n->id] = PACK_STALE;
             t[i].dst_dtype = prog->is_i8[n->id] ? LANCIUS_HIP_FILE_I8 : LANCIUS_HIP_FILE_F32;
             t[i].file_dtype = r->file_dtype == LANCIUS_DTYPE_INT8   ? LANCIUS_HIP_FILE_I8
                               : r->file_dtype == LANCIUS_DTYPE_FP32 ? LANCIUS_HIP_FILE_F32

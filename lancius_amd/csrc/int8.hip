@@ -532,7 +532,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Par
 // and B^T [N][Kp]) and are loaded straight into LDS with 16-byte buffer
 // loads (LDS destination): k-tiles of 128 bytes, two static buffers, the
 // loads of tile kt + 2 issued from the last k-step of tile kt over SPREAD
-// k-steps (SPREAD 0: in one burst ahead of that step's MFMAs).  In LDS a row
+// k-steps (1 to 3).  In LDS a row
 // is 8 chunks of 16 bytes, chunk c stored at slot c ^ ((row >> 1) & 7): the
 // 16 rows one fragment read touches in a cycle fall on 16 distinct bank
 // groups.  Fragments of k-step s + 1 are read while the MFMAs of step s run.
@@ -541,6 +541,7 @@ __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Par
 // Requires (M + 1) * Kp and (N + 1) * Kp below 2^31 - 16.
 template <int SPREAD>
 __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
+    static_assert(SPREAD >= 1 && SPREAD <= 3, "loads spread over 1 to 3 k-steps");
     constexpr int BM = 256, BN = 256, BK = 128, TM = 4, TN = 4;
     constexpr int kTileBytes = BM * BK;  // one operand's k-tile (BM == BN)
     typedef __attribute__((address_space(3))) void lds_void;
@@ -594,11 +595,9 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (4 * (i - 8) + wave) * 1024), 16,
                                                          (int)(b_off[i - 8] + k0), 0, 0, 0);
         }
-        // keep the loads ahead of the MFMAs that follow
-        if (SPREAD == 0) __builtin_amdgcn_sched_barrier(0);
     };
-    // part q of SPREAD (SPREAD 0: one part) holds loads [lo(q), lo(q + 1))
-    constexpr int kParts = SPREAD > 0 ? SPREAD : 1;
+    // part q of SPREAD holds loads [lo(q), lo(q + 1))
+    constexpr int kParts = SPREAD;
     auto lo = [](int q) { return 16 * q / kParts; };
 
     // fragment addresses (bytes) at k-step 0; step s reads chunk 2s + lh
@@ -649,7 +648,7 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_direct(const I8Params p) {
         for (int i = 0; i < 16; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                     // MFMA
             if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);          // LDS read
-            if (SPREAD > 0 && (i + 1) * n / 16 > i * n / 16)
+            if ((i + 1) * n / 16 > i * n / 16)
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);                 // global load
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -824,30 +823,21 @@ int gemm_i8_core(lancius_hip_ctx* ctx, char* ws, float* C, const float* A, const
     p.N = (int)N;
     p.Kp = (int)Kp;
     p.act = act;
-    // 256 x 256 tiles when they still give every CU one (fewer bytes per
-    // MFMA), else 128 x 128 (more workgroups for small products)
-    const int big = tune("gemm_i8_big", ((M + 255) / 256) * ((N + 255) / 256) >= 240 ? 1 : 0);
-    const int bk = tune("gemm_i8_bk", 128);
+    // gemm_i8_direct (256 x 256 tiles, fewer bytes per MFMA) when they
+    // still give every CU one and both operands are under 2 GiB, else
+    // gemm_i8_mfma at 128 x 128 (more workgroups for small products; 64-bit
+    // addressing)
     const bool fits31 = (M + 1) * Kp < ((size_t)1 << 31) - 16 && (N + 1) * Kp < ((size_t)1 << 31) - 16;
+    const bool big = ((M + 255) / 256) * ((N + 255) / 256) >= 240 && fits31;
     const int BM = big ? 256 : 128, BN = BM;
     p.tiles_m = (uint32_t)((M + BM - 1) / BM);
     p.tiles_n = (uint32_t)((N + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;
     LANCIUS_REQUIRE(grid < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "gemm_i8: too many tiles");
-    // the k-tile loads of gemm_i8_direct spread over this many k-steps (0: in one burst)
-    const int spread = tune("gemm_i8_spread", 3);
-    if (big && bk == 128 && tune("gemm_i8_direct", 1) && fits31)
-        hipLaunchKernelGGL(spread == 0   ? gemm_i8_direct<0>
-                           : spread == 1 ? gemm_i8_direct<1>
-                           : spread == 2 ? gemm_i8_direct<2>
-                                         : gemm_i8_direct<3>,
-                           dim3((unsigned)grid), dim3(256), 0, ctx->stream, p);
-    else if (big && bk == 128)
-        hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 128, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,
-                           p);
-    else if (big)
-        hipLaunchKernelGGL((gemm_i8_mfma<256, 256, 2, 4, 64, false>), dim3((unsigned)grid), dim3(512), 0, ctx->stream,
-                           p);
+    // the k-tile loads of gemm_i8_direct spread over three k-steps
+    // (measured against one burst, one and two steps: kernel 67 -> 65 us)
+    if (big)
+        hipLaunchKernelGGL(gemm_i8_direct<3>, dim3((unsigned)grid), dim3(256), 0, ctx->stream, p);
     else
         hipLaunchKernelGGL((gemm_i8_mfma<128, 128, 2, 2, 128, false>), dim3((unsigned)grid), dim3(256), 0, ctx->stream,
                            p);
@@ -967,8 +957,7 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
                        (const float*)part, parts, scales, scale_w, (int)N, (int)C_in, HW, (int)Cp, tiles_p, tiles_c,
                        cw);
     if (int rc = check_launch("quantize_nchw_to_nhwc")) return rc;
-    constexpr int BM = 128;
-    const int BN = tune("conv_i8_bn", 64) == 128 ? 128 : 64;  // pixels per tile
+    constexpr int BM = 128, BN = 64;  // output channels x pixels per tile
     I8Params p{};
     p.C = out;
     p.A = wq;
@@ -998,12 +987,8 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     // 128 x 64 tiles, 4 workgroups per CU: the bench conv's 1568 tiles run
     // 40 us against 47 us for 784 tiles of 128 x 128 at 3 per CU (5 per CU
     // spilled and measured 41-43 us)
-    if (BN == 64)
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, 64, 2, 2, (int)BK, true, 4>), dim3((unsigned)grid), dim3(kThreads), 0,
-                           ctx->stream, p);
-    else
-        hipLaunchKernelGGL((gemm_i8_mfma<BM, 128, 2, 2, (int)BK, true, 3>), dim3((unsigned)grid), dim3(kThreads), 0,
-                           ctx->stream, p);
+    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, 2, 2, (int)BK, true, 4>), dim3((unsigned)grid), dim3(kThreads), 0,
+                       ctx->stream, p);
     return check_launch("conv2d_i8_mfma");
 }
 

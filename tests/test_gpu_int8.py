@@ -352,3 +352,32 @@ def test_int8_matmul_program_repacks_changed_weights(dev):
     prog.close()
     lib.lancius_schedule_destroy(sched)
     lib.lancius_graph_destroy(g)
+
+
+def test_int8_matmul_program_weight_pointer_kept(dev):
+    """The int8 weight's device address taken once, then written before
+    each of several runs: every write must reach the product, whose kernel
+    reads a packed copy of the weight."""
+    lib = graph_lib()
+    M, Kd, N = 96, 300, 130
+    g = lib.lancius_graph_create()
+    na, nb = lib.lancius_input(g, M, Kd), lib.lancius_input(g, Kd, N)
+    mm = lib.lancius_matmul(g, na, nb)
+    lib.lancius_graph_set_dtype(g, abi.DTYPE_FP32)
+    nb.contents.dtype = abi.DTYPE_INT8
+    nb.contents.scale = 0.004
+    sched = lib.lancius_ir_schedule(g)
+    case("int8 matmul program, weight written through a kept pointer")
+    prog = DeviceProgram(dev, g, sched)
+    a = prng.normal(98, (M, Kd))
+    prog.upload(na, a)
+    bptr = prog.buffer(nb)
+    for seed in (11, 12, 13):
+        bq = np.round(prng.uniform(200 + seed, (Kd, N), -127.4, 127.4)).astype(np.int8)
+        dev.write(bptr, bq)
+        prog.run()
+        got = prog.download(mm).reshape(M, N)
+        assert oracle.normwise_error(got, oracle.matmul_i8(f64(a), bq, 0.004)) <= TOL, seed
+    prog.close()
+    lib.lancius_schedule_destroy(sched)
+    lib.lancius_graph_destroy(g)

@@ -23,7 +23,7 @@ import pytest
 import oracle
 from lancius_amd import DEVICE_KEEP_ALL, DeviceProgram, HipError, abi, graph_lib, prng
 from lancius_amd.runtime import FileTensor
-from tests.conftest import case
+from tests.conftest import case, record_parity, top2_margin
 
 pytestmark = pytest.mark.gpu
 
@@ -87,6 +87,10 @@ def test_lenet_from_file_matches_onnx_and_reference(dev):
     res = run_mapped(dev, MODELS / "pytorch_lenet.lancius", feed=feed_lenet)
     prog, g = res[0], res[1]
     got = prog.download(lenet_io(g, res[2])[1]).ravel()
+    record_parity("LeNet (pytorch_lenet.lancius) logits vs ONNX Runtime", oracle.normwise_error(got, ONNX), TOL,
+                  argmax_exact=True, top2_margin_ref=top2_margin(ONNX), top2_margin_dev=top2_margin(got))
+    record_parity("LeNet (pytorch_lenet.lancius) logits vs the reference executor",
+                  oracle.normwise_error(got, K["lenet_logits"]), TOL, top2_margin_ref=top2_margin(K["lenet_logits"]))
     assert oracle.normwise_error(got, ONNX) <= TOL
     assert oracle.normwise_error(got, K["lenet_logits"]) <= TOL
     assert int(np.argmax(got)) == int(np.argmax(ONNX)) == 7

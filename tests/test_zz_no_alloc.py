@@ -88,3 +88,46 @@ def test_noalloc_gemm_refuses_beyond_scratch(dev):
     assert (dev.download(dC, (M, N)) == float(K)).all()
     for b in (dA, dB, dC):
         b.free()
+
+
+def test_noalloc_gemm_under_capture():
+    """The first no-alloc calls of a fresh context made inside a stream
+    capture: the recorded graph, replayed several times with eager work of
+    the same context between the replays, gives lancius_hip_gemm_f32's
+    output bit for bit on every replay (the scratch's address and its zeroed
+    counters come from context creation, not from the first call)."""
+    d = Device(0, own_stream=True)
+    shapes = [(16, 4096, 4096, ACT_RELU), (520, 1100, 500, ACT_GELU)]
+    bufs = []
+    for i, (M, K, N, act) in enumerate(shapes):
+        A, B = prng.normal(1700 + i, (M, K)), prng.normal(1800 + i, (K, N))
+        bias = prng.normal(1900 + i, (N,))
+        dA, dB, db = d.upload(A), d.upload(B), d.upload(bias)
+        c_ref, c_new = d.alloc(M * N * 4), d.alloc(M * N * 4)
+        d.gemm(c_ref, dA, dB, M, K, N, bias=db, act=act)
+        bufs.append((M, K, N, act, dA, dB, db, c_ref, c_new))
+    d.synchronize()
+    want = [d.download(b[7], (b[0], b[2])) for b in bufs]
+    case("gemm_f32_noalloc captured into a graph")
+    assert d.lib.lancius_hip_capture_begin(d.ctx) == 0, d.lib.lancius_hip_last_error()
+    rcs = [_noalloc(d, c_new, dA, dB, M, K, N, db, act) for (M, K, N, act, dA, dB, db, _, c_new) in bufs]
+    graph = C.c_void_p()
+    rc_end = d.lib.lancius_hip_capture_end(d.ctx, C.byref(graph))
+    assert rcs == [0, 0] and rc_end == 0, d.lib.lancius_hip_last_error()
+    for rep in range(3):
+        for (M, K, N, act, dA, dB, db, c_ref, c_new) in bufs:
+            d.fill(c_new, float("nan"), M * N)
+        # eager work of the same context between replays (its own split-K)
+        M, K, N, act, dA, dB, db, c_ref, _ = bufs[1]
+        d.gemm(c_ref, dA, dB, M, K, N, bias=db, act=act)
+        d.synchronize()
+        assert d.lib.lancius_hip_graph_launch(graph, d.ctx) == 0, d.lib.lancius_hip_last_error()
+        d.synchronize()
+        for j, b in enumerate(bufs):
+            got = d.download(b[8], (b[0], b[2]))
+            assert np.array_equal(got.view(np.uint32), want[j].view(np.uint32)), (rep, j)
+    d.lib.lancius_hip_graph_destroy(graph)
+    for b in bufs:
+        for buf in b[4:]:
+            buf.free()
+    d.close()
