@@ -175,6 +175,15 @@ LANCIUS_HIP_EXPORT int lancius_hip_attention_grouped_f32(lancius_hip_ctx* ctx, s
 LANCIUS_HIP_EXPORT int lancius_hip_layernorm_f32(lancius_hip_ctx* ctx, float* out, const float* in,
                                                  const float* gamma, const float* beta,
                                                  size_t rows, size_t hidden, float eps);
+/* `count` independent LayerNorms of one shape in one launch (the device
+ * executor's launch for the LAYERNORM nodes of one scheduler wave, which
+ * the reference runs one by one, lancius_scheduler.c:109-115); each member
+ * has its own out, in, gamma and beta (count <= LANCIUS_HIP_MAX_GROUP).
+ * Results equal lancius_hip_layernorm_f32's member by member. */
+LANCIUS_HIP_EXPORT int lancius_hip_layernorm_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* out,
+                                                         const float* const* in, const float* const* gamma,
+                                                         const float* const* beta, size_t rows, size_t hidden,
+                                                         float eps);
 
 /* Row softmax (max-subtracted, lancius_scheduler.c:284-294).  When argmax
  * is not NULL it receives int32 per row: the index of the first maximum of

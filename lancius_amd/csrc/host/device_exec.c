@@ -558,6 +558,7 @@ static int same_group(const launch_t* a, const launch_t* b) {
                a->has_bias == b->has_bias && a->has_res == b->has_res && a->ta == b->ta && a->tb == b->tb;
     if (a->kind == L_ATTN)
         return a->d[0] == b->d[0] && a->d[1] == b->d[1] && a->d[2] == b->d[2] && a->causal == b->causal;
+    if (a->kind == L_LN) return a->d[0] == b->d[0] && a->d[1] == b->d[1];
     return 0;
 }
 
@@ -1185,9 +1186,17 @@ static int run_launch(lancius_device_program* prog, const launch_t* L) {
                                                      L->d[6], L->d[7], L->d[8], L->act);
             return lancius_hip_conv2d_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), NULL, L->d[0], L->d[1], L->d[2],
                                           L->d[3], L->d[4], L->d[5], L->d[6], L->d[7], L->d[8], L->act);
-        case L_LN:
-            return lancius_hip_layernorm_f32(ctx, P(m->out), P(m->in[0]), P(m->in[1]), P(m->in[2]), L->d[0],
-                                             L->d[1], 1e-5f);
+        case L_LN: {
+            float* O[MAXG];
+            const float *X[MAXG], *G[MAXG], *Bt[MAXG];
+            for (uint32_t k = 0; k < L->count; k++) {
+                O[k] = P(L->m[k].out);
+                X[k] = P(L->m[k].in[0]);
+                G[k] = P(L->m[k].in[1]);
+                Bt[k] = P(L->m[k].in[2]);
+            }
+            return lancius_hip_layernorm_grouped_f32(ctx, L->count, O, X, G, Bt, L->d[0], L->d[1], 1e-5f);
+        }
         case L_SOFTMAX:
             return lancius_hip_softmax_f32(ctx, P(m->out), prog->argmax[m->out], P(m->in[0]), L->d[0], L->d[1]);
         case L_ADD:

@@ -43,15 +43,23 @@ __device__ __forceinline__ void load_row_f4(const float* __restrict__ x, int col
 // LayerNorm with the row in registers.  Statistics follow
 // bleeding/v11A1/src/math/lancius_kernels.c:217-236: mean, then the biased
 // variance of (x - mean), then (x - mean) * inv_std * g + b.
+// Member blockIdx.y of a group of LayerNorms of one shape.
+struct LnGroup {
+    float* out[LANCIUS_HIP_MAX_GROUP];
+    const float* in[LANCIUS_HIP_MAX_GROUP];
+    const float* gamma[LANCIUS_HIP_MAX_GROUP];
+    const float* beta[LANCIUS_HIP_MAX_GROUP];
+};
+
 template <int NV>
-__global__ void __launch_bounds__(kRowThreads) layernorm_regs(float* __restrict__ out, const float* __restrict__ in,
-                                                              const float* __restrict__ gamma,
-                                                              const float* __restrict__ beta, int rows, int H,
-                                                              float eps) {
+__global__ void __launch_bounds__(kRowThreads) layernorm_regs(const LnGroup grp, int rows, int H, float eps) {
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
-    const float* x = in + (size_t)row * H;
+    float* __restrict__ out = grp.out[blockIdx.y];
+    const float* __restrict__ gamma = grp.gamma[blockIdx.y];
+    const float* __restrict__ beta = grp.beta[blockIdx.y];
+    const float* x = grp.in[blockIdx.y] + (size_t)row * H;
     f32x4 v[NV];
     load_row_f4<NV>(x, H, lane, v);
     float s = 0.0f;
@@ -535,28 +543,49 @@ using namespace lancius;
 
 extern "C" {
 
-int lancius_hip_layernorm_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* gamma,
-                              const float* beta, size_t rows, size_t hidden, float eps) {
+int lancius_hip_layernorm_grouped_f32(lancius_hip_ctx* ctx, size_t count, float* const* out, const float* const* in,
+                                      const float* const* gamma, const float* const* beta, size_t rows, size_t hidden,
+                                      float eps) {
     LANCIUS_REQUIRE(ctx && out && in && gamma && beta, LANCIUS_HIP_ERR_NULL_PTR, "layernorm: NULL argument");
+    LANCIUS_REQUIRE(count >= 1 && count <= LANCIUS_HIP_MAX_GROUP, LANCIUS_HIP_ERR_SHAPE, "layernorm: group count %zu",
+                    count);
     LANCIUS_REQUIRE(hidden > 0 && hidden < (1u << 30) && rows < (1u << 30), LANCIUS_HIP_ERR_SHAPE,
                     "layernorm: rows=%zu hidden=%zu", rows, hidden);
+    LnGroup grp{};
+    bool aligned = true;
+    for (size_t g = 0; g < count; ++g) {
+        LANCIUS_REQUIRE(out[g] && in[g] && gamma[g] && beta[g], LANCIUS_HIP_ERR_NULL_PTR,
+                        "layernorm: NULL operand in group %zu", g);
+        grp.out[g] = out[g];
+        grp.in[g] = in[g];
+        grp.gamma[g] = gamma[g];
+        grp.beta[g] = beta[g];
+        aligned = aligned && aligned16(out[g]) && aligned16(in[g]) && aligned16(gamma[g]) && aligned16(beta[g]);
+    }
     if (rows == 0) return ok();
     if (int rc = bind_device(ctx)) return rc;
-    const dim3 grid(ceil_div(rows, kRowsPerBlock)), block(kRowThreads);
+    const dim3 grid(ceil_div(rows, kRowsPerBlock), (unsigned)count), block(kRowThreads);
     const int r = (int)rows, h = (int)hidden;
-    switch (regs_width(hidden, aligned16(out) && aligned16(in) && aligned16(gamma) && aligned16(beta))) {
-        case 1: hipLaunchKernelGGL(layernorm_regs<1>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
-        case 2: hipLaunchKernelGGL(layernorm_regs<2>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
-        case 4: hipLaunchKernelGGL(layernorm_regs<4>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
-        case 8: hipLaunchKernelGGL(layernorm_regs<8>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps); break;
-        case 16:
-            hipLaunchKernelGGL(layernorm_regs<16>, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps);
-            break;
-        default:
-            hipLaunchKernelGGL(layernorm_any, grid, block, 0, ctx->stream, out, in, gamma, beta, r, h, eps);
+    switch (regs_width(hidden, aligned)) {
+        case 1: hipLaunchKernelGGL(layernorm_regs<1>, grid, block, 0, ctx->stream, grp, r, h, eps); break;
+        case 2: hipLaunchKernelGGL(layernorm_regs<2>, grid, block, 0, ctx->stream, grp, r, h, eps); break;
+        case 4: hipLaunchKernelGGL(layernorm_regs<4>, grid, block, 0, ctx->stream, grp, r, h, eps); break;
+        case 8: hipLaunchKernelGGL(layernorm_regs<8>, grid, block, 0, ctx->stream, grp, r, h, eps); break;
+        case 16: hipLaunchKernelGGL(layernorm_regs<16>, grid, block, 0, ctx->stream, grp, r, h, eps); break;
+        default:  // rows that are not float4-shaped: one three-pass launch per member
+            for (size_t g = 0; g < count; ++g) {
+                hipLaunchKernelGGL(layernorm_any, dim3(grid.x), block, 0, ctx->stream, out[g], in[g], gamma[g], beta[g],
+                                   r, h, eps);
+                if (int rc = check_launch("layernorm")) return rc;
+            }
     }
     if (int rc = check_launch("layernorm")) return rc;
     return ok();
+}
+
+int lancius_hip_layernorm_f32(lancius_hip_ctx* ctx, float* out, const float* in, const float* gamma,
+                              const float* beta, size_t rows, size_t hidden, float eps) {
+    return lancius_hip_layernorm_grouped_f32(ctx, 1, &out, &in, &gamma, &beta, rows, hidden, eps);
 }
 
 int lancius_hip_softmax_f32(lancius_hip_ctx* ctx, float* probs, int32_t* argmax, const float* in, size_t rows,

@@ -80,6 +80,8 @@ def _declare_hip(lib: C.CDLL) -> C.CDLL:
     lib.lancius_hip_attention_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, sz, sz, i32, f32]
     lib.lancius_hip_attention_grouped_f32.argtypes = [vp, sz, vpp, vpp, vpp, vpp, sz, sz, sz, i32, f32]
     lib.lancius_hip_layernorm_f32.argtypes = [vp, vp, vp, vp, vp, sz, sz, f32]
+    lib.lancius_hip_layernorm_grouped_f32.argtypes = [vp, sz, C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
+                                                      C.POINTER(vp), sz, sz, f32]
     lib.lancius_hip_softmax_f32.argtypes = [vp, vp, vp, vp, sz, sz]
     lib.lancius_hip_mlp2_f32.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, vp, sz, sz, sz, sz, i32]
     lib.lancius_hip_mlp2_ex_f32.argtypes = [vp, vp, vp, vp, vp, vp, i32, vp, vp, i32, sz, sz, sz, sz, i32]
@@ -303,6 +305,10 @@ class Device:
     def layernorm(self, out, x, gamma, beta, rows, hidden, eps=1e-5) -> None:
         _check(self.lib.lancius_hip_layernorm_f32(self.ctx, _vp(out), _vp(x), _vp(gamma), _vp(beta), rows, hidden,
                                                   float(eps)))
+
+    def layernorm_grouped(self, outs, xs, gammas, betas, rows, hidden, eps=1e-5) -> None:
+        _check(self.lib.lancius_hip_layernorm_grouped_f32(self.ctx, len(outs), _ptrs(outs), _ptrs(xs), _ptrs(gammas),
+                                                          _ptrs(betas), rows, hidden, float(eps)))
 
     def softmax(self, probs, argmax, x, rows, cols) -> None:
         _check(self.lib.lancius_hip_softmax_f32(self.ctx, _vp(probs), _vp(argmax), _vp(x), rows, cols))

@@ -340,9 +340,9 @@ def test_block_small_golden(dev):
         got = prog.download(pl.bg.node(name))
         assert oracle.normwise_error(got, GO[f"block_out_{name}"]) <= oracle.tolerance(256), name
     info = prog.info()
-    # LN x2, QKV grouped (6 GEMMs), attention grouped, Wo grouped,
-    # LN x2, FFN1 grouped, FFN2 grouped
-    assert info["launches"] == 9, info
+    # LN grouped, QKV grouped (6 GEMMs), attention grouped, Wo grouped,
+    # LN grouped, FFN1 grouped, FFN2 grouped
+    assert info["launches"] == 7, info
     prog.close()
     pl.close()
 
@@ -382,7 +382,7 @@ def test_block_config_every_sequence(dev, noncausal):
     info = prog.info()
     prog.close()
     pl.close()
-    assert info["launches"] == 13, info
+    assert info["launches"] == 7, info
     for name, y in got.items():
         assert np.isfinite(y).all(), name
     one = Planned(graphs.build_block(lib, batch=1, noncausal=noncausal), plan=False)

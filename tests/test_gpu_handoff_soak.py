@@ -178,3 +178,4 @@ def test_soak_mlp_chain(dev, M, K1, N1, N2, act):
             b.free()
     for b in (out, am):
         b.free()
+

@@ -617,6 +617,28 @@ def test_layernorm(dev, rows, hidden):
     assert oracle.normwise_error(dev.download(do, x.shape), ref) <= oracle.tolerance(hidden)
 
 
+@pytest.mark.parametrize("rows,hidden", [(1024, 1024), (9, 1500), (5, 1001)])
+def test_layernorm_grouped(dev, rows, hidden):
+    """Three LayerNorms of one shape in one launch (the executor's launch
+    for one wave's LAYERNORM nodes), each with its own gamma and beta; equal
+    bit for bit to the single call, member by member (1001 columns: the
+    three-pass kernel once per member)."""
+    xs = [prng.normal(30 + j, (rows, hidden), mean=0.5, std=2.0) for j in range(3)]
+    gs = [prng.normal(40 + j, (hidden,), mean=1.0, std=0.1) for j in range(3)]
+    bs = [prng.normal(50 + j, (hidden,), std=0.1) for j in range(3)]
+    dx, dg, db = [dev.upload(a) for a in xs], [dev.upload(a) for a in gs], [dev.upload(a) for a in bs]
+    dos, d1 = [dev.alloc(4 * rows * hidden) for _ in range(3)], dev.alloc(4 * rows * hidden)
+    case(f"layernorm grouped x3 {rows}x{hidden}")
+    dev.layernorm_grouped(dos, dx, dg, db, rows, hidden)
+    for j in range(3):
+        got = dev.download(dos[j], (rows, hidden))
+        assert oracle.normwise_error(got, oracle.layernorm(xs[j], gs[j], bs[j])) <= oracle.tolerance(hidden)
+        dev.layernorm(d1, dx[j], dg[j], db[j], rows, hidden)
+        assert np.array_equal(got.view(np.uint32), dev.download(d1, (rows, hidden)).view(np.uint32))
+    for b in dx + dg + db + dos + [d1]:
+        b.free()
+
+
 def test_layernorm_constant_row_gives_beta(dev):
     x = np.full((4, 1024), 3.25, np.float32)
     g = prng.normal(1, (1024,))
