@@ -831,6 +831,9 @@ PROFILE_CASES = {
     "attn_s2048_causal": "SDPA B8 H16 D64 S2048 causal",
     "attn_s2048_noncausal": "SDPA B8 H16 D64 S2048 non-causal",
     "gemm_i8": "int8 GEMM 4096^3: quantize A + int8 product, weight packed once",
+    "conv_i8": "int8 conv 3x3 N32 64->128 56x56 + ReLU: quantize + implicit-GEMM int8 conv",
+    "gemm1024": "fp32 GEMM 1024^3",
+    "block": "transformer block B4 S1024 d1024 H16 F4096 forward through the device executor",
     "copy": "HBM copy probe (1 GiB read + 1 GiB written per launch)",
 }
 
@@ -857,6 +860,27 @@ def profile_case(dev, name: str, reps: int) -> float:
         t = time_steps(dev, lambda: dev.gemm_i8p(c, a, pk, 0.01, n, n, n), reps, 2)
         for buf in (a, b, c, pk):
             buf.free()
+        return t
+    if name == "conv_i8":
+        N, C_in, H, W, C_out = 32, 64, 56, 56, 128
+        x = dev.upload(prng.normal(45, (N, C_in, H, W)))
+        w = dev.upload(np.round(prng.uniform(145, (C_out, C_in, 3, 3), -127.4, 127.4)).astype(np.int8))
+        o = dev.alloc(N * C_out * H * W * 4)
+        t = time_steps(dev, lambda: dev.conv2d_i8(o, x, w, 0.001, None, N, C_in, H, W, C_out, 3, 3, 1, 1, 1), reps, 2)
+        for buf in (x, w, o):
+            buf.free()
+        return t
+    if name == "gemm1024":
+        return gemm_case(dev, 1024, 1024, 1024, 43, reps, 2)[0]
+    if name == "block":
+        bg = graphs.build_block(graph_lib())
+        feeds = {}
+        for i, nm in enumerate(bg.inputs):
+            shape = abi.node_shape(bg.node(nm))
+            feeds[nm] = (prng.normal(46 + 1000 * i, shape) if nm.startswith("x") else np.ones(shape, np.float32)
+                         if nm in ("g1", "g2") else prng.normal(46 + 1000 * i, shape, 0, 0.02))
+        t, _ = graph_case(dev, bg, feeds, reps, 2)
+        bg.destroy()
         return t
     S = 512 if "s512" in name else 2048
     return attention_case(dev, 8, S, 16, 64, name.endswith("_causal"), 44, reps, 2)[0]

@@ -647,11 +647,13 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
 // waves on its tile instead of 4.  At the end the groups' sums are added
 // through LDS in the fixed order (g0 + g1) + (g2 + g3) and group 0 runs the
 // epilogue: results are run-to-run identical.
-template <int BM, int KG>
+template <int BM, int KG, int BK = 16>
 __global__ void __launch_bounds__(256 * KG, 1) gemm_f32_direct_kg(const GemmParams p) {
-    constexpr int BN = BM, BK = 16;
+    constexpr int BN = BM;
+    static_assert(BK == 16 || BK == 32, "k-tile");
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
-    constexpr int AI = BM / 64, BI = BN / 64;  // 16-byte loads per wave per k-tile
+    constexpr int AI = BM * BK / 1024, BI = BN * BK / 1024;  // 16-byte loads per wave per k-tile
+    constexpr int ACH = BK / 4;                                // 16-byte chunks of an A row
     constexpr int ASZ = BM * BK, BSZ = BK * BN;
     constexpr int STAGE = KG * 2 * (ASZ + BSZ);
     constexpr int RED = (KG > 2 ? 2 : 1) * BM * BN;  // partial tiles in LDS at once
@@ -688,20 +690,26 @@ __global__ void __launch_bounds__(256 * KG, 1) gemm_f32_direct_kg(const GemmPara
     constexpr int kOut = 0x7ffffff0;  // an offset past the end of any operand: the load returns 0
 
     // A chunks: instruction i of wave gw fills chunks (AI gw + i) * 64 + lane
-    // (row q >> 2, chunk (q & 3) ^ ((row >> 2) & 3)); B chunks likewise
-    // (row q / (BN / 4), chunk swizzled by 8 ((row >> 3) & 1)).
+    // (row q / ACH, chunk (q % ACH) ^ aswz(row)); B chunks likewise (row
+    // q / (BN / 4), chunk swizzled by 8 for the rows the second lane half
+    // reads).  With BK = 16 a row is 4 chunks (4 rows per 256 bytes of
+    // banks) and aswz(r) = (r >> 2) & 3; with BK = 32 it is 8 chunks (2 rows
+    // per 256 bytes) and aswz(r) = (r >> 1) & 7: either way the 16-byte
+    // reads of 16 consecutive rows at one chunk hit 16 different bank groups.
+    auto aswz = [](int row) { return BK == 16 ? (row >> 2) & 3 : (row >> 1) & 7; };
+    constexpr int BHALF = BK / 2;  // B row of the second lane half's first k
     int a_k[AI], a_off0[AI], b_kr[BI], b_off0[BI];
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
         const int q = (AI * gw + i) * 64 + lane;
-        const int row = q >> 2, c = (q & 3) ^ ((row >> 2) & 3);
+        const int row = q / ACH, c = (q % ACH) ^ aswz(row);
         a_k[i] = 4 * c;
         a_off0[i] = (min(m0 + row, M - 1) * K + 4 * c) * (int)sizeof(float);
     }
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
         const int q = (BI * gw + i) * 64 + lane;
-        const int kr = q / (BN / 4), lc = (q % (BN / 4)) ^ (((kr >> 3) & 1) << 3);
+        const int kr = q / (BN / 4), lc = (q % (BN / 4)) ^ (((kr / BHALF) & 1) << 3);
         b_kr[i] = kr;
         b_off0[i] = (kr * N + min(n0 + 4 * lc, N - 4)) * (int)sizeof(float);
     }
@@ -727,29 +735,32 @@ __global__ void __launch_bounds__(256 * KG, 1) gemm_f32_direct_kg(const GemmPara
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    int a_rd[TM][2];
+    // lane half lk of the MFMAs takes k in [lk BK/2, (lk + 1) BK/2) of the
+    // k-tile (A chunks lk BK/8 .., B rows lk BK/2 ..)
+    constexpr int AH = BK / 8;  // A chunks per lane half
+    int a_rd[TM][AH];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int row = wm * WM + i * 32 + lr, c = 2 * lk + h;
-            a_rd[i][h] = row * BK + 4 * (c ^ ((row >> 2) & 3));
+        for (int h = 0; h < AH; ++h) {
+            const int row = wm * WM + i * 32 + lr, c = AH * lk + h;
+            a_rd[i][h] = row * BK + 4 * (c ^ aswz(row));
         }
     int b_rd[TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int n = wn * WN + j * 32 + lr;
-        b_rd[j] = 8 * lk * BN + 4 * ((n >> 2) ^ (lk << 3)) + (n & 3);
+        b_rd[j] = BHALF * lk * BN + 4 * ((n >> 2) ^ (lk << 3)) + (n & 3);
     }
     // one global load after each of the k-tile's first MFMAs
     auto compute = [&](const float* As, const float* Bs) {
-        f32x4 av[TM][2];
+        f32x4 av[TM][AH];
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int h = 0; h < 2; ++h) av[i][h] = *(const f32x4*)(As + a_rd[i][h]);
+            for (int h = 0; h < AH; ++h) av[i][h] = *(const f32x4*)(As + a_rd[i][h]);
 #pragma unroll
-        for (int kp = 0; kp < 8; ++kp) {
+        for (int kp = 0; kp < BK / 2; ++kp) {
             float bf[TN];
 #pragma unroll
             for (int j = 0; j < TN; ++j) bf[j] = Bs[b_rd[j] + kp * BN];
@@ -764,7 +775,7 @@ __global__ void __launch_bounds__(256 * KG, 1) gemm_f32_direct_kg(const GemmPara
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * 8 - (AI + BI), 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN * BK / 2 - (AI + BI), 0);
         __builtin_amdgcn_sched_barrier(0);
     };
 
@@ -1477,9 +1488,12 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         if (kg_tiles >= 128) {
             p.tiles_m = (uint32_t)((M + bm_kg - 1) / bm_kg);
             p.tiles_n = (uint32_t)((N + bm_kg - 1) / bm_kg);
-            void (*kern)(const GemmParams) = bm_kg == 128 ? gemm_f32_direct_kg<128, 2>
-                                                          : (kg == 2 ? gemm_f32_direct_kg<64, 2>
-                                                                     : gemm_f32_direct_kg<64, 4>);
+            // 128 x 128 tiles take k-tiles of 32 (half the barriers per k):
+            // 1024x4096x1024 77.4 -> 70.0 us, four of them grouped 259.5 ->
+            // 257.5 us; the 64 x 64 tiles measured no better with 32
+            // (1024^3 23.9 -> 24.3 us, four grouped 72.1 -> 72.7 us)
+            void (*kern)(const GemmParams) = bm_kg == 128 ? gemm_f32_direct_kg<128, 2, 32>
+                                                          : (kg == 2 ? gemm_f32_direct_kg<64, 2> : gemm_f32_direct_kg<64, 4>);
             hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256 * (kg == 2 ? 2 : 4)), 0,
                                ctx->stream, p);
             if (int rc = check_launch("gemm_f32_direct_kg")) return rc;
