@@ -219,3 +219,39 @@ def test_device_ceiling_probes(dev, which, low):
     read in GB/s) run and report a plausible rate."""
     case(f"peak probe {which}")
     assert dev.peak_probe(which) > low
+
+
+def test_conv_input_beyond_2gib(dev):
+    """An input over 2 GiB (1040 images of 64 x 90 x 90): the conv runs as
+    launches over runs of whole images under 2 GiB each (the direct kernel's
+    32-bit offsets), 1035 images and then 5.  Images on both sides of the
+    split carry random data and are checked against the oracle; the rest
+    hold a constant, and every output must be finite."""
+    N, C_in, H, W, C_out = 1040, 64, 90, 90, 64
+    img = C_in * H * W
+    assert N * img * 4 >= 1 << 31
+    per = ((1 << 31) - 65) // (img * 4)
+    sample = [0, per - 1, per, N - 1]
+    w = prng.normal(2100, (C_out, C_in, 3, 3), 0, float(np.sqrt(2.0 / (9 * C_in))))
+    dx, dw, do = dev.alloc(4 * N * img), _up(dev, w), dev.alloc(4 * N * C_out * H * W)
+    dev.fill(dx, 0.25, N * img)
+    dev.fill(do, float("nan"), N * C_out * H * W)
+    xs = {}
+    for i, n in enumerate(sample):
+        xs[n] = prng.normal(2110 + i, (1, C_in, H, W))
+        dev.write(int(dx) + 4 * n * img, np.ascontiguousarray(xs[n], np.float32))
+    case(f"conv input beyond 2 GiB: N={N} C_in={C_in} {H}x{W} C_out={C_out}")
+    dev.conv2d(do, dx, dw, None, N, C_in, H, W, C_out, 3, 3, 1, 1, act=ACT_RELU)
+    dev.synchronize()
+    for n in sample:
+        got = dev.download(int(do) + 4 * n * C_out * H * W, (1, C_out, H, W))
+        ref = oracle.conv2d(xs[n], w, 1, 1, True)
+        assert oracle.normwise_error(got, ref) <= oracle.tolerance(9 * C_in), n
+    # a constant image's interior is the filter sum times the constant (ReLU of it)
+    mid = dev.download(int(do) + 4 * (N // 2) * C_out * H * W, (C_out, H, W))
+    want = np.maximum(0.25 * w.astype(np.float32).astype(np.float64).sum(axis=(1, 2, 3)), 0.0)
+    assert np.allclose(mid[:, 1:-1, 1:-1], want[:, None, None], rtol=1e-5, atol=1e-6)
+    big = dev.download(do, (N * C_out * H * W,))
+    assert np.isfinite(big).all()
+    for b in (dx, dw, do):
+        b.free()
