@@ -526,6 +526,247 @@ __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Par
     }
 }
 
+// The int8 conv as a loop over output pixels with the filter resident in
+// LDS.  A workgroup holds ROWS = 32 TM output channels of the filter
+// ([ROWS][Kp] int8; the LDS row stride, ldw bytes, is an odd number of
+// 16-byte chunks, so the 16-byte fragment reads of 8 consecutive rows fall
+// on distinct bank groups) for the whole launch.  Each wave takes tiles of
+// 32 consecutive output pixels, all ROWS channels (TM accumulators of
+// 32 x 32), and gathers its pixel operands straight from the NHWC int8
+// activation into registers: one 16-byte buffer load per lane per k-step
+// (lane half h: k bytes [32 ks + 16 h, +16) = 16 channels of one tap at the
+// lane's pixel), kConvI8Ring k-steps ahead; taps outside the image, and k
+// past the filter's KHW * Cp, load from an offset past the buffer's end
+// (zeros).  After the prologue the filter is read-only, so the k loop has
+// no barrier.  Workgroup b serves output-channel block b % co_blocks; a
+// block's pixel tiles are dealt 4 consecutive tiles per workgroup (the
+// tiles share input rows in the CU's L1), then in strides of all its
+// workgroups.  The epilogue is gemm_i8_mfma's (fp64 scale, fp32 result,
+// bias, activation, NCHW store), so both kernels give the same bits.
+// Requires Kp % (32 kConvI8Ring) == 0, Kp <= kConvI8MaxKp, ROWS * ldw + 32 <= kConvI8Lds, KHW <= 64
+// and the activation under 2 GiB - 64 (b_bytes: its size; the past-the-end
+// offset lies beyond it).
+constexpr int kConvI8Lds = 78848;
+constexpr int kConvI8Threads = 512;  // 8 waves, one workgroup per CU
+constexpr int kConvI8Ring = 3;
+constexpr int kConvI8MaxKp = 2400;  // whole rings; 32 rows of it fit kConvI8Lds
+constexpr int kConvI8KtPad = 2 * kConvI8Ring + 2;
+
+template <int TM, int TN>
+__global__ void __launch_bounds__(kConvI8Threads, 2) conv_i8_direct(const I8Params p, int co_blocks, int ldw,
+                                                                     int b_bytes) {
+    constexpr int ROWS = 32 * TM, PX = 32 * TN, NT = kConvI8Threads, NW = NT / 64;
+    __shared__ __attribute__((aligned(16))) int8_t wl[kConvI8Lds];
+    __shared__ __attribute__((aligned(16))) float bl[ROWS];
+    __shared__ int2 kt[kConvI8MaxKp / 16 + kConvI8KtPad];
+    const int cb = (int)blockIdx.x % co_blocks;
+    const int wg = (int)blockIdx.x / co_blocks, wgs = (int)gridDim.x / co_blocks;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lr = lane & 31, lh = lane >> 5;
+    const int Kp = p.Kp, chunks = Kp / 16;
+
+    // k-step s, lane half h: k = 32 s + 16 h is channel c of tap (kh, kw);
+    // kt[2 s + h] = (tap, input offset of the tap and channel relative to
+    // the pixel's top-left tap), tap 64 for k past the filter (the table
+    // runs a ring and one entry past Kp: the loads issued ahead of the
+    // loop's end)
+    for (int i = tid; i < Kp / 16 + kConvI8KtPad; i += NT) {
+        const int k = 16 * i, tap = k / p.Cp, c = k - tap * p.Cp;
+        const int kh = tap / p.KW, kw = tap - kh * p.KW;
+        kt[i] = int2{tap < p.KHW ? tap : 64, (kh * p.W + kw) * p.Cp + c};
+    }
+    for (int r = tid; r < ROWS; r += NT) bl[r] = p.bias && cb * ROWS + r < p.M ? p.bias[cb * ROWS + r] : 0.0f;
+    __syncthreads();
+
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(p.B), 0, b_bytes, kBufferRsrcWord3);
+    constexpr int kOut = 0x7ffffff0;
+    const int KH = p.KHW / p.KW;
+    const int ksteps = Kp / 32;
+    const int tiles = (p.N - 1) / PX + 1;
+
+    // The current tile: PX output pixels from t * PX; B fragment j holds
+    // pixel t * PX + 32 j + l%32 of this lane (pv: it exists), with its
+    // image, offset in the image's plane, the input offset of its top-left
+    // tap (base) and which taps lie inside the image (bit tap of inside).
+    // ls / e walk the k-step table one load ahead.  A workgroup takes an
+    // equal share of consecutive tiles (its waves share input rows in L1),
+    // dealt to the waves one per SIMD first (waves w and w + 4 share a
+    // SIMD).
+    const int t_end = (int)((long long)(wg + 1) * tiles / wgs);
+    const int slot = (wave & 3) * 2 + (wave >> 2);
+    int t = (int)((long long)wg * tiles / wgs) + slot;
+    bool pv[TN];
+    int img[TN], pix[TN], base[TN];
+    uint64_t inside[TN];
+    int ls = 0;
+    int2 e = int2{64, 0};
+    auto setup = [&]() {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int P = t * PX + 32 * j + lr;
+            pv[j] = P < p.N;
+            img[j] = pix[j] = 0;
+            int hi0 = 0, wi0 = 0;
+            if (pv[j]) {
+                img[j] = P / p.HWo;
+                pix[j] = P - img[j] * p.HWo;
+                const int ho = pix[j] / p.Wo, wo = pix[j] - (pix[j] / p.Wo) * p.Wo;
+                hi0 = ho * p.stride - p.pad;
+                wi0 = wo * p.stride - p.pad;
+            }
+            uint64_t in_mask = 0;
+            for (int kh = 0, tap = 0; kh < KH; ++kh)
+                for (int kw = 0; kw < p.KW; ++kw, ++tap) {
+                    const bool in = pv[j] && hi0 + kh >= 0 && hi0 + kh < p.H && wi0 + kw >= 0 && wi0 + kw < p.W;
+                    in_mask |= (uint64_t)in << tap;
+                }
+            inside[j] = in_mask;
+            base[j] = ((img[j] * p.H + hi0) * p.W + wi0) * p.Cp;
+        }
+        ls = 0;
+        e = kt[lh];
+    };
+    v4i bq[kConvI8Ring][TN];
+    auto next_loads = [&](v4i* dst) {
+        const int2 cur = e;
+        e = kt[2 * ++ls + lh];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const bool in = (inside[j] >> (cur.x & 63)) & (uint64_t)(cur.x < 64);
+            const int off = pick(in, base[j] + cur.y, kOut);
+            dst[j] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+        }
+    };
+    // the first ring of loads, issued in slot order as the loop issues them
+    // (so the wait counts at the loop head agree on every edge)
+    auto prime = [&]() {
+#pragma unroll
+        for (int u = 0; u < kConvI8Ring; ++u) {
+            next_loads(bq[u]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    if (t < t_end) {
+        setup();
+        prime();
+    }
+
+    // The filter block into LDS while the first tile's loads are in flight:
+    // TPR threads per row, each taking every TPR-th 16-byte chunk, 10 loads
+    // in flight at a time (every workgroup reads the same block: loads
+    // issued one at a time made this a chain of L2 round trips).
+    {
+        constexpr int TPR = NT / ROWS;
+        const int r = tid / TPR, co = cb * ROWS + r;
+        const int8_t* src = p.A + (size_t)min(co, p.M - 1) * Kp;
+        for (int c0 = tid % TPR; c0 < chunks; c0 += 10 * TPR) {
+            v4i v[10];
+#pragma unroll
+            for (int j = 0; j < 10; ++j) {
+                const int c = c0 + j * TPR;
+                v[j] = c < chunks && co < p.M ? *(const v4i*)(src + 16 * c) : v4i{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int j = 0; j < 10; ++j) {
+                const int c = c0 + j * TPR;
+                if (c < chunks) *(v4i*)(wl + r * ldw + 16 * c) = v[j];
+            }
+        }
+    }
+    __syncthreads();
+
+    const double scale = p.scale_a[0] * p.scale_b[0];
+    const int8_t* const a_lane = wl + lr * ldw + 16 * lh;
+    while (t < t_end) {
+        v16i acc[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+        // the filter fragments of k-step s + 1 are read while the MFMAs of
+        // step s run (past the last step: padding inside the LDS array)
+        v4i a[TM];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) a[i] = *(const v4i*)(a_lane + i * 32 * ldw);
+        for (int ks = 0; ks < ksteps; ks += kConvI8Ring) {
+#pragma unroll
+            for (int u = 0; u < kConvI8Ring; ++u) {
+                v4i an[TM];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) an[i] = *(const v4i*)(a_lane + i * 32 * ldw + 32 * (ks + u + 1));
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bq[u][j], acc[i][j], 0, 0, 0);
+                // refill the slot with k-step ks + u + ring (past the last
+                // k-step the table says tap 64: zero loads, never used)
+                next_loads(bq[u]);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) a[i] = an[i];
+                // next step's fragment reads first, then the MFMAs, then the loads
+                __builtin_amdgcn_sched_group_barrier(0x100, TM + 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+                __builtin_amdgcn_sched_group_barrier(0x020, TN, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+
+        // The next tile's first loads go out before this tile's stores: a
+        // wave's loads and stores retire in issue order, so loads issued
+        // after the stores would wait for all of them.
+        bool out_pv[TN];
+        int out_img[TN], out_pix[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            out_pv[j] = pv[j];
+            out_img[j] = img[j];
+            out_pix[j] = pix[j];
+        }
+        t += NW;
+        if (t < t_end) {
+            setup();
+            prime();
+        }
+
+        // register r of accumulator (i, j), lane l: channel 8(4i + r/4) +
+        // 4(l/32) + r%4 of the block, pixel 32 j + l%32 of the tile.  The row
+        // pointer steps 8 rows per register quad (no per-row offsets stay
+        // live across tiles), a quad's four biases are one LDS read, and
+        // blocks wholly inside C_out store without a per-row check (the
+        // int8 conv takes no activation but ReLU).
+        const size_t hw = (size_t)p.HWo;
+        const bool relu = p.act == kActRelu;
+        const bool full = (cb + 1) * ROWS <= p.M;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            if (!out_pv[j]) continue;
+            float* o = p.C + ((size_t)out_img[j] * p.out_channels + cb * ROWS + 4 * lh) * hw + out_pix[j];
+            auto quad = [&](int g, bool check) {
+                const f32x4 bv = *(const f32x4*)(bl + 8 * g + 4 * lh);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    float v = (float)((double)acc[g >> 2][j][4 * (g & 3) + s] * scale) + bv[s];
+                    v = relu ? relu_ref(v) : v;
+                    if (!check || cb * ROWS + 8 * g + 4 * lh + s < p.M) o[s * hw] = v;
+                }
+                o += 8 * hw;
+            };
+            if (full) {
+#pragma unroll
+                for (int g = 0; g < 4 * TM; ++g) quad(g, false);
+            } else {
+#pragma unroll
+                for (int g = 0; g < 4 * TM; ++g) quad(g, true);
+            }
+        }
+    }
+}
+
 // GEMM only: 256 x 256 tiles, one workgroup of 4 waves per CU, each wave
 // a 128 x 128 block (16 accumulators of 32 x 32, so every 16-byte fragment
 // read from LDS feeds 4 MFMAs).  Both operands are k-contiguous ([M][Kp]
@@ -917,13 +1158,20 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
                     "conv2d_i8: activation %d", act);
     const size_t Cp = align_up(C_in, 16);
     const size_t KHW = K_h * K_w;
-    // k-tiles of 64 (k padded to 64, not 128) at 3 waves per SIMD: 40 KB of
-    // LDS and <= 168 VGPRs per 128 x 128 workgroup, 3 per CU.  The bench
-    // conv's 784 tiles then take one round plus 16 tiles instead of 1.5
-    // rounds at 2 per CU (k-tiles of 128): 55.0 -> 51.3 us per call.  4 per
-    // CU (one round) needs <= 128 VGPRs and spilled: 85 us.
+    // conv_i8_direct when a block of at least 32 output channels of the
+    // filter fits its LDS: TM = 4, 2 or 1 accumulators per wave (128, 64 or
+    // 32 channels per workgroup), k padded to whole rings of k-steps.
+    // Otherwise the LDS-staged implicit GEMM (gemm_i8_mfma, k-tiles of 64).
+    const size_t xq_bytes = N * H * W * Cp;
+    const size_t Kp_d = align_up(KHW * Cp, 32 * kConvI8Ring);
+    const size_t ldw = Kp_d + ((Kp_d / 16) % 2 == 0 ? 16 : 0);
+    int tm = C_out > 64 ? 4 : C_out > 32 ? 2 : 1;
+    // (+32: the fragment reads one k-step past the end stay in the array)
+    while (tm > 1 && 32 * tm * ldw + 32 > (size_t)kConvI8Lds) tm /= 2;
+    const bool direct = 32 * tm * ldw + 32 <= (size_t)kConvI8Lds && Kp_d <= (size_t)kConvI8MaxKp && KHW <= 64 &&
+                        xq_bytes < (size_t)0x7fffffc0;
     constexpr size_t BK = 64;
-    const size_t Kp = align_up(KHW * Cp, BK);
+    const size_t Kp = direct ? Kp_d : align_up(KHW * Cp, BK);
     const size_t Ho = (H + 2 * pad - K_h) / stride + 1, Wo = (W + 2 * pad - K_w) / stride + 1;
     const size_t P = N * Ho * Wo;
     LANCIUS_REQUIRE(Kp < (1u << 30) && P < (1u << 31) && N * H * W * Cp < ((size_t)1 << 40) && C_out < (1u << 30),
@@ -980,6 +1228,22 @@ int lancius_hip_conv2d_i8_f32(lancius_hip_ctx* ctx, float* out, const float* in,
     p.Wo = (int)Wo;
     p.HWo = (int)(Ho * Wo);
     p.out_channels = (int)C_out;
+    if (direct) {
+        // one workgroup per CU over the channel blocks (8 waves, each at
+        // least one pixel tile of 32).  Tiles of 32 pixels (one B fragment
+        // per k-step) measured 34.0 us per bench call against 35.0 for 64
+        // (two fragments, half the filter reads per MFMA, fewer tiles to
+        // overlap the stores of one with the MFMAs of the next).
+        const int rows = 32 * tm;
+        const size_t co_blocks = (C_out + rows - 1) / rows, tiles = (P + 31) / 32;
+        const size_t wgs = std::max<size_t>(1, std::min<size_t>((tiles + 7) / 8, (size_t)cu_count(ctx) / co_blocks));
+        LANCIUS_REQUIRE(co_blocks * wgs < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "conv2d_i8: too many channel blocks");
+        void (*kern)(const I8Params, int, int, int) =
+            tm == 4 ? conv_i8_direct<4, 1> : tm == 2 ? conv_i8_direct<2, 1> : conv_i8_direct<1, 1>;
+        hipLaunchKernelGGL(kern, dim3((unsigned)(co_blocks * wgs)), dim3(kConvI8Threads), 0, ctx->stream, p, (int)co_blocks,
+                           (int)ldw, (int)xq_bytes);
+        return check_launch("conv_i8_direct");
+    }
     p.tiles_m = (uint32_t)((C_out + BM - 1) / BM);
     p.tiles_n = (uint32_t)((P + BN - 1) / BN);
     const size_t grid = (size_t)p.tiles_m * p.tiles_n;

@@ -211,7 +211,9 @@ def test_conv_i8_golden(dev):
 
 @pytest.mark.parametrize("shape", [(2, 3, 32, 32, 16, 5, 5, 1, 2), (4, 16, 16, 16, 32, 5, 5, 1, 2),
                                    (2, 64, 28, 28, 128, 3, 3, 1, 1), (1, 20, 13, 11, 7, 3, 3, 2, 0),
-                                   (3, 8, 9, 9, 5, 1, 1, 1, 0), (1, 130, 7, 7, 33, 3, 3, 1, 1)])
+                                   (3, 8, 9, 9, 5, 1, 1, 1, 0), (1, 130, 7, 7, 33, 3, 3, 1, 1),
+                                   # filter too large for the LDS-resident kernel: the staged implicit GEMM
+                                   (1, 300, 9, 9, 40, 3, 3, 1, 1)])
 def test_conv_i8_shapes(dev, shape):
     N, Ci, H, W, Co, KH, KW, st, pd = shape
     x = prng.normal(100 + sum(shape), (N, Ci, H, W))
@@ -247,6 +249,53 @@ def test_conv_i8_bench_shape_bit_exact(dev):
             acc += xp[:, kh:kh + H, kw:kw + W, :].reshape(-1, Ci) @ wq[:, :, kh, kw].astype(np.float64).T
     ref = (acc * (sw * sx)).astype(np.float32).reshape(N, H, W, Co).transpose(0, 3, 1, 2)
     np.testing.assert_array_equal(got, ref)
+
+
+def _conv_i8_exact(x, wq, sw, stride, pad, bias=None, relu=False):
+    """The exact int8 conv: integer sums over the quantized operands (exact
+    in float64), times scale_w * scale_x in fp64, rounded once to fp32, then
+    the fp32 bias add and ReLU of the kernel's epilogue."""
+    N, Ci, H, W = x.shape
+    Co, _, KH, KW = wq.shape
+    Ho, Wo = (H + 2 * pad - KH) // stride + 1, (W + 2 * pad - KW) // stride + 1
+    qx, sx = oracle.quantize_i8(f64(x).ravel())
+    xp = np.zeros((N, H + 2 * pad, W + 2 * pad, Ci))
+    xp[:, pad:pad + H, pad:pad + W, :] = qx.reshape(N, Ci, H, W).transpose(0, 2, 3, 1)
+    acc = np.zeros((N * Ho * Wo, Co))
+    for kh in range(KH):
+        for kw in range(KW):
+            win = xp[:, kh:kh + stride * (Ho - 1) + 1:stride, kw:kw + stride * (Wo - 1) + 1:stride, :]
+            acc += win.reshape(-1, Ci) @ wq[:, :, kh, kw].astype(np.float64).T
+    v = (acc * (sw * sx)).astype(np.float32)
+    if bias is not None:
+        v = v + bias.astype(np.float32)[None, :]
+    if relu:
+        v = np.where(v > 0, v, np.float32(0))
+    return v.reshape(N, Ho, Wo, Co).transpose(0, 3, 1, 2)
+
+
+# (N, Ci, H, W, Co, K, stride, pad): the LDS-resident kernel with 128-channel
+# blocks (two of them for 200 channels), 64-channel blocks with 7 x 7 taps
+# over 16 channels (two taps per k-step), stride 2, and 32-channel blocks.
+EXACT = [(3, 64, 20, 20, 128, 3, 1, 1), (2, 32, 14, 14, 200, 3, 1, 1), (2, 16, 10, 10, 70, 7, 1, 3),
+         (2, 48, 15, 17, 96, 3, 2, 1), (1, 20, 9, 9, 30, 5, 1, 2)]
+
+
+@pytest.mark.parametrize("N,Ci,H,W,Co,Kk,stride,pad", EXACT)
+def test_conv_i8_bit_exact_bias_relu(dev, N, Ci, H, W, Co, Kk, stride, pad):
+    x = prng.normal(140 + Co, (N, Ci, H, W))
+    wq = np.round(prng.uniform(141 + Co, (Co, Ci, Kk, Kk), -127.4, 127.4)).astype(np.int8)
+    bias = prng.normal(142 + Co, (Co,), 0.0, 0.5)
+    sw = 0.0023
+    Ho, Wo = (H + 2 * pad - Kk) // stride + 1, (W + 2 * pad - Kk) // stride + 1
+    dx, dw, db = dev.upload(x.astype(np.float32)), dev.upload(wq), dev.upload(bias.astype(np.float32))
+    do = dev.upload(np.full((N, Co, Ho, Wo), np.nan, np.float32))
+    case(f"conv2d_i8 N={N} Ci={Ci} {H}x{W} Co={Co} {Kk}x{Kk} s={stride} p={pad} bias+relu, bits")
+    dev.conv2d_i8(do, dx, dw, sw, db, N, Ci, H, W, Co, Kk, Kk, stride, pad, ACT_RELU)
+    got = dev.download(do, (N, Co, Ho, Wo))
+    for b in (dx, dw, db, do):
+        b.free()
+    np.testing.assert_array_equal(got, _conv_i8_exact(x, wq, sw, stride, pad, bias, True))
 
 
 # ---- through the device executor ------------------------------------------------------
