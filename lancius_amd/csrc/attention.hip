@@ -48,6 +48,12 @@ struct AttnParams {
 
 constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
 
+// 2^x as the one v_exp_f32.  exp2f adds a range fix-up (compare, select,
+// add, select, ldexp: five more instructions) that only changes results
+// below 2^-126; the softmax exponents here are <= 0 and a probability under
+// 2^-126 does not move a sum that is >= 1.
+__device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // D = head dim (a multiple of 32, at most 128); BKV = keys per LDS block
 // (64 for D <= 64, 32 above, so the K/V blocks of two workgroups fit a
 // CU's LDS).  KS = key split: with KS = 2 the workgroup has 8 waves, and
@@ -232,13 +238,13 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
             // Register r of lane l holds key kb + 32*sb + 8*(r/4) + 4*(l/32) + r%4.
             const bool need_mask = (p.causal && kb + BKV - 1 > qw0 + off) || (kb + BKV > Skv);
             if (need_mask) {
+                // the lane's last visible key, relative to its first in the block
+                const int lim = min(Skv - 1, p.causal ? q + off : Skv - 1) - (kb + 4 * lk);
 #pragma unroll
                 for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = kb + 32 * sb + 8 * (r >> 2) + 4 * lk + (r & 3);
-                        if (key >= Skv || (p.causal && key > q + off)) s_acc[sb][r] = -INFINITY;
-                    }
+                    for (int r = 0; r < 16; ++r)
+                        if (32 * sb + 8 * (r >> 2) + (r & 3) > lim) s_acc[sb][r] = -INFINITY;
             }
             float mx = -INFINITY;
 #pragma unroll
@@ -247,22 +253,29 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
                 for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_acc[sb][r]);
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             const float m_new = fmaxf(m_run, mx);
-            const float corr = exp2f(m_run - m_new);
+            // The running sums are rescaled only when some lane's maximum
+            // grew: otherwise every lane's factor is 2^0 = 1 and skipping
+            // the multiplies changes no bit (after the first blocks of a
+            // row the maximum rarely moves).
+            float corr = 1.0f;
+            if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
+                corr = exp2_raw(m_run - m_new);
+#pragma unroll
+                for (int db = 0; db < DB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o_acc[db][r] *= corr;
+            }
             m_run = m_new;
             float psum = 0.0f;
 #pragma unroll
             for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float pv = exp2f(s_acc[sb][r] - m_new);
+                    const float pv = exp2_raw(s_acc[sb][r] - m_new);
                     s_acc[sb][r] = pv;
                     psum += pv;
                 }
             l_part = l_part * corr + psum;
-#pragma unroll
-            for (int db = 0; db < DB; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o_acc[db][r] *= corr;
             // O^T += V^T . P^T over the BKV keys of this block.
 #pragma unroll
             for (int sb = 0; sb < SB; ++sb)
