@@ -1489,12 +1489,14 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         K >= 256 && big_tiles < 768) {
         // 64 x 64 tiles, with 4 k-groups when that gives about one tile per
         // CU and 2 otherwise; 128 x 128 tiles (2 k-groups: 4 would leave 128
-        // registers a wave and spill) for K >= 4096 with >= 192 of them.
+        // registers a wave and spill) for K >= 2048 with >= 192 of them
+        // (K >= 2048 rather than 4096 since the spread epilogue: 2048^3
+        // 136.3 -> 131.9 us, 2048x2048x4096 268 -> 260 us).
         // Measured on MI355X (old dispatch -> this): 1024^3 27.0 -> 23.7 us,
         // 2048^3 146.0 -> 135.6, 4096x1024x1024 82.4 -> 71.3,
         // 1024x4096x1024 84.4 -> 76.4, 4096x4096x1024 275.2 -> 257.3,
         // 3000x1000x2000 145.8 -> 104.3.
-        const int bm_kg = K >= 4096 && big_tiles >= 192 ? 128 : 64;
+        const int bm_kg = K >= 2048 && big_tiles >= 192 ? 128 : 64;
         const int kg = bm_kg == 128 || t64 > 384 ? 2 : 4;
         const size_t kg_tiles = count * ((M + bm_kg - 1) / bm_kg) * ((N + bm_kg - 1) / bm_kg);
         if (kg_tiles >= 128) {

@@ -112,13 +112,18 @@ enum : int { kActNone = 0, kActRelu = 1, kActGelu = 2, kActTanh = 3 };
 __device__ __forceinline__ float relu_ref(float x) { return x > 0.0f ? x : 0.0f; }
 
 // tanh-approximation GELU with the +-100 input clamp of
-// bleeding/v11A1/src/math/lancius_kernels.c:238-246 (NaN passes through).
+// bleeding/v11A1/src/math/lancius_kernels.c:238-246 (NaN passes through),
+// evaluated as 0.5 x (1 + tanh u) = x / (1 + e^(-2u)): one v_exp_f32 and
+// one v_rcp_f32 (a few ulp) instead of tanhf's sequence, and no
+// cancellation in 1 + tanh u for negative u.  At the clamp, e^(-2u) is 0
+// (x = 100 gives 100) or +inf (x = -100 gives -0, as 0.5 x (1 + tanh u)).
 __device__ __forceinline__ float gelu_ref(float x) {
     x = x > 100.0f ? 100.0f : x;
     x = x < -100.0f ? -100.0f : x;
     const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
     const float u = k0 * (x + 0.044715f * x * x * x);
-    return 0.5f * x * (1.0f + tanhf(u));
+    const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * u);  // e^(-2u) = 2^(-2u log2 e)
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 __device__ __forceinline__ float apply_act(float x, int act) {
