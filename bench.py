@@ -64,9 +64,10 @@ def time_steps(dev: Device, fn, steps: int, warmup: int, settle_ms: float = 40.0
     """Average ms per call of fn over `steps` calls, HIP events on the
     context stream, after `warmup` untimed calls and, with settle_ms > 0,
     enough further untimed calls for about settle_ms of GPU work (at most
-    500): the clock drops while the host prepares a case and settles again
-    over tens of milliseconds of load.  info["settle_launches"] receives the
-    number of those further calls."""
+    4000): the clock drops while the host prepares a case and settles again
+    over tens of milliseconds of load (with at most 500, a 21 us case
+    settled for 10 ms and timed about 10% slow).  info["settle_launches"]
+    receives the number of those further calls."""
     for _ in range(warmup):
         fn()
     dev.synchronize()
@@ -75,7 +76,7 @@ def time_steps(dev: Device, fn, steps: int, warmup: int, settle_ms: float = 40.0
         dev.timer_start()
         fn()
         one = max(dev.timer_stop(), 1e-3)
-        settled = 1 + min(500, int(settle_ms / one))
+        settled = 1 + min(4000, int(settle_ms / one))
         for _ in range(settled - 1):
             fn()
         dev.synchronize()
