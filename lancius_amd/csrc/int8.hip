@@ -538,11 +538,13 @@ __global__ void __launch_bounds__(64 * WGM * WGN, MINW) gemm_i8_mfma(const I8Par
 // lane's pixel), kConvI8Ring k-steps ahead; taps outside the image, and k
 // past the filter's KHW * Cp, load from an offset past the buffer's end
 // (zeros).  After the prologue the filter is read-only, so the k loop has
-// no barrier.  Workgroup b serves output-channel block b % co_blocks; a
-// block's pixel tiles are dealt 4 consecutive tiles per workgroup (the
-// tiles share input rows in the CU's L1), then in strides of all its
-// workgroups.  The epilogue is gemm_i8_mfma's (fp64 scale, fp32 result,
-// bias, activation, NCHW store), so both kernels give the same bits.
+// no barrier.  One workgroup of 8 waves per CU: workgroup b serves
+// output-channel block b % co_blocks and an equal share of its consecutive
+// pixel tiles (they share input rows in the CU's L1), dealt to the waves
+// one per SIMD first; a wave issues its next tile's first loads before its
+// current tile's stores.  The epilogue computes what gemm_i8_mfma's does
+// (fp64 scale, fp32 result, bias, ReLU, NCHW store), so both kernels give
+// the same bits.
 // Requires Kp % (32 kConvI8Ring) == 0, Kp <= kConvI8MaxKp, ROWS * ldw + 32 <= kConvI8Lds, KHW <= 64
 // and the activation under 2 GiB - 64 (b_bytes: its size; the past-the-end
 // offset lies beyond it).
