@@ -1488,27 +1488,31 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
     if (vec && plain && M * K * sizeof(float) < ((size_t)1 << 31) && K * N * sizeof(float) < ((size_t)1 << 31) &&
         K >= 256 && big_tiles < 768) {
         // 64 x 64 tiles, with 4 k-groups when that gives about one tile per
-        // CU and 2 otherwise; 128 x 128 tiles (2 k-groups: 4 would leave 128
-        // registers a wave and spill) for K >= 2048 with >= 192 of them
-        // (K >= 2048 rather than 4096 since the spread epilogue: 2048^3
-        // 136.3 -> 131.9 us, 2048x2048x4096 268 -> 260 us).
+        // CU and 2 otherwise; 128 x 128 tiles with 4 k-groups (16 waves, 100
+        // registers each) for K >= 2048 with >= 192 of them.
         // Measured on MI355X (old dispatch -> this): 1024^3 27.0 -> 23.7 us,
         // 2048^3 146.0 -> 135.6, 4096x1024x1024 82.4 -> 71.3,
         // 1024x4096x1024 84.4 -> 76.4, 4096x4096x1024 275.2 -> 257.3,
-        // 3000x1000x2000 145.8 -> 104.3.
+        // 3000x1000x2000 145.8 -> 104.3.  The 128 x 128 tiles with 4 k-groups
+        // of 16-deep k-tiles against 2 k-groups of 32-deep ones (one box, the
+        // two builds alternated): 2048^3 131.3 -> 129.0 us, 2048x4096x2048
+        // 251.1 -> 246.7, 2048x2048x4096 259.3 -> 254.2, four grouped
+        // 1024x4096x1024 (bias and residual) 259.8 -> 251.4.  At K = 1024 they
+        // lose to 64 x 64 tiles unless the grid is exactly 256 of them (3072 x
+        // 1024 x 1024: 54.9 -> 69.2 us; 4096 x 1024 x 1024: 70.5 -> 69.9).
         const int bm_kg = K >= 2048 && big_tiles >= 192 ? 128 : 64;
-        const int kg = bm_kg == 128 || t64 > 384 ? 2 : 4;
+        const int kg = bm_kg == 128 || t64 <= 384 ? 4 : 2;
         const size_t kg_tiles = count * ((M + bm_kg - 1) / bm_kg) * ((N + bm_kg - 1) / bm_kg);
         if (kg_tiles >= 128) {
             p.tiles_m = (uint32_t)((M + bm_kg - 1) / bm_kg);
             p.tiles_n = (uint32_t)((N + bm_kg - 1) / bm_kg);
-            // 128 x 128 tiles take k-tiles of 32 (half the barriers per k):
-            // 1024x4096x1024 77.4 -> 70.0 us, four of them grouped 259.5 ->
-            // 257.5 us; the 64 x 64 tiles measured no better with 32
-            // (1024^3 23.9 -> 24.3 us, four grouped 72.1 -> 72.7 us)
-            void (*kern)(const GemmParams) = bm_kg == 128 ? gemm_f32_direct_kg<128, 2, 32>
+            // k-tiles of 16: with 32 (half the barriers per k) the 64 x 64
+            // tiles measured no better (1024^3 23.9 -> 24.3 us, four grouped
+            // 72.1 -> 72.7 us), and 128 x 128 tiles with 4 k-groups would
+            // need 256 KB of LDS
+            void (*kern)(const GemmParams) = bm_kg == 128 ? gemm_f32_direct_kg<128, 4>
                                                           : (kg == 2 ? gemm_f32_direct_kg<64, 2> : gemm_f32_direct_kg<64, 4>);
-            hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256 * (kg == 2 ? 2 : 4)), 0,
+            hipLaunchKernelGGL(kern, dim3(p.tiles_m * p.tiles_n, 1, (unsigned)count), dim3(256 * kg), 0,
                                ctx->stream, p);
             if (int rc = check_launch("gemm_f32_direct_kg")) return rc;
             return ok();

@@ -108,7 +108,7 @@ def test_gemm_config_every_band(dev, n):
 @pytest.mark.parametrize("M,K,N", [
     (2048, 1000, 2048),  # direct loads, 64x64 tiles, 2 k-groups; K crosses a 16-deep k-tile
     (1000, 1028, 1100),  # direct loads, 64x64 tiles, 4 k-groups, ragged edges
-    (3000, 4096, 1500),  # direct loads, 128x128 tiles, 2 k-groups, ragged edges
+    (3000, 4096, 1500),  # direct loads, 128x128 tiles, 4 k-groups, ragged edges
     (2048, 72, 3072),    # K < 256: staged, 384 tiles of 128^2 with 2 k-groups
     (2000, 40, 2990),    # 384 tiles, N % 4 != 0: scalar loads
     (520, 2100, 500),    # 20 tiles, K >= 2048: 2 k-groups with split K, ragged edges
