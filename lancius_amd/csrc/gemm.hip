@@ -614,29 +614,62 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
     }
 
     // ---- epilogue: bias, activation, residual, one store -----------------
+    // The activation is chosen once per launch and a tile wholly inside C
+    // takes a copy without bounds checks: per element, a four-way switch
+    // and the row check made the unrolled epilogue thousands of branchy
+    // instructions, fetched by every CU at once at the end of the launch.
     const float* __restrict__ bias = p.bias[g];
-    const int act = p.act;
+    const int cb = n0 + wn * WN + lr;
+    float bv[TN];
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * WN + j * 32 + lr;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
+    for (int j = 0; j < TN; ++j) bv[j] = bias && cb + 32 * j < N ? bias[cb + 32 * j] : 0.0f;
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+    with_act(p.act, [&](auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
+        if (full) {
+            // one 32 x 32 block at a time (a scheduling barrier between
+            // blocks keeps the residual loads from all being hoisted at once)
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = rbase + 8 * (r >> 2) + (r & 3);
-                if (row < M) {
-                    float v = acc[i][j][r] + bv;
-                    v = apply_act(v, act);
-                    const size_t o = (size_t)row * N + col;
-                    if (R) v += R[o];
-                    C[o] = v;
+                for (int i = 0; i < TM; ++i) {
+                    const size_t o0 = (size_t)(m0 + wm * WM + i * 32 + 4 * lk) * N + cb + 32 * j;
+                    float* __restrict__ cp = C + o0;
+                    if (R) {
+                        const float* __restrict__ rp = R + o0;
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int ro = (8 * (r >> 2) + (r & 3)) * N;
+                            cp[ro] = act_fixed<ACT>(acc[i][j][r] + bv[j]) + rp[ro];
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 16; ++r)
+                            cp[(8 * (r >> 2) + (r & 3)) * N] = act_fixed<ACT>(acc[i][j][r] + bv[j]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            return;
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = cb + 32 * j;
+            if (col >= N) continue;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = rbase + 8 * (r >> 2) + (r & 3);
+                    if (row < M) {
+                        const size_t o = (size_t)row * N + col;
+                        const float v = act_fixed<ACT>(acc[i][j][r] + bv[j]);
+                        C[o] = R ? v + R[o] : v;
+                    }
                 }
             }
         }
-    }
+    });
 }
 
 // The direct-load pipeline of gemm_f32_direct for grids too small to give
@@ -847,34 +880,35 @@ __global__ void __launch_bounds__(256 * KG, 1) gemm_f32_direct_kg(const GemmPara
     // piece pi = (source wave pw, accumulator (i, j), quad q): lane l's four
     // values are rows 8q + 4(l/32) + 0..3, column l%32 of accumulator (i, j)
     // of wave pw's WM x WN block
+    // (the activation chosen once per launch, as in gemm_f32_direct)
     constexpr int NP = 4 * QUADS, NW = 4 * KG;
     const float* __restrict__ bias = p.bias[g];
-    const int act = p.act;
     const int w = grp * 4 + gw;
+    with_act(p.act, [&](auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-    for (int t = 0; t < NP / NW; ++t) {
-        const int pi = w + NW * t;
-        const int pw = pi / QUADS, rest = pi % QUADS;
-        const int i = (rest / 4) / TN, j = (rest / 4) % TN, q = rest % 4;
-        const f32x4 s0 = *(const f32x4*)(smem + (pi * 64 + lane) * 4);
-        const f32x4 s1 = *(const f32x4*)(smem + BM * BN + (pi * 64 + lane) * 4);
-        const float sum[4] = {s0.x + s1.x, s0.y + s1.y, s0.z + s1.z, s0.w + s1.w};
-        const int col = n0 + (pw & 1) * WN + j * 32 + lr;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
-        const int rbase = m0 + (pw >> 1) * WM + i * 32 + 8 * q + 4 * lk;
+        for (int t = 0; t < NP / NW; ++t) {
+            const int pi = w + NW * t;
+            const int pw = pi / QUADS, rest = pi % QUADS;
+            const int i = (rest / 4) / TN, j = (rest / 4) % TN, q = rest % 4;
+            const f32x4 s0 = *(const f32x4*)(smem + (pi * 64 + lane) * 4);
+            const f32x4 s1 = *(const f32x4*)(smem + BM * BN + (pi * 64 + lane) * 4);
+            const float sum[4] = {s0.x + s1.x, s0.y + s1.y, s0.z + s1.z, s0.w + s1.w};
+            const int col = n0 + (pw & 1) * WN + j * 32 + lr;
+            if (col >= N) continue;
+            const float bv = bias ? bias[col] : 0.0f;
+            const int rbase = m0 + (pw >> 1) * WM + i * 32 + 8 * q + 4 * lk;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            const int row = rbase + s;
-            if (row < M) {
-                float v = sum[s] + bv;
-                v = apply_act(v, act);
-                const size_t o = (size_t)row * N + col;
-                if (R) v += R[o];
-                C[o] = v;
+            for (int s = 0; s < 4; ++s) {
+                const int row = rbase + s;
+                if (row < M) {
+                    const size_t o = (size_t)row * N + col;
+                    const float v = act_fixed<ACT>(sum[s] + bv);
+                    C[o] = R ? v + R[o] : v;
+                }
             }
         }
-    }
+    });
 }
 
 // Skinny GEMM (M <= 16*MT): the product is bound by reading B once from
