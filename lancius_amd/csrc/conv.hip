@@ -245,29 +245,38 @@ __global__ void __launch_bounds__(kThreads) conv2d_implicit_gemm(const ConvParam
     }
 
     // Epilogue: register r of lane l is channel row 8*(r/4)+4*(l/32)+r%4,
-    // pixel column l%32 of its 32x32 sub-tile.
-    const float* __restrict__ bias = p.bias;
-    const int act = p.act;
+    // pixel column l%32 of its 32x32 sub-tile.  The tile's bias goes through
+    // LDS (free after the loop's last barrier), four values per read: a bias
+    // load from global memory issued after a store would wait for that store,
+    // since a wave's loads and stores complete in order.  The activation is
+    // chosen once per launch.
+    if (threadIdx.x < BM) smem[threadIdx.x] = p.bias && m0 + (int)threadIdx.x < C_out ? p.bias[m0 + threadIdx.x] : 0.0f;
+    __syncthreads();
+    with_act(p.act, [&](auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const long long Pc = P0 + wn * WN + j * 32 + lr;
-        if (Pc >= p.Ptotal) continue;
-        const int n_o = (int)(Pc / HWo);
-        const int pix = (int)(Pc - (long long)n_o * HWo);
-        float* obase = p.out + (size_t)n_o * C_out * HWo + pix;
+        for (int j = 0; j < TN; ++j) {
+            const long long Pc = P0 + wn * WN + j * 32 + lr;
+            if (Pc >= p.Ptotal) continue;
+            const int n_o = (int)(Pc / HWo);
+            const int pix = (int)(Pc - (long long)n_o * HWo);
+            float* obase = p.out + (size_t)n_o * C_out * HWo + pix;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int cbase = m0 + wm * WM + i * 32 + 4 * lk;
+            for (int i = 0; i < TM; ++i) {
+                const int cl = wm * WM + i * 32 + 4 * lk;  // the lane's first channel row in the tile
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int co = cbase + 8 * (r >> 2) + (r & 3);
-                if (co < C_out) {
-                    float v = acc[i][j][r] + (bias ? bias[co] : 0.0f);
-                    obase[(size_t)co * HWo] = apply_act(v, act);
+                for (int q = 0; q < 4; ++q) {
+                    const f32x4 b4 = *(const f32x4*)&smem[cl + 8 * q];
+                    const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int co = m0 + cl + 8 * q + e;
+                        if (co < C_out) obase[(size_t)co * HWo] = act_fixed<ACT>(acc[i][j][4 * q + e] + bq[e]);
+                    }
                 }
             }
         }
-    }
+    });
 }
 
 // The per-channel path (C_in % 16 == 0, weights re-laid as wt) with both
@@ -295,6 +304,7 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
     __shared__ __attribute__((aligned(16))) float Bs0[BK * BN];
     __shared__ __attribute__((aligned(16))) float Bs1[BK * BN];
     __shared__ int s_flag;
+    __shared__ __attribute__((aligned(16))) float s_bias[BM];
 
     const int KH = KH_T > 0 ? KH_T : p.KH;
     const int KW = KW_T > 0 ? KW_T : p.KW;
@@ -437,8 +447,14 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
     };
 
     // register r of lane l: channel row 8(r/4) + 4(l/32) + r%4, pixel l%32
+    // The tile's bias goes through LDS, read four values at a time: a
+    // wave's loads and stores complete in order, so a bias load from global
+    // memory issued after a store waits for that store (one such load per
+    // element made the epilogue a chain of store round trips).  The
+    // activation is chosen once per launch.
     auto store = [&]() {
-        const float* __restrict__ bias = p.bias;
+        if (tid < BM) s_bias[tid] = p.bias && m0 + tid < C_out ? p.bias[m0 + tid] : 0.0f;
+        __syncthreads();
         with_act(p.act, [&](auto act_c) {
             constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
@@ -450,12 +466,16 @@ __global__ void __launch_bounds__(kThreads, 2) conv2d_direct(const ConvParams p)
                 float* obase = p.out + (size_t)n_o * C_out * HWo + pix;
 #pragma unroll
                 for (int i = 0; i < TM; ++i) {
-                    const int cbase = m0 + wm * WM + i * 32 + 4 * lk;
+                    const int cl = wm * WM + i * 32 + 4 * lk;  // the lane's first channel row in the tile
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int co = cbase + 8 * (r >> 2) + (r & 3);
-                        if (co < C_out)
-                            obase[(size_t)co * HWo] = act_fixed<ACT>(acc[i][j][r] + (bias ? bias[co] : 0.0f));
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x4 b4 = *(const f32x4*)&s_bias[cl + 8 * q];
+                        const float bq[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int co = m0 + cl + 8 * q + e;
+                            if (co < C_out) obase[(size_t)co * HWo] = act_fixed<ACT>(acc[i][j][4 * q + e] + bq[e]);
+                        }
                     }
                 }
             }

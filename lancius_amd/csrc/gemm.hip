@@ -437,29 +437,30 @@ __global__ void __launch_bounds__(kThreads * KG, OCC) gemm_f32_mfma(const GemmPa
         }
         return;
     }
+    // (the activation chosen once per launch, as in gemm_f32_direct)
     const float* __restrict__ bias = p.bias[g];
-    const int act = p.act;
+    with_act(p.act, [&](auto act_c) {
+        constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = n0 + wn * WN + j * 32 + lr;
-        if (col >= N) continue;
-        const float bv = bias ? bias[col] : 0.0f;
+        for (int j = 0; j < TN; ++j) {
+            const int col = n0 + wn * WN + j * 32 + lr;
+            if (col >= N) continue;
+            const float bv = bias ? bias[col] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) {
-            const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+            for (int i = 0; i < TM; ++i) {
+                const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = rbase + 8 * (r >> 2) + (r & 3);
-                if (row < M) {
-                    float v = acc[i][j][r] + bv;
-                    v = apply_act(v, act);
-                    const size_t o = (size_t)row * N + col;
-                    if (R) v += R[o];
-                    C[o] = v;
+                for (int r = 0; r < 16; ++r) {
+                    const int row = rbase + 8 * (r >> 2) + (r & 3);
+                    if (row < M) {
+                        const size_t o = (size_t)row * N + col;
+                        const float v = act_fixed<ACT>(acc[i][j][r] + bv);
+                        C[o] = R ? v + R[o] : v;
+                    }
                 }
             }
         }
-    }
+    });
 }
 
 // 128x128 tiles, k-tiles of 16, 4 waves of 64x64, with both operand tiles
