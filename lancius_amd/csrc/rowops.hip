@@ -18,6 +18,28 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// The same sum without LDS traffic: DPP moves inside each row of 16 lanes
+// (xor 1 and xor 2 in the quad, the half-row and row mirrors) leave every
+// lane with its row's sum, and the four row sums are read from lanes 0, 16,
+// 32 and 48 and added in that order, so every lane gets the same value.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -60,34 +82,56 @@ __global__ void __launch_bounds__(kRowThreads) layernorm_regs(const LnGroup grp,
     const float* __restrict__ gamma = grp.gamma[blockIdx.y];
     const float* __restrict__ beta = grp.beta[blockIdx.y];
     const float* x = grp.in[blockIdx.y] + (size_t)row * H;
-    f32x4 v[NV];
-    load_row_f4<NV>(x, H, lane, v);
+    // Up to 4 pieces a lane, gamma and beta are requested with the row,
+    // before the first wait: loaded between the output stores, each would
+    // wait for the stores before it (a wave's loads and stores complete in
+    // order).  Pieces past the row are zero and skipped.
+    constexpr bool PRE = NV <= 4;
+    constexpr int NP = PRE ? NV : 1;
+    const bool full = H == 256 * NV;
+    f32x4 v[NV], g[NP], b[NP];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * lane + 256 * i;
+        const bool in = full || c0 < H;
+        v[i] = in ? *(const f32x4*)(x + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (PRE) {
+            g[i] = in ? *(const f32x4*)(gamma + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            b[i] = in ? *(const f32x4*)(beta + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    }
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    const float mean = wave_sum(s) / (float)H;
+    const float mean = wave_sum_dpp(s) / (float)H;
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        if (4 * lane + 256 * i < H) {
-            const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
-            q += (a * a + b * b) + (c * c + d * d);
+        if (full || 4 * lane + 256 * i < H) {
+            const float a = v[i].x - mean, bb = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+            q += (a * a + bb * bb) + (c * c + d * d);
         }
     }
-    const float var = wave_sum(q) / (float)H;
+    const float var = wave_sum_dpp(q) / (float)H;
     const float inv_std = 1.0f / sqrtf(var + eps);
     float* y = out + (size_t)row * H;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c0 = 4 * lane + 256 * i;
-        if (c0 >= H) continue;
-        const f32x4 g = *(const f32x4*)(gamma + c0);
-        const f32x4 b = *(const f32x4*)(beta + c0);
+        if (!full && c0 >= H) continue;
+        f32x4 gi, bi;
+        if constexpr (PRE) {
+            gi = g[i];
+            bi = b[i];
+        } else {
+            gi = *(const f32x4*)(gamma + c0);
+            bi = *(const f32x4*)(beta + c0);
+        }
         f32x4 o;
-        o.x = (v[i].x - mean) * inv_std * g.x + b.x;
-        o.y = (v[i].y - mean) * inv_std * g.y + b.y;
-        o.z = (v[i].z - mean) * inv_std * g.z + b.z;
-        o.w = (v[i].w - mean) * inv_std * g.w + b.w;
+        o.x = (v[i].x - mean) * inv_std * gi.x + bi.x;
+        o.y = (v[i].y - mean) * inv_std * gi.y + bi.y;
+        o.z = (v[i].z - mean) * inv_std * gi.z + bi.z;
+        o.w = (v[i].w - mean) * inv_std * gi.w + bi.w;
         *(f32x4*)(y + c0) = o;
     }
 }
@@ -358,8 +402,20 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_regs(float* __restrict__ 
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= rows) return;
-    f32x4 v[NV];
-    load_row_f4<NV>(in + (size_t)row * hidden, hidden, lane, v);
+    // gamma requested with the row (up to 4 pieces a lane), as in
+    // layernorm_regs; pieces past the row are zero
+    constexpr bool PRE = NV <= 4;
+    constexpr int NP = PRE ? NV : 1;
+    const bool full = hidden == 256 * NV;
+    const float* x = in + (size_t)row * hidden;
+    f32x4 v[NV], g[NP];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c0 = 4 * lane + 256 * i;
+        const bool inside = full || c0 < hidden;
+        v[i] = inside ? *(const f32x4*)(x + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (PRE) g[i] = inside ? *(const f32x4*)(gamma + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -368,19 +424,23 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_regs(float* __restrict__ 
         q += v[i].z * v[i].z;
         q += v[i].w * v[i].w;
     }
-    q = wave_sum(q);
+    q = wave_sum_dpp(q);
     const float inv = 1.0f / sqrtf(q / (float)hidden + eps);
     float* y = out + (size_t)row * hidden;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c0 = 4 * lane + 256 * i;
-        if (c0 >= hidden) continue;
-        const f32x4 g = *(const f32x4*)(gamma + c0);
+        if (!full && c0 >= hidden) continue;
+        f32x4 gi;
+        if constexpr (PRE)
+            gi = g[i];
+        else
+            gi = *(const f32x4*)(gamma + c0);
         f32x4 o;
-        o.x = (v[i].x * inv) * g.x;
-        o.y = (v[i].y * inv) * g.y;
-        o.z = (v[i].z * inv) * g.z;
-        o.w = (v[i].w * inv) * g.w;
+        o.x = (v[i].x * inv) * gi.x;
+        o.y = (v[i].y * inv) * gi.y;
+        o.z = (v[i].z * inv) * gi.z;
+        o.w = (v[i].w * inv) * gi.w;
         *(f32x4*)(y + c0) = o;
     }
 }
