@@ -881,31 +881,41 @@ __global__ void __launch_bounds__(256 * KG, 1) gemm_f32_direct_kg(const GemmPara
     // piece pi = (source wave pw, accumulator (i, j), quad q): lane l's four
     // values are rows 8q + 4(l/32) + 0..3, column l%32 of accumulator (i, j)
     // of wave pw's WM x WN block
-    // (the activation chosen once per launch, as in gemm_f32_direct)
-    constexpr int NP = 4 * QUADS, NW = 4 * KG;
+    // Bias and residual values are all requested before the first store (a
+    // load issued after a store waits for it: loads and stores complete in
+    // order), and the activation is chosen once per launch.
+    constexpr int NP = 4 * QUADS, NW = 4 * KG, T = NP / NW;
     const float* __restrict__ bias = p.bias[g];
     const int w = grp * 4 + gw;
+    int col[T], rbase[T];
+    float bv[T], rv[T][4];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int pi = w + NW * t;
+        const int pw = pi / QUADS, rest = pi % QUADS;
+        const int i = (rest / 4) / TN, j = (rest / 4) % TN, q = rest % 4;
+        col[t] = n0 + (pw & 1) * WN + j * 32 + lr;
+        rbase[t] = m0 + (pw >> 1) * WM + i * 32 + 8 * q + 4 * lk;
+        bv[t] = bias && col[t] < N ? bias[col[t]] : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            rv[t][s] = R && col[t] < N && rbase[t] + s < M ? R[(size_t)(rbase[t] + s) * N + col[t]] : 0.0f;
+    }
     with_act(p.act, [&](auto act_c) {
         constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-        for (int t = 0; t < NP / NW; ++t) {
+        for (int t = 0; t < T; ++t) {
             const int pi = w + NW * t;
-            const int pw = pi / QUADS, rest = pi % QUADS;
-            const int i = (rest / 4) / TN, j = (rest / 4) % TN, q = rest % 4;
             const f32x4 s0 = *(const f32x4*)(smem + (pi * 64 + lane) * 4);
             const f32x4 s1 = *(const f32x4*)(smem + BM * BN + (pi * 64 + lane) * 4);
             const float sum[4] = {s0.x + s1.x, s0.y + s1.y, s0.z + s1.z, s0.w + s1.w};
-            const int col = n0 + (pw & 1) * WN + j * 32 + lr;
-            if (col >= N) continue;
-            const float bv = bias ? bias[col] : 0.0f;
-            const int rbase = m0 + (pw >> 1) * WM + i * 32 + 8 * q + 4 * lk;
+            if (col[t] >= N) continue;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const int row = rbase + s;
+                const int row = rbase[t] + s;
                 if (row < M) {
-                    const size_t o = (size_t)row * N + col;
-                    const float v = act_fixed<ACT>(sum[s] + bv);
-                    C[o] = R ? v + R[o] : v;
+                    const float v = act_fixed<ACT>(sum[s] + bv[t]);
+                    C[(size_t)row * N + col[t]] = R ? v + rv[t][s] : v;
                 }
             }
         }
