@@ -73,23 +73,40 @@ struct LnGroup {
     const float* beta[LANCIUS_HIP_MAX_GROUP];
 };
 
+// Gamma (and beta) of rows wider than 1024 columns: the workgroup copies them
+// to LDS with the rows' own loads (one float4 piece per lane and register
+// slot, as the rows are held), so that no global load follows an output
+// store (a wave's loads and stores complete in order: such a load would wait
+// for the stores before it).  Up to 1024 columns they stay in registers.
+template <int NV>
+__device__ __forceinline__ void stage_rows_param(f32x4* dst, const float* __restrict__ src, int H, bool full) {
+#pragma unroll
+    for (int k = 0; k < NV / 4; ++k) {
+        const int piece = threadIdx.x + kRowThreads * k;  // lane + 64 i of the register layout
+        dst[piece] = full || 4 * piece < H ? *(const f32x4*)(src + 4 * piece) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
 template <int NV>
 __global__ void __launch_bounds__(kRowThreads) layernorm_regs(const LnGroup grp, int rows, int H, float eps) {
+    constexpr bool PRE = NV <= 4;  // gamma and beta in registers, else in LDS
+    constexpr int NP = PRE ? NV : 1, NS = PRE ? 1 : 64 * NV;
+    __shared__ f32x4 gs[NS], bs[NS];
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
     float* __restrict__ out = grp.out[blockIdx.y];
     const float* __restrict__ gamma = grp.gamma[blockIdx.y];
     const float* __restrict__ beta = grp.beta[blockIdx.y];
-    const float* x = grp.in[blockIdx.y] + (size_t)row * H;
+    const bool full = H == 256 * NV;
+    if constexpr (!PRE) {
+        stage_rows_param<NV>(gs, gamma, H, full);
+        stage_rows_param<NV>(bs, beta, H, full);
+    }
     // Up to 4 pieces a lane, gamma and beta are requested with the row,
     // before the first wait: loaded between the output stores, each would
-    // wait for the stores before it (a wave's loads and stores complete in
-    // order).  Pieces past the row are zero and skipped.
-    constexpr bool PRE = NV <= 4;
-    constexpr int NP = PRE ? NV : 1;
-    const bool full = H == 256 * NV;
+    // wait for the stores before it.  Pieces past the row are zero and skipped.
     f32x4 v[NV], g[NP], b[NP];
+    const float* x = grp.in[blockIdx.y] + (size_t)min(row, rows - 1) * H;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c0 = 4 * lane + 256 * i;
@@ -100,6 +117,8 @@ __global__ void __launch_bounds__(kRowThreads) layernorm_regs(const LnGroup grp,
             b[i] = in ? *(const f32x4*)(beta + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     }
+    if constexpr (!PRE) __syncthreads();
+    if (row >= rows) return;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
@@ -124,8 +143,8 @@ __global__ void __launch_bounds__(kRowThreads) layernorm_regs(const LnGroup grp,
             gi = g[i];
             bi = b[i];
         } else {
-            gi = *(const f32x4*)(gamma + c0);
-            bi = *(const f32x4*)(beta + c0);
+            gi = gs[lane + 64 * i];
+            bi = bs[lane + 64 * i];
         }
         f32x4 o;
         o.x = (v[i].x - mean) * inv_std * gi.x + bi.x;
@@ -399,15 +418,16 @@ template <int NV>
 __global__ void __launch_bounds__(kRowThreads) rmsnorm_regs(float* __restrict__ out, const float* __restrict__ in,
                                                             const float* __restrict__ gamma, int rows, int hidden,
                                                             float eps) {
+    // gamma as in layernorm_regs: with the row in registers up to 4 pieces a
+    // lane, else staged in LDS with the row loads; pieces past the row are zero
+    constexpr bool PRE = NV <= 4;
+    constexpr int NP = PRE ? NV : 1, NS = PRE ? 1 : 64 * NV;
+    __shared__ f32x4 gs[NS];
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    // gamma requested with the row (up to 4 pieces a lane), as in
-    // layernorm_regs; pieces past the row are zero
-    constexpr bool PRE = NV <= 4;
-    constexpr int NP = PRE ? NV : 1;
     const bool full = hidden == 256 * NV;
-    const float* x = in + (size_t)row * hidden;
+    if constexpr (!PRE) stage_rows_param<NV>(gs, gamma, hidden, full);
+    const float* x = in + (size_t)min(row, rows - 1) * hidden;
     f32x4 v[NV], g[NP];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -416,6 +436,8 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_regs(float* __restrict__ 
         v[i] = inside ? *(const f32x4*)(x + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (PRE) g[i] = inside ? *(const f32x4*)(gamma + c0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    if constexpr (!PRE) __syncthreads();
+    if (row >= rows) return;
     float q = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -435,7 +457,7 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_regs(float* __restrict__ 
         if constexpr (PRE)
             gi = g[i];
         else
-            gi = *(const f32x4*)(gamma + c0);
+            gi = gs[lane + 64 * i];
         f32x4 o;
         o.x = (v[i].x * inv) * gi.x;
         o.y = (v[i].y * inv) * gi.y;
