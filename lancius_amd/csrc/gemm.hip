@@ -652,6 +652,8 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
                 }
             return;
         }
+        // a tile on the edge of C: the same blocks with bounds, the block's
+        // residual values loaded before its stores
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int col = cb + 32 * j;
@@ -659,15 +661,21 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
 #pragma unroll
             for (int i = 0; i < TM; ++i) {
                 const int rbase = m0 + wm * WM + i * 32 + 4 * lk;
+                float rv[16];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = rbase + 8 * (r >> 2) + (r & 3);
+                    rv[r] = R && row < M ? R[(size_t)row * N + col] : 0.0f;
+                }
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int row = rbase + 8 * (r >> 2) + (r & 3);
                     if (row < M) {
-                        const size_t o = (size_t)row * N + col;
                         const float v = act_fixed<ACT>(acc[i][j][r] + bv[j]);
-                        C[o] = R ? v + R[o] : v;
+                        C[(size_t)row * N + col] = R ? v + rv[r] : v;
                     }
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
     });
