@@ -640,13 +640,13 @@ __global__ void __launch_bounds__(256, OCC) gemm_f32_direct(const GemmParams p) 
                         const float* __restrict__ rp = R + o0;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
-                            const int ro = (8 * (r >> 2) + (r & 3)) * N;
+                            const size_t ro = (size_t)(8 * (r >> 2) + (r & 3)) * N;
                             cp[ro] = act_fixed<ACT>(acc[i][j][r] + bv[j]) + rp[ro];
                         }
                     } else {
 #pragma unroll
                         for (int r = 0; r < 16; ++r)
-                            cp[(8 * (r >> 2) + (r & 3)) * N] = act_fixed<ACT>(acc[i][j][r] + bv[j]);
+                            cp[(size_t)(8 * (r >> 2) + (r & 3)) * N] = act_fixed<ACT>(acc[i][j][r] + bv[j]);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
