@@ -85,6 +85,20 @@ def test_gemm_epilogues(dev, act, bias, residual):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(200)
 
 
+@pytest.mark.parametrize("act", [ACT_NONE, ACT_RELU, ACT_GELU])
+@pytest.mark.parametrize("bias,residual", [(True, True), (False, True), (True, False)])
+def test_gemm_direct_epilogues(dev, act, bias, residual):
+    """The 128x128 direct kernel (>= 768 tiles) with every epilogue: whole
+    tiles take the unchecked store path, the last tile-row (3000 = 23 x 128
+    + 56) and tile-column (4000 = 31 x 128 + 32) the bounded one, each
+    loading a block's residual values before its stores.  Rows sampled from
+    every 128-row band, the edge band's included."""
+    M, K, N = 3000, 256, 4000
+    rows = band_rows(M) + [2944, 2999]
+    got, ref = _gemm_case(dev, M, K, N, seed=61, bias=bias, act=act, residual=residual, row_list=sorted(set(rows)))
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
 @pytest.mark.parametrize("M,K,N", [(1024, 1024, 1024), (16, 4096, 4096)])
 def test_gemm_config_full(dev, M, K, N):
     got, ref = _gemm_case(dev, M, K, N, seed=43)

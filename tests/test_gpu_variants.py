@@ -140,6 +140,8 @@ def test_decode_variants(dev, D, G):
 CONVS = [
     (2, 16, 20, 20, 128, 5, 1, 2, "direct 128x64 tiles, 5x5 filter"),
     (2, 16, 21, 19, 64, 1, 1, 0, "direct 64x64 tiles, 1x1 filter"),
+    (2, 16, 20, 20, 100, 3, 1, 1, "direct 128x64 tiles, a partial channel block (bias rows past C_out)"),
+    (3, 32, 13, 17, 36, 3, 1, 1, "direct 64x64 tiles, a partial channel block"),
     (2, 3, 20, 20, 128, 5, 1, 2, "implicit GEMM 128x64 tiles, OIHW filter"),
     (2, 3, 20, 20, 64, 5, 2, 1, "implicit GEMM 64x64 tiles, OIHW filter"),
     (2, 6, 15, 15, 96, 3, 1, 1, "implicit GEMM 128x64 tiles, 3x3 OIHW filter"),
