@@ -586,15 +586,18 @@ __global__ void __launch_bounds__(256) attention_decode(const DecodeParams p) {
                 mx = fmaxf(mx, sc[u]);
             }
             // branch-free: while the stream has seen no key, m = mn = -inf,
-            // corr = 0 and every p = 0, so (o, l) stay 0
+            // corr = 0 and every p = 0, so (o, l) stay 0.  The exponents are
+            // <= 0, so the bare v_exp_f32 serves (see exp2_raw): decode
+            // B16 x 4096 keys 105.9 -> 104.7 us, same results at the tested
+            // shapes
             const float mn = fmaxf(m[h], mx);
-            const float corr = m[h] > -INFINITY ? exp2f(m[h] - mn) : 0.0f;
+            const float corr = m[h] > -INFINITY ? exp2_raw(m[h] - mn) : 0.0f;
             float ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < NV; ++i) o[h][i] *= corr;
 #pragma unroll
             for (int u = 0; u < UNR; ++u) {
-                const float pu = valid[u] ? exp2f(sc[u] - mn) : 0.0f;
+                const float pu = valid[u] ? exp2_raw(sc[u] - mn) : 0.0f;
                 ps += pu;
 #pragma unroll
                 for (int i = 0; i < NV; ++i) o[h][i] += pu * vr[u][i];
