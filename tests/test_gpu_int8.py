@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
-from lancius_amd import ACT_NONE, ACT_RELU, DeviceProgram, abi, graph_lib, graphs, prng
+from lancius_amd import ACT_NONE, ACT_RELU, DEVICE_GRAPH, DeviceProgram, abi, graph_lib, graphs, prng
 from tests.conftest import case
 
 pytestmark = pytest.mark.gpu
@@ -427,6 +427,41 @@ def test_int8_matmul_program_weight_pointer_kept(dev):
         prog.run()
         got = prog.download(mm).reshape(M, N)
         assert oracle.normwise_error(got, oracle.matmul_i8(f64(a), bq, 0.004)) <= TOL, seed
+    prog.close()
+    lib.lancius_schedule_destroy(sched)
+    lib.lancius_graph_destroy(g)
+
+
+def test_int8_matmul_program_graph_replay(dev):
+    """An int8 MATMUL program run as a recorded graph (the quantizer's two
+    launches and the product replayed): each replay takes a new A, whose
+    scale differs, and is checked against the oracle, with eager int8 work
+    on the same context in between."""
+    lib = graph_lib()
+    M, Kd, N = 200, 512, 260
+    g = lib.lancius_graph_create()
+    na, nb = lib.lancius_input(g, M, Kd), lib.lancius_input(g, Kd, N)
+    mm = lib.lancius_matmul(g, na, nb)
+    lib.lancius_graph_set_dtype(g, abi.DTYPE_FP32)
+    nb.contents.dtype = abi.DTYPE_INT8
+    nb.contents.scale = 0.004
+    sched = lib.lancius_ir_schedule(g)
+    case("int8 matmul program as a recorded graph")
+    prog = DeviceProgram(dev, g, sched, flags=DEVICE_GRAPH)
+    bq = np.round(prng.uniform(230, (Kd, N), -127.4, 127.4)).astype(np.int8)
+    prog.upload(nb, bq)
+    for rep in range(4):
+        a = prng.normal(240 + rep, (M, Kd), std=1.0 + rep)
+        prog.upload(na, a)
+        prog.run()
+        got = prog.download(mm).reshape(M, N)
+        assert oracle.normwise_error(got, oracle.matmul_i8(f64(a), bq, 0.004)) <= TOL, rep
+        x = prng.normal(250 + rep, (4096,))
+        dx, dq, ds = dev.upload(x), dev.alloc(4096), dev.alloc(8)
+        dev.quantize_i8(dq, ds, dx, 4096)
+        np.testing.assert_array_equal(dev.download(dq, (4096,), np.int8), oracle.quantize_i8(f64(x))[0])
+        for b in (dx, dq, ds):
+            b.free()
     prog.close()
     lib.lancius_schedule_destroy(sched)
     lib.lancius_graph_destroy(g)
