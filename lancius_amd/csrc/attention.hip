@@ -107,6 +107,14 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
     const int qt = !p.causal                        ? t_rank
                    : (p.pair_tiles && t_rank >= p.q_tiles - half_t) ? t_rank - (p.q_tiles - half_t)
                                                                       : p.q_tiles - 1 - t_rank;
+    // The short tile of a resident causal pair waits about 3.4 us (127 x 64
+    // clocks at 2.4 GHz) before its first loads, so the long tiles, which
+    // bound the launch, get the HBM to themselves for their Q and first K/V
+    // blocks: S=512 causal 48.7 / 49.8 -> 47.9 / 47.4 us, B4 S=1024 causal
+    // 85.1 / 84.7 -> 82.8 / 82.8 us (one box, builds alternated; half and
+    // twice the wait measured no better).
+    if constexpr (KS == 2)
+        if (p.causal && p.pair_tiles && t_rank >= p.q_tiles - half_t) __builtin_amdgcn_s_sleep(127);
     const int S = p.S, H = p.H, Skv = p.Skv;
     const int off = Skv - S;  // causal offset of the query rows into the key sequence
     const int hk = h / (H / p.Hkv);
