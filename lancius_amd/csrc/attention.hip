@@ -62,12 +62,17 @@ __device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp
 // the end the odd-block waves hand their (O, m, l) to the even-block waves
 // through LDS, which merge them in that fixed order.  That puts four waves on a SIMD instead of two
 // (at most 128 registers each), each with half the key blocks.  KS = 1:
-// 4 waves, every key block.  The staged keys are double-buffered in LDS.
-template <int D, int BKV, int KS>
-__global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnParams p) {
+// 4 waves, every key block.  BQ = queries per workgroup (128, or 64 for
+// small causal grids).  The staged keys are double-buffered in LDS, or
+// with SINGLE held in one buffer (K and V each refilled once every wave is
+// done with them: two more barriers a step, half the LDS, so three 4-wave
+// workgroups fit a CU).
+template <int D, int BKV, int KS, int BQ = kBQ, bool SINGLE = false>
+__global__ void __launch_bounds__(BQ / 32 * KS * 64, SINGLE ? 3 : 2 * KS) attention_mfma(const AttnParams p) {
     static_assert(D % 32 == 0 && D <= 128 && BKV % 32 == 0, "tile shape");
     static_assert(KS == 1 || KS == 2, "key split");
-    constexpr int NT = 256 * KS;
+    constexpr int NQB = BQ / 32;         // 32-query blocks of the workgroup
+    constexpr int NT = NQB * KS * 64;
     constexpr int LDK = D + 1;  // K rows padded: lanes read 32 different keys at one d
     // V rows: lanes read 32 consecutive d of one key, the two lane halves
     // keys 4 rows apart; D + 8 puts those 32 banks apart (64 banks).
@@ -78,9 +83,10 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
     constexpr int KB = KS * BKV;         // keys staged per step
     constexpr int NKV = KB * D / (4 * NT);  // float4 of each K/V step per thread
     static_assert(NKV * 4 * NT == KB * D, "staging covers the step");
-    constexpr int K_FLOATS = 2 * KB * LDK, V_FLOATS = 2 * KB * LDV;
+    constexpr int NBUF = SINGLE ? 1 : 2;
+    constexpr int K_FLOATS = NBUF * KB * LDK, V_FLOATS = NBUF * KB * LDV;
     constexpr int PER = 16 * DB + 2;  // a lane's hand-off: O^T registers, m, l
-    constexpr int RED_FLOATS = KS > 1 ? 4 * PER * 64 : 0;
+    constexpr int RED_FLOATS = KS > 1 ? NQB * PER * 64 : 0;
     constexpr int SMEM = K_FLOATS + V_FLOATS > RED_FLOATS ? K_FLOATS + V_FLOATS : RED_FLOATS;
     static_assert(K_FLOATS % 4 == 0, "V rows 16-byte aligned");
     __shared__ __attribute__((aligned(16))) float smem[SMEM];
@@ -100,7 +106,7 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
     const int h = rem - z * p.H;
     const int g = z / p.batch, b = z % p.batch;
     // Causal order: longest tiles first.  When every workgroup is resident at
-    // once (p.pair_tiles: two per CU), ranks T/2.. run the shortest tiles
+    // once (p.pair_tiles: two or three per CU), ranks T/2.. run the shortest tiles
     // first instead, so the workgroup that shares a CU with the k-th longest
     // tile gets the k-th shortest one (tile T-1-k with tile k).
     const int half_t = p.q_tiles / 2;
@@ -113,7 +119,7 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
     // blocks: S=512 causal 48.7 / 49.8 -> 47.9 / 47.4 us, B4 S=1024 causal
     // 85.1 / 84.7 -> 82.8 / 82.8 us (one box, builds alternated; half and
     // twice the wait measured no better).
-    if constexpr (KS == 2)
+    if constexpr (KS == 2 && BQ == kBQ)
         if (p.causal && p.pair_tiles && t_rank >= p.q_tiles - half_t) __builtin_amdgcn_s_sleep(127);
     const int S = p.S, H = p.H, Skv = p.Skv;
     const int off = Skv - S;  // causal offset of the query rows into the key sequence
@@ -129,16 +135,16 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
-    // KS = 2: wave w < 4 takes the even key blocks of query block w, wave
-    // w + 4 the odd key blocks of query block 3 - w.  The hardware puts
-    // waves w and w + 4 of a workgroup on the same SIMD (measured on MI355X
-    // from the HW_ID register), so each SIMD gets half of a short and half
-    // of a long query block of a causal tile, and the four SIMDs of the CU
-    // finish together.
-    const int kh = wave >> 2;                 // key parity
-    const int wq = kh ? 7 - wave : wave;      // query block of the wave
+    // KS = 2: wave w < NQB takes the even key blocks of query block w, wave
+    // w + NQB the odd key blocks of query block NQB - 1 - w.  The hardware
+    // puts waves w and w + 4 of a workgroup on the same SIMD (measured on
+    // MI355X from the HW_ID register), so with 128 queries each SIMD gets
+    // half of a short and half of a long query block of a causal tile, and
+    // the four SIMDs of the CU finish together.
+    const int kh = wave / NQB;                      // key parity
+    const int wq = kh ? 2 * NQB - 1 - wave : wave;  // query block of the wave
     const int lq = lane & 31, lk = lane >> 5;
-    const int q0 = qt * kBQ;
+    const int q0 = qt * BQ;
     const int qw0 = q0 + wq * 32;     // first query of this wave
     const int q = qw0 + lq;           // this lane's query
     const bool q_valid = q < S;
@@ -161,7 +167,7 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
     }
 
     // Key range of this workgroup, in blocks of BKV and steps of KS blocks.
-    const int kv_end = p.causal ? max(0, min(Skv, q0 + kBQ + off)) : Skv;
+    const int kv_end = p.causal ? max(0, min(Skv, q0 + BQ + off)) : Skv;
     const int nblocks = (kv_end + BKV - 1) / BKV;
     const int nsteps = (nblocks + KS - 1) / KS;
 
@@ -176,6 +182,41 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
     const __amdgpu_buffer_rsrc_t vbuf =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Vg), 0, kv_bytes, kBufferRsrcWord3);
     f32x4 kreg[NKV], vreg[NKV];
+    // SINGLE: K and V staged in separate halves of the step (K loaded at the
+    // step's start and stored once every wave has formed its scores, V
+    // loaded then and stored at the step's end), so only one tensor's
+    // registers are live at a time
+    auto load_one = [&](const __amdgpu_buffer_rsrc_t& buf, f32x4* reg, int k0) {
+#pragma unroll
+        for (int i = 0; i < NKV; ++i) {
+            const int idx = tid + NT * i;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
+            const int gk = k0 + key;
+            const int off = pick(gk < Skv, (gk * (int)kv_stride + 4 * dq) * (int)sizeof(float), kOut);
+            reg[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(buf, off, 0, 0));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto store_k = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NKV; ++i) {
+            const int idx = tid + NT * i;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
+            float* kd = &Ks[buf][key][4 * dq];
+            kd[0] = kreg[i].x;
+            kd[1] = kreg[i].y;
+            kd[2] = kreg[i].z;
+            kd[3] = kreg[i].w;
+        }
+    };
+    auto store_v = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < NKV; ++i) {
+            const int idx = tid + NT * i;
+            const int key = idx / (D / 4), dq = idx % (D / 4);
+            *(f32x4*)&Vs[buf][key][4 * dq] = kreg[i];
+        }
+    };
     auto load_kv = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < NKV; ++i) {
@@ -219,9 +260,13 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
     __syncthreads();
 
     for (int st = 0; st < nsteps; ++st) {
-        const int cur = st & 1;
+        const int cur = SINGLE ? 0 : st & 1;
         const bool more = st + 1 < nsteps;
-        if (more) load_kv((st + 1) * KB);
+        if constexpr (SINGLE) {
+            if (more) load_one(kbuf, kreg, (st + 1) * KB);
+        } else {
+            if (more) load_kv((st + 1) * KB);
+        }
         const int blk = st * KS + kh;  // this wave's block
         const int kb = blk * BKV;
         const int kl = kh * BKV;       // its first row in the staged keys
@@ -229,8 +274,8 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
         // Wave-uniform skip of blocks past the keys or entirely above this
         // wave's diagonal.
         const bool active = blk < nblocks && (!p.causal || kb <= qw0 + 31 + off);
+        f32x16 s_acc[SB];
         if (active) {
-            f32x16 s_acc[SB];
 #pragma unroll
             for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
@@ -243,6 +288,15 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
                     s_acc[sb] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[cur][kl + 32 * sb + lq][d], qf[s], s_acc[sb],
                                                                      0, 0, 0);
             }
+        }
+        if constexpr (SINGLE) {
+            __syncthreads();  // every wave has read the staged K
+            if (more) {
+                store_k(0);
+                load_one(vbuf, kreg, (st + 1) * KB);
+            }
+        }
+        if (active) {
             // Register r of lane l holds key kb + 32*sb + 8*(r/4) + 4*(l/32) + r%4.
             const bool need_mask = (p.causal && kb + BKV - 1 > qw0 + off) || (kb + BKV > Skv);
             if (need_mask) {
@@ -296,7 +350,14 @@ __global__ void __launch_bounds__(256 * KS, 2 * KS) attention_mfma(const AttnPar
                                                                          s_acc[sb][s], o_acc[db], 0, 0, 0);
                 }
         }
-        if (more) store_kv(cur ^ 1);
+        if constexpr (SINGLE) {
+            if (more) {
+                __syncthreads();  // every wave has read the staged V
+                store_v(0);
+            }
+        } else {
+            if (more) store_kv(cur ^ 1);
+        }
         __syncthreads();
     }
 
@@ -763,6 +824,24 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
     p.Z = (int)z;
     // the MFMA kernel addresses a sequence's K and V rows with 32-bit buffer offsets
     if (vec && D % 32 == 0 && D <= 128 && Skv * Hkv * D * sizeof(float) < ((size_t)1 << 31) - 64) {
+        // Causal D = 64 grids of at most three 64-query tiles per CU: 4-wave
+        // workgroups with one LDS buffer, three resident per CU (the
+        // 128-query grid leaves CUs idle or half-loaded there).  Measured
+        // against the 128-query kernel (one box, builds alternated): B1 H16
+        // S=512 39.3 -> 26.3 us, B2 H8 S=256 21.9 -> 15.5 us, B8 H16 S=256
+        // 22.9 -> 18.7 us, S=384 37.5 -> 33.5 us, B4 H16 S=768 69.5 ->
+        // 56.5 us.  At four tiles per CU (B8 S=512, B4 S=1024) it does not
+        // fit (three workgroups a CU by registers).
+        {
+            const size_t qt64 = (S + 63) / 64, t64 = qt64 * H * z;
+            if (D == 64 && causal && t64 <= 3 * (size_t)cu_count(ctx)) {
+                p.q_tiles = (int)qt64;
+                p.pair_tiles = 1;
+                hipLaunchKernelGGL((attention_mfma<64, 32, 2, 64, true>), dim3((unsigned)t64), dim3(256), 0, ctx->stream, p);
+                if (int rc = check_launch("attention_mfma")) return rc;
+                return ok();
+            }
+        }
         p.q_tiles = (int)((S + kBQ - 1) / kBQ);
         const size_t tasks = (size_t)p.q_tiles * H * z;
         LANCIUS_REQUIRE(tasks < kMaxGridX, LANCIUS_HIP_ERR_SHAPE, "attention: too many tiles");
