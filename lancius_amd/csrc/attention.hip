@@ -824,19 +824,25 @@ int attention_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* O, cons
     p.Z = (int)z;
     // the MFMA kernel addresses a sequence's K and V rows with 32-bit buffer offsets
     if (vec && D % 32 == 0 && D <= 128 && Skv * Hkv * D * sizeof(float) < ((size_t)1 << 31) - 64) {
-        // Causal D = 64 grids of at most three 64-query tiles per CU: 4-wave
-        // workgroups with one LDS buffer, three resident per CU (the
-        // 128-query grid leaves CUs idle or half-loaded there).  Measured
-        // against the 128-query kernel (one box, builds alternated): B1 H16
+        // D = 64 grids of at most three 64-query tiles per CU: 4-wave
+        // workgroups with one LDS buffer, three resident per CU, where the
+        // 128-query grid leaves CUs idle or half-loaded.  Measured against
+        // the 128-query kernel (one box, builds alternated), causal: B1 H16
         // S=512 39.3 -> 26.3 us, B2 H8 S=256 21.9 -> 15.5 us, B8 H16 S=256
         // 22.9 -> 18.7 us, S=384 37.5 -> 33.5 us, B4 H16 S=768 69.5 ->
-        // 56.5 us.  At four tiles per CU (B8 S=512, B4 S=1024) it does not
-        // fit (three workgroups a CU by registers).
+        // 56.5 us; non-causal: B1 H16 S=512 41.2 -> 26.3 us, S=1024 76 ->
+        // 48 us, B4 H16 S=768 108.5 -> 86.6 us.  Non-causal grids whose
+        // 128-query tiles give every CU the same count keep them (B2 S=1024
+        // 77.4 -> 80, B1 S=2048 147.5 -> 153 us, B8 S=256 even).  At four
+        // tiles per CU (B8 S=512, B4 S=1024) it does not fit (three
+        // workgroups a CU by registers).
         {
+            const size_t cus = (size_t)cu_count(ctx);
             const size_t qt64 = (S + 63) / 64, t64 = qt64 * H * z;
-            if (D == 64 && causal && t64 <= 3 * (size_t)cu_count(ctx)) {
+            const size_t t128 = (S + kBQ - 1) / kBQ * H * z;
+            if (D == 64 && t64 <= 3 * cus && (causal || t128 % cus != 0)) {
                 p.q_tiles = (int)qt64;
-                p.pair_tiles = 1;
+                p.pair_tiles = causal ? 1 : 0;
                 hipLaunchKernelGGL((attention_mfma<64, 32, 2, 64, true>), dim3((unsigned)t64), dim3(256), 0, ctx->stream, p);
                 if (int rc = check_launch("attention_mfma")) return rc;
                 return ok();

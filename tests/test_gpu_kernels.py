@@ -440,14 +440,15 @@ def test_attention_config_s512(dev, causal):
     assert err <= oracle.tolerance(512)
 
 
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("B,S,H", [(4, 768, 16), (1, 512, 16), (2, 300, 8), (3, 64, 5)])
-def test_attention_small_causal_grids(dev, B, S, H):
-    """Causal D = 64 grids of at most three 64-query tiles per CU run the
-    64-query kernel (4-wave workgroups, one LDS buffer, three resident a CU,
+def test_attention_small_grids(dev, B, S, H, causal):
+    """D = 64 grids of at most three 64-query tiles per CU run the 64-query
+    kernel (4-wave workgroups, one LDS buffer, three resident a CU; causal
     long and short tiles paired): every element against the oracle, the
     output NaN-filled first.  B4 H16 S=768 is three tiles per CU on 256 CUs,
     B1 S=512 fewer workgroups than CUs, S=300 a ragged last tile."""
-    got, ref = _attn_case(dev, B, S, H, 64, True, seed=970 + S)
+    got, ref = _attn_case(dev, B, S, H, 64, causal, seed=970 + S)
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(S)
 
 
