@@ -173,12 +173,13 @@ def decode_cases(dev, steps, warmup) -> dict:
             t, f, _ = attention_case(dev, 8, 2048, 16, D, causal, 44, steps, warmup)
             out[name] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
                          "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
-    # one sequence and four of S=768, causal: grids too small to fill the
-    # CUs with 128-query tiles (the 64-query kernel)
-    for B, S in ((1, 512), (4, 768)):
-        t, f, _ = attention_case(dev, B, S, 16, 64, True, 44, steps, warmup)
-        out[f"attention_B{B}_H16_D64_S{S}_causal"] = {"ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
-                                                       "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
+    # one sequence, and four of S=768: grids too small to fill the CUs
+    # with 128-query tiles (the 64-query kernel)
+    for B, S, causal in ((1, 512, True), (1, 512, False), (4, 768, True)):
+        t, f, _ = attention_case(dev, B, S, 16, 64, causal, 44, steps, warmup)
+        out[f"attention_B{B}_H16_D64_S{S}_{'causal' if causal else 'noncausal'}"] = {
+            "ms": round(t, 4), "GFLOP/s": round(f / t / 1e6, 1),
+            "frac_fp32_mfma": round(f / t / 1e9 / PEAK_FP32_MFMA, 4)}
     rows, hid = 4096, 4096
     x = dev.upload(prng.normal(66, (rows, hid)))
     g = dev.upload(np.ones((hid,), np.float32))
