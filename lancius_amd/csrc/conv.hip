@@ -1078,7 +1078,21 @@ int launch(lancius_hip_ctx* ctx, ConvParams& p) {
         // 143.7 us; N31: 5.93, 122.7 against 141.3).
         const size_t cus = (size_t)cu_count(ctx), per = grid / cus, rem = grid % cus;
         const size_t units = (grid - (per > 0 ? per - 1 : 0) * cus) * (size_t)p.Kdim / 16;
-        if (per >= 1 && per <= (size_t)occ && rem != 0 && rem <= cus / 4 && units * cus < ((size_t)1 << 31)) {
+        // Grids under half the CUs (small batches): every workgroup takes an
+        // equal share of all (tile, k-tile) units, each share at least 18
+        // k-tiles and a tile split at most 8 ways (the finishing workgroup
+        // reads every share through the point of coherence, about 30 GB/s
+        // for one workgroup).  Measured with the filter re-laid in the call:
+        // N1 64->128 56^2 30.8 -> 25.9 us, N2 30.9 -> 26.8, N1 128->256 28^2
+        // 55.7 -> 32.0, N1 256->512 14^2 107.6 -> 46.6, N2 64->64 56^2 21.1
+        // -> 17.2; shares of at least 8 or 12 k-tiles measured slower at 56^2.
+        const size_t sk_small =
+            std::min(cus, grid * std::min<size_t>(8, std::max<size_t>(1, (size_t)p.Kdim / 16 / 18)));
+        if (per == 0 && sk_small >= 2 * grid && units >= 4 * sk_small && units * sk_small < ((size_t)1 << 31)) {
+            p.sk_dp = 0;
+            p.sk_wgs = (int)sk_small;
+            part_bytes = 2 * sk_small * BM * BN * sizeof(float);
+        } else if (per >= 1 && per <= (size_t)occ && rem != 0 && rem <= cus / 4 && units * cus < ((size_t)1 << 31)) {
             p.sk_dp = (int)((per - 1) * cus);
             p.sk_wgs = (int)cus;
             part_bytes = 2 * cus * BM * BN * sizeof(float);

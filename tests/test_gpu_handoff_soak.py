@@ -71,8 +71,9 @@ def test_soak_skinny_gemm(dev, M, K, N, act):
 
 # Tile counts a little over a whole number per CU on a 256-CU part, so the
 # last tiles are shared (stream-K): 294 (128x64 tiles), 282 (64x64 tiles)
-# and the bench conv's 1568.  5 / 5 / 2 inputs x 11 calls.
-CONV = [(6, 16, 56, 56, 128, 5), (23, 32, 28, 28, 64, 5), (32, 64, 56, 56, 128, 2)]
+# and the bench conv's 1568; a small grid split over all CUs (26 tiles, each
+# shared 4 ways).  5 / 5 / 2 / 3 inputs x 11 calls.
+CONV = [(6, 16, 56, 56, 128, 5), (23, 32, 28, 28, 64, 5), (32, 64, 56, 56, 128, 2), (1, 128, 28, 28, 256, 3)]
 
 
 @pytest.mark.parametrize("N,C_in,H,W,C_out,inputs", CONV)

@@ -145,6 +145,12 @@ CONVS = [
     (2, 3, 20, 20, 128, 5, 1, 2, "implicit GEMM 128x64 tiles, OIHW filter"),
     (2, 3, 20, 20, 64, 5, 2, 1, "implicit GEMM 64x64 tiles, OIHW filter"),
     (2, 6, 15, 15, 96, 3, 1, 1, "implicit GEMM 128x64 tiles, 3x3 OIHW filter"),
+    # grids under half the CUs: every workgroup an equal share of the
+    # (tile, k-tile) units, a tile split 2, 4, 8 ways, the last sharer adding
+    (1, 64, 56, 56, 128, 3, 1, 1, "direct, small grid split 2 ways (49 tiles)"),
+    (1, 128, 28, 28, 256, 3, 1, 1, "direct, small grid split 4 ways (26 tiles)"),
+    (1, 256, 14, 14, 512, 3, 1, 1, "direct, small grid split 8 ways (16 tiles)"),
+    (1, 80, 23, 23, 100, 3, 1, 1, "direct, small grid split 2 ways, ragged tiles"),
 ]
 
 
