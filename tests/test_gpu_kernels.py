@@ -189,6 +189,16 @@ def test_gemm_skinny_wide(dev, M, K, N):
     assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K,N", [(64, 4096, 2048), (48, 2048, 4096), (33, 4096, 2050)])
+def test_gemm_rows_33_to_64_as_two_skinny_products(dev, M, K, N):
+    """32 < M <= 64 with B of at least 32 MiB: rows 0-31 and 32..M-1 run as
+    two skinny products (A, C and the residual offset by 32 rows).  C is
+    NaN-filled; bias, GELU and a residual; every row against the oracle;
+    M = 33 leaves a one-row second product, N % 4 != 0 the scalar-B path."""
+    got, ref = _gemm_case(dev, M, K, N, seed=160 + M + K, bias=True, act=ACT_GELU, residual=True)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
 def test_gemm_skinny_grouped(dev):
     """A grouped call (blockIdx.z = member) through the skinny kernel: each
     member against its own oracle product."""
