@@ -1574,7 +1574,12 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         const int bm_kg = K >= 2048 && big_tiles >= 192 ? 128 : 64;
         const int kg = bm_kg == 128 || t64 <= 384 ? 4 : 2;
         const size_t kg_tiles = count * ((M + bm_kg - 1) / bm_kg) * ((N + bm_kg - 1) / bm_kg);
-        if (kg_tiles >= 128) {
+        // at least 192 tiles: with 128 to 191 the split-K tiled kernels
+        // below are faster (128x4096x4096 72.0 -> 52.2 us, 4096x4096x128
+        // 74.6 -> 51.3 us, 96x4096x4096 71.5 -> 51.5 us, 128x2048x4096 38.1
+        // -> 35.0 us; 192 tiles, e.g. 192x4096x4096, measured 71.7 against
+        // 84.0 us split)
+        if (kg_tiles >= 192) {
             p.tiles_m = (uint32_t)((M + bm_kg - 1) / bm_kg);
             p.tiles_n = (uint32_t)((N + bm_kg - 1) / bm_kg);
             // k-tiles of 16: with 32 (half the barriers per k) the 64 x 64

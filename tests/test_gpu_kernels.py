@@ -199,6 +199,15 @@ def test_gemm_rows_33_to_64_as_two_skinny_products(dev, M, K, N):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
 
 
+@pytest.mark.parametrize("M,K,N", [(128, 2048, 4096), (4096, 1024, 96)])
+def test_gemm_mid_grids_split_k(dev, M, K, N):
+    """128 to 191 tiles of 64 x 64 run the split-K tiled kernels (partials
+    added by the reduce kernel) rather than the k-group kernel: every
+    element against the oracle, with bias, GELU and a residual."""
+    got, ref = _gemm_case(dev, M, K, N, seed=165 + M + K, bias=True, act=ACT_GELU, residual=True)
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
 def test_gemm_skinny_grouped(dev):
     """A grouped call (blockIdx.z = member) through the skinny kernel: each
     member against its own oracle product."""
