@@ -1571,7 +1571,10 @@ int gemm_dispatch(lancius_hip_ctx* ctx, size_t count, float* const* C, const flo
         // 1024x4096x1024 (bias and residual) 259.8 -> 251.4.  At K = 1024 they
         // lose to 64 x 64 tiles unless the grid is exactly 256 of them (3072 x
         // 1024 x 1024: 54.9 -> 69.2 us; 4096 x 1024 x 1024: 70.5 -> 69.9).
-        const int bm_kg = K >= 2048 && big_tiles >= 192 ? 128 : 64;
+        // (128 x 128 tiles from 256 of them: with 192 to 255 the 64 x 64
+        // tiles measured faster, 768x4096x4096 245.5 -> 195.5 us and
+        // 4096x2048x768 127.7 -> 101.8 us, one box, builds alternated)
+        const int bm_kg = K >= 2048 && big_tiles >= 256 ? 128 : 64;
         const int kg = bm_kg == 128 || t64 <= 384 ? 4 : 2;
         const size_t kg_tiles = count * ((M + bm_kg - 1) / bm_kg) * ((N + bm_kg - 1) / bm_kg);
         // at least 192 tiles: with 128 to 191 the split-K tiled kernels

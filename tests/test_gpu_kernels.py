@@ -208,6 +208,16 @@ def test_gemm_mid_grids_split_k(dev, M, K, N):
     assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
 
 
+@pytest.mark.parametrize("M,K,N", [(768, 2048, 4096), (4096, 2048, 768)])
+def test_gemm_k_groups_192_to_255_big_tiles(dev, M, K, N):
+    """K >= 2048 with 192 to 255 tiles of 128 x 128: the k-group kernel at
+    64 x 64 tiles, two k-groups.  C NaN-filled, bias and a residual, two rows
+    of every 128-row band against the oracle (every column)."""
+    got, ref = _gemm_case(dev, M, K, N, seed=168 + M, bias=True, residual=True, row_list=band_rows(M))
+    assert np.isfinite(got).all()
+    assert oracle.normwise_error(got, ref) <= oracle.tolerance(K)
+
+
 def test_gemm_skinny_grouped(dev):
     """A grouped call (blockIdx.z = member) through the skinny kernel: each
     member against its own oracle product."""
