@@ -63,7 +63,7 @@ __device__ __forceinline__ float exp2_raw(float x) { return __builtin_amdgcn_exp
 // through LDS, which merge them in that fixed order.  That puts four waves on a SIMD instead of two
 // (at most 128 registers each), each with half the key blocks.  KS = 1:
 // 4 waves, every key block.  BQ = queries per workgroup (128, or 64 for
-// small causal grids).  The staged keys are double-buffered in LDS, or
+// grids too small to fill the CUs with 128-query tiles).  The staged keys are double-buffered in LDS, or
 // with SINGLE held in one buffer (K and V each refilled once every wave is
 // done with them: two more barriers a step, half the LDS, so three 4-wave
 // workgroups fit a CU).
